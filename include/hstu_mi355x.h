@@ -1,0 +1,98 @@
+/*
+ * C ABI of the MI355X-native HSTU hot path (gfx950).
+ *
+ * Plain pointers and sizes only; every pointer is a device pointer unless it
+ * says otherwise, and every entry point launches on the given HIP stream and
+ * returns 0 (hipSuccess) or a hipError_t / HSTU_E* code without synchronising.
+ * No entry point allocates device memory.
+ *
+ * Reference paths are relative to
+ * recommendation_v4/hstu/generative_recommenders/ in zirui/mlperf-training.
+ *
+ * Layouts
+ *   q, k, v, out, dq, dk, dv : jagged [T, H, D]; element (t, h, d) lives at
+ *       base + t*row_stride + h*D + d (row_stride in elements, >= H*D), so
+ *       column slices of a fused [T, 2048] UVQK buffer are accepted in place.
+ *   seq_offsets               : int64 [B+1], exclusive cumsum of lengths.
+ *   scales (FP8 inputs)       : fp32, scale(t, h) = s[t*scale_row_stride +
+ *       h*scale_head_stride]; strides (0, 0) give one per-tensor scalar,
+ *       (H, 1) per-token-per-head.  Dequantized value = e4m3 * scale.
+ *   attn_bias                 : optional fp32 [H, 2R-1]; score(i, j) gets
+ *       bias[h][clamp(i-j, -(R-1), R-1) + R-1] added before SiLU.  This bias
+ *       is an extension: the reference has none (pass NULL for parity).
+ */
+#ifndef HSTU_MI355X_H_
+#define HSTU_MI355X_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* input element types */
+#define HSTU_DTYPE_BF16 0
+#define HSTU_DTYPE_FP8_E4M3 1
+
+/* error codes beyond hipError_t (all negative) */
+#define HSTU_E_BAD_ARG (-1)
+#define HSTU_E_UNSUPPORTED (-2)
+
+/* Library version / self-description; host pointer to a static string. */
+const char* hstu_version(void);
+
+/*
+ * Jagged causal SiLU attention, forward:
+ *   out_i = sum_{valid j} silu(alpha * q_i.k_j [+ bias]) / N * v_j
+ * (N = max_seq_len).  Output is bf16 for both input types.
+ * Mask options follow _get_valid_attn_mask: num_targets (int32 [B], nullable),
+ * max_attn_len, contextual_seq_len (0 = off).
+ * Replaces: triton_hstu_attention_fwd, ops/triton/triton_hstu_attention.py:3166-3295
+ *           (launch of _hstu_attn_fwd, grid at :3247-3250), and the FlyDSL
+ *           forward launches fn(q, k, v, out, cu, batch, m_blocks, 1/N[, qkv_scale])
+ *           at ops/flydsl/hstu_flydsl_mha.py:2045-2046 and :2428-2429.
+ */
+int hstu_attn_fwd(int dtype,
+                  const void* q, const void* k, const void* v,
+                  int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                  const float* q_scale, const float* k_scale, const float* v_scale,
+                  int64_t scale_row_stride, int64_t scale_head_stride,
+                  const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                  float alpha,
+                  const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
+                  const float* attn_bias, int bias_R,
+                  void* out, int64_t out_row_stride,
+                  hipStream_t stream);
+
+/*
+ * Backward of hstu_attn_fwd.  Writes dq, dk, dv (bf16, caller-owned, may be
+ * strided views) completely -- no accumulation into existing contents, so no
+ * zero-fill is needed -- and, if dbias != NULL, overwrites dbias (fp32
+ * [H, 2R-1]) with the bias gradient.  Gradients are with respect to the
+ * dequantized q, k, v.  Deterministic: no atomics on dq/dk/dv.
+ * Replaces: triton_hstu_attention_bwd, ops/triton/triton_hstu_attention.py:3298-3410
+ *           (mutates_args dq/dk/dv), and the FlyDSL backward launch
+ *           fn(q, k, v, dout, dk, dv, dq_slot, cu, batch, n_blocks, 1/N, qkv_scale)
+ *           at ops/flydsl/hstu_flydsl_mha.py:1707-1723.
+ */
+int hstu_attn_bwd(int dtype,
+                  const void* dout, int64_t dout_row_stride,
+                  const void* q, const void* k, const void* v,
+                  int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                  const float* q_scale, const float* k_scale, const float* v_scale,
+                  int64_t scale_row_stride, int64_t scale_head_stride,
+                  const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                  float alpha,
+                  const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
+                  const float* attn_bias, int bias_R,
+                  void* dq, void* dk, void* dv,
+                  int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
+                  float* dbias,
+                  hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HSTU_MI355X_H_ */

@@ -1,0 +1,1145 @@
+// HSTU jagged causal SiLU attention for MI355X (gfx950, CDNA4).
+//
+//   out_i = sum_{valid j <= i} silu(alpha * q_i.k_j [+ bias(i-j)]) / N * v_j
+//
+// Forward and backward over jagged [T, H, D] tensors addressed through int64
+// seq_offsets, no padding.  bf16 inputs use v_mfma_f32_16x16x32_bf16 for both
+// contractions; e4m3 (OCP) inputs use v_mfma_f32_16x16x128_f8f6f4 for Q.K^T
+// with per-(token, head) fp32 scales applied as a rank-1 factor on the score
+// tile, and bf16 MFMA for P.V with V dequantized while it is staged into LDS
+// (the reference's FP8 forward does the same: P and V go to bf16,
+// ops/triton/triton_hstu_attention.py:503-520).
+//
+// Reference behaviour followed (paths relative to
+// recommendation_v4/hstu/generative_recommenders/):
+//   forward tile math   ops/triton/triton_hstu_attention.py:415-522
+//   n-loop / diagonal   ops/triton/triton_hstu_attention.py:584-911
+//   backward tile math  ops/triton/triton_hstu_attention.py:2090-2212, 2500
+//   mask                ops/pytorch/pt_hstu_attention.py:32-84
+//
+// Design (per kernel, one workgroup = 4 waves of 64 lanes):
+//   * every MFMA is 16x16; a lane's C fragment holds rows 4*(lane/16)+r,
+//     column lane%16.  Scores are computed transposed (S^T = K.Q^T) where the
+//     next contraction runs over keys, so the C fragment of S^T is already
+//     the A operand of P.V: no shuffles between the two GEMMs.
+//   * an operand whose contraction index runs along rows in memory (V for
+//     P.V, dO / Q for dV / dK, K for dQ) is staged into LDS transposed, in a
+//     key order ("sigma") that makes each lane's eight keys contiguous, so the
+//     B operand is one ds_read_b128.  LDS row pitches are padded by 16 bytes,
+//     which makes the 16-lane row reads of every operand conflict-free.
+//   * SiLU uses the hardware exp2 / rcp: with t = -x*log2(e),
+//     silu(x) = -ln2 * t / (1 + 2^t); the -ln2/N factor is applied once to
+//     the fp32 accumulator instead of per score.
+//   * tiles strictly below the diagonal skip the mask; tiles strictly above
+//     it are never visited (per wave), so causal work is ~P pairs, not N^2.
+//   * global -> register prefetch of tile t+1 overlaps the MFMAs of tile t;
+//     LDS is double buffered with one barrier per tile.
+//   * grids are 1-D with the heaviest blocks first (longest key range), and
+//     blocks of one (sequence, head) are B*H apart, which keeps them on one
+//     XCD (and its L2) whenever B*H is a multiple of 8.
+//   * dq/dk/dv are written exactly once (two kernels: dK/dV with the key block
+//     outer, dQ with the query block outer); no atomics, deterministic.
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+#include <vector>
+
+#include "hstu_mi355x.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kThreads = 256;
+
+// ---------------------------------------------------------------- primitives
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+// e4m3 x e4m3, K = 128, no block scaling (scale operands 0 select the plain
+// v_mfma_f32_16x16x128_f8f6f4).
+__device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ uint16_t to_bf16(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+__device__ __forceinline__ u32x4 lds_ld128(const uint8_t* p) { return *(const u32x4*)p; }
+__device__ __forceinline__ f32x4 lds_ldf4(const uint8_t* p) { return *(const f32x4*)p; }
+__device__ __forceinline__ i32x8 cat8(u32x4 lo, u32x4 hi) {
+  i32x8 r;
+  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
+  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
+  return r;
+}
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// t = -x*log2(e)  ->  t * sigmoid(x) = t / (1 + 2^t)   (== -silu(x)/ln2)
+__device__ __forceinline__ float sig_of_t(float t) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
+// 4 e4m3 bytes of a word -> 4 floats scaled by s, as 2 packed bf16 words.
+__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w, float s) {
+  f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+  f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+  return u32x2{pack_bf16(lo[0] * s, lo[1] * s), pack_bf16(hi[0] * s, hi[1] * s)};
+}
+
+// Key order inside a transposed LDS tile.  The S^T C fragment of key
+// sub-tiles 2c and 2c+1 gives lane group g the keys {32c+4g+r, 32c+16+4g+r};
+// storing key 32c+16h+4g+r at column 32c+8g+4h+r makes those eight keys one
+// contiguous 16-byte run, in register order.
+__device__ __forceinline__ int sigma(int kk) {
+  return (kk & ~31) | (((kk >> 2) & 3) << 3) | (((kk >> 4) & 1) << 2) | (kk & 3);
+}
+
+// ---------------------------------------------------------------- mask
+struct MaskCtx {
+  int L, nt, ctx, max_attn;
+  bool targets;
+};
+// _get_valid_attn_mask (ops/pytorch/pt_hstu_attention.py:32-84), per element.
+__device__ __forceinline__ bool valid_generic(int i, int j, const MaskCtx& m) {
+  int max_ids = m.L, ii = i, jj = j;
+  if (m.ctx > 0) {
+    ii = max(i - m.ctx + 1, 0);
+    jj = max(j - m.ctx + 1, 0);
+    max_ids = m.L - m.ctx + 1;
+  }
+  if (m.targets) {
+    max_ids -= m.nt;
+    ii = min(ii, max_ids);
+    jj = min(jj, max_ids);
+  }
+  const int dist = ii - jj;
+  bool v = (i == j) || (dist > 0);
+  if (m.max_attn > 0) v = v && (dist <= m.max_attn);
+  if (m.ctx > 0) v = v || (ii == 0 && jj < max_ids);
+  return v && j < m.L && i < m.L;
+}
+
+// ---------------------------------------------------------------- tile movers
+// Each mover is split into load() (global -> registers, issued before the
+// MFMAs of the current tile) and store() (registers -> LDS, after them).
+// Rows at or beyond `nrows` are zero-filled.
+
+// ROWS x D elements of ES bytes, copied as-is; LDS pitch D*ES + 16.
+template <int ROWS, int D, int ES>
+struct CopyTile {
+  static constexpr int CPR = D * ES / 16;
+  static constexpr int N = ROWS * CPR / kThreads;
+  static constexpr int PITCH = D * ES + 16;
+  static_assert(N >= 1 && ROWS * CPR % kThreads == 0, "tile/thread mismatch");
+  u32x4 r[N];
+  __device__ __forceinline__ void load(const uint8_t* base, int64_t rs_bytes, int row0, int nrows) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int item = threadIdx.x + kThreads * i, row = item / CPR, ch = item % CPR;
+      r[i] = u32x4{0u, 0u, 0u, 0u};
+      if (row0 + row < nrows) r[i] = *(const u32x4*)(base + (int64_t)(row0 + row) * rs_bytes + ch * 16);
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int item = threadIdx.x + kThreads * i, row = item / CPR, ch = item % CPR;
+      *(u32x4*)(lds + row * PITCH + ch * 16) = r[i];
+    }
+  }
+};
+
+// ROWS x D e4m3 rows -> bf16 rows (times the row's scale); LDS pitch 2D + 16.
+template <int ROWS, int D>
+struct DeqTile {
+  static constexpr int CPR = D / 16;
+  static constexpr int N = ROWS * CPR / kThreads;
+  static constexpr int PITCH = D * 2 + 16;
+  static_assert(N >= 1 && ROWS * CPR % kThreads == 0, "tile/thread mismatch");
+  u32x4 r[N];
+  float s[N];
+  __device__ __forceinline__ void load(const uint8_t* base, int64_t rs_bytes, const float* sbase,
+                                       int64_t srs, int row0, int nrows) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int item = threadIdx.x + kThreads * i, row = item / CPR, ch = item % CPR;
+      r[i] = u32x4{0u, 0u, 0u, 0u};
+      s[i] = 0.f;
+      if (row0 + row < nrows) {
+        r[i] = *(const u32x4*)(base + (int64_t)(row0 + row) * rs_bytes + ch * 16);
+        s[i] = sbase[(int64_t)(row0 + row) * srs];
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* lds) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int item = threadIdx.x + kThreads * i, row = item / CPR, ch = item % CPR;
+      u32x2 a = fp8x4_to_bf16x4(r[i][0], s[i]), b = fp8x4_to_bf16x4(r[i][1], s[i]);
+      u32x2 c = fp8x4_to_bf16x4(r[i][2], s[i]), d = fp8x4_to_bf16x4(r[i][3], s[i]);
+      uint8_t* dst = lds + row * PITCH + ch * 32;
+      *(u32x4*)dst = u32x4{a[0], a[1], b[0], b[1]};
+      *(u32x4*)(dst + 16) = u32x4{c[0], c[1], d[0], d[1]};
+    }
+  }
+};
+
+// ROWS x D rows (bf16, or e4m3 times the row's scale) -> transposed bf16
+// [D][ROWS] in sigma key order; LDS pitch 2*ROWS + 16.  One item = 4 rows x
+// 8 columns, transposed in registers into 8 runs of 4 keys (ds_write_b64).
+template <int ROWS, int D, bool FP8>
+struct TransTile {
+  static constexpr int ITEMS = (ROWS / 4) * (D / 8);
+  static constexpr int PITCH = ROWS * 2 + 16;
+  static_assert(ITEMS <= kThreads, "one item per thread");
+  u32x4 r[4];   // bf16: 8 values per row; fp8: r[kk][0..1] holds 8 bytes
+  float s[4];
+  __device__ __forceinline__ void load(const uint8_t* base, int64_t rs_bytes, const float* sbase,
+                                       int64_t srs, int row0, int nrows) {
+    const int item = threadIdx.x;
+    const int a = item % (ROWS / 4), c8 = item / (ROWS / 4);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      r[kk] = u32x4{0u, 0u, 0u, 0u};
+      s[kk] = 0.f;
+      const int row = row0 + 4 * a + kk;
+      if (item < ITEMS && row < nrows) {
+        const uint8_t* src = base + (int64_t)row * rs_bytes;
+        if constexpr (FP8) {
+          u32x2 w = *(const u32x2*)(src + c8 * 8);
+          r[kk][0] = w[0];
+          r[kk][1] = w[1];
+          s[kk] = sbase[(int64_t)row * srs];
+        } else {
+          r[kk] = *(const u32x4*)(src + c8 * 16);
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* lds) const {
+    const int item = threadIdx.x;
+    if (item >= ITEMS) return;
+    const int a = item % (ROWS / 4), c8 = item / (ROWS / 4);
+    u32x4 w[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if constexpr (FP8) {
+        u32x2 lo = fp8x4_to_bf16x4(r[kk][0], s[kk]);
+        u32x2 hi = fp8x4_to_bf16x4(r[kk][1], s[kk]);
+        w[kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        w[kk] = r[kk];
+      }
+    }
+    uint8_t* col = lds + sigma(4 * a) * 2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // column pair (2e, 2e+1) of the 8-column chunk
+      u32x2 ev = {(w[0][e] & 0xffffu) | (w[1][e] << 16), (w[2][e] & 0xffffu) | (w[3][e] << 16)};
+      u32x2 od = {(w[0][e] >> 16) | (w[1][e] & 0xffff0000u), (w[2][e] >> 16) | (w[3][e] & 0xffff0000u)};
+      *(u32x2*)(col + (8 * c8 + 2 * e) * PITCH) = ev;
+      *(u32x2*)(col + (8 * c8 + 2 * e + 1) * PITCH) = od;
+    }
+  }
+};
+
+// ROWS per-row fp32 scales -> LDS (zero beyond nrows).
+template <int ROWS>
+struct ScaleTile {
+  float s;
+  __device__ __forceinline__ void load(const float* sbase, int64_t srs, int row0, int nrows) {
+    s = 0.f;
+    if (threadIdx.x < ROWS && row0 + (int)threadIdx.x < nrows) s = sbase[(int64_t)(row0 + threadIdx.x) * srs];
+  }
+  __device__ __forceinline__ void store(uint8_t* lds) const {
+    if (threadIdx.x < ROWS) ((float*)lds)[threadIdx.x] = s;
+  }
+};
+
+// ---------------------------------------------------------------- params
+struct AttnParams {
+  const uint8_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  const uint8_t* dout;
+  int64_t q_rs, k_rs, v_rs, do_rs;  // row strides, elements
+  const float* q_scale;
+  const float* k_scale;
+  const float* v_scale;
+  int64_t s_rs, s_hs;
+  const int64_t* seq_offsets;
+  const int32_t* num_targets;
+  uint16_t* out;  // forward output
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t o_rs, dq_rs, dk_rs, dv_rs;
+  int B, H, N;
+  float alpha, inv_n;
+  int max_attn_len, contextual_seq_len;
+  int blocks_per_seq;  // grid = blocks_per_seq * B * H
+};
+
+struct SeqCtx {
+  int64_t start;
+  int L, b, h, blk;
+};
+__device__ __forceinline__ SeqCtx seq_ctx(const AttnParams& p, bool reverse) {
+  SeqCtx c;
+  const int BH = p.B * p.H;
+  const int slot = blockIdx.x / BH;
+  const int bh = blockIdx.x - slot * BH;
+  c.b = bh / p.H;
+  c.h = bh - c.b * p.H;
+  c.blk = reverse ? p.blocks_per_seq - 1 - slot : slot;
+  c.start = p.seq_offsets[c.b];
+  c.L = min((int)(p.seq_offsets[c.b + 1] - c.start), p.N);
+  return c;
+}
+__device__ __forceinline__ MaskCtx mask_ctx(const AttnParams& p, const SeqCtx& c) {
+  MaskCtx m;
+  m.L = c.L;
+  m.targets = p.num_targets != nullptr;
+  m.nt = m.targets ? p.num_targets[c.b] : 0;
+  m.ctx = p.contextual_seq_len;
+  m.max_attn = p.max_attn_len;
+  return m;
+}
+
+// =====================================================================
+// Forward.  Block = 128 query rows (32 per wave), key tiles of 64.
+// =====================================================================
+template <int D, bool FP8>
+struct FwdCfg {
+  static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
+  static constexpr int ES = FP8 ? 1 : 2;
+  using KTile = CopyTile<BN, D, ES>;
+  using VTile = TransTile<BN, D, FP8>;
+  static constexpr int K_OFF = 0;
+  static constexpr int VT_OFF = K_OFF + BN * KTile::PITCH;
+  static constexpr int SK_OFF = VT_OFF + D * VTile::PITCH;
+  static constexpr int BUF = SK_OFF + (FP8 ? BN * 4 : 0);
+  static constexpr int LDS = 2 * BUF;
+};
+
+template <int D, bool FP8, bool GENERIC>
+__global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
+  using C = FwdCfg<D, FP8>;
+  static_assert(!FP8 || D == 128, "e4m3 path is specialised for D = 128");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const SeqCtx sc = seq_ctx(p, /*reverse=*/true);
+  const int L = sc.L, h = sc.h;
+  const int m0 = sc.blk * C::BM;
+  if (m0 >= L) return;
+  const MaskCtx mc = mask_ctx(p, sc);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int mw0 = m0 + wave * 32;
+  const bool wave_active = mw0 < L;
+
+  const int64_t qrs = p.q_rs * C::ES, krs = p.k_rs * C::ES, vrs = p.v_rs * C::ES;
+  const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES;
+  const float* skb = FP8 ? p.k_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+  const float* svb = FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+
+  // Q fragments (B operand of S^T = K.Q^T): lane holds query mw0+16qt+li.
+  u32x4 qf[2][C::KS];
+  i32x8 qf8[2];
+  float cq[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int row = mw0 + qt * 16 + li;
+    const bool ok = row < L;
+    const uint8_t* src = qb + (int64_t)row * qrs;
+    cq[qt] = -p.alpha * kLog2e;
+    if constexpr (FP8) {
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      float s = 0.f;
+      if (ok) {
+        lo = *(const u32x4*)(src + 32 * g);
+        hi = *(const u32x4*)(src + 32 * g + 16);
+        s = p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
+      }
+      qf8[qt] = cat8(lo, hi);
+      cq[qt] *= s;
+    } else {
+#pragma unroll
+      for (int st = 0; st < C::KS; ++st) {
+        qf[qt][st] = u32x4{0u, 0u, 0u, 0u};
+        if (ok) qf[qt][st] = *(const u32x4*)(src + (32 * st + 8 * g) * 2);
+      }
+    }
+  }
+
+  f32x4 o[2][C::DT];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) o[qt][dt] = zero4();
+
+  int n_end = min(m0 + C::BM, L);
+  if (GENERIC && m0 < p.contextual_seq_len) n_end = L;
+  const int ntiles = (n_end + C::BN - 1) / C::BN;
+
+  typename C::KTile kt_ld;
+  typename C::VTile vt_ld;
+  ScaleTile<C::BN> sk_ld;
+  auto load = [&](int n0) {
+    kt_ld.load(kb, krs, n0, L);
+    vt_ld.load(vb, vrs, svb, p.s_rs, n0, L);
+    if constexpr (FP8) sk_ld.load(skb, p.s_rs, n0, L);
+  };
+  auto store = [&](uint8_t* buf) {
+    kt_ld.store(buf + C::K_OFF);
+    vt_ld.store(buf + C::VT_OFF);
+    if constexpr (FP8) sk_ld.store(buf + C::SK_OFF);
+  };
+
+  load(0);
+  store(smem);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = t * C::BN;
+    const uint8_t* buf = smem + (t & 1) * C::BUF;
+    if (t + 1 < ntiles) load(n0 + C::BN);
+
+    if (wave_active && (GENERIC || n0 <= mw0 + 31)) {
+      const bool need_mask = GENERIC || (n0 + C::BN - 1 > mw0);
+      // ---- S^T = K . Q^T : s[kt][qt], keys n0+16kt+4g+r, query mw0+16qt+li
+      f32x4 s[C::KT][2];
+#pragma unroll
+      for (int kt = 0; kt < C::KT; ++kt) {
+        const uint8_t* krow = buf + C::K_OFF + (kt * 16 + li) * C::KTile::PITCH;
+        if constexpr (FP8) {
+          i32x8 a = cat8(lds_ld128(krow + 32 * g), lds_ld128(krow + 32 * g + 16));
+          s[kt][0] = mfma_fp8(a, qf8[0], zero4());
+          s[kt][1] = mfma_fp8(a, qf8[1], zero4());
+        } else {
+          s[kt][0] = zero4();
+          s[kt][1] = zero4();
+#pragma unroll
+          for (int st = 0; st < C::KS; ++st) {
+            u32x4 a = lds_ld128(krow + (32 * st + 8 * g) * 2);
+            s[kt][0] = mfma_bf16(a, qf[0][st], s[kt][0]);
+            s[kt][1] = mfma_bf16(a, qf[1][st], s[kt][1]);
+          }
+        }
+      }
+      // ---- SiLU epilogue on the accumulators, packed into P (A operand)
+      u32x4 pa[2][C::BN / 32];
+#pragma unroll
+      for (int kt = 0; kt < C::KT; ++kt) {
+        f32x4 skv = {1.f, 1.f, 1.f, 1.f};
+        if constexpr (FP8) skv = lds_ldf4(buf + C::SK_OFF + (kt * 16 + 4 * g) * 4);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          float pv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = s[kt][qt][r] * cq[qt];
+            if constexpr (FP8) t *= skv[r];
+            float val = t * sig_of_t(t);
+            if (need_mask) {
+              const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
+              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+              val = ok ? val : 0.f;
+            }
+            pv[r] = val;
+          }
+          pa[qt][kt >> 1][(kt & 1) * 2 + 0] = pack_bf16(pv[0], pv[1]);
+          pa[qt][kt >> 1][(kt & 1) * 2 + 1] = pack_bf16(pv[2], pv[3]);
+        }
+      }
+      // ---- O += P . V
+#pragma unroll
+      for (int c = 0; c < C::BN / 32; ++c) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          u32x4 bv = lds_ld128(buf + C::VT_OFF + (dt * 16 + li) * C::VTile::PITCH + (32 * c + 8 * g) * 2);
+          o[0][dt] = mfma_bf16(pa[0][c], bv, o[0][dt]);
+          o[1][dt] = mfma_bf16(pa[1][c], bv, o[1][dt]);
+        }
+      }
+    }
+
+    if (t + 1 < ntiles) store(smem + ((t + 1) & 1) * C::BUF);
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+  const float fin = -kLn2 * p.inv_n;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = mw0 + qt * 16 + 4 * g + r;
+      if (row < L) {
+        uint16_t* dst = p.out + (sc.start + row) * p.o_rs + (int64_t)h * D + li;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) dst[dt * 16] = to_bf16(o[qt][dt][r] * fin);
+      }
+    }
+  }
+}
+
+// =====================================================================
+// Backward dQ.  Block = 128 query rows (32 per wave), key tiles of 64.
+//   S^T = K.Q^T, dP^T = V.dO^T, dS = dP*sig*(1 + x(1-sig)), dQ += dS.K
+// =====================================================================
+template <int D, bool FP8>
+struct DqCfg {
+  static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
+  static constexpr int ES = FP8 ? 1 : 2;
+  using KTile = CopyTile<BN, D, ES>;              // A operand of S^T
+  using VTileB = CopyTile<BN, D, 2>;              // A operand of dP^T (bf16 inputs)
+  using VTileF = DeqTile<BN, D>;                  // A operand of dP^T (e4m3 inputs)
+  using KtTile = TransTile<BN, D, FP8>;           // B operand of dQ
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = K_OFF + BN * KTile::PITCH;
+  static constexpr int KT_OFF = V_OFF + BN * (D * 2 + 16);
+  static constexpr int SK_OFF = KT_OFF + D * KtTile::PITCH;
+  static constexpr int BUF = SK_OFF + (FP8 ? BN * 4 : 0);
+  static constexpr int LDS = 2 * BUF;
+};
+
+template <int D, bool FP8, bool GENERIC>
+__global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dq_kernel(AttnParams p) {
+  using C = DqCfg<D, FP8>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const SeqCtx sc = seq_ctx(p, /*reverse=*/true);
+  const int L = sc.L, h = sc.h;
+  const int m0 = sc.blk * C::BM;
+  if (m0 >= L) return;
+  const MaskCtx mc = mask_ctx(p, sc);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int mw0 = m0 + wave * 32;
+  const bool wave_active = mw0 < L;
+
+  const int64_t qrs = p.q_rs * C::ES, krs = p.k_rs * C::ES, vrs = p.v_rs * C::ES, dors = p.do_rs * 2;
+  const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* dob = p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2;
+  const float* skb = FP8 ? p.k_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+  const float* svb = FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+
+  u32x4 qf[2][C::KS];
+  i32x8 qf8[2];
+  u32x4 dof[2][C::KS];
+  float cq[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int row = mw0 + qt * 16 + li;
+    const bool ok = row < L;
+    const uint8_t* src = qb + (int64_t)row * qrs;
+    const uint8_t* dsrc = dob + (int64_t)row * dors;
+    cq[qt] = -p.alpha * kLog2e;
+    if constexpr (FP8) {
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      float s = 0.f;
+      if (ok) {
+        lo = *(const u32x4*)(src + 32 * g);
+        hi = *(const u32x4*)(src + 32 * g + 16);
+        s = p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
+      }
+      qf8[qt] = cat8(lo, hi);
+      cq[qt] *= s;
+    } else {
+#pragma unroll
+      for (int st = 0; st < C::KS; ++st) {
+        qf[qt][st] = u32x4{0u, 0u, 0u, 0u};
+        if (ok) qf[qt][st] = *(const u32x4*)(src + (32 * st + 8 * g) * 2);
+      }
+    }
+#pragma unroll
+    for (int st = 0; st < C::KS; ++st) {
+      dof[qt][st] = u32x4{0u, 0u, 0u, 0u};
+      if (ok) dof[qt][st] = *(const u32x4*)(dsrc + (32 * st + 8 * g) * 2);
+    }
+  }
+
+  f32x4 acc[2][C::DT];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) acc[qt][dt] = zero4();
+
+  int n_end = min(m0 + C::BM, L);
+  if (GENERIC && m0 < p.contextual_seq_len) n_end = L;
+  const int ntiles = (n_end + C::BN - 1) / C::BN;
+
+  typename C::KTile k_ld;
+  typename C::VTileB vb_ld;
+  typename C::VTileF vf_ld;
+  typename C::KtTile kt_ld;
+  ScaleTile<C::BN> sk_ld;
+  auto load = [&](int n0) {
+    k_ld.load(kb, krs, n0, L);
+    if constexpr (FP8) {
+      vf_ld.load(vb, vrs, svb, p.s_rs, n0, L);
+      sk_ld.load(skb, p.s_rs, n0, L);
+    } else {
+      vb_ld.load(vb, vrs, n0, L);
+    }
+    kt_ld.load(kb, krs, skb, p.s_rs, n0, L);
+  };
+  auto store = [&](uint8_t* buf) {
+    k_ld.store(buf + C::K_OFF);
+    if constexpr (FP8) {
+      vf_ld.store(buf + C::V_OFF);
+      sk_ld.store(buf + C::SK_OFF);
+    } else {
+      vb_ld.store(buf + C::V_OFF);
+    }
+    kt_ld.store(buf + C::KT_OFF);
+  };
+
+  load(0);
+  store(smem);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = t * C::BN;
+    const uint8_t* buf = smem + (t & 1) * C::BUF;
+    if (t + 1 < ntiles) load(n0 + C::BN);
+
+    if (wave_active && (GENERIC || n0 <= mw0 + 31)) {
+      const bool need_mask = GENERIC || (n0 + C::BN - 1 > mw0);
+      f32x4 s[C::KT][2], dp[C::KT][2];
+#pragma unroll
+      for (int kt = 0; kt < C::KT; ++kt) {
+        const uint8_t* krow = buf + C::K_OFF + (kt * 16 + li) * C::KTile::PITCH;
+        const uint8_t* vrow = buf + C::V_OFF + (kt * 16 + li) * (D * 2 + 16);
+        if constexpr (FP8) {
+          i32x8 a = cat8(lds_ld128(krow + 32 * g), lds_ld128(krow + 32 * g + 16));
+          s[kt][0] = mfma_fp8(a, qf8[0], zero4());
+          s[kt][1] = mfma_fp8(a, qf8[1], zero4());
+        } else {
+          s[kt][0] = zero4();
+          s[kt][1] = zero4();
+#pragma unroll
+          for (int st = 0; st < C::KS; ++st) {
+            u32x4 a = lds_ld128(krow + (32 * st + 8 * g) * 2);
+            s[kt][0] = mfma_bf16(a, qf[0][st], s[kt][0]);
+            s[kt][1] = mfma_bf16(a, qf[1][st], s[kt][1]);
+          }
+        }
+        dp[kt][0] = zero4();
+        dp[kt][1] = zero4();
+#pragma unroll
+        for (int st = 0; st < C::KS; ++st) {
+          u32x4 a = lds_ld128(vrow + (32 * st + 8 * g) * 2);
+          dp[kt][0] = mfma_bf16(a, dof[0][st], dp[kt][0]);
+          dp[kt][1] = mfma_bf16(a, dof[1][st], dp[kt][1]);
+        }
+      }
+      u32x4 dsa[2][C::BN / 32];
+#pragma unroll
+      for (int kt = 0; kt < C::KT; ++kt) {
+        f32x4 skv = {1.f, 1.f, 1.f, 1.f};
+        if constexpr (FP8) skv = lds_ldf4(buf + C::SK_OFF + (kt * 16 + 4 * g) * 4);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+          float dsv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = s[kt][qt][r] * cq[qt];
+            if constexpr (FP8) t *= skv[r];
+            const float sg = sig_of_t(t);
+            const float x = -kLn2 * t;
+            float val = dp[kt][qt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+            if (need_mask) {
+              const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
+              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+              val = ok ? val : 0.f;
+            }
+            dsv[r] = val;
+          }
+          dsa[qt][kt >> 1][(kt & 1) * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
+          dsa[qt][kt >> 1][(kt & 1) * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < C::BN / 32; ++c) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          u32x4 bk = lds_ld128(buf + C::KT_OFF + (dt * 16 + li) * C::KtTile::PITCH + (32 * c + 8 * g) * 2);
+          acc[0][dt] = mfma_bf16(dsa[0][c], bk, acc[0][dt]);
+          acc[1][dt] = mfma_bf16(dsa[1][c], bk, acc[1][dt]);
+        }
+      }
+    }
+
+    if (t + 1 < ntiles) store(smem + ((t + 1) & 1) * C::BUF);
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+  const float fin = p.alpha * p.inv_n;
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = mw0 + qt * 16 + 4 * g + r;
+      if (row < L) {
+        uint16_t* dst = p.dq + (sc.start + row) * p.dq_rs + (int64_t)h * D + li;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) dst[dt * 16] = to_bf16(acc[qt][dt][r] * fin);
+      }
+    }
+  }
+}
+
+// =====================================================================
+// Backward dK / dV.  Block = 128 keys (32 per wave), query tiles of 64.
+//   S = Q.K^T, dP = dO.V^T (C fragments: query 4g+r, key li)
+//   dV += P^T.dO, dK += dS^T.Q
+// =====================================================================
+template <int D, bool FP8>
+struct DkvCfg {
+  static constexpr int BN = 128, BMQ = 64, QS = BMQ / 16, DT = D / 16, KS = D / 32;
+  static constexpr int ES = FP8 ? 1 : 2;
+  using QTile = CopyTile<BMQ, D, ES>;          // A operand of S
+  using DoTile = CopyTile<BMQ, D, 2>;          // A operand of dP
+  using QtTile = TransTile<BMQ, D, FP8>;       // B operand of dK
+  using DotTile = TransTile<BMQ, D, false>;    // B operand of dV
+  static constexpr int Q_OFF = 0;
+  static constexpr int DO_OFF = Q_OFF + BMQ * QTile::PITCH;
+  static constexpr int QT_OFF = DO_OFF + BMQ * DoTile::PITCH;
+  static constexpr int DOT_OFF = QT_OFF + D * QtTile::PITCH;
+  static constexpr int SQ_OFF = DOT_OFF + D * DotTile::PITCH;
+  static constexpr int BUF = SQ_OFF + (FP8 ? BMQ * 4 : 0);
+  static constexpr int LDS = 2 * BUF;
+};
+
+template <int D, bool FP8, bool GENERIC>
+__global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dkdv_kernel(AttnParams p) {
+  using C = DkvCfg<D, FP8>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const SeqCtx sc = seq_ctx(p, /*reverse=*/false);
+  const int L = sc.L, h = sc.h;
+  const int n0 = sc.blk * C::BN;
+  if (n0 >= L) return;
+  const MaskCtx mc = mask_ctx(p, sc);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int kw0 = n0 + wave * 32;
+  const bool wave_active = kw0 < L;
+
+  const int64_t qrs = p.q_rs * C::ES, krs = p.k_rs * C::ES, vrs = p.v_rs * C::ES, dors = p.do_rs * 2;
+  const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES;
+  const uint8_t* dob = p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2;
+  const float* sqb = FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+
+  // K and V fragments (B operands of S and dP): lane holds key kw0+16kt+li.
+  u32x4 kf[2][C::KS];
+  i32x8 kf8[2];
+  u32x4 vf[2][C::KS];
+  float ck[2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int row = kw0 + kt * 16 + li;
+    const bool ok = row < L;
+    const uint8_t* ksrc = kb + (int64_t)row * krs;
+    const uint8_t* vsrc = vb + (int64_t)row * vrs;
+    ck[kt] = -p.alpha * kLog2e;
+    if constexpr (FP8) {
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      float sk = 0.f, sv = 0.f;
+      if (ok) {
+        lo = *(const u32x4*)(ksrc + 32 * g);
+        hi = *(const u32x4*)(ksrc + 32 * g + 16);
+        sk = p.k_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
+        sv = p.v_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
+      }
+      kf8[kt] = cat8(lo, hi);
+      ck[kt] *= sk;
+#pragma unroll
+      for (int st = 0; st < C::KS; ++st) {
+        u32x2 w = {0u, 0u};
+        if (ok) w = *(const u32x2*)(vsrc + 32 * st + 8 * g);
+        u32x2 a = fp8x4_to_bf16x4(w[0], sv), b = fp8x4_to_bf16x4(w[1], sv);
+        vf[kt][st] = u32x4{a[0], a[1], b[0], b[1]};
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < C::KS; ++st) {
+        kf[kt][st] = u32x4{0u, 0u, 0u, 0u};
+        vf[kt][st] = u32x4{0u, 0u, 0u, 0u};
+        if (ok) {
+          kf[kt][st] = *(const u32x4*)(ksrc + (32 * st + 8 * g) * 2);
+          vf[kt][st] = *(const u32x4*)(vsrc + (32 * st + 8 * g) * 2);
+        }
+      }
+    }
+  }
+
+  f32x4 dk[2][C::DT], dv[2][C::DT];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+      dk[kt][dt] = zero4();
+      dv[kt][dt] = zero4();
+    }
+
+  const int m_begin = GENERIC ? 0 : n0;
+  const int ntiles = (L - m_begin + C::BMQ - 1) / C::BMQ;
+
+  typename C::QTile q_ld;
+  typename C::DoTile do_ld;
+  typename C::QtTile qt_ld;
+  typename C::DotTile dot_ld;
+  ScaleTile<C::BMQ> sq_ld;
+  auto load = [&](int m0) {
+    q_ld.load(qb, qrs, m0, L);
+    do_ld.load(dob, dors, m0, L);
+    qt_ld.load(qb, qrs, sqb, p.s_rs, m0, L);
+    dot_ld.load(dob, dors, nullptr, 0, m0, L);
+    if constexpr (FP8) sq_ld.load(sqb, p.s_rs, m0, L);
+  };
+  auto store = [&](uint8_t* buf) {
+    q_ld.store(buf + C::Q_OFF);
+    do_ld.store(buf + C::DO_OFF);
+    qt_ld.store(buf + C::QT_OFF);
+    dot_ld.store(buf + C::DOT_OFF);
+    if constexpr (FP8) sq_ld.store(buf + C::SQ_OFF);
+  };
+
+  load(m_begin);
+  store(smem);
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int m0 = m_begin + t * C::BMQ;
+    const uint8_t* buf = smem + (t & 1) * C::BUF;
+    if (t + 1 < ntiles) load(m0 + C::BMQ);
+
+    if (wave_active && (GENERIC || m0 + C::BMQ - 1 >= kw0)) {
+      const bool need_mask = GENERIC || (m0 <= kw0 + 31);
+      f32x4 s[C::QS][2], dp[C::QS][2];
+#pragma unroll
+      for (int qs = 0; qs < C::QS; ++qs) {
+        const uint8_t* qrow = buf + C::Q_OFF + (qs * 16 + li) * C::QTile::PITCH;
+        const uint8_t* drow = buf + C::DO_OFF + (qs * 16 + li) * C::DoTile::PITCH;
+        if constexpr (FP8) {
+          i32x8 a = cat8(lds_ld128(qrow + 32 * g), lds_ld128(qrow + 32 * g + 16));
+          s[qs][0] = mfma_fp8(a, kf8[0], zero4());
+          s[qs][1] = mfma_fp8(a, kf8[1], zero4());
+        } else {
+          s[qs][0] = zero4();
+          s[qs][1] = zero4();
+#pragma unroll
+          for (int st = 0; st < C::KS; ++st) {
+            u32x4 a = lds_ld128(qrow + (32 * st + 8 * g) * 2);
+            s[qs][0] = mfma_bf16(a, kf[0][st], s[qs][0]);
+            s[qs][1] = mfma_bf16(a, kf[1][st], s[qs][1]);
+          }
+        }
+        dp[qs][0] = zero4();
+        dp[qs][1] = zero4();
+#pragma unroll
+        for (int st = 0; st < C::KS; ++st) {
+          u32x4 a = lds_ld128(drow + (32 * st + 8 * g) * 2);
+          dp[qs][0] = mfma_bf16(a, vf[0][st], dp[qs][0]);
+          dp[qs][1] = mfma_bf16(a, vf[1][st], dp[qs][1]);
+        }
+      }
+      u32x4 pa[2][C::BMQ / 32], dsa[2][C::BMQ / 32];
+#pragma unroll
+      for (int qs = 0; qs < C::QS; ++qs) {
+        f32x4 sqv = {1.f, 1.f, 1.f, 1.f};
+        if constexpr (FP8) sqv = lds_ldf4(buf + C::SQ_OFF + (qs * 16 + 4 * g) * 4);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          float pv[4], dsv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float t = s[qs][kt][r] * ck[kt];
+            if constexpr (FP8) t *= sqv[r];
+            const float sg = sig_of_t(t);
+            const float x = -kLn2 * t;
+            float pval = t * sg;
+            float dval = dp[qs][kt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+            if (need_mask) {
+              const int i = m0 + qs * 16 + 4 * g + r, j = kw0 + kt * 16 + li;
+              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+              pval = ok ? pval : 0.f;
+              dval = ok ? dval : 0.f;
+            }
+            pv[r] = pval;
+            dsv[r] = dval;
+          }
+          pa[kt][qs >> 1][(qs & 1) * 2 + 0] = pack_bf16(pv[0], pv[1]);
+          pa[kt][qs >> 1][(qs & 1) * 2 + 1] = pack_bf16(pv[2], pv[3]);
+          dsa[kt][qs >> 1][(qs & 1) * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
+          dsa[kt][qs >> 1][(qs & 1) * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < C::BMQ / 32; ++c) {
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          u32x4 bdo = lds_ld128(buf + C::DOT_OFF + (dt * 16 + li) * C::DotTile::PITCH + (32 * c + 8 * g) * 2);
+          u32x4 bq = lds_ld128(buf + C::QT_OFF + (dt * 16 + li) * C::QtTile::PITCH + (32 * c + 8 * g) * 2);
+          dv[0][dt] = mfma_bf16(pa[0][c], bdo, dv[0][dt]);
+          dv[1][dt] = mfma_bf16(pa[1][c], bdo, dv[1][dt]);
+          dk[0][dt] = mfma_bf16(dsa[0][c], bq, dk[0][dt]);
+          dk[1][dt] = mfma_bf16(dsa[1][c], bq, dk[1][dt]);
+        }
+      }
+    }
+
+    if (t + 1 < ntiles) store(smem + ((t + 1) & 1) * C::BUF);
+    __syncthreads();
+  }
+
+  if (!wave_active) return;
+  const float fin_v = -kLn2 * p.inv_n;
+  const float fin_k = p.alpha * p.inv_n;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = kw0 + kt * 16 + 4 * g + r;
+      if (row < L) {
+        uint16_t* dstk = p.dk + (sc.start + row) * p.dk_rs + (int64_t)h * D + li;
+        uint16_t* dstv = p.dv + (sc.start + row) * p.dv_rs + (int64_t)h * D + li;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          dstk[dt * 16] = to_bf16(dk[kt][dt][r] * fin_k);
+          dstv[dt * 16] = to_bf16(dv[kt][dt][r] * fin_v);
+        }
+      }
+    }
+  }
+}
+
+// Rows of a sequence beyond max_seq_len are not computed by the kernels (the
+// reference's padded path drops them, so their output is zero); zero them so
+// every output element is written.  Exits at once when every L <= N.
+__global__ void zero_rows_beyond_n(const int64_t* seq_offsets, int N, int width, uint16_t* a, int64_t a_rs,
+                                   uint16_t* b, int64_t b_rs, uint16_t* c, int64_t c_rs) {
+  const int s = blockIdx.y;
+  const int64_t start = seq_offsets[s];
+  const int L = (int)(seq_offsets[s + 1] - start);
+  for (int row = N + blockIdx.x; row < L; row += gridDim.x) {
+    for (int col = threadIdx.x; col < width; col += blockDim.x) {
+      a[(start + row) * a_rs + col] = 0;
+      if (b) b[(start + row) * b_rs + col] = 0;
+      if (c) c[(start + row) * c_rs + col] = 0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- launch
+// Raise the dynamic-LDS limit once per kernel (the forward uses 70 KiB, the
+// dK/dV kernel 140 KiB of the 160 KiB a CU has).
+hipError_t ensure_lds(const void* fn, int lds) {
+  static std::mutex mu;
+  static std::vector<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const void* d : done)
+    if (d == fn) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  if (e == hipSuccess) done.push_back(fn);
+  return e;
+}
+
+hipError_t launch(void (*kernel)(AttnParams), int lds, int grid, AttnParams p, hipStream_t stream) {
+  hipError_t e = ensure_lds((const void*)kernel, lds);
+  if (e != hipSuccess) return e;
+  void* args[] = {&p};
+  return hipLaunchKernel((const void*)kernel, dim3(grid), dim3(kThreads), args, (size_t)lds, stream);
+}
+
+bool check_common(int dtype, int H, int D, int B, int N, int64_t rs_q, int64_t rs_k, int64_t rs_v,
+                  const float* qs, const float* ks, const float* vs, int bias_R, const float* bias) {
+  if (dtype != HSTU_DTYPE_BF16 && dtype != HSTU_DTYPE_FP8_E4M3) return false;
+  if (B < 0 || H <= 0 || N <= 0) return false;
+  if (rs_q < (int64_t)H * D || rs_k < (int64_t)H * D || rs_v < (int64_t)H * D) return false;
+  if (dtype == HSTU_DTYPE_FP8_E4M3 && (!qs || !ks || !vs)) return false;
+  if (bias != nullptr) return false;  // relative bias: not in this build yet
+  (void)bias_R;
+  return true;
+}
+
+int row_alignment_ok(int dtype, int64_t rs, const void* ptr) {
+  // 16-byte vector loads need every row (and the head offset) 16-byte aligned.
+  const int es = dtype == HSTU_DTYPE_BF16 ? 2 : 1;
+  return ((rs * es) % 16 == 0) && (((uintptr_t)ptr) % 16 == 0);
+}
+
+}  // namespace
+
+extern "C" const char* hstu_version(void) {
+  return "hstu-mi355x 0.1 (gfx950: bf16 16x16x32 / e4m3 16x16x128 MFMA)";
+}
+
+extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void* v, int64_t q_row_stride,
+                             int64_t k_row_stride, int64_t v_row_stride, const float* q_scale,
+                             const float* k_scale, const float* v_scale, int64_t scale_row_stride,
+                             int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
+                             int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len,
+                             int contextual_seq_len, const float* attn_bias, int bias_R, void* out,
+                             int64_t out_row_stride, hipStream_t stream) {
+  if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
+                    v_scale, bias_R, attn_bias))
+    return HSTU_E_BAD_ARG;
+  if (!(D == 128 || (D == 64 && dtype == HSTU_DTYPE_BF16))) return HSTU_E_UNSUPPORTED;
+  if (!row_alignment_ok(dtype, q_row_stride, q) || !row_alignment_ok(dtype, k_row_stride, k) ||
+      !row_alignment_ok(dtype, v_row_stride, v))
+    return HSTU_E_UNSUPPORTED;
+  if (B == 0) return 0;
+  AttnParams p{};
+  p.q = (const uint8_t*)q;
+  p.k = (const uint8_t*)k;
+  p.v = (const uint8_t*)v;
+  p.q_rs = q_row_stride;
+  p.k_rs = k_row_stride;
+  p.v_rs = v_row_stride;
+  p.q_scale = q_scale;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.s_rs = scale_row_stride;
+  p.s_hs = scale_head_stride;
+  p.seq_offsets = seq_offsets;
+  p.num_targets = num_targets;
+  p.out = (uint16_t*)out;
+  p.o_rs = out_row_stride;
+  p.B = B;
+  p.H = H;
+  p.N = max_seq_len;
+  p.alpha = alpha;
+  p.inv_n = 1.0f / (float)max_seq_len;
+  p.max_attn_len = max_attn_len;
+  p.contextual_seq_len = contextual_seq_len;
+  const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
+  p.blocks_per_seq = (max_seq_len + 127) / 128;
+  const int grid = p.blocks_per_seq * B * H;
+#define HSTU_FWD(DD, F8, G) launch(hstu_fwd_kernel<DD, F8, G>, FwdCfg<DD, F8>::LDS, grid, p, stream)
+  hipError_t e;
+  if (dtype == HSTU_DTYPE_FP8_E4M3) {
+    e = generic ? HSTU_FWD(128, true, true) : HSTU_FWD(128, true, false);
+  } else if (D == 128) {
+    e = generic ? HSTU_FWD(128, false, true) : HSTU_FWD(128, false, false);
+  } else {
+    e = generic ? HSTU_FWD(64, false, true) : HSTU_FWD(64, false, false);
+  }
+#undef HSTU_FWD
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
+                     p.out, p.o_rs, (uint16_t*)nullptr, (int64_t)0, (uint16_t*)nullptr, (int64_t)0);
+  return (int)hipGetLastError();
+}
+
+extern "C" int hstu_attn_bwd(int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
+                             const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                             const float* q_scale, const float* k_scale, const float* v_scale,
+                             int64_t scale_row_stride, int64_t scale_head_stride, const int64_t* seq_offsets,
+                             int B, int H, int D, int max_seq_len, float alpha, const int32_t* num_targets,
+                             int max_attn_len, int contextual_seq_len, const float* attn_bias, int bias_R,
+                             void* dq, void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride,
+                             int64_t dv_row_stride, float* dbias, hipStream_t stream) {
+  if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
+                    v_scale, bias_R, attn_bias) ||
+      dbias != nullptr)
+    return HSTU_E_BAD_ARG;
+  if (!(D == 128 || (D == 64 && dtype == HSTU_DTYPE_BF16))) return HSTU_E_UNSUPPORTED;
+  if (!row_alignment_ok(dtype, q_row_stride, q) || !row_alignment_ok(dtype, k_row_stride, k) ||
+      !row_alignment_ok(dtype, v_row_stride, v) || !row_alignment_ok(HSTU_DTYPE_BF16, dout_row_stride, dout))
+    return HSTU_E_UNSUPPORTED;
+  if (dq_row_stride < (int64_t)H * D || dk_row_stride < (int64_t)H * D || dv_row_stride < (int64_t)H * D)
+    return HSTU_E_BAD_ARG;
+  if (B == 0) return 0;
+  AttnParams p{};
+  p.q = (const uint8_t*)q;
+  p.k = (const uint8_t*)k;
+  p.v = (const uint8_t*)v;
+  p.dout = (const uint8_t*)dout;
+  p.q_rs = q_row_stride;
+  p.k_rs = k_row_stride;
+  p.v_rs = v_row_stride;
+  p.do_rs = dout_row_stride;
+  p.q_scale = q_scale;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.s_rs = scale_row_stride;
+  p.s_hs = scale_head_stride;
+  p.seq_offsets = seq_offsets;
+  p.num_targets = num_targets;
+  p.dq = (uint16_t*)dq;
+  p.dk = (uint16_t*)dk;
+  p.dv = (uint16_t*)dv;
+  p.dq_rs = dq_row_stride;
+  p.dk_rs = dk_row_stride;
+  p.dv_rs = dv_row_stride;
+  p.B = B;
+  p.H = H;
+  p.N = max_seq_len;
+  p.alpha = alpha;
+  p.inv_n = 1.0f / (float)max_seq_len;
+  p.max_attn_len = max_attn_len;
+  p.contextual_seq_len = contextual_seq_len;
+  const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
+  hipError_t e;
+  // dK / dV: 128-key blocks, longest key range first.
+  {
+    AttnParams pk = p;
+    pk.blocks_per_seq = (max_seq_len + 127) / 128;
+    const int grid = pk.blocks_per_seq * B * H;
+#define HSTU_DKV(DD, F8, G) launch(hstu_bwd_dkdv_kernel<DD, F8, G>, DkvCfg<DD, F8>::LDS, grid, pk, stream)
+    if (dtype == HSTU_DTYPE_FP8_E4M3) {
+      e = generic ? HSTU_DKV(128, true, true) : HSTU_DKV(128, true, false);
+    } else if (D == 128) {
+      e = generic ? HSTU_DKV(128, false, true) : HSTU_DKV(128, false, false);
+    } else {
+      e = generic ? HSTU_DKV(64, false, true) : HSTU_DKV(64, false, false);
+    }
+#undef HSTU_DKV
+    if (e != hipSuccess) return (int)e;
+  }
+  // dQ: 128-query blocks, longest key range first.
+  {
+    AttnParams pq = p;
+    pq.blocks_per_seq = (max_seq_len + 127) / 128;
+    const int grid = pq.blocks_per_seq * B * H;
+#define HSTU_DQ(DD, F8, G) launch(hstu_bwd_dq_kernel<DD, F8, G>, DqCfg<DD, F8>::LDS, grid, pq, stream)
+    if (dtype == HSTU_DTYPE_FP8_E4M3) {
+      e = generic ? HSTU_DQ(128, true, true) : HSTU_DQ(128, true, false);
+    } else if (D == 128) {
+      e = generic ? HSTU_DQ(128, false, true) : HSTU_DQ(128, false, false);
+    } else {
+      e = generic ? HSTU_DQ(64, false, true) : HSTU_DQ(64, false, false);
+    }
+#undef HSTU_DQ
+    if (e != hipSuccess) return (int)e;
+  }
+  hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
+                     p.dq, p.dq_rs, p.dk, p.dk_rs, p.dv, p.dv_rs);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,15 @@
+"""MI355X-native (gfx950) HSTU hot path: jagged causal SiLU attention (bf16 and
+FP8 e4m3) and the FP8 projections around it, behind the reference's op
+signatures.  Kernels live in ``libhstu_mi355x.so`` (C ABI, include/hstu_mi355x.h)."""
+
+from ._lib import HstuKernelError, HstuUnavailableError, load_library  # noqa: F401
+from .hstu_attention import (  # noqa: F401
+    HammerKernel,
+    hstu_mha,
+    triton_hstu_attention_bwd,
+    triton_hstu_attention_fwd,
+    triton_hstu_mha,
+    try_hstu_attention_bwd,
+    try_hstu_attention_fwd,
+    unsupported_shape_reason,
+)

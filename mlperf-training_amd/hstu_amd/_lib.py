@@ -1,0 +1,119 @@
+"""Loader for the C-ABI library ``libhstu_mi355x.so`` (declared in
+``include/hstu_mi355x.h``).
+
+The library is built ahead of time (``mlperf-training_amd/build.py``) and
+bound with ctypes, the same FFI the reference uses for its native kernels
+(``ops/hip/k512_fp8_gemm.py:260-270``).  There is no fallback: if the library
+is missing or does not load, every entry point raises ``HstuUnavailableError``
+(mirroring ``FlyDSLUnavailableError``, ``ops/flydsl/hstu_flydsl_mha.py:183-188``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+LIB_NAME = "libhstu_mi355x.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+
+HSTU_DTYPE_BF16 = 0
+HSTU_DTYPE_FP8_E4M3 = 1
+HSTU_E_BAD_ARG = -1
+HSTU_E_UNSUPPORTED = -2
+
+# Every extern "C" symbol include/hstu_mi355x.h declares.
+EXPORTED_SYMBOLS = (
+    "hstu_version",
+    "hstu_attn_fwd",
+    "hstu_attn_bwd",
+    "hstu_fp8_gemm_rowcol",
+    "hstu_quantize_e4m3_rows",
+)
+
+
+class HstuUnavailableError(RuntimeError):
+    """The native library cannot run on this host (missing build, no GPU)."""
+
+
+class HstuKernelError(RuntimeError):
+    """A C-ABI entry point returned a non-zero status."""
+
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+
+_SIGNATURES = {
+    "hstu_version": (ctypes.c_char_p, []),
+    "hstu_attn_fwd": (
+        _i32,
+        [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
+         _f32, _vp, _i32, _i32, _vp, _i32, _vp, _i64, _vp],
+    ),
+    "hstu_attn_bwd": (
+        _i32,
+        [_i32, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32,
+         _i32, _f32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp],
+    ),
+    "hstu_fp8_gemm_rowcol": (
+        _i32,
+        [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "hstu_quantize_e4m3_rows": (
+        _i32,
+        [_vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _vp],
+    ),
+}
+
+
+def load_library(path: Optional[Path] = None) -> ctypes.CDLL:
+    """Load (once per process) and return the bound library."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise HstuUnavailableError(
+                f"{p} is not built; run `python mlperf-training_amd/build.py` "
+                "(or __graft_entry__.build()) first.  There is no fallback path."
+            )
+        try:
+            lib = ctypes.CDLL(str(p))
+        except OSError as e:  # pragma: no cover - depends on host
+            raise HstuUnavailableError(f"cannot load {p}: {e}") from e
+        _lib = lib
+        return lib
+
+
+_bound = {}
+
+
+def fn(name: str):
+    """The typed ctypes function for one exported symbol."""
+    f = _bound.get(name)
+    if f is None:
+        f = getattr(load_library(), name)
+        res, args = _SIGNATURES[name]
+        f.restype = res
+        f.argtypes = args
+        _bound[name] = f
+    return f
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = {HSTU_E_BAD_ARG: "bad argument", HSTU_E_UNSUPPORTED: "unsupported shape/layout"}.get(
+            status, f"hipError {status}")
+        raise HstuKernelError(f"{what} failed: {msg}")
+
+
+def ptr(t) -> Optional[int]:
+    """Device address of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,446 @@
+"""CPU oracle for the HSTU jagged attention hot path and its FP8 projections.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this file:
+only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg use it, and only as the checker (or, for the baseline, as the timed CPU
+restatement of the reference's PyTorch path).
+
+Every function restates the reference algorithm on the CPU in float32 or
+float64 torch (no fbgemm, no GPU) and cites the reference file:line it follows.
+Reference paths are relative to
+``recommendation_v4/hstu/generative_recommenders/``.
+
+Pinning (how each function is checked independently of its own formula; the
+checks live in ``tests/test_oracle.py``):
+
+* ``valid_attn_mask``            -- brute-force per-element restatement of the
+  reference's id arithmetic on tiny shapes, plus closed forms: plain causal is
+  the lower triangle incl. the diagonal; num_targets<=1 equals plain causal.
+* ``hstu_mha_dense``             -- per-sequence float64 loop
+  (``hstu_mha_loop``), closed forms (L=1, alpha=0, linearity in v, causal
+  prefix invariance, jagged independence, 1/N scaling).
+* ``hstu_mha_bwd``               -- torch.autograd on the float64 dense
+  restatement and ``torch.autograd.gradcheck``.
+* ``rel_bias_index`` / bias path -- brute force; with ``attn_bias=None`` the
+  result equals the reference path exactly.  The bias itself has NO reference
+  counterpart (the reference has no attention bias): it is this build's own
+  extension, defined here and pinned only by brute force.
+* ``quantize_e4m3_*``            -- torch's ``Tensor.to(torch.float8_e4m3fn)``
+  (a library routine) plus the closed form scale = amax/448.
+* ``fp8_rowcol_gemm``            -- float64 matmul of the dequantized operands.
+* ``jagged_to_padded`` / ``padded_to_jagged`` -- restatements of FBGEMM
+  ``jagged_to_padded_dense`` / ``dense_to_jagged`` (FBGEMM-GPU commit
+  10b775730212923f65f7b78f79b6a01d80cf3c29, pinned in the reference
+  Dockerfile:30-31).  Pure data movement; pinned by a round trip and by
+  explicit per-element copies.  The reference holds no test vectors for them:
+  parity unpinned beyond these properties.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Tuple
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+E4M3_MAX = 448.0
+
+
+# --------------------------------------------------------------------------
+# jagged <-> padded (FBGEMM restatements)
+# --------------------------------------------------------------------------
+def jagged_to_padded(values: torch.Tensor, seq_offsets: torch.Tensor, N: int) -> torch.Tensor:
+    """[T, F] jagged -> [B, N, F] zero padded; rows beyond N are dropped.
+
+    Restates ``torch.ops.fbgemm.jagged_to_padded_dense`` as used in
+    ``ops/pytorch/pt_hstu_attention.py:96-125``.
+    """
+    offs = [int(x) for x in seq_offsets.tolist()]
+    B = len(offs) - 1
+    out = values.new_zeros((B, N) + tuple(values.shape[1:]))
+    for b in range(B):
+        n = min(offs[b + 1] - offs[b], N)
+        if n > 0:
+            out[b, :n] = values[offs[b]: offs[b] + n]
+    return out
+
+
+def padded_to_jagged(dense: torch.Tensor, seq_offsets: torch.Tensor, T: int) -> torch.Tensor:
+    """[B, N, F] -> [T, F]; rows of a sequence beyond N come back as zero.
+
+    Restates ``torch.ops.fbgemm.dense_to_jagged`` (``pt_hstu_attention.py:183-187``).
+    """
+    offs = [int(x) for x in seq_offsets.tolist()]
+    N = dense.shape[1]
+    out = dense.new_zeros((T,) + tuple(dense.shape[2:]))
+    for b in range(len(offs) - 1):
+        n = min(offs[b + 1] - offs[b], N)
+        if n > 0:
+            out[offs[b]: offs[b] + n] = dense[b, :n]
+    return out
+
+
+# --------------------------------------------------------------------------
+# mask
+# --------------------------------------------------------------------------
+def valid_attn_mask(
+    N: int,
+    seq_lengths: torch.Tensor,
+    num_targets: Optional[torch.Tensor] = None,
+    max_attn_len: int = 0,
+    contextual_seq_len: int = 0,
+    min_full_attn_seq_len: int = 0,
+    causal: bool = True,
+) -> torch.Tensor:
+    """Boolean [B or 1, N, N] mask, restating ``_get_valid_attn_mask``
+    (``ops/pytorch/pt_hstu_attention.py:32-84``) step by step."""
+    ids = torch.arange(0, N).view(1, N)
+    max_ids = seq_lengths.view(-1, 1, 1)
+    if contextual_seq_len > 0:
+        ids = torch.clamp(ids - contextual_seq_len + 1, min=0)
+        max_ids = max_ids - contextual_seq_len + 1
+    if num_targets is not None:
+        max_ids = max_ids - num_targets.view(-1, 1, 1)
+        ids = torch.minimum(ids, max_ids)  # clamp(ids, max=max_ids), per batch
+        row_ids = ids.view(-1, N, 1).expand(-1, N, N)
+        col_ids = ids.view(-1, 1, N).expand(-1, N, N)
+    else:
+        row_ids = ids.view(N, 1).expand(N, N).reshape(1, N, N)
+        col_ids = ids.view(1, N).expand(N, N).reshape(1, N, N)
+    dist = row_ids - col_ids
+    valid = torch.eye(N, dtype=torch.bool).view(1, N, N)
+    if not causal:
+        dist = torch.where(dist > 0, dist, -dist)
+    valid = valid | (dist > 0)
+    if max_attn_len > 0:
+        if min_full_attn_seq_len > 0:
+            valid = valid & ((dist <= max_attn_len) | (row_ids >= max_ids - min_full_attn_seq_len))
+        else:
+            valid = valid & (dist <= max_attn_len)
+    if contextual_seq_len > 0:
+        valid = valid | ((row_ids == 0) & (col_ids < max_ids))
+    return valid
+
+
+def valid_pair(i: int, j: int, L: int, nt: Optional[int], max_attn_len: int, ctx: int) -> bool:
+    """Scalar restatement of the same predicate for one (row i, col j) of a
+    sequence of length L (``triton_hstu_attention.py:461-497`` spells the
+    identical arithmetic per tile).  Used by the brute-force loop."""
+    max_ids = L
+    ii, jj = i, j
+    if ctx > 0:
+        ii = max(i - ctx + 1, 0)
+        jj = max(j - ctx + 1, 0)
+        max_ids = L - ctx + 1
+    if nt is not None:
+        max_ids -= nt
+        ii = min(ii, max_ids)
+        jj = min(jj, max_ids)
+    dist = ii - jj
+    v = (i == j) or dist > 0
+    if max_attn_len > 0:
+        v = v and dist <= max_attn_len
+    if ctx > 0:
+        v = v or (ii == 0 and jj < max_ids)
+    return v
+
+
+# --------------------------------------------------------------------------
+# relative-position bias (this build's extension; no reference counterpart)
+# --------------------------------------------------------------------------
+def rel_bias_index(i: torch.Tensor, j: torch.Tensor, R: int) -> torch.Tensor:
+    """Index into a [H, 2R-1] table for offset i-j, clamped to +-(R-1)."""
+    return torch.clamp(i - j, -(R - 1), R - 1) + (R - 1)
+
+
+def dense_bias(attn_bias: torch.Tensor, N: int) -> torch.Tensor:
+    """[H, 2R-1] table -> [H, N, N] additive score bias."""
+    R = (attn_bias.shape[1] + 1) // 2
+    ar = torch.arange(N)
+    idx = rel_bias_index(ar.view(N, 1), ar.view(1, N), R)
+    return attn_bias[:, idx]
+
+
+# --------------------------------------------------------------------------
+# attention forward
+# --------------------------------------------------------------------------
+def hstu_mha_dense(
+    max_seq_len: int,
+    alpha: float,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_offsets: torch.Tensor,
+    num_targets: Optional[torch.Tensor] = None,
+    max_attn_len: int = 0,
+    contextual_seq_len: int = 0,
+    attn_bias: Optional[torch.Tensor] = None,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Padded-dense restatement of ``pytorch_hstu_mha``
+    (``ops/pytorch/pt_hstu_attention.py:129-187``) computed in ``dtype``.
+
+    out[i] = sum_{valid j} silu(alpha * q_i . k_j [+ bias[i-j]]) / N * v_j
+
+    Differentiable (autograd) so it also serves as the backward oracle.
+    """
+    T, H, Dq = q.shape
+    Dv = v.shape[2]
+    N = max_seq_len
+    qp = jagged_to_padded(q.reshape(T, H * Dq).to(dtype), seq_offsets, N).view(-1, N, H, Dq).transpose(1, 2)
+    kp = jagged_to_padded(k.reshape(T, H * Dq).to(dtype), seq_offsets, N).view(-1, N, H, Dq).transpose(1, 2)
+    vp = jagged_to_padded(v.reshape(T, H * Dv).to(dtype), seq_offsets, N).view(-1, N, H, Dv).transpose(1, 2)
+    s = torch.matmul(qp, kp.transpose(-1, -2)) * alpha  # einsum bhxa,bhya->bhxy (:151)
+    if attn_bias is not None:
+        s = s + dense_bias(attn_bias.to(dtype), N).unsqueeze(0)
+    p = F.silu(s) / N  # (:167)
+    lengths = seq_offsets[1:] - seq_offsets[:-1]
+    mask = valid_attn_mask(N, lengths, num_targets, max_attn_len, contextual_seq_len)
+    p = p * mask.unsqueeze(1).to(dtype)  # (:168-179)
+    o = torch.matmul(p, vp)  # einsum bhxd,bhdv->bhxv (:182)
+    return padded_to_jagged(o.transpose(1, 2).reshape(-1, N, H * Dv), seq_offsets, T).view(T, H, Dv)
+
+
+def hstu_mha_loop(
+    max_seq_len: int,
+    alpha: float,
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    seq_offsets: np.ndarray,
+    num_targets: Optional[np.ndarray] = None,
+    max_attn_len: int = 0,
+    contextual_seq_len: int = 0,
+    attn_bias: Optional[np.ndarray] = None,
+) -> np.ndarray:
+    """Brute-force float64 loop over (sequence, head, i, j): the independent
+    pin for ``hstu_mha_dense``.  Small inputs only."""
+    T, H, _ = q.shape
+    Dv = v.shape[2]
+    out = np.zeros((T, H, Dv), dtype=np.float64)
+    N = max_seq_len
+    R = None if attn_bias is None else (attn_bias.shape[1] + 1) // 2
+    for b in range(len(seq_offsets) - 1):
+        s0 = int(seq_offsets[b])
+        L = min(int(seq_offsets[b + 1]) - s0, N)
+        nt = None if num_targets is None else int(num_targets[b])
+        for h in range(H):
+            for i in range(L):
+                acc = np.zeros(Dv)
+                for j in range(L):
+                    if not valid_pair(i, j, L, nt, max_attn_len, contextual_seq_len):
+                        continue
+                    x = alpha * float(np.dot(q[s0 + i, h].astype(np.float64), k[s0 + j, h].astype(np.float64)))
+                    if attn_bias is not None:
+                        x += float(attn_bias[h, max(-(R - 1), min(R - 1, i - j)) + R - 1])
+                    silu = x / (1.0 + math.exp(-x)) if x > -700 else 0.0
+                    acc += (silu / N) * v[s0 + j, h].astype(np.float64)
+                out[s0 + i, h] = acc
+    return out
+
+
+def hstu_mha_bwd(
+    max_seq_len: int,
+    alpha: float,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_offsets: torch.Tensor,
+    dout: torch.Tensor,
+    num_targets: Optional[torch.Tensor] = None,
+    max_attn_len: int = 0,
+    contextual_seq_len: int = 0,
+    attn_bias: Optional[torch.Tensor] = None,
+    dtype: torch.dtype = torch.float64,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """(dq, dk, dv, dbias) by autograd through ``hstu_mha_dense``.
+
+    The reference's backward kernel spells the same gradients in closed form
+    (``ops/triton/triton_hstu_attention.py:2158-2212, 2500``):
+      dv += silu^T . dO ;  dS = (dO . v^T) * sig * (1 + x (1 - sig)) / N ;
+      dk += alpha * dS^T . q ;  dq += alpha * dS . k.
+    ``hstu_mha_bwd_closed_form`` restates that and is pinned against this.
+    """
+    qq = q.detach().to(dtype).requires_grad_(True)
+    kk = k.detach().to(dtype).requires_grad_(True)
+    vv = v.detach().to(dtype).requires_grad_(True)
+    bb = None if attn_bias is None else attn_bias.detach().to(dtype).requires_grad_(True)
+    out = hstu_mha_dense(max_seq_len, alpha, qq, kk, vv, seq_offsets, num_targets,
+                         max_attn_len, contextual_seq_len, bb, dtype=dtype)
+    out.backward(dout.to(dtype))
+    return qq.grad, kk.grad, vv.grad, (None if bb is None else bb.grad)
+
+
+def hstu_mha_bwd_closed_form(
+    max_seq_len: int,
+    alpha: float,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_offsets: torch.Tensor,
+    dout: torch.Tensor,
+    attn_bias: Optional[torch.Tensor] = None,
+    dtype: torch.dtype = torch.float64,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Per-sequence closed-form backward for plain causal masking, following
+    ``triton_hstu_attention.py:2158-2212`` (dv, dqk formula) and ``:2500``
+    (alpha applied to dk at the end).  dbias[h, idx] sums dS over each
+    diagonal offset (this build's bias extension)."""
+    T, H, D = q.shape
+    N = max_seq_len
+    dq = torch.zeros(T, H, D, dtype=dtype)
+    dk = torch.zeros(T, H, D, dtype=dtype)
+    dv = torch.zeros(T, H, v.shape[2], dtype=dtype)
+    db = None if attn_bias is None else torch.zeros_like(attn_bias, dtype=dtype)
+    R = None if attn_bias is None else (attn_bias.shape[1] + 1) // 2
+    offs = [int(x) for x in seq_offsets.tolist()]
+    for b in range(len(offs) - 1):
+        s0, L = offs[b], min(offs[b + 1] - offs[b], N)
+        if L <= 0:
+            continue
+        ar = torch.arange(L)
+        mask = (ar.view(L, 1) >= ar.view(1, L)).to(dtype)
+        for h in range(H):
+            qh = q[s0:s0 + L, h].to(dtype)
+            kh = k[s0:s0 + L, h].to(dtype)
+            vh = v[s0:s0 + L, h].to(dtype)
+            doh = dout[s0:s0 + L, h].to(dtype)
+            x = alpha * qh @ kh.T
+            if attn_bias is not None:
+                idx = rel_bias_index(ar.view(L, 1), ar.view(1, L), R)
+                x = x + attn_bias[h].to(dtype)[idx]
+            sig = torch.sigmoid(x)
+            silu = x * sig / N * mask
+            dv[s0:s0 + L, h] = silu.T @ doh
+            dp = doh @ vh.T
+            ds = dp * sig * (1 + x * (1 - sig)) / N * mask
+            dk[s0:s0 + L, h] = alpha * ds.T @ qh
+            dq[s0:s0 + L, h] = alpha * ds @ kh
+            if db is not None:
+                db[h].index_add_(0, idx.reshape(-1), ds.reshape(-1))
+    return dq, dk, dv, db
+
+
+# --------------------------------------------------------------------------
+# FP8 quantizers (OCP e4m3fn, max 448)
+# --------------------------------------------------------------------------
+def quantize_e4m3_per_tensor(x: torch.Tensor, margin: float = 1.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """scale = amax*margin/448; q = clamp(x/scale, +-448).to(e4m3fn).
+
+    Restates ``calibrated_scale`` + ``quantize_with_scale``
+    (``ops/triton/triton_fp8.py:396-413, 760-781``)."""
+    amax = x.detach().abs().amax().float().clamp_min(1e-12)
+    scale = (amax * margin / E4M3_MAX).reshape(1, 1)
+    q8 = (x.float() / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return q8, scale
+
+
+def quantize_e4m3_rows(x: torch.Tensor, dim: int = -1) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Scale per slice along ``dim`` reduced: scale = amax/448 over ``dim``.
+
+    For [T, H, D] with dim=-1 this is the per-token-per-head quantizer that the
+    FP8 attention config asks for; for [M, K] with dim=1 per-row, with dim=0
+    per-column.  A zero slice gets scale 1/448 (q is all zeros either way)."""
+    amax = x.detach().float().abs().amax(dim=dim, keepdim=True)
+    scale = torch.where(amax > 0, amax / E4M3_MAX, torch.full_like(amax, 1.0 / E4M3_MAX))
+    q8 = (x.float() / scale).clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return q8, scale.squeeze(dim)
+
+
+def dequantize(q8: torch.Tensor, scale: torch.Tensor, dim: int = -1) -> torch.Tensor:
+    return q8.float() * scale.unsqueeze(dim)
+
+
+# --------------------------------------------------------------------------
+# FP8 GEMMs around the attention
+# --------------------------------------------------------------------------
+def fp8_rowcol_gemm(
+    a8: torch.Tensor,
+    a_scale: torch.Tensor,
+    w8: torch.Tensor,
+    w_scale: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    silu_cols: Optional[Tuple[int, int]] = None,
+    residual: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """float64 C = (A8*sa) @ (W8*sw) [+ bias] [+ residual]; SiLU applied to
+    columns [c0, c1) (the U slice; ``ops/hstu_compute.py:140``).
+
+    A8 [M, K] e4m3 with per-row ``a_scale`` [M] (or [1]); W8 [K, N] e4m3 with
+    per-column ``w_scale`` [N] (or [1]).  Generalises the reference's
+    per-tensor ``acc * (sa*sb) + bias`` (``ops/hip/k512_fp8_gemm.cu:13-17``)
+    and the K=1536 residual add-mm (``ops/hip/k1536_fp8_addmm.cu:10-18``)."""
+    a = a8.double() * a_scale.double().reshape(-1, 1)
+    w = w8.double() * w_scale.double().reshape(1, -1)
+    c = a @ w
+    if bias is not None:
+        c = c + bias.double().reshape(1, -1)
+    if silu_cols is not None:
+        c0, c1 = silu_cols
+        c[:, c0:c1] = F.silu(c[:, c0:c1])
+    if residual is not None:
+        c = c + residual.double()
+    return c
+
+
+# --------------------------------------------------------------------------
+# workload generators
+# --------------------------------------------------------------------------
+def lengths_for_config(cfg: int) -> np.ndarray:
+    rng = np.random.default_rng(0)
+    if cfg == 1:
+        return rng.integers(16, 257, 8)
+    if cfg == 2:
+        return rng.integers(128, 1025, 64)
+    if cfg in (3, 4, 5):
+        return rng.zipf(1.2, 128).clip(32, 4096)
+    raise ValueError(cfg)
+
+
+def offsets_from_lengths(lengths) -> torch.Tensor:
+    lengths = torch.as_tensor(np.asarray(lengths), dtype=torch.int64)
+    return torch.cat([torch.zeros(1, dtype=torch.int64), torch.cumsum(lengths, 0)])
+
+
+def causal_pairs(lengths) -> int:
+    """P = sum_b L_b (L_b + 1) / 2, the causal (i, j) pairs per head."""
+    return int(sum(int(l) * (int(l) + 1) // 2 for l in lengths))
+
+
+def attn_flops(lengths, H: int, D: int, fwd: bool = True, bwd: bool = True) -> int:
+    """Causal-effective FLOPs: fwd 4*D*H*P (2 GEMMs), bwd 10*D*H*P (5 GEMMs),
+    matching ``modules/dlrm_hstu.py:541-561``'s 2*3.5*(S^2/2)*H*(dqk+dv)."""
+    P = causal_pairs(lengths)
+    return (4 * D * H * P if fwd else 0) + (10 * D * H * P if bwd else 0)
+
+
+def make_qkv(lengths, H: int, D: int, std: float, seed: int = 0, dtype=torch.float32):
+    T = int(np.sum(lengths))
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(T, H, D, generator=g) * std).to(dtype)
+    k = (torch.randn(T, H, D, generator=g) * std).to(dtype)
+    v = (torch.randn(T, H, D, generator=g) * std).to(dtype)
+    return q, k, v
+
+
+def make_bias(H: int, R: int = 1024, seed: int = 1, std: float = 0.02) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(H, 2 * R - 1, generator=g) * std
+
+
+def snr_db(ref: torch.Tensor, x: torch.Tensor) -> float:
+    """Signal-to-noise in dB, the reference's backend cross-check metric
+    (``ops/flydsl/hstu_flydsl_mha.py:2503-2516``)."""
+    ref = ref.double()
+    err = (x.double() - ref).pow(2).sum()
+    sig = ref.pow(2).sum()
+    if err == 0:
+        return float("inf")
+    return float(10 * torch.log10(sig / err))
+
+
+def rel_l2(ref: torch.Tensor, x: torch.Tensor) -> float:
+    ref = ref.double()
+    return float((x.double() - ref).norm() / ref.norm().clamp_min(1e-30))

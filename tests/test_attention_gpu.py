@@ -1,0 +1,208 @@
+"""GPU parity of the HIP attention kernels against the CPU oracle.
+
+Every test calls the kernels through the C ABI (via the reference-signature
+ops) and compares with ``oracle/hstu_oracle.py`` evaluated in float64 on the
+same (bf16- or e4m3-rounded) inputs.
+
+Tolerances (stated bar):
+* bf16: ``assert_close(rtol=1e-2, atol=1e-2)`` (the BASELINE bar) and, since
+  outputs are small, relative L2 <= 1e-2 as the discriminating check.
+* e4m3 inputs: against fp32/fp64 on the dequantized inputs, relative L2
+  <= 1.5e-2 and max |err| <= 3e-2 * max |ref|.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hstu_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _ops():
+    import hstu_amd
+
+    return hstu_amd
+
+
+def _case(lengths, H, D, std=0.5, seed=0, dtype=torch.bfloat16):
+    q, k, v = orc.make_qkv(lengths, H, D, std, seed=seed)
+    offs = orc.offsets_from_lengths(lengths)
+    return q.to(dtype), k.to(dtype), v.to(dtype), offs
+
+
+def _check_bf16(out, ref, what):
+    out = out.float().cpu()
+    ref = ref.float()
+    torch.testing.assert_close(out, ref, rtol=1e-2, atol=1e-2, msg=what)
+    err = orc.rel_l2(ref, out)
+    assert err <= 1e-2, f"{what}: rel L2 {err:.3e}"
+
+
+LENGTH_CASES = [
+    [1],
+    [5, 17, 64],
+    [221, 169, 139, 81, 90, 25, 34, 19],
+    [128, 256, 1, 300, 0, 77],
+]
+
+
+@pytest.mark.parametrize("lengths", LENGTH_CASES)
+@pytest.mark.parametrize("D", [64, 128])
+def test_fwd_bf16(hip_lib, lengths, D):
+    ops = _ops()
+    H = 2
+    N = max(max(lengths), 1)
+    q, k, v, offs = _case(lengths, H, D)
+    alpha = 1.0 / D ** 0.5
+    out = ops.triton_hstu_mha(N, alpha, q.to(DEV), k.to(DEV), v.to(DEV), offs.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, alpha, q.double(), k.double(), v.double(), offs, dtype=torch.float64)
+    # magnitudes: rescale so the absolute bar is meaningful
+    scale = ref.abs().max().clamp_min(1e-6)
+    _check_bf16(out.float().cpu() / scale, ref / scale, f"fwd bf16 D={D} L={lengths}")
+
+
+@pytest.mark.parametrize("lengths", LENGTH_CASES[1:])
+@pytest.mark.parametrize("D", [64, 128])
+def test_bwd_bf16(hip_lib, lengths, D):
+    ops = _ops()
+    H = 2
+    N = max(lengths)
+    q, k, v, offs = _case(lengths, H, D)
+    g = torch.Generator().manual_seed(7)
+    dout = torch.randn(q.shape, generator=g).to(torch.bfloat16)
+    alpha = 1.0 / D ** 0.5
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = ops.triton_hstu_mha(N, alpha, qd, kd, vd, offs.to(DEV))
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    dq, dk, dv, _ = orc.hstu_mha_bwd(N, alpha, q, k, v, offs, dout)
+    for name, got, ref in (("dq", qd.grad, dq), ("dk", kd.grad, dk), ("dv", vd.grad, dv)):
+        scale = ref.abs().max().clamp_min(1e-6)
+        _check_bf16(got.float().cpu() / scale, ref / scale, f"{name} bf16 D={D} L={lengths}")
+
+
+def test_bwd_deterministic(hip_lib):
+    ops = _ops()
+    lengths = [300, 129, 64]
+    H, D, N = 2, 128, 300
+    q, k, v, offs = _case(lengths, H, D)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    res = []
+    for _ in range(2):
+        dq, dk, dv = (torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+        ops.triton_hstu_attention_bwd(dout, q.to(DEV), k.to(DEV), v.to(DEV), dq, dk, dv, offs.to(DEV), None,
+                                      N, 0.1, 0, 0, None, False, 0)
+        res.append((dq, dk, dv))
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert not torch.isnan(a).any()
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mode", ["targets", "max_attn_len", "contextual", "all"])
+def test_generic_masks(hip_lib, mode):
+    ops = _ops()
+    lengths = [70, 33, 130, 5]
+    H, D = 2, 128
+    N = 130
+    q, k, v, offs = _case(lengths, H, D, seed=4)
+    nt = torch.tensor([3, 1, 20, 2], dtype=torch.int64) if mode in ("targets", "all") else None
+    mal = 17 if mode in ("max_attn_len", "all") else 0
+    ctx = 6 if mode in ("contextual", "all") else 0
+    alpha = 0.2
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = ops.triton_hstu_mha(N, alpha, qd, kd, vd, offs.to(DEV), None if nt is None else nt.to(DEV), mal, ctx)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, alpha, q.double(), k.double(), v.double(), offs, nt, mal, ctx,
+                             dtype=torch.float64)
+    scale = ref.abs().max()
+    _check_bf16(out.detach().float().cpu() / scale, ref / scale, f"fwd {mode}")
+    dq, dk, dv, _ = orc.hstu_mha_bwd(N, alpha, q, k, v, offs, dout, nt, mal, ctx)
+    for name, got, r in (("dq", qd.grad, dq), ("dk", kd.grad, dk), ("dv", vd.grad, dv)):
+        s = r.abs().max()
+        _check_bf16(got.float().cpu() / s, r / s, f"{name} {mode}")
+
+
+def test_strided_uvqk_views(hip_lib):
+    """q/k/v read in place as column slices of a fused [T, 2048] buffer, and
+    dq/dk/dv written into strided views of a fused gradient buffer."""
+    ops = _ops()
+    lengths = [100, 37, 256]
+    H, D = 4, 128
+    T = sum(lengths)
+    N = 256
+    g = torch.Generator().manual_seed(11)
+    uvqk = (torch.randn(T, 4 * H * D, generator=g) * 0.3).to(torch.bfloat16)
+    u, v, q, k = torch.split(uvqk, [H * D] * 4, dim=1)
+    q, k, v = q.view(T, H, D), k.view(T, H, D), v.view(T, H, D)
+    offs = orc.offsets_from_lengths(lengths)
+    ud = uvqk.to(DEV)
+    _, vd, qd, kd = torch.split(ud, [H * D] * 4, dim=1)
+    qd, kd, vd = qd.view(T, H, D), kd.view(T, H, D), vd.view(T, H, D)
+    assert qd.stride(0) == 4 * H * D
+    out = ops.triton_hstu_attention_fwd(N, 0.1, qd, kd, vd, offs.to(DEV), None, 0, 0, None, False, 0)
+    dout = (torch.randn(T, H, D, generator=g)).to(torch.bfloat16)
+    duvqk = torch.full((T, 4 * H * D), 7.0, dtype=torch.bfloat16, device=DEV)
+    du, dvv, dqq, dkk = torch.split(duvqk, [H * D] * 4, dim=1)
+    ops.triton_hstu_attention_bwd(dout.to(DEV), qd, kd, vd, dqq.view(T, H, D), dkk.view(T, H, D),
+                                  dvv.view(T, H, D), offs.to(DEV), None, N, 0.1, 0, 0, None, False, 0)
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, 0.1, q.double(), k.double(), v.double(), offs, dtype=torch.float64)
+    s = ref.abs().max()
+    _check_bf16(out.float().cpu() / s, ref / s, "strided fwd")
+    dq, dk, dv, _ = orc.hstu_mha_bwd(N, 0.1, q, k, v, offs, dout)
+    got = duvqk.float().cpu()
+    assert torch.all(got[:, :H * D] == 7.0), "u slice of the gradient buffer was touched"
+    for name, sl, r in (("dv", slice(H * D, 2 * H * D), dv), ("dq", slice(2 * H * D, 3 * H * D), dq),
+                        ("dk", slice(3 * H * D, 4 * H * D), dk)):
+        s = r.abs().max()
+        _check_bf16(got[:, sl].reshape(T, H, D) / s, r / s, f"strided {name}")
+
+
+def test_empty_batch(hip_lib):
+    ops = _ops()
+    q = torch.empty(0, 2, 128, dtype=torch.bfloat16, device=DEV)
+    offs = torch.zeros(3, dtype=torch.int64, device=DEV)
+    out = ops.triton_hstu_attention_fwd(16, 0.1, q, q, q, offs, None, 0, 0, None, False, 0)
+    assert out.shape == (0, 2, 128)
+    dq = torch.empty_like(q)
+    ops.triton_hstu_attention_bwd(q, q, q, q, dq, dq.clone(), dq.clone(), offs, None, 16, 0.1, 0, 0, None,
+                                  False, 0)
+
+
+def _quantize(x):
+    q8, s = orc.quantize_e4m3_rows(x, dim=-1)  # per (token, head)
+    return q8, s
+
+
+@pytest.mark.parametrize("lengths", [[5, 17, 64], [300, 129, 1, 64, 200]])
+def test_fp8_fwd_bwd(hip_lib, lengths):
+    ops = _ops()
+    H, D = 2, 128
+    N = max(lengths)
+    q, k, v, offs = _case(lengths, H, D, std=1.0, dtype=torch.float32)
+    (q8, sq), (k8, sk), (v8, sv) = _quantize(q), _quantize(k), _quantize(v)
+    qd, kd, vd = orc.dequantize(q8, sq), orc.dequantize(k8, sk), orc.dequantize(v8, sv)
+    alpha = 1.0 / D ** 0.5
+    dev = [t.to(DEV) for t in (q8, k8, v8, sq, sk, sv)]
+    out = ops.triton_hstu_attention_fwd(N, alpha, dev[0], dev[1], dev[2], offs.to(DEV), None, 0, 0, None,
+                                        False, 0, dev[3], dev[4], dev[5])
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    dq, dk, dv = (torch.empty(q.shape, dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    ops.triton_hstu_attention_bwd(dout.to(DEV), dev[0], dev[1], dev[2], dq, dk, dv, offs.to(DEV), None, N,
+                                  alpha, 0, 0, None, False, 0, dev[3], dev[4], dev[5])
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, alpha, qd.double(), kd.double(), vd.double(), offs, dtype=torch.float64)
+    rq, rk, rv, _ = orc.hstu_mha_bwd(N, alpha, qd, kd, vd, offs, dout)
+    for name, got, r in (("out", out, ref), ("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        got = got.float().cpu()
+        err = orc.rel_l2(r, got)
+        mx = float((got.double() - r).abs().max() / r.abs().max())
+        assert err <= 1.5e-2 and mx <= 3e-2, f"fp8 {name}: rel L2 {err:.3e}, max {mx:.3e}, snr {orc.snr_db(r, got):.1f} dB"
