@@ -1057,14 +1057,16 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
   return (int)hipGetLastError();
 }
 
-extern "C" int hstu_attn_bwd(int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
-                             const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
-                             const float* q_scale, const float* k_scale, const float* v_scale,
-                             int64_t scale_row_stride, int64_t scale_head_stride, const int64_t* seq_offsets,
-                             int B, int H, int D, int max_seq_len, float alpha, const int32_t* num_targets,
-                             int max_attn_len, int contextual_seq_len, const float* attn_bias, int bias_R,
-                             void* dq, void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride,
-                             int64_t dv_row_stride, float* dbias, hipStream_t stream) {
+namespace {
+enum BwdParts { kBwdDkdv = 1, kBwdDq = 2, kBwdAll = 3 };
+
+int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
+                  const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                  const float* q_scale, const float* k_scale, const float* v_scale, int64_t scale_row_stride,
+                  int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                  float alpha, const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
+                  const float* attn_bias, int bias_R, void* dq, void* dk, void* dv, int64_t dq_row_stride,
+                  int64_t dk_row_stride, int64_t dv_row_stride, float* dbias, hipStream_t stream) {
   if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
                     v_scale, bias_R, attn_bias) ||
       dbias != nullptr)
@@ -1073,7 +1075,9 @@ extern "C" int hstu_attn_bwd(int dtype, const void* dout, int64_t dout_row_strid
   if (!row_alignment_ok(dtype, q_row_stride, q) || !row_alignment_ok(dtype, k_row_stride, k) ||
       !row_alignment_ok(dtype, v_row_stride, v) || !row_alignment_ok(HSTU_DTYPE_BF16, dout_row_stride, dout))
     return HSTU_E_UNSUPPORTED;
-  if (dq_row_stride < (int64_t)H * D || dk_row_stride < (int64_t)H * D || dv_row_stride < (int64_t)H * D)
+  if (((parts & kBwdDq) && (dq == nullptr || dq_row_stride < (int64_t)H * D)) ||
+      ((parts & kBwdDkdv) && (dk == nullptr || dv == nullptr || dk_row_stride < (int64_t)H * D ||
+                              dv_row_stride < (int64_t)H * D)))
     return HSTU_E_BAD_ARG;
   if (B == 0) return 0;
   AttnParams p{};
@@ -1105,14 +1109,13 @@ extern "C" int hstu_attn_bwd(int dtype, const void* dout, int64_t dout_row_strid
   p.inv_n = 1.0f / (float)max_seq_len;
   p.max_attn_len = max_attn_len;
   p.contextual_seq_len = contextual_seq_len;
+  p.blocks_per_seq = (max_seq_len + 127) / 128;
   const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
+  const int grid = p.blocks_per_seq * B * H;
   hipError_t e;
-  // dK / dV: 128-key blocks, longest key range first.
-  {
-    AttnParams pk = p;
-    pk.blocks_per_seq = (max_seq_len + 127) / 128;
-    const int grid = pk.blocks_per_seq * B * H;
-#define HSTU_DKV(DD, F8, G) launch(hstu_bwd_dkdv_kernel<DD, F8, G>, DkvCfg<DD, F8>::LDS, grid, pk, stream)
+  if (parts & kBwdDkdv) {
+    // dK / dV: 128-key blocks, longest query range first.
+#define HSTU_DKV(DD, F8, G) launch(hstu_bwd_dkdv_kernel<DD, F8, G>, DkvCfg<DD, F8>::LDS, grid, p, stream)
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
       e = generic ? HSTU_DKV(128, true, true) : HSTU_DKV(128, true, false);
     } else if (D == 128) {
@@ -1123,12 +1126,9 @@ extern "C" int hstu_attn_bwd(int dtype, const void* dout, int64_t dout_row_strid
 #undef HSTU_DKV
     if (e != hipSuccess) return (int)e;
   }
-  // dQ: 128-query blocks, longest key range first.
-  {
-    AttnParams pq = p;
-    pq.blocks_per_seq = (max_seq_len + 127) / 128;
-    const int grid = pq.blocks_per_seq * B * H;
-#define HSTU_DQ(DD, F8, G) launch(hstu_bwd_dq_kernel<DD, F8, G>, DqCfg<DD, F8>::LDS, grid, pq, stream)
+  if (parts & kBwdDq) {
+    // dQ: 128-query blocks, longest key range first.
+#define HSTU_DQ(DD, F8, G) launch(hstu_bwd_dq_kernel<DD, F8, G>, DqCfg<DD, F8>::LDS, grid, p, stream)
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
       e = generic ? HSTU_DQ(128, true, true) : HSTU_DQ(128, true, false);
     } else if (D == 128) {
@@ -1140,6 +1140,27 @@ extern "C" int hstu_attn_bwd(int dtype, const void* dout, int64_t dout_row_strid
     if (e != hipSuccess) return (int)e;
   }
   hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
-                     p.dq, p.dq_rs, p.dk, p.dk_rs, p.dv, p.dv_rs);
+                     (parts & kBwdDq) ? p.dq : p.dk, (parts & kBwdDq) ? p.dq_rs : p.dk_rs,
+                     (parts & kBwdDkdv) ? p.dk : (uint16_t*)nullptr, p.dk_rs,
+                     (parts & kBwdDkdv) ? p.dv : (uint16_t*)nullptr, p.dv_rs);
   return (int)hipGetLastError();
 }
+}  // namespace
+
+#define HSTU_BWD_ARGS                                                                                        \
+  dtype, dout, dout_row_stride, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale, \
+      scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, num_targets,             \
+      max_attn_len, contextual_seq_len, attn_bias, bias_R, dq, dk, dv, dq_row_stride, dk_row_stride,          \
+      dv_row_stride, dbias, stream
+#define HSTU_BWD_PARAMS                                                                                        \
+  int dtype, const void *dout, int64_t dout_row_stride, const void *q, const void *k, const void *v,           \
+      int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, const float *q_scale,                 \
+      const float *k_scale, const float *v_scale, int64_t scale_row_stride, int64_t scale_head_stride,        \
+      const int64_t *seq_offsets, int B, int H, int D, int max_seq_len, float alpha,                          \
+      const int32_t *num_targets, int max_attn_len, int contextual_seq_len, const float *attn_bias,           \
+      int bias_R, void *dq, void *dk, void *dv, int64_t dq_row_stride, int64_t dk_row_stride,                 \
+      int64_t dv_row_stride, float *dbias, hipStream_t stream
+
+extern "C" int hstu_attn_bwd(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdAll, HSTU_BWD_ARGS); }
+extern "C" int hstu_attn_bwd_dkdv(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDkdv, HSTU_BWD_ARGS); }
+extern "C" int hstu_attn_bwd_dq(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDq, HSTU_BWD_ARGS); }

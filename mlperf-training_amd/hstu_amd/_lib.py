@@ -28,6 +28,8 @@ EXPORTED_SYMBOLS = (
     "hstu_version",
     "hstu_attn_fwd",
     "hstu_attn_bwd",
+    "hstu_attn_bwd_dkdv",
+    "hstu_attn_bwd_dq",
     "hstu_fp8_gemm_rowcol",
     "hstu_quantize_e4m3_rows",
 )
@@ -61,6 +63,8 @@ _SIGNATURES = {
         [_i32, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32,
          _i32, _f32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp],
     ),
+    "hstu_attn_bwd_dkdv": None,
+    "hstu_attn_bwd_dq": None,
     "hstu_fp8_gemm_rowcol": (
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
@@ -100,7 +104,7 @@ def fn(name: str):
     f = _bound.get(name)
     if f is None:
         f = getattr(load_library(), name)
-        res, args = _SIGNATURES[name]
+        res, args = _SIGNATURES[name] or _SIGNATURES["hstu_attn_bwd"]
         f.restype = res
         f.argtypes = args
         _bound[name] = f
