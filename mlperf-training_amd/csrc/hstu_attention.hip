@@ -34,9 +34,9 @@
 //     it are never visited (per wave), so causal work is ~P pairs, not N^2.
 //   * global -> register prefetch of tile t+1 overlaps the MFMAs of tile t;
 //     LDS is double buffered with one barrier per tile.
-//   * grids are 1-D with the heaviest blocks first (longest key range), and
-//     blocks of one (sequence, head) are B*H apart, which keeps them on one
-//     XCD (and its L2) whenever B*H is a multiple of 8.
+//   * grids are 1-D with the heaviest blocks first (longest key range); the
+//     (sequence, head) index is rotated per block level so that the 8 XCDs
+//     (workgroup i runs on XCD i % 8) get equal shares of long sequences.
 //   * dq/dk/dv are written exactly once (two kernels: dK/dV with the key block
 //     outer, dQ with the query block outer); no atomics, deterministic.
 
@@ -44,6 +44,7 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "hstu_mi355x.h"
@@ -88,6 +89,39 @@ __device__ __forceinline__ i32x8 cat8(u32x4 lo, u32x4 hi) {
   return r;
 }
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Raw buffer access: 32-bit offsets from a per-(sequence, head) base, with
+// hardware zero-fill beyond `bytes` (rows past the sequence end).
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_ld128(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+// Transposed LDS read (gfx950 ds_read_b64_tr_b16).  Within each 16-lane
+// group, lane j supplies the address of 4 consecutive bf16 M[j][0..3]; lane i
+// receives M[4r + i/4][i%4] for r = 0..3.  With lane j pointing at row
+// base + j/4, column 4*(j%4) of a row-major tile, lane i gets rows
+// base..base+3 of column i: the B operand of an MFMA whose contraction runs
+// along the rows.
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_tr16(const uint8_t* p) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const lds_bf16x4* lp = (const lds_bf16x4*)(__attribute__((address_space(3))) const uint8_t*)(p);
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)lp));
+}
+__device__ __forceinline__ u32x4 cat_tr(u32x2 a, u32x2 b) { return u32x4{a[0], a[1], b[0], b[1]}; }
+
+// two e4m3 bytes (low or high half of w) -> two bf16, exact (scale 1.0)
+template <bool HI>
+__device__ __forceinline__ uint32_t cvt_fp8x2_bf16(uint32_t w) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
+}
 
 // t = -x*log2(e)  ->  t * sigmoid(x) = t / (1 + 2^t)   (== -silu(x)/ln2)
 __device__ __forceinline__ float sig_of_t(float t) {
@@ -292,6 +326,8 @@ struct AttnParams {
   int B, H, N;
   float alpha, inv_n;
   int max_attn_len, contextual_seq_len;
+  const float* bias;  // [H, 2*bias_R - 1] or null
+  int bias_R;
   int blocks_per_seq;  // grid = blocks_per_seq * B * H
 };
 
@@ -303,7 +339,11 @@ __device__ __forceinline__ SeqCtx seq_ctx(const AttnParams& p, bool reverse) {
   SeqCtx c;
   const int BH = p.B * p.H;
   const int slot = blockIdx.x / BH;
-  const int bh = blockIdx.x - slot * BH;
+  // Rotate (sequence, head) by the block level: workgroup i runs on XCD i % 8,
+  // so without the rotation every block of one (sequence, head) would land on
+  // one XCD and XCD load would follow the length distribution.
+  int bh = blockIdx.x - slot * BH + slot;
+  bh = bh >= BH ? bh - BH : bh;
   c.b = bh / p.H;
   c.h = bh - c.b * p.H;
   c.blk = reverse ? p.blocks_per_seq - 1 - slot : slot;
@@ -328,16 +368,31 @@ template <int D, bool FP8>
 struct FwdCfg {
   static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
   static constexpr int ES = FP8 ? 1 : 2;
-  using KTile = CopyTile<BN, D, ES>;
-  using VTile = TransTile<BN, D, FP8>;
+  static constexpr int KP = D * ES + 16;  // K row pitch (A-operand rows, b128 reads)
+  static constexpr int VP = D * 2 + 32;   // bf16 V row pitch (tr16 reads: 4 rows x 32 B disjoint)
   static constexpr int K_OFF = 0;
-  static constexpr int VT_OFF = K_OFF + BN * KTile::PITCH;
-  static constexpr int SK_OFF = VT_OFF + D * VTile::PITCH;
-  static constexpr int BUF = SK_OFF + (FP8 ? BN * 4 : 0);
+  static constexpr int V_OFF = K_OFF + BN * KP;
+  static constexpr int SC_OFF = V_OFF + BN * VP;              // e4m3: (sk, sv) per key
+  static constexpr int BIAS_OFF = SC_OFF + (FP8 ? BN * 8 : 0);  // BM + BN bias values
+  static constexpr int BUF = BIAS_OFF + (BM + BN) * 4;
   static constexpr int LDS = 2 * BUF;
+  static constexpr int K_CPR = D * ES / 16;                 // 16-byte chunks per K row
+  static constexpr int K_N = BN * K_CPR / kThreads;         // K chunks per thread
+  static constexpr int V_CPR = D * ES / 16;                 // 16-byte source chunks per V row
+  static constexpr int V_N = BN * V_CPR / kThreads;
 };
 
-template <int D, bool FP8, bool GENERIC>
+// Registers of one staged K/V tile (global -> registers -> LDS).
+template <int D, bool FP8>
+struct FwdStage {
+  using C = FwdCfg<D, FP8>;
+  u32x4 k[C::K_N];
+  u32x4 v[C::V_N];
+  float sc;    // e4m3: sk (threads 0..63) or sv (threads 64..127) of one key
+  float bias;  // threads 0..BM+BN-2: one bias value of the tile's offset band
+};
+
+template <int D, bool FP8, bool GENERIC, bool BIAS>
 __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   using C = FwdCfg<D, FP8>;
   static_assert(!FP8 || D == 128, "e4m3 path is specialised for D = 128");
@@ -353,12 +408,35 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   const int mw0 = m0 + wave * 32;
   const bool wave_active = mw0 < L;
 
-  const int64_t qrs = p.q_rs * C::ES, krs = p.k_rs * C::ES, vrs = p.v_rs * C::ES;
+  const uint32_t krs = (uint32_t)(p.k_rs * C::ES), vrs = (uint32_t)(p.v_rs * C::ES);
+  const int64_t qrs = p.q_rs * C::ES;
   const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES;
-  const float* skb = FP8 ? p.k_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
-  const float* svb = FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+  // Buffer resources over this (sequence, head): rows >= L read as zero.
+  const BufRsrc krsrc = make_rsrc(p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES,
+                                  (uint32_t)(L > 0 ? (L - 1) * krs + D * C::ES : 0));
+  const BufRsrc vrsrc = make_rsrc(p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES,
+                                  (uint32_t)(L > 0 ? (L - 1) * vrs + D * C::ES : 0));
+  const uint32_t s_step = FP8 ? (uint32_t)(p.s_rs * 4) : 0u;
+  const uint32_t sbytes = FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u;
+  const BufRsrc sk_rsrc = make_rsrc(FP8 ? p.k_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
+  const BufRsrc sv_rsrc = make_rsrc(FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
+  const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
+  const int R1 = p.bias_R - 1;
+
+  // per-thread constant staging offsets
+  uint32_t k_voff[C::K_N], k_loff[C::K_N], v_voff[C::V_N], v_loff[C::V_N];
+#pragma unroll
+  for (int i = 0; i < C::K_N; ++i) {
+    const int item = tid + kThreads * i, row = item / C::K_CPR, ch = item % C::K_CPR;
+    k_voff[i] = row * krs + ch * 16;
+    k_loff[i] = C::K_OFF + row * C::KP + ch * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < C::V_N; ++i) {
+    const int item = tid + kThreads * i, row = item / C::V_CPR, ch = item % C::V_CPR;
+    v_voff[i] = row * vrs + ch * 16;
+    v_loff[i] = C::V_OFF + row * C::VP + ch * 16 * (FP8 ? 2 : 1);
+  }
 
   // Q fragments (B operand of S^T = K.Q^T): lane holds query mw0+16qt+li.
   u32x4 qf[2][C::KS];
@@ -399,19 +477,63 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   if (GENERIC && m0 < p.contextual_seq_len) n_end = L;
   const int ntiles = (n_end + C::BN - 1) / C::BN;
 
-  typename C::KTile kt_ld;
-  typename C::VTile vt_ld;
-  ScaleTile<C::BN> sk_ld;
+  FwdStage<D, FP8> stg;
   auto load = [&](int n0) {
-    kt_ld.load(kb, krs, n0, L);
-    vt_ld.load(vb, vrs, svb, p.s_rs, n0, L);
-    if constexpr (FP8) sk_ld.load(skb, p.s_rs, n0, L);
+#pragma unroll
+    for (int i = 0; i < C::K_N; ++i) stg.k[i] = buf_ld128(krsrc, k_voff[i], n0 * krs);
+#pragma unroll
+    for (int i = 0; i < C::V_N; ++i) stg.v[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
+    if constexpr (FP8) {
+      if (tid < 64) {
+        stg.sc = buf_ldf(sk_rsrc, (uint32_t)tid * s_step, n0 * s_step);
+      } else if (tid < 128) {
+        stg.sc = buf_ldf(sv_rsrc, (uint32_t)(tid - 64) * s_step, n0 * s_step);
+      }
+    }
+    if constexpr (BIAS) {
+      // offsets i-j of this tile span [m0-n0-(BN-1), m0-n0+BM-1]
+      if (tid < C::BM + C::BN - 1) {
+        const int off = m0 - n0 - (C::BN - 1) + tid;
+        stg.bias = biasb[min(max(off, -R1), R1) + R1] * -kLog2e;
+      }
+    }
   };
   auto store = [&](uint8_t* buf) {
-    kt_ld.store(buf + C::K_OFF);
-    vt_ld.store(buf + C::VT_OFF);
-    if constexpr (FP8) sk_ld.store(buf + C::SK_OFF);
+#pragma unroll
+    for (int i = 0; i < C::K_N; ++i) *(u32x4*)(buf + k_loff[i]) = stg.k[i];
+#pragma unroll
+    for (int i = 0; i < C::V_N; ++i) {
+      if constexpr (FP8) {
+        // exact e4m3 -> bf16 (scale 1); the per-key V scale is folded into P
+        const u32x4 w = stg.v[i];
+        u32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          lo[2 * e] = cvt_fp8x2_bf16<false>(w[e]);
+          lo[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e]);
+          hi[2 * e] = cvt_fp8x2_bf16<false>(w[e + 2]);
+          hi[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e + 2]);
+        }
+        *(u32x4*)(buf + v_loff[i]) = lo;
+        *(u32x4*)(buf + v_loff[i] + 16) = hi;
+      } else {
+        *(u32x4*)(buf + v_loff[i]) = stg.v[i];
+      }
+    }
+    if constexpr (FP8) {
+      if (tid < 128) ((float*)(buf + C::SC_OFF))[(tid & 63) * 2 + (tid >> 6)] = stg.sc;
+    }
+    if constexpr (BIAS) {
+      if (tid < C::BM + C::BN - 1) ((float*)(buf + C::BIAS_OFF))[tid] = stg.bias;
+    }
   };
+
+  // Per-lane LDS addresses (tile-invariant).
+  const int k_rd = C::K_OFF + li * C::KP + (FP8 ? 32 * g : 16 * g);
+  // tr16: lane j of group g addresses row 4g + j/4 (+16 for the second half), column 4*(j%4)
+  const int v_rd = C::V_OFF + (4 * g + (li >> 2)) * C::VP + (li & 3) * 8;
+  // bias index of element (qt, kt, r) = bias_rd + 16*(qt-kt) - r
+  const int bias_rd = 32 * wave + (C::BN - 1) + li - 4 * g;
 
   load(0);
   store(smem);
@@ -423,14 +545,13 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
     if (t + 1 < ntiles) load(n0 + C::BN);
 
     if (wave_active && (GENERIC || n0 <= mw0 + 31)) {
-      const bool need_mask = GENERIC || (n0 + C::BN - 1 > mw0);
       // ---- S^T = K . Q^T : s[kt][qt], keys n0+16kt+4g+r, query mw0+16qt+li
       f32x4 s[C::KT][2];
 #pragma unroll
       for (int kt = 0; kt < C::KT; ++kt) {
-        const uint8_t* krow = buf + C::K_OFF + (kt * 16 + li) * C::KTile::PITCH;
+        const uint8_t* krow = buf + k_rd + kt * 16 * C::KP;
         if constexpr (FP8) {
-          i32x8 a = cat8(lds_ld128(krow + 32 * g), lds_ld128(krow + 32 * g + 16));
+          i32x8 a = cat8(lds_ld128(krow), lds_ld128(krow + 16));
           s[kt][0] = mfma_fp8(a, qf8[0], zero4());
           s[kt][1] = mfma_fp8(a, qf8[1], zero4());
         } else {
@@ -438,43 +559,67 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
           s[kt][1] = zero4();
 #pragma unroll
           for (int st = 0; st < C::KS; ++st) {
-            u32x4 a = lds_ld128(krow + (32 * st + 8 * g) * 2);
+            u32x4 a = lds_ld128(krow + st * 64);
             s[kt][0] = mfma_bf16(a, qf[0][st], s[kt][0]);
             s[kt][1] = mfma_bf16(a, qf[1][st], s[kt][1]);
           }
         }
       }
       // ---- SiLU epilogue on the accumulators, packed into P (A operand)
+      const bool need_mask = GENERIC || (n0 + C::BN - 1 > mw0);
+      // whole tile in the clamped bias region: one constant
+      const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
+      const float* bias_lds = (const float*)(buf + C::BIAS_OFF);
       u32x4 pa[2][C::BN / 32];
+      auto epilogue = [&](auto masked_tag, auto bconst_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        constexpr bool BCONST = decltype(bconst_tag)::value;
+        const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
 #pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt) {
-        f32x4 skv = {1.f, 1.f, 1.f, 1.f};
-        if constexpr (FP8) skv = lds_ldf4(buf + C::SK_OFF + (kt * 16 + 4 * g) * 4);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          float pv[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = s[kt][qt][r] * cq[qt];
-            if constexpr (FP8) t *= skv[r];
-            float val = t * sig_of_t(t);
-            if (need_mask) {
-              const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
-              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
-              val = ok ? val : 0.f;
-            }
-            pv[r] = val;
+        for (int kt = 0; kt < C::KT; ++kt) {
+          f32x4 skv = {1.f, 1.f, 1.f, 1.f}, svv = {1.f, 1.f, 1.f, 1.f};
+          if constexpr (FP8) {
+            const float* scp = (const float*)(buf + C::SC_OFF) + (kt * 16 + 4 * g) * 2;
+            f32x4 a = *(const f32x4*)scp, b = *(const f32x4*)(scp + 4);
+            skv = f32x4{a[0], a[2], b[0], b[2]};
+            svv = f32x4{a[1], a[3], b[1], b[3]};
           }
-          pa[qt][kt >> 1][(kt & 1) * 2 + 0] = pack_bf16(pv[0], pv[1]);
-          pa[qt][kt >> 1][(kt & 1) * 2 + 1] = pack_bf16(pv[2], pv[3]);
+#pragma unroll
+          for (int qt = 0; qt < 2; ++qt) {
+            float pv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float t = s[kt][qt][r] * cq[qt];
+              if constexpr (FP8) t *= skv[r];
+              if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + 16 * (qt - kt) - r];
+              float val = t * sig_of_t(t);
+              if constexpr (FP8) val *= svv[r];
+              if constexpr (MASKED) {
+                const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
+                const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+                val = ok ? val : 0.f;
+              }
+              pv[r] = val;
+            }
+            pa[qt][kt >> 1][(kt & 1) * 2 + 0] = pack_bf16(pv[0], pv[1]);
+            pa[qt][kt >> 1][(kt & 1) * 2 + 1] = pack_bf16(pv[2], pv[3]);
+          }
         }
+      };
+      if (need_mask) {
+        if (bias_const) epilogue(std::true_type{}, std::true_type{});
+        else epilogue(std::true_type{}, std::false_type{});
+      } else {
+        if (bias_const) epilogue(std::false_type{}, std::true_type{});
+        else epilogue(std::false_type{}, std::false_type{});
       }
-      // ---- O += P . V
+      // ---- O += P . V  (V rows read transposed by ds_read_b64_tr_b16)
 #pragma unroll
       for (int c = 0; c < C::BN / 32; ++c) {
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt) {
-          u32x4 bv = lds_ld128(buf + C::VT_OFF + (dt * 16 + li) * C::VTile::PITCH + (32 * c + 8 * g) * 2);
+          const uint8_t* vp = buf + v_rd + c * 32 * C::VP + dt * 32;
+          u32x4 bv = cat_tr(lds_tr16(vp), lds_tr16(vp + 16 * C::VP));
           o[0][dt] = mfma_bf16(pa[0][c], bv, o[0][dt]);
           o[1][dt] = mfma_bf16(pa[1][c], bv, o[1][dt]);
         }
@@ -983,8 +1128,7 @@ bool check_common(int dtype, int H, int D, int B, int N, int64_t rs_q, int64_t r
   if (B < 0 || H <= 0 || N <= 0) return false;
   if (rs_q < (int64_t)H * D || rs_k < (int64_t)H * D || rs_v < (int64_t)H * D) return false;
   if (dtype == HSTU_DTYPE_FP8_E4M3 && (!qs || !ks || !vs)) return false;
-  if (bias != nullptr) return false;  // relative bias: not in this build yet
-  (void)bias_R;
+  if (bias != nullptr && bias_R < 1) return false;
   return true;
 }
 
@@ -1041,15 +1185,20 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
   const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
   p.blocks_per_seq = (max_seq_len + 127) / 128;
   const int grid = p.blocks_per_seq * B * H;
-#define HSTU_FWD(DD, F8, G) launch(hstu_fwd_kernel<DD, F8, G>, FwdCfg<DD, F8>::LDS, grid, p, stream)
+  p.bias = attn_bias;
+  p.bias_R = bias_R;
+#define HSTU_FWD(DD, F8, G, BB) launch(hstu_fwd_kernel<DD, F8, G, BB>, FwdCfg<DD, F8>::LDS, grid, p, stream)
+#define HSTU_FWD_B(DD, F8, G) (has_bias ? HSTU_FWD(DD, F8, G, true) : HSTU_FWD(DD, F8, G, false))
+  const bool has_bias = attn_bias != nullptr;
   hipError_t e;
   if (dtype == HSTU_DTYPE_FP8_E4M3) {
-    e = generic ? HSTU_FWD(128, true, true) : HSTU_FWD(128, true, false);
+    e = generic ? HSTU_FWD_B(128, true, true) : HSTU_FWD_B(128, true, false);
   } else if (D == 128) {
-    e = generic ? HSTU_FWD(128, false, true) : HSTU_FWD(128, false, false);
+    e = generic ? HSTU_FWD_B(128, false, true) : HSTU_FWD_B(128, false, false);
   } else {
-    e = generic ? HSTU_FWD(64, false, true) : HSTU_FWD(64, false, false);
+    e = generic ? HSTU_FWD_B(64, false, true) : HSTU_FWD_B(64, false, false);
   }
+#undef HSTU_FWD_B
 #undef HSTU_FWD
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
@@ -1069,7 +1218,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
                   int64_t dk_row_stride, int64_t dv_row_stride, float* dbias, hipStream_t stream) {
   if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
                     v_scale, bias_R, attn_bias) ||
-      dbias != nullptr)
+      dbias != nullptr || attn_bias != nullptr)
     return HSTU_E_BAD_ARG;
   if (!(D == 128 || (D == 64 && dtype == HSTU_DTYPE_BF16))) return HSTU_E_UNSUPPORTED;
   if (!row_alignment_ok(dtype, q_row_stride, q) || !row_alignment_ok(dtype, k_row_stride, k) ||

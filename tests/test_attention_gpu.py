@@ -206,3 +206,52 @@ def test_fp8_fwd_bwd(hip_lib, lengths):
         err = orc.rel_l2(r, got)
         mx = float((got.double() - r).abs().max() / r.abs().max())
         assert err <= 1.5e-2 and mx <= 3e-2, f"fp8 {name}: rel L2 {err:.3e}, max {mx:.3e}, snr {orc.snr_db(r, got):.1f} dB"
+
+
+@pytest.mark.parametrize("R", [8, 1024])
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_fwd_rel_bias(hip_lib, R, dtype):
+    """Relative-position bias (this build's extension): bias[h][clamp(i-j)] is
+    added to the score before SiLU; R=8 exercises the clamped region."""
+    ops = _ops()
+    lengths = [300, 129, 1, 64, 200]
+    H, D = 2, 128
+    N = 300
+    bias = orc.make_bias(H, R, seed=3, std=0.5)
+    alpha = 1.0 / D ** 0.5
+    if dtype == "bf16":
+        q, k, v, offs = _case(lengths, H, D)
+        out = ops.triton_hstu_attention_fwd(N, alpha, q.to(DEV), k.to(DEV), v.to(DEV), offs.to(DEV), None, 0, 0,
+                                            None, False, 0, attn_bias=bias.to(DEV))
+        qd, kd, vd = q.double(), k.double(), v.double()
+        bar = 1e-2
+    else:
+        q, k, v, offs = _case(lengths, H, D, std=1.0, dtype=torch.float32)
+        (q8, sq), (k8, sk), (v8, sv) = _quantize(q), _quantize(k), _quantize(v)
+        qd, kd, vd = (orc.dequantize(a, b).double() for a, b in ((q8, sq), (k8, sk), (v8, sv)))
+        out = ops.triton_hstu_attention_fwd(N, alpha, q8.to(DEV), k8.to(DEV), v8.to(DEV), offs.to(DEV), None, 0,
+                                            0, None, False, 0, sq.to(DEV), sk.to(DEV), sv.to(DEV),
+                                            attn_bias=bias.to(DEV))
+        bar = 1.5e-2
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, alpha, qd, kd, vd, offs, attn_bias=bias.double(), dtype=torch.float64)
+    err = orc.rel_l2(ref, out.float().cpu())
+    assert err <= bar, f"bias fwd {dtype} R={R}: rel L2 {err:.3e}"
+
+
+def test_per_tensor_fp8_scales(hip_lib):
+    """The reference's per-tensor (scalar) FP8 scale is the special case of
+    per-token scales with all entries equal."""
+    ops = _ops()
+    lengths = [70, 200, 33]
+    H, D, N = 2, 128, 200
+    q, k, v, offs = _case(lengths, H, D, std=1.0, dtype=torch.float32)
+    qs = orc.quantize_e4m3_per_tensor(torch.cat([q, k, v]))[1]
+    s = float(qs)
+    q8, k8, v8 = ((x / s).clamp(-448, 448).to(torch.float8_e4m3fn) for x in (q, k, v))
+    out = ops.triton_hstu_attention_fwd(N, 0.1, q8.to(DEV), k8.to(DEV), v8.to(DEV), offs.to(DEV), None, 0, 0,
+                                        None, False, 0, s, s, s)
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, 0.1, q8.double() * s, k8.double() * s, v8.double() * s, offs, dtype=torch.float64)
+    err = orc.rel_l2(ref, out.float().cpu())
+    assert err <= 1.5e-2, f"per-tensor fp8: rel L2 {err:.3e}"
