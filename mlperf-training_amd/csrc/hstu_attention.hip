@@ -328,6 +328,7 @@ struct AttnParams {
   int max_attn_len, contextual_seq_len;
   const float* bias;  // [H, 2*bias_R - 1] or null
   int bias_R;
+  float* dbias;       // bias gradient, same shape (backward)
   int blocks_per_seq;  // grid = blocks_per_seq * B * H
 };
 
@@ -647,28 +648,105 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
 }
 
 // =====================================================================
-// Backward dQ.  Block = 128 query rows (32 per wave), key tiles of 64.
-//   S^T = K.Q^T, dP^T = V.dO^T, dS = dP*sig*(1 + x(1-sig)), dQ += dS.K
+// Backward.  Both kernels stage their per-tile operands as bf16 rows (e4m3
+// inputs are converted exactly, scale 1, while staging; the per-row scales
+// are applied in the epilogue), so one LDS copy of a tile serves as an A
+// operand (row reads, ds_read_b128) and as a B operand (ds_read_b64_tr_b16).
+// A row pitch of 2D+48 bytes keeps both read patterns free of bank
+// conflicts: 16 consecutive rows fall on 16 distinct 16-byte bank groups,
+// and 4 consecutive rows x 32 bytes fall on disjoint ranges.
 // =====================================================================
-template <int D, bool FP8>
-struct DqCfg {
-  static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
-  static constexpr int ES = FP8 ? 1 : 2;
-  using KTile = CopyTile<BN, D, ES>;              // A operand of S^T
-  using VTileB = CopyTile<BN, D, 2>;              // A operand of dP^T (bf16 inputs)
-  using VTileF = DeqTile<BN, D>;                  // A operand of dP^T (e4m3 inputs)
-  using KtTile = TransTile<BN, D, FP8>;           // B operand of dQ
-  static constexpr int K_OFF = 0;
-  static constexpr int V_OFF = K_OFF + BN * KTile::PITCH;
-  static constexpr int KT_OFF = V_OFF + BN * (D * 2 + 16);
-  static constexpr int SK_OFF = KT_OFF + D * KtTile::PITCH;
-  static constexpr int BUF = SK_OFF + (FP8 ? BN * 4 : 0);
-  static constexpr int LDS = 2 * BUF;
+template <int D>
+struct BwdPitch {
+  static constexpr int P = D * 2 + 48;
 };
 
-template <int D, bool FP8, bool GENERIC>
-__global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dq_kernel(AttnParams p) {
-  using C = DqCfg<D, FP8>;
+// ROWS x D input rows (bf16, or e4m3 converted exactly) -> bf16 LDS rows.
+template <int ROWS, int D, bool FP8>
+struct RowStage {
+  static constexpr int ES = FP8 ? 1 : 2;
+  static constexpr int CPR = D * ES / 16;  // 16-byte source chunks per row
+  static constexpr int N = ROWS * CPR / kThreads;
+  static_assert(N >= 1 && ROWS * CPR % kThreads == 0, "tile/thread mismatch");
+  u32x4 r[N];
+  uint32_t voff[N], loff[N];
+  __device__ __forceinline__ void init(uint32_t rs_bytes, int lds_off) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int item = threadIdx.x + kThreads * i, row = item / CPR, ch = item % CPR;
+      voff[i] = row * rs_bytes + ch * 16;
+      loff[i] = lds_off + row * BwdPitch<D>::P + ch * 16 * (FP8 ? 2 : 1);
+    }
+  }
+  __device__ __forceinline__ void load(BufRsrc rs, uint32_t soff) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = buf_ld128(rs, voff[i], soff);
+  }
+  __device__ __forceinline__ void store(uint8_t* buf) const {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if constexpr (FP8) {
+        const u32x4 w = r[i];
+        u32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          lo[2 * e] = cvt_fp8x2_bf16<false>(w[e]);
+          lo[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e]);
+          hi[2 * e] = cvt_fp8x2_bf16<false>(w[e + 2]);
+          hi[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e + 2]);
+        }
+        *(u32x4*)(buf + loff[i]) = lo;
+        *(u32x4*)(buf + loff[i] + 16) = hi;
+      } else {
+        *(u32x4*)(buf + loff[i]) = r[i];
+      }
+    }
+  }
+};
+
+// Fragment of 16 rows x D as the B operand of a 16x16x32 bf16 MFMA whose
+// contraction runs over d: lane (li, g) gets row `row`, columns 32st+8g..+7.
+// e4m3 rows are converted exactly; `scale` multiplies every element (only
+// used where the rounding of the scaled value to bf16 is acceptable).
+template <int D, bool FP8>
+__device__ __forceinline__ void load_row_frag(u32x4 (&f)[D / 32], const uint8_t* base, int64_t rs_bytes, int row,
+                                              bool ok, int g, float scale) {
+#pragma unroll
+  for (int st = 0; st < D / 32; ++st) {
+    f[st] = u32x4{0u, 0u, 0u, 0u};
+    if (!ok) continue;
+    if constexpr (FP8) {
+      const u32x2 w = *(const u32x2*)(base + (int64_t)row * rs_bytes + 32 * st + 8 * g);
+      const u32x2 a = fp8x4_to_bf16x4(w[0], scale), b = fp8x4_to_bf16x4(w[1], scale);
+      f[st] = u32x4{a[0], a[1], b[0], b[1]};
+    } else {
+      f[st] = *(const u32x4*)(base + (int64_t)row * rs_bytes + (32 * st + 8 * g) * 2);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------
+// dQ (and the bias gradient).  Block = 128 queries (32 per wave), key tiles
+// of 64.  S^T = K.Q^T, dP^T = V.dO^T (C fragments: key 4g+r, query li),
+// dS = dP*sig*(1 + x(1-sig)), dQ += dS.K.
+// ---------------------------------------------------------------------
+template <int D>
+struct DqCfg {
+  static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
+  static constexpr int P = BwdPitch<D>::P;
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = K_OFF + BN * P;
+  static constexpr int SC_OFF = V_OFF + BN * P;  // (sk, sv) per key
+  static constexpr int BIAS_OFF = SC_OFF + BN * 8;
+  static constexpr int BUF = BIAS_OFF + (BM + BN) * 4;
+  static constexpr int HIST_OFF = 2 * BUF;  // bias-gradient histogram, R floats
+  static int lds(bool bias, int R) { return HIST_OFF + (bias ? R * 4 : 0); }
+};
+
+template <int D, bool FP8, bool GENERIC, bool BIAS>
+__global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) {
+  using C = DqCfg<D>;
+  constexpr int ES = FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const SeqCtx sc = seq_ctx(p, /*reverse=*/true);
@@ -681,46 +759,36 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dq_kernel(AttnParams p) 
   const int mw0 = m0 + wave * 32;
   const bool wave_active = mw0 < L;
 
-  const int64_t qrs = p.q_rs * C::ES, krs = p.k_rs * C::ES, vrs = p.v_rs * C::ES, dors = p.do_rs * 2;
-  const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* dob = p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2;
-  const float* skb = FP8 ? p.k_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
-  const float* svb = FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+  const uint32_t krs = (uint32_t)(p.k_rs * ES), vrs = (uint32_t)(p.v_rs * ES);
+  const BufRsrc krsrc = make_rsrc(p.k + (sc.start * p.k_rs + (int64_t)h * D) * ES,
+                                  (uint32_t)(L > 0 ? (L - 1) * krs + D * ES : 0));
+  const BufRsrc vrsrc = make_rsrc(p.v + (sc.start * p.v_rs + (int64_t)h * D) * ES,
+                                  (uint32_t)(L > 0 ? (L - 1) * vrs + D * ES : 0));
+  const uint32_t s_step = FP8 ? (uint32_t)(p.s_rs * 4) : 0u;
+  const uint32_t sbytes = FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u;
+  const BufRsrc sk_rsrc = make_rsrc(FP8 ? p.k_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
+  const BufRsrc sv_rsrc = make_rsrc(FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
+  const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
+  const int R1 = p.bias_R - 1;
+  float* hist = (float*)(smem + C::HIST_OFF);
+  if constexpr (BIAS) {
+    for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
+  }
 
-  u32x4 qf[2][C::KS];
-  i32x8 qf8[2];
-  u32x4 dof[2][C::KS];
+  // Q and dO fragments (B operands): lane holds query mw0+16qt+li.
+  u32x4 qf[2][C::KS], dof[2][C::KS];
   float cq[2];
+  {
+    const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * ES;
+    const uint8_t* dob = p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int row = mw0 + qt * 16 + li;
-    const bool ok = row < L;
-    const uint8_t* src = qb + (int64_t)row * qrs;
-    const uint8_t* dsrc = dob + (int64_t)row * dors;
-    cq[qt] = -p.alpha * kLog2e;
-    if constexpr (FP8) {
-      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-      float s = 0.f;
-      if (ok) {
-        lo = *(const u32x4*)(src + 32 * g);
-        hi = *(const u32x4*)(src + 32 * g + 16);
-        s = p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
-      }
-      qf8[qt] = cat8(lo, hi);
-      cq[qt] *= s;
-    } else {
-#pragma unroll
-      for (int st = 0; st < C::KS; ++st) {
-        qf[qt][st] = u32x4{0u, 0u, 0u, 0u};
-        if (ok) qf[qt][st] = *(const u32x4*)(src + (32 * st + 8 * g) * 2);
-      }
-    }
-#pragma unroll
-    for (int st = 0; st < C::KS; ++st) {
-      dof[qt][st] = u32x4{0u, 0u, 0u, 0u};
-      if (ok) dof[qt][st] = *(const u32x4*)(dsrc + (32 * st + 8 * g) * 2);
+    for (int qt = 0; qt < 2; ++qt) {
+      const int row = mw0 + qt * 16 + li;
+      const bool ok = row < L;
+      load_row_frag<D, FP8>(qf[qt], qb, p.q_rs * ES, row, ok, g, 1.f);
+      load_row_frag<D, false>(dof[qt], dob, p.do_rs * 2, row, ok, g, 1.f);
+      cq[qt] = -p.alpha * kLog2e;
+      if constexpr (FP8) cq[qt] *= ok ? p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 0.f;
     }
   }
 
@@ -734,31 +802,40 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dq_kernel(AttnParams p) 
   if (GENERIC && m0 < p.contextual_seq_len) n_end = L;
   const int ntiles = (n_end + C::BN - 1) / C::BN;
 
-  typename C::KTile k_ld;
-  typename C::VTileB vb_ld;
-  typename C::VTileF vf_ld;
-  typename C::KtTile kt_ld;
-  ScaleTile<C::BN> sk_ld;
+  RowStage<C::BN, D, FP8> k_st, v_st;
+  k_st.init(krs, C::K_OFF);
+  v_st.init(vrs, C::V_OFF);
+  float sc_v = 0.f, bias_v = 0.f;
   auto load = [&](int n0) {
-    k_ld.load(kb, krs, n0, L);
+    k_st.load(krsrc, n0 * krs);
+    v_st.load(vrsrc, n0 * vrs);
     if constexpr (FP8) {
-      vf_ld.load(vb, vrs, svb, p.s_rs, n0, L);
-      sk_ld.load(skb, p.s_rs, n0, L);
-    } else {
-      vb_ld.load(vb, vrs, n0, L);
+      if (tid < 64) sc_v = buf_ldf(sk_rsrc, (uint32_t)tid * s_step, n0 * s_step);
+      else if (tid < 128) sc_v = buf_ldf(sv_rsrc, (uint32_t)(tid - 64) * s_step, n0 * s_step);
     }
-    kt_ld.load(kb, krs, skb, p.s_rs, n0, L);
+    if constexpr (BIAS) {
+      if (tid < C::BM + C::BN - 1) {
+        const int off = m0 - n0 - (C::BN - 1) + tid;
+        bias_v = biasb[min(max(off, -R1), R1) + R1] * -kLog2e;
+      }
+    }
   };
   auto store = [&](uint8_t* buf) {
-    k_ld.store(buf + C::K_OFF);
+    k_st.store(buf);
+    v_st.store(buf);
     if constexpr (FP8) {
-      vf_ld.store(buf + C::V_OFF);
-      sk_ld.store(buf + C::SK_OFF);
-    } else {
-      vb_ld.store(buf + C::V_OFF);
+      if (tid < 128) ((float*)(buf + C::SC_OFF))[(tid & 63) * 2 + (tid >> 6)] = sc_v;
     }
-    kt_ld.store(buf + C::KT_OFF);
+    if constexpr (BIAS) {
+      if (tid < C::BM + C::BN - 1) ((float*)(buf + C::BIAS_OFF))[tid] = bias_v;
+    }
   };
+
+  const int k_rd = C::K_OFF + li * C::P + 16 * g;
+  const int v_rd = C::V_OFF + li * C::P + 16 * g;
+  const int kt_rd = C::K_OFF + (4 * g + (li >> 2)) * C::P + (li & 3) * 8;  // tr16
+  const int bias_rd = 32 * wave + (C::BN - 1) + li - 4 * g;
+  float dclamp = 0.f;  // bias gradient of elements in the clamped region
 
   load(0);
   store(smem);
@@ -771,73 +848,113 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dq_kernel(AttnParams p) 
 
     if (wave_active && (GENERIC || n0 <= mw0 + 31)) {
       const bool need_mask = GENERIC || (n0 + C::BN - 1 > mw0);
-      f32x4 s[C::KT][2], dp[C::KT][2];
-#pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt) {
-        const uint8_t* krow = buf + C::K_OFF + (kt * 16 + li) * C::KTile::PITCH;
-        const uint8_t* vrow = buf + C::V_OFF + (kt * 16 + li) * (D * 2 + 16);
-        if constexpr (FP8) {
-          i32x8 a = cat8(lds_ld128(krow + 32 * g), lds_ld128(krow + 32 * g + 16));
-          s[kt][0] = mfma_fp8(a, qf8[0], zero4());
-          s[kt][1] = mfma_fp8(a, qf8[1], zero4());
-        } else {
-          s[kt][0] = zero4();
-          s[kt][1] = zero4();
-#pragma unroll
-          for (int st = 0; st < C::KS; ++st) {
-            u32x4 a = lds_ld128(krow + (32 * st + 8 * g) * 2);
-            s[kt][0] = mfma_bf16(a, qf[0][st], s[kt][0]);
-            s[kt][1] = mfma_bf16(a, qf[1][st], s[kt][1]);
-          }
-        }
-        dp[kt][0] = zero4();
-        dp[kt][1] = zero4();
-#pragma unroll
-        for (int st = 0; st < C::KS; ++st) {
-          u32x4 a = lds_ld128(vrow + (32 * st + 8 * g) * 2);
-          dp[kt][0] = mfma_bf16(a, dof[0][st], dp[kt][0]);
-          dp[kt][1] = mfma_bf16(a, dof[1][st], dp[kt][1]);
-        }
-      }
-      u32x4 dsa[2][C::BN / 32];
-#pragma unroll
-      for (int kt = 0; kt < C::KT; ++kt) {
-        f32x4 skv = {1.f, 1.f, 1.f, 1.f};
-        if constexpr (FP8) skv = lds_ldf4(buf + C::SK_OFF + (kt * 16 + 4 * g) * 4);
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-          float dsv[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = s[kt][qt][r] * cq[qt];
-            if constexpr (FP8) t *= skv[r];
-            const float sg = sig_of_t(t);
-            const float x = -kLn2 * t;
-            float val = dp[kt][qt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
-            if (need_mask) {
-              const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
-              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
-              val = ok ? val : 0.f;
-            }
-            dsv[r] = val;
-          }
-          dsa[qt][kt >> 1][(kt & 1) * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
-          dsa[qt][kt >> 1][(kt & 1) * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
-        }
-      }
+      const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
+      const float* bias_lds = (const float*)(buf + C::BIAS_OFF);
+      // Two halves of 32 keys each (key sub-tiles 2c, 2c+1), to keep the
+      // score registers of one half live at a time.
 #pragma unroll
       for (int c = 0; c < C::BN / 32; ++c) {
+        if (!GENERIC && n0 + 32 * c > mw0 + 31) break;  // half entirely above the diagonal
+        f32x4 s[2][2], dp[2][2];
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const int kt = 2 * c + h2;
+          s[h2][0] = s[h2][1] = dp[h2][0] = dp[h2][1] = zero4();
+#pragma unroll
+          for (int st = 0; st < C::KS; ++st) {
+            const u32x4 a = lds_ld128(buf + k_rd + kt * 16 * C::P + st * 64);
+            s[h2][0] = mfma_bf16(a, qf[0][st], s[h2][0]);
+            s[h2][1] = mfma_bf16(a, qf[1][st], s[h2][1]);
+            const u32x4 b = lds_ld128(buf + v_rd + kt * 16 * C::P + st * 64);
+            dp[h2][0] = mfma_bf16(b, dof[0][st], dp[h2][0]);
+            dp[h2][1] = mfma_bf16(b, dof[1][st], dp[h2][1]);
+          }
+        }
+        u32x4 dsa[2];
+        auto epilogue = [&](auto masked_tag, auto bconst_tag) {
+          constexpr bool MASKED = decltype(masked_tag)::value;
+          constexpr bool BCONST = decltype(bconst_tag)::value;
+          const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const int kt = 2 * c + h2;
+            f32x4 skv = {1.f, 1.f, 1.f, 1.f}, svv = {1.f, 1.f, 1.f, 1.f};
+            if constexpr (FP8) {
+              const float* scp = (const float*)(buf + C::SC_OFF) + (kt * 16 + 4 * g) * 2;
+              const f32x4 a = *(const f32x4*)scp, b = *(const f32x4*)(scp + 4);
+              skv = f32x4{a[0], a[2], b[0], b[2]};
+              svv = f32x4{a[1], a[3], b[1], b[3]};
+            }
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+              float dsv[4];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                float t = s[h2][qt][r] * cq[qt];
+                if constexpr (FP8) t *= skv[r];
+                const int boff = 16 * (qt - kt) - r;
+                if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + boff];
+                const float sg = sig_of_t(t);
+                const float x = -kLn2 * t;
+                float dpv = dp[h2][qt][r];
+                if constexpr (FP8) dpv *= svv[r];
+                float ds = dpv * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+                int off = 0;
+                if constexpr (MASKED || (BIAS && !BCONST)) {
+                  off = (mw0 + qt * 16 + li) - (n0 + kt * 16 + 4 * g + r);
+                }
+                if constexpr (MASKED) {
+                  const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
+                  const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+                  ds = ok ? ds : 0.f;
+                }
+                if constexpr (BIAS) {
+                  if constexpr (BCONST) {
+                    dclamp += ds;
+                  } else if (off >= 0) {
+                    atomicAdd(&hist[min(off, R1)], ds);
+                  } else if (GENERIC && ds != 0.f) {
+                    atomicAdd(&p.dbias[(int64_t)h * (2 * p.bias_R - 1) + max(off, -R1) + R1], ds * p.inv_n);
+                  }
+                }
+                if constexpr (FP8) ds *= skv[r];
+                dsv[r] = ds;
+              }
+              dsa[qt][h2 * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
+              dsa[qt][h2 * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
+            }
+          }
+        };
+        if (need_mask) {
+          if (bias_const) epilogue(std::true_type{}, std::true_type{});
+          else epilogue(std::true_type{}, std::false_type{});
+        } else {
+          if (bias_const) epilogue(std::false_type{}, std::true_type{});
+          else epilogue(std::false_type{}, std::false_type{});
+        }
+        // ---- dQ += dS . K  (K rows read transposed)
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt) {
-          u32x4 bk = lds_ld128(buf + C::KT_OFF + (dt * 16 + li) * C::KtTile::PITCH + (32 * c + 8 * g) * 2);
-          acc[0][dt] = mfma_bf16(dsa[0][c], bk, acc[0][dt]);
-          acc[1][dt] = mfma_bf16(dsa[1][c], bk, acc[1][dt]);
+          const uint8_t* kp = buf + kt_rd + c * 32 * C::P + dt * 32;
+          const u32x4 bk = cat_tr(lds_tr16(kp), lds_tr16(kp + 16 * C::P));
+          acc[0][dt] = mfma_bf16(dsa[0], bk, acc[0][dt]);
+          acc[1][dt] = mfma_bf16(dsa[1], bk, acc[1][dt]);
         }
       }
     }
 
     if (t + 1 < ntiles) store(smem + ((t + 1) & 1) * C::BUF);
     __syncthreads();
+  }
+
+  if constexpr (BIAS) {
+    if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
+    __syncthreads();
+    float* dst = p.dbias + (int64_t)h * (2 * p.bias_R - 1) + R1;
+    for (int i = tid; i < p.bias_R; i += kThreads) {
+      const float v = hist[i];
+      if (v != 0.f) atomicAdd(&dst[i], v * p.inv_n);
+    }
   }
 
   if (!wave_active) return;
@@ -856,31 +973,27 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dq_kernel(AttnParams p) 
   }
 }
 
-// =====================================================================
-// Backward dK / dV.  Block = 128 keys (32 per wave), query tiles of 64.
+// ---------------------------------------------------------------------
+// dK / dV.  Block = 128 keys (32 per wave), query tiles of 32.
 //   S = Q.K^T, dP = dO.V^T (C fragments: query 4g+r, key li)
 //   dV += P^T.dO, dK += dS^T.Q
-// =====================================================================
-template <int D, bool FP8>
+// ---------------------------------------------------------------------
+template <int D>
 struct DkvCfg {
-  static constexpr int BN = 128, BMQ = 64, QS = BMQ / 16, DT = D / 16, KS = D / 32;
-  static constexpr int ES = FP8 ? 1 : 2;
-  using QTile = CopyTile<BMQ, D, ES>;          // A operand of S
-  using DoTile = CopyTile<BMQ, D, 2>;          // A operand of dP
-  using QtTile = TransTile<BMQ, D, FP8>;       // B operand of dK
-  using DotTile = TransTile<BMQ, D, false>;    // B operand of dV
+  static constexpr int BN = 128, BMQ = 32, QS = BMQ / 16, DT = D / 16, KS = D / 32;
+  static constexpr int P = BwdPitch<D>::P;
   static constexpr int Q_OFF = 0;
-  static constexpr int DO_OFF = Q_OFF + BMQ * QTile::PITCH;
-  static constexpr int QT_OFF = DO_OFF + BMQ * DoTile::PITCH;
-  static constexpr int DOT_OFF = QT_OFF + D * QtTile::PITCH;
-  static constexpr int SQ_OFF = DOT_OFF + D * DotTile::PITCH;
-  static constexpr int BUF = SQ_OFF + (FP8 ? BMQ * 4 : 0);
+  static constexpr int DO_OFF = Q_OFF + BMQ * P;
+  static constexpr int SQ_OFF = DO_OFF + BMQ * P;
+  static constexpr int BIAS_OFF = SQ_OFF + BMQ * 4;
+  static constexpr int BUF = BIAS_OFF + (BN + BMQ) * 4;
   static constexpr int LDS = 2 * BUF;
 };
 
-template <int D, bool FP8, bool GENERIC>
-__global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dkdv_kernel(AttnParams p) {
-  using C = DkvCfg<D, FP8>;
+template <int D, bool FP8, bool GENERIC, bool BIAS>
+__global__ void __launch_bounds__(kThreads, D == 128 ? 1 : 2) hstu_bwd_dkdv_kernel(AttnParams p) {
+  using C = DkvCfg<D>;
+  constexpr int ES = FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
   const SeqCtx sc = seq_ctx(p, /*reverse=*/false);
@@ -893,53 +1006,36 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dkdv_kernel(AttnParams p
   const int kw0 = n0 + wave * 32;
   const bool wave_active = kw0 < L;
 
-  const int64_t qrs = p.q_rs * C::ES, krs = p.k_rs * C::ES, vrs = p.v_rs * C::ES, dors = p.do_rs * 2;
-  const uint8_t* qb = p.q + (sc.start * p.q_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * C::ES;
-  const uint8_t* dob = p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2;
-  const float* sqb = FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr;
+  const uint32_t qrs = (uint32_t)(p.q_rs * ES), dors = (uint32_t)(p.do_rs * 2);
+  const BufRsrc qrsrc = make_rsrc(p.q + (sc.start * p.q_rs + (int64_t)h * D) * ES,
+                                  (uint32_t)(L > 0 ? (L - 1) * qrs + D * ES : 0));
+  const BufRsrc dorsrc = make_rsrc(p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2,
+                                   (uint32_t)(L > 0 ? (L - 1) * dors + D * 2 : 0));
+  const uint32_t s_step = FP8 ? (uint32_t)(p.s_rs * 4) : 0u;
+  const uint32_t sbytes = FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u;
+  const BufRsrc sq_rsrc = make_rsrc(FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
+  const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
+  const int R1 = p.bias_R - 1;
 
-  // K and V fragments (B operands of S and dP): lane holds key kw0+16kt+li.
-  u32x4 kf[2][C::KS];
-  i32x8 kf8[2];
-  u32x4 vf[2][C::KS];
+  // K and V fragments (B operands): lane holds key kw0+16kt+li.  V is
+  // dequantized (scale applied) once here; K's scale goes into ck.
+  u32x4 kf[2][C::KS], vf[2][C::KS];
   float ck[2];
+  {
+    const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * ES;
+    const uint8_t* vb = p.v + (sc.start * p.v_rs + (int64_t)h * D) * ES;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    const int row = kw0 + kt * 16 + li;
-    const bool ok = row < L;
-    const uint8_t* ksrc = kb + (int64_t)row * krs;
-    const uint8_t* vsrc = vb + (int64_t)row * vrs;
-    ck[kt] = -p.alpha * kLog2e;
-    if constexpr (FP8) {
-      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
-      float sk = 0.f, sv = 0.f;
-      if (ok) {
-        lo = *(const u32x4*)(ksrc + 32 * g);
-        hi = *(const u32x4*)(ksrc + 32 * g + 16);
-        sk = p.k_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
-        sv = p.v_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
+    for (int kt = 0; kt < 2; ++kt) {
+      const int row = kw0 + kt * 16 + li;
+      const bool ok = row < L;
+      float sv = 1.f;
+      ck[kt] = -p.alpha * kLog2e;
+      if constexpr (FP8) {
+        sv = ok ? p.v_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 0.f;
+        ck[kt] *= ok ? p.k_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 0.f;
       }
-      kf8[kt] = cat8(lo, hi);
-      ck[kt] *= sk;
-#pragma unroll
-      for (int st = 0; st < C::KS; ++st) {
-        u32x2 w = {0u, 0u};
-        if (ok) w = *(const u32x2*)(vsrc + 32 * st + 8 * g);
-        u32x2 a = fp8x4_to_bf16x4(w[0], sv), b = fp8x4_to_bf16x4(w[1], sv);
-        vf[kt][st] = u32x4{a[0], a[1], b[0], b[1]};
-      }
-    } else {
-#pragma unroll
-      for (int st = 0; st < C::KS; ++st) {
-        kf[kt][st] = u32x4{0u, 0u, 0u, 0u};
-        vf[kt][st] = u32x4{0u, 0u, 0u, 0u};
-        if (ok) {
-          kf[kt][st] = *(const u32x4*)(ksrc + (32 * st + 8 * g) * 2);
-          vf[kt][st] = *(const u32x4*)(vsrc + (32 * st + 8 * g) * 2);
-        }
-      }
+      load_row_frag<D, FP8>(kf[kt], kb, p.k_rs * ES, row, ok, g, 1.f);
+      load_row_frag<D, FP8>(vf[kt], vb, p.v_rs * ES, row, ok, g, sv);
     }
   }
 
@@ -947,33 +1043,46 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dkdv_kernel(AttnParams p
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) {
-      dk[kt][dt] = zero4();
-      dv[kt][dt] = zero4();
-    }
+    for (int dt = 0; dt < C::DT; ++dt) dk[kt][dt] = dv[kt][dt] = zero4();
 
   const int m_begin = GENERIC ? 0 : n0;
   const int ntiles = (L - m_begin + C::BMQ - 1) / C::BMQ;
 
-  typename C::QTile q_ld;
-  typename C::DoTile do_ld;
-  typename C::QtTile qt_ld;
-  typename C::DotTile dot_ld;
-  ScaleTile<C::BMQ> sq_ld;
+  RowStage<C::BMQ, D, FP8> q_st;
+  RowStage<C::BMQ, D, false> do_st;
+  q_st.init(qrs, C::Q_OFF);
+  do_st.init(dors, C::DO_OFF);
+  float sq_v = 0.f, bias_v = 0.f;
   auto load = [&](int m0) {
-    q_ld.load(qb, qrs, m0, L);
-    do_ld.load(dob, dors, m0, L);
-    qt_ld.load(qb, qrs, sqb, p.s_rs, m0, L);
-    dot_ld.load(dob, dors, nullptr, 0, m0, L);
-    if constexpr (FP8) sq_ld.load(sqb, p.s_rs, m0, L);
+    q_st.load(qrsrc, m0 * qrs);
+    do_st.load(dorsrc, m0 * dors);
+    if constexpr (FP8) {
+      if (tid < C::BMQ) sq_v = buf_ldf(sq_rsrc, (uint32_t)tid * s_step, m0 * s_step);
+    }
+    if constexpr (BIAS) {
+      // offsets i-j of this tile span [m0-n0-(BN-1), m0-n0+BMQ-1]
+      if (tid < C::BN + C::BMQ - 1) {
+        const int off = m0 - n0 - (C::BN - 1) + tid;
+        bias_v = biasb[min(max(off, -R1), R1) + R1] * -kLog2e;
+      }
+    }
   };
   auto store = [&](uint8_t* buf) {
-    q_ld.store(buf + C::Q_OFF);
-    do_ld.store(buf + C::DO_OFF);
-    qt_ld.store(buf + C::QT_OFF);
-    dot_ld.store(buf + C::DOT_OFF);
-    if constexpr (FP8) sq_ld.store(buf + C::SQ_OFF);
+    q_st.store(buf);
+    do_st.store(buf);
+    if constexpr (FP8) {
+      if (tid < C::BMQ) ((float*)(buf + C::SQ_OFF))[tid] = sq_v;
+    }
+    if constexpr (BIAS) {
+      if (tid < C::BN + C::BMQ - 1) ((float*)(buf + C::BIAS_OFF))[tid] = bias_v;
+    }
   };
+
+  const int q_rd = C::Q_OFF + li * C::P + 16 * g;
+  const int do_rd = C::DO_OFF + li * C::P + 16 * g;
+  const int tr_rd = (4 * g + (li >> 2)) * C::P + (li & 3) * 8;  // tr16, relative to a tile
+  // bias index of element (qs, kt, r) = bias_rd + 16*(qs-kt) + r
+  const int bias_rd = (C::BN - 1) - 32 * wave + 4 * g - li;
 
   load(m_begin);
   store(smem);
@@ -985,77 +1094,79 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dkdv_kernel(AttnParams p
     if (t + 1 < ntiles) load(m0 + C::BMQ);
 
     if (wave_active && (GENERIC || m0 + C::BMQ - 1 >= kw0)) {
-      const bool need_mask = GENERIC || (m0 <= kw0 + 31);
       f32x4 s[C::QS][2], dp[C::QS][2];
 #pragma unroll
       for (int qs = 0; qs < C::QS; ++qs) {
-        const uint8_t* qrow = buf + C::Q_OFF + (qs * 16 + li) * C::QTile::PITCH;
-        const uint8_t* drow = buf + C::DO_OFF + (qs * 16 + li) * C::DoTile::PITCH;
-        if constexpr (FP8) {
-          i32x8 a = cat8(lds_ld128(qrow + 32 * g), lds_ld128(qrow + 32 * g + 16));
-          s[qs][0] = mfma_fp8(a, kf8[0], zero4());
-          s[qs][1] = mfma_fp8(a, kf8[1], zero4());
-        } else {
-          s[qs][0] = zero4();
-          s[qs][1] = zero4();
-#pragma unroll
-          for (int st = 0; st < C::KS; ++st) {
-            u32x4 a = lds_ld128(qrow + (32 * st + 8 * g) * 2);
-            s[qs][0] = mfma_bf16(a, kf[0][st], s[qs][0]);
-            s[qs][1] = mfma_bf16(a, kf[1][st], s[qs][1]);
-          }
-        }
-        dp[qs][0] = zero4();
-        dp[qs][1] = zero4();
+        s[qs][0] = s[qs][1] = dp[qs][0] = dp[qs][1] = zero4();
 #pragma unroll
         for (int st = 0; st < C::KS; ++st) {
-          u32x4 a = lds_ld128(drow + (32 * st + 8 * g) * 2);
-          dp[qs][0] = mfma_bf16(a, vf[0][st], dp[qs][0]);
-          dp[qs][1] = mfma_bf16(a, vf[1][st], dp[qs][1]);
+          const u32x4 a = lds_ld128(buf + q_rd + qs * 16 * C::P + st * 64);
+          s[qs][0] = mfma_bf16(a, kf[0][st], s[qs][0]);
+          s[qs][1] = mfma_bf16(a, kf[1][st], s[qs][1]);
+          const u32x4 b = lds_ld128(buf + do_rd + qs * 16 * C::P + st * 64);
+          dp[qs][0] = mfma_bf16(b, vf[0][st], dp[qs][0]);
+          dp[qs][1] = mfma_bf16(b, vf[1][st], dp[qs][1]);
         }
       }
-      u32x4 pa[2][C::BMQ / 32], dsa[2][C::BMQ / 32];
+      const bool need_mask = GENERIC || (m0 < kw0 + 31);
+      const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
+      const float* bias_lds = (const float*)(buf + C::BIAS_OFF);
+      u32x4 pa[2], dsa[2];
+      auto epilogue = [&](auto masked_tag, auto bconst_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
+        constexpr bool BCONST = decltype(bconst_tag)::value;
+        const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
 #pragma unroll
-      for (int qs = 0; qs < C::QS; ++qs) {
-        f32x4 sqv = {1.f, 1.f, 1.f, 1.f};
-        if constexpr (FP8) sqv = lds_ldf4(buf + C::SQ_OFF + (qs * 16 + 4 * g) * 4);
+        for (int qs = 0; qs < C::QS; ++qs) {
+          f32x4 sqv = {1.f, 1.f, 1.f, 1.f};
+          if constexpr (FP8) sqv = lds_ldf4(buf + C::SQ_OFF + (qs * 16 + 4 * g) * 4);
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          float pv[4], dsv[4];
+          for (int kt = 0; kt < 2; ++kt) {
+            float pv[4], dsv[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float t = s[qs][kt][r] * ck[kt];
-            if constexpr (FP8) t *= sqv[r];
-            const float sg = sig_of_t(t);
-            const float x = -kLn2 * t;
-            float pval = t * sg;
-            float dval = dp[qs][kt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
-            if (need_mask) {
-              const int i = m0 + qs * 16 + 4 * g + r, j = kw0 + kt * 16 + li;
-              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
-              pval = ok ? pval : 0.f;
-              dval = ok ? dval : 0.f;
+            for (int r = 0; r < 4; ++r) {
+              float t = s[qs][kt][r] * ck[kt];
+              if constexpr (FP8) t *= sqv[r];
+              if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + 16 * (qs - kt) + r];
+              const float sg = sig_of_t(t);
+              const float x = -kLn2 * t;
+              float pval = t * sg;
+              float dval = dp[qs][kt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+              if constexpr (FP8) dval *= sqv[r];
+              if constexpr (MASKED) {
+                const int i = m0 + qs * 16 + 4 * g + r, j = kw0 + kt * 16 + li;
+                const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+                pval = ok ? pval : 0.f;
+                dval = ok ? dval : 0.f;
+              }
+              pv[r] = pval;
+              dsv[r] = dval;
             }
-            pv[r] = pval;
-            dsv[r] = dval;
+            pa[kt][qs * 2 + 0] = pack_bf16(pv[0], pv[1]);
+            pa[kt][qs * 2 + 1] = pack_bf16(pv[2], pv[3]);
+            dsa[kt][qs * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
+            dsa[kt][qs * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
           }
-          pa[kt][qs >> 1][(qs & 1) * 2 + 0] = pack_bf16(pv[0], pv[1]);
-          pa[kt][qs >> 1][(qs & 1) * 2 + 1] = pack_bf16(pv[2], pv[3]);
-          dsa[kt][qs >> 1][(qs & 1) * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
-          dsa[kt][qs >> 1][(qs & 1) * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
         }
+      };
+      if (need_mask) {
+        if (bias_const) epilogue(std::true_type{}, std::true_type{});
+        else epilogue(std::true_type{}, std::false_type{});
+      } else {
+        if (bias_const) epilogue(std::false_type{}, std::true_type{});
+        else epilogue(std::false_type{}, std::false_type{});
       }
+      // ---- dV += P^T . dO, dK += dS^T . Q  (dO and Q rows read transposed)
 #pragma unroll
-      for (int c = 0; c < C::BMQ / 32; ++c) {
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) {
-          u32x4 bdo = lds_ld128(buf + C::DOT_OFF + (dt * 16 + li) * C::DotTile::PITCH + (32 * c + 8 * g) * 2);
-          u32x4 bq = lds_ld128(buf + C::QT_OFF + (dt * 16 + li) * C::QtTile::PITCH + (32 * c + 8 * g) * 2);
-          dv[0][dt] = mfma_bf16(pa[0][c], bdo, dv[0][dt]);
-          dv[1][dt] = mfma_bf16(pa[1][c], bdo, dv[1][dt]);
-          dk[0][dt] = mfma_bf16(dsa[0][c], bq, dk[0][dt]);
-          dk[1][dt] = mfma_bf16(dsa[1][c], bq, dk[1][dt]);
-        }
+      for (int dt = 0; dt < C::DT; ++dt) {
+        const uint8_t* dop = buf + C::DO_OFF + tr_rd + dt * 32;
+        const uint8_t* qp = buf + C::Q_OFF + tr_rd + dt * 32;
+        const u32x4 bdo = cat_tr(lds_tr16(dop), lds_tr16(dop + 16 * C::P));
+        const u32x4 bq = cat_tr(lds_tr16(qp), lds_tr16(qp + 16 * C::P));
+        dv[0][dt] = mfma_bf16(pa[0], bdo, dv[0][dt]);
+        dv[1][dt] = mfma_bf16(pa[1], bdo, dv[1][dt]);
+        dk[0][dt] = mfma_bf16(dsa[0], bq, dk[0][dt]);
+        dk[1][dt] = mfma_bf16(dsa[1], bq, dk[1][dt]);
       }
     }
 
@@ -1084,6 +1195,11 @@ __global__ void __launch_bounds__(kThreads, 1) hstu_bwd_dkdv_kernel(AttnParams p
   }
 }
 
+__global__ void fill_f32(float* p, int n, float v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
 // Rows of a sequence beyond max_seq_len are not computed by the kernels (the
 // reference's padded path drops them, so their output is zero); zero them so
 // every output element is written.  Exits at once when every L <= N.
@@ -1102,21 +1218,23 @@ __global__ void zero_rows_beyond_n(const int64_t* seq_offsets, int N, int width,
 }
 
 // ---------------------------------------------------------------- launch
-// Raise the dynamic-LDS limit once per kernel (the forward uses 70 KiB, the
-// dK/dV kernel 140 KiB of the 160 KiB a CU has).
-hipError_t ensure_lds(const void* fn, int lds) {
+// Raise each kernel's dynamic-LDS limit to the CU's 160 KiB once; the actual
+// allocation is the launch's size (the forward uses ~72 KiB, so two
+// workgroups share a CU).
+hipError_t ensure_lds(const void* fn) {
   static std::mutex mu;
   static std::vector<const void*> done;
   std::lock_guard<std::mutex> lock(mu);
   for (const void* d : done)
     if (d == fn) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (e == hipSuccess) done.push_back(fn);
   return e;
 }
 
 hipError_t launch(void (*kernel)(AttnParams), int lds, int grid, AttnParams p, hipStream_t stream) {
-  hipError_t e = ensure_lds((const void*)kernel, lds);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  hipError_t e = ensure_lds((const void*)kernel);
   if (e != hipSuccess) return e;
   void* args[] = {&p};
   return hipLaunchKernel((const void*)kernel, dim3(grid), dim3(kThreads), args, (size_t)lds, stream);
@@ -1218,7 +1336,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
                   int64_t dk_row_stride, int64_t dv_row_stride, float* dbias, hipStream_t stream) {
   if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
                     v_scale, bias_R, attn_bias) ||
-      dbias != nullptr || attn_bias != nullptr)
+      (dbias != nullptr && attn_bias == nullptr))
     return HSTU_E_BAD_ARG;
   if (!(D == 128 || (D == 64 && dtype == HSTU_DTYPE_BF16))) return HSTU_E_UNSUPPORTED;
   if (!row_alignment_ok(dtype, q_row_stride, q) || !row_alignment_ok(dtype, k_row_stride, k) ||
@@ -1261,30 +1379,44 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   p.blocks_per_seq = (max_seq_len + 127) / 128;
   const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
   const int grid = p.blocks_per_seq * B * H;
+  p.bias = attn_bias;
+  p.bias_R = bias_R;
+  p.dbias = dbias;
+  const bool has_bias = attn_bias != nullptr;
   hipError_t e;
   if (parts & kBwdDkdv) {
     // dK / dV: 128-key blocks, longest query range first.
-#define HSTU_DKV(DD, F8, G) launch(hstu_bwd_dkdv_kernel<DD, F8, G>, DkvCfg<DD, F8>::LDS, grid, p, stream)
+#define HSTU_DKV(DD, F8, G, BB) launch(hstu_bwd_dkdv_kernel<DD, F8, G, BB>, DkvCfg<DD>::LDS, grid, p, stream)
+#define HSTU_DKV_B(DD, F8, G) (has_bias ? HSTU_DKV(DD, F8, G, true) : HSTU_DKV(DD, F8, G, false))
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
-      e = generic ? HSTU_DKV(128, true, true) : HSTU_DKV(128, true, false);
+      e = generic ? HSTU_DKV_B(128, true, true) : HSTU_DKV_B(128, true, false);
     } else if (D == 128) {
-      e = generic ? HSTU_DKV(128, false, true) : HSTU_DKV(128, false, false);
+      e = generic ? HSTU_DKV_B(128, false, true) : HSTU_DKV_B(128, false, false);
     } else {
-      e = generic ? HSTU_DKV(64, false, true) : HSTU_DKV(64, false, false);
+      e = generic ? HSTU_DKV_B(64, false, true) : HSTU_DKV_B(64, false, false);
     }
+#undef HSTU_DKV_B
 #undef HSTU_DKV
     if (e != hipSuccess) return (int)e;
   }
   if (parts & kBwdDq) {
-    // dQ: 128-query blocks, longest key range first.
-#define HSTU_DQ(DD, F8, G) launch(hstu_bwd_dq_kernel<DD, F8, G>, DqCfg<DD, F8>::LDS, grid, p, stream)
-    if (dtype == HSTU_DTYPE_FP8_E4M3) {
-      e = generic ? HSTU_DQ(128, true, true) : HSTU_DQ(128, true, false);
-    } else if (D == 128) {
-      e = generic ? HSTU_DQ(128, false, true) : HSTU_DQ(128, false, false);
-    } else {
-      e = generic ? HSTU_DQ(64, false, true) : HSTU_DQ(64, false, false);
+    if (dbias != nullptr) {
+      const int n = H * (2 * bias_R - 1);
+      hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, dbias, n, 0.f);
     }
+    // dQ (+ bias gradient): 128-query blocks, longest key range first.
+    const int lds = DqCfg<128>::lds(has_bias, bias_R);
+    const int lds64 = DqCfg<64>::lds(has_bias, bias_R);
+#define HSTU_DQ(DD, F8, G, BB) launch(hstu_bwd_dq_kernel<DD, F8, G, BB>, DD == 128 ? lds : lds64, grid, p, stream)
+#define HSTU_DQ_B(DD, F8, G) (has_bias ? HSTU_DQ(DD, F8, G, true) : HSTU_DQ(DD, F8, G, false))
+    if (dtype == HSTU_DTYPE_FP8_E4M3) {
+      e = generic ? HSTU_DQ_B(128, true, true) : HSTU_DQ_B(128, true, false);
+    } else if (D == 128) {
+      e = generic ? HSTU_DQ_B(128, false, true) : HSTU_DQ_B(128, false, false);
+    } else {
+      e = generic ? HSTU_DQ_B(64, false, true) : HSTU_DQ_B(64, false, false);
+    }
+#undef HSTU_DQ_B
 #undef HSTU_DQ
     if (e != hipSuccess) return (int)e;
   }

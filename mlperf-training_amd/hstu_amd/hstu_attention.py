@@ -203,6 +203,9 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
     offs = _seq_offsets_i64(seq_offsets)
     nt = _num_targets_i32(num_targets)
     bias, R = _bias_args(attn_bias, H)
+    if dbias is not None:
+        if bias is None or dbias.shape != bias.shape or dbias.dtype != torch.float32 or not dbias.is_contiguous():
+            raise ValueError("dbias must be a contiguous fp32 tensor shaped like attn_bias")
     st = _lib.fn("hstu_attn_bwd")(
         _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16,
         dout.data_ptr(), _row_stride(dout),
@@ -249,7 +252,7 @@ def _op_fwd_fake(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len, cont
     return q.new_empty((q.shape[0], q.shape[1], v.shape[2]), dtype=torch.bfloat16)
 
 
-@torch.library.custom_op("hstu_amd::hstu_attention_bwd", mutates_args=("dq", "dk", "dv"))
+@torch.library.custom_op("hstu_amd::hstu_attention_bwd", mutates_args=("dq", "dk", "dv", "dbias"))
 def _op_bwd(
     dout: torch.Tensor,
     q: torch.Tensor,
@@ -268,19 +271,22 @@ def _op_bwd(
     k_scale: Optional[torch.Tensor],
     v_scale: Optional[torch.Tensor],
     attn_bias: Optional[torch.Tensor],
+    dbias: Optional[torch.Tensor],
 ) -> None:
     if dout.shape[0] == 0:
         dq.zero_()
         dk.zero_()
         dv.zero_()
+        if dbias is not None:
+            dbias.zero_()
         return
     _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, max_attn_len,
-                contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, None)
+                contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias)
 
 
 @_op_bwd.register_fake
 def _op_bwd_fake(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, max_attn_len,
-                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias):
+                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias):
     return None
 
 
@@ -351,10 +357,12 @@ def triton_hstu_attention_bwd(
     v_scale: ScaleArg = None,
     *,
     attn_bias: Optional[torch.Tensor] = None,
+    dbias: Optional[torch.Tensor] = None,
 ) -> None:
     """Backward op (``triton_hstu_attention.py:3298-3319``): writes dq, dk, dv
     in place (they may be strided views of a fused gradient buffer); an empty
-    batch zeroes them."""
+    batch zeroes them.  With ``attn_bias``, ``dbias`` (fp32, same shape, if
+    given) is overwritten with the bias gradient."""
     del sort_by_length_indices, enable_tma
     reason = unsupported_shape_reason(q, k, v, num_softmax_heads)
     if reason is not None:
@@ -365,7 +373,7 @@ def triton_hstu_attention_bwd(
             _scale_or_none(q_scale, q) if fp8 else None,
             _scale_or_none(k_scale, q) if fp8 else None,
             _scale_or_none(v_scale, q) if fp8 else None,
-            attn_bias)
+            attn_bias, dbias)
 
 
 # ---------------------------------------------------------------------------
@@ -451,11 +459,9 @@ class _AttentionFunction(torch.autograd.Function):
             dbias = None
             if attn_bias is not None:
                 dbias = torch.empty(attn_bias.shape, dtype=torch.float32, device=q.device)
-                _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, ctx.N, ctx.alpha,
-                            ctx.max_attn_len, ctx.contextual_seq_len, None, None, None, attn_bias, dbias)
-            else:
-                triton_hstu_attention_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, ctx.N,
-                                          ctx.alpha, ctx.max_attn_len, ctx.contextual_seq_len, None, False, 0)
+            triton_hstu_attention_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, ctx.N,
+                                      ctx.alpha, ctx.max_attn_len, ctx.contextual_seq_len, None, False, 0,
+                                      attn_bias=attn_bias, dbias=dbias)
         return (None, None, dq, dk, dv, None, None, None, None, None, None,
                 None if dbias is None else dbias.to(attn_bias.dtype))
 

@@ -255,3 +255,84 @@ def test_per_tensor_fp8_scales(hip_lib):
     ref = orc.hstu_mha_dense(N, 0.1, q8.double() * s, k8.double() * s, v8.double() * s, offs, dtype=torch.float64)
     err = orc.rel_l2(ref, out.float().cpu())
     assert err <= 1.5e-2, f"per-tensor fp8: rel L2 {err:.3e}"
+
+
+@pytest.mark.parametrize("R", [8, 1024])
+@pytest.mark.parametrize("dtype", ["bf16", "fp8"])
+def test_bwd_rel_bias(hip_lib, R, dtype):
+    """Backward with the relative-position bias: dq/dk/dv and the bias
+    gradient (a sum of dS over each diagonal offset) against autograd on the
+    float64 oracle."""
+    ops = _ops()
+    lengths = [300, 129, 1, 64, 200]
+    H, D = 2, 128
+    N = 300
+    bias = orc.make_bias(H, R, seed=3, std=0.5)
+    alpha = 1.0 / D ** 0.5
+    dout = torch.randn(sum(lengths), H, D, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    if dtype == "bf16":
+        q, k, v, offs = _case(lengths, H, D)
+        args = (q.to(DEV), k.to(DEV), v.to(DEV))
+        scales = ()
+        qd, kd, vd = q, k, v
+        bar = 1e-2
+    else:
+        q, k, v, offs = _case(lengths, H, D, std=1.0, dtype=torch.float32)
+        (q8, sq), (k8, sk), (v8, sv) = _quantize(q), _quantize(k), _quantize(v)
+        qd, kd, vd = (orc.dequantize(a, b) for a, b in ((q8, sq), (k8, sk), (v8, sv)))
+        args = (q8.to(DEV), k8.to(DEV), v8.to(DEV))
+        scales = (sq.to(DEV), sk.to(DEV), sv.to(DEV))
+        bar = 1.5e-2
+    dq, dk, dv = (torch.empty(q.shape, dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    db = torch.full(bias.shape, float("nan"), dtype=torch.float32, device=DEV)
+    ops.triton_hstu_attention_bwd(dout.to(DEV), *args, dq, dk, dv, offs.to(DEV), None, N, alpha, 0, 0, None,
+                                  False, 0, *scales, attn_bias=bias.to(DEV), dbias=db)
+    torch.cuda.synchronize()
+    rq, rk, rv, rb = orc.hstu_mha_bwd(N, alpha, qd, kd, vd, offs, dout, attn_bias=bias)
+    for name, got, r in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv), ("dbias", db, rb)):
+        err = orc.rel_l2(r, got.float().cpu())
+        assert err <= bar, f"bias bwd {dtype} R={R} {name}: rel L2 {err:.3e}"
+
+
+def test_autograd_rel_bias(hip_lib):
+    """triton_hstu_mha with attn_bias is differentiable in q, k, v and the bias."""
+    ops = _ops()
+    lengths = [90, 17, 160]
+    H, D, N = 2, 64, 160
+    q, k, v, offs = _case(lengths, H, D)
+    bias = orc.make_bias(H, 32, seed=5, std=0.3)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    bd = bias.to(DEV).requires_grad_(True)
+    out = ops.triton_hstu_mha(N, 0.125, qd, kd, vd, offs.to(DEV), attn_bias=bd)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    rq, rk, rv, rb = orc.hstu_mha_bwd(N, 0.125, q, k, v, offs, dout, attn_bias=bias)
+    for name, got, r in (("dq", qd.grad, rq), ("dk", kd.grad, rk), ("dv", vd.grad, rv), ("dbias", bd.grad, rb)):
+        err = orc.rel_l2(r, got.float().cpu())
+        assert err <= 1e-2, f"autograd bias {name}: rel L2 {err:.3e}"
+
+
+@pytest.mark.parametrize("mode", ["targets", "contextual"])
+def test_generic_masks_with_bias(hip_lib, mode):
+    ops = _ops()
+    lengths = [70, 33, 130, 5]
+    H, D, N = 2, 128, 130
+    q, k, v, offs = _case(lengths, H, D, seed=4)
+    nt = torch.tensor([3, 1, 20, 2], dtype=torch.int64) if mode == "targets" else None
+    ctx = 6 if mode == "contextual" else 0
+    bias = orc.make_bias(H, 16, seed=8, std=0.4)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    bd = bias.to(DEV).requires_grad_(True)
+    out = ops.triton_hstu_mha(N, 0.2, qd, kd, vd, offs.to(DEV), None if nt is None else nt.to(DEV), 0, ctx,
+                              attn_bias=bd)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.hstu_mha_dense(N, 0.2, q.double(), k.double(), v.double(), offs, nt, 0, ctx,
+                             attn_bias=bias.double(), dtype=torch.float64)
+    assert orc.rel_l2(ref, out.detach().float().cpu()) <= 1e-2
+    rq, rk, rv, rb = orc.hstu_mha_bwd(N, 0.2, q, k, v, offs, dout, nt, 0, ctx, attn_bias=bias)
+    for name, got, r in (("dq", qd.grad, rq), ("dk", kd.grad, rk), ("dv", vd.grad, rv), ("dbias", bd.grad, rb)):
+        err = orc.rel_l2(r, got.float().cpu())
+        assert err <= 1e-2, f"{mode} bias {name}: rel L2 {err:.3e}"
