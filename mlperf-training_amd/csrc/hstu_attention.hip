@@ -305,6 +305,56 @@ struct ScaleTile {
   }
 };
 
+
+// Global -> LDS tile copy without registers (buffer_load_dwordx4 ... lds).
+// One wave instruction writes 64 consecutive 16-byte LDS slots, so the tile's
+// padded rows are laid out as PITCH/16 slots per row and lane l of
+// instruction i fills slot 64i+l: a data slot loads its (row, chunk), a pad
+// slot reloads a data chunk of the same row (never read).  Rows beyond the
+// buffer's end read as zero.  Completion is tracked by vmcnt: wait_vm() then a
+// barrier before the tile is read.
+template <int ROWS, int ROW_BYTES, int PITCH>
+struct DirectTile {
+  static_assert(PITCH % 16 == 0 && ROW_BYTES % 16 == 0 && PITCH - ROW_BYTES <= ROW_BYTES, "layout");
+  static constexpr int CPR = PITCH / 16, DATA_CPR = ROW_BYTES / 16;
+  static constexpr int NINSTR = (ROWS * CPR + 63) / 64;
+  static constexpr int BYTES = NINSTR * 1024;  // LDS footprint, >= ROWS * PITCH
+  static constexpr int PER_WAVE = (NINSTR + kThreads / 64 - 1) / (kThreads / 64);
+  uint32_t voff[PER_WAVE];
+  __device__ __forceinline__ void init(uint32_t rs_bytes) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int c = (wave + 4 * j) * 64 + lane;
+      int row = c / CPR, col = c - (c / CPR) * CPR;
+      if (col >= DATA_CPR) col -= DATA_CPR;
+      row = row < ROWS ? row : ROWS - 1;
+      voff[j] = row * rs_bytes + col * 16;
+    }
+  }
+  __device__ __forceinline__ void load(BufRsrc rs, uint32_t soff, uint8_t* tile) const {
+    // Device pass only: the host pass cannot form the LDS address-space
+    // pointer, and a failed host instantiation would drop the kernel's
+    // launch stub.
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int i = wave + 4 * j;
+      if (i < NINSTR)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(tile + i * 1024), 16,
+                                                 voff[j], soff, 0, 0);
+    }
+#else
+    (void)rs;
+    (void)soff;
+    (void)tile;
+#endif
+  }
+};
+// vmcnt(0); expcnt and lgkmcnt left at their maxima.
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // ---------------------------------------------------------------- params
 struct AttnParams {
   const uint8_t* q;
@@ -666,8 +716,8 @@ template <int ROWS, int D, bool FP8>
 struct RowStage {
   static constexpr int ES = FP8 ? 1 : 2;
   static constexpr int CPR = D * ES / 16;  // 16-byte source chunks per row
-  static constexpr int N = ROWS * CPR / kThreads;
-  static_assert(N >= 1 && ROWS * CPR % kThreads == 0, "tile/thread mismatch");
+  static constexpr int ITEMS = ROWS * CPR;
+  static constexpr int N = (ITEMS + kThreads - 1) / kThreads;
   u32x4 r[N];
   uint32_t voff[N], loff[N];
   __device__ __forceinline__ void init(uint32_t rs_bytes, int lds_off) {
@@ -680,11 +730,14 @@ struct RowStage {
   }
   __device__ __forceinline__ void load(BufRsrc rs, uint32_t soff) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) r[i] = buf_ld128(rs, voff[i], soff);
+    for (int i = 0; i < N; ++i) {
+      if (ITEMS % kThreads == 0 || threadIdx.x + kThreads * i < ITEMS) r[i] = buf_ld128(rs, voff[i], soff);
+    }
   }
   __device__ __forceinline__ void store(uint8_t* buf) const {
 #pragma unroll
     for (int i = 0; i < N; ++i) {
+      if (!(ITEMS % kThreads == 0 || threadIdx.x + kThreads * i < ITEMS)) continue;
       if constexpr (FP8) {
         const u32x4 w = r[i];
         u32x4 lo, hi;
@@ -982,16 +1035,18 @@ template <int D>
 struct DkvCfg {
   static constexpr int BN = 128, BMQ = 32, QS = BMQ / 16, DT = D / 16, KS = D / 32;
   static constexpr int P = BwdPitch<D>::P;
+  using DTile = DirectTile<BMQ, D * 2, P>;  // bf16 rows straight from global
+  static constexpr int TILE = DTile::BYTES;
   static constexpr int Q_OFF = 0;
-  static constexpr int DO_OFF = Q_OFF + BMQ * P;
-  static constexpr int SQ_OFF = DO_OFF + BMQ * P;
+  static constexpr int DO_OFF = Q_OFF + TILE;
+  static constexpr int SQ_OFF = DO_OFF + TILE;
   static constexpr int BIAS_OFF = SQ_OFF + BMQ * 4;
   static constexpr int BUF = BIAS_OFF + (BN + BMQ) * 4;
   static constexpr int LDS = 2 * BUF;
 };
 
 template <int D, bool FP8, bool GENERIC, bool BIAS>
-__global__ void __launch_bounds__(kThreads, D == 128 ? 1 : 2) hstu_bwd_dkdv_kernel(AttnParams p) {
+__global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p) {
   using C = DkvCfg<D>;
   constexpr int ES = FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1048,14 +1103,18 @@ __global__ void __launch_bounds__(kThreads, D == 128 ? 1 : 2) hstu_bwd_dkdv_kern
   const int m_begin = GENERIC ? 0 : n0;
   const int ntiles = (L - m_begin + C::BMQ - 1) / C::BMQ;
 
-  RowStage<C::BMQ, D, FP8> q_st;
-  RowStage<C::BMQ, D, false> do_st;
-  q_st.init(qrs, C::Q_OFF);
-  do_st.init(dors, C::DO_OFF);
+  // dO (and bf16 Q) rows go global -> LDS directly; e4m3 Q is converted
+  // through registers.
+  RowStage<C::BMQ, D, true> q8_st;
+  typename C::DTile q_dt, do_dt;
+  if constexpr (FP8) q8_st.init(qrs, C::Q_OFF);
+  else q_dt.init(qrs);
+  do_dt.init(dors);
   float sq_v = 0.f, bias_v = 0.f;
-  auto load = [&](int m0) {
-    q_st.load(qrsrc, m0 * qrs);
-    do_st.load(dorsrc, m0 * dors);
+  auto load = [&](int m0, uint8_t* buf) {
+    if constexpr (FP8) q8_st.load(qrsrc, m0 * qrs);
+    else q_dt.load(qrsrc, m0 * qrs, buf + C::Q_OFF);
+    do_dt.load(dorsrc, m0 * dors, buf + C::DO_OFF);
     if constexpr (FP8) {
       if (tid < C::BMQ) sq_v = buf_ldf(sq_rsrc, (uint32_t)tid * s_step, m0 * s_step);
     }
@@ -1068,14 +1127,14 @@ __global__ void __launch_bounds__(kThreads, D == 128 ? 1 : 2) hstu_bwd_dkdv_kern
     }
   };
   auto store = [&](uint8_t* buf) {
-    q_st.store(buf);
-    do_st.store(buf);
+    if constexpr (FP8) q8_st.store(buf);
     if constexpr (FP8) {
       if (tid < C::BMQ) ((float*)(buf + C::SQ_OFF))[tid] = sq_v;
     }
     if constexpr (BIAS) {
       if (tid < C::BN + C::BMQ - 1) ((float*)(buf + C::BIAS_OFF))[tid] = bias_v;
     }
+    wait_vm();
   };
 
   const int q_rd = C::Q_OFF + li * C::P + 16 * g;
@@ -1084,14 +1143,14 @@ __global__ void __launch_bounds__(kThreads, D == 128 ? 1 : 2) hstu_bwd_dkdv_kern
   // bias index of element (qs, kt, r) = bias_rd + 16*(qs-kt) + r
   const int bias_rd = (C::BN - 1) - 32 * wave + 4 * g - li;
 
-  load(m_begin);
+  load(m_begin, smem);
   store(smem);
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
     const int m0 = m_begin + t * C::BMQ;
     const uint8_t* buf = smem + (t & 1) * C::BUF;
-    if (t + 1 < ntiles) load(m0 + C::BMQ);
+    if (t + 1 < ntiles) load(m0 + C::BMQ, smem + ((t + 1) & 1) * C::BUF);
 
     if (wave_active && (GENERIC || m0 + C::BMQ - 1 >= kw0)) {
       f32x4 s[C::QS][2], dp[C::QS][2];
