@@ -91,11 +91,13 @@ class Workload:
         self.fwd_args = (dt, self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), H * D, H * D, H * D,
                          sp(self.sq), sp(self.sk), sp(self.sv), srs, shs, self.offs.data_ptr(), B, H, D, N,
                          self.alpha, None, 0, 0, None, 0, self.out.data_ptr(), H * D, stream)
+        ws_bytes = lib.fn("hstu_attn_bwd_workspace_bytes")(dt, T, H, D, N, 0)
+        self.ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         self.bwd_args = (dt, self.dout.data_ptr(), H * D, self.q.data_ptr(), self.k.data_ptr(),
                          self.v.data_ptr(), H * D, H * D, H * D, sp(self.sq), sp(self.sk), sp(self.sv), srs, shs,
                          self.offs.data_ptr(), B, H, D, N, self.alpha, None, 0, 0, None, 0,
                          self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), H * D, H * D, H * D, None,
-                         stream)
+                         self.ws.data_ptr(), ws_bytes, T, stream)
         self.f_fwd = lib.fn("hstu_attn_fwd")
         self.f_dkdv = lib.fn("hstu_attn_bwd_dkdv")
         self.f_dq = lib.fn("hstu_attn_bwd_dq")

@@ -89,12 +89,23 @@ int hstu_attn_bwd(int dtype,
                   void* dq, void* dk, void* dv,
                   int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
                   float* dbias,
+                  void* workspace, int64_t workspace_bytes, int64_t total_tokens,
                   hipStream_t stream);
 
 /*
+ * Device workspace the backward needs (bytes; 0 = none): a pre-clamped copy
+ * of the bias rows when attn_bias is given, and an exact bf16 copy of q for
+ * e4m3 inputs.  total_tokens = T = seq_offsets[B].  The caller allocates it
+ * (the reference's FlyDSL backward likewise takes its dq-split workspace from
+ * the caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).
+ */
+int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int H, int D, int max_seq_len,
+                                      int has_bias);
+
+/*
  * The two halves of hstu_attn_bwd, same arguments: hstu_attn_bwd_dkdv writes
- * dk and dv only (dq may be NULL); hstu_attn_bwd_dq writes dq only (dk, dv may
- * be NULL).  They read the same inputs and may run concurrently on two
+ * dk and dv only (dq may be NULL; it alone uses the workspace);
+ * hstu_attn_bwd_dq writes dq and dbias only (dk, dv may be NULL).  They read the same inputs and may run concurrently on two
  * streams.  The reference launches its backward in the same two parts when
  * the dq-split is armed: the fused dK/dV kernel, then dq from the stored ds
  * tiles (ops/flydsl/hstu_flydsl_mha.py:1707-1740, ops/flydsl/hstu_dq_split.py:348);
@@ -107,7 +118,8 @@ int hstu_attn_bwd_dkdv(int dtype, const void* dout, int64_t dout_row_stride, con
                        int B, int H, int D, int max_seq_len, float alpha, const int32_t* num_targets,
                        int max_attn_len, int contextual_seq_len, const float* attn_bias, int bias_R,
                        void* dq, void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride,
-                       int64_t dv_row_stride, float* dbias, hipStream_t stream);
+                       int64_t dv_row_stride, float* dbias, void* workspace, int64_t workspace_bytes,
+                       int64_t total_tokens, hipStream_t stream);
 int hstu_attn_bwd_dq(int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
                      const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
                      const float* q_scale, const float* k_scale, const float* v_scale,
@@ -115,7 +127,8 @@ int hstu_attn_bwd_dq(int dtype, const void* dout, int64_t dout_row_stride, const
                      int B, int H, int D, int max_seq_len, float alpha, const int32_t* num_targets,
                      int max_attn_len, int contextual_seq_len, const float* attn_bias, int bias_R,
                      void* dq, void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride,
-                     int64_t dv_row_stride, float* dbias, hipStream_t stream);
+                     int64_t dv_row_stride, float* dbias, void* workspace, int64_t workspace_bytes,
+                     int64_t total_tokens, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -379,6 +379,8 @@ struct AttnParams {
   const float* bias;  // [H, 2*bias_R - 1] or null
   int bias_R;
   float* dbias;       // bias gradient, same shape (backward)
+  const float* bias_ext;  // workspace: pre-clamped, pre-scaled bias rows [H, 2N+192]
+  const uint8_t* q16;     // workspace: bf16 copy of e4m3 q, [T, H, D]
   int blocks_per_seq;  // grid = blocks_per_seq * B * H
 };
 
@@ -419,8 +421,11 @@ template <int D, bool FP8>
 struct FwdCfg {
   static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
   static constexpr int ES = FP8 ? 1 : 2;
-  static constexpr int KP = D * ES + 16;  // K row pitch (A-operand rows, b128 reads)
-  static constexpr int VP = D * 2 + 32;   // bf16 V row pitch (tr16 reads: 4 rows x 32 B disjoint)
+  // Row pitches of row bytes + 32 (== 32 mod 64): the pitch at which 16-row
+  // ds_read_b128 operand reads and ds_read_b64_tr_b16 reads run without bank
+  // conflicts on gfx950 (measured: 2x the b128 bandwidth of +16 or +48).
+  static constexpr int KP = D * ES + 32;
+  static constexpr int VP = D * 2 + 32;
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = K_OFF + BN * KP;
   static constexpr int SC_OFF = V_OFF + BN * VP;              // e4m3: (sk, sv) per key
@@ -503,8 +508,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
       u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
       float s = 0.f;
       if (ok) {
-        lo = *(const u32x4*)(src + 32 * g);
-        hi = *(const u32x4*)(src + 32 * g + 16);
+        lo = *(const u32x4*)(src + 16 * g);
+        hi = *(const u32x4*)(src + 64 + 16 * g);
         s = p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs];
       }
       qf8[qt] = cat8(lo, hi);
@@ -580,7 +585,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   };
 
   // Per-lane LDS addresses (tile-invariant).
-  const int k_rd = C::K_OFF + li * C::KP + (FP8 ? 32 * g : 16 * g);
+  // e4m3: lane group g holds the 16-byte k-chunks g and g+4 of a row (the
+  // same order in both MFMA operands), so each b128 read is conflict-free.
+  const int k_rd = C::K_OFF + li * C::KP + 16 * g;
   // tr16: lane j of group g addresses row 4g + j/4 (+16 for the second half), column 4*(j%4)
   const int v_rd = C::V_OFF + (4 * g + (li >> 2)) * C::VP + (li & 3) * 8;
   // bias index of element (qt, kt, r) = bias_rd + 16*(qt-kt) - r
@@ -602,7 +609,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
       for (int kt = 0; kt < C::KT; ++kt) {
         const uint8_t* krow = buf + k_rd + kt * 16 * C::KP;
         if constexpr (FP8) {
-          i32x8 a = cat8(lds_ld128(krow), lds_ld128(krow + 16));
+          i32x8 a = cat8(lds_ld128(krow), lds_ld128(krow + 64));
           s[kt][0] = mfma_fp8(a, qf8[0], zero4());
           s[kt][1] = mfma_fp8(a, qf8[1], zero4());
         } else {
@@ -702,13 +709,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
 // inputs are converted exactly, scale 1, while staging; the per-row scales
 // are applied in the epilogue), so one LDS copy of a tile serves as an A
 // operand (row reads, ds_read_b128) and as a B operand (ds_read_b64_tr_b16).
-// A row pitch of 2D+48 bytes keeps both read patterns free of bank
-// conflicts: 16 consecutive rows fall on 16 distinct 16-byte bank groups,
-// and 4 consecutive rows x 32 bytes fall on disjoint ranges.
+// A row pitch of 2D+32 bytes (== 32 mod 64) keeps both read patterns free
+// of bank conflicts.
 // =====================================================================
 template <int D>
 struct BwdPitch {
-  static constexpr int P = D * 2 + 48;
+  static constexpr int P = D * 2 + 32;
 };
 
 // ROWS x D input rows (bf16, or e4m3 converted exactly) -> bf16 LDS rows.
@@ -1030,24 +1036,41 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
 // dK / dV.  Block = 128 keys (32 per wave), query tiles of 32.
 //   S = Q.K^T, dP = dO.V^T (C fragments: query 4g+r, key li)
 //   dV += P^T.dO, dK += dS^T.Q
+// A query tile is too little work to hide a global load behind, so tiles
+// stream through a 3-stage LDS ring fed only by direct global->LDS loads
+// (bf16 Q -- for e4m3 inputs an exact bf16 copy made by a prepass --, dO,
+// the per-query scales and the bias band), with the same number of load
+// instructions per wave per tile so that one vmcnt bound covers a tile.
 // ---------------------------------------------------------------------
-template <int D>
+template <int D, bool FP8, bool BIAS>
 struct DkvCfg {
   static constexpr int BN = 128, BMQ = 32, QS = BMQ / 16, DT = D / 16, KS = D / 32;
+  static constexpr int NSTAGE = 3;
   static constexpr int P = BwdPitch<D>::P;
-  using DTile = DirectTile<BMQ, D * 2, P>;  // bf16 rows straight from global
+  using DTile = DirectTile<BMQ, D * 2, P>;
   static constexpr int TILE = DTile::BYTES;
   static constexpr int Q_OFF = 0;
   static constexpr int DO_OFF = Q_OFF + TILE;
-  static constexpr int SQ_OFF = DO_OFF + TILE;
-  static constexpr int BIAS_OFF = SQ_OFF + BMQ * 4;
-  static constexpr int BUF = BIAS_OFF + (BN + BMQ) * 4;
-  static constexpr int LDS = 2 * BUF;
+  static constexpr int SQ_OFF = DO_OFF + TILE;   // 64 floats (one 4-byte load instruction)
+  static constexpr int BIAS_OFF = SQ_OFF + 256;  // 192 floats (three)
+  static constexpr int DUMMY_OFF = BIAS_OFF + 768;
+  static constexpr int STAGE = DUMMY_OFF + 1024;
+  static constexpr int N_Q = DTile::NINSTR, N_DO = DTile::NINSTR, N_SQ = FP8 ? 1 : 0, N_BIAS = BIAS ? 3 : 0;
+  static constexpr int N_REAL = N_Q + N_DO + N_SQ + N_BIAS;
+  static constexpr int CNT = (N_REAL + 3) / 4;  // load instructions per wave per tile
+  static constexpr int LDS = NSTAGE * STAGE;
 };
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 template <int D, bool FP8, bool GENERIC, bool BIAS>
 __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p) {
-  using C = DkvCfg<D>;
+  using C = DkvCfg<D, FP8, BIAS>;
   constexpr int ES = FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
@@ -1061,16 +1084,21 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   const int kw0 = n0 + wave * 32;
   const bool wave_active = kw0 < L;
 
-  const uint32_t qrs = (uint32_t)(p.q_rs * ES), dors = (uint32_t)(p.do_rs * 2);
-  const BufRsrc qrsrc = make_rsrc(p.q + (sc.start * p.q_rs + (int64_t)h * D) * ES,
-                                  (uint32_t)(L > 0 ? (L - 1) * qrs + D * ES : 0));
+  // bf16 Q rows: the input itself, or the prepass's copy of the e4m3 input.
+  const uint8_t* q16 = FP8 ? p.q16 + (sc.start * p.H + h) * (int64_t)D * 2
+                           : p.q + (sc.start * p.q_rs + (int64_t)h * D) * 2;
+  const uint32_t qrs = FP8 ? (uint32_t)(p.H * D * 2) : (uint32_t)(p.q_rs * 2);
+  const uint32_t dors = (uint32_t)(p.do_rs * 2);
+  const BufRsrc qrsrc = make_rsrc(q16, (uint32_t)(L > 0 ? (L - 1) * qrs + D * 2 : 0));
   const BufRsrc dorsrc = make_rsrc(p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2,
                                    (uint32_t)(L > 0 ? (L - 1) * dors + D * 2 : 0));
   const uint32_t s_step = FP8 ? (uint32_t)(p.s_rs * 4) : 0u;
-  const uint32_t sbytes = FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u;
-  const BufRsrc sq_rsrc = make_rsrc(FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
-  const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
-  const int R1 = p.bias_R - 1;
+  const BufRsrc sq_rsrc = make_rsrc(FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr,
+                                    FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u);
+  // pre-clamped, pre-scaled bias table: entry off + N + 127 holds the bias of offset off
+  const int ext_len = 2 * p.N + 192;
+  const BufRsrc b_rsrc = make_rsrc(BIAS ? p.bias_ext + (int64_t)h * ext_len : nullptr,
+                                   BIAS ? (uint32_t)(ext_len * 4) : 0u);
 
   // K and V fragments (B operands): lane holds key kw0+16kt+li.  V is
   // dequantized (scale applied) once here; K's scale goes into ck.
@@ -1103,38 +1131,48 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   const int m_begin = GENERIC ? 0 : n0;
   const int ntiles = (L - m_begin + C::BMQ - 1) / C::BMQ;
 
-  // dO (and bf16 Q) rows go global -> LDS directly; e4m3 Q is converted
-  // through registers.
-  RowStage<C::BMQ, D, true> q8_st;
-  typename C::DTile q_dt, do_dt;
-  if constexpr (FP8) q8_st.init(qrs, C::Q_OFF);
-  else q_dt.init(qrs);
-  do_dt.init(dors);
-  float sq_v = 0.f, bias_v = 0.f;
-  auto load = [&](int m0, uint8_t* buf) {
-    if constexpr (FP8) q8_st.load(qrsrc, m0 * qrs);
-    else q_dt.load(qrsrc, m0 * qrs, buf + C::Q_OFF);
-    do_dt.load(dorsrc, m0 * dors, buf + C::DO_OFF);
-    if constexpr (FP8) {
-      if (tid < C::BMQ) sq_v = buf_ldf(sq_rsrc, (uint32_t)tid * s_step, m0 * s_step);
-    }
-    if constexpr (BIAS) {
-      // offsets i-j of this tile span [m0-n0-(BN-1), m0-n0+BMQ-1]
-      if (tid < C::BN + C::BMQ - 1) {
-        const int off = m0 - n0 - (C::BN - 1) + tid;
-        bias_v = biasb[min(max(off, -R1), R1) + R1] * -kLog2e;
+  // Per-lane global offset of this wave's load instruction j (slot = wave + 4j);
+  // recomputed at each issue rather than held in registers.
+  auto voff_of = [&](int slot) -> uint32_t {
+    const int c = (slot < C::N_Q ? slot : slot - C::N_Q) * 64 + lane;
+    int row = c / (C::P / 16), col = c % (C::P / 16);
+    if (col >= D * 2 / 16) col -= D * 2 / 16;
+    row = row < C::BMQ ? row : C::BMQ - 1;
+    if (slot < C::N_Q) return row * qrs + col * 16;
+    if (slot < C::N_Q + C::N_DO) return row * dors + col * 16;
+    if (FP8 && slot == C::N_Q + C::N_DO) return (uint32_t)min(lane, C::BMQ - 1) * s_step;
+    if (BIAS && slot < C::N_REAL) return (uint32_t)((slot - C::N_Q - C::N_DO - C::N_SQ) * 64 + lane) * 4;
+    return 0u;
+  };
+  auto issue = [&](int m0, uint8_t* stage) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef __attribute__((address_space(3))) void lds_t;
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int j = 0; j < C::CNT; ++j) {
+      const int slot = w + 4 * j;
+      const uint32_t vo = voff_of(slot);
+      if (slot < C::N_Q) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16, vo,
+                                                 m0 * qrs, 0, 0);
+      } else if (slot < C::N_Q + C::N_DO) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - C::N_Q) * 1024),
+                                                 16, vo, m0 * dors, 0, 0);
+      } else if (FP8 && slot == C::N_Q + C::N_DO) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4, vo, m0 * s_step, 0,
+                                                 0);
+      } else if (BIAS && slot < C::N_REAL) {
+        const int b = slot - C::N_Q - C::N_DO - C::N_SQ;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4, vo,
+                                                 (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
+      } else {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, vo, 0, 0, 0);
       }
     }
-  };
-  auto store = [&](uint8_t* buf) {
-    if constexpr (FP8) q8_st.store(buf);
-    if constexpr (FP8) {
-      if (tid < C::BMQ) ((float*)(buf + C::SQ_OFF))[tid] = sq_v;
-    }
-    if constexpr (BIAS) {
-      if (tid < C::BN + C::BMQ - 1) ((float*)(buf + C::BIAS_OFF))[tid] = bias_v;
-    }
-    wait_vm();
+#else
+    (void)m0;
+    (void)stage;
+#endif
   };
 
   const int q_rd = C::Q_OFF + li * C::P + 16 * g;
@@ -1142,15 +1180,27 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   const int tr_rd = (4 * g + (li >> 2)) * C::P + (li & 3) * 8;  // tr16, relative to a tile
   // bias index of element (qs, kt, r) = bias_rd + 16*(qs-kt) + r
   const int bias_rd = (C::BN - 1) - 32 * wave + 4 * g - li;
+  const int R1 = p.bias_R - 1;
 
-  load(m_begin, smem);
-  store(smem);
+#pragma unroll
+  for (int st = 0; st < C::NSTAGE - 1; ++st) issue(m_begin + st * C::BMQ, smem + st * C::STAGE);
+  wait_vm_le<(C::NSTAGE - 2) * C::CNT>();
   __syncthreads();
 
-  for (int t = 0; t < ntiles; ++t) {
+  int cur = 0;  // stage holding the current tile
+  // One query tile; MASKED / BCONST select the epilogue at compile time so
+  // each loop below has a single code path (two paths in one loop push the
+  // register allocation past the 256 VGPRs of two waves per SIMD).
+  auto tile_body = [&](int t, auto masked_tag, auto bconst_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool BCONST = decltype(bconst_tag)::value;
     const int m0 = m_begin + t * C::BMQ;
-    const uint8_t* buf = smem + (t & 1) * C::BUF;
-    if (t + 1 < ntiles) load(m0 + C::BMQ, smem + ((t + 1) & 1) * C::BUF);
+    const uint8_t* buf = smem + cur * C::STAGE;
+    {
+      int nxt = cur + C::NSTAGE - 1;
+      nxt = nxt >= C::NSTAGE ? nxt - C::NSTAGE : nxt;
+      issue(m0 + (C::NSTAGE - 1) * C::BMQ, smem + nxt * C::STAGE);
+    }
 
     if (wave_active && (GENERIC || m0 + C::BMQ - 1 >= kw0)) {
       f32x4 s[C::QS][2], dp[C::QS][2];
@@ -1167,53 +1217,40 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
           dp[qs][1] = mfma_bf16(b, vf[1][st], dp[qs][1]);
         }
       }
-      const bool need_mask = GENERIC || (m0 < kw0 + 31);
-      const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
       const float* bias_lds = (const float*)(buf + C::BIAS_OFF);
+      const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
       u32x4 pa[2], dsa[2];
-      auto epilogue = [&](auto masked_tag, auto bconst_tag) {
-        constexpr bool MASKED = decltype(masked_tag)::value;
-        constexpr bool BCONST = decltype(bconst_tag)::value;
-        const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
 #pragma unroll
-        for (int qs = 0; qs < C::QS; ++qs) {
-          f32x4 sqv = {1.f, 1.f, 1.f, 1.f};
-          if constexpr (FP8) sqv = lds_ldf4(buf + C::SQ_OFF + (qs * 16 + 4 * g) * 4);
+      for (int qs = 0; qs < C::QS; ++qs) {
+        f32x4 sqv = {1.f, 1.f, 1.f, 1.f};
+        if constexpr (FP8) sqv = lds_ldf4(buf + C::SQ_OFF + (qs * 16 + 4 * g) * 4);
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
-            float pv[4], dsv[4];
+        for (int kt = 0; kt < 2; ++kt) {
+          float pv[4], dsv[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float t = s[qs][kt][r] * ck[kt];
-              if constexpr (FP8) t *= sqv[r];
-              if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + 16 * (qs - kt) + r];
-              const float sg = sig_of_t(t);
-              const float x = -kLn2 * t;
-              float pval = t * sg;
-              float dval = dp[qs][kt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
-              if constexpr (FP8) dval *= sqv[r];
-              if constexpr (MASKED) {
-                const int i = m0 + qs * 16 + 4 * g + r, j = kw0 + kt * 16 + li;
-                const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
-                pval = ok ? pval : 0.f;
-                dval = ok ? dval : 0.f;
-              }
-              pv[r] = pval;
-              dsv[r] = dval;
+          for (int r = 0; r < 4; ++r) {
+            float t = s[qs][kt][r] * ck[kt];
+            if constexpr (FP8) t *= sqv[r];
+            if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + 16 * (qs - kt) + r];
+            const float sg = sig_of_t(t);
+            const float x = -kLn2 * t;
+            float pval = t * sg;
+            float dval = dp[qs][kt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+            if constexpr (FP8) dval *= sqv[r];
+            if constexpr (MASKED) {
+              const int i = m0 + qs * 16 + 4 * g + r, j = kw0 + kt * 16 + li;
+              const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
+              pval = ok ? pval : 0.f;
+              dval = ok ? dval : 0.f;
             }
-            pa[kt][qs * 2 + 0] = pack_bf16(pv[0], pv[1]);
-            pa[kt][qs * 2 + 1] = pack_bf16(pv[2], pv[3]);
-            dsa[kt][qs * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
-            dsa[kt][qs * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
+            pv[r] = pval;
+            dsv[r] = dval;
           }
+          pa[kt][qs * 2 + 0] = pack_bf16(pv[0], pv[1]);
+          pa[kt][qs * 2 + 1] = pack_bf16(pv[2], pv[3]);
+          dsa[kt][qs * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
+          dsa[kt][qs * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
         }
-      };
-      if (need_mask) {
-        if (bias_const) epilogue(std::true_type{}, std::true_type{});
-        else epilogue(std::true_type{}, std::false_type{});
-      } else {
-        if (bias_const) epilogue(std::false_type{}, std::true_type{});
-        else epilogue(std::false_type{}, std::false_type{});
       }
       // ---- dV += P^T . dO, dK += dS^T . Q  (dO and Q rows read transposed)
 #pragma unroll
@@ -1229,8 +1266,22 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
       }
     }
 
-    if (t + 1 < ntiles) store(smem + ((t + 1) & 1) * C::BUF);
+    wait_vm_le<(C::NSTAGE - 2) * C::CNT>();
     __syncthreads();
+    cur = cur + 1 == C::NSTAGE ? 0 : cur + 1;
+  };
+
+  // Tiles [0, t_mask) touch the diagonal of some wave's keys (queries below
+  // n0 + BN - 1); tiles from t_const on have every offset i-j >= R-1 and so a
+  // constant bias.
+  const int t_mask = GENERIC ? ntiles : min(ntiles, (C::BN - 1 + C::BMQ - 1) / C::BMQ);
+  int t_const = ntiles;
+  if (BIAS && !GENERIC) t_const = max(t_mask, min(ntiles, (R1 + C::BN - 1 + C::BMQ - 1) / C::BMQ));
+  int t = 0;
+  for (; t < t_mask; ++t) tile_body(t, std::true_type{}, std::false_type{});
+  for (; t < t_const; ++t) tile_body(t, std::false_type{}, std::false_type{});
+  if constexpr (BIAS) {
+    for (; t < ntiles; ++t) tile_body(t, std::false_type{}, std::true_type{});
   }
 
   if (!wave_active) return;
@@ -1251,6 +1302,41 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
         }
       }
     }
+  }
+}
+
+// e4m3 q rows -> exact bf16 copy [T, H, D] for the dK/dV kernel (scale 1).
+__global__ void convert_q8_bf16(const uint8_t* q8, int64_t q_rs, const int64_t* seq_offsets, int B, int H, int D,
+                                uint16_t* q16) {
+  const int64_t T = seq_offsets[B];
+  const int cpr = H * D / 16;  // 16-element chunks per token
+  const int64_t n = T * cpr;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / cpr;
+    const int c = (int)(i - t * cpr);
+    const u32x4 w = *(const u32x4*)(q8 + t * q_rs + c * 16);
+    u32x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      lo[2 * e] = cvt_fp8x2_bf16<false>(w[e]);
+      lo[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e]);
+      hi[2 * e] = cvt_fp8x2_bf16<false>(w[e + 2]);
+      hi[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e + 2]);
+    }
+    u32x4* dst = (u32x4*)(q16 + t * (int64_t)H * D + c * 16);
+    dst[0] = lo;
+    dst[1] = hi;
+  }
+}
+
+// bias table [H, 2R-1] -> [H, 2N+192] with entry off+N+127 = bias(clamp(off)) * -log2(e)
+__global__ void build_bias_ext(const float* bias, int H, int R, int N, float* ext) {
+  const int len = 2 * N + 192;
+  const int h = blockIdx.y;
+  const int R1 = R - 1;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < len; i += gridDim.x * blockDim.x) {
+    const int off = i - N - 127;
+    ext[(int64_t)h * len + i] = bias[(int64_t)h * (2 * R - 1) + min(max(off, -R1), R1) + R1] * -kLog2e;
   }
 }
 
@@ -1386,13 +1472,21 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
 namespace {
 enum BwdParts { kBwdDkdv = 1, kBwdDq = 2, kBwdAll = 3 };
 
+int64_t bias_ext_bytes(int H, int N) { return ((int64_t)H * (2 * N + 192) * 4 + 255) / 256 * 256; }
+int64_t bwd_workspace_bytes(int dtype, int64_t T, int H, int D, int N, bool bias) {
+  int64_t b = bias ? bias_ext_bytes(H, N) : 0;
+  if (dtype == HSTU_DTYPE_FP8_E4M3) b += T * H * D * 2;
+  return b;
+}
+
 int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
                   const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
                   const float* q_scale, const float* k_scale, const float* v_scale, int64_t scale_row_stride,
                   int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
                   float alpha, const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
                   const float* attn_bias, int bias_R, void* dq, void* dk, void* dv, int64_t dq_row_stride,
-                  int64_t dk_row_stride, int64_t dv_row_stride, float* dbias, hipStream_t stream) {
+                  int64_t dk_row_stride, int64_t dv_row_stride, float* dbias, void* workspace,
+                  int64_t workspace_bytes, int64_t total_tokens, hipStream_t stream) {
   if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
                     v_scale, bias_R, attn_bias) ||
       (dbias != nullptr && attn_bias == nullptr))
@@ -1444,8 +1538,23 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   const bool has_bias = attn_bias != nullptr;
   hipError_t e;
   if (parts & kBwdDkdv) {
+    if (total_tokens < 0 || workspace_bytes < bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias) ||
+        (workspace == nullptr && bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias) > 0))
+      return HSTU_E_BAD_ARG;
+    uint8_t* ws = (uint8_t*)workspace;
+    if (has_bias) {
+      p.bias_ext = (const float*)ws;
+      hipLaunchKernelGGL(build_bias_ext, dim3((2 * max_seq_len + 192 + 255) / 256, H), dim3(256), 0, stream,
+                         attn_bias, H, bias_R, max_seq_len, (float*)ws);
+      ws += bias_ext_bytes(H, max_seq_len);
+    }
+    if (dtype == HSTU_DTYPE_FP8_E4M3) {
+      p.q16 = ws;
+      hipLaunchKernelGGL(convert_q8_bf16, dim3(1024), dim3(256), 0, stream, (const uint8_t*)q, q_row_stride,
+                         seq_offsets, B, H, D, (uint16_t*)ws);
+    }
     // dK / dV: 128-key blocks, longest query range first.
-#define HSTU_DKV(DD, F8, G, BB) launch(hstu_bwd_dkdv_kernel<DD, F8, G, BB>, DkvCfg<DD>::LDS, grid, p, stream)
+#define HSTU_DKV(DD, F8, G, BB) launch(hstu_bwd_dkdv_kernel<DD, F8, G, BB>, DkvCfg<DD, F8, BB>::LDS, grid, p, stream)
 #define HSTU_DKV_B(DD, F8, G) (has_bias ? HSTU_DKV(DD, F8, G, true) : HSTU_DKV(DD, F8, G, false))
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
       e = generic ? HSTU_DKV_B(128, true, true) : HSTU_DKV_B(128, true, false);
@@ -1491,7 +1600,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   dtype, dout, dout_row_stride, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale, \
       scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, num_targets,             \
       max_attn_len, contextual_seq_len, attn_bias, bias_R, dq, dk, dv, dq_row_stride, dk_row_stride,          \
-      dv_row_stride, dbias, stream
+      dv_row_stride, dbias, workspace, workspace_bytes, total_tokens, stream
 #define HSTU_BWD_PARAMS                                                                                        \
   int dtype, const void *dout, int64_t dout_row_stride, const void *q, const void *k, const void *v,           \
       int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, const float *q_scale,                 \
@@ -1499,8 +1608,13 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
       const int64_t *seq_offsets, int B, int H, int D, int max_seq_len, float alpha,                          \
       const int32_t *num_targets, int max_attn_len, int contextual_seq_len, const float *attn_bias,           \
       int bias_R, void *dq, void *dk, void *dv, int64_t dq_row_stride, int64_t dk_row_stride,                 \
-      int64_t dv_row_stride, float *dbias, hipStream_t stream
+      int64_t dv_row_stride, float *dbias, void *workspace, int64_t workspace_bytes, int64_t total_tokens,        \
+      hipStream_t stream
 
+extern "C" int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int H, int D, int max_seq_len,
+                                                 int has_bias) {
+  return bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias != 0);
+}
 extern "C" int hstu_attn_bwd(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdAll, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dkdv(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDkdv, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dq(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDq, HSTU_BWD_ARGS); }

@@ -206,6 +206,9 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
     if dbias is not None:
         if bias is None or dbias.shape != bias.shape or dbias.dtype != torch.float32 or not dbias.is_contiguous():
             raise ValueError("dbias must be a contiguous fp32 tensor shaped like attn_bias")
+    dtype_code = _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16
+    ws_bytes = _lib.fn("hstu_attn_bwd_workspace_bytes")(dtype_code, T, H, D, int(N), int(bias is not None))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     st = _lib.fn("hstu_attn_bwd")(
         _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16,
         dout.data_ptr(), _row_stride(dout),
@@ -216,7 +219,7 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
         _lib.ptr(bias), R,
         targets[0].data_ptr(), targets[1].data_ptr(), targets[2].data_ptr(),
         _row_stride(targets[0]), _row_stride(targets[1]), _row_stride(targets[2]),
-        _lib.ptr(dbias), _stream(q.device))
+        _lib.ptr(dbias), ws.data_ptr(), ws_bytes, T, _stream(q.device))
     _lib.check(st, "hstu_attn_bwd")
     for dst, src in zip((dq, dk, dv), targets):
         if dst is not src:
