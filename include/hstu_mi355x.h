@@ -130,6 +130,45 @@ int hstu_attn_bwd_dq(int dtype, const void* dout, int64_t dout_row_stride, const
                      int64_t dv_row_stride, float* dbias, void* workspace, int64_t workspace_bytes,
                      int64_t total_tokens, hipStream_t stream);
 
+/*
+ * FP8 e4m3 projection GEMM: C[m][n] = epilogue(sum_k A[m][k] * W[n][k]).
+ *   A: [M, K] e4m3 row-major, lda bytes; a_scale: a_scale_mode 0 -> one
+ *      fp32 scalar, 1 -> [M] per row.
+ *   W: [N, K] e4m3 row-major (the transposed weight), ldw bytes; w_scale:
+ *      w_scale_mode 0 -> scalar, 1 -> [N] per output column.
+ *   epilogue: v = acc * sa * sw [+ bias[n] (bf16 [N])]; v = silu(v) for
+ *      silu_begin <= n < silu_end; [+ residual[m][n] (bf16, ldr elements)];
+ *      out_dtype HSTU_DTYPE_BF16 -> bf16 C, HSTU_DTYPE_FP8_E4M3 -> e4m3 of
+ *      clamp(v / out_scale[0], +-448).  ldc in elements.
+ *   N % 128 == 0, K % 128 == 0; any M (rows past M are not touched).
+ * Replaces: k512_fp8_gemm_e4m3_bias_N{N}(A, B, C, bias, sa, sb, M, stream),
+ *           ops/hip/k512_fp8_gemm.cu:555-578 (e4m3 out, K=512); the K=1536
+ *           residual add-mm k1536_fp8_addmm_res_bf16_N512, ops/hip/k1536_fp8_addmm.cu:435-441;
+ *           and the hipBLASLt scaled GEMMs behind scaled_addmm_fp8_preq /
+ *           scaled_mm_fp8_out_preq (ops/triton/triton_fp8.py:1756, 2409).
+ */
+int hstu_fp8_gemm_rowcol(const void* A, int64_t lda, const void* W, int64_t ldw,
+                         const float* a_scale, int a_scale_mode,
+                         const float* w_scale, int w_scale_mode,
+                         const void* bias, const void* residual, int64_t ldr,
+                         void* C, int64_t ldc, int out_dtype, const float* out_scale,
+                         int M, int N, int K, int silu_begin, int silu_end,
+                         hipStream_t stream);
+
+/*
+ * e4m3 quantization of bf16 rows in groups of `group` consecutive elements:
+ * scale = amax/448 per group (1/448 for an all-zero group), written to
+ * scale_out[row * (cols/group) + group_index]; out = e4m3(clamp(x/scale,
+ * +-448)).  With scale_in != NULL, that single per-tensor scale is used and
+ * nothing is written to scale_out.  group % 8 == 0, group <= 4096.
+ * [T, H, D] per-(token, head): rows=T, cols=H*D, group=D.  Per-row: group=cols.
+ * Replaces: quantize_with_scale / calibrated_scale,
+ *           ops/triton/triton_fp8.py:396-413, 760-781.
+ */
+int hstu_quantize_e4m3_rows(const void* x, int64_t ldx, int rows, int cols, int group,
+                            const float* scale_in, void* out, int64_t ldo, float* scale_out,
+                            hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,101 +47,11 @@
 #include <type_traits>
 #include <vector>
 
+#include "hstu_common.h"
 #include "hstu_mi355x.h"
 
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kThreads = 256;
-
-// ---------------------------------------------------------------- primitives
-__device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-// e4m3 x e4m3, K = 128, no block scaling (scale operands 0 select the plain
-// v_mfma_f32_16x16x128_f8f6f4).
-__device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-}
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  f32x2 v = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-}
-__device__ __forceinline__ uint16_t to_bf16(float x) {
-  return __builtin_bit_cast(uint16_t, (__bf16)x);
-}
-__device__ __forceinline__ u32x4 lds_ld128(const uint8_t* p) { return *(const u32x4*)p; }
-__device__ __forceinline__ f32x4 lds_ldf4(const uint8_t* p) { return *(const f32x4*)p; }
-__device__ __forceinline__ i32x8 cat8(u32x4 lo, u32x4 hi) {
-  i32x8 r;
-  r[0] = lo[0]; r[1] = lo[1]; r[2] = lo[2]; r[3] = lo[3];
-  r[4] = hi[0]; r[5] = hi[1]; r[6] = hi[2]; r[7] = hi[3];
-  return r;
-}
-__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-
-// Raw buffer access: 32-bit offsets from a per-(sequence, head) base, with
-// hardware zero-fill beyond `bytes` (rows past the sequence end).
-typedef __amdgpu_buffer_rsrc_t BufRsrc;
-__device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ u32x4 buf_ld128(BufRsrc r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-}
-__device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
-}
-
-// Transposed LDS read (gfx950 ds_read_b64_tr_b16).  Within each 16-lane
-// group, lane j supplies the address of 4 consecutive bf16 M[j][0..3]; lane i
-// receives M[4r + i/4][i%4] for r = 0..3.  With lane j pointing at row
-// base + j/4, column 4*(j%4) of a row-major tile, lane i gets rows
-// base..base+3 of column i: the B operand of an MFMA whose contraction runs
-// along the rows.
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x2 lds_tr16(const uint8_t* p) {
-  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-  const lds_bf16x4* lp = (const lds_bf16x4*)(__attribute__((address_space(3))) const uint8_t*)(p);
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)lp));
-}
-__device__ __forceinline__ u32x4 cat_tr(u32x2 a, u32x2 b) { return u32x4{a[0], a[1], b[0], b[1]}; }
-
-// two e4m3 bytes (low or high half of w) -> two bf16, exact (scale 1.0)
-template <bool HI>
-__device__ __forceinline__ uint32_t cvt_fp8x2_bf16(uint32_t w) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, HI));
-}
-
-// t = -x*log2(e)  ->  t * sigmoid(x) = t / (1 + 2^t)   (== -silu(x)/ln2)
-__device__ __forceinline__ float sig_of_t(float t) {
-  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
-}
-
-// 4 e4m3 bytes of a word -> 4 floats scaled by s, as 2 packed bf16 words.
-__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w, float s) {
-  f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-  f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  return u32x2{pack_bf16(lo[0] * s, lo[1] * s), pack_bf16(hi[0] * s, hi[1] * s)};
-}
-
-// Key order inside a transposed LDS tile.  The S^T C fragment of key
-// sub-tiles 2c and 2c+1 gives lane group g the keys {32c+4g+r, 32c+16+4g+r};
-// storing key 32c+16h+4g+r at column 32c+8g+4h+r makes those eight keys one
-// contiguous 16-byte run, in register order.
-__device__ __forceinline__ int sigma(int kk) {
-  return (kk & ~31) | (((kk >> 2) & 3) << 3) | (((kk >> 4) & 1) << 2) | (kk & 3);
-}
+using namespace hstu;
 
 // ---------------------------------------------------------------- mask
 struct MaskCtx {
@@ -305,55 +215,6 @@ struct ScaleTile {
   }
 };
 
-
-// Global -> LDS tile copy without registers (buffer_load_dwordx4 ... lds).
-// One wave instruction writes 64 consecutive 16-byte LDS slots, so the tile's
-// padded rows are laid out as PITCH/16 slots per row and lane l of
-// instruction i fills slot 64i+l: a data slot loads its (row, chunk), a pad
-// slot reloads a data chunk of the same row (never read).  Rows beyond the
-// buffer's end read as zero.  Completion is tracked by vmcnt: wait_vm() then a
-// barrier before the tile is read.
-template <int ROWS, int ROW_BYTES, int PITCH>
-struct DirectTile {
-  static_assert(PITCH % 16 == 0 && ROW_BYTES % 16 == 0 && PITCH - ROW_BYTES <= ROW_BYTES, "layout");
-  static constexpr int CPR = PITCH / 16, DATA_CPR = ROW_BYTES / 16;
-  static constexpr int NINSTR = (ROWS * CPR + 63) / 64;
-  static constexpr int BYTES = NINSTR * 1024;  // LDS footprint, >= ROWS * PITCH
-  static constexpr int PER_WAVE = (NINSTR + kThreads / 64 - 1) / (kThreads / 64);
-  uint32_t voff[PER_WAVE];
-  __device__ __forceinline__ void init(uint32_t rs_bytes) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-#pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-      const int c = (wave + 4 * j) * 64 + lane;
-      int row = c / CPR, col = c - (c / CPR) * CPR;
-      if (col >= DATA_CPR) col -= DATA_CPR;
-      row = row < ROWS ? row : ROWS - 1;
-      voff[j] = row * rs_bytes + col * 16;
-    }
-  }
-  __device__ __forceinline__ void load(BufRsrc rs, uint32_t soff, uint8_t* tile) const {
-    // Device pass only: the host pass cannot form the LDS address-space
-    // pointer, and a failed host instantiation would drop the kernel's
-    // launch stub.
-#if defined(__HIP_DEVICE_COMPILE__)
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-      const int i = wave + 4 * j;
-      if (i < NINSTR)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(tile + i * 1024), 16,
-                                                 voff[j], soff, 0, 0);
-    }
-#else
-    (void)rs;
-    (void)soff;
-    (void)tile;
-#endif
-  }
-};
-// vmcnt(0); expcnt and lgkmcnt left at their maxima.
-__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // ---------------------------------------------------------------- params
 struct AttnParams {

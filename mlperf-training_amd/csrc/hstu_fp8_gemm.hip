@@ -1,0 +1,319 @@
+// FP8 (OCP e4m3) projection GEMMs and the e4m3 quantizer of the HSTU layer,
+// for MI355X (gfx950).
+//
+//   C[m][n] = epilogue( sum_k A[m][k] * W[n][k] )
+//   epilogue: v = acc * sa(m) * sw(n) [+ bias[n]]; silu(v) for n in [silu_begin,
+//             silu_end) (the U slice); [+ residual[m][n]]; store bf16, or e4m3 of
+//             clamp(v / out_scale, +-448).
+//
+// A is [M, K] row-major e4m3 (per-tensor or per-row scale), W is [N, K]
+// row-major e4m3 (the transposed weight, per-tensor or per-column scale).
+// Reference behaviour followed (paths relative to
+// recommendation_v4/hstu/generative_recommenders/):
+//   UVQK / VQK projection  ops/triton/triton_hstu_preprocess_and_attention.py:1257-1289
+//   K=512 e4m3-output GEMM ops/hip/k512_fp8_gemm.cu:13-17 (acc*(sa*sb) + bias, sat448, e4m3)
+//   K=1536 out-projection  ops/hip/k1536_fp8_addmm.cu:10-18 (bf16(acc*s + C))
+//   SiLU on U only         ops/hstu_compute.py:140
+//   quantizer              ops/triton/triton_fp8.py:396-413, 760-781 (scale = amax/448)
+//
+// Design: workgroup tile 128 (M) x 128 (N), 4 waves as 2 x 2 of 64 x 64.  The
+// MFMA (v_mfma_f32_16x16x128_f8f6f4) is issued operand-swapped, W rows as the
+// A operand and A rows as the B operand, so a lane's C fragment holds 4
+// consecutive output columns of one row (8-byte bf16 / 4-byte e4m3 stores).
+// K steps of 128 stream through a 2-stage LDS ring of direct global->LDS
+// loads (80 KiB per workgroup, two workgroups per CU so one's epilogue and
+// loads overlap the other's MFMAs).  Rows are padded to 160 bytes and lane
+// group g holds the 16-byte k-chunks g and g+4 of a row in both operands,
+// which keeps the operand reads free of bank conflicts.  Tiles are numbered
+// so that each XCD runs a contiguous range and the N tiles of one A row panel
+// run back to back on the same XCD (A panel reuse in that XCD's L2).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <mutex>
+#include <vector>
+
+#include "hstu_common.h"
+#include "hstu_mi355x.h"
+
+namespace {
+using namespace hstu;
+
+struct GemmParams {
+  const uint8_t* A;
+  const uint8_t* W;
+  int64_t lda, ldw;  // bytes
+  const float* a_scale;
+  const float* w_scale;
+  int a_mode, w_mode;  // 0: per-tensor scalar, 1: per-row (A) / per-column (W)
+  const uint16_t* bias;  // bf16 [N] or null
+  const uint16_t* resid;  // bf16 [M, N] or null
+  int64_t ldr;            // elements
+  void* C;
+  int64_t ldc;  // elements
+  const float* out_scale;  // e4m3 output only
+  int M, N, K;
+  int silu_begin, silu_end;
+  int tiles_m, tiles_n;
+};
+
+constexpr int kBM = 128, kBN = 128, kBK = 128;
+constexpr int kPitch = kBK + 32;  // 160: conflict-free operand reads
+using GTile = DirectTile<128, kBK, kPitch>;  // 20 load instructions, 5 per wave
+constexpr int kTileBytes = GTile::BYTES;     // 20 KiB
+constexpr int kStage = 2 * kTileBytes;       // W tile then A tile
+constexpr int kGemmLds = 2 * kStage;         // 80 KiB
+constexpr int kCnt = 2 * GTile::PER_WAVE;    // load instructions per wave per stage
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+template <bool E4M3_OUT, bool RESID>
+__global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // XCD-contiguous tile order: workgroup i runs on XCD i % 8.
+  const int total = p.tiles_m * p.tiles_n;
+  const int per_xcd = (total + 7) / 8;
+  const int idx = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (idx >= total) return;
+  const int mt = idx / p.tiles_n, nt = idx - mt * p.tiles_n;
+  const int m0 = mt * kBM, n0 = nt * kBN;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;  // wave's n / m offsets in the tile
+
+  const int mrows = min(kBM, p.M - m0);
+  const BufRsrc arsrc = make_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)((mrows - 1) * p.lda + p.K));
+  const BufRsrc wrsrc = make_rsrc(p.W + (int64_t)n0 * p.ldw, (uint32_t)((kBN - 1) * p.ldw + p.K));
+  GTile at, wt;
+  at.init((uint32_t)p.lda);
+  wt.init((uint32_t)p.ldw);
+  const int nk = p.K / kBK;
+
+  f32x4 acc[4][4];  // [n sub-tile][m sub-tile] of C^T
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
+
+  wt.load(wrsrc, 0, smem);
+  at.load(arsrc, 0, smem + kTileBytes);
+  wait_vm();
+  __syncthreads();
+
+  // lane group g holds 16-byte k-chunks g and g+4 of a row
+  const int w_rd = (wn + li) * kPitch + 16 * g;
+  const int a_rd = kTileBytes + (wm + li) * kPitch + 16 * g;
+  for (int kk = 0; kk < nk; ++kk) {
+    const uint8_t* buf = smem + (kk & 1) * kStage;
+    if (kk + 1 < nk) {
+      uint8_t* nb = smem + ((kk + 1) & 1) * kStage;
+      wt.load(wrsrc, (kk + 1) * kBK, nb);
+      at.load(arsrc, (kk + 1) * kBK, nb + kTileBytes);
+    }
+    i32x8 bop[4];
+#pragma unroll
+    for (int ms = 0; ms < 4; ++ms) {
+      const uint8_t* r = buf + a_rd + ms * 16 * kPitch;
+      bop[ms] = cat8(lds_ld128(r), lds_ld128(r + 64));
+    }
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const uint8_t* r = buf + w_rd + ns * 16 * kPitch;
+      const i32x8 aop = cat8(lds_ld128(r), lds_ld128(r + 64));
+#pragma unroll
+      for (int ms = 0; ms < 4; ++ms) acc[ns][ms] = mfma_fp8(aop, bop[ms], acc[ns][ms]);
+    }
+    wait_vm();
+    __syncthreads();
+  }
+
+  // ---- epilogue: lane holds C[m = m0+wm+16ms+li][n = n0+wn+16ns+4g .. +3]
+  const float out_s = E4M3_OUT ? p.out_scale[0] : 1.f;
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int m = m0 + wm + 16 * ms + li;
+    if (m >= p.M) continue;
+    const float sa = p.a_mode ? p.a_scale[m] : p.a_scale[0];
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const int n = n0 + wn + 16 * ns + 4 * g;
+      f32x4 sw;
+      if (p.w_mode) sw = *(const f32x4*)(p.w_scale + n);
+      else sw = f32x4{p.w_scale[0], p.w_scale[0], p.w_scale[0], p.w_scale[0]};
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[ns][ms][r] * (sa * sw[r]);
+      if (p.bias) {
+        const u32x2 b = *(const u32x2*)(p.bias + n);
+        v[0] += bf16_to_f32(b[0] & 0xffff);
+        v[1] += bf16_to_f32(b[0] >> 16);
+        v[2] += bf16_to_f32(b[1] & 0xffff);
+        v[3] += bf16_to_f32(b[1] >> 16);
+      }
+      if (n < p.silu_end && n + 4 > p.silu_begin) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (n + r >= p.silu_begin && n + r < p.silu_end)
+            v[r] = v[r] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * v[r]));
+        }
+      }
+      if constexpr (RESID) {
+        const u32x2 c = *(const u32x2*)(p.resid + (int64_t)m * p.ldr + n);
+        v[0] += bf16_to_f32(c[0] & 0xffff);
+        v[1] += bf16_to_f32(c[0] >> 16);
+        v[2] += bf16_to_f32(c[1] & 0xffff);
+        v[3] += bf16_to_f32(c[1] >> 16);
+      }
+      if constexpr (E4M3_OUT) {
+        float c[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c[r] = __builtin_fminf(__builtin_fmaxf(v[r] / out_s, -448.f), 448.f);
+        int w = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+        w = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], w, true);
+        *(uint32_t*)((uint8_t*)p.C + (int64_t)m * p.ldc + n) = (uint32_t)w;
+      } else {
+        *(u32x2*)((uint16_t*)p.C + (int64_t)m * p.ldc + n) = u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+      }
+    }
+  }
+}
+
+// Per-group e4m3 quantization of bf16 rows: scale = amax/448 over each group
+// of `group` consecutive elements (1/448 for an all-zero group), out =
+// e4m3(clamp(x / scale, +-448)).  One wave per (row, group); group <= 4096 and
+// a multiple of 8.  With a given per-tensor scale (scale_in != null) no amax
+// is taken.
+__global__ void quantize_e4m3_kernel(const uint16_t* x, int64_t ldx, int rows, int cols, int group,
+                                     const float* scale_in, uint8_t* out, int64_t ldo, float* scale_out) {
+  const int groups_per_row = cols / group;
+  const int gid = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (gid >= rows * groups_per_row) return;
+  const int lane = threadIdx.x & 63;
+  const int row = gid / groups_per_row, gc = (gid - row * groups_per_row) * group;
+  const uint16_t* src = x + (int64_t)row * ldx + gc;
+  // each lane handles 8-element chunks lane, lane+64, ...
+  float amax = 0.f;
+  constexpr int kMaxCh = 8;  // 8-element chunks per lane (group <= 8 * 8 * 64)
+  u32x4 chunk[kMaxCh];
+  const int nch = group / 8;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const int ch = lane + 64 * c;
+    chunk[c] = u32x4{0u, 0u, 0u, 0u};
+    if (ch < nch) chunk[c] = *(const u32x4*)(src + ch * 8);
+    if (!scale_in) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(bf16_to_f32(chunk[c][e] & 0xffff)));
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(bf16_to_f32(chunk[c][e] >> 16)));
+      }
+    }
+  }
+  float scale;
+  if (scale_in) {
+    scale = scale_in[0];
+  } else {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off));
+    scale = amax > 0.f ? amax / 448.f : 1.f / 448.f;
+    if (lane == 0) scale_out[gid] = scale;
+  }
+  uint8_t* dst = out + (int64_t)row * ldo + gc;
+#pragma unroll
+  for (int c = 0; c < kMaxCh; ++c) {
+    const int ch = lane + 64 * c;
+    if (ch >= nch) continue;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // true division, as the reference quantizer computes value / scale
+      f[2 * e] = __builtin_fminf(__builtin_fmaxf(bf16_to_f32(chunk[c][e] & 0xffff) / scale, -448.f), 448.f);
+      f[2 * e + 1] = __builtin_fminf(__builtin_fmaxf(bf16_to_f32(chunk[c][e] >> 16) / scale, -448.f), 448.f);
+    }
+    int lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true);
+    int hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], 0, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], hi, true);
+    *(u32x2*)(dst + ch * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
+  }
+}
+
+hipError_t set_gemm_lds(const void* fn) {
+  static std::mutex mu;
+  static std::vector<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const void* d : done)
+    if (d == fn) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmLds);
+  if (e == hipSuccess) done.push_back(fn);
+  return e;
+}
+
+}  // namespace
+
+extern "C" int hstu_fp8_gemm_rowcol(const void* A, int64_t lda, const void* W, int64_t ldw, const float* a_scale,
+                                    int a_scale_mode, const float* w_scale, int w_scale_mode, const void* bias,
+                                    const void* residual, int64_t ldr, void* C, int64_t ldc, int out_dtype,
+                                    const float* out_scale, int M, int N, int K, int silu_begin, int silu_end,
+                                    hipStream_t stream) {
+  if (M < 0 || N <= 0 || K <= 0 || N % kBN != 0 || K % kBK != 0 || !A || !W || !C || !a_scale || !w_scale)
+    return HSTU_E_BAD_ARG;
+  if (lda < K || ldw < K || lda % 16 != 0 || ldw % 16 != 0 || ((uintptr_t)A | (uintptr_t)W) % 16 != 0)
+    return HSTU_E_UNSUPPORTED;
+  if (ldc < N || (residual && ldr < N) || (out_dtype != HSTU_DTYPE_BF16 && out_dtype != HSTU_DTYPE_FP8_E4M3) ||
+      (out_dtype == HSTU_DTYPE_FP8_E4M3 && !out_scale))
+    return HSTU_E_BAD_ARG;
+  if ((int64_t)(kBM - 1) * lda + K > 0xffffffffLL || (int64_t)(kBN - 1) * ldw + K > 0xffffffffLL)
+    return HSTU_E_UNSUPPORTED;
+  if (M == 0) return 0;
+  GemmParams p{};
+  p.A = (const uint8_t*)A;
+  p.W = (const uint8_t*)W;
+  p.lda = lda;
+  p.ldw = ldw;
+  p.a_scale = a_scale;
+  p.w_scale = w_scale;
+  p.a_mode = a_scale_mode != 0;
+  p.w_mode = w_scale_mode != 0;
+  p.bias = (const uint16_t*)bias;
+  p.resid = (const uint16_t*)residual;
+  p.ldr = ldr;
+  p.C = C;
+  p.ldc = ldc;
+  p.out_scale = out_scale;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.silu_begin = silu_begin;
+  p.silu_end = silu_end;
+  p.tiles_m = (M + kBM - 1) / kBM;
+  p.tiles_n = N / kBN;
+  const int total = p.tiles_m * p.tiles_n;
+  const int grid = (total + 7) / 8 * 8;
+  void (*kern)(GemmParams);
+  if (out_dtype == HSTU_DTYPE_FP8_E4M3) {
+    kern = residual ? fp8_gemm_kernel<true, true> : fp8_gemm_kernel<true, false>;
+  } else {
+    kern = residual ? fp8_gemm_kernel<false, true> : fp8_gemm_kernel<false, false>;
+  }
+  hipError_t e = set_gemm_lds((const void*)kern);
+  if (e != hipSuccess) return (int)e;
+  void* args[] = {&p};
+  return (int)hipLaunchKernel((const void*)kern, dim3(grid), dim3(kThreads), args, (size_t)kGemmLds, stream);
+}
+
+extern "C" int hstu_quantize_e4m3_rows(const void* x, int64_t ldx, int rows, int cols, int group,
+                                       const float* scale_in, void* out, int64_t ldo, float* scale_out,
+                                       hipStream_t stream) {
+  if (rows < 0 || cols <= 0 || group <= 0 || cols % group != 0 || group % 8 != 0 || group > 4096 || !x || !out ||
+      ldx < cols || ldo < cols || ldx % 8 != 0 || ldo % 8 != 0 || (!scale_in && !scale_out))
+    return HSTU_E_BAD_ARG;
+  if (((uintptr_t)x % 16) != 0 || ((uintptr_t)out % 8) != 0) return HSTU_E_UNSUPPORTED;
+  if (rows == 0) return 0;
+  const int64_t groups = (int64_t)rows * (cols / group);
+  const int grid = (int)((groups + 3) / 4);
+  hipLaunchKernelGGL(quantize_e4m3_kernel, dim3(grid), dim3(256), 0, stream, (const uint16_t*)x, ldx, rows, cols,
+                     group, scale_in, (uint8_t*)out, ldo, scale_out);
+  return (int)hipGetLastError();
+}

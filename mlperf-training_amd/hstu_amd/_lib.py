@@ -69,11 +69,12 @@ _SIGNATURES = {
     "hstu_attn_bwd_dq": None,
     "hstu_fp8_gemm_rowcol": (
         _i32,
-        [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _vp],
+        [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i32, _vp,
+         _i32, _i32, _i32, _i32, _i32, _vp],
     ),
     "hstu_quantize_e4m3_rows": (
         _i32,
-        [_vp, _i64, _i32, _i32, _i32, _vp, _i64, _vp, _vp],
+        [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp],
     ),
 }
 

@@ -1,0 +1,151 @@
+"""FP8 (OCP e4m3) quantization and projection GEMMs of the HSTU layer on the
+gfx950 kernels of ``libhstu_mi355x.so``.
+
+Mirrors the reference's FP8 boundary (``ops/triton/triton_fp8.py``, paths
+relative to ``recommendation_v4/hstu/generative_recommenders/``):
+
+* ``quantize_with_scale`` (:760-781) / ``calibrated_scale`` (:396-413)
+  -> ``quantize_with_scale`` / ``quantize_e4m3_rows`` (also per row and per
+  (token, head) groups, which the reference does not have);
+* ``scaled_addmm_fp8_preq`` (:1756) -> ``scaled_addmm_fp8_preq`` (bf16 out,
+  bias or residual);
+* ``scaled_mm_fp8_out_preq`` (:2409) -> ``scaled_mm_fp8_out_preq`` (e4m3 out
+  at an output scale, the VQK projection feeding the FP8 attention).
+
+Weights are passed as bf16 ``[K, N]`` (the layer's parameter layout) or as a
+pre-quantized ``(w8_nk, w_scale)`` pair from ``quantize_weight_e4m3``.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import torch
+
+from . import _lib
+
+E4M3 = torch.float8_e4m3fn
+E4M3_MAX = 448.0
+Weight = Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def quantize_e4m3_rows(x: torch.Tensor, group: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bf16 [R, C] (or [T, H, D] with group=D) -> (e4m3 same shape, fp32 scales
+    [R, C/group]); scale = amax/448 per group of ``group`` consecutive
+    elements of a row (default: the whole row)."""
+    shape = x.shape
+    x2 = x.reshape(shape[0], -1)
+    if x2.dtype != torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    x2 = x2.contiguous()
+    R, C = x2.shape
+    group = C if group is None else int(group)
+    out = torch.empty((R, C), dtype=E4M3, device=x.device)
+    scales = torch.empty((R, C // group), dtype=torch.float32, device=x.device)
+    st = _lib.fn("hstu_quantize_e4m3_rows")(x2.data_ptr(), C, R, C, group, None, out.data_ptr(), C,
+                                            scales.data_ptr(), _stream(x))
+    _lib.check(st, "hstu_quantize_e4m3_rows")
+    return out.view(shape), scales
+
+
+def quantize_with_scale(value: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """e4m3(clamp(value / scale, +-448)) with one per-tensor fp32 scale
+    (``quantize_with_scale``, ``triton_fp8.py:760-781``)."""
+    x2 = value.reshape(value.shape[0], -1).to(torch.bfloat16).contiguous()
+    R, C = x2.shape
+    group = C if C <= 4096 else next(g for g in (4096, 2048, 1024, 512, 256, 128, 64, 32, 16, 8) if C % g == 0)
+    out = torch.empty((R, C), dtype=E4M3, device=value.device)
+    s = scale.reshape(1).to(torch.float32).contiguous()
+    st = _lib.fn("hstu_quantize_e4m3_rows")(x2.data_ptr(), C, R, C, group, s.data_ptr(), out.data_ptr(), C,
+                                            None, _stream(value))
+    _lib.check(st, "hstu_quantize_with_scale")
+    return out.view(value.shape)
+
+
+def calibrated_scale(value: torch.Tensor, *, margin: float = 1.0) -> torch.Tensor:
+    """Per-tensor scale amax*margin/448 as a (1, 1) fp32 tensor
+    (``calibrated_scale``, ``triton_fp8.py:396-413``)."""
+    amax = value.detach().abs().amax().float().clamp_min(1.0e-12)
+    return (amax * margin / E4M3_MAX).reshape(1, 1)
+
+
+def quantize_weight_e4m3(w_kn: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """bf16 weight [K, N] -> (e4m3 [N, K] row-major, per-column scales [N])."""
+    w8, s = quantize_e4m3_rows(w_kn.t().contiguous())
+    return w8, s.reshape(-1)
+
+
+def _weight(weight: Weight) -> Tuple[torch.Tensor, torch.Tensor, int]:
+    if isinstance(weight, tuple):
+        w8, ws = weight
+    else:
+        w8, ws = quantize_weight_e4m3(weight)
+    ws = ws.to(torch.float32).contiguous()
+    return w8, ws, 1 if ws.numel() > 1 else 0
+
+
+def fp8_gemm(a8: torch.Tensor, a_scale: torch.Tensor, weight: Weight, *, bias: Optional[torch.Tensor] = None,
+             residual: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+             out_scale: Optional[torch.Tensor] = None,
+             silu_cols: Optional[Tuple[int, int]] = None) -> torch.Tensor:
+    """C = epilogue(a8 @ W^T) on the HIP kernel; see ``hstu_fp8_gemm_rowcol``."""
+    if a8.dtype != E4M3:
+        raise TypeError(f"expected e4m3 activation, got {a8.dtype}")
+    w8, ws, w_mode = _weight(weight)
+    M, K = a8.shape
+    N = w8.shape[0]
+    if w8.shape[1] != K:
+        raise ValueError(f"K mismatch: a {tuple(a8.shape)} w8 {tuple(w8.shape)}")
+    a8 = a8.contiguous()
+    a_scale = a_scale.to(torch.float32).contiguous().reshape(-1)
+    a_mode = 1 if a_scale.numel() > 1 else 0
+    if a_mode and a_scale.numel() != M:
+        raise ValueError("per-row activation scale must have M entries")
+    fp8_out = out_dtype == E4M3
+    out = torch.empty((M, N), dtype=out_dtype, device=a8.device)
+    if M == 0:
+        return out
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    r = None if residual is None else residual.to(torch.bfloat16).contiguous()
+    os_ = None
+    if fp8_out:
+        if out_scale is None:
+            raise ValueError("e4m3 output needs out_scale")
+        os_ = out_scale.to(torch.float32).reshape(1).contiguous()
+    c0, c1 = silu_cols if silu_cols is not None else (0, 0)
+    st = _lib.fn("hstu_fp8_gemm_rowcol")(
+        a8.data_ptr(), K, w8.data_ptr(), w8.stride(0), a_scale.data_ptr(), a_mode, ws.data_ptr(), w_mode,
+        _lib.ptr(b), _lib.ptr(r), N if r is not None else 0, out.data_ptr(), N,
+        _lib.HSTU_DTYPE_FP8_E4M3 if fp8_out else _lib.HSTU_DTYPE_BF16, _lib.ptr(os_),
+        M, N, K, int(c0), int(c1), _stream(a8))
+    _lib.check(st, "hstu_fp8_gemm_rowcol")
+    return out
+
+
+def scaled_addmm_fp8_preq(activation_fp8: torch.Tensor, scale_a: torch.Tensor, weight: Weight,
+                          bias_or_residual: Optional[torch.Tensor], *, out_dtype: torch.dtype = torch.bfloat16,
+                          silu_cols: Optional[Tuple[int, int]] = None) -> torch.Tensor:
+    """bf16 projection of an e4m3 activation with a 1-D bias or a 2-D residual
+    (``scaled_addmm_fp8_preq``, ``triton_fp8.py:1756``).  ``silu_cols`` fuses
+    SiLU on a column range (the U slice)."""
+    if out_dtype != torch.bfloat16:
+        raise ValueError("scaled_addmm_fp8_preq produces bf16")
+    bias = residual = None
+    if bias_or_residual is not None:
+        if bias_or_residual.dim() == 1:
+            bias = bias_or_residual
+        else:
+            residual = bias_or_residual
+    return fp8_gemm(activation_fp8, scale_a, weight, bias=bias, residual=residual, silu_cols=silu_cols)
+
+
+def scaled_mm_fp8_out_preq(activation_fp8: torch.Tensor, scale_a: torch.Tensor, weight: Weight,
+                           bias: Optional[torch.Tensor] = None, *,
+                           output_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """e4m3 projection at ``output_scale`` (``scaled_mm_fp8_out_preq``,
+    ``triton_fp8.py:2409``): e4m3(clamp((acc*sa*sw + bias)/output_scale, +-448))."""
+    return fp8_gemm(activation_fp8, scale_a, weight, bias=bias, out_dtype=E4M3, out_scale=output_scale)

@@ -1,0 +1,130 @@
+"""GPU parity of the FP8 projection GEMM and the e4m3 quantizer.
+
+* quantizer: bit-exact against the oracle (torch's e4m3fn conversion of
+  x / (amax/448)), scales bit-exact.
+* GEMM, bf16 output: against the float64 product of the dequantized operands
+  (``oracle.fp8_rowcol_gemm``); bar: relative L2 <= 4e-3 and max |err| <=
+  1e-2 * max |ref| (bf16 output rounding is 2^-9 relative).
+* GEMM, e4m3 output: every element within one e4m3 rounding step (2^-4
+  relative, 2^-9 absolute near zero) of the float64 result / out_scale.
+"""
+
+import pytest
+import torch
+
+from oracle import hstu_oracle as orc
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _fp8():
+    from hstu_amd import fp8
+
+    return fp8
+
+
+@pytest.mark.parametrize("shape,group", [((777, 512), 128), ((64, 4, 128), 128), ((33, 2048), 2048),
+                                         ((5, 16), 8)])
+def test_quantize_rows_bitexact(hip_lib, shape, group):
+    fp8 = _fp8()
+    g = torch.Generator().manual_seed(1)
+    x = (torch.randn(shape, generator=g) * 3).to(torch.bfloat16)
+    x.view(shape[0], -1)[0, :group] = 0  # an all-zero group
+    q8, s = fp8.quantize_e4m3_rows(x.to(DEV), group)
+    torch.cuda.synchronize()
+    R = shape[0]
+    xg = x.float().reshape(R, -1, group)
+    r8, rs = orc.quantize_e4m3_rows(xg, dim=-1)
+    assert torch.equal(s.cpu().reshape(rs.shape), rs), "scales differ"
+    assert torch.equal(q8.cpu().view(torch.uint8).reshape(-1), r8.view(torch.uint8).reshape(-1)), "bytes differ"
+
+
+def test_quantize_with_scale_bitexact(hip_lib):
+    fp8 = _fp8()
+    x = (torch.randn(300, 512, generator=torch.Generator().manual_seed(2)) * 5).to(torch.bfloat16)
+    s = orc.quantize_e4m3_per_tensor(x.float(), margin=1.5)[1]
+    out = fp8.quantize_with_scale(x.to(DEV), s.to(DEV))
+    torch.cuda.synchronize()
+    ref = (x.float() / s).clamp(-448, 448).to(torch.float8_e4m3fn)  # triton_fp8.py:760-781
+    assert torch.equal(out.cpu().view(torch.uint8), ref.view(torch.uint8))
+
+
+def _operands(M, N, K, seed=0, per_row=True, per_col=True):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g)
+    w = torch.randn(K, N, generator=g) * 0.05
+    a8, sa = orc.quantize_e4m3_rows(a, dim=1) if per_row else orc.quantize_e4m3_per_tensor(a)
+    w8t, sw = orc.quantize_e4m3_rows(w.t().contiguous(), dim=1) if per_col else orc.quantize_e4m3_per_tensor(w.t())
+    return a8, sa.reshape(-1), w8t.contiguous(), sw.reshape(-1)
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 2048, 512), (129, 512, 512), (1, 128, 128), (300, 256, 1536)])
+@pytest.mark.parametrize("scales", ["rowcol", "tensor"])
+def test_gemm_bf16(hip_lib, M, N, K, scales):
+    fp8 = _fp8()
+    a8, sa, w8t, sw = _operands(M, N, K, per_row=scales == "rowcol", per_col=scales == "rowcol")
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(3)) * 0.1).to(torch.bfloat16)
+    silu = (0, min(N, 512))
+    out = fp8.fp8_gemm(a8.to(DEV), sa.to(DEV), (w8t.to(DEV), sw.to(DEV)), bias=bias.to(DEV), silu_cols=silu)
+    torch.cuda.synchronize()
+    ref = orc.fp8_rowcol_gemm(a8, sa, w8t.t(), sw, bias=bias.float(), silu_cols=silu)
+    got = out.double().cpu()
+    err = orc.rel_l2(ref, got)
+    mx = float((got - ref).abs().max() / ref.abs().max())
+    assert err <= 4e-3 and mx <= 1e-2, f"rel L2 {err:.2e} max {mx:.2e}"
+
+
+def test_gemm_residual_k1536(hip_lib):
+    """The output projection: K=1536, bf16 residual add (k1536_fp8_addmm)."""
+    fp8 = _fp8()
+    M, N, K = 515, 512, 1536
+    a8, sa, w8t, sw = _operands(M, N, K, seed=4)
+    res = torch.randn(M, N, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    out = fp8.scaled_addmm_fp8_preq(a8.to(DEV), sa.to(DEV), (w8t.to(DEV), sw.to(DEV)), res.to(DEV))
+    torch.cuda.synchronize()
+    ref = orc.fp8_rowcol_gemm(a8, sa, w8t.t(), sw, residual=res.float())
+    got = out.double().cpu()
+    assert orc.rel_l2(ref, got) <= 4e-3
+    assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2
+
+
+def test_gemm_e4m3_out(hip_lib):
+    """VQK projection emitting e4m3 at an output scale (scaled_mm_fp8_out_preq).
+
+    Bar: every element within one e4m3 half-step (2^-4 relative) of the
+    float64 result / out_scale, plus 2.5e-5 * max|result| absolute.  The
+    absolute term is the FP8 MFMA accumulation error: measured on this test at
+    about 7e-6 * max (the same deviation appears on the bf16 output path), so
+    near-zero elements can land one e4m3 step from the float64 rounding."""
+    fp8 = _fp8()
+    M, N, K = 700, 1536, 512
+    a8, sa, w8t, sw = _operands(M, N, K, seed=6, per_row=False, per_col=False)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(7)) * 0.1).to(torch.bfloat16)
+    ref = orc.fp8_rowcol_gemm(a8, sa, w8t.t(), sw, bias=bias.float())
+    out_scale = (ref.abs().max() / 448.0).float().reshape(1)
+    out = fp8.scaled_mm_fp8_out_preq(a8.to(DEV), sa.to(DEV), (w8t.to(DEV), sw.to(DEV)), bias.to(DEV),
+                                     output_scale=out_scale.to(DEV))
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float8_e4m3fn
+    got = out.cpu().double()
+    want = (ref / out_scale.double()).clamp(-448, 448)
+    tol = want.abs() * 2.0 ** -4 + 2.5e-5 * 448.0
+    worst = float(((got - want).abs() - tol).max())
+    assert worst <= 0, f"exceeds the bar by {worst:.3e}"
+    # the e4m3 bytes must round-trip: no NaN encodings (saturating clamp)
+    assert not torch.isnan(got).any()
+
+
+def test_gemm_bf16_weight_path(hip_lib):
+    """bf16 [K, N] weight quantized per column on the device, as the layer holds it."""
+    fp8 = _fp8()
+    M, N, K = 256, 2048, 512
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(K, N, generator=g) * 0.05).to(torch.bfloat16)
+    x8, sx = fp8.quantize_e4m3_rows(x.to(DEV))
+    out = fp8.fp8_gemm(x8, sx, w.to(DEV))
+    torch.cuda.synchronize()
+    ref = x.double() @ w.double()
+    assert orc.rel_l2(ref, out.double().cpu()) <= 6e-2  # two e4m3 quantizations (~2^-4 each, averaged)
