@@ -1,0 +1,91 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point
+include/hstu_mi355x.h declares, and rejects bad arguments before any device
+call (no compute is launched here)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "hstu_mi355x.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(hstu_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared()
+    for n in ("hstu_attn_fwd", "hstu_attn_bwd", "hstu_attn_bwd_dkdv", "hstu_attn_bwd_dq",
+              "hstu_attn_bwd_workspace_bytes", "hstu_fp8_gemm_rowcol", "hstu_quantize_e4m3_rows", "hstu_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    import hstu_amd._lib as lib
+
+    so = lib.load_library()
+    for name in _declared():
+        assert hasattr(so, name), name
+    assert set(_declared()) == set(lib.EXPORTED_SYMBOLS)
+
+
+def test_version_string():
+    import hstu_amd._lib as lib
+
+    v = lib.fn("hstu_version")()
+    assert v.startswith(b"hstu-mi355x")
+
+
+def test_workspace_size():
+    import hstu_amd._lib as lib
+
+    f = lib.fn("hstu_attn_bwd_workspace_bytes")
+    assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 0) == 0
+    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, 4, 128, 4096, 0) == 1000 * 4 * 128 * 2
+    ext = 4 * (2 * 4096 + 192) * 4
+    assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 1) == (ext + 255) // 256 * 256
+
+
+def test_bad_arguments_rejected_before_launch():
+    import hstu_amd._lib as lib
+
+    fwd = lib.fn("hstu_attn_fwd")
+    # unknown dtype
+    assert fwd(7, 16, 16, 16, 512, 512, 512, None, None, None, 0, 0, 16, 1, 4, 128, 64, 0.1,
+               None, 0, 0, None, 0, 16, 512, None) == lib.HSTU_E_BAD_ARG
+    # row stride smaller than H*D
+    assert fwd(0, 16, 16, 16, 100, 512, 512, None, None, None, 0, 0, 16, 1, 4, 128, 64, 0.1,
+               None, 0, 0, None, 0, 16, 512, None) == lib.HSTU_E_BAD_ARG
+    # e4m3 without scales
+    assert fwd(1, 16, 16, 16, 512, 512, 512, None, None, None, 0, 0, 16, 1, 4, 128, 64, 0.1,
+               None, 0, 0, None, 0, 16, 512, None) == lib.HSTU_E_BAD_ARG
+    # unsupported head dim
+    assert fwd(0, 16, 16, 16, 384, 384, 384, None, None, None, 0, 0, 16, 1, 4, 96, 64, 0.1,
+               None, 0, 0, None, 0, 16, 384, None) == lib.HSTU_E_UNSUPPORTED
+    gemm = lib.fn("hstu_fp8_gemm_rowcol")
+    # N not a multiple of 128
+    assert gemm(16, 512, 16, 512, 16, 0, 16, 0, None, None, 0, 16, 100, 0, None, 8, 100, 512, 0, 0,
+                None) == lib.HSTU_E_BAD_ARG
+    q = lib.fn("hstu_quantize_e4m3_rows")
+    assert q(16, 100, 4, 100, 7, None, 16, 100, 16, None) == lib.HSTU_E_BAD_ARG  # group not a multiple of 8
+
+
+def test_missing_library_raises(tmp_path):
+    import hstu_amd._lib as lib
+
+    with pytest.raises(lib.HstuUnavailableError):
+        lib.load_library.__wrapped__(tmp_path / "nope.so") if hasattr(lib.load_library, "__wrapped__") else \
+            _load_fresh(lib, tmp_path / "nope.so")
+
+
+def _load_fresh(lib, path):
+    saved = lib._lib
+    lib._lib = None
+    try:
+        return lib.load_library(path)
+    finally:
+        lib._lib = saved
