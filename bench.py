@@ -5,10 +5,15 @@
 Workload: B=128 sequences, lengths
 numpy.default_rng(0).zipf(1.2, 128).clip(32, 4096) (T = 162 251 tokens),
 max_seq_len N=4096, H=4, D=128; q, k, v ~ N(0,1) quantized to OCP e4m3 with
-per-(token, head) fp32 scales amax/448; upstream gradient N(0,1) bf16.
-One step = forward + backward (dK/dV and dQ) over the whole batch, inputs
-resident in HBM.  value = causal-effective FLOPs (14*D*H*P, P = sum L(L+1)/2)
-per second.  The same step on bf16 inputs is reported under "bf16".
+per-(token, head) fp32 scales amax/448; learned relative-position bias table
+[H, 2*1024-1] ~ N(0, 0.02) (offsets beyond 1023 clamped); upstream gradient
+N(0,1) bf16.  One step = forward + backward (dK/dV, dQ and the bias gradient)
+over the whole batch, inputs resident in HBM.  value = causal-effective FLOPs
+(14*D*H*P, P = sum L(L+1)/2) per second.  Also reported: the same step without
+the bias (the reference's attention has none) and on bf16 inputs.
+
+    python bench.py --copy-calibration   # a 512 MiB device copy, for scaling
+                                         # the FETCH_SIZE / WRITE_SIZE counters
 
 Prints ONE JSON line.
 """
@@ -41,6 +46,7 @@ def parse():
     ap.add_argument("--no-bf16", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--copy-calibration", action="store_true")
     return ap.parse_args()
 
 
@@ -51,7 +57,7 @@ def lengths_cfg3():
 class Workload:
     """Device-resident inputs and the raw C-ABI argument tuples of one step."""
 
-    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0):
+    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True):
         from oracle import hstu_oracle as orc  # generator helpers only (not timed)
 
         self.torch = torch
@@ -84,20 +90,27 @@ class Workload:
         self.dv = torch.empty_like(self.out)
         self.alpha = 1.0 / D ** 0.5
         B = len(lengths)
+        self.bias = self.dbias = None
+        R = 0
+        if bias:
+            R = 1024
+            gb = torch.Generator(device=dev).manual_seed(seed + 1)
+            self.bias = (torch.randn(H, 2 * R - 1, device=dev, generator=gb) * 0.02).contiguous()
+            self.dbias = torch.empty_like(self.bias)
         stream = torch.cuda.current_stream().cuda_stream
         dt = 1 if self.fp8 else 0
         sp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         srs, shs = (H, 1) if self.fp8 else (0, 0)
         self.fwd_args = (dt, self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), H * D, H * D, H * D,
                          sp(self.sq), sp(self.sk), sp(self.sv), srs, shs, self.offs.data_ptr(), B, H, D, N,
-                         self.alpha, None, 0, 0, None, 0, self.out.data_ptr(), H * D, stream)
-        ws_bytes = lib.fn("hstu_attn_bwd_workspace_bytes")(dt, T, H, D, N, 0)
+                         self.alpha, None, 0, 0, sp(self.bias), R, self.out.data_ptr(), H * D, stream)
+        ws_bytes = lib.fn("hstu_attn_bwd_workspace_bytes")(dt, T, H, D, N, R)
         self.ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         self.bwd_args = (dt, self.dout.data_ptr(), H * D, self.q.data_ptr(), self.k.data_ptr(),
                          self.v.data_ptr(), H * D, H * D, H * D, sp(self.sq), sp(self.sk), sp(self.sv), srs, shs,
-                         self.offs.data_ptr(), B, H, D, N, self.alpha, None, 0, 0, None, 0,
-                         self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), H * D, H * D, H * D, None,
-                         self.ws.data_ptr(), ws_bytes, T, stream)
+                         self.offs.data_ptr(), B, H, D, N, self.alpha, None, 0, 0, sp(self.bias), R,
+                         self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), H * D, H * D, H * D,
+                         sp(self.dbias), self.ws.data_ptr(), ws_bytes, T, stream)
         self.f_fwd = lib.fn("hstu_attn_fwd")
         self.f_dkdv = lib.fn("hstu_attn_bwd_dkdv")
         self.f_dq = lib.fn("hstu_attn_bwd_dq")
@@ -184,12 +197,30 @@ def cpu_baseline(lengths, H, D, N, budget_s):
     }
 
 
+def copy_calibration():
+    """A plain device copy of known size (512 MiB read + 512 MiB written), run
+    under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE to scale those counters."""
+    import torch
+
+    n = 512 * 1024 * 1024
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is designed, not built: see DESIGN.md)"}))
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import torch
 
     import hstu_amd._lib as lib
@@ -197,12 +228,16 @@ def main():
     lib.load_library()
     lengths = lengths_cfg3()
     H, D, N = 4, 128, 4096
-    w8 = Workload(torch, lib, lengths, H, D, N, "fp8")
+    w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
     wall_ms, parts = w8.run(args.steps, args.warmup)
     total = w8.flops("step")
     value = total / (wall_ms * 1e-3) / 1e12
     dom = max(parts, key=parts.get)
     achieved = w8.flops(dom) / (parts[dom] * 1e-3) / 1e12
+    traffic = None
+    tfile = REPO / "profiles" / "hbm_traffic_cfg3.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(f"hstu_attn_{dom}")
     res = {
         "metric": "HSTU jagged attn fwd+bwd TFLOP/s (FP8 e4m3 inputs) + % MFMA peak, 1xMI355X",
         "value": round(value, 2),
@@ -216,21 +251,30 @@ def main():
         "vs_baseline": None,
         "dtype": "fp8_e4m3",
         "data": "synthetic",
-        "config": {"workload": "BASELINE config 3: jagged HSTU attention fwd+bwd, e4m3 q/k/v with per-token-per-head "
-                               "scales, bf16 out/grads",
+        "config": {"workload": "BASELINE config 3: jagged HSTU attention fwd+bwd (dq, dk, dv, dbias), e4m3 q/k/v "
+                               "with per-token-per-head scales, relative-position bias [4, 2047], bf16 out/grads",
                    "B": len(lengths), "T": w8.T, "max_seq_len": N, "H": H, "D": D,
-                   "causal_pairs_per_head": w8.P, "attn_bias": False, "parallelism": "none (1 GPU)"},
+                   "causal_pairs_per_head": w8.P, "attn_bias": True, "parallelism": "none (1 GPU)"},
         "pct_fp8_peak": round(100 * value / PEAK_TFLOPS["fp8"], 2),
         "kernels_ms": {k: round(v, 4) for k, v in parts.items()},
         "kernels_tflops": {k: round(w8.flops(k) / (v * 1e-3) / 1e12, 1) for k, v in parts.items()},
         "roofline": {"bound": "mfma", "kernel": f"hstu_attn_{dom}", "achieved": round(achieved, 1),
                      "peak": PEAK_TFLOPS["fp8"], "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_TFLOPS["fp8"], 4), "traffic": None},
+                     "frac": round(achieved / PEAK_TFLOPS["fp8"], 4), "traffic": traffic},
     }
     del w8
     torch.cuda.empty_cache()
+    wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False)
+    wall_n, parts_n = wn.run(args.steps, max(args.warmup, 2))
+    vn = wn.flops("step") / (wall_n * 1e-3) / 1e12
+    res["no_bias"] = {"value": round(vn, 2), "unit": "TFLOP/s", "ms_per_step": round(wall_n, 4),
+                      "pct_fp8_peak": round(100 * vn / PEAK_TFLOPS["fp8"], 2),
+                      "kernels_ms": {k: round(v, 4) for k, v in parts_n.items()},
+                      "note": "reference-equivalent attention (the reference has no attention bias)"}
+    del wn
+    torch.cuda.empty_cache()
     if not args.no_bf16:
-        wb = Workload(torch, lib, lengths, H, D, N, "bf16")
+        wb = Workload(torch, lib, lengths, H, D, N, "bf16", bias=True)
         wall_b, parts_b = wb.run(max(args.steps // 2, 3), 2)
         vb = wb.flops("step") / (wall_b * 1e-3) / 1e12
         res["bf16"] = {"value": round(vb, 2), "unit": "TFLOP/s", "ms_per_step": round(wall_b, 4),

@@ -93,14 +93,16 @@ int hstu_attn_bwd(int dtype,
                   hipStream_t stream);
 
 /*
- * Device workspace the backward needs (bytes; 0 = none): a pre-clamped copy
- * of the bias rows when attn_bias is given, and an exact bf16 copy of q for
- * e4m3 inputs.  total_tokens = T = seq_offsets[B].  The caller allocates it
- * (the reference's FlyDSL backward likewise takes its dq-split workspace from
- * the caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).
+ * Device workspace the backward needs (bytes; 0 = none): with a bias
+ * (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows and 64
+ * partial copies of the bias gradient; for e4m3 inputs an exact bf16 copy of
+ * q.  total_tokens = T = seq_offsets[B].  The caller allocates it (the
+ * reference's FlyDSL backward likewise takes its dq-split workspace from the
+ * caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).  hstu_attn_bwd_dkdv and
+ * hstu_attn_bwd_dq must be given the same workspace.
  */
 int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int H, int D, int max_seq_len,
-                                      int has_bias);
+                                      int bias_R);
 
 /*
  * The two halves of hstu_attn_bwd, same arguments: hstu_attn_bwd_dkdv writes

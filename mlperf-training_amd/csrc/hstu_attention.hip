@@ -217,6 +217,8 @@ struct ScaleTile {
 
 
 // ---------------------------------------------------------------- params
+constexpr int kDbiasCopies = 64;
+
 struct AttnParams {
   const uint8_t* q;
   const uint8_t* k;
@@ -242,6 +244,7 @@ struct AttnParams {
   float* dbias;       // bias gradient, same shape (backward)
   const float* bias_ext;  // workspace: pre-clamped, pre-scaled bias rows [H, 2N+192]
   const uint8_t* q16;     // workspace: bf16 copy of e4m3 q, [T, H, D]
+  float* dbias_part;      // workspace: kDbiasCopies partial bias gradients [copies, H, 2R-1]
   int blocks_per_seq;  // grid = blocks_per_seq * B * H
 };
 
@@ -663,6 +666,62 @@ struct DqCfg {
   static int lds(bool bias, int R) { return HIST_OFF + (bias ? R * 4 : 0); }
 };
 
+// ---------------------------------------------------------------------------
+// Diagonal (relative-offset) sums of score gradients, for the bias gradient.
+//
+// A 16x16 MFMA result fragment holds element (row 4g+r, col li) in lane
+// 16g+li, register r; its diagonal index is li - 4g - r in [-15, 15].  Four
+// fragments of a 32x32 sub-tile, shifted by 16*S (S = -1, 0, +1), cover the
+// 63 diagonals -31..31.  diag_accumulate folds a fragment into four
+// per-lane partial sums a[k], where lane (g, p) of a[k] holds diagonal
+// p - 4g + 16(1-k); diag_reduce then gives each lane of the wave the whole
+// sum of one diagonal, p + 16(1-g), so that one conflict-free LDS add per
+// lane replaces 16 atomics that collide four ways.
+// ---------------------------------------------------------------------------
+
+// Row-local (16-lane) DPP move; a lane whose source is outside its row reads 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+template <int S>
+__device__ __forceinline__ void diag_accumulate(float (&a)[4], const float (&v)[4]) {
+  constexpr int HI = 1 - S, LO = 2 - S;
+  // lane p takes column p + r of register r (row_shl:r): diagonal p - 4g
+  a[HI] += v[0];
+  a[HI] += dpp_row<0x101>(v[1]);
+  a[HI] += dpp_row<0x102>(v[2]);
+  a[HI] += dpp_row<0x103>(v[3]);
+  // ... and column p + r - 16 (row_shr:16-r): diagonal p - 4g - 16
+  a[LO] += dpp_row<0x11F>(v[1]);
+  a[LO] += dpp_row<0x11E>(v[2]);
+  a[LO] += dpp_row<0x11D>(v[3]);
+}
+
+__device__ __forceinline__ float bperm(int src_lane, float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, x)));
+}
+
+// Sum over the wave of diagonal p + 16(1-g) for lane 16g+p (g = 3, p = 0 is
+// diagonal -32, always 0).
+__device__ __forceinline__ float diag_reduce(const float (&a)[4], int lane) {
+  const int g = lane >> 4, p = lane & 15;
+  // undo the 4g skew: lane (g, p) reads lane (g, p + 4g mod 16); wrapped
+  // reads land one bucket (16 diagonals) lower
+  const bool wrap = p + 4 * g >= 16;
+  const int src = 16 * g + ((p + 4 * g) & 15);
+  const float g0 = bperm(src, a[0]), g1 = bperm(src, a[1]), g2 = bperm(src, a[2]), g3 = bperm(src, a[3]);
+  const float b0 = wrap ? 0.f : g0, b1 = wrap ? g0 : g1, b2 = wrap ? g1 : g2, b3 = wrap ? g2 : g3;
+  // reduce-scatter over the four rows: row g keeps bucket g
+  const bool upper = lane >= 32, odd = (g & 1) != 0;
+  float ka = upper ? b2 : b0, kb = upper ? b3 : b1;
+  const float sa = upper ? b0 : b2, sb = upper ? b1 : b3;
+  ka += bperm(lane ^ 32, sa);
+  kb += bperm(lane ^ 32, sb);
+  return (odd ? kb : ka) + bperm(lane ^ 16, odd ? ka : kb);
+}
+
 template <int D, bool FP8, bool GENERIC, bool BIAS>
 __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) {
   using C = DqCfg<D>;
@@ -691,6 +750,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
   const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
   const int R1 = p.bias_R - 1;
   float* hist = (float*)(smem + C::HIST_OFF);
+  // This block's partial bias gradient: one of kDbiasCopies copies, so that
+  // the flushing atomics of different blocks rarely meet on one address.
+  float* dbias_copy = BIAS ? p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1)
+                           : nullptr;
   if constexpr (BIAS) {
     for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
   }
@@ -795,6 +858,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
           constexpr bool MASKED = decltype(masked_tag)::value;
           constexpr bool BCONST = decltype(bconst_tag)::value;
           const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
+          float dacc[4] = {0.f, 0.f, 0.f, 0.f};  // diagonal partial sums (bias gradient)
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {
             const int kt = 2 * c + h2;
@@ -807,7 +871,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
             }
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-              float dsv[4];
+              float dsv[4], dsr[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 float t = s[h2][qt][r] * cq[qt];
@@ -819,30 +883,34 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
                 float dpv = dp[h2][qt][r];
                 if constexpr (FP8) dpv *= svv[r];
                 float ds = dpv * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
-                int off = 0;
-                if constexpr (MASKED || (BIAS && !BCONST)) {
-                  off = (mw0 + qt * 16 + li) - (n0 + kt * 16 + 4 * g + r);
-                }
                 if constexpr (MASKED) {
                   const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
                   const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
                   ds = ok ? ds : 0.f;
                 }
                 if constexpr (BIAS) {
-                  if constexpr (BCONST) {
-                    dclamp += ds;
-                  } else if (off >= 0) {
-                    atomicAdd(&hist[min(off, R1)], ds);
-                  } else if (GENERIC && ds != 0.f) {
-                    atomicAdd(&p.dbias[(int64_t)h * (2 * p.bias_R - 1) + max(off, -R1) + R1], ds * p.inv_n);
-                  }
+                  if constexpr (BCONST) dclamp += ds;
+                  else dsr[r] = ds;
                 }
                 if constexpr (FP8) ds *= skv[r];
                 dsv[r] = ds;
               }
+              if constexpr (BIAS && !BCONST) {
+                if (qt == h2) diag_accumulate<0>(dacc, dsr);
+                else if (qt > h2) diag_accumulate<1>(dacc, dsr);
+                else diag_accumulate<-1>(dacc, dsr);
+              }
               dsa[qt][h2 * 2 + 0] = pack_bf16(dsv[0], dsv[1]);
               dsa[qt][h2 * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
             }
+          }
+          if constexpr (BIAS && !BCONST) {
+            // this lane's diagonal of the 32x32 sub-tile, as a relative offset i - j
+            const float dv = diag_reduce(dacc, lane);
+            const int off = (mw0 - n0 - 32 * c) + li + 16 - 16 * g;
+            if (off >= R1) dclamp += dv;
+            else if (off >= 0) atomicAdd(&hist[off], dv);
+            else if (GENERIC && dv != 0.f) atomicAdd(&dbias_copy[max(off, -R1) + R1], dv);
           }
         };
         if (need_mask) {
@@ -870,10 +938,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
   if constexpr (BIAS) {
     if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
     __syncthreads();
-    float* dst = p.dbias + (int64_t)h * (2 * p.bias_R - 1) + R1;
+    float* dst = dbias_copy + R1;
     for (int i = tid; i < p.bias_R; i += kThreads) {
       const float v = hist[i];
-      if (v != 0.f) atomicAdd(&dst[i], v * p.inv_n);
+      if (v != 0.f) atomicAdd(&dst[i], v);
     }
   }
 
@@ -1201,6 +1269,15 @@ __global__ void build_bias_ext(const float* bias, int H, int R, int N, float* ex
   }
 }
 
+// dbias = inv_n * sum of the kDbiasCopies partial copies.
+__global__ void reduce_dbias(const float* part, int n, float inv_n, float* dbias) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int c = 0; c < kDbiasCopies; ++c) s += part[(int64_t)c * n + i];
+  dbias[i] = s * inv_n;
+}
+
 __global__ void fill_f32(float* p, int n, float v) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -1333,10 +1410,14 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
 namespace {
 enum BwdParts { kBwdDkdv = 1, kBwdDq = 2, kBwdAll = 3 };
 
-int64_t bias_ext_bytes(int H, int N) { return ((int64_t)H * (2 * N + 192) * 4 + 255) / 256 * 256; }
-int64_t bwd_workspace_bytes(int dtype, int64_t T, int H, int D, int N, bool bias) {
-  int64_t b = bias ? bias_ext_bytes(H, N) : 0;
-  if (dtype == HSTU_DTYPE_FP8_E4M3) b += T * H * D * 2;
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+int64_t bias_ext_bytes(int H, int N) { return align256((int64_t)H * (2 * N + 192) * 4); }
+int64_t dbias_part_bytes(int H, int R) { return align256((int64_t)kDbiasCopies * H * (2 * R - 1) * 4); }
+// layout: [pre-clamped bias rows][bf16 copy of e4m3 q][partial bias gradients]
+int64_t bwd_workspace_bytes(int dtype, int64_t T, int H, int D, int N, int R) {
+  int64_t b = R > 0 ? bias_ext_bytes(H, N) : 0;
+  if (dtype == HSTU_DTYPE_FP8_E4M3) b += align256(T * H * D * 2);
+  if (R > 0) b += dbias_part_bytes(H, R);
   return b;
 }
 
@@ -1398,21 +1479,26 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   p.dbias = dbias;
   const bool has_bias = attn_bias != nullptr;
   hipError_t e;
+  const int64_t need = bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias ? bias_R : 0);
+  if (total_tokens < 0 || workspace_bytes < need || (workspace == nullptr && need > 0)) return HSTU_E_BAD_ARG;
+  uint8_t* ws = (uint8_t*)workspace;
+  uint8_t* ws_part = nullptr;
+  {
+    uint8_t* w = ws;
+    if (has_bias) w += bias_ext_bytes(H, max_seq_len);
+    if (dtype == HSTU_DTYPE_FP8_E4M3) w += align256(total_tokens * H * D * 2);
+    ws_part = has_bias ? w : nullptr;
+  }
   if (parts & kBwdDkdv) {
-    if (total_tokens < 0 || workspace_bytes < bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias) ||
-        (workspace == nullptr && bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias) > 0))
-      return HSTU_E_BAD_ARG;
-    uint8_t* ws = (uint8_t*)workspace;
     if (has_bias) {
       p.bias_ext = (const float*)ws;
       hipLaunchKernelGGL(build_bias_ext, dim3((2 * max_seq_len + 192 + 255) / 256, H), dim3(256), 0, stream,
                          attn_bias, H, bias_R, max_seq_len, (float*)ws);
-      ws += bias_ext_bytes(H, max_seq_len);
     }
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
-      p.q16 = ws;
+      p.q16 = ws + (has_bias ? bias_ext_bytes(H, max_seq_len) : 0);
       hipLaunchKernelGGL(convert_q8_bf16, dim3(1024), dim3(256), 0, stream, (const uint8_t*)q, q_row_stride,
-                         seq_offsets, B, H, D, (uint16_t*)ws);
+                         seq_offsets, B, H, D, (uint16_t*)p.q16);
     }
     // dK / dV: 128-key blocks, longest query range first.
 #define HSTU_DKV(DD, F8, G, BB) launch(hstu_bwd_dkdv_kernel<DD, F8, G, BB>, DkvCfg<DD, F8, BB>::LDS, grid, p, stream)
@@ -1429,9 +1515,10 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
     if (e != hipSuccess) return (int)e;
   }
   if (parts & kBwdDq) {
-    if (dbias != nullptr) {
-      const int n = H * (2 * bias_R - 1);
-      hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, dbias, n, 0.f);
+    if (has_bias) {
+      p.dbias_part = (float*)ws_part;
+      const int n = kDbiasCopies * H * (2 * bias_R - 1);
+      hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 0.f);
     }
     // dQ (+ bias gradient): 128-query blocks, longest key range first.
     const int lds = DqCfg<128>::lds(has_bias, bias_R);
@@ -1448,6 +1535,11 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
 #undef HSTU_DQ_B
 #undef HSTU_DQ
     if (e != hipSuccess) return (int)e;
+    if (has_bias && dbias != nullptr) {
+      const int n = H * (2 * bias_R - 1);
+      hipLaunchKernelGGL(reduce_dbias, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, p.inv_n,
+                         dbias);
+    }
   }
   hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
                      (parts & kBwdDq) ? p.dq : p.dk, (parts & kBwdDq) ? p.dq_rs : p.dk_rs,
@@ -1473,8 +1565,8 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
       hipStream_t stream
 
 extern "C" int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int H, int D, int max_seq_len,
-                                                 int has_bias) {
-  return bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias != 0);
+                                                 int bias_R) {
+  return bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, bias_R);
 }
 extern "C" int hstu_attn_bwd(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdAll, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dkdv(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDkdv, HSTU_BWD_ARGS); }

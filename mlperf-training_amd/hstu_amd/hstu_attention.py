@@ -207,7 +207,7 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
         if bias is None or dbias.shape != bias.shape or dbias.dtype != torch.float32 or not dbias.is_contiguous():
             raise ValueError("dbias must be a contiguous fp32 tensor shaped like attn_bias")
     dtype_code = _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16
-    ws_bytes = _lib.fn("hstu_attn_bwd_workspace_bytes")(dtype_code, T, H, D, int(N), int(bias is not None))
+    ws_bytes = _lib.fn("hstu_attn_bwd_workspace_bytes")(dtype_code, T, H, D, int(N), R)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     st = _lib.fn("hstu_attn_bwd")(
         _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16,

@@ -46,8 +46,9 @@ def test_workspace_size():
     f = lib.fn("hstu_attn_bwd_workspace_bytes")
     assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 0) == 0
     assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, 4, 128, 4096, 0) == 1000 * 4 * 128 * 2
-    ext = 4 * (2 * 4096 + 192) * 4
-    assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 1) == (ext + 255) // 256 * 256
+    ext = (4 * (2 * 4096 + 192) * 4 + 255) // 256 * 256
+    part = (64 * 4 * (2 * 1024 - 1) * 4 + 255) // 256 * 256
+    assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 1024) == ext + part
 
 
 def test_bad_arguments_rejected_before_launch():
