@@ -63,7 +63,16 @@ int hstu_attn_fwd(int dtype,
                   const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
                   const float* attn_bias, int bias_R,
                   void* out, int64_t out_row_stride,
+                  void* workspace, int64_t workspace_bytes, int64_t total_tokens,
                   hipStream_t stream);
+
+/*
+ * Device workspace hstu_attn_fwd needs (bytes, > 0): the per-call block
+ * schedule (which XCD runs which (sequence, head) block).  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.
+ * No reference counterpart: the reference's launchers size their grids from
+ * the host arguments alone (ops/flydsl/hstu_flydsl_mha.py:2036-2040).
+ */
+int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len);
 
 /*
  * Backward of hstu_attn_fwd.  Writes dq, dk, dv (bf16, caller-owned, may be
@@ -93,15 +102,15 @@ int hstu_attn_bwd(int dtype,
                   hipStream_t stream);
 
 /*
- * Device workspace the backward needs (bytes; 0 = none): with a bias
- * (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows and 64
+ * Device workspace the backward needs (bytes): the block schedule; with a
+ * bias (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows and 64
  * partial copies of the bias gradient; for e4m3 inputs an exact bf16 copy of
- * q.  total_tokens = T = seq_offsets[B].  The caller allocates it (the
+ * q.  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.  The caller allocates it (the
  * reference's FlyDSL backward likewise takes its dq-split workspace from the
  * caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).  hstu_attn_bwd_dkdv and
  * hstu_attn_bwd_dq must be given the same workspace.
  */
-int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int H, int D, int max_seq_len,
+int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len,
                                       int bias_R);
 
 /*

@@ -245,28 +245,42 @@ struct AttnParams {
   const float* bias_ext;  // workspace: pre-clamped, pre-scaled bias rows [H, 2N+192]
   const uint8_t* q16;     // workspace: bf16 copy of e4m3 q, [T, H, D]
   float* dbias_part;      // workspace: kDbiasCopies partial bias gradients [copies, H, 2R-1]
-  int blocks_per_seq;  // grid = blocks_per_seq * B * H
+  const int* sched_items;  // block schedule (build_schedule): [8][sched_cap] (sequence*H + head)
+  const int* sched_start;  // [8][sched_cap + 1] first block position of each item on its XCD
+  const int* sched_count;  // [8] items per XCD
+  int sched_cap;
+  int blocks_per_seq;  // ceil(N / 128)
 };
 
 struct SeqCtx {
   int64_t start;
   int L, b, h, blk;
 };
-__device__ __forceinline__ SeqCtx seq_ctx(const AttnParams& p, bool reverse) {
-  SeqCtx c;
-  const int BH = p.B * p.H;
-  const int slot = blockIdx.x / BH;
-  // Rotate (sequence, head) by the block level: workgroup i runs on XCD i % 8,
-  // so without the rotation every block of one (sequence, head) would land on
-  // one XCD and XCD load would follow the length distribution.
-  int bh = blockIdx.x - slot * BH + slot;
-  bh = bh >= BH ? bh - BH : bh;
+// Workgroup -> (sequence, head, 128-row block), from the schedule that
+// build_schedule wrote: workgroup i runs on XCD x = i % 8 and takes the
+// (i / 8)-th block of that XCD's list.  heavy_last: the block with the most
+// key tiles is the last one of its sequence (forward, dQ) rather than the
+// first (dK/dV); each item's blocks run heaviest first.  False = no work.
+__device__ __forceinline__ bool seq_ctx(const AttnParams& p, bool heavy_last, SeqCtx& c) {
+  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int n = p.sched_count[x];
+  const int* st = p.sched_start + x * (p.sched_cap + 1);
+  if (k >= st[n]) return false;
+  int lo = 0, hi = n - 1;  // the last item whose first block is <= k
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (st[mid] <= k) lo = mid;
+    else hi = mid - 1;
+  }
+  const int bh = p.sched_items[x * p.sched_cap + lo];
+  const int m = k - st[lo];
   c.b = bh / p.H;
   c.h = bh - c.b * p.H;
-  c.blk = reverse ? p.blocks_per_seq - 1 - slot : slot;
   c.start = p.seq_offsets[c.b];
   c.L = min((int)(p.seq_offsets[c.b + 1] - c.start), p.N);
-  return c;
+  const int nb = (c.L + 127) / 128;
+  c.blk = heavy_last ? nb - 1 - m : m;
+  return true;
 }
 __device__ __forceinline__ MaskCtx mask_ctx(const AttnParams& p, const SeqCtx& c) {
   MaskCtx m;
@@ -318,7 +332,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   static_assert(!FP8 || D == 128, "e4m3 path is specialised for D = 128");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
-  const SeqCtx sc = seq_ctx(p, /*reverse=*/true);
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/true, sc)) return;
   const int L = sc.L, h = sc.h;
   const int m0 = sc.blk * C::BM;
   if (m0 >= L) return;
@@ -728,7 +743,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
   constexpr int ES = FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
-  const SeqCtx sc = seq_ctx(p, /*reverse=*/true);
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/true, sc)) return;
   const int L = sc.L, h = sc.h;
   const int m0 = sc.blk * C::BM;
   if (m0 >= L) return;
@@ -1003,7 +1019,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   constexpr int ES = FP8 ? 1 : 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
 
-  const SeqCtx sc = seq_ctx(p, /*reverse=*/false);
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/false, sc)) return;
   const int L = sc.L, h = sc.h;
   const int n0 = sc.blk * C::BN;
   if (n0 >= L) return;
@@ -1269,6 +1286,138 @@ __global__ void build_bias_ext(const float* bias, int H, int R, int N, float* ex
   }
 }
 
+// ---------------------------------------------------------------------------
+// Block schedule.  Workgroups are dispatched to the 8 XCDs round-robin
+// (workgroup i -> XCD i % 8), and each XCD has its own L2.  The schedule
+// gives every XCD whole (sequence, head) items, so the 128-row blocks of one
+// item run on one XCD at about the same time and re-read that item's K/V
+// (forward, dQ) or Q/dO (dK/dV) tiles from that XCD's L2 instead of from
+// HBM.  Items are ranked by block count (descending; counting sort, ties in
+// any order) and dealt in snake order 0..7,7..0,..., which keeps the per-XCD
+// work of a sorted list within one item of even; on an XCD they run in rank
+// order, heaviest first.  One workgroup of 1024 threads; O(B*H) work.
+// Output (ints): items[8][cap], start[8][cap+1] (exclusive block-count
+// prefix per XCD, start[x][n_x] = the XCD's total), count[8]; scratch nb[B],
+// rank[B].
+// ---------------------------------------------------------------------------
+constexpr int kSchedBins = 1024;  // block counts >= 1023 share the last bin (order only)
+
+__host__ __device__ inline int sched_cap(int B, int H) { return (B * H + 7) / 8; }
+inline int64_t sched_ints(int B, int H) {
+  const int64_t cap = sched_cap(B, H);
+  return 8 * cap + 8 * (cap + 1) + 8 + 2 * (int64_t)B;
+}
+
+__global__ void __launch_bounds__(1024) build_schedule(const int64_t* seq_offsets, int B, int H, int N, int* ws) {
+  const int cap = sched_cap(B, H);
+  int* items = ws;
+  int* start = items + 8 * cap;
+  int* count = start + 8 * (cap + 1);
+  int* nbv = count + 8;
+  int* rank = nbv + B;
+  __shared__ int bins[kSchedBins];
+  __shared__ int scan[kSchedBins];
+  const int tid = threadIdx.x;  // blockDim.x == kSchedBins
+  bins[tid] = 0;
+  __syncthreads();
+  for (int b = tid; b < B; b += kSchedBins) {
+    const int64_t L = min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N);
+    const int nb = (int)((max(L, (int64_t)0) + 127) / 128);
+    nbv[b] = nb;
+    atomicAdd(&bins[min(nb, kSchedBins - 1)], 1);
+  }
+  __syncthreads();
+  // exclusive prefix in descending bin order: first rank of bin v = sum of bins above v
+  const int v = kSchedBins - 1 - tid;
+  const int mine = bins[v];
+  scan[tid] = mine;
+  __syncthreads();
+  for (int off = 1; off < kSchedBins; off <<= 1) {
+    const int add = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  bins[v] = scan[tid] - mine;
+  __syncthreads();
+  for (int b = tid; b < B; b += kSchedBins) rank[b] = atomicAdd(&bins[min(nbv[b], kSchedBins - 1)], 1);
+  __syncthreads();
+  // item r = rank*H + head -> XCD by snake order, dense index j on that XCD
+  for (int b = tid; b < B; b += kSchedBins) {
+    const int nb = nbv[b];
+    for (int h = 0; h < H; ++h) {
+      const int r = rank[b] * H + h, q = r & 15;
+      const int x = q < 8 ? q : 15 - q;
+      const int j = (r >> 4) * 2 + (q >= 8 ? 1 : 0);
+      items[x * cap + j] = b * H + h;
+      start[x * (cap + 1) + j] = nb;
+    }
+  }
+  __syncthreads();
+  // per XCD (one wave each): exclusive scan of the block counts
+  const int wave = tid >> 6, lane = tid & 63;
+  if (wave < 8) {
+    const int x = wave, BH = B * H, full = BH >> 4, rem = BH & 15;
+    const int n = 2 * full + (x < rem ? 1 : 0) + (15 - x < rem ? 1 : 0);
+    int* st = start + x * (cap + 1);
+    int carry = 0;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      const int j = j0 + lane;
+      const int c = j < n ? st[j] : 0;
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      if (j < n) st[j] = carry + incl - c;
+      carry += __shfl(incl, 63);
+    }
+    if (lane == 0) {
+      st[n] = carry;
+      count[x] = n;
+    }
+  }
+}
+
+// Launch build_schedule into ws (sched_ints(B, H) ints) and point p at it.
+hipError_t schedule(AttnParams& p, const int64_t* seq_offsets, int B, int H, int N, int* ws, hipStream_t stream) {
+  hipLaunchKernelGGL(build_schedule, dim3(1), dim3(kSchedBins), 0, stream, seq_offsets, B, H, N, ws);
+  p.sched_cap = sched_cap(B, H);
+  p.sched_items = ws;
+  p.sched_start = ws + 8 * p.sched_cap;
+  p.sched_count = p.sched_start + 8 * (p.sched_cap + 1);
+  return hipGetLastError();
+}
+// grid covering every XCD's longest possible list
+int sched_grid(int B, int H, int N) { return 8 * sched_cap(B, H) * ((N + 127) / 128); }
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+int64_t bias_ext_bytes(int H, int N) { return align256((int64_t)H * (2 * N + 192) * 4); }
+int64_t dbias_part_bytes(int H, int R) { return align256((int64_t)kDbiasCopies * H * (2 * R - 1) * 4); }
+int64_t sched_bytes(int B, int H) { return align256(sched_ints(B, H) * 4); }
+int64_t fwd_workspace_bytes(int /*dtype*/, int64_t /*T*/, int B, int H, int /*D*/) { return sched_bytes(B, H); }
+// Backward workspace: [block schedule][pre-clamped bias rows][bf16 copy of
+// e4m3 q][partial bias gradients]; byte offsets of each part.
+struct BwdWs {
+  int64_t sched, bias_ext, q16, part, total;
+};
+BwdWs bwd_ws(int dtype, int64_t T, int B, int H, int D, int N, int R) {
+  BwdWs w;
+  int64_t o = 0;
+  w.sched = o;
+  o += sched_bytes(B, H);
+  w.bias_ext = o;
+  if (R > 0) o += bias_ext_bytes(H, N);
+  w.q16 = o;
+  if (dtype == HSTU_DTYPE_FP8_E4M3) o += align256(T * H * D * 2);
+  w.part = o;
+  if (R > 0) o += dbias_part_bytes(H, R);
+  w.total = o;
+  return w;
+}
+
+
 // dbias = inv_n * sum of the kDbiasCopies partial copies.
 __global__ void reduce_dbias(const float* part, int n, float inv_n, float* dbias) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1351,7 +1500,8 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
                              int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
                              int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len,
                              int contextual_seq_len, const float* attn_bias, int bias_R, void* out,
-                             int64_t out_row_stride, hipStream_t stream) {
+                             int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                             int64_t total_tokens, hipStream_t stream) {
   if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
                     v_scale, bias_R, attn_bias))
     return HSTU_E_BAD_ARG;
@@ -1360,6 +1510,9 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
       !row_alignment_ok(dtype, v_row_stride, v))
     return HSTU_E_UNSUPPORTED;
   if (B == 0) return 0;
+  if (total_tokens < 0 || workspace == nullptr ||
+      workspace_bytes < fwd_workspace_bytes(dtype, total_tokens, B, H, D))
+    return HSTU_E_BAD_ARG;
   AttnParams p{};
   p.q = (const uint8_t*)q;
   p.k = (const uint8_t*)k;
@@ -1385,13 +1538,14 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
   p.contextual_seq_len = contextual_seq_len;
   const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
   p.blocks_per_seq = (max_seq_len + 127) / 128;
-  const int grid = p.blocks_per_seq * B * H;
+  const int grid = sched_grid(B, H, max_seq_len);
   p.bias = attn_bias;
   p.bias_R = bias_R;
+  hipError_t e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)workspace, stream);
+  if (e != hipSuccess) return (int)e;
 #define HSTU_FWD(DD, F8, G, BB) launch(hstu_fwd_kernel<DD, F8, G, BB>, FwdCfg<DD, F8>::LDS, grid, p, stream)
 #define HSTU_FWD_B(DD, F8, G) (has_bias ? HSTU_FWD(DD, F8, G, true) : HSTU_FWD(DD, F8, G, false))
   const bool has_bias = attn_bias != nullptr;
-  hipError_t e;
   if (dtype == HSTU_DTYPE_FP8_E4M3) {
     e = generic ? HSTU_FWD_B(128, true, true) : HSTU_FWD_B(128, true, false);
   } else if (D == 128) {
@@ -1409,17 +1563,6 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
 
 namespace {
 enum BwdParts { kBwdDkdv = 1, kBwdDq = 2, kBwdAll = 3 };
-
-int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
-int64_t bias_ext_bytes(int H, int N) { return align256((int64_t)H * (2 * N + 192) * 4); }
-int64_t dbias_part_bytes(int H, int R) { return align256((int64_t)kDbiasCopies * H * (2 * R - 1) * 4); }
-// layout: [pre-clamped bias rows][bf16 copy of e4m3 q][partial bias gradients]
-int64_t bwd_workspace_bytes(int dtype, int64_t T, int H, int D, int N, int R) {
-  int64_t b = R > 0 ? bias_ext_bytes(H, N) : 0;
-  if (dtype == HSTU_DTYPE_FP8_E4M3) b += align256(T * H * D * 2);
-  if (R > 0) b += dbias_part_bytes(H, R);
-  return b;
-}
 
 int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
                   const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
@@ -1473,30 +1616,26 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   p.contextual_seq_len = contextual_seq_len;
   p.blocks_per_seq = (max_seq_len + 127) / 128;
   const bool generic = num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0;
-  const int grid = p.blocks_per_seq * B * H;
+  const int grid = sched_grid(B, H, max_seq_len);
   p.bias = attn_bias;
   p.bias_R = bias_R;
   p.dbias = dbias;
   const bool has_bias = attn_bias != nullptr;
   hipError_t e;
-  const int64_t need = bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, has_bias ? bias_R : 0);
-  if (total_tokens < 0 || workspace_bytes < need || (workspace == nullptr && need > 0)) return HSTU_E_BAD_ARG;
+  const BwdWs wl = bwd_ws(dtype, total_tokens, B, H, D, max_seq_len, has_bias ? bias_R : 0);
+  if (total_tokens < 0 || workspace_bytes < wl.total || workspace == nullptr) return HSTU_E_BAD_ARG;
   uint8_t* ws = (uint8_t*)workspace;
-  uint8_t* ws_part = nullptr;
-  {
-    uint8_t* w = ws;
-    if (has_bias) w += bias_ext_bytes(H, max_seq_len);
-    if (dtype == HSTU_DTYPE_FP8_E4M3) w += align256(total_tokens * H * D * 2);
-    ws_part = has_bias ? w : nullptr;
-  }
+  uint8_t* ws_part = has_bias ? ws + wl.part : nullptr;
+  e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)(ws + wl.sched), stream);
+  if (e != hipSuccess) return (int)e;
   if (parts & kBwdDkdv) {
     if (has_bias) {
-      p.bias_ext = (const float*)ws;
+      p.bias_ext = (const float*)(ws + wl.bias_ext);
       hipLaunchKernelGGL(build_bias_ext, dim3((2 * max_seq_len + 192 + 255) / 256, H), dim3(256), 0, stream,
-                         attn_bias, H, bias_R, max_seq_len, (float*)ws);
+                         attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
     }
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
-      p.q16 = ws + (has_bias ? bias_ext_bytes(H, max_seq_len) : 0);
+      p.q16 = ws + wl.q16;
       hipLaunchKernelGGL(convert_q8_bf16, dim3(1024), dim3(256), 0, stream, (const uint8_t*)q, q_row_stride,
                          seq_offsets, B, H, D, (uint16_t*)p.q16);
     }
@@ -1564,9 +1703,17 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
       int64_t dv_row_stride, float *dbias, void *workspace, int64_t workspace_bytes, int64_t total_tokens,        \
       hipStream_t stream
 
-extern "C" int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int H, int D, int max_seq_len,
-                                                 int bias_R) {
-  return bwd_workspace_bytes(dtype, total_tokens, H, D, max_seq_len, bias_R);
+extern "C" int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D,
+                                                 int max_seq_len, int bias_R) {
+  if (B < 0 || H <= 0 || total_tokens < 0) return -1;
+  return bwd_ws(dtype, total_tokens, B, H, D, max_seq_len, bias_R).total;
+}
+
+extern "C" int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D,
+                                                 int max_seq_len) {
+  (void)max_seq_len;
+  if (B < 0 || H <= 0 || total_tokens < 0) return -1;
+  return fwd_workspace_bytes(dtype, total_tokens, B, H, D);
 }
 extern "C" int hstu_attn_bwd(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdAll, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dkdv(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDkdv, HSTU_BWD_ARGS); }

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "hstu_version",
     "hstu_attn_fwd",
     "hstu_attn_bwd",
+    "hstu_attn_fwd_workspace_bytes",
     "hstu_attn_bwd_workspace_bytes",
     "hstu_attn_bwd_dkdv",
     "hstu_attn_bwd_dq",
@@ -57,14 +58,15 @@ _SIGNATURES = {
     "hstu_attn_fwd": (
         _i32,
         [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
-         _f32, _vp, _i32, _i32, _vp, _i32, _vp, _i64, _vp],
+         _f32, _vp, _i32, _i32, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp],
     ),
+    "hstu_attn_fwd_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i32, _i32]),
     "hstu_attn_bwd": (
         _i32,
         [_i32, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32,
          _i32, _f32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp],
     ),
-    "hstu_attn_bwd_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i32, _i32]),
+    "hstu_attn_bwd_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i32, _i32, _i32]),
     "hstu_attn_bwd_dkdv": None,
     "hstu_attn_bwd_dq": None,
     "hstu_fp8_gemm_rowcol": (

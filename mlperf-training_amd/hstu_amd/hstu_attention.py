@@ -121,6 +121,13 @@ def _scale_tensor(s: ScaleArg, T: int, H: int, device) -> Tuple[Optional[torch.T
     return s, H, 1
 
 
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    """Caller-owned device workspace of an entry point (the library allocates nothing)."""
+    if nbytes < 0:
+        raise ValueError("bad sizes for the workspace query")
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
 def _seq_offsets_i64(seq_offsets: torch.Tensor) -> torch.Tensor:
     return seq_offsets.to(torch.int64).contiguous()
 
@@ -169,14 +176,17 @@ def _launch_fwd(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len, conte
     offs = _seq_offsets_i64(seq_offsets)
     nt = _num_targets_i32(num_targets)
     bias, R = _bias_args(attn_bias, H)
+    dt = _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16
+    B = offs.numel() - 1
+    ws = _workspace(_lib.fn("hstu_attn_fwd_workspace_bytes")(dt, T, B, H, D, int(N)), q.device)
     st = _lib.fn("hstu_attn_fwd")(
-        _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16,
+        dt,
         q.data_ptr(), k.data_ptr(), v.data_ptr(), _row_stride(q), _row_stride(k), _row_stride(v),
         _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs), srs, shs,
         offs.data_ptr(), offs.numel() - 1, H, D, int(N), float(alpha),
         _lib.ptr(nt), int(max_attn_len), int(contextual_seq_len),
         _lib.ptr(bias), R,
-        out.data_ptr(), H * D, _stream(q.device))
+        out.data_ptr(), H * D, ws.data_ptr(), ws.numel(), T, _stream(q.device))
     _lib.check(st, "hstu_attn_fwd")
     return out
 
@@ -207,8 +217,8 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
         if bias is None or dbias.shape != bias.shape or dbias.dtype != torch.float32 or not dbias.is_contiguous():
             raise ValueError("dbias must be a contiguous fp32 tensor shaped like attn_bias")
     dtype_code = _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16
-    ws_bytes = _lib.fn("hstu_attn_bwd_workspace_bytes")(dtype_code, T, H, D, int(N), R)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    ws = _workspace(_lib.fn("hstu_attn_bwd_workspace_bytes")(dtype_code, T, offs.numel() - 1, H, D, int(N), R),
+                    q.device)
     st = _lib.fn("hstu_attn_bwd")(
         _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16,
         dout.data_ptr(), _row_stride(dout),
@@ -219,7 +229,7 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
         _lib.ptr(bias), R,
         targets[0].data_ptr(), targets[1].data_ptr(), targets[2].data_ptr(),
         _row_stride(targets[0]), _row_stride(targets[1]), _row_stride(targets[2]),
-        _lib.ptr(dbias), ws.data_ptr(), ws_bytes, T, _stream(q.device))
+        _lib.ptr(dbias), ws.data_ptr(), ws.numel(), T, _stream(q.device))
     _lib.check(st, "hstu_attn_bwd")
     for dst, src in zip((dq, dk, dv), targets):
         if dst is not src:

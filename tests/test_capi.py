@@ -19,7 +19,7 @@ def _declared():
 
 def test_header_declares_expected_entry_points():
     names = _declared()
-    for n in ("hstu_attn_fwd", "hstu_attn_bwd", "hstu_attn_bwd_dkdv", "hstu_attn_bwd_dq",
+    for n in ("hstu_attn_fwd", "hstu_attn_fwd_workspace_bytes", "hstu_attn_bwd", "hstu_attn_bwd_dkdv", "hstu_attn_bwd_dq",
               "hstu_attn_bwd_workspace_bytes", "hstu_fp8_gemm_rowcol", "hstu_quantize_e4m3_rows", "hstu_version"):
         assert n in names
 
@@ -43,12 +43,22 @@ def test_version_string():
 def test_workspace_size():
     import hstu_amd._lib as lib
 
+    def a256(n):
+        return (n + 255) // 256 * 256
+
+    B, H = 10, 4
+    cap = (B * H + 7) // 8
+    sched = a256(4 * (8 * cap + 8 * (cap + 1) + 8 + 2 * B))  # items, starts, counts, per-sequence scratch
     f = lib.fn("hstu_attn_bwd_workspace_bytes")
-    assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 0) == 0
-    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, 4, 128, 4096, 0) == 1000 * 4 * 128 * 2
-    ext = (4 * (2 * 4096 + 192) * 4 + 255) // 256 * 256
-    part = (64 * 4 * (2 * 1024 - 1) * 4 + 255) // 256 * 256
-    assert f(lib.HSTU_DTYPE_BF16, 1000, 4, 128, 4096, 1024) == ext + part
+    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 0) == sched
+    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096, 0) == sched + 1000 * 4 * 128 * 2
+    ext = a256(4 * (2 * 4096 + 192) * 4)
+    part = a256(64 * 4 * (2 * 1024 - 1) * 4)
+    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 1024) == sched + ext + part
+    assert f(lib.HSTU_DTYPE_BF16, -1, B, H, 128, 4096, 0) == -1
+    g = lib.fn("hstu_attn_fwd_workspace_bytes")
+    assert g(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096) == sched
+    assert g(lib.HSTU_DTYPE_BF16, 1000, -1, H, 128, 4096) == -1
 
 
 def test_bad_arguments_rejected_before_launch():
@@ -57,16 +67,16 @@ def test_bad_arguments_rejected_before_launch():
     fwd = lib.fn("hstu_attn_fwd")
     # unknown dtype
     assert fwd(7, 16, 16, 16, 512, 512, 512, None, None, None, 0, 0, 16, 1, 4, 128, 64, 0.1,
-               None, 0, 0, None, 0, 16, 512, None) == lib.HSTU_E_BAD_ARG
+               None, 0, 0, None, 0, 16, 512, 16, 4096, 1000, None) == lib.HSTU_E_BAD_ARG
     # row stride smaller than H*D
     assert fwd(0, 16, 16, 16, 100, 512, 512, None, None, None, 0, 0, 16, 1, 4, 128, 64, 0.1,
-               None, 0, 0, None, 0, 16, 512, None) == lib.HSTU_E_BAD_ARG
+               None, 0, 0, None, 0, 16, 512, 16, 4096, 1000, None) == lib.HSTU_E_BAD_ARG
     # e4m3 without scales
     assert fwd(1, 16, 16, 16, 512, 512, 512, None, None, None, 0, 0, 16, 1, 4, 128, 64, 0.1,
-               None, 0, 0, None, 0, 16, 512, None) == lib.HSTU_E_BAD_ARG
+               None, 0, 0, None, 0, 16, 512, 16, 4096, 1000, None) == lib.HSTU_E_BAD_ARG
     # unsupported head dim
     assert fwd(0, 16, 16, 16, 384, 384, 384, None, None, None, 0, 0, 16, 1, 4, 96, 64, 0.1,
-               None, 0, 0, None, 0, 16, 384, None) == lib.HSTU_E_UNSUPPORTED
+               None, 0, 0, None, 0, 16, 384, 16, 4096, 1000, None) == lib.HSTU_E_UNSUPPORTED
     gemm = lib.fn("hstu_fp8_gemm_rowcol")
     # N not a multiple of 128
     assert gemm(16, 512, 16, 512, 16, 0, 16, 0, None, None, 0, 16, 100, 0, None, 8, 100, 512, 0, 0,
