@@ -68,9 +68,9 @@ int hstu_attn_fwd(int dtype,
 
 /*
  * Device workspace hstu_attn_fwd needs (bytes, > 0): the per-call block
- * schedule (which XCD runs which (sequence, head) block).  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.
- * No reference counterpart: the reference's launchers size their grids from
- * the host arguments alone (ops/flydsl/hstu_flydsl_mha.py:2036-2040).
+ * schedule (which XCD runs which (sequence, head) block).  total_tokens = T
+ * = seq_offsets[B].  Returns -1 for bad sizes.  The reference's launchers
+ * take no workspace (ops/flydsl/hstu_flydsl_mha.py:2036-2046).
  */
 int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len);
 
@@ -105,19 +105,19 @@ int hstu_attn_bwd(int dtype,
  * Device workspace the backward needs (bytes): the block schedule; with a
  * bias (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows and 64
  * partial copies of the bias gradient; for e4m3 inputs an exact bf16 copy of
- * q.  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.  The caller allocates it (the
- * reference's FlyDSL backward likewise takes its dq-split workspace from the
- * caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).  hstu_attn_bwd_dkdv and
- * hstu_attn_bwd_dq must be given the same workspace.
+ * q.  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.  The
+ * caller allocates it (the reference's FlyDSL backward likewise takes its
+ * dq-split workspace from the caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).
+ * hstu_attn_bwd_dkdv and hstu_attn_bwd_dq must be given the same workspace.
  */
 int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len,
                                       int bias_R);
 
 /*
  * The two halves of hstu_attn_bwd, same arguments: hstu_attn_bwd_dkdv writes
- * dk and dv only (dq may be NULL; it alone uses the workspace);
- * hstu_attn_bwd_dq writes dq and dbias only (dk, dv may be NULL).  They read the same inputs and may run concurrently on two
- * streams.  The reference launches its backward in the same two parts when
+ * dk and dv only (dq may be NULL); hstu_attn_bwd_dq writes dq and dbias only
+ * (dk, dv may be NULL).  Each writes its own parts of the shared workspace,
+ * so run them in order on one stream.  The reference launches its backward in the same two parts when
  * the dq-split is armed: the fused dK/dV kernel, then dq from the stored ds
  * tiles (ops/flydsl/hstu_flydsl_mha.py:1707-1740, ops/flydsl/hstu_dq_split.py:348);
  * here dq recomputes the score tile instead of storing it.

@@ -219,6 +219,11 @@ struct ScaleTile {
 // ---------------------------------------------------------------- params
 constexpr int kDbiasCopies = 64;
 
+// Length of one head's row of the pre-clamped bias table (build_bias_ext):
+// entry off + N + 127 holds the bias of relative offset off, for every off a
+// forward or dK/dV tile window can ask for.
+__host__ __device__ inline int bias_ext_len(int N) { return 2 * N + 256; }
+
 struct AttnParams {
   const uint8_t* q;
   const uint8_t* k;
@@ -295,6 +300,13 @@ __device__ __forceinline__ MaskCtx mask_ctx(const AttnParams& p, const SeqCtx& c
 // =====================================================================
 // Forward.  Block = 128 query rows (32 per wave), key tiles of 64.
 // =====================================================================
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 template <int D, bool FP8>
 struct FwdCfg {
   static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
@@ -1006,12 +1018,6 @@ struct DkvCfg {
   static constexpr int LDS = NSTAGE * STAGE;
 };
 
-// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm_le() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 template <int D, bool FP8, bool GENERIC, bool BIAS>
 __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p) {
@@ -1042,7 +1048,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   const BufRsrc sq_rsrc = make_rsrc(FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr,
                                     FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u);
   // pre-clamped, pre-scaled bias table: entry off + N + 127 holds the bias of offset off
-  const int ext_len = 2 * p.N + 192;
+  const int ext_len = bias_ext_len(p.N);
   const BufRsrc b_rsrc = make_rsrc(BIAS ? p.bias_ext + (int64_t)h * ext_len : nullptr,
                                    BIAS ? (uint32_t)(ext_len * 4) : 0u);
 
@@ -1275,9 +1281,9 @@ __global__ void convert_q8_bf16(const uint8_t* q8, int64_t q_rs, const int64_t* 
   }
 }
 
-// bias table [H, 2R-1] -> [H, 2N+192] with entry off+N+127 = bias(clamp(off)) * -log2(e)
+// bias table [H, 2R-1] -> [H, bias_ext_len(N)] with entry off+N+127 = bias(clamp(off)) * -log2(e)
 __global__ void build_bias_ext(const float* bias, int H, int R, int N, float* ext) {
-  const int len = 2 * N + 192;
+  const int len = bias_ext_len(N);
   const int h = blockIdx.y;
   const int R1 = R - 1;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < len; i += gridDim.x * blockDim.x) {
@@ -1393,10 +1399,11 @@ hipError_t schedule(AttnParams& p, const int64_t* seq_offsets, int B, int H, int
 int sched_grid(int B, int H, int N) { return 8 * sched_cap(B, H) * ((N + 127) / 128); }
 
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
-int64_t bias_ext_bytes(int H, int N) { return align256((int64_t)H * (2 * N + 192) * 4); }
+int64_t bias_ext_bytes(int H, int N) { return align256((int64_t)H * bias_ext_len(N) * 4); }
 int64_t dbias_part_bytes(int H, int R) { return align256((int64_t)kDbiasCopies * H * (2 * R - 1) * 4); }
 int64_t sched_bytes(int B, int H) { return align256(sched_ints(B, H) * 4); }
-int64_t fwd_workspace_bytes(int /*dtype*/, int64_t /*T*/, int B, int H, int /*D*/) { return sched_bytes(B, H); }
+// Forward workspace: the block schedule.
+int64_t fwd_workspace_bytes(int B, int H) { return sched_bytes(B, H); }
 // Backward workspace: [block schedule][pre-clamped bias rows][bf16 copy of
 // e4m3 q][partial bias gradients]; byte offsets of each part.
 struct BwdWs {
@@ -1510,9 +1517,7 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
       !row_alignment_ok(dtype, v_row_stride, v))
     return HSTU_E_UNSUPPORTED;
   if (B == 0) return 0;
-  if (total_tokens < 0 || workspace == nullptr ||
-      workspace_bytes < fwd_workspace_bytes(dtype, total_tokens, B, H, D))
-    return HSTU_E_BAD_ARG;
+  if (total_tokens < 0 || workspace == nullptr || workspace_bytes < fwd_workspace_bytes(B, H)) return HSTU_E_BAD_ARG;
   AttnParams p{};
   p.q = (const uint8_t*)q;
   p.k = (const uint8_t*)k;
@@ -1631,7 +1636,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   if (parts & kBwdDkdv) {
     if (has_bias) {
       p.bias_ext = (const float*)(ws + wl.bias_ext);
-      hipLaunchKernelGGL(build_bias_ext, dim3((2 * max_seq_len + 192 + 255) / 256, H), dim3(256), 0, stream,
+      hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
                          attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
     }
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
@@ -1711,9 +1716,10 @@ extern "C" int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens
 
 extern "C" int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D,
                                                  int max_seq_len) {
-  (void)max_seq_len;
-  if (B < 0 || H <= 0 || total_tokens < 0) return -1;
-  return fwd_workspace_bytes(dtype, total_tokens, B, H, D);
+  (void)dtype;
+  (void)D;
+  if (B < 0 || H <= 0 || total_tokens < 0 || max_seq_len < 0) return -1;
+  return fwd_workspace_bytes(B, H);
 }
 extern "C" int hstu_attn_bwd(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdAll, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dkdv(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDkdv, HSTU_BWD_ARGS); }

@@ -52,12 +52,13 @@ def test_workspace_size():
     f = lib.fn("hstu_attn_bwd_workspace_bytes")
     assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 0) == sched
     assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096, 0) == sched + 1000 * 4 * 128 * 2
-    ext = a256(4 * (2 * 4096 + 192) * 4)
+    ext = a256(4 * (2 * 4096 + 256) * 4)  # pre-clamped bias rows, 2N+256 per head
     part = a256(64 * 4 * (2 * 1024 - 1) * 4)
     assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 1024) == sched + ext + part
     assert f(lib.HSTU_DTYPE_BF16, -1, B, H, 128, 4096, 0) == -1
     g = lib.fn("hstu_attn_fwd_workspace_bytes")
     assert g(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096) == sched
+    assert g(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096) == sched
     assert g(lib.HSTU_DTYPE_BF16, 1000, -1, H, 128, 4096) == -1
 
 
