@@ -1086,45 +1086,57 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   // Per-lane global offset of this wave's load instruction j (slot = wave + 4j);
   // recomputed at each issue rather than held in registers.
   auto voff_of = [&](int slot) -> uint32_t {
-    const int c = (slot < C::N_Q ? slot : slot - C::N_Q) * 64 + lane;
+    // The lane index passes through an empty asm so these few instructions
+    // are redone at each issue instead of being hoisted into registers.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int c = (slot < C::N_Q ? slot : slot - C::N_Q) * 64 + ln;
     int row = c / (C::P / 16), col = c % (C::P / 16);
     if (col >= D * 2 / 16) col -= D * 2 / 16;
     row = row < C::BMQ ? row : C::BMQ - 1;
     if (slot < C::N_Q) return row * qrs + col * 16;
     if (slot < C::N_Q + C::N_DO) return row * dors + col * 16;
-    if (FP8 && slot == C::N_Q + C::N_DO) return (uint32_t)min(lane, C::BMQ - 1) * s_step;
-    if (BIAS && slot < C::N_REAL) return (uint32_t)((slot - C::N_Q - C::N_DO - C::N_SQ) * 64 + lane) * 4;
+    if (FP8 && slot == C::N_Q + C::N_DO) return (uint32_t)min(ln, C::BMQ - 1) * s_step;
+    if (BIAS && slot < C::N_REAL) return (uint32_t)((slot - C::N_Q - C::N_DO - C::N_SQ) * 64 + ln) * 4;
     return 0u;
   };
-  auto issue = [&](int m0, uint8_t* stage) {
+  // One load instruction; the slot (which tile piece it moves) is a
+  // compile-time constant, so each wave's issue sequence is straight-line.
+  auto issue_slot = [&](auto slot_c, int m0, uint8_t* stage) {
 #if defined(__HIP_DEVICE_COMPILE__)
     typedef __attribute__((address_space(3))) void lds_t;
-    const int w = __builtin_amdgcn_readfirstlane(wave);
-#pragma unroll
-    for (int j = 0; j < C::CNT; ++j) {
-      const int slot = w + 4 * j;
-      const uint32_t vo = voff_of(slot);
-      if (slot < C::N_Q) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16, vo,
-                                                 m0 * qrs, 0, 0);
-      } else if (slot < C::N_Q + C::N_DO) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - C::N_Q) * 1024),
-                                                 16, vo, m0 * dors, 0, 0);
-      } else if (FP8 && slot == C::N_Q + C::N_DO) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4, vo, m0 * s_step, 0,
-                                                 0);
-      } else if (BIAS && slot < C::N_REAL) {
-        const int b = slot - C::N_Q - C::N_DO - C::N_SQ;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4, vo,
-                                                 (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
-      } else {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, vo, 0, 0, 0);
-      }
+    constexpr int slot = decltype(slot_c)::value;
+    const uint32_t vo = voff_of(slot);
+    if constexpr (slot < C::N_Q) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16, vo, m0 * qrs,
+                                               0, 0);
+    } else if constexpr (slot < C::N_Q + C::N_DO) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - C::N_Q) * 1024), 16,
+                                               vo, m0 * dors, 0, 0);
+    } else if constexpr (FP8 && slot == C::N_Q + C::N_DO) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4, vo, m0 * s_step, 0, 0);
+    } else if constexpr (BIAS && slot < C::N_REAL) {
+      constexpr int b = slot - C::N_Q - C::N_DO - C::N_SQ;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4, vo,
+                                               (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
+    } else {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, vo, 0, 0, 0);
     }
 #else
     (void)m0;
     (void)stage;
 #endif
+  };
+  auto issue = [&](int m0, uint8_t* stage) {
+    auto run = [&](auto wave_c) {
+      constexpr int W = decltype(wave_c)::value;
+      static_for<C::CNT>([&](auto j) { issue_slot(std::integral_constant<int, W + 4 * decltype(j)::value>{}, m0, stage); });
+    };
+    const int w = __builtin_amdgcn_readfirstlane(wave);
+    if (w == 0) run(std::integral_constant<int, 0>{});
+    else if (w == 1) run(std::integral_constant<int, 1>{});
+    else if (w == 2) run(std::integral_constant<int, 2>{});
+    else run(std::integral_constant<int, 3>{});
   };
 
   const int q_rd = C::Q_OFF + li * C::P + 16 * g;

@@ -4,6 +4,7 @@
 #define HSTU_COMMON_H_
 
 #include <hip/hip_runtime.h>
+#include <utility>
 #include <stdint.h>
 
 namespace hstu {
@@ -147,6 +148,16 @@ struct DirectTile {
 #endif
   }
 };
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N-1>{})
+template <int N, typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
+}
+
 // vmcnt(0); expcnt and lgkmcnt left at their maxima.
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
