@@ -538,9 +538,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
             float pv[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              float t = s[kt][qt][r] * cq[qt];
-              if constexpr (FP8) t *= skv[r];
-              if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + 16 * (qt - kt) - r];
+              float b = 0.f;
+              if constexpr (BIAS) b = BCONST ? bconst : bias_lds[bias_rd + 16 * (qt - kt) - r];
+              const float t = scaled_score<FP8, BIAS>(s[kt][qt][r], cq[qt], skv[r], b);
               float val = t * sig_of_t(t);
               if constexpr (FP8) val *= svv[r];
               if constexpr (MASKED) {
@@ -902,15 +902,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
               float dsv[4], dsr[4];
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
-                float t = s[h2][qt][r] * cq[qt];
-                if constexpr (FP8) t *= skv[r];
-                const int boff = 16 * (qt - kt) - r;
-                if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + boff];
-                const float sg = sig_of_t(t);
-                const float x = -kLn2 * t;
-                float dpv = dp[h2][qt][r];
-                if constexpr (FP8) dpv *= svv[r];
-                float ds = dpv * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+                float b = 0.f;
+                if constexpr (BIAS) b = BCONST ? bconst : bias_lds[bias_rd + 16 * (qt - kt) - r];
+                const float t = scaled_score<FP8, BIAS>(s[h2][qt][r], cq[qt], skv[r], b);
+                float ds = dsilu_dp(t, FP8 ? dp[h2][qt][r] * svv[r] : dp[h2][qt][r]);
                 if constexpr (MASKED) {
                   const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
                   const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
@@ -1193,13 +1188,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
           float pv[4], dsv[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float t = s[qs][kt][r] * ck[kt];
-            if constexpr (FP8) t *= sqv[r];
-            if constexpr (BIAS) t += BCONST ? bconst : bias_lds[bias_rd + 16 * (qs - kt) + r];
+            float b = 0.f;
+            if constexpr (BIAS) b = BCONST ? bconst : bias_lds[bias_rd + 16 * (qs - kt) + r];
+            const float t = scaled_score<FP8, BIAS>(s[qs][kt][r], ck[kt], sqv[r], b);
             const float sg = sig_of_t(t);
-            const float x = -kLn2 * t;
             float pval = t * sg;
-            float dval = dp[qs][kt][r] * sg * __builtin_fmaf(x, 1.f - sg, 1.f);
+            float dval = dp[qs][kt][r] * dsilu_factor(sg, pval);
             if constexpr (FP8) dval *= sqv[r];
             if constexpr (MASKED) {
               const int i = m0 + qs * 16 + 4 * g + r, j = kw0 + kt * 16 + li;

@@ -86,6 +86,29 @@ __device__ __forceinline__ float sig_of_t(float t) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
+// Exponent argument t = -x*log2(e) of a score: raw MFMA dot product s times
+// the row factor c1 (-alpha*log2(e), times one operand's e4m3 scale) and the
+// other operand's scale c2 (e4m3 only), plus the pre-scaled bias b.
+template <bool FP8, bool BIAS>
+__device__ __forceinline__ float scaled_score(float s, float c1, float c2, float b) {
+  const float a = s * c1;
+  if constexpr (FP8 && BIAS) return __builtin_fmaf(a, c2, b);
+  else if constexpr (FP8) return a * c2;
+  else if constexpr (BIAS) return a + b;
+  else return a;
+}
+
+// silu'(x) in terms of sg = sigmoid(x) and p = t * sg, where t = -x*log2(e):
+//   silu'(x) = sg + x*sg*(1 - sg) = sg + p*(ln2*sg - ln2)   (x*sg = -ln2 * p)
+__device__ __forceinline__ float dsilu_factor(float sg, float p) {
+  return __builtin_fmaf(p, __builtin_fmaf(sg, kLn2, -kLn2), sg);
+}
+// dS before the 1/N factor: dP * silu'(x), from t = -x*log2(e).
+__device__ __forceinline__ float dsilu_dp(float t, float dp) {
+  const float sg = sig_of_t(t);
+  return dp * dsilu_factor(sg, t * sg);
+}
+
 // 4 e4m3 bytes of a word -> 4 floats scaled by s, as 2 packed bf16 words.
 __device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w, float s) {
   f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
