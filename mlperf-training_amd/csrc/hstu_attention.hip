@@ -1210,13 +1210,19 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
           dsa[kt][qs * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
         }
       }
-      // ---- dV += P^T . dO, dK += dS^T . Q  (dO and Q rows read transposed)
+      // ---- dV += P^T . dO, dK += dS^T . Q  (dO and Q rows read transposed,
+      // one d-step ahead of their MFMAs)
+      auto tr_pair = [&](int off) {
+        return cat_tr(lds_tr16(buf + off + tr_rd), lds_tr16(buf + off + tr_rd + 16 * C::P));
+      };
+      u32x4 nbdo = tr_pair(C::DO_OFF), nbq = tr_pair(C::Q_OFF);
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
-        const uint8_t* dop = buf + C::DO_OFF + tr_rd + dt * 32;
-        const uint8_t* qp = buf + C::Q_OFF + tr_rd + dt * 32;
-        const u32x4 bdo = cat_tr(lds_tr16(dop), lds_tr16(dop + 16 * C::P));
-        const u32x4 bq = cat_tr(lds_tr16(qp), lds_tr16(qp + 16 * C::P));
+        const u32x4 bdo = nbdo, bq = nbq;
+        if (dt + 1 < C::DT) {
+          nbdo = tr_pair(C::DO_OFF + (dt + 1) * 32);
+          nbq = tr_pair(C::Q_OFF + (dt + 1) * 32);
+        }
         dv[0][dt] = mfma_bf16(pa[0], bdo, dv[0][dt]);
         dv[1][dt] = mfma_bf16(pa[1], bdo, dv[1][dt]);
         dk[0][dt] = mfma_bf16(dsa[0], bq, dk[0][dt]);
