@@ -128,3 +128,43 @@ def test_gemm_bf16_weight_path(hip_lib):
     torch.cuda.synchronize()
     ref = x.double() @ w.double()
     assert orc.rel_l2(ref, out.double().cpu()) <= 6e-2  # two e4m3 quantizations (~2^-4 each, averaged)
+
+
+@pytest.mark.parametrize("M", [162251, 262144])
+def test_gemm_config4_full_size(hip_lib, M):
+    """BASELINE config 4 at full size: X [M, 512] e4m3 per-row scales times
+    W [512, 2048] e4m3 per-column scales (W stored transposed, [2048, 512]),
+    bf16 out with bias and SiLU on the U slice (columns 0-511), M = T of
+    config 3 and 262 144.  The whole product runs on the GPU; the float64
+    oracle checks 1024 sampled rows (incl. the first and last) to the bf16
+    bar of test_gemm_bf16."""
+    fp8 = _fp8()
+    N, K = 2048, 512
+    a8, sa, w8t, sw = _operands(M, N, K, seed=11)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(12)) * 0.1).to(torch.bfloat16)
+    out = fp8.fp8_gemm(a8.to(DEV), sa.to(DEV), (w8t.to(DEV), sw.to(DEV)), bias=bias.to(DEV), silu_cols=(0, 512))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.tensor([0, M - 1]),
+                      torch.randint(1, M - 1, (1022,), generator=torch.Generator().manual_seed(13))])
+    ref = orc.fp8_rowcol_gemm(a8[rows], sa[rows], w8t.t(), sw, bias=bias.float(), silu_cols=(0, 512))
+    got = out[rows.to(DEV)].double().cpu()
+    err = orc.rel_l2(ref, got)
+    mx = float((got - ref).abs().max() / ref.abs().max())
+    assert err <= 4e-3 and mx <= 1e-2, f"rel L2 {err:.2e} max {mx:.2e}"
+
+
+def test_gemm_outproj_config4_full_size(hip_lib):
+    """The output projection at config-4 size: [T=162 251, 1536] e4m3 times
+    [1536, 512] e4m3 plus a bf16 residual, checked on 1024 sampled rows."""
+    fp8 = _fp8()
+    M, N, K = 162251, 512, 1536
+    a8, sa, w8t, sw = _operands(M, N, K, seed=14)
+    res = torch.randn(M, N, generator=torch.Generator().manual_seed(15)).to(torch.bfloat16)
+    out = fp8.scaled_addmm_fp8_preq(a8.to(DEV), sa.to(DEV), (w8t.to(DEV), sw.to(DEV)), res.to(DEV))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.tensor([0, M - 1]),
+                      torch.randint(1, M - 1, (1022,), generator=torch.Generator().manual_seed(16))])
+    ref = orc.fp8_rowcol_gemm(a8[rows], sa[rows], w8t.t(), sw, residual=res[rows].float())
+    got = out[rows.to(DEV)].double().cpu()
+    assert orc.rel_l2(ref, got) <= 4e-3
+    assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2

@@ -1,0 +1,149 @@
+"""GPU parity at the BASELINE configurations' full sizes.
+
+Where the CPU oracle finishes in seconds it runs on the whole batch (configs
+1 and 2).  At config 3 (B=128, N=4096) the padded oracle would need tens of
+GB, so the oracle runs per sequence on a sample that includes the longest
+sequence, and size-independent properties cover the whole batch:
+
+* jagged independence: a sub-batch of the sampled sequences gives bitwise
+  the same out / dq / dk / dv rows as the full batch;
+* linearity of the bias gradient: dbias(full) = dbias(first half) +
+  dbias(second half) up to fp32 summation order.
+
+Tolerances are the ones stated in ``test_attention_gpu.py``: bf16
+``assert_close(rtol=1e-2, atol=1e-2)``; e4m3 inputs relative L2 <= 1.5e-2
+and max |err| <= 3e-2 * max |ref| against fp32/fp64 on the dequantized
+inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hstu_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _ops():
+    import hstu_amd
+
+    return hstu_amd
+
+
+def _fp8_close(ref, got, what):
+    got = got.float().cpu().double()
+    ref = ref.double()
+    err = orc.rel_l2(ref, got)
+    mx = float((got - ref).abs().max() / ref.abs().max())
+    assert err <= 1.5e-2 and mx <= 3e-2, f"{what}: rel L2 {err:.3e}, max {mx:.3e}, snr {orc.snr_db(ref, got):.1f} dB"
+
+
+def test_config1_shapes(hip_lib):
+    """BASELINE config 1 shapes (B=8, lengths U[16,256], H=2, D=64, N=max L=221)
+    through the HIP path in bf16, fwd and bwd, against the fp64 oracle."""
+    ops = _ops()
+    lengths = orc.lengths_for_config(1)
+    assert list(lengths) == [221, 169, 139, 81, 90, 25, 34, 19]
+    H, D, N = 2, 64, int(max(lengths))
+    q, k, v = orc.make_qkv(lengths, H, D, 0.5, seed=0)
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    offs = orc.offsets_from_lengths(lengths)
+    alpha = 1.0 / D ** 0.5
+    out = ops.triton_hstu_mha(N, alpha, q.to(DEV), k.to(DEV), v.to(DEV), offs.to(DEV))
+    ref = orc.hstu_mha_dense(N, alpha, q.double(), k.double(), v.double(), offs, dtype=torch.float64)
+    torch.testing.assert_close(out.float().cpu(), ref.float(), rtol=1e-2, atol=1e-2)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    dq, dk, dv = (torch.empty(q.shape, dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    ops.triton_hstu_attention_bwd(dout.to(DEV), q.to(DEV), k.to(DEV), v.to(DEV), dq, dk, dv, offs.to(DEV), None,
+                                  N, alpha, 0, 0, None, False, 0)
+    rq, rk, rv, _ = orc.hstu_mha_bwd(N, alpha, q.float(), k.float(), v.float(), offs, dout.float())
+    for name, got, r in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        torch.testing.assert_close(got.float().cpu(), r.float(), rtol=1e-2, atol=1e-2, msg=name)
+
+
+def test_config2_full_forward_with_bias(hip_lib):
+    """BASELINE config 2 in full: B=64, lengths U[128,1024] (T=37 429), N=1024,
+    H=4, D=128, bf16 q/k/v ~ N(0,1)*0.3, relative bias [4, 2047] ~ N(0, 0.02)."""
+    ops = _ops()
+    lengths = orc.lengths_for_config(2)
+    H, D, N = 4, 128, 1024
+    q, k, v = orc.make_qkv(lengths, H, D, 0.3, seed=0)
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    assert q.shape[0] == 37429
+    offs = orc.offsets_from_lengths(lengths)
+    bias = orc.make_bias(H, 1024)
+    alpha = 1.0 / D ** 0.5
+    out = ops.triton_hstu_attention_fwd(N, alpha, q.to(DEV), k.to(DEV), v.to(DEV), offs.to(DEV), None, 0, 0,
+                                        None, False, 0, attn_bias=bias.to(DEV))
+    ref = orc.hstu_mha_dense(N, alpha, q.float(), k.float(), v.float(), offs, attn_bias=bias, dtype=torch.float32)
+    torch.testing.assert_close(out.float().cpu(), ref, rtol=1e-2, atol=1e-2)
+    assert orc.rel_l2(ref.double(), out.float().cpu().double()) <= 1e-2
+
+
+def _cfg3_inputs():
+    lengths = orc.lengths_for_config(3)
+    H, D = 4, 128
+    q, k, v = orc.make_qkv(lengths, H, D, 1.0, seed=0)
+    (q8, sq), (k8, sk), (v8, sv) = (orc.quantize_e4m3_rows(x, dim=-1) for x in (q, k, v))
+    bias = orc.make_bias(H, 1024)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16)
+    return lengths, (q8, k8, v8), (sq, sk, sv), bias, dout
+
+
+def _run_fp8(ops, lengths, q8, k8, v8, sq, sk, sv, bias, dout, N, alpha):
+    offs = orc.offsets_from_lengths(lengths).to(DEV)
+    dev = [t.to(DEV) for t in (q8, k8, v8, sq, sk, sv)]
+    b = bias.to(DEV)
+    out = ops.triton_hstu_attention_fwd(N, alpha, dev[0], dev[1], dev[2], offs, None, 0, 0, None, False, 0,
+                                        dev[3], dev[4], dev[5], attn_bias=b)
+    dq, dk, dv = (torch.empty(q8.shape, dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    dbias = torch.empty_like(b)
+    ops.triton_hstu_attention_bwd(dout.to(DEV), dev[0], dev[1], dev[2], dq, dk, dv, offs, None, N, alpha, 0, 0,
+                                  None, False, 0, dev[3], dev[4], dev[5], attn_bias=b, dbias=dbias)
+    torch.cuda.synchronize()
+    return out.cpu(), dq.cpu(), dk.cpu(), dv.cpu(), dbias.cpu()
+
+
+def test_config3_full_fp8_fwd_bwd(hip_lib):
+    """BASELINE config 3 in full (B=128 Zipf lengths, T=162 251, N=4096, H=4,
+    D=128, e4m3 per-(token, head) scales, bias): the oracle on a sample of
+    sequences incl. the longest, bitwise jagged independence, and dbias
+    linearity over the two halves of the batch."""
+    ops = _ops()
+    lengths, (q8, k8, v8), (sq, sk, sv), bias, dout = _cfg3_inputs()
+    assert int(np.sum(lengths)) == 162251
+    N, alpha = 4096, 1.0 / 128 ** 0.5
+    offs = orc.offsets_from_lengths(lengths)
+    full = _run_fp8(ops, lengths, q8, k8, v8, sq, sk, sv, bias, dout, N, alpha)
+
+    order = np.argsort(lengths)
+    sample = sorted({int(order[-1]), int(order[len(order) // 2]), int(order[0]), int(order[int(len(order) * 0.9)])})
+    assert int(max(lengths[sample])) == int(max(lengths)) == 4096
+    rows = torch.cat([torch.arange(int(offs[b]), int(offs[b + 1])) for b in sample])
+    sub_len = lengths[sample]
+    sub = _run_fp8(ops, sub_len, q8[rows], k8[rows], v8[rows], sq[rows], sk[rows], sv[rows], bias, dout[rows],
+                   N, alpha)
+    for name, a, b in zip(("out", "dq", "dk", "dv"), full[:4], sub[:4]):
+        assert torch.equal(a[rows], b), f"{name}: sub-batch rows differ from the full batch"
+
+    # oracle on the sampled sequences (dequantized inputs, fp32 autograd)
+    deq = [orc.dequantize(x8[rows], s[rows]) for x8, s in ((q8, sq), (k8, sk), (v8, sv))]
+    sub_offs = orc.offsets_from_lengths(sub_len)
+    ref_out = orc.hstu_mha_dense(N, alpha, *deq, sub_offs, attn_bias=bias, dtype=torch.float32)
+    rq, rk, rv, rb = orc.hstu_mha_bwd(N, alpha, *deq, sub_offs, dout[rows].float(), attn_bias=bias,
+                                      dtype=torch.float32)
+    for name, ref, got in (("out", ref_out, sub[0]), ("dq", rq, sub[1]), ("dk", rk, sub[2]), ("dv", rv, sub[3])):
+        _fp8_close(ref, got, f"config 3 sample {name}")
+    _fp8_close(rb, sub[4], "config 3 sample dbias")
+
+    # dbias linearity over the two halves of the batch
+    half = len(lengths) // 2
+    cut = int(offs[half])
+    first = _run_fp8(ops, lengths[:half], q8[:cut], k8[:cut], v8[:cut], sq[:cut], sk[:cut], sv[:cut], bias,
+                     dout[:cut], N, alpha)
+    second = _run_fp8(ops, lengths[half:], q8[cut:], k8[cut:], v8[cut:], sq[cut:], sk[cut:], sv[cut:], bias,
+                      dout[cut:], N, alpha)
+    torch.testing.assert_close(full[4], first[4] + second[4], rtol=1e-4, atol=1e-6 * float(full[4].abs().max()))
