@@ -1001,14 +1001,19 @@ struct DkvCfg {
   static constexpr int P = BwdPitch<D>::P;
   using DTile = DirectTile<BMQ, D * 2, P>;
   static constexpr int TILE = DTile::BYTES;
+  // e4m3 inputs: the raw q rows as well, A operand of the e4m3 S MFMA
+  static constexpr int P8 = D + 32;
+  using Q8Tile = DirectTile<BMQ, D, P8>;
   static constexpr int Q_OFF = 0;
-  static constexpr int DO_OFF = Q_OFF + TILE;
+  static constexpr int Q8_OFF = Q_OFF + TILE;
+  static constexpr int DO_OFF = Q8_OFF + (FP8 ? Q8Tile::BYTES : 0);
   static constexpr int SQ_OFF = DO_OFF + TILE;   // 64 floats (one 4-byte load instruction)
   static constexpr int BIAS_OFF = SQ_OFF + 256;  // 192 floats (three)
   static constexpr int DUMMY_OFF = BIAS_OFF + 768;
   static constexpr int STAGE = DUMMY_OFF + 1024;
-  static constexpr int N_Q = DTile::NINSTR, N_DO = DTile::NINSTR, N_SQ = FP8 ? 1 : 0, N_BIAS = BIAS ? 3 : 0;
-  static constexpr int N_REAL = N_Q + N_DO + N_SQ + N_BIAS;
+  static constexpr int N_Q = DTile::NINSTR, N_Q8 = FP8 ? Q8Tile::NINSTR : 0, N_DO = DTile::NINSTR;
+  static constexpr int N_SQ = FP8 ? 1 : 0, N_BIAS = BIAS ? 3 : 0;
+  static constexpr int N_REAL = N_Q + N_Q8 + N_DO + N_SQ + N_BIAS;
   static constexpr int CNT = (N_REAL + 3) / 4;  // load instructions per wave per tile
   static constexpr int LDS = NSTAGE * STAGE;
 };
@@ -1039,6 +1044,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   const BufRsrc qrsrc = make_rsrc(q16, (uint32_t)(L > 0 ? (L - 1) * qrs + D * 2 : 0));
   const BufRsrc dorsrc = make_rsrc(p.dout + (sc.start * p.do_rs + (int64_t)h * D) * 2,
                                    (uint32_t)(L > 0 ? (L - 1) * dors + D * 2 : 0));
+  const uint32_t q8rs = (uint32_t)p.q_rs;  // e4m3 q rows, bytes
+  const BufRsrc q8rsrc = make_rsrc(FP8 ? p.q + sc.start * p.q_rs + (int64_t)h * D : nullptr,
+                                   FP8 ? (uint32_t)(L > 0 ? (L - 1) * q8rs + D : 0) : 0u);
   const uint32_t s_step = FP8 ? (uint32_t)(p.s_rs * 4) : 0u;
   const BufRsrc sq_rsrc = make_rsrc(FP8 ? p.q_scale + sc.start * p.s_rs + h * p.s_hs : nullptr,
                                     FP8 ? (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4) : 0u);
@@ -1049,7 +1057,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
 
   // K and V fragments (B operands): lane holds key kw0+16kt+li.  V is
   // dequantized (scale applied) once here; K's scale goes into ck.
+  // e4m3 K stays raw (B operand of the e4m3 MFMA: lane group g holds the
+  // 16-byte k-chunks g and g+4 of its key row, as the Q8 tile reads below).
   u32x4 kf[2][C::KS], vf[2][C::KS];
+  i32x8 kf8[2];
   float ck[2];
   {
     const uint8_t* kb = p.k + (sc.start * p.k_rs + (int64_t)h * D) * ES;
@@ -1063,8 +1074,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
       if constexpr (FP8) {
         sv = ok ? p.v_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 0.f;
         ck[kt] *= ok ? p.k_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 0.f;
+        u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+        if (ok) {
+          lo = *(const u32x4*)(kb + (int64_t)row * p.k_rs + 16 * g);
+          hi = *(const u32x4*)(kb + (int64_t)row * p.k_rs + 64 + 16 * g);
+        }
+        kf8[kt] = cat8(lo, hi);
+      } else {
+        load_row_frag<D, false>(kf[kt], kb, p.k_rs * 2, row, ok, g, 1.f);
       }
-      load_row_frag<D, FP8>(kf[kt], kb, p.k_rs * ES, row, ok, g, 1.f);
       load_row_frag<D, FP8>(vf[kt], vb, p.v_rs * ES, row, ok, g, sv);
     }
   }
@@ -1078,44 +1096,54 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   const int m_begin = GENERIC ? 0 : n0;
   const int ntiles = (L - m_begin + C::BMQ - 1) / C::BMQ;
 
-  // Per-lane global offset of this wave's load instruction j (slot = wave + 4j);
-  // recomputed at each issue rather than held in registers.
-  auto voff_of = [&](int slot) -> uint32_t {
+  // Per-lane global offset of load instruction i of a tile of padded rows
+  // (cpr 16-byte slots per LDS row, dcpr of them data); recomputed at each
+  // issue rather than held in registers.
+  auto tile_voff = [&](int i, int cpr, int dcpr, uint32_t rs) -> uint32_t {
     // The lane index passes through an empty asm so these few instructions
     // are redone at each issue instead of being hoisted into registers.
     int ln = lane;
     asm volatile("" : "+v"(ln));
-    const int c = (slot < C::N_Q ? slot : slot - C::N_Q) * 64 + ln;
-    int row = c / (C::P / 16), col = c % (C::P / 16);
-    if (col >= D * 2 / 16) col -= D * 2 / 16;
+    const int c = i * 64 + ln;
+    int row = c / cpr, col = c % cpr;
+    if (col >= dcpr) col -= dcpr;
     row = row < C::BMQ ? row : C::BMQ - 1;
-    if (slot < C::N_Q) return row * qrs + col * 16;
-    if (slot < C::N_Q + C::N_DO) return row * dors + col * 16;
-    if (FP8 && slot == C::N_Q + C::N_DO) return (uint32_t)min(ln, C::BMQ - 1) * s_step;
-    if (BIAS && slot < C::N_REAL) return (uint32_t)((slot - C::N_Q - C::N_DO - C::N_SQ) * 64 + ln) * 4;
-    return 0u;
+    return row * rs + col * 16;
+  };
+  auto lane_of = [&]() -> uint32_t {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    return (uint32_t)ln;
   };
   // One load instruction; the slot (which tile piece it moves) is a
   // compile-time constant, so each wave's issue sequence is straight-line.
+  // Slots: [bf16 Q][e4m3 Q][dO][q scales][bias band][dummies].
   auto issue_slot = [&](auto slot_c, int m0, uint8_t* stage) {
 #if defined(__HIP_DEVICE_COMPILE__)
     typedef __attribute__((address_space(3))) void lds_t;
     constexpr int slot = decltype(slot_c)::value;
-    const uint32_t vo = voff_of(slot);
-    if constexpr (slot < C::N_Q) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16, vo, m0 * qrs,
-                                               0, 0);
-    } else if constexpr (slot < C::N_Q + C::N_DO) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - C::N_Q) * 1024), 16,
-                                               vo, m0 * dors, 0, 0);
-    } else if constexpr (FP8 && slot == C::N_Q + C::N_DO) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4, vo, m0 * s_step, 0, 0);
+    constexpr int S_Q8 = C::N_Q, S_DO = S_Q8 + C::N_Q8, S_SQ = S_DO + C::N_DO, S_BIAS = S_SQ + C::N_SQ;
+    if constexpr (slot < S_Q8) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16,
+                                               tile_voff(slot, C::P / 16, D * 2 / 16, qrs), m0 * qrs, 0, 0);
+    } else if constexpr (slot < S_DO) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q8rsrc, (lds_t*)(stage + C::Q8_OFF + (slot - S_Q8) * 1024), 16,
+                                               tile_voff(slot - S_Q8, C::P8 / 16, D / 16, q8rs), m0 * q8rs, 0, 0);
+    } else if constexpr (slot < S_SQ) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - S_DO) * 1024), 16,
+                                               tile_voff(slot - S_DO, C::P / 16, D * 2 / 16, dors), m0 * dors, 0,
+                                               0);
+    } else if constexpr (FP8 && slot == S_SQ) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4,
+                                               (uint32_t)min((int)lane_of(), C::BMQ - 1) * s_step, m0 * s_step, 0,
+                                               0);
     } else if constexpr (BIAS && slot < C::N_REAL) {
-      constexpr int b = slot - C::N_Q - C::N_DO - C::N_SQ;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4, vo,
-                                               (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
+      constexpr int b = slot - S_BIAS;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4,
+                                               (b * 64 + lane_of()) * 4, (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
     } else {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, vo, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, lane_of() * 16, 0, 0,
+                                               0);
     }
 #else
     (void)m0;
@@ -1135,6 +1163,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   };
 
   const int q_rd = C::Q_OFF + li * C::P + 16 * g;
+  const int q8_rd = C::Q8_OFF + li * C::P8 + 16 * g;
   const int do_rd = C::DO_OFF + li * C::P + 16 * g;
   const int tr_rd = (4 * g + (li >> 2)) * C::P + (li & 3) * 8;  // tr16, relative to a tile
   // bias index of element (qs, kt, r) = bias_rd + 16*(qs-kt) + r
@@ -1166,11 +1195,20 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
 #pragma unroll
       for (int qs = 0; qs < C::QS; ++qs) {
         s[qs][0] = s[qs][1] = dp[qs][0] = dp[qs][1] = zero4();
+        if constexpr (FP8) {
+          // e4m3 q.k products are exact in the fp32 accumulator, as in the bf16 form
+          const uint8_t* a8 = buf + q8_rd + qs * 16 * C::P8;
+          const i32x8 a = cat8(lds_ld128(a8), lds_ld128(a8 + 64));
+          s[qs][0] = mfma_fp8(a, kf8[0], s[qs][0]);
+          s[qs][1] = mfma_fp8(a, kf8[1], s[qs][1]);
+        }
 #pragma unroll
         for (int st = 0; st < C::KS; ++st) {
-          const u32x4 a = lds_ld128(buf + q_rd + qs * 16 * C::P + st * 64);
-          s[qs][0] = mfma_bf16(a, kf[0][st], s[qs][0]);
-          s[qs][1] = mfma_bf16(a, kf[1][st], s[qs][1]);
+          if constexpr (!FP8) {
+            const u32x4 a = lds_ld128(buf + q_rd + qs * 16 * C::P + st * 64);
+            s[qs][0] = mfma_bf16(a, kf[0][st], s[qs][0]);
+            s[qs][1] = mfma_bf16(a, kf[1][st], s[qs][1]);
+          }
           const u32x4 b = lds_ld128(buf + do_rd + qs * 16 * C::P + st * 64);
           dp[qs][0] = mfma_bf16(b, vf[0][st], dp[qs][0]);
           dp[qs][1] = mfma_bf16(b, vf[1][st], dp[qs][1]);
