@@ -96,6 +96,24 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = zero4();
 
+  // Epilogue operands, loaded now so their latency hides under the k-loop:
+  // lane holds C[m = m0+wm+16ms+li][n = n0+wn+16ns+4g .. +3].
+  float sa[4];
+  f32x4 sw[4];
+  u32x2 bias[4];
+#pragma unroll
+  for (int ms = 0; ms < 4; ++ms) {
+    const int m = min(m0 + wm + 16 * ms + li, p.M - 1);
+    sa[ms] = p.a_mode ? p.a_scale[m] : p.a_scale[0];
+  }
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) {
+    const int n = n0 + wn + 16 * ns + 4 * g;
+    if (p.w_mode) sw[ns] = *(const f32x4*)(p.w_scale + n);
+    else sw[ns] = f32x4{p.w_scale[0], p.w_scale[0], p.w_scale[0], p.w_scale[0]};
+    bias[ns] = p.bias ? *(const u32x2*)(p.bias + n) : u32x2{0u, 0u};
+  }
+
   wt.load(wrsrc, 0, smem);
   at.load(arsrc, 0, smem + kTileBytes);
   wait_vm();
@@ -134,18 +152,14 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
   for (int ms = 0; ms < 4; ++ms) {
     const int m = m0 + wm + 16 * ms + li;
     if (m >= p.M) continue;
-    const float sa = p.a_mode ? p.a_scale[m] : p.a_scale[0];
 #pragma unroll
     for (int ns = 0; ns < 4; ++ns) {
       const int n = n0 + wn + 16 * ns + 4 * g;
-      f32x4 sw;
-      if (p.w_mode) sw = *(const f32x4*)(p.w_scale + n);
-      else sw = f32x4{p.w_scale[0], p.w_scale[0], p.w_scale[0], p.w_scale[0]};
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[ns][ms][r] * (sa * sw[r]);
+      for (int r = 0; r < 4; ++r) v[r] = acc[ns][ms][r] * (sa[ms] * sw[ns][r]);
       if (p.bias) {
-        const u32x2 b = *(const u32x2*)(p.bias + n);
+        const u32x2 b = bias[ns];
         v[0] += bf16_to_f32(b[0] & 0xffff);
         v[1] += bf16_to_f32(b[0] >> 16);
         v[2] += bf16_to_f32(b[1] & 0xffff);
