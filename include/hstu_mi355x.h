@@ -180,6 +180,69 @@ int hstu_quantize_e4m3_rows(const void* x, int64_t ldx, int rows, int cols, int 
                             const float* scale_in, void* out, int64_t ldo, float* scale_out,
                             hipStream_t stream);
 
+/*
+ * LayerNorm * U * dropout of the output block, and the weighted LayerNorm.
+ * Rows of x, u: bf16 [rows, D] with row strides (elements); D = 256 or 512.
+ * weight, bias: fp32 [D].  mean, rstd: fp32 [rows] (written by the forward).
+ * mul_u_act: 0 none (ln * u), 1 silu (ln * silu(u)), 2 sigmoid.
+ * u == NULL: plain weighted LayerNorm, y = ln (concat_u, mul_u_act, silu_u
+ * ignored).
+ * Output columns, in order: [u' if concat_u][x if concat_x][ln * m(u)], each
+ * D wide; u' = silu(u) when silu_u.  Dropout (training && ratio > 0) zeroes or
+ * scales each element by fp32(1 / fp32(1 - ratio)) with an int8 keep mask
+ * [rows, D] (row stride ldm): bit 0 = y, then x (if concat_x), then u (if
+ * concat_u).  The mask is Philox4x32-10 (key = seed's two 32-bit words) at
+ * counter p * nmasks * BLOCK_D + j * BLOCK_D + col for mask j of row group p
+ * (BLOCK_D = next power of two of D); mask16 = 0: groups of 4 rows, word i
+ * decides row i, kept iff (x ^ (x >> 31)) > keep_above(ratio); mask16 = 1:
+ * groups of 8 rows, word i's low / high half decides row i / i + 4, kept iff
+ * half >= round(ratio * 65536).
+ * Replaces: _create_dropout_mask, ops/triton/triton_hstu_linear.py:2547-2600
+ *           (_generate_random_mask :331-375, _generate_random_mask16 :428-470).
+ */
+int hstu_dropout_mask(int rows, int D, int num_masks, int mask16, float dropout_ratio, uint64_t seed,
+                      void* mask, int64_t ldm, hipStream_t stream);
+
+/*
+ * Forward.  y: bf16 or e4m3 (out_dtype) [rows, ncols * D] with row stride
+ * ldy; e4m3 stores e4m3(clamp(value * inv_scale, +-448)).  With dropout the
+ * keep mask is generated (as by hstu_dropout_mask) and written to `mask`.
+ * Replaces: triton_layer_norm_mul_dropout_fwd, triton_hstu_linear.py:3034-3146
+ *           (kernels _ln_mul_dropout_fwd :1429-1563, _ln_mul_dropout_fwd_rng
+ *           :529-700); triton_weighted_layer_norm_fwd,
+ *           ops/triton/triton_layer_norm.py:1668-1740 (u == NULL).
+ */
+int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_t ldu,
+                    const float* weight, const float* bias, float eps, int rows, int D,
+                    int mul_u_act, int silu_u, int concat_u, int concat_x,
+                    int training, float dropout_ratio, uint64_t seed, int mask16,
+                    void* mask, int64_t ldm,
+                    void* y, int64_t ldy, int out_dtype, float inv_scale,
+                    float* mean, float* rstd, hipStream_t stream);
+
+/* Workspace of hstu_ln_mul_bwd (per-block dweight / dbias partials). */
+int64_t hstu_ln_mul_bwd_workspace_bytes(int rows, int D);
+
+/*
+ * Backward.  dy: bf16 [rows, ncols * D] (the gradient of y, in y's column
+ * order); mask as written by the forward (NULL: no dropout).  Writes dx, du
+ * (bf16, du only with u), dweight and dbias (fp32 [D], deterministic: fixed
+ * summation order) and, when y != NULL, the bf16 forward output recomputed
+ * (for the output projection's weight gradient).
+ * Replaces: triton_layer_norm_mul_dropout_bwd, triton_hstu_linear.py:3689-3747
+ *           (kernel _ln_mul_dropout_bwd_dx_du_rng :1566-1760, finalize
+ *           _lnmd_bwd_finalize :3402-3431); triton_weighted_layer_norm_bwd,
+ *           ops/triton/triton_layer_norm.py:3574-3640 (u == NULL, no residual).
+ */
+int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
+                    const void* u, int64_t ldu, const float* weight, const float* bias,
+                    const float* mean, const float* rstd, int rows, int D,
+                    int mul_u_act, int silu_u, int concat_u, int concat_x,
+                    float dropout_ratio, const void* mask, int64_t ldm,
+                    void* dx, int64_t lddx, void* du, int64_t lddu, void* y, int64_t ldy,
+                    float* dweight, float* dbias, void* workspace, int64_t workspace_bytes,
+                    hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,6 @@
 """MI355X-native (gfx950) HSTU hot path: jagged causal SiLU attention (bf16 and
-FP8 e4m3) and the FP8 projections around it, behind the reference's op
-signatures.  Kernels live in ``libhstu_mi355x.so`` (C ABI, include/hstu_mi355x.h)."""
+FP8 e4m3), the FP8 projections around it and the output block's
+LayerNorm * U * dropout, behind the reference's op signatures.  Kernels live in ``libhstu_mi355x.so`` (C ABI, include/hstu_mi355x.h)."""
 
 from ._lib import HstuKernelError, HstuUnavailableError, load_library  # noqa: F401
 from .hstu_attention import (  # noqa: F401
@@ -12,4 +12,16 @@ from .hstu_attention import (  # noqa: F401
     try_hstu_attention_bwd,
     try_hstu_attention_fwd,
     unsupported_shape_reason,
+)
+from .hstu_linear import (  # noqa: F401
+    HSTUComputeOutputFunction,
+    LayerNormMulDropoutFunction,
+    create_dropout_mask,
+    hstu_compute_output,
+    triton_hstu_compute_output,
+    triton_layer_norm_mul_dropout_bwd,
+    triton_layer_norm_mul_dropout_fwd,
+    triton_norm_mul_dropout,
+    triton_weighted_layer_norm_bwd,
+    triton_weighted_layer_norm_fwd,
 )

@@ -34,6 +34,10 @@ EXPORTED_SYMBOLS = (
     "hstu_attn_bwd_dq",
     "hstu_fp8_gemm_rowcol",
     "hstu_quantize_e4m3_rows",
+    "hstu_dropout_mask",
+    "hstu_ln_mul_fwd",
+    "hstu_ln_mul_bwd_workspace_bytes",
+    "hstu_ln_mul_bwd",
 )
 
 
@@ -52,6 +56,7 @@ _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
+_u64 = ctypes.c_uint64
 
 _SIGNATURES = {
     "hstu_version": (ctypes.c_char_p, []),
@@ -77,6 +82,18 @@ _SIGNATURES = {
     "hstu_quantize_e4m3_rows": (
         _i32,
         [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp],
+    ),
+    "hstu_dropout_mask": (_i32, [_i32, _i32, _i32, _i32, _f32, _u64, _vp, _i64, _vp]),
+    "hstu_ln_mul_fwd": (
+        _i32,
+        [_vp, _i64, _vp, _i64, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _u64, _i32,
+         _vp, _i64, _vp, _i64, _i32, _f32, _vp, _vp, _vp],
+    ),
+    "hstu_ln_mul_bwd_workspace_bytes": (_i64, [_i32, _i32]),
+    "hstu_ln_mul_bwd": (
+        _i32,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+         _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
     ),
 }
 

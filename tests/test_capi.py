@@ -101,3 +101,46 @@ def _load_fresh(lib, path):
         return lib.load_library(path)
     finally:
         lib._lib = saved
+
+
+def test_ln_mul_entry_points_reject_before_launch():
+    import hstu_amd._lib as lib
+
+    ws = lib.fn("hstu_ln_mul_bwd_workspace_bytes")
+    assert ws(162251, 512) == 256 * 2 * 512 * 4
+    assert ws(10, 384) == -1 and ws(-1, 512) == -1
+    fwd = lib.fn("hstu_ln_mul_fwd")
+    X, W = 4096, 8192  # fake device addresses: none of these calls may launch
+
+    def f(**kw):
+        a = dict(x=X, ldx=512, u=X, ldu=512, w=W, b=W, eps=1e-6, rows=64, D=512, act=1, silu_u=1, cu=1, cx=1,
+                 training=0, ratio=0.0, seed=0, mask16=0, mask=None, ldm=0, y=X, ldy=1536, odt=0, inv=1.0,
+                 mean=W, rstd=W, stream=None)
+        a.update(kw)
+        return fwd(*a.values())
+
+    assert f(D=384, ldx=384, ldu=384, ldy=3 * 384) == lib.HSTU_E_UNSUPPORTED
+    assert f(ldy=1024) == lib.HSTU_E_BAD_ARG  # three 512-wide blocks do not fit
+    assert f(act=3) == lib.HSTU_E_BAD_ARG
+    assert f(odt=5) == lib.HSTU_E_BAD_ARG
+    assert f(training=1, ratio=0.3) == lib.HSTU_E_BAD_ARG  # dropout without a mask buffer
+    assert f(training=1, ratio=1.5, mask=X, ldm=512) == lib.HSTU_E_BAD_ARG
+    assert f(x=X + 2) == lib.HSTU_E_UNSUPPORTED  # rows not 16-byte aligned
+    assert f(rows=-1) == lib.HSTU_E_BAD_ARG
+    mask = lib.fn("hstu_dropout_mask")
+    assert mask(64, 512, 4, 0, 0.3, 1, X, 512, None) == lib.HSTU_E_BAD_ARG
+    assert mask(64, 320, 1, 0, 0.3, 1, X, 320, None) == lib.HSTU_E_UNSUPPORTED
+    bwd = lib.fn("hstu_ln_mul_bwd")
+
+    def g(**kw):
+        a = dict(dy=X, lddy=1536, x=X, ldx=512, u=X, ldu=512, w=W, b=W, mean=W, rstd=W, rows=64, D=512, act=1,
+                 silu_u=1, cu=1, cx=1, ratio=0.0, mask=None, ldm=0, dx=X, lddx=512, du=X, lddu=512, y=None, ldy=0,
+                 dw=W, db=W, ws=W, wsb=ws(64, 512), stream=None)
+        a.update(kw)
+        return bwd(*a.values())
+
+    assert g(wsb=100) == lib.HSTU_E_BAD_ARG
+    assert g(du=None) == lib.HSTU_E_BAD_ARG
+    assert g(lddy=1024) == lib.HSTU_E_BAD_ARG
+    assert g(y=X, ldy=512) == lib.HSTU_E_BAD_ARG
+    assert g(D=128, ldx=128, ldu=128, lddx=128, lddu=128, lddy=384) == lib.HSTU_E_UNSUPPORTED

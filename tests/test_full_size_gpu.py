@@ -147,3 +147,57 @@ def test_config3_full_fp8_fwd_bwd(hip_lib):
     second = _run_fp8(ops, lengths[half:], q8[cut:], k8[cut:], v8[cut:], sq[cut:], sk[cut:], sv[cut:], bias,
                       dout[cut:], N, alpha)
     torch.testing.assert_close(full[4], first[4] + second[4], rtol=1e-4, atol=1e-6 * float(full[4].abs().max()))
+
+
+def test_output_block_config3_tokens(hip_lib, monkeypatch):
+    """The output block at config 3's token count (T = 162 251, D = 4*128 =
+    512) with the production flags (silu, concat u and x, dropout 0.3 with the
+    16-bit mask, e4m3 output): the fused forward's mask equals the standalone
+    mask kernel's bitwise and the oracle's on sampled rows (incl. the ragged
+    last group); sampled rows of y, dx, du against the oracle; per-bit keep
+    rates within binomial bounds; dweight / dbias linear over two halves."""
+    from oracle import hstu_ln_oracle as L
+
+    ops = _ops()
+    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1")
+    T, D, p, eps, seed, inv = 162251, 512, 0.3, 1e-6, 2 ** 61 + 12345, 1.0 / 0.05
+    assert int(np.sum(orc.lengths_for_config(3))) == T
+    g = torch.Generator(device=DEV).manual_seed(0)
+    attn = (torch.randn(T, D, device=DEV, generator=g) * 1.5 + 0.3).to(torch.bfloat16)
+    u = torch.randn(T, D, device=DEV, generator=g).to(torch.bfloat16)
+    w = 1.0 + 0.2 * torch.randn(D, device=DEV, generator=g)
+    b = 0.1 * torch.randn(D, device=DEV, generator=g)
+    y8, mean, rstd, BD, nw, s, mask = ops.triton_layer_norm_mul_dropout_fwd(
+        attn, u, w, b, eps, p, True, True, True, True, "silu", seed, output_fp8=True, inv_scale=inv)
+    assert torch.equal(mask, ops.create_dropout_mask(T, D, True, True, p, seed, attn.device))
+    for j in range(3):
+        rate = float(((mask.to(torch.int32) >> j) & 1).float().mean())
+        assert abs(rate - (1 - 19661 / 65536)) < 5 * (0.21 / (T * D)) ** 0.5, (j, rate)
+
+    rng = np.random.default_rng(1)
+    rows = np.unique(np.concatenate([np.arange(8), np.arange(T - 11, T), rng.integers(0, T, 1500)]))
+    ref_mask = L.dropout_mask_rows(rows, D, 3, p, seed, True)
+    assert np.array_equal(mask[torch.from_numpy(rows).to(DEV)].cpu().numpy(), ref_mask)
+    ri = torch.from_numpy(rows)
+    xs, us, ws, bs = attn.cpu()[ri].double(), u.cpu()[ri].double(), w.cpu().double(), b.cpu().double()
+    kw = dict(dropout_ratio=p, mask=ref_mask, silu_u=True, concat_u=True, concat_x=True,
+              mul_u_activation_type="silu")
+    ry, _, _ = L.ln_mul_dropout_fwd(xs, us, ws, bs, eps, **kw)
+    r = (ry * inv).clamp(-448, 448)
+    got = y8.cpu()[ri].float().double()
+    assert bool(((got - r).abs() <= r.abs() / 16 * (1 + 1e-3) + 2.0 ** -10).all())
+
+    dy = torch.randn(T, 3 * D, device=DEV, generator=g).to(torch.bfloat16)
+    dx, du, dw, db, _ = ops.triton_layer_norm_mul_dropout_bwd(
+        dy, attn, u, w, b, mean, rstd, BD, nw, eps, True, p, s, True, True, True, "silu", random_mask=mask)
+    rdx, rdu, _, _ = L.ln_mul_dropout_bwd(dy.cpu()[ri].double(), xs, us, ws, bs, eps, **kw)
+    for name, a, ref in (("dx", dx, rdx), ("du", du, rdu)):
+        torch.testing.assert_close(a.cpu()[ri].float(), ref.float(), rtol=1e-2, atol=1e-2, msg=name)
+    cut = T // 2 + 3
+    halves = [ops.triton_layer_norm_mul_dropout_bwd(
+        dy[sl], attn[sl], u[sl], w, b, mean[sl], rstd[sl], BD, nw, eps, True, p, s, True, True, True, "silu",
+        random_mask=mask[sl]) for sl in (slice(0, cut), slice(cut, T))]
+    assert torch.equal(torch.cat([halves[0][0], halves[1][0]]), dx)
+    for k, full in ((2, dw), (3, db)):
+        two = halves[0][k] + halves[1][k]
+        torch.testing.assert_close(full, two, rtol=1e-4, atol=1e-5 * float(full.abs().max()))
