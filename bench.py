@@ -10,7 +10,9 @@ per-(token, head) fp32 scales amax/448; learned relative-position bias table
 N(0,1) bf16.  One step = forward + backward (dK/dV, dQ and the bias gradient)
 over the whole batch, inputs resident in HBM.  value = causal-effective FLOPs
 (14*D*H*P, P = sum L(L+1)/2) per second.  Also reported: the same step without
-the bias (the reference's attention has none) and on bf16 inputs.
+the bias (the reference's attention has none) and on bf16 inputs, the output
+block's LN * U * dropout kernels (GB/s against HBM), and one whole HSTU layer
+forward + backward in FP8 at config 3's shapes.
 
     python bench.py --copy-calibration   # a 512 MiB device copy, for scaling
                                          # the FETCH_SIZE / WRITE_SIZE counters
@@ -56,18 +58,22 @@ def lengths_cfg3():
     return np.random.default_rng(0).zipf(1.2, 128).clip(32, 4096)
 
 
+def causal_pairs(lengths) -> int:
+    """P = sum L(L+1)/2: the (query, key) pairs the causal mask keeps, per head."""
+    L = np.asarray(lengths, dtype=np.int64)
+    return int(np.sum(L * (L + 1) // 2))
+
+
 class Workload:
     """Device-resident inputs and the raw C-ABI argument tuples of one step."""
 
     def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True):
-        from oracle import hstu_oracle as orc  # generator helpers only (not timed)
-
         self.torch = torch
         dev = "cuda"
         self.lengths = lengths
         self.H, self.D, self.N = H, D, N
         self.T = int(np.sum(lengths))
-        self.P = orc.causal_pairs(lengths)
+        self.P = causal_pairs(lengths)
         g = torch.Generator(device=dev).manual_seed(seed)
         T = self.T
         q = torch.randn(T, H, D, device=dev, generator=g)
@@ -167,6 +173,134 @@ class Workload:
         stats = {"median": float(np.median(step)), "p10": float(np.percentile(step, 10)),
                  "p90": float(np.percentile(step, 90))}
         return wall_ms, stats, parts
+
+
+def _cold_events(torch, fn, steps, warmup, flush, marks=1):
+    """Median / p10 / p90 ms of fn() with HIP events on the current stream,
+    each call after a 512 MiB cache-evicting write (fn may record ``marks``
+    intermediate events through the list it is given)."""
+    for _ in range(warmup):
+        fn(None)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(marks + 1)] for _ in range(steps)]
+    for i in range(steps):
+        flush.zero_()
+        fn(evs[i])
+    torch.cuda.synchronize()
+    segs = [np.array([e[j].elapsed_time(e[j + 1]) for e in evs]) for j in range(marks)]
+    tot = np.array([e[0].elapsed_time(e[-1]) for e in evs])
+    return tot, segs
+
+
+def output_block_bench(torch, T, steps, warmup, flush):
+    """LN * U * dropout of the output block at config 3's token count
+    (D = 512, silu, concat u and x, dropout 0.3 with the 16-bit mask, e4m3
+    output for the FP8 out-projection) and its backward (dx, du, dweight,
+    dbias, recomputed bf16 y): time and GB/s of algorithmic bytes."""
+    import hstu_amd
+
+    os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
+    D = 512
+    g = torch.Generator(device="cuda").manual_seed(5)
+    attn = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
+    u = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.ones(D, device="cuda", dtype=torch.bfloat16)
+    b = torch.zeros(D, device="cuda", dtype=torch.bfloat16)
+    dy = torch.randn(T, 3 * D, device="cuda", generator=g).to(torch.bfloat16)
+    st = {}
+
+    def fwd(ev):
+        if ev is not None:
+            ev[0].record()
+        st["r"] = hstu_amd.triton_layer_norm_mul_dropout_fwd(attn, u, w, b, 1e-6, 0.3, True, True, True, True,
+                                                              "silu", 11, output_fp8=True, inv_scale=1 / 0.02)
+        if ev is not None:
+            ev[1].record()
+
+    tf, _ = _cold_events(torch, fwd, steps, warmup, flush)
+    _, mean, rstd, BD, nw, seed, mask = st["r"]
+
+    def bwd(ev):
+        if ev is not None:
+            ev[0].record()
+        hstu_amd.triton_layer_norm_mul_dropout_bwd(dy, attn, u, w, b, mean, rstd, BD, nw, 1e-6, True, 0.3, seed,
+                                                   True, True, True, "silu", compute_y=True, random_mask=mask)
+        if ev is not None:
+            ev[1].record()
+
+    tb, _ = _cold_events(torch, bwd, steps, warmup, flush)
+    fwd_bytes = T * (2 * D + 2 * D + 3 * D + D + 8)  # x, u in; e4m3 y, mask, mean/rstd out
+    bwd_bytes = T * (6 * D + 2 * D + 2 * D + D + 8 + 2 * D + 2 * D + 6 * D)  # dy, x, u, mask, stats; dx, du, y
+    mf, mb = float(np.median(tf)), float(np.median(tb))
+    return {"workload": "output block LN(attn) * silu(u) * dropout(0.3, mask16) -> [u|attn|y] e4m3 "
+                        "(fwd) and dx, du, dweight, dbias, bf16 y (bwd); T=%d, D=512" % T,
+            "fwd_us": round(mf * 1e3, 1), "fwd_GBps": round(fwd_bytes / (mf * 1e-3) / 1e9, 1),
+            "bwd_us": round(mb * 1e3, 1), "bwd_GBps": round(bwd_bytes / (mb * 1e-3) / 1e9, 1),
+            "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes}, "peak_GBps": HBM_GBS}
+
+
+def layer_params(torch, E=512, H=4, D=128, seed=0):
+    """Random-init STU layer parameters (bf16, modules/stu.py:274-328 shapes)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    r = lambda *s: torch.randn(*s, device="cuda", generator=g)  # noqa: E731
+    n = 2 * H * 2 * D
+    p = {"input_norm_weight": 1 + 0.1 * r(E), "input_norm_bias": 0.05 * r(E),
+         "uvqk_weight": r(E, n) / E ** 0.5, "uvqk_bias": 0.02 * r(n),
+         "output_norm_weight": 1 + 0.1 * r(H * D), "output_norm_bias": 0.05 * r(H * D),
+         "output_weight": r(3 * H * D, E) / (3 * H * D) ** 0.5}
+    return {k: v.to(torch.bfloat16).requires_grad_(True) for k, v in p.items()}
+
+
+def layer_bench(torch, lengths, N, steps, warmup, flush):
+    """one whole HSTU layer in FP8, forward + backward, at
+    config 3's shapes (T = 162 251, N = 4096, E = 512, H = 4, D = 128), with
+    the relative bias and output dropout 0.3 (mask16).  Scales are calibrated
+    once from the data (amax * 1.25 / 448) before timing."""
+    import hstu_amd
+
+    os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
+    E, H, D = 512, 4, 128
+    T = int(np.sum(lengths))
+    g = torch.Generator(device="cuda").manual_seed(21)
+    x = torch.randn(T, E, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(T, E, device="cuda", generator=g).to(torch.bfloat16)
+    p = layer_params(torch, E, H, D)
+    bias = (0.02 * torch.randn(H, 2047, device="cuda", generator=g)).requires_grad_(True)
+    offs = torch.as_tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int64, device="cuda")
+    with torch.no_grad():
+        xn = torch.nn.functional.layer_norm(x.float(), (E,), p["input_norm_weight"].float(),
+                                            p["input_norm_bias"].float(), 1e-6)
+        s_x = float(xn.abs().max()) * 1.25 / 448
+        s_qkv = float((xn @ p["uvqk_weight"].float()[:, H * D:]).abs().max()) * 1.25 / 448
+        del xn
+    sc = lambda s: torch.full((1, 1), s, device="cuda")  # noqa: E731
+    scales = dict(fp8_input_scale=sc(s_x), fp8_qkv_scale=sc(s_qkv), fp8_output_scale=sc(0.02))
+
+    def step(ev):
+        for t in [x, bias, *p.values()]:
+            t.grad = None
+        if ev is not None:
+            ev[0].record()
+        out = hstu_amd.hstu_layer(x, offs, N, p, dropout_ratio=0.3, training=True, attn_bias=bias, seed=7, **scales)
+        if ev is not None:
+            ev[1].record()
+        out.backward(dy)
+        if ev is not None:
+            ev[2].record()
+
+    tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
+    m = float(np.median(tot))
+    P = causal_pairs(lengths)
+    gemm_fwd = 2 * T * E * (2 * H * 2 * D) + 2 * T * (3 * H * D) * E
+    flops = 3 * gemm_fwd + 14 * D * H * P
+    return {"workload": "BASELINE config 5: HSTU layer fwd+bwd in FP8 (LN -> FP8 UVQK GEMM -> FP8 attention with "
+                        "bias -> LN(attn)*silu(u)*dropout -> FP8 out-proj + residual; bf16 dgrad/wgrad), "
+                        "config 3 shapes, E=512",
+            "T": T, "ms_per_step": round(m, 4), "fwd_ms": round(float(np.median(tf)), 4),
+            "bwd_ms": round(float(np.median(tb)), 4),
+            "p10": round(float(np.percentile(tot, 10)), 4), "p90": round(float(np.percentile(tot, 90)), 4),
+            "flops": flops, "value": round(flops / (m * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+            "flops_note": "UVQK + out-proj GEMMs (fwd 1x, bwd 2x) + attention 14*D*H*P"}
 
 
 def cpu_baseline(lengths, H, D, N, budget_s):
@@ -298,6 +432,12 @@ def main():
                        "pct_bf16_peak": round(100 * vb / PEAK_TFLOPS["bf16"], 2),
                        "kernels_ms": {k: round(v, 4) for k, v in parts_b.items()}}
         del wb
+    if not args.headline_only:
+        torch.cuda.empty_cache()
+        res["output_block"] = output_block_bench(torch, int(np.sum(lengths)), max(args.steps // 2, 5), 2, flush)
+        torch.cuda.empty_cache()
+        res["layer"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush)
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(lengths, H, D, N, args.cpu_seconds)
     print(json.dumps(res), flush=True)

@@ -25,3 +25,9 @@ from .hstu_linear import (  # noqa: F401
     triton_weighted_layer_norm_bwd,
     triton_weighted_layer_norm_fwd,
 )
+from .hstu_preprocess import (  # noqa: F401
+    hstu_compute_uqvk,
+    hstu_layer,
+    hstu_preprocess_and_attention,
+    triton_hstu_preprocess_and_attention,
+)

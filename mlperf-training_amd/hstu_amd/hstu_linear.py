@@ -354,6 +354,9 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         ctx.save_for_backward(*saved)
         ctx.recompute = bool(recompute_y_in_backward)
         ctx.has_mask = mask is not None
+        # the preprocess forward tags u with its d(uvqk) row width: du is then
+        # written as the leading columns of that buffer (triton_hstu_linear.py:5347-5350)
+        ctx.du_row_width = int(getattr(u, "_hstu_duvqk_width", 0))
         ctx.cfg = (dropout_ratio, silu_u, concat_u, concat_x, mul_u_activation_type)
         return out
 
@@ -370,7 +373,7 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         dout = dout.contiguous()
         dy = torch.mm(dout, output_weight.to(dout.dtype).t())
         dattn, du, dw, db, y_re = _ln_bwd(dy, attn, u, norm_weight, norm_bias, mean, rstd, ratio, mask, silu_u,
-                                          concat_u, concat_x, act, ctx.recompute)
+                                          concat_u, concat_x, act, ctx.recompute, ctx.du_row_width)
         if y is None:
             y = y_re
         d_out_w = torch.mm(y.t(), dout).to(output_weight.dtype)

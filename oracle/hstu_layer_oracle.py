@@ -1,0 +1,121 @@
+"""CPU oracle for one whole HSTU (STU) layer in FP8 -- BASELINE config 5:
+LayerNorm -> UVQK projection -> jagged attention -> LayerNorm(attn) * U *
+dropout -> output projection + residual -- forward and backward.
+
+TEST INFRASTRUCTURE ONLY (imported by ``tests/`` and nowhere in the product).
+
+Composition of the pinned restatements in ``hstu_oracle`` (attention, e4m3
+quantizers) and ``hstu_ln_oracle`` (LayerNorm * U * dropout, masks), in
+float64 with torch autograd, following the layer's dataflow
+(``modules/stu.py:567-651``; ``ops/hstu_compute.py:86-144, 290-433``;
+``ops/triton/triton_hstu_preprocess_and_attention.py:1206-1289``;
+``ops/triton/triton_hstu_linear.py:5109-5330``).  Quantization follows the
+FP8 contract: forward values are computed from e4m3 operands (LN output at
+s_x, per-column e4m3 weights, V/Q/K at s_qkv, the LN * U output at s_out)
+while gradients flow as in the reference's default backward: bf16 dgrad /
+wgrad GEMMs on the unquantized weights and the recomputed LN(x) / y, and the
+attention backward on the e4m3 V/Q/K values (a straight-through estimator at
+each quantizer).  Parity pins: those of the composed functions; the
+composition itself is checked for shapes, the residual gradient (= dY) and
+agreement with plain autograd when the quantizers are identities.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle import hstu_ln_oracle as L
+from oracle import hstu_oracle as orc
+
+
+def _ste(full: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """``value`` in the forward, d/d``full`` in the backward."""
+    return full + (value - full).detach()
+
+
+def _q_tensor(v: torch.Tensor, scale: Optional[float]) -> torch.Tensor:
+    if scale is None:
+        return v.detach()
+    return L.e4m3_bytes(v.detach(), 1.0 / scale).double() * scale
+
+
+def _q_weight_cols(w_kn: torch.Tensor) -> torch.Tensor:
+    """Per-column e4m3 weight (amax/448 per output column), dequantized."""
+    w8, ws = orc.quantize_e4m3_rows(w_kn.detach().t().contiguous().float())
+    return orc.dequantize(w8, ws).double().t()
+
+
+def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128, hidden_dim=128, eps=1e-6,
+                   alpha=None, s_x=None, s_qkv=None, s_out=None, dropout_ratio=0.0, mask=None, attn_bias=None,
+                   quantize=True):
+    """Layer output [T, E] (float64, differentiable w.r.t. x and every
+    parameter tensor in ``params``).  ``s_*`` = None with ``quantize`` keeps
+    that stage in full precision; ``quantize=False`` disables every
+    quantizer."""
+    H, Dq, Dv = num_heads, attn_dim, hidden_dim
+    nu = H * Dv
+    T = x.shape[0]
+    alpha = alpha if alpha is not None else 1.0 / Dq ** 0.5
+    p = params
+    xn = F.layer_norm(x, (x.shape[1],), p["input_norm_weight"], p["input_norm_bias"], eps)
+    uvqk_f = xn @ p["uvqk_weight"] + p["uvqk_bias"]
+    if quantize and s_x is not None:
+        xq = _q_tensor(xn, s_x)
+        uvqk_q = xq @ _q_weight_cols(p["uvqk_weight"]) + p["uvqk_bias"].detach()
+    else:
+        uvqk_q = uvqk_f.detach()
+    # with quantize, the stages the kernels hand over in bf16 (u, a bf16 vqk,
+    # attn) are rounded to bf16 as well
+    bf = (lambda t: t.to(torch.bfloat16).double()) if quantize else (lambda t: t)
+    u = _ste(uvqk_f[:, :nu], bf(uvqk_q[:, :nu]))
+    vqk_val = uvqk_q[:, nu:]
+    vqk_val = _q_tensor(vqk_val, s_qkv) if (quantize and s_qkv is not None) else bf(vqk_val)
+    vqk = _ste(uvqk_f[:, nu:], vqk_val)
+    v = vqk[:, :nu].reshape(T, H, Dv)
+    q = vqk[:, nu:nu + H * Dq].reshape(T, H, Dq)
+    k = vqk[:, nu + H * Dq:].reshape(T, H, Dq)
+    offs = orc.offsets_from_lengths(lengths)
+    attn = orc.hstu_mha_dense(max_seq_len, alpha, q, k, v, offs, attn_bias=attn_bias,
+                              dtype=torch.float64).reshape(T, H * Dv)
+    attn = _ste(attn, bf(attn.detach()))
+    y, _, _ = L.ln_mul_dropout_fwd(attn, u, p["output_norm_weight"], p["output_norm_bias"], eps,
+                                   dropout_ratio=dropout_ratio, mask=mask, silu_u=True, concat_u=True,
+                                   concat_x=True, mul_u_activation_type="silu")
+    W = p["output_weight"]
+    full = y @ W
+    if quantize and s_out is not None:
+        val = _q_tensor(y, s_out) @ _q_weight_cols(W)
+    else:
+        val = full.detach()
+    return x + _ste(full, val)
+
+
+def make_layer_params(E=512, H=4, Dq=128, Dv=128, seed=0, dtype=torch.bfloat16):
+    """Random-init STU parameters (``modules/stu.py:274-328`` shapes)."""
+    g = torch.Generator().manual_seed(seed)
+    n_uvqk = 2 * H * (Dq + Dv)
+    return {
+        "input_norm_weight": (1 + 0.1 * torch.randn(E, generator=g)).to(dtype),
+        "input_norm_bias": (0.05 * torch.randn(E, generator=g)).to(dtype),
+        "uvqk_weight": (torch.randn(E, n_uvqk, generator=g) / E ** 0.5).to(dtype),
+        "uvqk_bias": (0.02 * torch.randn(n_uvqk, generator=g)).to(dtype),
+        "output_norm_weight": (1 + 0.1 * torch.randn(H * Dv, generator=g)).to(dtype),
+        "output_norm_bias": (0.05 * torch.randn(H * Dv, generator=g)).to(dtype),
+        "output_weight": (torch.randn(3 * H * Dv, E, generator=g) / (3 * H * Dv) ** 0.5).to(dtype),
+    }
+
+
+def layer_flops(lengths, E=512, H=4, D=128) -> dict:
+    """Algorithmic FLOPs of one layer: the UVQK GEMM 2*T*E*(4*H*D) and the
+    output projection 2*T*(3*H*D)*E (forward once, backward twice: dgrad and
+    wgrad), attention 4*D*H*P forward and 10*D*H*P backward."""
+    T = int(np.sum(lengths))
+    gemm_fwd = 2 * T * E * (2 * H * 2 * D) + 2 * T * (3 * H * D) * E
+    attn_f = orc.attn_flops(lengths, H, D, fwd=True, bwd=False)
+    attn_b = orc.attn_flops(lengths, H, D, fwd=False, bwd=True)
+    return {"gemm_fwd": gemm_fwd, "gemm_bwd": 2 * gemm_fwd, "attn_fwd": attn_f, "attn_bwd": attn_b,
+            "total": 3 * gemm_fwd + attn_f + attn_b}

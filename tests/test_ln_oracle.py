@@ -179,3 +179,25 @@ def test_e4m3_bytes_saturate_and_round():
     v = torch.tensor([0.0, 1.0, 1.0625, 1.1875, 500.0, -1000.0], dtype=torch.float64)
     q = L.e4m3_bytes(v, 1.0).to(torch.float32)
     assert q.tolist() == [0.0, 1.0, 1.0, 1.25, 448.0, -448.0]
+
+
+def test_layer_oracle_composition_gradcheck():
+    """The layer composition is differentiable end to end (gradcheck on a
+    tiny unquantized instance: E = 8, one head of width 4, no dropout)."""
+    from oracle import hstu_layer_oracle as LO
+
+    lengths = np.array([3, 2])
+    E, H, Dq, Dv = 8, 1, 4, 4
+    p = LO.make_layer_params(E, H, Dq, Dv, seed=1, dtype=torch.float64)
+    x = torch.randn(5, E, dtype=torch.float64, generator=torch.Generator().manual_seed(2))
+    names = list(p)
+
+    def f(x_, *ps):
+        return LO.hstu_layer_ref(x_, dict(zip(names, ps)), lengths, 3, num_heads=H, attn_dim=Dq, hidden_dim=Dv,
+                                 quantize=False)
+
+    args = (x.requires_grad_(True),) + tuple(p[k].clone().requires_grad_(True) for k in names)
+    assert torch.autograd.gradcheck(f, args, eps=1e-6, atol=1e-5)
+    # the residual: d out / d x contains the identity
+    out = f(*args)
+    assert out.shape == x.shape
