@@ -49,6 +49,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--only", choices=("output_block", "layer"), default=None,
+                    help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the FP8-with-bias line (no no-bias / bf16 sub-results); for profiler runs")
     return ap.parse_args()
@@ -232,11 +234,18 @@ def output_block_bench(torch, T, steps, warmup, flush):
     fwd_bytes = T * (2 * D + 2 * D + 3 * D + D + 8)  # x, u in; e4m3 y, mask, mean/rstd out
     bwd_bytes = T * (6 * D + 2 * D + 2 * D + D + 8 + 2 * D + 2 * D + 6 * D)  # dy, x, u, mask, stats; dx, du, y
     mf, mb = float(np.median(tf)), float(np.median(tb))
+    traffic = None
+    tfile = REPO / "profiles" / "hbm_traffic_output_block_cfg3.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hstu_ln_mul_bwd")
+    bwd_gbs = bwd_bytes / (mb * 1e-3) / 1e9
     return {"workload": "output block LN(attn) * silu(u) * dropout(0.3, mask16) -> [u|attn|y] e4m3 "
                         "(fwd) and dx, du, dweight, dbias, bf16 y (bwd); T=%d, D=512" % T,
             "fwd_us": round(mf * 1e3, 1), "fwd_GBps": round(fwd_bytes / (mf * 1e-3) / 1e9, 1),
             "bwd_us": round(mb * 1e3, 1), "bwd_GBps": round(bwd_bytes / (mb * 1e-3) / 1e9, 1),
-            "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes}, "peak_GBps": HBM_GBS}
+            "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes}, "peak_GBps": HBM_GBS,
+            "roofline": {"bound": "hbm", "kernel": "hstu_ln_mul_bwd", "achieved": round(bwd_gbs, 1), "peak": HBM_GBS,
+                         "unit": "GB/s", "frac": round(bwd_gbs / HBM_GBS, 4), "traffic": traffic}}
 
 
 def layer_params(torch, E=512, H=4, D=128, seed=0):
@@ -375,6 +384,12 @@ def main():
     lengths = lengths_cfg3()
     H, D, N = 4, 128, 4096
     flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda")
+    if args.only == "output_block":
+        print(json.dumps(output_block_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
+        return
+    if args.only == "layer":
+        print(json.dumps(layer_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
+        return
     w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
     wall_ms, st, parts = w8.run(args.steps, args.warmup, flush)
     total = w8.flops("step")

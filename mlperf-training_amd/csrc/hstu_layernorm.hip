@@ -24,7 +24,11 @@ namespace {
 enum Act { kActNone = 0, kActSilu = 1, kActSigmoid = 2 };
 
 constexpr int kFwdRows = 8;       // rows per forward block: one mask16 Philox group
-constexpr int kBwdBlocks = 256;  // backward grid: one block per CU, rows strided over its waves (measured best)
+// Backward grid: rows are strided over the waves.  With u (the output block,
+// ~11 KB of traffic per row) one block per CU measured best; the plain
+// LayerNorm backward (6 KB per row, fewer registers) needs 4 per CU to cover
+// the memory latency.
+constexpr int kBwdBlocksU = 256, kBwdBlocksMax = 1024;
 
 // ------------------------------------------------------------------ Philox
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11) on counter (c0, 0, 0, 0)
@@ -626,7 +630,7 @@ void launch_fwd(int D, int act, bool drop, bool e4m3, const FwdArgs& a, hipStrea
 
 template <int EPT, int ACT>
 void launch_bwd_act(bool drop, bool y, const BwdArgs& a, hipStream_t st) {
-  const dim3 g(kBwdBlocks), b(kThreads);
+  const dim3 g(ACT == kNoU ? kBwdBlocksMax : kBwdBlocksU), b(kThreads);
   if (drop && y) hipLaunchKernelGGL((ln_mul_bwd_kernel<EPT, ACT, true, true>), g, b, 0, st, a);
   else if (drop) hipLaunchKernelGGL((ln_mul_bwd_kernel<EPT, ACT, true, false>), g, b, 0, st, a);
   else if (y) hipLaunchKernelGGL((ln_mul_bwd_kernel<EPT, ACT, false, true>), g, b, 0, st, a);
@@ -710,7 +714,7 @@ extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_
 
 extern "C" int64_t hstu_ln_mul_bwd_workspace_bytes(int rows, int D) {
   if (rows < 0 || !d_served(D)) return -1;
-  return (int64_t)kBwdBlocks * 2 * D * 4;
+  return (int64_t)kBwdBlocksMax * 2 * D * 4;
 }
 
 extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const void* u,
@@ -761,7 +765,7 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   a.ldy = ldy;
   a.partial = (float*)workspace;
   launch_bwd(D, u == nullptr ? kNoU : mul_u_act, mask != nullptr, y != nullptr, a, stream);
-  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial, kBwdBlocks,
-                     D, dweight, dbias);
+  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial,
+                     u == nullptr ? kBwdBlocksMax : kBwdBlocksU, D, dweight, dbias);
   return (int)hipGetLastError();
 }

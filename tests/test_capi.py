@@ -107,7 +107,7 @@ def test_ln_mul_entry_points_reject_before_launch():
     import hstu_amd._lib as lib
 
     ws = lib.fn("hstu_ln_mul_bwd_workspace_bytes")
-    assert ws(162251, 512) == 256 * 2 * 512 * 4
+    assert ws(162251, 512) == 1024 * 2 * 512 * 4
     assert ws(10, 384) == -1 and ws(-1, 512) == -1
     fwd = lib.fn("hstu_ln_mul_fwd")
     X, W = 4096, 8192  # fake device addresses: none of these calls may launch
