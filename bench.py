@@ -11,8 +11,9 @@ N(0,1) bf16.  One step = forward + backward (dK/dV, dQ and the bias gradient)
 over the whole batch, inputs resident in HBM.  value = causal-effective FLOPs
 (14*D*H*P, P = sum L(L+1)/2) per second.  Also reported: the same step without
 the bias (the reference's attention has none) and on bf16 inputs, the output
-block's LN * U * dropout kernels (GB/s against HBM), and one whole HSTU layer
-forward + backward in FP8 at config 3's shapes.
+block's LN * U * dropout kernels (GB/s against HBM), one whole HSTU layer
+forward + backward in FP8 at config 3's shapes, and the
+targets-only delta-q attention.
 
     python bench.py --copy-calibration   # a 512 MiB device copy, for scaling
                                          # the FETCH_SIZE / WRITE_SIZE counters
@@ -39,6 +40,26 @@ PEAK_TFLOPS = {"fp8": 5000.0, "bf16": 2500.0}
 HBM_GBS = 8000.0
 
 
+class CacheFlush:
+    """Evicts L2 and the 256 MB MALL before a timed call, so that the timed
+    kernels find their inputs in HBM.  Mode "read" (default) reads a 512 MiB
+    buffer and leaves only clean lines behind; mode "write" zero-fills it and
+    leaves ~256 MB of dirty lines whose write-back then competes with the
+    timed kernel's own traffic (a plain 166 MB read kernel takes ~30 us after
+    a read flush and ~59 us after a write flush on MI355X)."""
+
+    def __init__(self, torch, mode="read"):
+        self.torch, self.mode = torch, mode
+        self.buf = torch.zeros(512 * 1024 * 1024, dtype=torch.uint8, device="cuda")
+        self.words = self.buf.view(torch.int64)
+
+    def __call__(self):
+        if self.mode == "write":
+            self.buf.zero_()
+        else:
+            self.torch.sum(self.words)
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -49,8 +70,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--only", choices=("output_block", "layer"), default=None,
+    ap.add_argument("--only", choices=("output_block", "layer", "delta"), default=None,
                     help="run just one secondary measurement and print its JSON (for profiling)")
+    ap.add_argument("--flush", choices=("read", "write"), default="read",
+                    help="how the caches are evicted before each timed call (see CacheFlush)")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the FP8-with-bias line (no no-bias / bf16 sub-results); for profiler runs")
     return ap.parse_args()
@@ -149,9 +172,9 @@ class Workload:
     def run(self, steps, warmup, flush):
         """Returns (back-to-back wall ms/step, cold-cache step stats, per-kernel medians).
 
-        Cold-cache pass: before each step a 512 MiB device write evicts L2
-        and the 256 MB MALL, then HIP events on the launch stream bracket the
-        step and each of its three entry points."""
+        Cold-cache pass: before each step ``flush()`` evicts L2 and the
+        256 MB MALL, then HIP events on the launch stream bracket the step and
+        each of its three entry points."""
         torch = self.torch
         for _ in range(warmup):
             self.step()
@@ -163,7 +186,7 @@ class Workload:
         wall_ms = (time.perf_counter() - t0) * 1e3 / steps
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
         for i in range(steps):
-            flush.zero_()
+            flush()
             self.step(evs[i])
         torch.cuda.synchronize()
         step = np.array([e[0].elapsed_time(e[3]) for e in evs])
@@ -179,14 +202,14 @@ class Workload:
 
 def _cold_events(torch, fn, steps, warmup, flush, marks=1):
     """Median / p10 / p90 ms of fn() with HIP events on the current stream,
-    each call after a 512 MiB cache-evicting write (fn may record ``marks``
-    intermediate events through the list it is given)."""
+    each call after ``flush()`` has evicted the caches (fn may record
+    ``marks`` intermediate events through the list it is given)."""
     for _ in range(warmup):
         fn(None)
     torch.cuda.synchronize()
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(marks + 1)] for _ in range(steps)]
     for i in range(steps):
-        flush.zero_()
+        flush()
         fn(evs[i])
     torch.cuda.synchronize()
     segs = [np.array([e[j].elapsed_time(e[j + 1]) for e in evs]) for j in range(marks)]
@@ -246,6 +269,51 @@ def output_block_bench(torch, T, steps, warmup, flush):
             "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes}, "peak_GBps": HBM_GBS,
             "roofline": {"bound": "hbm", "kernel": "hstu_ln_mul_bwd", "achieved": round(bwd_gbs, 1), "peak": HBM_GBS,
                          "unit": "GB/s", "frac": round(bwd_gbs / HBM_GBS, 4), "traffic": traffic}}
+
+
+def delta_bench(torch, lengths, N, steps, warmup, flush):
+    """Targets-only delta-q attention at config 3's sequences: one query per
+    sequence over its whole e4m3 K/V (per-tensor scales), forward and backward
+    (dq, dk, dv for every row).  HBM-bound: GB/s of algorithmic bytes."""
+    import hstu_amd
+
+    H, D = 4, 128
+    B, T = len(lengths), int(np.sum(lengths))
+    g = torch.Generator(device="cuda").manual_seed(31)
+    q = (torch.randn(B, H, D, device="cuda", generator=g) / 4).to(torch.float8_e4m3fn)
+    k = (torch.randn(T, H, D, device="cuda", generator=g) / 4).to(torch.float8_e4m3fn)
+    v = (torch.randn(T, H, D, device="cuda", generator=g) / 4).to(torch.float8_e4m3fn)
+    do = torch.randn(B, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    offs = torch.as_tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int64, device="cuda")
+    dq = torch.empty(B, H, D, dtype=torch.bfloat16, device="cuda")
+    dk = torch.empty(T, H, D, dtype=torch.bfloat16, device="cuda")
+    dv = torch.empty_like(dk)
+    alpha = 1 / D ** 0.5
+
+    def fwd(ev):
+        if ev is not None:
+            ev[0].record()
+        hstu_amd.triton_cached_hstu_mha(N, alpha, q, k, v, offs, q_scale=0.01, k_scale=0.01, v_scale=0.01)
+        if ev is not None:
+            ev[1].record()
+
+    def bwd(ev):
+        if ev is not None:
+            ev[0].record()
+        hstu_amd.triton_hstu_attention_delta_bwd(do, q, k, v, dq, dk, dv, offs, N, alpha, 0.01, 0.01, q_scale=0.01)
+        if ev is not None:
+            ev[1].record()
+
+    tf, _ = _cold_events(torch, fwd, steps, warmup, flush)
+    tb, _ = _cold_events(torch, bwd, steps, warmup, flush)
+    fwd_bytes = 2 * T * H * D + B * H * D * 3  # e4m3 k, v; q in, bf16 out
+    bwd_bytes = 2 * T * H * D + 2 * 2 * T * H * D + B * H * D * 5  # k, v in; bf16 dk, dv out; q, dO, dq
+    mf, mb = float(np.median(tf)), float(np.median(tb))
+    return {"workload": "delta-q (targets-only) attention, one query per sequence over its whole e4m3 K/V, "
+                        "config 3 sequences (B=128, T=%d), N=4096, H=4, D=128" % T,
+            "fwd_us": round(mf * 1e3, 1), "fwd_GBps": round(fwd_bytes / (mf * 1e-3) / 1e9, 1),
+            "bwd_us": round(mb * 1e3, 1), "bwd_GBps": round(bwd_bytes / (mb * 1e-3) / 1e9, 1),
+            "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes}, "peak_GBps": HBM_GBS}
 
 
 def layer_params(torch, E=512, H=4, D=128, seed=0):
@@ -383,12 +451,15 @@ def main():
     lib.load_library()
     lengths = lengths_cfg3()
     H, D, N = 4, 128, 4096
-    flush = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda")
+    flush = CacheFlush(torch, args.flush)
     if args.only == "output_block":
         print(json.dumps(output_block_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
         return
     if args.only == "layer":
         print(json.dumps(layer_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
+        return
+    if args.only == "delta":
+        print(json.dumps(delta_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
         return
     w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
     wall_ms, st, parts = w8.run(args.steps, args.warmup, flush)
@@ -419,7 +490,8 @@ def main():
                    "causal_pairs_per_head": w8.P, "attn_bias": True, "parallelism": "none (1 GPU)"},
         "timing": {"ms_per_step_median_cold": round(st["median"], 4), "p10": round(st["p10"], 4),
                    "p90": round(st["p90"], 4), "ms_per_step_back_to_back": round(wall_ms, 4),
-                   "method": "HIP events per step after a 512 MiB cache-evicting write; value uses the median"},
+                   "method": "HIP events per step after a 512 MiB cache-evicting %s (CacheFlush); value uses the "
+                             "median" % args.flush},
         "pct_fp8_peak": round(100 * value / PEAK_TFLOPS["fp8"], 2),
         "kernels_ms": {k: round(v, 4) for k, v in parts.items()},
         "kernels_tflops": {k: round(w8.flops(k) / (v * 1e-3) / 1e12, 1) for k, v in parts.items()},
@@ -452,6 +524,8 @@ def main():
         res["output_block"] = output_block_bench(torch, int(np.sum(lengths)), max(args.steps // 2, 5), 2, flush)
         torch.cuda.empty_cache()
         res["layer"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush)
+        torch.cuda.empty_cache()
+        res["delta"] = delta_bench(torch, lengths, N, args.steps, 3, flush)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(lengths, H, D, N, args.cpu_seconds)

@@ -243,6 +243,44 @@ int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
                     float* dweight, float* dbias, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
 
+/*
+ * Delta-q ("cached" / targets-only) attention: DS compact query rows per
+ * sequence (delta_q [B*DS, H, D]) at positions L-DS .. L-1 of each sequence,
+ * against that sequence's whole k / v [T, H, D] (L = min(length, N)), with
+ * the _get_valid_attn_mask rows of those positions.  dtype is the k / v type
+ * (bf16, or e4m3 with the per-tensor scales k_scale / v_scale), q_dtype the
+ * delta q's (e4m3 with q_scale).  Output bf16 [B*DS, H, D]; D = 64 or 128.
+ * Per-chunk fp32 partials go to the workspace and are summed in chunk order
+ * (bitwise deterministic).
+ * Replaces: triton_cached_hstu_mha, ops/triton/triton_hstu_attention.py:3710-3866
+ *           (math of pytorch_cached_hstu_mha, ops/pytorch/pt_hstu_attention.py:191-251).
+ */
+int64_t hstu_delta_attn_workspace_bytes(int B, int H, int D, int N, int delta_size);
+int hstu_delta_attn_fwd(int dtype, int q_dtype, const void* q, const void* k, const void* v,
+                        int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                        float q_scale, float k_scale, float v_scale,
+                        const int64_t* seq_offsets, int B, int H, int D, int max_seq_len, int delta_size,
+                        float alpha, const int* num_targets, int max_attn_len, int contextual_seq_len,
+                        void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                        hipStream_t stream);
+
+/*
+ * Backward of the delta attention (delta_size <= 4): writes dq [B*DS, H, D],
+ * and dk, dv for every row of every sequence (zero where no delta query
+ * attends, including rows past max_seq_len).  As in the reference, k and v
+ * are dequantized and rounded to bf16 and silu / dS rounded to bf16 before use.
+ * Replaces: triton_hstu_attention_delta_bwd, ops/triton/triton_hstu_attention.py:3413-3480
+ *           (kernel _hstu_attn_delta_bwd :3033-3163).
+ */
+int hstu_delta_attn_bwd(int dtype, int q_dtype, const void* dout, int64_t dout_row_stride,
+                        const void* q, const void* k, const void* v,
+                        int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                        float q_scale, float k_scale, float v_scale,
+                        const int64_t* seq_offsets, int B, int H, int D, int max_seq_len, int delta_size,
+                        float alpha, const int* num_targets, int max_attn_len, int contextual_seq_len,
+                        void* dq, void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride,
+                        int64_t dv_row_stride, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

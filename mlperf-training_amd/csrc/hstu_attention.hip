@@ -53,31 +53,6 @@
 namespace {
 using namespace hstu;
 
-// ---------------------------------------------------------------- mask
-struct MaskCtx {
-  int L, nt, ctx, max_attn;
-  bool targets;
-};
-// _get_valid_attn_mask (ops/pytorch/pt_hstu_attention.py:32-84), per element.
-__device__ __forceinline__ bool valid_generic(int i, int j, const MaskCtx& m) {
-  int max_ids = m.L, ii = i, jj = j;
-  if (m.ctx > 0) {
-    ii = max(i - m.ctx + 1, 0);
-    jj = max(j - m.ctx + 1, 0);
-    max_ids = m.L - m.ctx + 1;
-  }
-  if (m.targets) {
-    max_ids -= m.nt;
-    ii = min(ii, max_ids);
-    jj = min(jj, max_ids);
-  }
-  const int dist = ii - jj;
-  bool v = (i == j) || (dist > 0);
-  if (m.max_attn > 0) v = v && (dist <= m.max_attn);
-  if (m.ctx > 0) v = v || (ii == 0 && jj < max_ids);
-  return v && j < m.L && i < m.L;
-}
-
 // ---------------------------------------------------------------- tile movers
 // Each mover is split into load() (global -> registers, issued before the
 // MFMAs of the current tile) and store() (registers -> LDS, after them).

@@ -181,6 +181,31 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl<N>(f, std::make_integer_sequence<int, N>{});
 }
 
+// ---------------------------------------------------------------- mask
+struct MaskCtx {
+  int L, nt, ctx, max_attn;
+  bool targets;
+};
+// _get_valid_attn_mask (ops/pytorch/pt_hstu_attention.py:32-84), per element.
+__device__ __forceinline__ bool valid_generic(int i, int j, const MaskCtx& m) {
+  int max_ids = m.L, ii = i, jj = j;
+  if (m.ctx > 0) {
+    ii = max(i - m.ctx + 1, 0);
+    jj = max(j - m.ctx + 1, 0);
+    max_ids = m.L - m.ctx + 1;
+  }
+  if (m.targets) {
+    max_ids -= m.nt;
+    ii = min(ii, max_ids);
+    jj = min(jj, max_ids);
+  }
+  const int dist = ii - jj;
+  bool v = (i == j) || (dist > 0);
+  if (m.max_attn > 0) v = v && (dist <= m.max_attn);
+  if (m.ctx > 0) v = v || (ii == 0 && jj < max_ids);
+  return v && j < m.L && i < m.L;
+}
+
 // vmcnt(0); expcnt and lgkmcnt left at their maxima.
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 

@@ -31,3 +31,4 @@ from .hstu_preprocess import (  # noqa: F401
     hstu_preprocess_and_attention,
     triton_hstu_preprocess_and_attention,
 )
+from .hstu_delta import delta_hstu_mha, triton_cached_hstu_mha, triton_hstu_attention_delta_bwd  # noqa: F401

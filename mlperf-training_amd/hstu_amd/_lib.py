@@ -38,6 +38,9 @@ EXPORTED_SYMBOLS = (
     "hstu_ln_mul_fwd",
     "hstu_ln_mul_bwd_workspace_bytes",
     "hstu_ln_mul_bwd",
+    "hstu_delta_attn_workspace_bytes",
+    "hstu_delta_attn_fwd",
+    "hstu_delta_attn_bwd",
 )
 
 
@@ -90,6 +93,17 @@ _SIGNATURES = {
          _vp, _i64, _vp, _i64, _i32, _f32, _vp, _vp, _vp],
     ),
     "hstu_ln_mul_bwd_workspace_bytes": (_i64, [_i32, _i32]),
+    "hstu_delta_attn_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),
+    "hstu_delta_attn_fwd": (
+        _i32,
+        [_i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _vp, _i32, _i32, _i32, _i32, _i32, _f32,
+         _vp, _i32, _i32, _vp, _i64, _vp, _i64, _vp],
+    ),
+    "hstu_delta_attn_bwd": (
+        _i32,
+        [_i32, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _vp, _i32, _i32, _i32, _i32,
+         _i32, _f32, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
+    ),
     "hstu_ln_mul_bwd": (
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,

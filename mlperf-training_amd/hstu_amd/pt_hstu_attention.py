@@ -121,3 +121,36 @@ def pytorch_hstu_mha(
         s = F.dropout(s, p=dropout_pr, training=training)
     o = torch.matmul(s, vp)
     return dense_to_jagged(o.transpose(1, 2).flatten(2, 3), seq_offsets, L).view(L, H, V)
+
+
+def pytorch_cached_hstu_mha(
+    max_seq_len: int,
+    alpha: float,
+    delta_q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_offsets: torch.Tensor,
+    num_targets: Optional[torch.Tensor] = None,
+    max_attn_len: int = 0,
+    contextual_seq_len: int = 0,
+) -> torch.Tensor:
+    """Delta-q attention (``pt_hstu_attention.py:191-251``): the DS = rows/B
+    compact queries of each sequence sit at its last DS positions and use those
+    rows of the valid mask against the padded keys."""
+    Ld, H, D = delta_q.shape
+    V = v.shape[2]
+    B = seq_offsets.numel() - 1
+    ds = Ld // B
+    N = max_seq_len
+    qd = delta_q.view(B, ds, H, D).transpose(1, 2)
+    kp = jagged_to_padded_dense(k.reshape(-1, H * D), seq_offsets, N).view(B, N, H, D).transpose(1, 2)
+    vp = jagged_to_padded_dense(v.reshape(-1, H * V), seq_offsets, N).view(B, N, H, V).transpose(1, 2)
+    s = F.silu(torch.matmul(qd, kp.transpose(-1, -2).contiguous()) * alpha) / N
+    lengths = seq_offsets[1:] - seq_offsets[:-1]
+    full = get_valid_attn_mask(delta_q.device, True, N, lengths, num_targets, max_attn_len,
+                               contextual_seq_len).expand(B, N, N)
+    pos = torch.arange(N, device=delta_q.device).view(1, -1)
+    rows = (pos >= (lengths - ds).view(-1, 1)) & (pos < lengths.view(-1, 1))
+    mask = full[rows.view(B, N, 1).expand(B, N, N)].view(B, ds, N)
+    s = s * mask.unsqueeze(1)
+    return torch.matmul(s, vp).transpose(1, 2).reshape(Ld, H, V)

@@ -21,6 +21,9 @@ checks live in ``tests/test_oracle.py``):
   prefix invariance, jagged independence, 1/N scaling).
 * ``hstu_mha_bwd``               -- torch.autograd on the float64 dense
   restatement and ``torch.autograd.gradcheck``.
+* ``cached_hstu_mha``           -- the last DS rows of ``hstu_mha_dense`` on
+  the same sequences (the delta rows are those rows of the full attention);
+  its backward against ``hstu_mha_bwd`` with dO zero outside those rows.
 * ``rel_bias_index`` / bias path -- brute force; with ``attn_bias=None`` the
   result equals the reference path exactly.  The bias itself has NO reference
   counterpart (the reference has no attention bias): it is this build's own
@@ -321,6 +324,46 @@ def hstu_mha_bwd_closed_form(
             if db is not None:
                 db[h].index_add_(0, idx.reshape(-1), ds.reshape(-1))
     return dq, dk, dv, db
+
+
+# --------------------------------------------------------------------------
+# delta-q ("cached") attention
+# --------------------------------------------------------------------------
+def cached_hstu_mha(
+    max_seq_len: int,
+    alpha: float,
+    delta_q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    seq_offsets: torch.Tensor,
+    num_targets: Optional[torch.Tensor] = None,
+    max_attn_len: int = 0,
+    contextual_seq_len: int = 0,
+    dtype: torch.dtype = torch.float64,
+) -> torch.Tensor:
+    """Restatement of ``pytorch_cached_hstu_mha``
+    (``ops/pytorch/pt_hstu_attention.py:191-251``): the DS = rows/B compact
+    queries of each sequence sit at positions L-DS .. L-1 and use those rows of
+    the valid mask against the padded [N] keys.  Differentiable (autograd)."""
+    Ld, H, D = delta_q.shape
+    Dv = v.shape[2]
+    B = seq_offsets.numel() - 1
+    ds = Ld // B
+    N = max_seq_len
+    qd = delta_q.to(dtype).view(B, ds, H, D).transpose(1, 2)
+    kp = jagged_to_padded(k.reshape(-1, H * D).to(dtype), seq_offsets, N).view(B, N, H, D).transpose(1, 2)
+    vp = jagged_to_padded(v.reshape(-1, H * Dv).to(dtype), seq_offsets, N).view(B, N, H, Dv).transpose(1, 2)
+    s = torch.matmul(qd, kp.transpose(-1, -2)) * alpha  # [B, H, ds, N]
+    p = F.silu(s) / N
+    lengths = seq_offsets[1:] - seq_offsets[:-1]
+    full = valid_attn_mask(N, lengths, num_targets, max_attn_len, contextual_seq_len)
+    full = full.expand(B, N, N)
+    pos = torch.arange(N).view(1, -1)
+    rows = (pos >= (lengths - ds).view(-1, 1)) & (pos < lengths.view(-1, 1))  # the delta rows
+    mask = full[rows.view(B, N, 1).expand(B, N, N)].view(B, ds, N)
+    p = p * mask.unsqueeze(1).to(dtype)
+    out = torch.matmul(p, vp)  # [B, H, ds, Dv]
+    return out.transpose(1, 2).reshape(Ld, H, Dv)
 
 
 # --------------------------------------------------------------------------

@@ -144,3 +144,30 @@ def test_ln_mul_entry_points_reject_before_launch():
     assert g(lddy=1024) == lib.HSTU_E_BAD_ARG
     assert g(y=X, ldy=512) == lib.HSTU_E_BAD_ARG
     assert g(D=128, ldx=128, ldu=128, lddx=128, lddu=128, lddy=384) == lib.HSTU_E_UNSUPPORTED
+
+
+def test_delta_entry_points_reject_before_launch():
+    import hstu_amd._lib as lib
+
+    wsq = lib.fn("hstu_delta_attn_workspace_bytes")
+    assert wsq(128, 4, 128, 4096, 1) == 128 * 4 * 16 * 128 * 4
+    assert wsq(-1, 4, 128, 4096, 1) == -1
+    fwd = lib.fn("hstu_delta_attn_fwd")
+    X, W = 4096, 8192
+
+    def f(**kw):
+        a = dict(dt=1, qdt=1, q=X, k=X, v=X, qrs=512, krs=512, vrs=512, qs=1.0, ks=1.0, vs=1.0, offs=W, B=8, H=4,
+                 D=128, N=1024, ds=1, alpha=0.1, nt=None, win=0, ctx=0, out=X, ors=512, ws=W, wsb=wsq(8, 4, 128, 1024, 1),
+                 stream=None)
+        a.update(kw)
+        return fwd(*a.values())
+
+    assert f(D=96, qrs=384, krs=384, vrs=384, ors=384) == lib.HSTU_E_UNSUPPORTED
+    assert f(wsb=16) == lib.HSTU_E_BAD_ARG
+    assert f(dt=3) == lib.HSTU_E_BAD_ARG
+    assert f(krs=100) == lib.HSTU_E_BAD_ARG
+    assert f(k=X + 4) == lib.HSTU_E_UNSUPPORTED  # 8-element pieces must be aligned
+    bwd = lib.fn("hstu_delta_attn_bwd")
+    args = [1, 1, X, 512, X, X, X, 512, 512, 512, 1.0, 1.0, 1.0, W, 8, 4, 128, 1024, 5, 0.1, None, 0, 0, X, X, X,
+            512, 512, 512, W, wsq(8, 4, 128, 1024, 5), None]
+    assert bwd(*args) == lib.HSTU_E_UNSUPPORTED  # more than 4 delta rows per sequence

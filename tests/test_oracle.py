@@ -235,3 +235,33 @@ def test_rowcol_gemm_matches_matmul():
     assert torch.allclose(c, want, atol=1e-12)
     # and the dequantized product approximates the unquantized one
     assert orc.rel_l2(a.double() @ w.double(), ad @ wd) < 0.06
+
+
+# ---------------------------------------------------------------- delta-q attention
+@pytest.mark.parametrize("ds,nt,ctx,win", [(1, None, 0, 0), (2, None, 0, 0), (1, [1, 2, 1], 0, 0), (3, None, 2, 3)])
+def test_cached_attention_equals_last_rows_of_full(ds, nt, ctx, win):
+    lengths = [9, 5, 12]
+    H, D, N = 2, 8, 12
+    q, k, v, offs = _rand(lengths, H, D, seed=4)
+    num_targets = None if nt is None else torch.tensor(nt)
+    full = orc.hstu_mha_dense(N, 0.3, q, k, v, offs, num_targets=num_targets, max_attn_len=win,
+                              contextual_seq_len=ctx, dtype=torch.float64)
+    rows = torch.cat([torch.arange(int(offs[b + 1]) - ds, int(offs[b + 1])) for b in range(len(lengths))])
+    got = orc.cached_hstu_mha(N, 0.3, q[rows], k, v, offs, num_targets=num_targets, max_attn_len=win,
+                              contextual_seq_len=ctx)
+    assert torch.allclose(got, full[rows], rtol=1e-12, atol=1e-14)
+
+
+def test_cached_attention_backward_matches_full_backward_on_delta_rows():
+    lengths = [7, 11]
+    H, D, N, ds = 2, 8, 11, 1
+    q, k, v, offs = _rand(lengths, H, D, seed=6)
+    rows = torch.cat([torch.arange(int(offs[b + 1]) - ds, int(offs[b + 1])) for b in range(len(lengths))])
+    dout_d = torch.randn(len(rows), H, D, dtype=torch.float64, generator=torch.Generator().manual_seed(2))
+    dout = torch.zeros_like(q)
+    dout[rows] = dout_d
+    rq, rk, rv, _ = orc.hstu_mha_bwd(N, 0.25, q, k, v, offs, dout, dtype=torch.float64)
+    qd = q[rows].clone().requires_grad_(True)
+    kk, vv = k.clone().requires_grad_(True), v.clone().requires_grad_(True)
+    orc.cached_hstu_mha(N, 0.25, qd, kk, vv, offs).backward(dout_d)
+    assert torch.allclose(qd.grad, rq[rows]) and torch.allclose(kk.grad, rk) and torch.allclose(vv.grad, rv)
