@@ -12,8 +12,8 @@ over the whole batch, inputs resident in HBM.  value = causal-effective FLOPs
 (14*D*H*P, P = sum L(L+1)/2) per second.  Also reported: the same step without
 the bias (the reference's attention has none) and on bf16 inputs, the output
 block's LN * U * dropout kernels (GB/s against HBM), one whole HSTU layer
-forward + backward in FP8 at config 3's shapes, and the
-targets-only delta-q attention.
+forward + backward in FP8 at config 3's shapes, the
+targets-only delta-q attention, and the full-FP8 backward's dO block quantizer.
 
     python bench.py --copy-calibration   # a 512 MiB device copy, for scaling
                                          # the FETCH_SIZE / WRITE_SIZE counters
@@ -70,7 +70,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--only", choices=("output_block", "layer", "delta"), default=None,
+    ap.add_argument("--only", choices=("output_block", "layer", "delta", "do_quant"), default=None,
                     help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
                     help="how the caches are evicted before each timed call (see CacheFlush)")
@@ -316,6 +316,32 @@ def delta_bench(torch, lengths, N, steps, warmup, flush):
             "algorithmic_bytes": {"fwd": fwd_bytes, "bwd": bwd_bytes}, "peak_GBps": HBM_GBS}
 
 
+def do_quant_bench(torch, lengths, N, steps, warmup, flush):
+    """The full-FP8 backward's dO block quantizer at config 3 tokens: bf16 dO
+    [T, 4, 128] -> e4m3 + E8 bytes.  HBM-bound: GB/s of algorithmic bytes."""
+    import hstu_amd
+
+    H, D = 4, 128
+    T = int(np.sum(lengths))
+    g = torch.Generator(device="cuda").manual_seed(17)
+    do = torch.randn(T, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    offs = torch.as_tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int64, device="cuda")
+
+    def run(ev):
+        if ev is not None:
+            ev[0].record()
+        hstu_amd.quantize_do_e4m3_blk(do, offs, N)
+        if ev is not None:
+            ev[1].record()
+
+    t, _ = _cold_events(torch, run, steps, warmup, flush)
+    m = float(np.median(t))
+    nbytes = 2 * T * H * D + T * H * D + T * H
+    return {"workload": "dO block e4m3 quantizer (pow2 scale per sequence, head, 32-token group), bf16 dO "
+                        "[%d, 4, 128]" % T, "us": round(m * 1e3, 1), "GBps": round(nbytes / (m * 1e-3) / 1e9, 1),
+            "algorithmic_bytes": nbytes, "peak_GBps": HBM_GBS}
+
+
 def layer_params(torch, E=512, H=4, D=128, seed=0):
     """Random-init STU layer parameters (bf16, modules/stu.py:274-328 shapes)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -461,6 +487,9 @@ def main():
     if args.only == "delta":
         print(json.dumps(delta_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
         return
+    if args.only == "do_quant":
+        print(json.dumps(do_quant_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
+        return
     w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
     wall_ms, st, parts = w8.run(args.steps, args.warmup, flush)
     total = w8.flops("step")
@@ -526,6 +555,7 @@ def main():
         res["layer"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush)
         torch.cuda.empty_cache()
         res["delta"] = delta_bench(torch, lengths, N, args.steps, 3, flush)
+        res["do_quant"] = do_quant_bench(torch, lengths, N, args.steps, 3, flush)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(lengths, H, D, N, args.cpu_seconds)

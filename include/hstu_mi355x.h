@@ -34,6 +34,7 @@ extern "C" {
 /* input element types */
 #define HSTU_DTYPE_BF16 0
 #define HSTU_DTYPE_FP8_E4M3 1
+#define HSTU_DTYPE_FP32 2 /* only where an entry point says so */
 
 /* error codes beyond hipError_t (all negative) */
 #define HSTU_E_BAD_ARG (-1)
@@ -280,6 +281,24 @@ int hstu_delta_attn_bwd(int dtype, int q_dtype, const void* dout, int64_t dout_r
                         float alpha, const int* num_targets, int max_attn_len, int contextual_seq_len,
                         void* dq, void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride,
                         int64_t dv_row_stride, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Block e4m3 quantization of the attention's upstream gradient (the input of
+ * the full-FP8 backward): dout [T, H, D] bf16 (dtype HSTU_DTYPE_BF16) or fp32
+ * (HSTU_DTYPE_FP32), row stride dout_row_stride elements, 16-byte aligned.
+ * One power-of-two scale per (sequence, head, token group), the groups being
+ * tokens p % 16 < 8 and p % 16 >= 8 of each 64-token tile of a sequence:
+ * e = floor(log2(448 / amax)) from the fp32 bits, clamped to [-60, 60] (60 for
+ * a subnormal amax, 0 for an all-zero group); dout_e4m3 [T, H, D] contiguous
+ * = e4m3(dout * 2^e); e8 [T, H] uint8 = 127 - e.  Tiles cover the first
+ * ceil(max_seq_len / 64) * 64 tokens of each sequence (max_seq_len >= every
+ * length).  H * D in {128, 256, 512}, D in {64, 128}.
+ * Replaces: quantize_do_e4m3_blk, ops/flydsl/hstu_do_fp8.py:95-121
+ *           (kernel _blk_kernel :42-86, contract :16-38).
+ */
+int hstu_quantize_do_e4m3_blk(int dtype, const void* dout, int64_t dout_row_stride, const int64_t* seq_offsets,
+                              int B, int H, int D, int max_seq_len, void* dout_e4m3, void* e8,
+                              hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
 HSTU_DTYPE_BF16 = 0
 HSTU_DTYPE_FP8_E4M3 = 1
+HSTU_DTYPE_FP32 = 2
 HSTU_E_BAD_ARG = -1
 HSTU_E_UNSUPPORTED = -2
 
@@ -41,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "hstu_delta_attn_workspace_bytes",
     "hstu_delta_attn_fwd",
     "hstu_delta_attn_bwd",
+    "hstu_quantize_do_e4m3_blk",
 )
 
 
@@ -104,6 +106,7 @@ _SIGNATURES = {
         [_i32, _i32, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _f32, _f32, _vp, _i32, _i32, _i32, _i32,
          _i32, _f32, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     ),
+    "hstu_quantize_do_e4m3_blk": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
     "hstu_ln_mul_bwd": (
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,

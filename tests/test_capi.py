@@ -171,3 +171,23 @@ def test_delta_entry_points_reject_before_launch():
     args = [1, 1, X, 512, X, X, X, 512, 512, 512, 1.0, 1.0, 1.0, W, 8, 4, 128, 1024, 5, 0.1, None, 0, 0, X, X, X,
             512, 512, 512, W, wsq(8, 4, 128, 1024, 5), None]
     assert bwd(*args) == lib.HSTU_E_UNSUPPORTED  # more than 4 delta rows per sequence
+
+
+def test_do_quantizer_rejects_before_launch():
+    import hstu_amd._lib as lib
+
+    q = lib.fn("hstu_quantize_do_e4m3_blk")
+    X, W = 4096, 8192
+
+    def f(**kw):
+        a = dict(dt=0, x=X, rs=512, offs=W, B=8, H=4, D=128, N=1024, y=X, e8=W, stream=None)
+        a.update(kw)
+        return q(*a.values())
+
+    assert f(dt=1) == lib.HSTU_E_BAD_ARG          # e4m3 input
+    assert f(rs=100) == lib.HSTU_E_BAD_ARG         # row stride below H * D
+    assert f(N=0) == lib.HSTU_E_BAD_ARG
+    assert f(D=96, rs=384) == lib.HSTU_E_UNSUPPORTED
+    assert f(H=8, rs=1024) == lib.HSTU_E_UNSUPPORTED  # H * D = 1024
+    assert f(x=X + 8) == lib.HSTU_E_UNSUPPORTED    # rows read as 16-byte pieces
+    assert f(B=0) == 0
