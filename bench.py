@@ -70,7 +70,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--only", choices=("output_block", "layer", "delta", "do_quant"), default=None,
+    ap.add_argument("--only", choices=("output_block", "layer", "layer_fp8_dgrad", "delta", "do_quant"), default=None,
                     help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
                     help="how the caches are evicted before each timed call (see CacheFlush)")
@@ -354,14 +354,21 @@ def layer_params(torch, E=512, H=4, D=128, seed=0):
     return {k: v.to(torch.bfloat16).requires_grad_(True) for k, v in p.items()}
 
 
-def layer_bench(torch, lengths, N, steps, warmup, flush):
+def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     """one whole HSTU layer in FP8, forward + backward, at
     config 3's shapes (T = 162 251, N = 4096, E = 512, H = 4, D = 128), with
     the relative bias and output dropout 0.3 (mask16).  Scales are calibrated
-    once from the data (amax * 1.25 / 448) before timing."""
+    once from the data (amax * 1.25 / 448) before timing.  fp8_dgrad: the
+    output projection's dgrad in FP8 (e5m2 dY, DLRM_HSTU_FP8_BWD=1), with
+    enough warm-up steps for its delayed scale to publish."""
     import hstu_amd
+    import hstu_amd.bwd_fp8 as bwd_fp8
 
     os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
+    os.environ["DLRM_HSTU_FP8_BWD"] = "1" if fp8_dgrad else "0"
+    bwd_fp8.reset_sites()
+    if fp8_dgrad:
+        warmup = max(warmup, 5)
     E, H, D = 512, 4, 128
     T = int(np.sum(lengths))
     g = torch.Generator(device="cuda").manual_seed(21)
@@ -392,13 +399,16 @@ def layer_bench(torch, lengths, N, steps, warmup, flush):
             ev[2].record()
 
     tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
+    os.environ["DLRM_HSTU_FP8_BWD"] = "0"
+    bwd_fp8.reset_sites()
     m = float(np.median(tot))
     P = causal_pairs(lengths)
     gemm_fwd = 2 * T * E * (2 * H * 2 * D) + 2 * T * (3 * H * D) * E
     flops = 3 * gemm_fwd + 14 * D * H * P
     return {"workload": "BASELINE config 5: HSTU layer fwd+bwd in FP8 (LN -> FP8 UVQK GEMM -> FP8 attention with "
-                        "bias -> LN(attn)*silu(u)*dropout -> FP8 out-proj + residual; bf16 dgrad/wgrad), "
-                        "config 3 shapes, E=512",
+                        "bias -> LN(attn)*silu(u)*dropout -> FP8 out-proj + residual; %s), "
+                        "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj dgrad, bf16 other dgrad/wgrad" if fp8_dgrad
+                                                    else "bf16 dgrad/wgrad"),
             "T": T, "ms_per_step": round(m, 4), "fwd_ms": round(float(np.median(tf)), 4),
             "bwd_ms": round(float(np.median(tb)), 4),
             "p10": round(float(np.percentile(tot, 10)), 4), "p90": round(float(np.percentile(tot, 90)), 4),
@@ -481,8 +491,9 @@ def main():
     if args.only == "output_block":
         print(json.dumps(output_block_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
         return
-    if args.only == "layer":
-        print(json.dumps(layer_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
+    if args.only in ("layer", "layer_fp8_dgrad"):
+        print(json.dumps(layer_bench(torch, lengths, N, args.steps, args.warmup, flush,
+                                     fp8_dgrad=args.only == "layer_fp8_dgrad")), flush=True)
         return
     if args.only == "delta":
         print(json.dumps(delta_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
@@ -553,6 +564,7 @@ def main():
         res["output_block"] = output_block_bench(torch, int(np.sum(lengths)), max(args.steps // 2, 5), 2, flush)
         torch.cuda.empty_cache()
         res["layer"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush)
+        res["layer_fp8_dgrad"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush, fp8_dgrad=True)
         torch.cuda.empty_cache()
         res["delta"] = delta_bench(torch, lengths, N, args.steps, 3, flush)
         res["do_quant"] = do_quant_bench(torch, lengths, N, args.steps, 3, flush)

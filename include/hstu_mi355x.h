@@ -35,6 +35,7 @@ extern "C" {
 #define HSTU_DTYPE_BF16 0
 #define HSTU_DTYPE_FP8_E4M3 1
 #define HSTU_DTYPE_FP32 2 /* only where an entry point says so */
+#define HSTU_DTYPE_FP8_E5M2 3 /* only where an entry point says so */
 
 /* error codes beyond hipError_t (all negative) */
 #define HSTU_E_BAD_ARG (-1)
@@ -166,6 +167,32 @@ int hstu_fp8_gemm_rowcol(const void* A, int64_t lda, const void* W, int64_t ldw,
                          void* C, int64_t ldc, int out_dtype, const float* out_scale,
                          int M, int N, int K, int silu_begin, int silu_end,
                          hipStream_t stream);
+
+/*
+ * The same GEMM with the A format explicit: a_dtype HSTU_DTYPE_FP8_E4M3 is
+ * hstu_fp8_gemm_rowcol; HSTU_DTYPE_FP8_E5M2 takes A in e5m2 (a backward
+ * gradient) against the e4m3 W, bf16 output, no residual -- the FP8 dgrad
+ * dX = dY8 . W8^T with per-tensor scales.
+ * Replaces: output_projection_dgrad's torch._scaled_mm(gradient_e5m2, weight_e4m3.t(),
+ *           scale_a, scale_b, out_dtype=bf16), ops/triton/bwd_fp8.py:1347-1395.
+ */
+int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void* W, int64_t ldw, const float* a_scale,
+                  int a_scale_mode, const float* w_scale, int w_scale_mode, const void* bias, const void* residual,
+                  int64_t ldr, void* C, int64_t ldc, int out_dtype, const float* out_scale, int M, int N, int K,
+                  int silu_begin, int silu_end, hipStream_t stream);
+
+/*
+ * One-pass FP8 cast with the input's amax: out[i] = fp8(clamp(x[i] *
+ * inv_scale[0], +-limit)) (out_dtype e4m3 or e5m2, round to nearest even)
+ * over n contiguous bf16 / fp32 elements (n % 32 == 0, 16-byte aligned), and
+ * partial_amax[b] = max |x| over elements [8192 b, 8192 (b + 1)), before
+ * scaling; hstu_cast_fp8_amax_partials(n) partials.  inv_scale stays on
+ * the device (no host sync).
+ * Replaces: quantize_row_major / _quantize_amax_kernel, ops/triton/bwd_fp8.py:194-217, 827-866.
+ */
+int64_t hstu_cast_fp8_amax_partials(int64_t n);
+int hstu_cast_fp8_amax(int in_dtype, const void* x, int64_t n, const float* inv_scale, int out_dtype, float limit,
+                       void* out, float* partial_amax, int64_t partial_count, hipStream_t stream);
 
 /*
  * e4m3 quantization of bf16 rows in groups of `group` consecutive elements:

@@ -230,6 +230,8 @@ struct AttnParams {
   const int* sched_count;  // [8] items per XCD
   int sched_cap;
   int blocks_per_seq;  // ceil(N / 128)
+  uint8_t* ds_ws;           // workspace: bf16 dS tiles written by dK/dV, read by dQ (causal masks)
+  const int64_t* ds_base;   // workspace: per-sequence exclusive prefix of ds_tiles(L) [B + 1]
 };
 
 struct SeqCtx {
@@ -262,6 +264,27 @@ __device__ __forceinline__ bool seq_ctx(const AttnParams& p, bool heavy_last, Se
   c.blk = heavy_last ? nb - 1 - m : m;
   return true;
 }
+// dS tiles.  For the causal mask the dK/dV kernel computes dS for key block
+// kb (128 keys) against query tiles qt = 4 kb .. ceil(L/32) - 1 (32 queries);
+// it stores each such (kb, qt) tile, bf16, for the dQ kernel to contract
+// with K instead of recomputing S, dP and the SiLU derivative.  Tiles of one
+// (sequence, head) are consecutive in kb-major order, so tile (kb, qt) is at
+// kb * QT - 2 kb^2 - 2 kb + qt, and a sequence has ds_tiles(L) of them.
+// Inside a tile (8 KiB): [wave w][key sub-tile kt][lane] 16-byte packs, the
+// A operand of dK/dV's dK MFMA: keys 32 w + 16 kt + li, queries
+// {4g .. 4g+3, 16+4g .. 16+4g+3} of the tile (times the query's e4m3 scale).
+constexpr int kDsTileBytes = 8192;
+__host__ __device__ inline int64_t ds_tiles(int64_t L) {
+  const int64_t nb = (L + 127) / 128, qt = (L + 31) / 32;
+  return nb * qt - 2 * nb * nb + 2 * nb;
+}
+__device__ __forceinline__ uint8_t* ds_tile(const AttnParams& p, const SeqCtx& c, int kb, int qt) {
+  const int64_t QT = (c.L + 31) / 32;
+  const int64_t idx = p.ds_base[c.b] * p.H + (int64_t)c.h * ds_tiles(c.L) + (int64_t)kb * QT -
+                      2 * (int64_t)kb * kb - 2 * (int64_t)kb + qt;
+  return p.ds_ws + idx * kDsTileBytes;
+}
+
 __device__ __forceinline__ MaskCtx mask_ctx(const AttnParams& p, const SeqCtx& c) {
   MaskCtx m;
   m.L = c.L;
@@ -960,6 +983,233 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
 }
 
 // ---------------------------------------------------------------------
+// dQ from the stored dS tiles (causal masks).  Block = 128 queries (one
+// 32-query tile per wave), key steps of 64.  No recompute: the block stages
+// K (bf16; e4m3 rows times their key scale, rounded to bf16), each wave
+// stages its own dS tile rows, and both are read transposed so that
+// dQ^T = K^T . dS^T comes out of 16x16x32 bf16 MFMAs with a lane holding
+// four consecutive d of one query (8-byte stores).  The bias gradient is
+// taken from the dS values the wave holds in registers (C-fragment layout:
+// query 4g+r, key li), as the recomputing dQ kernel does.
+// ---------------------------------------------------------------------
+template <int D>
+struct DqWsCfg {
+  static constexpr int BM = 128, BNK = 64, DT = D / 16;
+  static constexpr int P = BwdPitch<D>::P;  // K rows [key][d], bf16
+  static constexpr int PS = 96;             // dS rows [key][32 queries], bf16 (64 B + pad, conflict-free tr reads)
+  static constexpr int K_OFF = 0;
+  static constexpr int DS_OFF = K_OFF + BNK * P;
+  static constexpr int DS_WAVE = BNK * PS;
+  static constexpr int HIST_OFF = DS_OFF + 4 * DS_WAVE;
+  static int lds(bool bias, int R) { return HIST_OFF + (bias ? R * 4 : 0); }
+};
+
+template <int D, bool FP8, bool BIAS>
+__global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_ws_kernel(AttnParams p) {
+  using C = DqWsCfg<D>;
+  constexpr int ES = FP8 ? 1 : 2;
+  constexpr int KCH = D * ES / 16;                 // 16-byte K chunks per row
+  constexpr int KIT = C::BNK * KCH / kThreads;     // K chunks per thread per step
+  static_assert(C::BNK * KCH % kThreads == 0, "K staging");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/true, sc)) return;
+  const int L = sc.L, h = sc.h;
+  const int m0 = sc.blk * C::BM;
+  if (m0 >= L) return;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int qw0 = m0 + wave * 32;  // the wave's query tile
+  const bool wave_active = qw0 < L;
+  const int qt = qw0 / 32;
+  const int n_end = min(m0 + C::BM, L);
+  const int nsteps = (n_end + C::BNK - 1) / C::BNK;
+
+  const uint32_t krs = (uint32_t)(p.k_rs * ES);
+  const BufRsrc krsrc = make_rsrc(p.k + (sc.start * p.k_rs + (int64_t)h * D) * ES,
+                                  (uint32_t)(L > 0 ? (L - 1) * krs + D * ES : 0));
+  const int R1 = p.bias_R - 1;
+  float* hist = (float*)(smem + C::HIST_OFF);
+  float* dbias_copy = BIAS ? p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1)
+                           : nullptr;
+  if constexpr (BIAS) {
+    for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
+  }
+  // 1 / q_scale of the lane's queries: for the dQ store (query qs*16 + li) and
+  // for the bias gradient (queries qs*16 + 4g + r of the dS fragments)
+  float inv_st[2] = {1.f, 1.f}, inv_db[2][4];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) inv_db[qs][r] = 1.f;
+  if constexpr (FP8) {
+    auto qsc = [&](int row) {
+      return row < L ? 1.f / p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 1.f;
+    };
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      inv_st[qs] = qsc(qw0 + 16 * qs + li);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) inv_db[qs][r] = qsc(qw0 + 16 * qs + 4 * g + r);
+    }
+  }
+
+  f32x4 acc[C::DT][2];
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) acc[dt][0] = acc[dt][1] = zero4();
+
+  // staged registers of one step: K chunks (+ key scales) and this wave's 4 dS packs
+  u32x4 kraw[KIT];
+  float ksc[KIT];
+  u32x4 dsp[4] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  auto load = [&](int step) {
+    const int k0 = step * C::BNK;
+#pragma unroll
+    for (int i = 0; i < KIT; ++i) {
+      const int item = tid + kThreads * i, row = item / KCH, ch = item % KCH;
+      kraw[i] = buf_ld128(krsrc, (uint32_t)(row * krs + ch * 16), (uint32_t)(k0 * krs));
+      if constexpr (FP8) ksc[i] = k0 + row < L ? p.k_scale[(sc.start + k0 + row) * p.s_rs + h * p.s_hs] : 0.f;
+    }
+    if (wave_active) {
+      const int kb = step >> 1, c = step & 1;
+      const uint8_t* t = ds_tile(p, sc, kb, qt) + ((2 * c) * 2 * 64 + lane) * 16;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dsp[j] = *(const u32x4*)(t + j * 64 * 16);  // (w' = 2c + j/2, kt = j%2)
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < KIT; ++i) {
+      const int item = tid + kThreads * i, row = item / KCH, ch = item % KCH;
+      uint8_t* dst = smem + C::K_OFF + row * C::P + ch * 16 * (FP8 ? 2 : 1);
+      if constexpr (FP8) {
+        const u32x4 w = kraw[i];
+        const u32x2 a = fp8x4_to_bf16x4(w[0], ksc[i]), b = fp8x4_to_bf16x4(w[1], ksc[i]);
+        const u32x2 c = fp8x4_to_bf16x4(w[2], ksc[i]), d = fp8x4_to_bf16x4(w[3], ksc[i]);
+        *(u32x4*)dst = u32x4{a[0], a[1], b[0], b[1]};
+        *(u32x4*)(dst + 16) = u32x4{c[0], c[1], d[0], d[1]};
+      } else {
+        *(u32x4*)dst = kraw[i];
+      }
+    }
+    // the wave's dS rows: key 32 (j/2) + 16 (j%2) + li, queries 4g..4g+3 and 16+4g..16+4g+3
+    uint8_t* db = smem + C::DS_OFF + wave * C::DS_WAVE;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint8_t* row = db + (32 * (j >> 1) + 16 * (j & 1) + li) * C::PS;
+      *(u32x2*)(row + 8 * g) = u32x2{dsp[j][0], dsp[j][1]};
+      *(u32x2*)(row + 32 + 8 * g) = u32x2{dsp[j][2], dsp[j][3]};
+    }
+  };
+
+  // transposed reads (ds_read_b64_tr_b16): lane (li, g) starts at row 4g + li/4, byte (li%4)*8
+  const int trk = (4 * g + (li >> 2)) * C::P + (li & 3) * 8;   // K tile
+  const int trs = (4 * g + (li >> 2)) * C::PS + (li & 3) * 8;  // dS rows
+  float dclamp = 0.f;
+
+  load(0);
+  store();
+  __syncthreads();
+  for (int step = 0; step < nsteps; ++step) {
+    const int k0 = step * C::BNK;
+    u32x4 cur[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cur[j] = dsp[j];
+    if (step + 1 < nsteps) load(step + 1);
+    if (wave_active && k0 <= qw0 + 31) {
+      if constexpr (BIAS) {
+        // bias gradient from the held dS: 32x32 sub-tile per w' (keys k0 + 32wl ..)
+#pragma unroll
+        for (int wl = 0; wl < 2; ++wl) {
+          const int base = qw0 - (k0 + 32 * wl);  // i - j of (query 0, key 0) of the sub-tile
+          if (base + 31 < 0) continue;           // entirely above the diagonal (all zero)
+          float v[2][2][4];                      // [qs][kt][r]
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            const u32x4 w = cur[2 * wl + kt];
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs) {
+              v[qs][kt][0] = __builtin_bit_cast(float, w[2 * qs] << 16) * inv_db[qs][0];
+              v[qs][kt][1] = __builtin_bit_cast(float, w[2 * qs] & 0xffff0000u) * inv_db[qs][1];
+              v[qs][kt][2] = __builtin_bit_cast(float, w[2 * qs + 1] << 16) * inv_db[qs][2];
+              v[qs][kt][3] = __builtin_bit_cast(float, w[2 * qs + 1] & 0xffff0000u) * inv_db[qs][3];
+            }
+          }
+          if (base - 31 >= R1) {  // every offset clamps
+#pragma unroll
+            for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+              for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dclamp += v[qs][kt][r];
+            continue;
+          }
+          float dacc[4] = {0.f, 0.f, 0.f, 0.f};
+          // rows = queries (16 qs + 4g + r), cols = keys (16 kt + li): shift kt - qs
+          diag_accumulate<0>(dacc, v[0][0]);
+          diag_accumulate<0>(dacc, v[1][1]);
+          diag_accumulate<1>(dacc, v[0][1]);
+          diag_accumulate<-1>(dacc, v[1][0]);
+          const float dv = diag_reduce(dacc, lane);
+          // this lane's diagonal col - row = li + 16 - 16g, i.e. offset i - j = base - that
+          const int off = base - (li + 16 - 16 * g);
+          if (off >= R1) dclamp += dv;
+          else if (off >= 0) atomicAdd(&hist[off], dv);
+        }
+      }
+      const uint8_t* kb = smem + C::K_OFF;
+      const uint8_t* dsb = smem + C::DS_OFF + wave * C::DS_WAVE;
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        if (k0 + 32 * c2 > qw0 + 31) break;  // keys entirely after the wave's queries
+        u32x4 bq[2];
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+          const uint8_t* q = dsb + trs + c2 * 32 * C::PS + qs * 32;
+          bq[qs] = cat_tr(lds_tr16(q), lds_tr16(q + 16 * C::PS));
+        }
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          const uint8_t* kp = kb + trk + c2 * 32 * C::P + dt * 32;
+          const u32x4 ak = cat_tr(lds_tr16(kp), lds_tr16(kp + 16 * C::P));
+          acc[dt][0] = mfma_bf16(ak, bq[0], acc[dt][0]);
+          acc[dt][1] = mfma_bf16(ak, bq[1], acc[dt][1]);
+        }
+      }
+    }
+    __syncthreads();
+    if (step + 1 < nsteps) {
+      store();
+      __syncthreads();
+    }
+  }
+
+  if constexpr (BIAS) {
+    if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
+    __syncthreads();
+    float* dst = dbias_copy + R1;
+    for (int i = tid; i < p.bias_R; i += kThreads) {
+      const float v = hist[i];
+      if (v != 0.f) atomicAdd(&dst[i], v);
+    }
+  }
+
+  if (!wave_active) return;
+  const float fin = p.alpha * p.inv_n;
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int row = qw0 + 16 * qs + li;
+    if (row >= L) continue;
+    const float f = fin * inv_st[qs];
+    uint16_t* dst = p.dq + (sc.start + row) * p.dq_rs + (int64_t)h * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+      *(u32x2*)(dst + dt * 16) = u32x2{pack_bf16(acc[dt][qs][0] * f, acc[dt][qs][1] * f),
+                                       pack_bf16(acc[dt][qs][2] * f, acc[dt][qs][3] * f)};
+  }
+}
+
+// ---------------------------------------------------------------------
 // dK / dV.  Block = 128 keys (32 per wave), query tiles of 32.
 //   S = Q.K^T, dP = dO.V^T (C fragments: query 4g+r, key li)
 //   dV += P^T.dO, dK += dS^T.Q
@@ -1165,6 +1415,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
       issue(m0 + (C::NSTAGE - 1) * C::BMQ, smem + nxt * C::STAGE);
     }
 
+    u32x4 ds_out[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};  // this tile's dS for the dQ kernel
     if (wave_active && (GENERIC || m0 + C::BMQ - 1 >= kw0)) {
       f32x4 s[C::QS][2], dp[C::QS][2];
 #pragma unroll
@@ -1223,6 +1474,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
           dsa[kt][qs * 2 + 1] = pack_bf16(dsv[2], dsv[3]);
         }
       }
+      if constexpr (!GENERIC) {
+        ds_out[0] = dsa[0];
+        ds_out[1] = dsa[1];
+      }
       // ---- dV += P^T . dO, dK += dS^T . Q  (dO and Q rows read transposed,
       // one d-step ahead of their MFMAs)
       auto tr_pair = [&](int off) {
@@ -1246,6 +1501,13 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
     wait_vm_le<(C::NSTAGE - 2) * C::CNT>();
     __syncthreads();
     cur = cur + 1 == C::NSTAGE ? 0 : cur + 1;
+    if constexpr (!GENERIC) {
+      // after the wait: these stores are the newest vector-memory operations,
+      // so the next tile's vmcnt bound still covers its own loads first
+      uint8_t* dst = ds_tile(p, sc, sc.blk, m0 / C::BMQ) + ((wave * 2) * 64 + lane) * 16;
+      *(u32x4*)dst = ds_out[0];
+      *(u32x4*)(dst + 64 * 16) = ds_out[1];
+    }
   };
 
   // Tiles [0, t_mask) touch the diagonal of some wave's keys (queries below
@@ -1430,10 +1692,14 @@ int64_t sched_bytes(int B, int H) { return align256(sched_ints(B, H) * 4); }
 // Forward workspace: the block schedule.
 int64_t fwd_workspace_bytes(int B, int H) { return sched_bytes(B, H); }
 // Backward workspace: [block schedule][pre-clamped bias rows][bf16 copy of
-// e4m3 q][partial bias gradients]; byte offsets of each part.
+// e4m3 q][partial bias gradients][dS tile prefix][dS tiles]; byte offsets of
+// each part.  The dS tiles are sized by a bound that needs no lengths:
+// ds_tiles(L) <= 2 nb (nb + 1) with nb = ceil(L / 128) <= ceil(N / 128), so
+// the sum over sequences is at most 2 (ceil(N/128) + 1) (ceil(T/128) + B).
 struct BwdWs {
-  int64_t sched, bias_ext, q16, part, total;
+  int64_t sched, bias_ext, q16, part, ds_base, ds, total;
 };
+int64_t ds_tiles_bound(int64_t T, int B, int N) { return 2 * ((N + 127) / 128 + 1) * ((T + 127) / 128 + B); }
 BwdWs bwd_ws(int dtype, int64_t T, int B, int H, int D, int N, int R) {
   BwdWs w;
   int64_t o = 0;
@@ -1445,10 +1711,40 @@ BwdWs bwd_ws(int dtype, int64_t T, int B, int H, int D, int N, int R) {
   if (dtype == HSTU_DTYPE_FP8_E4M3) o += align256(T * H * D * 2);
   w.part = o;
   if (R > 0) o += dbias_part_bytes(H, R);
+  w.ds_base = o;
+  o += align256(((int64_t)B + 1) * 8);
+  w.ds = o;
+  o += ds_tiles_bound(T, B, N) * H * kDsTileBytes;
   w.total = o;
   return w;
 }
 
+
+// base[b] = sum over sequences b' < b of ds_tiles(min(length, N)); base[B] = the total.
+__global__ void __launch_bounds__(1024) ds_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base) {
+  __shared__ int64_t part[1024];
+  const int tid = threadIdx.x, per = (B + 1023) / 1024, b0 = tid * per;
+  auto tiles = [&](int b) { return ds_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); };
+  int64_t sum = 0;
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < B) sum += tiles(b0 + i);
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int64_t add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int64_t run = tid ? part[tid - 1] : 0;
+  for (int i = 0; i < per; ++i) {
+    if (b0 + i < B) {
+      base[b0 + i] = run;
+      run += tiles(b0 + i);
+    }
+  }
+  if (tid == 1023) base[B] = part[1023];
+}
 
 // dbias = inv_n * sum of the kDbiasCopies partial copies.
 __global__ void reduce_dbias(const float* part, int n, float inv_n, float* dbias) {
@@ -1658,6 +1954,13 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   uint8_t* ws_part = has_bias ? ws + wl.part : nullptr;
   e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)(ws + wl.sched), stream);
   if (e != hipSuccess) return (int)e;
+  if (!generic) {
+    // dS tiles pass from the dK/dV kernel to the dQ kernel through the workspace
+    p.ds_base = (const int64_t*)(ws + wl.ds_base);
+    p.ds_ws = ws + wl.ds;
+    hipLaunchKernelGGL(ds_tile_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
+                       (int64_t*)(ws + wl.ds_base));
+  }
   if (parts & kBwdDkdv) {
     if (has_bias) {
       p.bias_ext = (const float*)(ws + wl.bias_ext);
@@ -1689,7 +1992,15 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
       const int n = kDbiasCopies * H * (2 * bias_R - 1);
       hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 0.f);
     }
-    // dQ (+ bias gradient): 128-query blocks, longest key range first.
+    // dQ (+ bias gradient): 128-query blocks, longest key range first.  With
+    // the causal mask, from the dS tiles the dK/dV kernel stored.
+    if (!generic) {
+#define HSTU_DQW(DD, F8, BB) launch(hstu_bwd_dq_ws_kernel<DD, F8, BB>, DqWsCfg<DD>::lds(BB, bias_R), grid, p, stream)
+      if (dtype == HSTU_DTYPE_FP8_E4M3) e = has_bias ? HSTU_DQW(128, true, true) : HSTU_DQW(128, true, false);
+      else if (D == 128) e = has_bias ? HSTU_DQW(128, false, true) : HSTU_DQW(128, false, false);
+      else e = has_bias ? HSTU_DQW(64, false, true) : HSTU_DQW(64, false, false);
+#undef HSTU_DQW
+    } else {
     const int lds = DqCfg<128>::lds(has_bias, bias_R);
     const int lds64 = DqCfg<64>::lds(has_bias, bias_R);
 #define HSTU_DQ(DD, F8, G, BB) launch(hstu_bwd_dq_kernel<DD, F8, G, BB>, DD == 128 ? lds : lds64, grid, p, stream)
@@ -1703,6 +2014,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
     }
 #undef HSTU_DQ_B
 #undef HSTU_DQ
+    }
     if (e != hipSuccess) return (int)e;
     if (has_bias && dbias != nullptr) {
       const int n = H * (2 * bias_R - 1);

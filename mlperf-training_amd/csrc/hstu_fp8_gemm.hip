@@ -6,8 +6,9 @@
 //             silu_end) (the U slice); [+ residual[m][n]]; store bf16, or e4m3 of
 //             clamp(v / out_scale, +-448).
 //
-// A is [M, K] row-major e4m3 (per-tensor or per-row scale), W is [N, K]
-// row-major e4m3 (the transposed weight, per-tensor or per-column scale).
+// A is [M, K] row-major e4m3 -- or e5m2, for the backward's gradient operand --
+// (per-tensor or per-row scale), W is [N, K] row-major e4m3 (the transposed
+// weight, per-tensor or per-column scale).
 // Reference behaviour followed (paths relative to
 // recommendation_v4/hstu/generative_recommenders/):
 //   UVQK / VQK projection  ops/triton/triton_hstu_preprocess_and_attention.py:1257-1289
@@ -15,6 +16,8 @@
 //   K=1536 out-projection  ops/hip/k1536_fp8_addmm.cu:10-18 (bf16(acc*s + C))
 //   SiLU on U only         ops/hstu_compute.py:140
 //   quantizer              ops/triton/triton_fp8.py:396-413, 760-781 (scale = amax/448)
+//   FP8 backward dgrad     ops/triton/bwd_fp8.py:1347-1395 (e5m2 dY x e4m3 W^T, per-tensor scales)
+//   one-pass cast + amax   ops/triton/bwd_fp8.py:194-217, 827-866
 //
 // Design: workgroup tile 128 (M) x 128 (N), 4 waves as 2 x 2 of 64 x 64.  The
 // MFMA (v_mfma_f32_16x16x128_f8f6f4) is issued operand-swapped, W rows as the
@@ -68,7 +71,8 @@ constexpr int kCnt = 2 * GTile::PER_WAVE;    // load instructions per wave per s
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-template <bool E4M3_OUT, bool RESID>
+// A_BF8: A holds e5m2 (the MFMA's B operand format 1, bf8).
+template <bool E4M3_OUT, bool RESID, bool A_BF8>
 __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // XCD-contiguous tile order: workgroup i runs on XCD i % 8.
@@ -140,7 +144,12 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
       const uint8_t* r = buf + w_rd + ns * 16 * kPitch;
       const i32x8 aop = cat8(lds_ld128(r), lds_ld128(r + 64));
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) acc[ns][ms] = mfma_fp8(aop, bop[ms], acc[ns][ms]);
+      for (int ms = 0; ms < 4; ++ms) {
+        if constexpr (A_BF8)  // W rows e4m3 (format 0), A rows e5m2 (format 1)
+          acc[ns][ms] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop, bop[ms], acc[ns][ms], 0, 1, 0, 0, 0, 0);
+        else
+          acc[ns][ms] = mfma_fp8(aop, bop[ms], acc[ns][ms]);
+      }
     }
     wait_vm();
     __syncthreads();
@@ -253,6 +262,71 @@ __global__ void quantize_e4m3_kernel(const uint16_t* x, int64_t ldx, int rows, i
   }
 }
 
+// One-pass FP8 cast with the amax of the input: out = fp8(clamp(x * inv_scale,
+// +-limit)) (e4m3 or e5m2, RNE) over n contiguous elements, and per 8192-element
+// block the max |x| (before scaling) into partial[block].  A thread casts 32
+// consecutive elements: 4 (bf16) or 8 (fp32) 16-byte loads, two 16-byte stores.
+constexpr int kCastBlock = 8192;
+template <bool IN_F32, bool OUT_BF8>
+__global__ void __launch_bounds__(256) cast_fp8_amax_kernel(const uint8_t* __restrict__ x, int64_t n,
+                                                            const float* __restrict__ inv_scale, float limit,
+                                                            uint8_t* __restrict__ out, float* __restrict__ partial) {
+  constexpr int ES = IN_F32 ? 4 : 2, NL = 32 * ES / 16;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t e0 = (int64_t)blockIdx.x * kCastBlock + (int64_t)tid * 32;
+  u32x4 w[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t e = e0 + i * (16 / ES);
+    w[i] = e < n ? *(const u32x4*)(x + e * ES) : u32x4{0u, 0u, 0u, 0u};
+  }
+  const float s = inv_scale[0];
+  float amax = 0.f, v[32];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = w[i][j];
+      if constexpr (IN_F32) {
+        v[4 * i + j] = __builtin_bit_cast(float, u);
+      } else {
+        v[8 * i + 2 * j] = __builtin_bit_cast(float, u << 16);
+        v[8 * i + 2 * j + 1] = __builtin_bit_cast(float, u & 0xffff0000u);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 32; ++k) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[k]));
+  if (e0 < n) {
+    uint32_t o[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float c[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) c[r] = __builtin_fminf(__builtin_fmaxf(v[4 * q + r] * s, -limit), limit);
+      int t;
+      if constexpr (OUT_BF8) {
+        t = __builtin_amdgcn_cvt_pk_bf8_f32(c[0], c[1], 0, false);
+        t = __builtin_amdgcn_cvt_pk_bf8_f32(c[2], c[3], t, true);
+      } else {
+        t = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+        t = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], t, true);
+      }
+      o[q] = (uint32_t)t;
+    }
+    // n % 32 == 0, so a thread's 32 elements are all in range or all out
+    *(u32x4*)(out + e0) = u32x4{o[0], o[1], o[2], o[3]};
+    *(u32x4*)(out + e0 + 16) = u32x4{o[4], o[5], o[6], o[7]};
+  }
+  // block max: wave reduction, then four waves through LDS
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  if (tid == 0) partial[blockIdx.x] = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+}
+
 hipError_t set_gemm_lds(const void* fn) {
   static std::mutex mu;
   static std::vector<const void*> done;
@@ -266,11 +340,12 @@ hipError_t set_gemm_lds(const void* fn) {
 
 }  // namespace
 
-extern "C" int hstu_fp8_gemm_rowcol(const void* A, int64_t lda, const void* W, int64_t ldw, const float* a_scale,
-                                    int a_scale_mode, const float* w_scale, int w_scale_mode, const void* bias,
-                                    const void* residual, int64_t ldr, void* C, int64_t ldc, int out_dtype,
-                                    const float* out_scale, int M, int N, int K, int silu_begin, int silu_end,
-                                    hipStream_t stream) {
+extern "C" int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
+                             const float* a_scale, int a_scale_mode, const float* w_scale, int w_scale_mode,
+                             const void* bias, const void* residual, int64_t ldr, void* C, int64_t ldc,
+                             int out_dtype, const float* out_scale, int M, int N, int K, int silu_begin,
+                             int silu_end, hipStream_t stream) {
+  if (a_dtype != HSTU_DTYPE_FP8_E4M3 && a_dtype != HSTU_DTYPE_FP8_E5M2) return HSTU_E_BAD_ARG;
   if (M < 0 || N <= 0 || K <= 0 || N % kBN != 0 || K % kBK != 0 || !A || !W || !C || !a_scale || !w_scale)
     return HSTU_E_BAD_ARG;
   if (lda < K || ldw < K || lda % 16 != 0 || ldw % 16 != 0 || ((uintptr_t)A | (uintptr_t)W) % 16 != 0)
@@ -306,15 +381,27 @@ extern "C" int hstu_fp8_gemm_rowcol(const void* A, int64_t lda, const void* W, i
   const int total = p.tiles_m * p.tiles_n;
   const int grid = (total + 7) / 8 * 8;
   void (*kern)(GemmParams);
-  if (out_dtype == HSTU_DTYPE_FP8_E4M3) {
-    kern = residual ? fp8_gemm_kernel<true, true> : fp8_gemm_kernel<true, false>;
+  if (a_dtype == HSTU_DTYPE_FP8_E5M2) {
+    if (out_dtype != HSTU_DTYPE_BF16 || residual) return HSTU_E_UNSUPPORTED;  // the dgrad form only
+    kern = fp8_gemm_kernel<false, false, true>;
+  } else if (out_dtype == HSTU_DTYPE_FP8_E4M3) {
+    kern = residual ? fp8_gemm_kernel<true, true, false> : fp8_gemm_kernel<true, false, false>;
   } else {
-    kern = residual ? fp8_gemm_kernel<false, true> : fp8_gemm_kernel<false, false>;
+    kern = residual ? fp8_gemm_kernel<false, true, false> : fp8_gemm_kernel<false, false, false>;
   }
   hipError_t e = set_gemm_lds((const void*)kern);
   if (e != hipSuccess) return (int)e;
   void* args[] = {&p};
   return (int)hipLaunchKernel((const void*)kern, dim3(grid), dim3(kThreads), args, (size_t)kGemmLds, stream);
+}
+
+extern "C" int hstu_fp8_gemm_rowcol(const void* A, int64_t lda, const void* W, int64_t ldw, const float* a_scale,
+                                    int a_scale_mode, const float* w_scale, int w_scale_mode, const void* bias,
+                                    const void* residual, int64_t ldr, void* C, int64_t ldc, int out_dtype,
+                                    const float* out_scale, int M, int N, int K, int silu_begin, int silu_end,
+                                    hipStream_t stream) {
+  return hstu_fp8_gemm(HSTU_DTYPE_FP8_E4M3, A, lda, W, ldw, a_scale, a_scale_mode, w_scale, w_scale_mode, bias,
+                       residual, ldr, C, ldc, out_dtype, out_scale, M, N, K, silu_begin, silu_end, stream);
 }
 
 extern "C" int hstu_quantize_e4m3_rows(const void* x, int64_t ldx, int rows, int cols, int group,
@@ -329,5 +416,29 @@ extern "C" int hstu_quantize_e4m3_rows(const void* x, int64_t ldx, int rows, int
   const int grid = (int)((groups + 3) / 4);
   hipLaunchKernelGGL(quantize_e4m3_kernel, dim3(grid), dim3(256), 0, stream, (const uint16_t*)x, ldx, rows, cols,
                      group, scale_in, (uint8_t*)out, ldo, scale_out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t hstu_cast_fp8_amax_partials(int64_t n) { return n < 0 ? -1 : (n + kCastBlock - 1) / kCastBlock; }
+
+extern "C" int hstu_cast_fp8_amax(int in_dtype, const void* x, int64_t n, const float* inv_scale, int out_dtype,
+                                  float limit, void* out, float* partial_amax, int64_t partial_count,
+                                  hipStream_t stream) {
+  if ((in_dtype != HSTU_DTYPE_BF16 && in_dtype != HSTU_DTYPE_FP32) ||
+      (out_dtype != HSTU_DTYPE_FP8_E4M3 && out_dtype != HSTU_DTYPE_FP8_E5M2) || n < 0 || !x || !inv_scale || !out ||
+      !partial_amax || !(limit > 0.f))
+    return HSTU_E_BAD_ARG;
+  if (partial_count < hstu_cast_fp8_amax_partials(n)) return HSTU_E_BAD_ARG;
+  if (n % 32 != 0 || (uintptr_t)x % 16 || (uintptr_t)out % 16) return HSTU_E_UNSUPPORTED;
+  if (n == 0) return 0;
+  const int64_t grid = hstu_cast_fp8_amax_partials(n);
+  if (grid >= ((int64_t)1 << 31)) return HSTU_E_UNSUPPORTED;
+  const bool f32 = in_dtype == HSTU_DTYPE_FP32, bf8 = out_dtype == HSTU_DTYPE_FP8_E5M2;
+  auto* xp = (const uint8_t*)x;
+  auto* op = (uint8_t*)out;
+  if (f32 && bf8) hipLaunchKernelGGL((cast_fp8_amax_kernel<true, true>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
+  else if (f32) hipLaunchKernelGGL((cast_fp8_amax_kernel<true, false>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
+  else if (bf8) hipLaunchKernelGGL((cast_fp8_amax_kernel<false, true>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
+  else hipLaunchKernelGGL((cast_fp8_amax_kernel<false, false>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
   return (int)hipGetLastError();
 }

@@ -21,6 +21,7 @@ LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 HSTU_DTYPE_BF16 = 0
 HSTU_DTYPE_FP8_E4M3 = 1
 HSTU_DTYPE_FP32 = 2
+HSTU_DTYPE_FP8_E5M2 = 3
 HSTU_E_BAD_ARG = -1
 HSTU_E_UNSUPPORTED = -2
 
@@ -43,6 +44,9 @@ EXPORTED_SYMBOLS = (
     "hstu_delta_attn_fwd",
     "hstu_delta_attn_bwd",
     "hstu_quantize_do_e4m3_blk",
+    "hstu_fp8_gemm",
+    "hstu_cast_fp8_amax_partials",
+    "hstu_cast_fp8_amax",
 )
 
 
@@ -84,6 +88,13 @@ _SIGNATURES = {
         [_vp, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i32, _vp,
          _i32, _i32, _i32, _i32, _i32, _vp],
     ),
+    "hstu_fp8_gemm": (
+        _i32,
+        [_i32, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i32, _vp,
+         _i32, _i32, _i32, _i32, _i32, _vp],
+    ),
+    "hstu_cast_fp8_amax_partials": (_i64, [_i64]),
+    "hstu_cast_fp8_amax": (_i32, [_i32, _vp, _i64, _vp, _i32, _f32, _vp, _vp, _i64, _vp]),
     "hstu_quantize_e4m3_rows": (
         _i32,
         [_vp, _i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp],

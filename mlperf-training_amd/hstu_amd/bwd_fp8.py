@@ -1,0 +1,230 @@
+"""FP8 backward projection GEMMs: the e5m2-gradient output-projection dgrad and
+its delayed-scale controller, on this build's kernels (``hstu_cast_fp8_amax``,
+``hstu_fp8_gemm`` with an e5m2 A operand).
+
+Mirrors ``ops/triton/bwd_fp8.py`` (reference paths relative to
+``recommendation_v4/hstu/generative_recommenders/``):
+
+* ``quantize_row_major``        <- ``:827-866`` (one pass: cast at a device-side
+  inverse scale, clamp to the format's max, and the input's amax)
+* ``SiteScale``                 <- ``_SiteScale`` ``:869-1003`` (scale published
+  from the window amax times MARGIN / FP8_MAX, refreshed every REFRESH_CALLS)
+* ``quantize_gradient``         <- ``:1073-1154`` (None while warming up: the
+  caller runs bf16)
+* ``quantize_weight``           <- ``:1157-1189`` (e4m3 at unit margin)
+* ``output_projection_dgrad``   <- ``:1347-1395`` (dY_e5m2 . W_e4m3^T, bf16 out)
+
+Switches (the reference's names): ``DLRM_HSTU_FP8_BWD=1`` enables the path;
+``DLRM_HSTU_FP8_BWD_MARGIN`` (8), ``_REFRESH_CALLS`` (200), ``_WARMUP_CALLS``
+(4), ``_GRAD_FORMAT`` (e5m2 | e4m3).  They are read when a call needs them,
+so a process can switch the path on and off.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+
+E4M3 = torch.float8_e4m3fn
+E5M2 = torch.float8_e5m2
+E4M3_MAX = 448.0
+E5M2_MAX = 57344.0
+
+
+def enabled() -> bool:
+    return os.environ.get("DLRM_HSTU_FP8_BWD", "0") == "1"
+
+
+def _margin() -> float:
+    return float(os.environ.get("DLRM_HSTU_FP8_BWD_MARGIN", "8"))
+
+
+def _refresh_calls() -> int:
+    return max(1, int(os.environ.get("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "200")))
+
+
+def _warmup_calls() -> int:
+    return max(1, int(os.environ.get("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "4")))
+
+
+def grad_dtype_and_limit() -> Tuple[torch.dtype, float]:
+    fmt = os.environ.get("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e5m2").lower()
+    if fmt not in ("e5m2", "e4m3"):
+        raise ValueError(f"DLRM_HSTU_FP8_BWD_GRAD_FORMAT={fmt!r}")
+    return (E4M3, E4M3_MAX) if fmt == "e4m3" else (E5M2, E5M2_MAX)
+
+
+def _code(dtype: torch.dtype) -> int:
+    return {torch.bfloat16: _lib.HSTU_DTYPE_BF16, torch.float32: _lib.HSTU_DTYPE_FP32, E4M3: _lib.HSTU_DTYPE_FP8_E4M3,
+            E5M2: _lib.HSTU_DTYPE_FP8_E5M2}[dtype]
+
+
+def quantize_row_major(value: torch.Tensor, inv_scale: torch.Tensor, dtype: Optional[torch.dtype] = None,
+                       limit: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(fp8(clamp(value * inv_scale, +-limit)), amax(|value|)) in one pass;
+    the amax is of the input, before scaling."""
+    gdt, glim = grad_dtype_and_limit()
+    dtype = gdt if dtype is None else dtype
+    limit = glim if limit is None else limit
+    src = value.detach()
+    if src.dtype not in (torch.bfloat16, torch.float32):
+        src = src.float()
+    if not src.is_contiguous() or src.data_ptr() % 16:
+        src = src.contiguous()
+    n = src.numel()
+    out = torch.empty(src.shape, dtype=dtype, device=src.device)
+    if n % 32:
+        raise NotImplementedError("the FP8 cast takes a multiple of 32 elements")
+    parts = int(_lib.fn("hstu_cast_fp8_amax_partials")(n))
+    partial = torch.empty(max(parts, 1), dtype=torch.float32, device=src.device)
+    if n == 0:
+        return out, torch.zeros((), dtype=torch.float32, device=src.device)
+    inv = inv_scale.to(torch.float32).reshape(-1)[:1].contiguous()
+    st = _lib.fn("hstu_cast_fp8_amax")(
+        _code(src.dtype), src.data_ptr(), n, inv.data_ptr(), _code(dtype), float(limit), out.data_ptr(),
+        partial.data_ptr(), parts, torch.cuda.current_stream(src.device).cuda_stream)
+    _lib.check(st, "hstu_cast_fp8_amax")
+    return out, partial[:parts].amax()
+
+
+class SiteScale:
+    """One backward tensor's scale, held and published on the device.
+
+    ``scale`` dequantizes (fp8 value * scale = original), ``inv_scale`` is what
+    the cast multiplies by.  The window's amax accumulates in ``pending``.
+    """
+
+    def __init__(self, site: str, device: torch.device) -> None:
+        self.site = site
+        self.calls = 0
+        self.scale = torch.zeros(1, dtype=torch.float32, device=device)
+        self.inv_scale = torch.zeros(1, dtype=torch.float32, device=device)
+        self.pending = torch.zeros((), dtype=torch.float32, device=device)
+        self.clipped_windows = torch.zeros((), dtype=torch.int64, device=device)
+        self.published = False
+
+    def accumulate(self, amax: torch.Tensor) -> None:
+        torch.maximum(self.pending, amax, out=self.pending)
+
+    def publish(self) -> None:
+        """The window's amax becomes the next window's scale (clamped away
+        from zero so an all-zero window cannot publish an infinite inverse)."""
+        _, limit = grad_dtype_and_limit()
+        self.scale.copy_((self.pending.clamp_min(1.0e-30) * (_margin() / limit)).reshape(1))
+        self.inv_scale.copy_(1.0 / self.scale)
+        self.pending.zero_()
+        self.published = True
+
+    def note_clipping(self, amax: torch.Tensor) -> None:
+        _, limit = grad_dtype_and_limit()
+        self.clipped_windows += (amax > self.scale.reshape(()) * limit).to(torch.int64)
+
+
+_sites: Dict[str, SiteScale] = {}
+_layer_index: Dict[Tuple[str, int], int] = {}
+
+
+def reset_sites() -> None:
+    """Forget every site's state (tests, or a new run in the same process)."""
+    _sites.clear()
+    _layer_index.clear()
+
+
+def site_name(site: str, discriminator: Optional[int]) -> str:
+    """One layer's instance of a site, indexed in order of first appearance."""
+    if discriminator is None:
+        return site
+    key = (site, discriminator)
+    if key not in _layer_index:
+        _layer_index[key] = sum(1 for k in _layer_index if k[0] == site)
+    return f"{site}.L{_layer_index[key]}"
+
+
+def site_state(site: str, device: torch.device) -> SiteScale:
+    st = _sites.get(site)
+    if st is None:
+        st = _sites[site] = SiteScale(site, device)
+    return st
+
+
+def quantize_gradient(site: str, gradient: torch.Tensor, discriminator: Optional[int] = None,
+                      snapshot_decode_scale: bool = False) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """(fp8 gradient, dequantization scale) under the delayed-scale policy, or
+    None while the site warms up (the caller's signal to run bf16).
+
+    As in the reference, the returned scale is the site's scale tensor, which
+    a refresh on this call has already updated in place; with
+    ``snapshot_decode_scale`` it is a copy of the scale the payload was cast
+    with, taken before the refresh."""
+    if not enabled():
+        return None
+    if gradient.numel() == 0 or gradient.dtype not in (torch.bfloat16, torch.float32, torch.float16):
+        return None
+    state = site_state(site_name(site, discriminator), gradient.device)
+    state.calls += 1
+    if not state.published:
+        state.accumulate(gradient.detach().abs().amax().float())
+        if state.calls >= _warmup_calls():
+            state.publish()
+        return None
+    q, amax = quantize_row_major(gradient, state.inv_scale)
+    state.note_clipping(amax)
+    state.accumulate(amax)
+    decode = state.scale.clone() if snapshot_decode_scale else state.scale
+    if state.calls % _refresh_calls() == 0:
+        state.publish()
+    return q, decode
+
+
+def quantize_weight(weight: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """e4m3 at unit margin: scale = amax / 448 on the device, cast at 1 / scale."""
+    amax = weight.detach().abs().amax().float().clamp_min(1.0e-30)
+    scale = (amax / E4M3_MAX).reshape(1)
+    q, _ = quantize_row_major(weight, 1.0 / scale, dtype=E4M3, limit=E4M3_MAX)
+    return q, scale
+
+
+def _has_stable_identity(weight: torch.Tensor) -> bool:
+    return weight.is_leaf and weight.requires_grad
+
+
+def fp8_dgrad(grad8: torch.Tensor, grad_scale: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor,
+              out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """grad8 [M, K] (e5m2 or e4m3) . w8 [N, K]^T (e4m3) * grad_scale * w_scale -> bf16 [M, N]."""
+    if out_dtype != torch.bfloat16:
+        raise NotImplementedError("the FP8 dgrad writes bf16")
+    M, K = grad8.shape
+    N = w8.shape[0]
+    if w8.shape[1] != K or w8.dtype != E4M3:
+        raise ValueError("w8 must be e4m3 [N, K]")
+    g = grad8.contiguous()
+    w = w8.contiguous()
+    sa = grad_scale.to(torch.float32).reshape(-1)[:1].contiguous()
+    sb = w_scale.to(torch.float32).reshape(-1)[:1].contiguous()
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=g.device)
+    if M == 0:
+        return out
+    st = _lib.fn("hstu_fp8_gemm")(
+        _code(g.dtype), g.data_ptr(), K, w.data_ptr(), K, sa.data_ptr(), 0, sb.data_ptr(), 0, None, None, 0,
+        out.data_ptr(), N, _lib.HSTU_DTYPE_BF16, None, M, N, K, 0, 0, torch.cuda.current_stream(g.device).cuda_stream)
+    _lib.check(st, "hstu_fp8_gemm")
+    return out
+
+
+def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor) -> Optional[torch.Tensor]:
+    """``dy = gradient @ weight^T`` in FP8 (gradient [M, N_out], weight
+    [K_in, N_out] as stored by the layer), or None to fall back to bf16."""
+    if not enabled() or not _has_stable_identity(weight):
+        return None
+    if gradient.dim() != 2 or gradient.shape[-1] % 128 or weight.shape[0] % 128:
+        return None
+    quantized = quantize_gradient("output_projection", gradient, discriminator=weight.data_ptr())
+    if quantized is None:
+        return None
+    g8, gs = quantized
+    w8, ws = quantize_weight(weight)
+    return fp8_dgrad(g8, gs, w8, ws, gradient.dtype if gradient.dtype == torch.bfloat16 else torch.bfloat16)

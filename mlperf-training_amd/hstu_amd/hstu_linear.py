@@ -34,7 +34,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from . import _lib
+from . import _lib, bwd_fp8
 from .hstu_attention import HammerKernel
 from .pt_hstu_linear import pytorch_hstu_compute_output, pytorch_norm_mul_dropout
 
@@ -318,8 +318,9 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
     """``HSTUComputeOutputFunction`` (``triton_hstu_linear.py:5109-5900``),
     default (unfused-backward) contract: e4m3 LN output into the FP8 output
     projection when ``fp8_output_scale`` is given and y is recomputed in the
-    backward, bf16 otherwise; backward = bf16 dgrad, the LN * U * dropout
-    backward (recomputing y), bf16 wgrad."""
+    backward, bf16 otherwise; backward = dgrad (bf16, or e5m2 x e4m3 FP8 with
+    ``DLRM_HSTU_FP8_BWD=1`` once its scale is calibrated), the LN * U *
+    dropout backward (recomputing y), bf16 wgrad."""
 
     @staticmethod
     def forward(ctx, attn, u, x, norm_weight, norm_bias, output_weight, eps, dropout_ratio, training,
@@ -371,7 +372,11 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         mask = ctx.saved_tensors[i] if ctx.has_mask else None
         ratio, silu_u, concat_u, concat_x, act = ctx.cfg
         dout = dout.contiguous()
-        dy = torch.mm(dout, output_weight.to(dout.dtype).t())
+        # FP8 dgrad (DLRM_HSTU_FP8_BWD=1; triton_hstu_linear.py:5586-5588): None
+        # while the gradient's scale warms up, then e5m2 dout . e4m3 W^T
+        dy = bwd_fp8.output_projection_dgrad(dout, output_weight) if bwd_fp8.enabled() else None
+        if dy is None:
+            dy = torch.mm(dout, output_weight.to(dout.dtype).t())
         dattn, du, dw, db, y_re = _ln_bwd(dy, attn, u, norm_weight, norm_bias, mean, rstd, ratio, mask, silu_u,
                                           concat_u, concat_x, act, ctx.recompute, ctx.du_row_width)
         if y is None:

@@ -1,0 +1,183 @@
+"""FP8 backward projection arm (e5m2 output-projection dgrad): the oracle and
+the delayed-scale controller on the CPU, the one-pass cast (bit-exact), the
+e5m2 x e4m3 GEMM and the dgrad through the output block on the GPU.
+
+Tolerances: the cast and its amax are integer / exact results (equality);
+the GEMM against the fp64 product of the same fp8 operands: relative L2
+<= 4e-3 and max|err| <= 1e-2 max|ref| (bf16 output); the FP8 dgrad against
+the bf16 product: relative L2 <= 8e-2 (e5m2 keeps 2 mantissa bits), and the
+same bound for the output block's dattn / du."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hstu_bwd_fp8_oracle as O
+
+E5M2, E4M3 = torch.float8_e5m2, torch.float8_e4m3fn
+
+
+def _rel(ref, got):
+    ref, got = ref.double(), got.double()
+    return float((got - ref).norm() / ref.norm().clamp_min(1e-30))
+
+
+def test_oracle_cast_decode_bound_and_exact_powers():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4096, generator=g) * torch.exp(torch.randn(4096, generator=g) * 3)
+    for dtype, lim, mbits, sub in ((E5M2, 57344.0, 2, 2.0 ** -16), (E4M3, 448.0, 3, 2.0 ** -9)):
+        inv = 0.37
+        q, amax = O.cast_amax(x, inv, dtype, lim)
+        v = (x * torch.tensor(inv, dtype=torch.float32)).clamp(-lim, lim).double()
+        err = (q.double() - v).abs()
+        assert bool((err <= torch.maximum(v.abs() * 2.0 ** -(mbits + 1), torch.tensor(sub / 2))).all())
+        assert float(amax) == float(x.abs().max())
+        p2 = torch.tensor([2.0 ** k for k in range(-6, 8)])
+        qp, _ = O.cast_amax(p2, 1.0, dtype, lim)
+        assert torch.equal(qp.double(), p2.double())
+
+
+def test_oracle_published_scale_closed_form():
+    for amax in (1e-3, 0.5, 7.25, 3e4):
+        s = O.published_scale(amax, 8.0, 57344.0)
+        assert abs(amax / s - 57344.0 / 8.0) <= 1e-3 * 57344.0 / 8.0
+    assert O.published_scale(0.0, 8.0, 57344.0) > 0.0
+
+
+def test_controller_warmup_publish_refresh(monkeypatch):
+    """The delayed-scale policy on CPU tensors (the cast is the oracle's)."""
+    import hstu_amd.bwd_fp8 as B
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "2")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "3")
+    monkeypatch.setattr(B, "quantize_row_major",
+                        lambda v, inv, dtype=None, limit=None: O.cast_amax(v, float(inv.reshape(-1)[0]),
+                                                                            dtype or E5M2, limit or 57344.0))
+    B.reset_sites()
+    g = [torch.full((4, 128), float(a)) for a in (2.0, 3.0, 1.0, 9.0, 4.0, 1.0)]
+    assert B.quantize_gradient("site", g[0]) is None
+    assert B.quantize_gradient("site", g[1]) is None          # warm-up ends: publish max(2, 3)
+    st = B._sites["site"]
+    s0 = O.published_scale(3.0, 8.0, 57344.0)
+    assert st.published and float(st.scale) == pytest.approx(s0, rel=1e-6)
+    q, dec = B.quantize_gradient("site", g[2], snapshot_decode_scale=True)   # call 3: refresh
+    assert float(dec) == pytest.approx(s0, rel=1e-6)         # the scale it was cast with
+    assert float(q.float()[0, 0]) * s0 == pytest.approx(1.0, rel=0.13)
+    s1 = O.published_scale(1.0, 8.0, 57344.0)                 # window of call 3 only
+    assert float(st.scale) == pytest.approx(s1, rel=1e-6)
+    q4, dec4 = B.quantize_gradient("site", g[3])              # 9.0 > s1 * 57344 = 8: clipped
+    assert int(st.clipped_windows) == 1
+    assert float(dec4) == pytest.approx(s1, rel=1e-6)
+    _, dec5 = B.quantize_gradient("site", g[4])
+    q6, dec6 = B.quantize_gradient("site", g[5])              # call 6: refresh, default decode = new scale
+    assert float(dec6) == pytest.approx(O.published_scale(9.0, 8.0, 57344.0), rel=1e-6)
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "0")
+    assert B.quantize_gradient("site", g[0]) is None
+    B.reset_sites()
+
+
+def test_site_names_per_layer():
+    import hstu_amd.bwd_fp8 as B
+
+    B.reset_sites()
+    assert B.site_name("output_projection", 111) == "output_projection.L0"
+    assert B.site_name("output_projection", 222) == "output_projection.L1"
+    assert B.site_name("output_projection", 111) == "output_projection.L0"
+    assert B.site_name("x", None) == "x"
+    B.reset_sites()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dst,lim", [(E5M2, 57344.0), (E4M3, 448.0)])
+def test_cast_amax_bit_exact(hip_lib, src, dst, lim):
+    import hstu_amd.bwd_fp8 as B
+
+    g = torch.Generator().manual_seed(3)
+    n = 3 * 8192 + 96
+    x = torch.randn(n, generator=g) * torch.exp(torch.randn(n, generator=g) * 4)
+    x[:5] = torch.tensor([0.0, -0.0, 1e-30, 7e4, -9e4])   # zero, tiny, clipped both ways
+    x = x.to(src)
+    inv = torch.tensor([0.731], dtype=torch.float32)
+    q, amax = B.quantize_row_major(x.cuda(), inv.cuda(), dtype=dst, limit=lim)
+    wq, wamax = O.cast_amax(x, float(inv), dst, lim)
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+    assert float(amax) == float(wamax)
+
+
+@pytest.mark.gpu
+def test_e5m2_gemm_against_fp64(hip_lib):
+    import hstu_amd.bwd_fp8 as B
+
+    g = torch.Generator().manual_seed(5)
+    M, K, N = 300, 512, 1536
+    dy = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) / K ** 0.5
+    gs, ws = 1.0 / 4096, float(w.abs().max()) / 448
+    g8 = (dy / gs).clamp(-57344, 57344).to(E5M2)
+    w8 = (w / ws).to(E4M3)
+    out = B.fp8_dgrad(g8.cuda(), torch.tensor([gs]).cuda(), w8.cuda(), torch.tensor([ws]).cuda())
+    ref = O.dgrad(g8, gs, w8, ws)
+    got = out.cpu().double()
+    assert _rel(ref, got) <= 4e-3
+    assert float((got - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
+
+
+@pytest.mark.gpu
+def test_output_projection_dgrad_warmup_then_fp8(hip_lib, monkeypatch):
+    import hstu_amd.bwd_fp8 as B
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    B.reset_sites()
+    g = torch.Generator(device="cuda").manual_seed(7)
+    w = (torch.randn(1536, 512, device="cuda", generator=g) / 40).requires_grad_(True)
+    outs = []
+    for i in range(6):
+        dout = torch.randn(1000, 512, device="cuda", generator=g).to(torch.bfloat16)
+        outs.append((dout, B.output_projection_dgrad(dout, w)))
+    assert all(o is None for _, o in outs[:4])                 # 4 warm-up calls
+    for dout, o in outs[4:]:
+        ref = dout.double() @ w.detach().double().t()
+        assert o.dtype == torch.bfloat16 and o.shape == (1000, 1536)
+        assert _rel(ref, o) <= 8e-2
+    # a non-parameter weight (a per-call copy) never engages
+    assert B.output_projection_dgrad(outs[0][0], w.detach().clone()) is None
+    B.reset_sites()
+
+
+@pytest.mark.gpu
+def test_output_block_backward_with_fp8_dgrad(hip_lib, monkeypatch):
+    import hstu_amd
+    import hstu_amd.bwd_fp8 as B
+
+    T, D = 2000, 512
+    g = torch.Generator(device="cuda").manual_seed(11)
+    attn = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
+    u = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
+    x = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
+    nw = torch.ones(D, device="cuda", dtype=torch.bfloat16)
+    nb = torch.zeros(D, device="cuda", dtype=torch.bfloat16)
+    W = (torch.randn(3 * D, D, device="cuda", generator=g) / 40).to(torch.bfloat16).requires_grad_(True)
+    dout = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
+
+    def grads():
+        a, uu = attn.clone().requires_grad_(True), u.clone().requires_grad_(True)
+        out = hstu_amd.triton_hstu_compute_output(a, uu, x, nw, nb, W, 1e-6, 0.0, True, silu_u=True, concat_u=True,
+                                                  concat_x=True, mul_u_activation_type="silu",
+                                                  recompute_y_in_backward=True)
+        out.backward(dout)
+        return a.grad.float(), uu.grad.float()
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "0")
+    ref = grads()
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    B.reset_sites()
+    for _ in range(4):
+        warm = grads()                                        # warm-up: bf16, identical
+    assert torch.equal(warm[0], ref[0]) and torch.equal(warm[1], ref[1])
+    fp8 = grads()
+    for r, f in zip(ref, fp8):
+        assert _rel(r, f) <= 8e-2
+        assert not torch.equal(r, f)                          # the FP8 path ran
+    B.reset_sites()

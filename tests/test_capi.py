@@ -50,11 +50,14 @@ def test_workspace_size():
     cap = (B * H + 7) // 8
     sched = a256(4 * (8 * cap + 8 * (cap + 1) + 8 + 2 * B))  # items, starts, counts, per-sequence scratch
     f = lib.fn("hstu_attn_bwd_workspace_bytes")
-    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 0) == sched
-    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096, 0) == sched + 1000 * 4 * 128 * 2
+    # dS tiles (8 KiB each) for the dQ kernel: 2 (ceil(N/128) + 1) (ceil(T/128) + B) per head, plus the
+    # per-sequence tile prefix (int64 [B + 1])
+    ds = a256((B + 1) * 8) + 2 * (4096 // 128 + 1) * ((1000 + 127) // 128 + B) * H * 8192
+    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 0) == sched + ds
+    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096, 0) == sched + 1000 * 4 * 128 * 2 + ds
     ext = a256(4 * (2 * 4096 + 256) * 4)  # pre-clamped bias rows, 2N+256 per head
     part = a256(64 * 4 * (2 * 1024 - 1) * 4)
-    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 1024) == sched + ext + part
+    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 1024) == sched + ext + part + ds
     assert f(lib.HSTU_DTYPE_BF16, -1, B, H, 128, 4096, 0) == -1
     g = lib.fn("hstu_attn_fwd_workspace_bytes")
     assert g(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096) == sched
