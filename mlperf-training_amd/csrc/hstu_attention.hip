@@ -1401,6 +1401,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   __syncthreads();
 
   int cur = 0;  // stage holding the current tile
+
   // One query tile; MASKED / BCONST select the epilogue at compile time so
   // each loop below has a single code path (two paths in one loop push the
   // register allocation past the 256 VGPRs of two waves per SIMD).
@@ -1502,11 +1503,13 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
     __syncthreads();
     cur = cur + 1 == C::NSTAGE ? 0 : cur + 1;
     if constexpr (!GENERIC) {
-      // after the wait: these stores are the newest vector-memory operations,
-      // so the next tile's vmcnt bound still covers its own loads first
+      // after the wait, so these stores are the newest vector-memory
+      // operations and the next tile's vmcnt bound covers its loads first
+      // (a later placement measured slower); streaming stores, since the dQ
+      // kernel reads the tiles long after
       uint8_t* dst = ds_tile(p, sc, sc.blk, m0 / C::BMQ) + ((wave * 2) * 64 + lane) * 16;
-      *(u32x4*)dst = ds_out[0];
-      *(u32x4*)(dst + 64 * 16) = ds_out[1];
+      __builtin_nontemporal_store(ds_out[0], (u32x4*)dst);
+      __builtin_nontemporal_store(ds_out[1], (u32x4*)(dst + 64 * 16));
     }
   };
 
