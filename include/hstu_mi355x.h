@@ -107,10 +107,13 @@ int hstu_attn_bwd(int dtype,
  * Device workspace the backward needs (bytes): the block schedule; with a
  * bias (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows and 64
  * partial copies of the bias gradient; for e4m3 inputs an exact bf16 copy of
- * q.  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.  The
+ * q; the dS tiles (8 KiB per 128-key x 32-query tile, bounded by
+ * 2 (ceil(N/128) + 1) (ceil(T/128) + B) H tiles).  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.  The
  * caller allocates it (the reference's FlyDSL backward likewise takes its
  * dq-split workspace from the caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).
- * hstu_attn_bwd_dkdv and hstu_attn_bwd_dq must be given the same workspace.
+ * hstu_attn_bwd_dkdv and hstu_attn_bwd_dq must be given the same workspace,
+ * dkdv first: with the causal mask (no num_targets, window or contextual
+ * prefix) dkdv leaves the bf16 dS tiles there and dq contracts them with K.
  */
 int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len,
                                       int bias_R);
