@@ -13,7 +13,8 @@ over the whole batch, inputs resident in HBM.  value = causal-effective FLOPs
 the bias (the reference's attention has none) and on bf16 inputs, the output
 block's LN * U * dropout kernels (GB/s against HBM), one whole HSTU layer
 forward + backward in FP8 at config 3's shapes, the
-targets-only delta-q attention, and the full-FP8 backward's dO block quantizer.
+targets-only delta-q attention, the full-FP8 backward's dO block quantizer and
+the FP8 projection GEMM.
 
     python bench.py --copy-calibration   # a 512 MiB device copy, for scaling
                                          # the FETCH_SIZE / WRITE_SIZE counters
@@ -70,7 +71,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--only", choices=("output_block", "layer", "layer_fp8_dgrad", "delta", "do_quant"), default=None,
+    ap.add_argument("--only", choices=("output_block", "layer", "layer_fp8_dgrad", "delta", "do_quant", "gemm"),
+                    default=None,
                     help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
                     help="how the caches are evicted before each timed call (see CacheFlush)")
@@ -215,6 +217,39 @@ def _cold_events(torch, fn, steps, warmup, flush, marks=1):
     segs = [np.array([e[j].elapsed_time(e[j + 1]) for e in evs]) for j in range(marks)]
     tot = np.array([e[0].elapsed_time(e[-1]) for e in evs])
     return tot, segs
+
+
+def gemm_bench(torch, T, steps, warmup, flush):
+    """the FP8 row/column-scaled UVQK projection,
+    X e4m3 [M, 512] (per-row scales) x W e4m3 [512, 2048] (per-column
+    scales) -> bf16 with SiLU on the U columns, at M = config 3's T and
+    M = 262 144; and the [M, 512] x [512, 512] output-projection shape."""
+    import hstu_amd.fp8 as fp8
+
+    g = torch.Generator(device="cuda").manual_seed(13)
+    res = {}
+    for name, M, N, silu in (("uvqk_T", T, 2048, (0, 512)), ("uvqk_262144", 262144, 2048, (0, 512)),
+                             ("proj_512", 262144, 512, None)):
+        a8 = torch.randn(M, 512, device="cuda", generator=g).to(torch.float8_e4m3fn)
+        sa = torch.rand(M, device="cuda", generator=g) * 0.01 + 0.005
+        w8 = torch.randn(N, 512, device="cuda", generator=g).to(torch.float8_e4m3fn)
+        sw = torch.rand(N, device="cuda", generator=g) * 0.01 + 0.005
+        bias = torch.randn(N, device="cuda", generator=g).to(torch.bfloat16)
+
+        def run(ev):
+            if ev is not None:
+                ev[0].record()
+            fp8.fp8_gemm(a8, sa, (w8, sw), bias=bias, silu_cols=silu)
+            if ev is not None:
+                ev[1].record()
+
+        t, _ = _cold_events(torch, run, steps, warmup, flush)
+        m = float(np.median(t))
+        res[name] = {"M": M, "N": N, "K": 512, "ms": round(m, 4),
+                     "TFLOP/s": round(2 * M * N * 512 / (m * 1e-3) / 1e12, 1)}
+        del a8, w8
+    return {"workload": "BASELINE config 4: FP8 e4m3 GEMM, per-row x per-column scales, bias, bf16 out "
+                        "(SiLU on the 512 U columns of UVQK)", **res, "peak_TFLOPs": PEAK_TFLOPS["fp8"]}
 
 
 def output_block_bench(torch, T, steps, warmup, flush):
@@ -498,6 +533,9 @@ def main():
     if args.only == "delta":
         print(json.dumps(delta_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
         return
+    if args.only == "gemm":
+        print(json.dumps(gemm_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
+        return
     if args.only == "do_quant":
         print(json.dumps(do_quant_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
         return
@@ -568,6 +606,7 @@ def main():
         torch.cuda.empty_cache()
         res["delta"] = delta_bench(torch, lengths, N, args.steps, 3, flush)
         res["do_quant"] = do_quant_bench(torch, lengths, N, args.steps, 3, flush)
+        res["gemm"] = gemm_bench(torch, int(np.sum(lengths)), args.steps, 3, flush)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(lengths, H, D, N, args.cpu_seconds)

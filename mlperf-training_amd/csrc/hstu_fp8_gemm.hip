@@ -61,6 +61,9 @@ struct GemmParams {
   int tiles_m, tiles_n;
 };
 
+#ifndef HSTU_GEMM_REGSTAGE
+#define HSTU_GEMM_REGSTAGE 1
+#endif
 constexpr int kBM = 128, kBN = 128, kBK = 128;
 constexpr int kPitch = kBK + 32;  // 160: conflict-free operand reads
 using GTile = DirectTile<128, kBK, kPitch>;  // 20 load instructions, 5 per wave
@@ -68,6 +71,27 @@ constexpr int kTileBytes = GTile::BYTES;     // 20 KiB
 constexpr int kStage = 2 * kTileBytes;       // W tile then A tile
 constexpr int kGemmLds = 2 * kStage;         // 80 KiB
 constexpr int kCnt = 2 * GTile::PER_WAVE;    // load instructions per wave per stage
+
+// One operand's k-step tile (128 rows x 128 bytes) staged global -> registers
+// -> LDS: four 16-byte chunks per thread.  Loads issued a whole k-step ahead
+// land while the MFMAs run; only the LDS store waits for them.
+struct RegTile {
+  u32x4 r[4];
+  __device__ __forceinline__ void load(BufRsrc rs, uint32_t ld, uint32_t soff) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + kThreads * i, row = c >> 3, col = c & 7;
+      r[i] = buf_ld128(rs, (uint32_t)row * ld + col * 16, soff);
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* tile) const {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = threadIdx.x + kThreads * i, row = c >> 3, col = c & 7;
+      *(u32x4*)(tile + row * kPitch + col * 16) = r[i];
+    }
+  }
+};
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
@@ -118,10 +142,19 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
     bias[ns] = p.bias ? *(const u32x2*)(p.bias + n) : u32x2{0u, 0u};
   }
 
+#if HSTU_GEMM_REGSTAGE
+  RegTile wreg, areg;
+  wreg.load(wrsrc, (uint32_t)p.ldw, 0);
+  areg.load(arsrc, (uint32_t)p.lda, 0);
+  wreg.store(smem);
+  areg.store(smem + kTileBytes);
+  __syncthreads();
+#else
   wt.load(wrsrc, 0, smem);
   at.load(arsrc, 0, smem + kTileBytes);
   wait_vm();
   __syncthreads();
+#endif
 
   // lane group g holds 16-byte k-chunks g and g+4 of a row
   const int w_rd = (wn + li) * kPitch + 16 * g;
@@ -129,9 +162,14 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
   for (int kk = 0; kk < nk; ++kk) {
     const uint8_t* buf = smem + (kk & 1) * kStage;
     if (kk + 1 < nk) {
+#if HSTU_GEMM_REGSTAGE
+      wreg.load(wrsrc, (uint32_t)p.ldw, (kk + 1) * kBK);
+      areg.load(arsrc, (uint32_t)p.lda, (kk + 1) * kBK);
+#else
       uint8_t* nb = smem + ((kk + 1) & 1) * kStage;
       wt.load(wrsrc, (kk + 1) * kBK, nb);
       at.load(arsrc, (kk + 1) * kBK, nb + kTileBytes);
+#endif
     }
     i32x8 bop[4];
 #pragma unroll
@@ -151,8 +189,17 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
           acc[ns][ms] = mfma_fp8(aop, bop[ms], acc[ns][ms]);
       }
     }
+#if HSTU_GEMM_REGSTAGE
+    if (kk + 1 < nk) {
+      uint8_t* nb = smem + ((kk + 1) & 1) * kStage;
+      wreg.store(nb);
+      areg.store(nb + kTileBytes);
+    }
+    __syncthreads();
+#else
     wait_vm();
     __syncthreads();
+#endif
   }
 
   // ---- epilogue: lane holds C[m = m0+wm+16ms+li][n = n0+wn+16ns+4g .. +3]
