@@ -1325,50 +1325,54 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   // (cpr 16-byte slots per LDS row, dcpr of them data); recomputed at each
   // issue rather than held in registers.
   auto tile_voff = [&](int i, int cpr, int dcpr, uint32_t rs) -> uint32_t {
-    // The lane index passes through an empty asm so these few instructions
-    // are redone at each issue instead of being hoisted into registers.
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    const int c = i * 64 + ln;
+    const int c = i * 64 + lane;
     int row = c / cpr, col = c % cpr;
     if (col >= dcpr) col -= dcpr;
     row = row < C::BMQ ? row : C::BMQ - 1;
     return row * rs + col * 16;
   };
-  auto lane_of = [&]() -> uint32_t {
-    int ln = lane;
-    asm volatile("" : "+v"(ln));
-    return (uint32_t)ln;
-  };
   // One load instruction; the slot (which tile piece it moves) is a
   // compile-time constant, so each wave's issue sequence is straight-line.
   // Slots: [bf16 Q][e4m3 Q][dO][q scales][bias band][dummies].
-  auto issue_slot = [&](auto slot_c, int m0, uint8_t* stage) {
+  constexpr int S_Q8 = C::N_Q, S_DO = S_Q8 + C::N_Q8, S_SQ = S_DO + C::N_DO, S_BIAS = S_SQ + C::N_SQ;
+  // The per-lane voffset of each of this wave's load slots (slot wave + 4j)
+  // depends only on (slot, lane): computed once, the tile base goes into the
+  // scalar offset at each issue.
+  uint32_t voffc[C::CNT];
+#pragma unroll
+  for (int jj = 0; jj < C::CNT; ++jj) {
+    const int slot = wave + 4 * jj;
+    uint32_t v;
+    if (slot < S_Q8) v = tile_voff(slot, C::P / 16, D * 2 / 16, qrs);
+    else if (slot < S_DO) v = tile_voff(slot - S_Q8, C::P8 / 16, D / 16, q8rs);
+    else if (slot < S_SQ) v = tile_voff(slot - S_DO, C::P / 16, D * 2 / 16, dors);
+    else if (FP8 && slot == S_SQ) v = (uint32_t)min(lane, C::BMQ - 1) * s_step;
+    else if (BIAS && slot < C::N_REAL) v = ((slot - S_BIAS) * 64 + lane) * 4;
+    else v = lane * 16;
+    voffc[jj] = v;
+  }
+  auto issue_slot = [&](auto slot_c, auto j_c, int m0, uint8_t* stage) {
 #if defined(__HIP_DEVICE_COMPILE__)
     typedef __attribute__((address_space(3))) void lds_t;
     constexpr int slot = decltype(slot_c)::value;
-    constexpr int S_Q8 = C::N_Q, S_DO = S_Q8 + C::N_Q8, S_SQ = S_DO + C::N_DO, S_BIAS = S_SQ + C::N_SQ;
+    const uint32_t vo = voffc[decltype(j_c)::value];
     if constexpr (slot < S_Q8) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16,
-                                               tile_voff(slot, C::P / 16, D * 2 / 16, qrs), m0 * qrs, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::Q_OFF + slot * 1024), 16, vo, m0 * qrs, 0,
+                                               0);
     } else if constexpr (slot < S_DO) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(q8rsrc, (lds_t*)(stage + C::Q8_OFF + (slot - S_Q8) * 1024), 16,
-                                               tile_voff(slot - S_Q8, C::P8 / 16, D / 16, q8rs), m0 * q8rs, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(q8rsrc, (lds_t*)(stage + C::Q8_OFF + (slot - S_Q8) * 1024), 16, vo,
+                                               m0 * q8rs, 0, 0);
     } else if constexpr (slot < S_SQ) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - S_DO) * 1024), 16,
-                                               tile_voff(slot - S_DO, C::P / 16, D * 2 / 16, dors), m0 * dors, 0,
-                                               0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(dorsrc, (lds_t*)(stage + C::DO_OFF + (slot - S_DO) * 1024), 16, vo,
+                                               m0 * dors, 0, 0);
     } else if constexpr (FP8 && slot == S_SQ) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4,
-                                               (uint32_t)min((int)lane_of(), C::BMQ - 1) * s_step, m0 * s_step, 0,
-                                               0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sq_rsrc, (lds_t*)(stage + C::SQ_OFF), 4, vo, m0 * s_step, 0, 0);
     } else if constexpr (BIAS && slot < C::N_REAL) {
       constexpr int b = slot - S_BIAS;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4,
-                                               (b * 64 + lane_of()) * 4, (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b_rsrc, (lds_t*)(stage + C::BIAS_OFF + b * 256), 4, vo,
+                                               (uint32_t)(m0 - n0 + p.N) * 4u, 0, 0);
     } else {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, lane_of() * 16, 0, 0,
-                                               0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(qrsrc, (lds_t*)(stage + C::DUMMY_OFF), 16, vo, 0, 0, 0);
     }
 #else
     (void)m0;
@@ -1378,7 +1382,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   auto issue = [&](int m0, uint8_t* stage) {
     auto run = [&](auto wave_c) {
       constexpr int W = decltype(wave_c)::value;
-      static_for<C::CNT>([&](auto j) { issue_slot(std::integral_constant<int, W + 4 * decltype(j)::value>{}, m0, stage); });
+      static_for<C::CNT>([&](auto j) {
+        issue_slot(std::integral_constant<int, W + 4 * decltype(j)::value>{}, j, m0, stage);
+      });
     };
     const int w = __builtin_amdgcn_readfirstlane(wave);
     if (w == 0) run(std::integral_constant<int, 0>{});
