@@ -394,13 +394,16 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     config 3's shapes (T = 162 251, N = 4096, E = 512, H = 4, D = 128), with
     the relative bias and output dropout 0.3 (mask16).  Scales are calibrated
     once from the data (amax * 1.25 / 448) before timing.  fp8_dgrad: the
-    output projection's dgrad in FP8 (e5m2 dY, DLRM_HSTU_FP8_BWD=1), with
-    enough warm-up steps for its delayed scale to publish."""
+    output and UVQK projections' dgrads in FP8 (e5m2 gradients,
+    DLRM_HSTU_FP8_BWD=1 and DLRM_HSTU_FP8_BWD_UVQK=1; the UVQK gradient's cast
+    also gives the bias gradient), with enough warm-up steps for their delayed
+    scales to publish."""
     import hstu_amd
     import hstu_amd.bwd_fp8 as bwd_fp8
 
     os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
     os.environ["DLRM_HSTU_FP8_BWD"] = "1" if fp8_dgrad else "0"
+    os.environ["DLRM_HSTU_FP8_BWD_UVQK"] = "1" if fp8_dgrad else "0"
     bwd_fp8.reset_sites()
     if fp8_dgrad:
         warmup = max(warmup, 5)
@@ -435,6 +438,7 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
 
     tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
     os.environ["DLRM_HSTU_FP8_BWD"] = "0"
+    os.environ["DLRM_HSTU_FP8_BWD_UVQK"] = "0"
     bwd_fp8.reset_sites()
     m = float(np.median(tot))
     P = causal_pairs(lengths)
@@ -442,7 +446,7 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     flops = 3 * gemm_fwd + 14 * D * H * P
     return {"workload": "BASELINE config 5: HSTU layer fwd+bwd in FP8 (LN -> FP8 UVQK GEMM -> FP8 attention with "
                         "bias -> LN(attn)*silu(u)*dropout -> FP8 out-proj + residual; %s), "
-                        "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj dgrad, bf16 other dgrad/wgrad" if fp8_dgrad
+                        "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj and UVQK dgrads, bf16 wgrads" if fp8_dgrad
                                                     else "bf16 dgrad/wgrad"),
             "T": T, "ms_per_step": round(m, 4), "fwd_ms": round(float(np.median(tf)), 4),
             "bwd_ms": round(float(np.median(tb)), 4),

@@ -198,6 +198,46 @@ int hstu_cast_fp8_amax(int in_dtype, const void* x, int64_t n, const float* inv_
                        void* out, float* partial_amax, int64_t partial_count, hipStream_t stream);
 
 /*
+ * One read of a row-major bf16 gradient x [rows, cols] (row stride ldx,
+ * cols % 256 == 0) -> out [rows_out, cols] contiguous fp8 (out_dtype e4m3 or
+ * e5m2) = fp8(clamp(x * inv_scale[0], +-limit)), RNE, with rows in
+ * [rows, rows_out) written as zero (K padding for a token-contracting GEMM);
+ * amax[0] = max |x| and colsum[c] = fp32 sum over rows of x[:, c] (the bias
+ * gradient, of the unquantized input; a fixed reduction order: 512-row
+ * stripes, then the stripes).  workspace: at least
+ * hstu_cast_fp8_amax_colsum_workspace_bytes(rows, cols) bytes of device
+ * memory (the per-stripe partials).  inv_scale stays on the device.
+ * Replaces: quantize_amax_colsum / _quantize_amax_colsum_kernel,
+ *           ops/triton/bwd_fp8.py:378-434, 608-692.
+ */
+int64_t hstu_cast_fp8_amax_colsum_workspace_bytes(int64_t rows, int64_t cols);
+int hstu_cast_fp8_amax_colsum(const void* x, int64_t ldx, int64_t rows, int64_t cols, const float* inv_scale,
+                              int out_dtype, float limit, void* out, int64_t rows_out, float* colsum, float* amax,
+                              void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Weight gradient over the token axis from row-major (one token per row)
+ * operands: out[n1][n2] = sa * sb * sum_{t < T} A[t][n1] * B[t][n2], fp32
+ * accumulation, out bf16 (HSTU_DTYPE_BF16) or fp32 (HSTU_DTYPE_FP32) with row
+ * stride ldo.  A [T, N1] (row stride lda elements), B [T, N2] (ldb): both
+ * HSTU_DTYPE_BF16; N1, N2 multiples of 256; 16-byte aligned rows.  scale_a /
+ * scale_b: one fp32 on the device each, or NULL for 1.  The tokens are split
+ * over `split` ranges (<= 0: about one workgroup per CU); the per-split fp32
+ * partials go to workspace (hstu_wgrad_workspace_bytes bytes, 0 for one
+ * split) and are summed in a fixed order (bitwise reproducible).  T = 0
+ * writes zeros.  hstu_wgrad_split gives the split actually used.
+ * Replaces: dw = torch.mm(x.t(), dz) of triton_addmm_bwd,
+ *           ops/triton/triton_addmm.py:1737-1750, and the output projection's
+ *           torch.mm(y.t(), dout), ops/triton/triton_hstu_linear.py; the split-K
+ *           scheme of fp8_wgrad, ops/triton/fp8_wgrad.py:27-160.
+ */
+int hstu_wgrad_split(int64_t T, int N1, int N2, int split);
+int64_t hstu_wgrad_workspace_bytes(int64_t T, int N1, int N2, int split);
+int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, const void* B, int64_t ldb, int64_t T, int N1,
+               int N2, const float* scale_a, const float* scale_b, void* out, int64_t ldo, int out_dtype, int split,
+               void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * e4m3 quantization of bf16 rows in groups of `group` consecutive elements:
  * scale = amax/448 per group (1/448 for an all-zero group), written to
  * scale_out[row * (cols/group) + group_index]; out = e4m3(clamp(x/scale,

@@ -17,7 +17,8 @@ PKG_ROOT = Path(__file__).resolve().parent
 REPO_ROOT = PKG_ROOT.parent
 CSRC = PKG_ROOT / "csrc"
 OUT = PKG_ROOT / "hstu_amd" / "libhstu_mi355x.so"
-SOURCES = ["hstu_attention.hip", "hstu_fp8_gemm.hip", "hstu_layernorm.hip", "hstu_delta.hip", "hstu_do_fp8.hip"]
+SOURCES = ["hstu_attention.hip", "hstu_fp8_gemm.hip", "hstu_layernorm.hip", "hstu_delta.hip", "hstu_do_fp8.hip",
+           "hstu_wgrad.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -18,6 +18,7 @@
 //   quantizer              ops/triton/triton_fp8.py:396-413, 760-781 (scale = amax/448)
 //   FP8 backward dgrad     ops/triton/bwd_fp8.py:1347-1395 (e5m2 dY x e4m3 W^T, per-tensor scales)
 //   one-pass cast + amax   ops/triton/bwd_fp8.py:194-217, 827-866
+//   cast + amax + colsum   ops/triton/bwd_fp8.py:378-434, 608-692 (quantize_amax_colsum)
 //
 // Design: workgroup tile 128 (M) x 128 (N), 4 waves as 2 x 2 of 64 x 64.  The
 // MFMA (v_mfma_f32_16x16x128_f8f6f4) is issued operand-swapped, W rows as the
@@ -34,6 +35,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -374,6 +376,124 @@ __global__ void __launch_bounds__(256) cast_fp8_amax_kernel(const uint8_t* __res
   if (tid == 0) partial[blockIdx.x] = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
 }
 
+// One read of a row-major bf16 gradient [rows, cols] -> its FP8 copy
+// [rows_out, cols] (fp8(clamp(x * inv_scale, +-limit)), rows >= rows zero),
+// the max |x| and the fp32 column sums of the unquantized input (the bias
+// gradient).  A block owns kCsRows rows x 256 columns: 32 threads x 8 columns
+// across a row, 8 rows at a time, kCsUnroll row loads in flight per thread.
+// Each thread keeps its 8 column sums in registers; the block folds its 8 row
+// slots through LDS once, into part_col[stripe][cols].  Blocks are numbered
+// column block fastest, so the blocks in flight read whole rows.
+constexpr int kCsRows = 512, kCsCols = 256, kCsUnroll = 8;
+
+template <bool OUT_BF8>
+__global__ void __launch_bounds__(256) cast_fp8_amax_colsum_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t rows, int64_t rows_out, int cols, int ncb,
+    const float* __restrict__ inv_scale, float limit, uint8_t* __restrict__ out, float* __restrict__ part_col,
+    float* __restrict__ part_amax) {
+  __shared__ float red[8][kCsCols];
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x, c = tid & 31, r = tid >> 5;
+  const int cb = (int)(blockIdx.x % (unsigned)ncb);
+  const int64_t stripe = blockIdx.x / (unsigned)ncb;
+  const int col = cb * kCsCols + c * 8;
+  const int64_t row0 = stripe * kCsRows;
+  const float s = inv_scale[0];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float amax = 0.f;
+  for (int it = 0; it < kCsRows / 8; it += kCsUnroll) {
+    if (row0 + it * 8 >= rows_out) break;  // block-uniform
+    u32x4 w[kCsUnroll];
+#pragma unroll
+    for (int u = 0; u < kCsUnroll; ++u) {
+      const int64_t row = row0 + (it + u) * 8 + r;
+      w[u] = row < rows ? *(const u32x4*)(x + row * ldx + col) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kCsUnroll; ++u) {
+      const int64_t row = row0 + (it + u) * 8 + r;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t b = w[u][j];
+        v[2 * j] = __builtin_bit_cast(float, b << 16);
+        v[2 * j + 1] = __builtin_bit_cast(float, b & 0xffff0000u);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        acc[e] += v[e];
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(v[e]));
+      }
+      if (row < rows_out) {
+        float q[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = __builtin_fminf(__builtin_fmaxf(v[e] * s, -limit), limit);
+        int lo, hi;
+        if constexpr (OUT_BF8) {
+          lo = __builtin_amdgcn_cvt_pk_bf8_f32(q[0], q[1], 0, false);
+          lo = __builtin_amdgcn_cvt_pk_bf8_f32(q[2], q[3], lo, true);
+          hi = __builtin_amdgcn_cvt_pk_bf8_f32(q[4], q[5], 0, false);
+          hi = __builtin_amdgcn_cvt_pk_bf8_f32(q[6], q[7], hi, true);
+        } else {
+          lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false);
+          lo = __builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+          hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[4], q[5], 0, false);
+          hi = __builtin_amdgcn_cvt_pk_fp8_f32(q[6], q[7], hi, true);
+        }
+        *(u32x2*)(out + row * cols + col) = u32x2{(uint32_t)lo, (uint32_t)hi};
+      }
+    }
+  }
+  // stripes that start past the input store no partials (padding only)
+  if (row0 >= rows) return;  // block-uniform
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[r][c * 8 + e] = acc[e];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) t += red[k][tid];
+  part_col[stripe * cols + cb * kCsCols + tid] = t;
+  if (tid == 0)
+    part_amax[stripe * ncb + cb] = __builtin_fmaxf(__builtin_fmaxf(wmax[0], wmax[1]), __builtin_fmaxf(wmax[2], wmax[3]));
+}
+
+// colsum[col] = sum over stripes of part_col[stripe][col] (32 columns x 8
+// stripe lanes per block, folded in a fixed order), and in the last block
+// amax[0] = max of the amax partials.
+__global__ void __launch_bounds__(256) colsum_finish_kernel(const float* __restrict__ part_col, int64_t nstripes,
+                                                            int cols, float* __restrict__ colsum,
+                                                            const float* __restrict__ part_amax, int64_t namax,
+                                                            float* __restrict__ amax_out) {
+  __shared__ float red[8][32];
+  const int tid = threadIdx.x;
+  if ((int)blockIdx.x < cols / 32) {
+    const int c = tid & 31, g = tid >> 5, col = blockIdx.x * 32 + c;
+    float s = 0.f;
+    for (int64_t i = g; i < nstripes; i += 8) s += part_col[i * cols + col];
+    red[g][c] = s;
+    __syncthreads();
+    if (g == 0) {
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t += red[k][c];
+      colsum[col] = t;
+    }
+  } else {
+    float m = 0.f;
+    for (int64_t i = tid; i < namax; i += 256) m = __builtin_fmaxf(m, part_amax[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+    if ((tid & 63) == 0) red[0][tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) amax_out[0] = __builtin_fmaxf(__builtin_fmaxf(red[0][0], red[0][1]), __builtin_fmaxf(red[0][2], red[0][3]));
+  }
+}
+
+inline int64_t cs_align(int64_t n) { return (n + 255) / 256 * 256; }
+
 hipError_t set_gemm_lds(const void* fn) {
   static std::mutex mu;
   static std::vector<const void*> done;
@@ -487,5 +607,44 @@ extern "C" int hstu_cast_fp8_amax(int in_dtype, const void* x, int64_t n, const 
   else if (f32) hipLaunchKernelGGL((cast_fp8_amax_kernel<true, false>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
   else if (bf8) hipLaunchKernelGGL((cast_fp8_amax_kernel<false, true>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
   else hipLaunchKernelGGL((cast_fp8_amax_kernel<false, false>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t hstu_cast_fp8_amax_colsum_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows < 0 || cols <= 0 || cols % kCsCols != 0) return -1;
+  const int64_t stripes = (rows + kCsRows - 1) / kCsRows;
+  return cs_align(stripes * cols * 4) + cs_align(stripes * (cols / kCsCols) * 4);
+}
+
+extern "C" int hstu_cast_fp8_amax_colsum(const void* x, int64_t ldx, int64_t rows, int64_t cols,
+                                         const float* inv_scale, int out_dtype, float limit, void* out,
+                                         int64_t rows_out, float* colsum, float* amax, void* workspace,
+                                         int64_t workspace_bytes, hipStream_t stream) {
+  if ((out_dtype != HSTU_DTYPE_FP8_E4M3 && out_dtype != HSTU_DTYPE_FP8_E5M2) || rows < 0 || rows_out < rows ||
+      cols <= 0 || ldx < cols || !inv_scale || !colsum || !amax || !(limit > 0.f) || (rows > 0 && !x) ||
+      (rows_out > 0 && !out))
+    return HSTU_E_BAD_ARG;
+  if (cols % kCsCols != 0 || cols > (1 << 30) || ldx % 8 != 0 || (uintptr_t)x % 16 || (uintptr_t)out % 8)
+    return HSTU_E_UNSUPPORTED;
+  const int64_t need = hstu_cast_fp8_amax_colsum_workspace_bytes(rows, cols);
+  if (workspace_bytes < need || (need > 0 && !workspace)) return HSTU_E_BAD_ARG;
+  const int ncb = (int)(cols / kCsCols);
+  const int64_t stripes = (rows + kCsRows - 1) / kCsRows;
+  const int64_t launch = std::max(stripes, (rows_out + kCsRows - 1) / kCsRows) * ncb;
+  if (launch >= ((int64_t)1 << 31)) return HSTU_E_UNSUPPORTED;
+  float* part_col = (float*)workspace;
+  float* part_amax = (float*)((uint8_t*)workspace + cs_align(stripes * cols * 4));
+  if (launch > 0) {
+    if (out_dtype == HSTU_DTYPE_FP8_E5M2)
+      hipLaunchKernelGGL((cast_fp8_amax_colsum_kernel<true>), dim3((unsigned)launch), dim3(256), 0, stream,
+                         (const uint16_t*)x, ldx, rows, rows_out, (int)cols, ncb, inv_scale, limit, (uint8_t*)out,
+                         part_col, part_amax);
+    else
+      hipLaunchKernelGGL((cast_fp8_amax_colsum_kernel<false>), dim3((unsigned)launch), dim3(256), 0, stream,
+                         (const uint16_t*)x, ldx, rows, rows_out, (int)cols, ncb, inv_scale, limit, (uint8_t*)out,
+                         part_col, part_amax);
+  }
+  hipLaunchKernelGGL(colsum_finish_kernel, dim3((unsigned)(cols / 32 + 1)), dim3(256), 0, stream, part_col, stripes,
+                     (int)cols, colsum, part_amax, stripes * ncb, amax);
   return (int)hipGetLastError();
 }

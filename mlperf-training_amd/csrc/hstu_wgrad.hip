@@ -1,0 +1,286 @@
+// Weight gradients over the token axis of the HSTU layer's projections,
+//   C[n1][n2] = sa * sb * sum_t A[t][n1] * B[t][n2],
+// from row-major operands that hold one token per row: x^T dz of the UVQK
+// projection (A = LN(x) [T, 512], B = d(uvqk) [T, 2048]) and y^T dout of the
+// output projection (A = y [T, 1536], B = dout [T, 512]), for MI355X (gfx950).
+// Reference behaviour followed (paths relative to
+// recommendation_v4/hstu/generative_recommenders/):
+//   bf16 wgrad dw = x^T dz         ops/triton/triton_addmm.py:1737-1750
+//   output-projection wgrad        ops/triton/triton_hstu_linear.py (torch.mm(y.t(), dout))
+//   split-K over tokens, fixed-    ops/triton/fp8_wgrad.py:27-160 (fp8_wgrad: fp32
+//   order second pass                partials [SPLIT, N1, N2], reduce, then the scales)
+//
+// Design: the output is small (0.75-1 M elements) and the contraction long
+// (T ~ 162 K tokens), so the tokens are split over workgroups: tiles x split
+// ~ one workgroup per CU.  A workgroup owns a 256 (n1) x 256 (n2) tile of one
+// token range; 8 waves as 4 (n1) x 2 (n2) of 64 x 128.  Each k-step of 32
+// tokens stages both operands' 32 x 512-byte tile rows in LDS as they lie in
+// memory (token rows, 544-byte pitch), and the MFMA operands come out of LDS
+// with the transposed read ds_read_b64_tr_b16, which turns a token-major tile
+// into k(token)-contiguous fragments: lane group g gets tokens {4g..4g+3,
+// 16+4g..16+4g+3} of column li in both operands, so the contraction sees the
+// same token order on both sides.  The MFMA (v_mfma_f32_16x16x32_bf16) runs
+// with B as its A operand, so a lane's result is 4 consecutive n2 of one n1
+// row.  Global loads for step k+1 are issued into registers before step k's
+// MFMAs and written to the other LDS buffer after them (one barrier per
+// step).  Workgroups are numbered so that the tiles of one token range run on
+// one XCD and share its L2.  With split > 1 every workgroup writes an fp32
+// partial tile; a second kernel sums the splits in a fixed order, applies
+// sa * sb and writes bf16 or fp32 (bitwise reproducible, no atomics).
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "hstu_common.h"
+#include "hstu_mi355x.h"
+
+namespace {
+using namespace hstu;
+
+constexpr int kWThreads = 512;                 // 8 waves
+constexpr int kBN1 = 256, kBN2 = 256, kKT = 32;  // tile and tokens per k-step
+constexpr int kWPitch = 2 * kBN1 + 32;         // 544 bytes: conflict-free transposed reads
+constexpr int kWTile = kKT * kWPitch;          // one operand's k-step tile
+constexpr int kWStage = 2 * kWTile;            // A tile then B tile
+constexpr int kWLds = 2 * kWStage;             // 68 KiB
+constexpr int kCus = 256;
+
+struct WgradParams {
+  const uint8_t* A;
+  const uint8_t* B;
+  int64_t lda, ldb;  // bytes
+  int64_t T;
+  int64_t tps;  // tokens per split, a multiple of kKT
+  int N1, N2;
+  int split, tiles_n2, tiles;
+  float* ws;  // [split][N1][N2] fp32 partials when split > 1
+  void* out;
+  int64_t ldo;  // elements
+  int out_f32;
+  const float* sa;
+  const float* sb;
+};
+
+__global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  // XCD-contiguous numbering: workgroup b runs on XCD b % 8; consecutive idx
+  // (one token range, all its tiles) land on one XCD.
+  const int total = p.tiles * p.split;
+  const int per_xcd = (total + 7) / 8;
+  const int idx = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (idx >= total) return;
+  const int s = idx / p.tiles, tile = idx - s * p.tiles;
+  const int t1 = tile / p.tiles_n2, t2 = tile - t1 * p.tiles_n2;
+  const int n10 = t1 * kBN1, n20 = t2 * kBN2;
+  const int64_t tb = (int64_t)s * p.tps;
+  const int64_t te = min(tb + p.tps, p.T);
+  const int nk = (int)((te - tb + kKT - 1) / kKT);
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int w1 = (wave >> 1) * 64, w2 = (wave & 1) * 128;
+
+  // Token rows tb .. te-1 of the tile's 512-byte column band; rows past te
+  // (the next split's, or past T) read as zero.
+  const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)p.ldb;
+  const BufRsrc ar = make_rsrc(p.A + tb * p.lda + n10 * 2, (uint32_t)((te - tb - 1) * p.lda + kBN1 * 2));
+  const BufRsrc br = make_rsrc(p.B + tb * p.ldb + n20 * 2, (uint32_t)((te - tb - 1) * p.ldb + kBN2 * 2));
+  // staging: chunk c = tid + 512 q (q = 0, 1) of a 32 x 512-byte tile
+  uint32_t va[2], vb[2], lo[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = tid + kWThreads * q, row = c >> 5, col = c & 31;
+    va[q] = row * lda + col * 16;
+    vb[q] = row * ldb + col * 16;
+    lo[q] = row * kWPitch + col * 16;
+  }
+  u32x4 ra[2], rb[2];
+  auto load = [&](int kk) {
+    const uint32_t sa_off = (uint32_t)kk * kKT * lda, sb_off = (uint32_t)kk * kKT * ldb;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      ra[q] = buf_ld128(ar, va[q], sa_off);
+      rb[q] = buf_ld128(br, vb[q], sb_off);
+    }
+  };
+  auto store = [&](uint8_t* st) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      *(u32x4*)(st + lo[q]) = ra[q];
+      *(u32x4*)(st + kWTile + lo[q]) = rb[q];
+    }
+  };
+
+  f32x4 acc[8][4];  // [n2 block][n1 block], lane: n1 = 16i + li, n2 = 16j + 4g .. +3
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[j][i] = zero4();
+
+  if (nk > 0) {
+    load(0);
+    store(smem);
+  }
+  __syncthreads();
+  // transposed-read start: row 4g + li/4, 4-column group li % 4
+  const int tr = (4 * g + (li >> 2)) * kWPitch + (li & 3) * 8;
+  const int a_rd = tr + w1 * 2, b_rd = kWTile + tr + w2 * 2;
+  for (int kk = 0; kk < nk; ++kk) {
+    const uint8_t* buf = smem + (kk & 1) * kWStage;
+    if (kk + 1 < nk) load(kk + 1);
+    u32x4 af[4], bfr[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      af[i] = cat_tr(lds_tr16(buf + a_rd + 32 * i), lds_tr16(buf + a_rd + 32 * i + 16 * kWPitch));
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      bfr[j] = cat_tr(lds_tr16(buf + b_rd + 32 * j), lds_tr16(buf + b_rd + 32 * j + 16 * kWPitch));
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][i] = mfma_bf16(bfr[j], af[i], acc[j][i]);
+    if (kk + 1 < nk) store(smem + ((kk + 1) & 1) * kWStage);
+    __syncthreads();
+  }
+
+  if (p.split > 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n1 = n10 + w1 + 16 * i + li;
+      float* row = p.ws + ((int64_t)s * p.N1 + n1) * p.N2 + n20 + w2 + 4 * g;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *(f32x4*)(row + 16 * j) = acc[j][i];
+    }
+    return;
+  }
+  const float sc = (p.sa ? p.sa[0] : 1.f) * (p.sb ? p.sb[0] : 1.f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n1 = n10 + w1 + 16 * i + li;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n2 = n20 + w2 + 16 * j + 4 * g;
+      const f32x4 v = acc[j][i] * sc;
+      if (p.out_f32) *(f32x4*)((float*)p.out + (int64_t)n1 * p.ldo + n2) = v;
+      else *(u32x2*)((uint16_t*)p.out + (int64_t)n1 * p.ldo + n2) = u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+    }
+  }
+}
+
+// out[n1][n2] = sa * sb * sum_{s < split} ws[s][n1][n2], summed in split order;
+// 4 consecutive n2 per thread.  split == 0 writes zeros (no tokens).
+__global__ void __launch_bounds__(256) wgrad_reduce_kernel(const float* __restrict__ ws, int split, int N1, int N2,
+                                                           const float* __restrict__ sa,
+                                                           const float* __restrict__ sb, void* __restrict__ out,
+                                                           int64_t ldo, int out_f32) {
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const int64_t numel = (int64_t)N1 * N2;
+  if (e >= numel) return;
+  f32x4 acc = zero4();
+  for (int s = 0; s < split; ++s) acc += *(const f32x4*)(ws + s * numel + e);
+  acc *= (sa ? sa[0] : 1.f) * (sb ? sb[0] : 1.f);
+  const int64_t n1 = e / N2, n2 = e - n1 * N2;
+  if (out_f32) *(f32x4*)((float*)out + n1 * ldo + n2) = acc;
+  else *(u32x2*)((uint16_t*)out + n1 * ldo + n2) = u32x2{pack_bf16(acc[0], acc[1]), pack_bf16(acc[2], acc[3])};
+}
+
+hipError_t set_wgrad_lds(const void* fn) {
+  static std::mutex mu;
+  static std::vector<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const void* d : done)
+    if (d == fn) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kWLds);
+  if (e == hipSuccess) done.push_back(fn);
+  return e;
+}
+
+// tokens per split for a requested split (<= 0: about one workgroup per CU,
+// at least 4 k-steps per split), and the split that results
+void plan(int64_t T, int N1, int N2, int split, int64_t* tps, int* eff) {
+  const int tiles = (N1 / kBN1) * (N2 / kBN2);
+  if (split <= 0) split = (int)std::max<int64_t>(1, std::min<int64_t>(kCus / std::max(tiles, 1), (T + 127) / 128));
+  if (T <= 0) {
+    *tps = kKT;
+    *eff = 0;
+    return;
+  }
+  const int64_t per = (T + split - 1) / split;
+  *tps = (per + kKT - 1) / kKT * kKT;
+  *eff = (int)((T + *tps - 1) / *tps);
+}
+
+}  // namespace
+
+extern "C" int hstu_wgrad_split(int64_t T, int N1, int N2, int split) {
+  if (T < 0 || N1 <= 0 || N2 <= 0 || N1 % kBN1 || N2 % kBN2) return -1;
+  int64_t tps;
+  int eff;
+  plan(T, N1, N2, split, &tps, &eff);
+  return eff;
+}
+
+extern "C" int64_t hstu_wgrad_workspace_bytes(int64_t T, int N1, int N2, int split) {
+  const int eff = hstu_wgrad_split(T, N1, N2, split);
+  if (eff < 0) return -1;
+  return eff > 1 ? (int64_t)eff * N1 * N2 * 4 : 0;
+}
+
+extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, const void* B, int64_t ldb, int64_t T,
+                          int N1, int N2, const float* scale_a, const float* scale_b, void* out, int64_t ldo,
+                          int out_dtype, int split, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (T < 0 || N1 <= 0 || N2 <= 0 || !out || (T > 0 && (!A || !B)) || lda < N1 || ldb < N2 || ldo < N2 ||
+      (out_dtype != HSTU_DTYPE_BF16 && out_dtype != HSTU_DTYPE_FP32))
+    return HSTU_E_BAD_ARG;
+  if (a_dtype != HSTU_DTYPE_BF16 || b_dtype != HSTU_DTYPE_BF16) return HSTU_E_UNSUPPORTED;
+  if (N1 % kBN1 || N2 % kBN2 || lda % 8 || ldb % 8 || ((uintptr_t)A | (uintptr_t)B) % 16 ||
+      (uintptr_t)out % (out_dtype == HSTU_DTYPE_FP32 ? 16 : 8) || ldo % 4)
+    return HSTU_E_UNSUPPORTED;
+  int64_t tps;
+  int eff;
+  plan(T, N1, N2, split, &tps, &eff);
+  const int64_t need = eff > 1 ? (int64_t)eff * N1 * N2 * 4 : 0;
+  if (workspace_bytes < need || (need > 0 && !workspace)) return HSTU_E_BAD_ARG;
+  // one split's rows must stay within 32-bit buffer offsets
+  if ((tps + kKT) * std::max(lda, ldb) * 2 >= ((int64_t)1 << 32)) return HSTU_E_UNSUPPORTED;
+  const int tiles = (N1 / kBN1) * (N2 / kBN2);
+  const int out_f32 = out_dtype == HSTU_DTYPE_FP32;
+  if (eff > 0) {
+    WgradParams p{};
+    p.A = (const uint8_t*)A;
+    p.B = (const uint8_t*)B;
+    p.lda = lda * 2;
+    p.ldb = ldb * 2;
+    p.T = T;
+    p.tps = tps;
+    p.N1 = N1;
+    p.N2 = N2;
+    p.split = eff;
+    p.tiles_n2 = N2 / kBN2;
+    p.tiles = tiles;
+    p.ws = (float*)workspace;
+    p.out = out;
+    p.ldo = ldo;
+    p.out_f32 = out_f32;
+    p.sa = scale_a;
+    p.sb = scale_b;
+    const int64_t total = (int64_t)tiles * eff;
+    if (total >= ((int64_t)1 << 31)) return HSTU_E_UNSUPPORTED;
+    const int grid = (int)((total + 7) / 8 * 8);
+    const void* kern = (const void*)wgrad_bf16_kernel;
+    hipError_t e = set_wgrad_lds(kern);
+    if (e != hipSuccess) return (int)e;
+    void* args[] = {&p};
+    e = hipLaunchKernel(kern, dim3(grid), dim3(kWThreads), args, (size_t)kWLds, stream);
+    if (e != hipSuccess) return (int)e;
+  }
+  if (eff != 1) {
+    const int64_t threads = (int64_t)N1 * N2 / 4;
+    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)workspace, eff, N1, N2, scale_a, scale_b, out, ldo, out_f32);
+  }
+  return (int)hipGetLastError();
+}

@@ -1,33 +1,40 @@
-"""FP8 backward projection GEMMs: the e5m2-gradient output-projection dgrad and
-its delayed-scale controller, on this build's kernels (``hstu_cast_fp8_amax``,
-``hstu_fp8_gemm`` with an e5m2 A operand).
+"""FP8 backward projection GEMMs: the e5m2-gradient dgrads of the output and
+UVQK projections and their delayed-scale controller, on this build's kernels
+(``hstu_cast_fp8_amax``, ``hstu_cast_fp8_amax_colsum``, ``hstu_fp8_gemm`` with
+an e5m2 A operand).
 
 Mirrors ``ops/triton/bwd_fp8.py`` (reference paths relative to
 ``recommendation_v4/hstu/generative_recommenders/``):
 
 * ``quantize_row_major``        <- ``:827-866`` (one pass: cast at a device-side
   inverse scale, clamp to the format's max, and the input's amax)
+* ``quantize_amax_colsum``      <- ``:378-434, 608-692`` (the same cast plus the
+  fp32 column sums of the input, zero rows past M up to ``pad_to``)
 * ``SiteScale``                 <- ``_SiteScale`` ``:869-1003`` (scale published
   from the window amax times MARGIN / FP8_MAX, refreshed every REFRESH_CALLS)
 * ``quantize_gradient``         <- ``:1073-1154`` (None while warming up: the
   caller runs bf16)
 * ``quantize_weight``           <- ``:1157-1189`` (e4m3 at unit margin)
 * ``output_projection_dgrad``   <- ``:1347-1395`` (dY_e5m2 . W_e4m3^T, bf16 out)
+* ``uvqk_projection_backward``  <- ``:2313-2520`` (dZ_e5m2 . W_e4m3^T dgrad, bf16
+  wgrad, the cast's column sum as the bias gradient)
 
 Switches (the reference's names): ``DLRM_HSTU_FP8_BWD=1`` enables the path;
 ``DLRM_HSTU_FP8_BWD_MARGIN`` (8), ``_REFRESH_CALLS`` (200), ``_WARMUP_CALLS``
-(4), ``_GRAD_FORMAT`` (e5m2 | e4m3).  They are read when a call needs them,
-so a process can switch the path on and off.
+(4), ``_GRAD_FORMAT`` (e5m2 | e4m3); ``DLRM_HSTU_FP8_BWD_UVQK=1`` (with the
+e5m2 format) enables the UVQK backward on its own, as in the reference.  They
+are read when a call needs them, so a process can switch the path on and off.
 """
 
 from __future__ import annotations
 
 import os
-from typing import Dict, Optional, Tuple
+from typing import Callable, Dict, Optional, Tuple
 
 import torch
 
 from . import _lib
+from .wgrad import token_wgrad
 
 E4M3 = torch.float8_e4m3fn
 E5M2 = torch.float8_e5m2
@@ -89,6 +96,45 @@ def quantize_row_major(value: torch.Tensor, inv_scale: torch.Tensor, dtype: Opti
         partial.data_ptr(), parts, torch.cuda.current_stream(src.device).cuda_stream)
     _lib.check(st, "hstu_cast_fp8_amax")
     return out, partial[:parts].amax()
+
+
+def quantize_amax_colsum(value: torch.Tensor, inv_scale: torch.Tensor, pad_to: int = 1,
+                         out: Optional[torch.Tensor] = None,
+                         dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One read of a row-major bf16 [M, N] gradient -> (fp8 copy [Mp, N], amax,
+    colsum fp32 [N]); Mp = roundup(M, pad_to), rows >= M zero.  ``colsum`` is
+    the sum over rows of the unquantized input (the bias gradient), in a fixed
+    fp32 order (512-row stripes, then the stripes).  ``out``, if given, is a
+    contiguous [Mp' >= M, N] tensor of the gradient format, filled the same
+    way.  N % 256 == 0."""
+    dtype = grad_dtype_and_limit()[0] if dtype is None else dtype
+    limit = E4M3_MAX if dtype == E4M3 else E5M2_MAX
+    if value.dim() != 2 or value.dtype != torch.bfloat16:
+        raise ValueError("quantize_amax_colsum takes a 2-D bf16 gradient")
+    src = value.detach()
+    if src.stride(1) != 1 or src.stride(0) % 8 or src.data_ptr() % 16:
+        src = src.contiguous()
+    m, n = src.shape
+    if out is None:
+        if pad_to < 1:
+            raise ValueError("pad_to >= 1")
+        out = torch.empty(((m + pad_to - 1) // pad_to * pad_to, n), dtype=dtype, device=src.device)
+    elif (out.dim() != 2 or not out.is_contiguous() or out.dtype != dtype or out.shape[1] != n or out.shape[0] < m
+          or out.device != src.device):
+        raise ValueError("out must be a contiguous [>= M, N] tensor of the gradient format")
+    ws_bytes = int(_lib.fn("hstu_cast_fp8_amax_colsum_workspace_bytes")(m, n))
+    if ws_bytes < 0:
+        raise NotImplementedError("the column-sum cast takes N % 256 == 0")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=src.device)
+    colsum = torch.empty(n, dtype=torch.float32, device=src.device)
+    amax = torch.empty((), dtype=torch.float32, device=src.device)
+    inv = inv_scale.to(torch.float32).reshape(-1)[:1].contiguous()
+    st = _lib.fn("hstu_cast_fp8_amax_colsum")(
+        src.data_ptr(), src.stride(0), m, n, inv.data_ptr(), _code(dtype), float(limit), out.data_ptr(),
+        out.shape[0], colsum.data_ptr(), amax.data_ptr(), ws.data_ptr(), ws_bytes,
+        torch.cuda.current_stream(src.device).cuda_stream)
+    _lib.check(st, "hstu_cast_fp8_amax_colsum")
+    return out, amax, colsum
 
 
 class SiteScale:
@@ -228,3 +274,64 @@ def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor) -> Opt
     g8, gs = quantized
     w8, ws = quantize_weight(weight)
     return fp8_dgrad(g8, gs, w8, ws, gradient.dtype if gradient.dtype == torch.bfloat16 else torch.bfloat16)
+
+
+def uvqk_fp8_backward_enabled() -> bool:
+    """``DLRM_HSTU_FP8_BWD_UVQK=1`` with the e5m2 gradient format."""
+    return (os.environ.get("DLRM_HSTU_FP8_BWD_UVQK", "0") == "1"
+            and grad_dtype_and_limit()[0] == E5M2)
+
+
+def uvqk_projection_backward(
+    dz: Optional[torch.Tensor],
+    normed_x: Optional[torch.Tensor],
+    input_scale_value: Optional[float],
+    weight: torch.Tensor,
+    site: str = "uvqk_projection",
+    per_layer: bool = True,
+    normed_x_fp8_t: Optional[torch.Tensor] = None,
+    recompute_normed_x: Optional[Callable[[], torch.Tensor]] = None,
+) -> Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
+    """(d_normed_x, d_weight, d_bias fp32) of ``z = normed_x @ weight + b``
+    with an FP8 dgrad, or None for the caller's bf16 path.
+
+    dz [M, N] bf16 (N % 256 == 0), weight [K, N] as the layer stores it.  One
+    cast of dz gives its e5m2 copy, amax and column sum (the bias gradient);
+    the dgrad is dz_e5m2 . W_e4m3^T at the site's delayed scale (a snapshot
+    of the scale the payload was cast with, on a refresh call); the weight
+    gradient is the bf16 product normed_x^T dz (the split-K wgrad kernel).
+    ``per_layer`` keys the scale on the weight's storage (then it must be the
+    leaf parameter).
+    ``normed_x`` may be None when ``recompute_normed_x`` is given.  The
+    token-major FP8 wgrad (``normed_x_fp8_t``) is not served: the wgrad stays
+    bf16 whatever ``DLRM_HSTU_FP8_BWD_UVQK_WGRAD`` says."""
+    if not uvqk_fp8_backward_enabled():
+        return None
+    if per_layer and not _has_stable_identity(weight):
+        return None
+    if (dz is None or dz.dim() != 2 or not dz.is_contiguous() or dz.dtype != torch.bfloat16 or dz.shape[1] % 256
+            or dz.shape[0] == 0 or weight.dim() != 2 or weight.shape[1] != dz.shape[1] or weight.shape[0] % 128
+            or (normed_x is None and recompute_normed_x is None)
+            or (normed_x is not None and tuple(normed_x.shape) != (dz.shape[0], weight.shape[0]))):
+        return None
+    state = site_state(site_name(site, weight.data_ptr() if per_layer else None), dz.device)
+    state.calls += 1
+    if not state.published:
+        state.accumulate(dz.detach().abs().amax().float())
+        if state.calls >= _warmup_calls():
+            state.publish()
+        return None
+    dz8, amax, colsum = quantize_amax_colsum(dz, state.inv_scale, dtype=E5M2)
+    state.note_clipping(amax)
+    state.accumulate(amax)
+    # the payload was cast with the scale in use now; a refresh rewrites it in place
+    if state.calls % _refresh_calls() == 0:
+        grad_scale = state.scale.clone()
+        state.publish()
+    else:
+        grad_scale = state.scale
+    w8, w_scale = quantize_weight(weight)
+    xn = normed_x if normed_x is not None else recompute_normed_x()
+    d_w = token_wgrad(xn, dz)
+    d_x = fp8_dgrad(dz8, grad_scale, w8, w_scale)
+    return d_x, d_w, colsum

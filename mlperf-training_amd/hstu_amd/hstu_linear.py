@@ -35,6 +35,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib, bwd_fp8
+from .wgrad import token_wgrad
 from .hstu_attention import HammerKernel
 from .pt_hstu_linear import pytorch_hstu_compute_output, pytorch_norm_mul_dropout
 
@@ -381,7 +382,8 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
                                           concat_u, concat_x, act, ctx.recompute, ctx.du_row_width)
         if y is None:
             y = y_re
-        d_out_w = torch.mm(y.t(), dout).to(output_weight.dtype)
+        # y^T dout over the tokens: the split-K wgrad kernel
+        d_out_w = token_wgrad(y, dout).to(output_weight.dtype)
         return (dattn, du, dout, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
                 None, None, None, None, None, None, None, None, None, None, None, None, None, None)
 

@@ -16,8 +16,10 @@ U = bf16(x8 W8_u s_x s_w + b_u) (SiLU fused unless ``defer_silu``); with
 attention reads V, Q, K in place from that buffer at scale s_qkv, else VQK is
 bf16.  Backward: the attention backward writes dV, dQ, dK into one d(uvqk)
 [T, 2048] buffer whose U columns the output block's LN * U backward already
-filled (``du_row_width``, as :227-260 adopt it), then bf16 dgrad / wgrad
-GEMMs on the recomputed bf16 LN(x) and the LayerNorm backward.
+filled (``du_row_width``, as :227-260 adopt it), then the dgrad / wgrad
+GEMMs on the recomputed bf16 LN(x) -- bf16, or with ``DLRM_HSTU_FP8_BWD_UVQK=1``
+the e5m2 dgrad of ``bwd_fp8.uvqk_projection_backward`` (:2180-2300 call it) --
+and the LayerNorm backward.
 """
 
 from __future__ import annotations
@@ -27,9 +29,11 @@ from typing import Optional, Tuple
 import torch
 import torch.nn.functional as F
 
+from . import bwd_fp8
 from . import fp8 as _fp8
 from .hstu_attention import HammerKernel, hstu_mha, triton_hstu_attention_bwd, triton_hstu_attention_fwd
 from .hstu_linear import _ln_bwd, _ln_fwd, hstu_compute_output
+from .wgrad import token_wgrad
 
 DUVQK_WIDTH_ATTR = "_hstu_duvqk_width"
 
@@ -135,11 +139,20 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         triton_hstu_attention_bwd(dattn.contiguous().view(T, H, Dv), q, k, v, dq, dk, dv, seq_offsets, num_targets,
                                   N, alpha, max_attn_len, ctx_len, None, False, 0, qkv_scale, qkv_scale, qkv_scale,
                                   attn_bias=attn_bias, dbias=dbias)
-        # bf16 projection backward on the recomputed LN(x)
-        xn, _, _, _ = _ln_fwd(x, None, nw, nb, eps, 0.0, False, False, False, False, "none", 0, False, 1.0)
-        d_w = torch.mm(xn.t(), duvqk).to(W.dtype)
-        d_b = torch.sum(duvqk, 0, dtype=torch.float32).to(W.dtype)
-        dxn = torch.mm(duvqk, W.to(duvqk.dtype).t())
+        # projection backward on the recomputed bf16 LN(x): the FP8 dgrad arm
+        # (DLRM_HSTU_FP8_BWD_UVQK=1, after its warm-up), else bf16 GEMMs
+        def recompute_normed_x() -> torch.Tensor:
+            return _ln_fwd(x, None, nw, nb, eps, 0.0, False, False, False, False, "none", 0, False, 1.0)[0]
+
+        fp8_grads = bwd_fp8.uvqk_projection_backward(duvqk, None, None, W, recompute_normed_x=recompute_normed_x)
+        if fp8_grads is not None:
+            dxn, d_w, d_b = fp8_grads
+        else:
+            xn = recompute_normed_x()
+            d_w = token_wgrad(xn, duvqk)
+            d_b = torch.sum(duvqk, 0, dtype=torch.float32)
+            dxn = torch.mm(duvqk, W.to(duvqk.dtype).t())
+        d_w, d_b = d_w.to(W.dtype), d_b.to(W.dtype)
         dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False)
         return (dx, dnw.to(nw.dtype), dnb.to(nb.dtype), None, None, None, None, d_w, d_b, None, None, None, None,
                 None, None, None, None, None, None if dbias is None else dbias.to(attn_bias.dtype))

@@ -1,0 +1,72 @@
+"""Weight gradients over the token axis, ``a^T b`` for row-major [T, N1] and
+[T, N2] operands (one token per row), on this build's split-K kernel
+(``hstu_wgrad``).
+
+Reference call sites (paths relative to
+``recommendation_v4/hstu/generative_recommenders/``):
+
+* ``dw = torch.mm(x.t(), dz)`` of ``triton_addmm_bwd``
+  (``ops/triton/triton_addmm.py:1737-1750``): the UVQK projection's wgrad;
+* ``torch.mm(y.t(), dout)`` of the output block's backward
+  (``ops/triton/triton_hstu_linear.py``): the output projection's wgrad;
+* the split-K-over-tokens scheme with a fixed-order second pass of
+  ``fp8_wgrad`` (``ops/triton/fp8_wgrad.py:27-160``).
+
+``wgrad`` raises when the library is missing; ``token_wgrad`` takes the
+kernel for the shapes it serves (N1, N2 multiples of 256, bf16) and
+``torch.mm`` on the device for any other.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+
+def supported(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return (a.dim() == 2 and b.dim() == 2 and a.shape[0] == b.shape[0] and a.dtype == torch.bfloat16
+            and b.dtype == torch.bfloat16 and a.shape[1] % 256 == 0 and b.shape[1] % 256 == 0 and a.is_cuda
+            and b.is_cuda)
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0) else t.contiguous()
+
+
+def wgrad(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16, split: Optional[int] = None,
+          scale_a: Optional[torch.Tensor] = None, scale_b: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``(a * scale_a)^T @ (b * scale_b)`` [N1, N2] with fp32 accumulation, for
+    bf16 a [T, N1] and b [T, N2]; the scales are one-element fp32 device
+    tensors or None (1).  ``split``: token ranges (None: about one workgroup
+    per CU)."""
+    if not supported(a, b):
+        raise NotImplementedError("hstu_wgrad takes bf16 [T, N1], [T, N2] device operands, N1, N2 % 256 == 0")
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise NotImplementedError("hstu_wgrad writes bf16 or fp32")
+    a, b = _rows(a.detach()), _rows(b.detach())
+    T, n1 = a.shape
+    n2 = b.shape[1]
+    sp = 0 if split is None else int(split)
+    ws_bytes = int(_lib.fn("hstu_wgrad_workspace_bytes")(T, n1, n2, sp))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=a.device)
+    out = torch.empty((n1, n2), dtype=out_dtype, device=a.device)
+    sa = None if scale_a is None else scale_a.to(torch.float32).reshape(-1)[:1].contiguous()
+    sb = None if scale_b is None else scale_b.to(torch.float32).reshape(-1)[:1].contiguous()
+    code = _lib.HSTU_DTYPE_FP32 if out_dtype == torch.float32 else _lib.HSTU_DTYPE_BF16
+    st = _lib.fn("hstu_wgrad")(
+        _lib.HSTU_DTYPE_BF16, a.data_ptr(), a.stride(0), _lib.HSTU_DTYPE_BF16, b.data_ptr(), b.stride(0), T, n1, n2,
+        None if sa is None else sa.data_ptr(), None if sb is None else sb.data_ptr(), out.data_ptr(), out.stride(0),
+        code, sp, ws.data_ptr(), ws_bytes, torch.cuda.current_stream(a.device).cuda_stream)
+    _lib.check(st, "hstu_wgrad")
+    return out
+
+
+def token_wgrad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a^T b`` in bf16: the split-K kernel where it serves the shapes, else
+    ``torch.mm``."""
+    if supported(a, b):
+        return wgrad(a, b)
+    return torch.mm(a.t(), b)

@@ -15,9 +15,14 @@ s_x, per-column e4m3 weights, V/Q/K at s_qkv, the LN * U output at s_out)
 while gradients flow as in the reference's default backward: bf16 dgrad /
 wgrad GEMMs on the unquantized weights and the recomputed LN(x) / y, and the
 attention backward on the e4m3 V/Q/K values (a straight-through estimator at
-each quantizer).  Parity pins: those of the composed functions; the
-composition itself is checked for shapes, the residual gradient (= dY) and
-agreement with plain autograd when the quantizers are identities.
+each quantizer).  With ``grad_scales`` the output and / or UVQK projection's
+dgrad runs as the FP8 backward arm does (``ops/triton/bwd_fp8.py:1347-1395,
+2313-2520``): the incoming gradient cast to e5m2 at the given scale, the
+weight to per-tensor e4m3 (amax / 448), the wgrad and bias gradient exact.
+Parity pins: those of the composed functions; the composition itself is
+checked for shapes, the residual gradient (= dY) and agreement with plain
+autograd when the quantizers are identities; the FP8 dgrad against
+``hstu_bwd_fp8_oracle.dgrad`` of the same quantized operands.
 """
 
 from __future__ import annotations
@@ -28,6 +33,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from oracle import hstu_bwd_fp8_oracle as BO
 from oracle import hstu_ln_oracle as L
 from oracle import hstu_oracle as orc
 
@@ -49,20 +55,47 @@ def _q_weight_cols(w_kn: torch.Tensor) -> torch.Tensor:
     return orc.dequantize(w8, ws).double().t()
 
 
+class _Fp8DgradMatmul(torch.autograd.Function):
+    """a @ w in the forward; in the backward d(a) = e5m2(g / s_g) s_g .
+    (e4m3(w / s_w) s_w)^T with s_w = amax(w) / 448, and d(w) = a^T g."""
+
+    @staticmethod
+    def forward(ctx, a, w, s_g):
+        ctx.save_for_backward(a, w)
+        ctx.s_g = s_g
+        return a @ w
+
+    @staticmethod
+    def backward(ctx, g):
+        a, w = ctx.saved_tensors
+        g8 = (g / ctx.s_g).clamp(-57344.0, 57344.0).to(torch.float8_e5m2)
+        ws = float(BO.weight_scale(w))
+        w8 = (w.detach() / ws).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+        d_a = BO.dgrad(g8, ctx.s_g, w8, ws)
+        return d_a, a.t() @ g, None
+
+
+def fp8_dgrad_matmul(a: torch.Tensor, w: torch.Tensor, s_g: Optional[float]) -> torch.Tensor:
+    return a @ w if s_g is None else _Fp8DgradMatmul.apply(a, w, s_g)
+
+
 def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128, hidden_dim=128, eps=1e-6,
                    alpha=None, s_x=None, s_qkv=None, s_out=None, dropout_ratio=0.0, mask=None, attn_bias=None,
-                   quantize=True):
+                   quantize=True, grad_scales=None):
     """Layer output [T, E] (float64, differentiable w.r.t. x and every
     parameter tensor in ``params``).  ``s_*`` = None with ``quantize`` keeps
     that stage in full precision; ``quantize=False`` disables every
-    quantizer."""
+    quantizer.  ``grad_scales``: {"output_projection": s, "uvqk_projection":
+    s} -- the e5m2 gradient scale of each projection whose dgrad runs in
+    FP8."""
+    gs = grad_scales or {}
     H, Dq, Dv = num_heads, attn_dim, hidden_dim
     nu = H * Dv
     T = x.shape[0]
     alpha = alpha if alpha is not None else 1.0 / Dq ** 0.5
     p = params
     xn = F.layer_norm(x, (x.shape[1],), p["input_norm_weight"], p["input_norm_bias"], eps)
-    uvqk_f = xn @ p["uvqk_weight"] + p["uvqk_bias"]
+    uvqk_f = fp8_dgrad_matmul(xn, p["uvqk_weight"], gs.get("uvqk_projection")) + p["uvqk_bias"]
     if quantize and s_x is not None:
         xq = _q_tensor(xn, s_x)
         uvqk_q = xq @ _q_weight_cols(p["uvqk_weight"]) + p["uvqk_bias"].detach()
@@ -86,7 +119,7 @@ def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128
                                    dropout_ratio=dropout_ratio, mask=mask, silu_u=True, concat_u=True,
                                    concat_x=True, mul_u_activation_type="silu")
     W = p["output_weight"]
-    full = y @ W
+    full = fp8_dgrad_matmul(y, W, gs.get("output_projection"))
     if quantize and s_out is not None:
         val = _q_tensor(y, s_out) @ _q_weight_cols(W)
     else:

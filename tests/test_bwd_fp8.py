@@ -181,3 +181,150 @@ def test_output_block_backward_with_fp8_dgrad(hip_lib, monkeypatch):
         assert _rel(r, f) <= 8e-2
         assert not torch.equal(r, f)                          # the FP8 path ran
     B.reset_sites()
+
+
+def test_oracle_colsum_closed_forms():
+    M, N = 1000, 512
+    c = torch.linspace(-3, 3, N).to(torch.bfloat16).float()
+    x = c[None, :].expand(M, N).clone()
+    x[:, :128] = torch.where(torch.arange(M)[:, None] % 2 == 0, 1.5, -1.5).expand(M, 128)
+    out, amax, cs = O.cast_amax_colsum(x.to(torch.bfloat16), 0.5, E5M2, 57344.0, pad_to=128)
+    assert out.shape == (1024, N) and out.dtype == E5M2
+    assert bool((out[M:].view(torch.uint8) == 0).all())
+    q, a = O.cast_amax(x.to(torch.bfloat16), 0.5, E5M2, 57344.0)
+    assert torch.equal(out[:M].view(torch.uint8), q.view(torch.uint8)) and float(amax) == float(a)
+    assert torch.equal(cs[:128], torch.zeros(128, dtype=torch.float64))      # alternating +-1.5, M even
+    assert torch.equal(cs[128:], (c[128:] * M).double())                       # constant columns
+    z, za, zc = O.cast_amax_colsum(torch.zeros(0, 256, dtype=torch.bfloat16), 1.0, E5M2, 57344.0, pad_to=128)
+    assert z.shape == (0, 256) and float(za) == 0.0 and torch.equal(zc, torch.zeros(256, dtype=torch.float64))
+
+
+def test_oracle_uvqk_backward_unquantized_is_autograd():
+    """With unquantized operands (scale 1) the oracle's three gradients are
+    those of z = x W + b (a transposed operand or a dropped term fails)."""
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(37, 64, generator=g, dtype=torch.float64, requires_grad=True)
+    W = torch.randn(64, 256, generator=g, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(256, generator=g, dtype=torch.float64, requires_grad=True)
+    dz = torch.randn(37, 256, generator=g, dtype=torch.float64)
+    (x @ W + b).backward(dz)
+    d_x, d_w, d_b = O.uvqk_backward(dz, x.detach(), dz, 1.0, W.detach(), 1.0)
+    assert torch.allclose(d_x, x.grad) and torch.allclose(d_w, W.grad) and torch.allclose(d_b, b.grad)
+
+
+def test_uvqk_controller_declines_and_snapshot(monkeypatch):
+    """Host logic of uvqk_projection_backward on the CPU: declines, the
+    warm-up, and the decode-scale snapshot on a refresh call (the cast, the
+    weight cast and the GEMM are the oracle's)."""
+    import hstu_amd.bwd_fp8 as B
+
+    W = torch.randn(128, 256).to(torch.bfloat16).requires_grad_(True)
+    dz = torch.randn(64, 256).to(torch.bfloat16)
+    xn = torch.randn(64, 128).to(torch.bfloat16)
+    monkeypatch.delenv("DLRM_HSTU_FP8_BWD_UVQK", raising=False)
+    assert B.uvqk_projection_backward(dz, xn, None, W) is None                 # off by default
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e4m3")
+    assert B.uvqk_projection_backward(dz, xn, None, W) is None                 # needs e5m2
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e5m2")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "2")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "3")
+    B.reset_sites()
+    assert B.uvqk_projection_backward(dz, xn, None, W.detach()) is None        # not the leaf parameter
+    assert B.uvqk_projection_backward(dz[:, :200].contiguous(), xn, None, W[:, :200]) is None  # N % 256
+    assert B.uvqk_projection_backward(dz, None, None, W) is None               # no normed_x at all
+    assert not B._sites                                                        # declines touch no state
+    seen = []
+
+    def cast(v, inv, pad_to=1, out=None, dtype=None):
+        q, a, cs = O.cast_amax_colsum(v, float(inv.reshape(-1)[0]), E5M2, 57344.0, pad_to)
+        return q, a.float(), cs.float()
+
+    def gemm(g8, gs, w8, ws, out_dtype=torch.bfloat16):
+        seen.append(float(gs.reshape(-1)[0]))
+        return O.dgrad(g8, float(gs.reshape(-1)[0]), w8, float(ws.reshape(-1)[0])).to(out_dtype)
+
+    monkeypatch.setattr(B, "quantize_amax_colsum", cast)
+    monkeypatch.setattr(B, "quantize_weight", lambda w: (
+        (w.float() / O.weight_scale(w)).to(E4M3), O.weight_scale(w)))
+    monkeypatch.setattr(B, "fp8_dgrad", gemm)
+    amaxes = [2.0, 3.0, 1.0, 5.0]
+    outs = []
+    for a in amaxes:
+        d = dz.float() / dz.float().abs().max() * a
+        outs.append(B.uvqk_projection_backward(d.to(torch.bfloat16), None, None, W, recompute_normed_x=lambda: xn))
+    assert outs[0] is None and outs[1] is None                                  # warm-up
+    st = B._sites["uvqk_projection.L0"]
+    s0 = O.published_scale(3.0, 8.0, 57344.0)
+    assert seen[0] == pytest.approx(s0, rel=1e-6)                              # call 3 decodes with the cast's scale
+    assert seen[1] == pytest.approx(O.published_scale(1.0, 8.0, 57344.0), rel=1e-6)  # refreshed after call 3
+    d_x, d_w, d_b = outs[2]
+    assert d_w.shape == (128, 256) and d_b.dtype == torch.float32 and d_x.shape == (64, 128)
+    B.reset_sites()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,N,pad,ld", [(1000, 2048, 1, 2048), (513, 512, 128, 512), (1, 256, 128, 264),
+                                        (0, 256, 128, 256), (3 * 512 + 7, 768, 1, 768)])
+@pytest.mark.parametrize("dst", [E5M2, E4M3])
+def test_cast_amax_colsum_bit_exact(hip_lib, M, N, pad, ld, dst):
+    """Payload and amax equal to the oracle's; rows past M zero; colsum within
+    the fp32 summation bound of the float64 sum."""
+    import hstu_amd.bwd_fp8 as B
+
+    g = torch.Generator().manual_seed(M + N)
+    base = torch.randn(M, ld, generator=g) * torch.exp(torch.randn(M, ld, generator=g) * 2)
+    if M > 3:
+        base[:3, :3] = torch.tensor([[0.0, 7e4, -9e4], [1e-30, -0.0, 3.0], [2.0 ** -20, 1.0, -1.0]])
+    x = base.to(torch.bfloat16)[:, :N]                                          # row stride ld
+    inv = torch.tensor([0.37], dtype=torch.float32)
+    lim = 57344.0 if dst == E5M2 else 448.0
+    xd = x.cuda() if ld == N else base.to(torch.bfloat16).cuda()[:, :N]
+    q, amax, cs = B.quantize_amax_colsum(xd, inv.cuda(), pad_to=pad, dtype=dst)
+    wq, wamax, wcs = O.cast_amax_colsum(x, float(inv), dst, lim, pad_to=pad)
+    assert q.shape == wq.shape
+    assert torch.equal(q.cpu().view(torch.uint8), wq.view(torch.uint8))
+    assert float(amax) == float(wamax)
+    stripes = (M + 511) // 512
+    bound = (72 + stripes) * 2.0 ** -24 * x.double().abs().sum(0) + 1e-30
+    assert bool(((cs.cpu().double() - wcs).abs() <= bound).all())
+
+
+@pytest.mark.gpu
+def test_uvqk_projection_backward_warmup_then_fp8(hip_lib, monkeypatch):
+    import hstu_amd.bwd_fp8 as B
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
+    B.reset_sites()
+    g = torch.Generator(device="cuda").manual_seed(9)
+    W = (torch.randn(512, 2048, device="cuda", generator=g) / 25).to(torch.bfloat16).requires_grad_(True)
+    res = []
+    for i in range(6):
+        dz = torch.randn(1000, 2048, device="cuda", generator=g).to(torch.bfloat16)
+        xn = torch.randn(1000, 512, device="cuda", generator=g).to(torch.bfloat16)
+        res.append((dz, xn, B.uvqk_projection_backward(dz, xn, None, W)))
+    assert all(r is None for _, _, r in res[:4])
+    st = B._sites["uvqk_projection.L0"]
+    for dz, xn, r in res[4:]:
+        d_x, d_w, d_b = r
+        assert d_x.dtype == torch.bfloat16 and d_x.shape == (1000, 512)
+        ref_x = dz.double() @ W.detach().double().t()
+        assert _rel(ref_x, d_x) <= 8e-2
+        # against the same quantized operands: the GEMM's accumulation only
+        dz8, _, cs = O.cast_amax_colsum(dz.cpu(), float(st.inv_scale), E5M2, 57344.0)
+        w8, ws = (W.detach().float().cpu() / O.weight_scale(W.cpu())).to(E4M3), O.weight_scale(W.cpu())
+        rx, rw, rb = O.uvqk_backward(dz, xn, dz8, float(st.scale), w8, float(ws))
+        assert _rel(rx, d_x.cpu()) <= 4e-3
+        assert _rel(rw, d_w.cpu()) <= 1e-2
+        assert _rel(rb, d_b.cpu()) <= 1e-5
+    B.reset_sites()
+
+
+def test_oracle_wgrad_closed_forms():
+    g = torch.Generator().manual_seed(4)
+    b = torch.randn(50, 24, generator=g)
+    assert torch.allclose(O.wgrad(torch.ones(50, 3), b), b.double().sum(0)[None, :].expand(3, 24))
+    a = torch.randn(50, 7, generator=g)
+    hot = torch.zeros(50, 5)
+    hot[torch.arange(5) * 3, torch.arange(5)] = 1.0                        # token 3c -> column c
+    assert torch.allclose(O.wgrad(a, hot, 2.0, 0.5), a.double()[torch.arange(5) * 3].t())

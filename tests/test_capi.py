@@ -194,3 +194,61 @@ def test_do_quantizer_rejects_before_launch():
     assert f(H=8, rs=1024) == lib.HSTU_E_UNSUPPORTED  # H * D = 1024
     assert f(x=X + 8) == lib.HSTU_E_UNSUPPORTED    # rows read as 16-byte pieces
     assert f(B=0) == 0
+
+
+def test_colsum_cast_rejects_before_launch():
+    import hstu_amd._lib as lib
+
+    wsb = lib.fn("hstu_cast_fp8_amax_colsum_workspace_bytes")
+    assert wsb(1000, 2048) == 2 * 2048 * 4 + 256          # 2 stripes of 512 rows; 16 amax partials -> 256 B
+    assert wsb(0, 256) == 0
+    assert wsb(10, 300) == -1 and wsb(-1, 256) == -1
+    cast = lib.fn("hstu_cast_fp8_amax_colsum")
+    X, W = 4096, 8192
+
+    def f(**kw):
+        a = dict(x=X, ldx=2048, rows=1000, cols=2048, inv=W, odt=lib.HSTU_DTYPE_FP8_E5M2, lim=57344.0, out=X,
+                 rows_out=1000, colsum=W, amax=W, ws=W, wsb=wsb(1000, 2048), stream=None)
+        a.update(kw)
+        return cast(*a.values())
+
+    assert f(odt=lib.HSTU_DTYPE_BF16) == lib.HSTU_E_BAD_ARG
+    assert f(rows_out=999) == lib.HSTU_E_BAD_ARG             # padding rows below the input rows
+    assert f(ldx=1024) == lib.HSTU_E_BAD_ARG
+    assert f(lim=0.0) == lib.HSTU_E_BAD_ARG
+    assert f(wsb=100) == lib.HSTU_E_BAD_ARG
+    assert f(colsum=None) == lib.HSTU_E_BAD_ARG
+    assert f(cols=300, ldx=304) == lib.HSTU_E_UNSUPPORTED    # columns in blocks of 256
+    assert f(x=X + 8) == lib.HSTU_E_UNSUPPORTED              # 16-byte row pieces
+    assert f(ldx=2052) == lib.HSTU_E_UNSUPPORTED
+
+
+def test_wgrad_rejects_before_launch():
+    import hstu_amd._lib as lib
+
+    split = lib.fn("hstu_wgrad_split")
+    wsb = lib.fn("hstu_wgrad_workspace_bytes")
+    assert split(162251, 512, 2048, 0) == 16                 # 16 tiles -> one workgroup per CU
+    assert split(1000, 512, 2048, 0) == 8                    # at least 4 k-steps of 32 tokens per split
+    assert split(1000, 512, 2048, 1) == 1 and wsb(1000, 512, 2048, 1) == 0
+    assert wsb(162251, 512, 2048, 0) == 16 * 512 * 2048 * 4
+    assert split(100, 300, 256, 0) == -1 and split(0, 256, 256, 0) == 0
+    f = lib.fn("hstu_wgrad")
+    X, W = 4096, 8192
+    bf, f32 = lib.HSTU_DTYPE_BF16, lib.HSTU_DTYPE_FP32
+
+    def g(**kw):
+        a = dict(adt=bf, A=X, lda=512, bdt=bf, B=X, ldb=2048, T=1000, N1=512, N2=2048, sa=None, sb=None, out=W,
+                 ldo=2048, odt=bf, split=0, ws=W, wsb=wsb(1000, 512, 2048, 0), stream=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert g(odt=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_BAD_ARG
+    assert g(lda=256) == lib.HSTU_E_BAD_ARG
+    assert g(ldo=1024) == lib.HSTU_E_BAD_ARG
+    assert g(T=-1) == lib.HSTU_E_BAD_ARG
+    assert g(wsb=100) == lib.HSTU_E_BAD_ARG
+    assert g(adt=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_UNSUPPORTED
+    assert g(N1=384, lda=384) == lib.HSTU_E_UNSUPPORTED       # 256-wide tiles
+    assert g(A=X + 2) == lib.HSTU_E_UNSUPPORTED
+    assert g(odt=f32, out=W + 8) == lib.HSTU_E_UNSUPPORTED    # fp32 rows stored 16 bytes at a time

@@ -77,3 +77,49 @@ def test_hstu_layer_fwd_bwd(hip_lib, monkeypatch, fp8, with_bias, dropout):
     for name, r, got in grads:
         e = _rel_l2(r, got.float().cpu())
         assert e <= tol_grad, f"{name} rel L2 {e:.3e}"
+
+
+def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch):
+    """The FP8 layer with both e5m2 dgrad arms engaged (output projection and
+    UVQK, one warm-up call each): the second step against the oracle with the
+    same gradient quantizers at the scales the sites published, at the FP8
+    layer's tolerances (output 1.5e-2, gradients 3e-2)."""
+    import hstu_amd
+    import hstu_amd.bwd_fp8 as B
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "1")
+    B.reset_sites()
+    lengths = np.array([300, 77, 512, 129])
+    T, N, E = int(lengths.sum()), 512, 512
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    params = LO.make_layer_params(E, seed=5)
+    s_x, s_qkv = _calibrate(x, params)
+    s_out = 0.05
+    dy = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    offs = orc.offsets_from_lengths(lengths).to(DEV)
+    pd = {k: v.to(DEV).requires_grad_(True) for k, v in params.items()}
+    sc = (lambda s: torch.full((1, 1), s, device=DEV))
+    for _ in range(2):                      # step 1 publishes the scales (bf16), step 2 runs FP8
+        for t in pd.values():
+            t.grad = None
+        xd = x.to(DEV).requires_grad_(True)
+        out = hstu_amd.hstu_layer(xd, offs, N, pd, dropout_ratio=0.0, training=True, fp8_input_scale=sc(s_x),
+                                  fp8_qkv_scale=sc(s_qkv), fp8_output_scale=sc(s_out))
+        out.backward(dy.to(DEV))
+    assert B._sites["uvqk_projection.L0"].calls == 2 and B._sites["output_projection.L0"].calls == 2
+    xr = x.double().requires_grad_(True)
+    pr = {k: v.double().requires_grad_(True) for k, v in params.items()}
+    scales = {s: float(B._sites[f"{s}.L0"].scale) for s in ("output_projection", "uvqk_projection")}
+    ref = LO.hstu_layer_ref(xr, pr, lengths, N, s_x=s_x, s_qkv=s_qkv, s_out=s_out, dropout_ratio=0.0, quantize=True,
+                            grad_scales=scales)
+    ref.backward(dy.double())
+    e = _rel_l2(ref.detach(), out.detach().cpu())
+    assert e <= 1.5e-2, f"out rel L2 {e:.3e}"
+    for name, r, got in [("dx", xr.grad, xd.grad)] + [(f"d{k}", pr[k].grad, pd[k].grad) for k in params]:
+        e = _rel_l2(r, got.float().cpu())
+        assert e <= 3e-2, f"{name} rel L2 {e:.3e}"
+    B.reset_sites()

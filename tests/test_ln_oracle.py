@@ -201,3 +201,28 @@ def test_layer_oracle_composition_gradcheck():
     # the residual: d out / d x contains the identity
     out = f(*args)
     assert out.shape == x.shape
+
+
+def test_layer_oracle_fp8_dgrad_matmul_is_dgrad_of_quantized_operands():
+    """The layer oracle's FP8-dgrad projection: d(a) equals the bwd oracle's
+    dgrad of the e5m2 gradient and per-tensor e4m3 weight, d(w) = a^T g
+    exactly, and the forward is a @ w."""
+    from oracle import hstu_bwd_fp8_oracle as BO
+    from oracle import hstu_layer_oracle as LO
+
+    g = torch.Generator().manual_seed(6)
+    a = torch.randn(33, 64, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(64, 96, generator=g, dtype=torch.float64, requires_grad=True)
+    dz = torch.randn(33, 96, generator=g, dtype=torch.float64)
+    s = float(dz.abs().max()) * 8 / 57344
+    out = LO.fp8_dgrad_matmul(a, w, s)
+    assert torch.equal(out.detach(), (a @ w).detach())
+    out.backward(dz)
+    g8 = (dz / s).to(torch.float8_e5m2)
+    ws = float(w.detach().abs().max().float() / 448)
+    w8 = (w.detach() / ws).to(torch.float8_e4m3fn)
+    assert torch.allclose(a.grad, BO.dgrad(g8, s, w8, ws), rtol=1e-12, atol=0)
+    assert torch.allclose(w.grad, a.detach().t() @ dz, rtol=1e-12, atol=0)
+    rel = float((a.grad - dz @ w.detach().t()).norm() / (dz @ w.detach().t()).norm())
+    assert 1e-3 < rel < 0.1                                                    # quantized, but close
+    assert LO.fp8_dgrad_matmul(a, w, None).grad_fn is not None

@@ -1,0 +1,59 @@
+"""The split-K token-axis wgrad kernel (hstu_wgrad) against the float64
+oracle: a^T b of the same bf16 operands.
+
+Tolerances: fp32 output relative L2 <= 1e-5 (bf16 products are exact in fp32;
+only the fp32 summation order differs); bf16 output relative L2 <= 4e-3 and
+max |err| <= 2^-7 max |ref| (one bf16 rounding).  The fixed-order split
+reduction is checked bitwise: two calls give the same bytes."""
+
+import pytest
+import torch
+
+from oracle import hstu_bwd_fp8_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(ref, got):
+    ref, got = ref.double(), got.double().cpu()
+    return float((got - ref).norm() / ref.norm().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("T,N1,N2,split", [(1000, 512, 2048, None), (5000, 1536, 512, None), (777, 256, 256, 1),
+                                           (4099, 512, 512, 3), (1, 256, 512, None), (33, 768, 256, 7)])
+def test_wgrad_against_fp64(hip_lib, T, N1, N2, split):
+    from hstu_amd.wgrad import wgrad
+
+    g = torch.Generator(device="cuda").manual_seed(T + N1)
+    a = torch.randn(T, N1, device="cuda", generator=g).to(torch.bfloat16)
+    b = torch.randn(T, N2, device="cuda", generator=g).to(torch.bfloat16)
+    ref = O.wgrad(a, b)
+    out32 = wgrad(a, b, out_dtype=torch.float32, split=split)
+    assert out32.shape == (N1, N2) and out32.dtype == torch.float32
+    assert _rel(ref, out32) <= 1e-5
+    out16 = wgrad(a, b, split=split)
+    assert _rel(ref, out16) <= 4e-3
+    assert float((out16.double().cpu() - ref).abs().max()) <= 2.0 ** -7 * float(ref.abs().max())
+    again = wgrad(a, b, split=split)
+    assert torch.equal(out16, again)
+
+
+def test_wgrad_strided_operands_scales_and_empty(hip_lib):
+    """Column slices of wider buffers (the layer's d(uvqk) blocks), device
+    scales, and T = 0 (zeros)."""
+    from hstu_amd.wgrad import token_wgrad, wgrad
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    big_a = torch.randn(3001, 1024, device="cuda", generator=g).to(torch.bfloat16)
+    big_b = torch.randn(3001, 2048, device="cuda", generator=g).to(torch.bfloat16)
+    a, b = big_a[:, 256:768], big_b[:, 512:1536]
+    sa = torch.tensor([0.5], device="cuda")
+    sb = torch.tensor([3.0], device="cuda")
+    out = wgrad(a, b, out_dtype=torch.float32, scale_a=sa, scale_b=sb)
+    assert _rel(O.wgrad(a, b, 0.5, 3.0), out) <= 1e-5
+    z = wgrad(a[:0], b[:0])
+    assert z.shape == (512, 1024) and not bool(z.any())
+    # token_wgrad: the kernel for served shapes, torch.mm otherwise
+    assert _rel(O.wgrad(a, b), token_wgrad(a, b)) <= 4e-3
+    c = big_a[:, :300]
+    assert _rel(O.wgrad(c, b), token_wgrad(c, b)) <= 4e-3
