@@ -71,7 +71,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--only", choices=("output_block", "layer", "layer_fp8_dgrad", "delta", "do_quant", "gemm"),
+    ap.add_argument("--only", choices=("output_block", "layer", "layer_fp8_dgrad", "delta", "do_quant", "gemm", "wgrad"),
                     default=None,
                     help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
@@ -250,6 +250,34 @@ def gemm_bench(torch, T, steps, warmup, flush):
         del a8, w8
     return {"workload": "BASELINE config 4: FP8 e4m3 GEMM, per-row x per-column scales, bias, bf16 out "
                         "(SiLU on the 512 U columns of UVQK)", **res, "peak_TFLOPs": PEAK_TFLOPS["fp8"]}
+
+
+def wgrad_bench(torch, T, steps, warmup, flush):
+    """The layer's two projection weight gradients at config 3's token
+    count, bf16 a^T b over the tokens with fp32 accumulation (hstu_wgrad):
+    LN(x) [T, 512]^T d(uvqk) [T, 2048] and y [T, 1536]^T dout [T, 512]."""
+    from hstu_amd.wgrad import wgrad
+
+    g = torch.Generator(device="cuda").manual_seed(17)
+    res = {}
+    for name, n1, n2 in (("uvqk", 512, 2048), ("out_proj", 1536, 512)):
+        a = torch.randn(T, n1, device="cuda", generator=g).to(torch.bfloat16)
+        b = torch.randn(T, n2, device="cuda", generator=g).to(torch.bfloat16)
+
+        def run(ev):
+            if ev is not None:
+                ev[0].record()
+            wgrad(a, b)
+            if ev is not None:
+                ev[1].record()
+
+        t, _ = _cold_events(torch, run, steps, warmup, flush)
+        m = float(np.median(t))
+        res[name] = {"T": T, "N1": n1, "N2": n2, "ms": round(m, 4),
+                     "TFLOP/s": round(2 * T * n1 * n2 / (m * 1e-3) / 1e12, 1)}
+        del a, b
+    return {"workload": "layer weight gradients a^T b over T tokens, bf16 in, fp32 accumulate, bf16 out "
+                        "(split-K kernel + fixed-order reduce)", **res, "peak_TFLOPs": PEAK_TFLOPS["bf16"]}
 
 
 def output_block_bench(torch, T, steps, warmup, flush):
@@ -543,6 +571,9 @@ def main():
     if args.only == "do_quant":
         print(json.dumps(do_quant_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
         return
+    if args.only == "wgrad":
+        print(json.dumps(wgrad_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
+        return
     w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
     wall_ms, st, parts = w8.run(args.steps, args.warmup, flush)
     total = w8.flops("step")
@@ -611,6 +642,7 @@ def main():
         res["delta"] = delta_bench(torch, lengths, N, args.steps, 3, flush)
         res["do_quant"] = do_quant_bench(torch, lengths, N, args.steps, 3, flush)
         res["gemm"] = gemm_bench(torch, int(np.sum(lengths)), args.steps, 3, flush)
+        res["wgrad"] = wgrad_bench(torch, int(np.sum(lengths)), args.steps, 3, flush)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(lengths, H, D, N, args.cpu_seconds)

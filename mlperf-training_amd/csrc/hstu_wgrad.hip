@@ -42,11 +42,11 @@ namespace {
 using namespace hstu;
 
 constexpr int kWThreads = 512;                 // 8 waves
-constexpr int kBN1 = 256, kBN2 = 256, kKT = 32;  // tile and tokens per k-step
+constexpr int kBN1 = 256, kBN2 = 256, kKT = 64;  // tile and tokens per k-step
 constexpr int kWPitch = 2 * kBN1 + 32;         // 544 bytes: conflict-free transposed reads
 constexpr int kWTile = kKT * kWPitch;          // one operand's k-step tile
 constexpr int kWStage = 2 * kWTile;            // A tile then B tile
-constexpr int kWLds = 2 * kWStage;             // 68 KiB
+constexpr int kWLds = 2 * kWStage;             // 136 KiB
 constexpr int kCus = 256;
 
 struct WgradParams {
@@ -88,27 +88,28 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p)
   const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)p.ldb;
   const BufRsrc ar = make_rsrc(p.A + tb * p.lda + n10 * 2, (uint32_t)((te - tb - 1) * p.lda + kBN1 * 2));
   const BufRsrc br = make_rsrc(p.B + tb * p.ldb + n20 * 2, (uint32_t)((te - tb - 1) * p.ldb + kBN2 * 2));
-  // staging: chunk c = tid + 512 q (q = 0, 1) of a 32 x 512-byte tile
-  uint32_t va[2], vb[2], lo[2];
+  // staging: chunk c = tid + 512 q (q < kQ) of a kKT x 512-byte tile
+  constexpr int kQ = kKT * 32 / kWThreads;
+  uint32_t va[kQ], vb[kQ], lo[kQ];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < kQ; ++q) {
     const int c = tid + kWThreads * q, row = c >> 5, col = c & 31;
     va[q] = row * lda + col * 16;
     vb[q] = row * ldb + col * 16;
     lo[q] = row * kWPitch + col * 16;
   }
-  u32x4 ra[2], rb[2];
+  u32x4 ra[kQ], rb[kQ];
   auto load = [&](int kk) {
     const uint32_t sa_off = (uint32_t)kk * kKT * lda, sb_off = (uint32_t)kk * kKT * ldb;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < kQ; ++q) {
       ra[q] = buf_ld128(ar, va[q], sa_off);
       rb[q] = buf_ld128(br, vb[q], sb_off);
     }
   };
   auto store = [&](uint8_t* st) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
+    for (int q = 0; q < kQ; ++q) {
       *(u32x4*)(st + lo[q]) = ra[q];
       *(u32x4*)(st + kWTile + lo[q]) = rb[q];
     }
@@ -131,17 +132,21 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p)
   for (int kk = 0; kk < nk; ++kk) {
     const uint8_t* buf = smem + (kk & 1) * kWStage;
     if (kk + 1 < nk) load(kk + 1);
-    u32x4 af[4], bfr[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      af[i] = cat_tr(lds_tr16(buf + a_rd + 32 * i), lds_tr16(buf + a_rd + 32 * i + 16 * kWPitch));
+    for (int h = 0; h < kKT / 32; ++h) {
+      const uint8_t* hb = buf + h * 32 * kWPitch;
+      u32x4 af[4], bfr[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      bfr[j] = cat_tr(lds_tr16(buf + b_rd + 32 * j), lds_tr16(buf + b_rd + 32 * j + 16 * kWPitch));
+      for (int i = 0; i < 4; ++i)
+        af[i] = cat_tr(lds_tr16(hb + a_rd + 32 * i), lds_tr16(hb + a_rd + 32 * i + 16 * kWPitch));
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < 8; ++j)
+        bfr[j] = cat_tr(lds_tr16(hb + b_rd + 32 * j), lds_tr16(hb + b_rd + 32 * j + 16 * kWPitch));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[j][i] = mfma_bf16(bfr[j], af[i], acc[j][i]);
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[j][i] = mfma_bf16(bfr[j], af[i], acc[j][i]);
+    }
     if (kk + 1 < nk) store(smem + ((kk + 1) & 1) * kWStage);
     __syncthreads();
   }
