@@ -254,20 +254,25 @@ def gemm_bench(torch, T, steps, warmup, flush):
 
 def wgrad_bench(torch, T, steps, warmup, flush):
     """The layer's two projection weight gradients at config 3's token
-    count, bf16 a^T b over the tokens with fp32 accumulation (hstu_wgrad):
-    LN(x) [T, 512]^T d(uvqk) [T, 2048] and y [T, 1536]^T dout [T, 512]."""
+    count, a^T b over the tokens with fp32 accumulation (hstu_wgrad): LN(x)
+    [T, 512]^T d(uvqk) [T, 2048] and y [T, 1536]^T dout [T, 512], bf16
+    operands and e4m3 x e5m2 (the FP8 backward's form; peak 5 PFLOP/s)."""
     from hstu_amd.wgrad import wgrad
 
     g = torch.Generator(device="cuda").manual_seed(17)
     res = {}
-    for name, n1, n2 in (("uvqk", 512, 2048), ("out_proj", 1536, 512)):
+    one = torch.ones(1, device="cuda")
+    for name, n1, n2, f8 in (("uvqk", 512, 2048, False), ("out_proj", 1536, 512, False),
+                             ("uvqk_fp8", 512, 2048, True), ("out_proj_fp8", 1536, 512, True)):
         a = torch.randn(T, n1, device="cuda", generator=g).to(torch.bfloat16)
         b = torch.randn(T, n2, device="cuda", generator=g).to(torch.bfloat16)
+        if f8:  # e4m3 activation x e5m2 gradient (the FP8 backward's wgrad operands)
+            a, b = a.to(torch.float8_e4m3fn), b.to(torch.float8_e5m2)
 
         def run(ev):
             if ev is not None:
                 ev[0].record()
-            wgrad(a, b)
+            wgrad(a, b, scale_a=one if f8 else None, scale_b=one if f8 else None)
             if ev is not None:
                 ev[1].record()
 
@@ -276,8 +281,9 @@ def wgrad_bench(torch, T, steps, warmup, flush):
         res[name] = {"T": T, "N1": n1, "N2": n2, "ms": round(m, 4),
                      "TFLOP/s": round(2 * T * n1 * n2 / (m * 1e-3) / 1e12, 1)}
         del a, b
-    return {"workload": "layer weight gradients a^T b over T tokens, bf16 in, fp32 accumulate, bf16 out "
-                        "(split-K kernel + fixed-order reduce)", **res, "peak_TFLOPs": PEAK_TFLOPS["bf16"]}
+    return {"workload": "layer weight gradients a^T b over T tokens, bf16 or e4m3 x e5m2 in, fp32 accumulate, "
+                        "bf16 out (split-K kernel + fixed-order reduce)", **res,
+            "peak_TFLOPs": {"bf16": PEAK_TFLOPS["bf16"], "fp8": PEAK_TFLOPS["fp8"]}}
 
 
 def output_block_bench(torch, T, steps, warmup, flush):
@@ -424,14 +430,18 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     once from the data (amax * 1.25 / 448) before timing.  fp8_dgrad: the
     output and UVQK projections' dgrads in FP8 (e5m2 gradients,
     DLRM_HSTU_FP8_BWD=1 and DLRM_HSTU_FP8_BWD_UVQK=1; the UVQK gradient's cast
-    also gives the bias gradient), with enough warm-up steps for their delayed
-    scales to publish."""
+    also gives the bias gradient) and the UVQK weight gradient from the
+    forward's e4m3 LN output (DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t) and the output
+    projection's from the forward's e4m3 y (DLRM_HSTU_FP8_BWD_OUT_WGRAD=1), with enough
+    warm-up steps for their delayed scales to publish."""
     import hstu_amd
     import hstu_amd.bwd_fp8 as bwd_fp8
 
     os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
     os.environ["DLRM_HSTU_FP8_BWD"] = "1" if fp8_dgrad else "0"
     os.environ["DLRM_HSTU_FP8_BWD_UVQK"] = "1" if fp8_dgrad else "0"
+    os.environ["DLRM_HSTU_FP8_BWD_UVQK_WGRAD"] = "fp8t" if fp8_dgrad else "bf16"
+    os.environ["DLRM_HSTU_FP8_BWD_OUT_WGRAD"] = "1" if fp8_dgrad else "0"
     bwd_fp8.reset_sites()
     if fp8_dgrad:
         warmup = max(warmup, 5)
@@ -467,6 +477,8 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
     os.environ["DLRM_HSTU_FP8_BWD"] = "0"
     os.environ["DLRM_HSTU_FP8_BWD_UVQK"] = "0"
+    os.environ["DLRM_HSTU_FP8_BWD_UVQK_WGRAD"] = "bf16"
+    os.environ["DLRM_HSTU_FP8_BWD_OUT_WGRAD"] = "0"
     bwd_fp8.reset_sites()
     m = float(np.median(tot))
     P = causal_pairs(lengths)
@@ -474,7 +486,7 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     flops = 3 * gemm_fwd + 14 * D * H * P
     return {"workload": "BASELINE config 5: HSTU layer fwd+bwd in FP8 (LN -> FP8 UVQK GEMM -> FP8 attention with "
                         "bias -> LN(attn)*silu(u)*dropout -> FP8 out-proj + residual; %s), "
-                        "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj and UVQK dgrads, bf16 wgrads" if fp8_dgrad
+                        "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj and UVQK dgrads, e4m3 x e5m2 wgrads" if fp8_dgrad
                                                     else "bf16 dgrad/wgrad"),
             "T": T, "ms_per_step": round(m, 4), "fwd_ms": round(float(np.median(tf)), 4),
             "bwd_ms": round(float(np.median(tb)), 4),

@@ -27,6 +27,10 @@
 // one XCD and share its L2.  With split > 1 every workgroup writes an fp32
 // partial tile; a second kernel sums the splits in a fixed order, applies
 // sa * sb and writes bf16 or fp32 (bitwise reproducible, no atomics).
+// The fp8 form (e4m3 A, e4m3 or e5m2 B: the reference's fp8_wgrad operands)
+// takes 128-token steps of 256-byte rows through the same LDS budget, reads
+// its fragments with ds_read_b64_tr_b8 (four 8-token reads per 32-byte
+// fragment) and runs v_mfma_f32_16x16x128_f8f6f4 with the operands' formats.
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -41,13 +45,38 @@
 namespace {
 using namespace hstu;
 
-constexpr int kWThreads = 512;                 // 8 waves
-constexpr int kBN1 = 256, kBN2 = 256, kKT = 64;  // tile and tokens per k-step
-constexpr int kWPitch = 2 * kBN1 + 32;         // 544 bytes: conflict-free transposed reads
-constexpr int kWTile = kKT * kWPitch;          // one operand's k-step tile
-constexpr int kWStage = 2 * kWTile;            // A tile then B tile
-constexpr int kWLds = 2 * kWStage;             // 136 KiB
+constexpr int kWThreads = 512;  // 8 waves
+constexpr int kBN1 = 256, kBN2 = 256;  // output tile
 constexpr int kCus = 256;
+
+// Per operand format: bf16 steps of 64 tokens (512-byte tile rows, 544-byte
+// pitch) or fp8 steps of 128 tokens (256-byte rows, 272-byte pitch).  Both
+// stage 64 KiB per step and take 136 KiB of LDS for two steps.
+template <bool F8>
+struct WCfg {
+  static constexpr int KT = F8 ? 128 : 64;           // tokens per k-step
+  static constexpr int ES = F8 ? 1 : 2;              // bytes per element
+  static constexpr int ROW = kBN1 * ES;              // tile row bytes
+  static constexpr int PITCH = ROW + (F8 ? 16 : 32);  // conflict-free transposed reads
+  static constexpr int TILE = KT * PITCH;
+  static constexpr int STAGE = 2 * TILE;             // A tile then B tile
+  static constexpr int LDS = 2 * STAGE;
+  static constexpr int CPR = ROW / 16;               // 16-byte chunks per tile row
+  static constexpr int Q = KT * CPR / kWThreads;     // staged chunks per thread per operand
+};
+constexpr int kWLds = WCfg<false>::LDS;
+static_assert(WCfg<true>::LDS == kWLds, "one LDS size");
+
+// ds_read_b64_tr_b8: within a 16-lane group, lane i receives byte i % 8 of
+// the 8-byte chunks addressed by lanes 2r + i / 8, r = 0..7.  With lane j
+// addressing token row t0 + j / 2 at byte column c0 + 8 (j % 2), lane i gets
+// column c0 + i of tokens t0 .. t0 + 7, one token per byte.
+__device__ __forceinline__ u32x2 lds_tr8(const uint8_t* p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  const lds_v2i* lp = (const lds_v2i*)(__attribute__((address_space(3))) const uint8_t*)(p);
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)lp));
+}
 
 struct WgradParams {
   const uint8_t* A;
@@ -65,7 +94,11 @@ struct WgradParams {
   const float* sb;
 };
 
-__global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p) {
+// F8: A and B fp8 with MFMA formats FA / FB (0 e4m3, 1 e5m2); else bf16.
+template <bool F8, int FA, int FB>
+__global__ void __launch_bounds__(kWThreads, 1) wgrad_kernel(WgradParams p) {
+  using C = WCfg<F8>;
+  constexpr int kKT = C::KT, kWPitch = C::PITCH, kWTile = C::TILE, kWStage = C::STAGE, kQ = C::Q;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // XCD-contiguous numbering: workgroup b runs on XCD b % 8; consecutive idx
   // (one token range, all its tiles) land on one XCD.
@@ -83,17 +116,16 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p)
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
   const int w1 = (wave >> 1) * 64, w2 = (wave & 1) * 128;
 
-  // Token rows tb .. te-1 of the tile's 512-byte column band; rows past te
-  // (the next split's, or past T) read as zero.
+  // Token rows tb .. te-1 of the tile's column band; rows past te (the next
+  // split's, or past T) read as zero.
   const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)p.ldb;
-  const BufRsrc ar = make_rsrc(p.A + tb * p.lda + n10 * 2, (uint32_t)((te - tb - 1) * p.lda + kBN1 * 2));
-  const BufRsrc br = make_rsrc(p.B + tb * p.ldb + n20 * 2, (uint32_t)((te - tb - 1) * p.ldb + kBN2 * 2));
-  // staging: chunk c = tid + 512 q (q < kQ) of a kKT x 512-byte tile
-  constexpr int kQ = kKT * 32 / kWThreads;
+  const BufRsrc ar = make_rsrc(p.A + tb * p.lda + n10 * C::ES, (uint32_t)((te - tb - 1) * p.lda + C::ROW));
+  const BufRsrc br = make_rsrc(p.B + tb * p.ldb + n20 * C::ES, (uint32_t)((te - tb - 1) * p.ldb + C::ROW));
+  // staging: chunk c = tid + 512 q (q < kQ) of a kKT-row tile
   uint32_t va[kQ], vb[kQ], lo[kQ];
 #pragma unroll
   for (int q = 0; q < kQ; ++q) {
-    const int c = tid + kWThreads * q, row = c >> 5, col = c & 31;
+    const int c = tid + kWThreads * q, row = c / C::CPR, col = c % C::CPR;
     va[q] = row * lda + col * 16;
     vb[q] = row * ldb + col * 16;
     lo[q] = row * kWPitch + col * 16;
@@ -126,12 +158,35 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p)
     store(smem);
   }
   __syncthreads();
-  // transposed-read start: row 4g + li/4, 4-column group li % 4
-  const int tr = (4 * g + (li >> 2)) * kWPitch + (li & 3) * 8;
-  const int a_rd = tr + w1 * 2, b_rd = kWTile + tr + w2 * 2;
+  // transposed-read start.  bf16: row 4g + li/4, 4-column group li % 4.
+  // fp8: token row 8g + li/2 (plus 32 per read), 8-column half li % 2.
+  const int tr = F8 ? (8 * g + (li >> 1)) * kWPitch + (li & 1) * 8 : (4 * g + (li >> 2)) * kWPitch + (li & 3) * 8;
+  const int a_rd = tr + w1 * C::ES, b_rd = kWTile + tr + w2 * C::ES;
   for (int kk = 0; kk < nk; ++kk) {
     const uint8_t* buf = smem + (kk & 1) * kWStage;
     if (kk + 1 < nk) load(kk + 1);
+    if constexpr (F8) {
+      // one 128-token MFMA step: lane (li, g) holds tokens 32r + 8g .. +7 of
+      // its column in bytes 8r .. 8r+7 (r = 0..3), the same in both operands
+      auto frag = [&](const uint8_t* q0) {
+        const u32x2 r0 = lds_tr8(q0), r1 = lds_tr8(q0 + 32 * kWPitch);
+        const u32x2 r2 = lds_tr8(q0 + 64 * kWPitch), r3 = lds_tr8(q0 + 96 * kWPitch);
+        i32x8 f;
+        f[0] = (int)r0[0]; f[1] = (int)r0[1]; f[2] = (int)r1[0]; f[3] = (int)r1[1];
+        f[4] = (int)r2[0]; f[5] = (int)r2[1]; f[6] = (int)r3[0]; f[7] = (int)r3[1];
+        return f;
+      };
+      i32x8 af[4], bfr[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = frag(buf + a_rd + 16 * i);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bfr[j] = frag(buf + b_rd + 16 * j);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bfr[j], af[i], acc[j][i], FB, FA, 0, 0, 0, 0);
+    } else {
 #pragma unroll
     for (int h = 0; h < kKT / 32; ++h) {
       const uint8_t* hb = buf + h * 32 * kWPitch;
@@ -146,6 +201,7 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_bf16_kernel(WgradParams p)
       for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[j][i] = mfma_bf16(bfr[j], af[i], acc[j][i]);
+    }
     }
     if (kk + 1 < nk) store(smem + ((kk + 1) & 1) * kWStage);
     __syncthreads();
@@ -205,16 +261,17 @@ hipError_t set_wgrad_lds(const void* fn) {
 
 // tokens per split for a requested split (<= 0: about one workgroup per CU,
 // at least 4 k-steps per split), and the split that results
+constexpr int kPlanKT = 128;  // token ranges are multiples of both formats' k-steps
 void plan(int64_t T, int N1, int N2, int split, int64_t* tps, int* eff) {
   const int tiles = (N1 / kBN1) * (N2 / kBN2);
   if (split <= 0) split = (int)std::max<int64_t>(1, std::min<int64_t>(kCus / std::max(tiles, 1), (T + 127) / 128));
   if (T <= 0) {
-    *tps = kKT;
+    *tps = kPlanKT;
     *eff = 0;
     return;
   }
   const int64_t per = (T + split - 1) / split;
-  *tps = (per + kKT - 1) / kKT * kKT;
+  *tps = (per + kPlanKT - 1) / kPlanKT * kPlanKT;
   *eff = (int)((T + *tps - 1) / *tps);
 }
 
@@ -240,8 +297,11 @@ extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, 
   if (T < 0 || N1 <= 0 || N2 <= 0 || !out || (T > 0 && (!A || !B)) || lda < N1 || ldb < N2 || ldo < N2 ||
       (out_dtype != HSTU_DTYPE_BF16 && out_dtype != HSTU_DTYPE_FP32))
     return HSTU_E_BAD_ARG;
-  if (a_dtype != HSTU_DTYPE_BF16 || b_dtype != HSTU_DTYPE_BF16) return HSTU_E_UNSUPPORTED;
-  if (N1 % kBN1 || N2 % kBN2 || lda % 8 || ldb % 8 || ((uintptr_t)A | (uintptr_t)B) % 16 ||
+  const bool bf16 = a_dtype == HSTU_DTYPE_BF16 && b_dtype == HSTU_DTYPE_BF16;
+  const bool f8 = a_dtype == HSTU_DTYPE_FP8_E4M3 && (b_dtype == HSTU_DTYPE_FP8_E4M3 || b_dtype == HSTU_DTYPE_FP8_E5M2);
+  if (!bf16 && !f8) return HSTU_E_UNSUPPORTED;
+  const int es = bf16 ? 2 : 1;
+  if (N1 % kBN1 || N2 % kBN2 || (lda * es) % 16 || (ldb * es) % 16 || ((uintptr_t)A | (uintptr_t)B) % 16 ||
       (uintptr_t)out % (out_dtype == HSTU_DTYPE_FP32 ? 16 : 8) || ldo % 4)
     return HSTU_E_UNSUPPORTED;
   int64_t tps;
@@ -250,15 +310,15 @@ extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, 
   const int64_t need = eff > 1 ? (int64_t)eff * N1 * N2 * 4 : 0;
   if (workspace_bytes < need || (need > 0 && !workspace)) return HSTU_E_BAD_ARG;
   // one split's rows must stay within 32-bit buffer offsets
-  if ((tps + kKT) * std::max(lda, ldb) * 2 >= ((int64_t)1 << 32)) return HSTU_E_UNSUPPORTED;
+  if ((tps + kPlanKT) * std::max(lda, ldb) * es >= ((int64_t)1 << 32)) return HSTU_E_UNSUPPORTED;
   const int tiles = (N1 / kBN1) * (N2 / kBN2);
   const int out_f32 = out_dtype == HSTU_DTYPE_FP32;
   if (eff > 0) {
     WgradParams p{};
     p.A = (const uint8_t*)A;
     p.B = (const uint8_t*)B;
-    p.lda = lda * 2;
-    p.ldb = ldb * 2;
+    p.lda = lda * es;
+    p.ldb = ldb * es;
     p.T = T;
     p.tps = tps;
     p.N1 = N1;
@@ -275,7 +335,9 @@ extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, 
     const int64_t total = (int64_t)tiles * eff;
     if (total >= ((int64_t)1 << 31)) return HSTU_E_UNSUPPORTED;
     const int grid = (int)((total + 7) / 8 * 8);
-    const void* kern = (const void*)wgrad_bf16_kernel;
+    const void* kern = bf16 ? (const void*)wgrad_kernel<false, 0, 0>
+                       : b_dtype == HSTU_DTYPE_FP8_E5M2 ? (const void*)wgrad_kernel<true, 0, 1>
+                                                         : (const void*)wgrad_kernel<true, 0, 0>;
     hipError_t e = set_wgrad_lds(kern);
     if (e != hipSuccess) return (int)e;
     void* args[] = {&p};

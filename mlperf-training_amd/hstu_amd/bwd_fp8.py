@@ -17,7 +17,8 @@ Mirrors ``ops/triton/bwd_fp8.py`` (reference paths relative to
 * ``quantize_weight``           <- ``:1157-1189`` (e4m3 at unit margin)
 * ``output_projection_dgrad``   <- ``:1347-1395`` (dY_e5m2 . W_e4m3^T, bf16 out)
 * ``uvqk_projection_backward``  <- ``:2313-2520`` (dZ_e5m2 . W_e4m3^T dgrad, bf16
-  wgrad, the cast's column sum as the bias gradient)
+  wgrad or with ``DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t`` the e4m3 x e5m2 wgrad,
+  the cast's column sum as the bias gradient)
 
 Switches (the reference's names): ``DLRM_HSTU_FP8_BWD=1`` enables the path;
 ``DLRM_HSTU_FP8_BWD_MARGIN`` (8), ``_REFRESH_CALLS`` (200), ``_WARMUP_CALLS``
@@ -34,7 +35,7 @@ from typing import Callable, Dict, Optional, Tuple
 import torch
 
 from . import _lib
-from .wgrad import token_wgrad
+from .wgrad import fp8_wgrad, token_wgrad
 
 E4M3 = torch.float8_e4m3fn
 E5M2 = torch.float8_e5m2
@@ -261,9 +262,18 @@ def fp8_dgrad(grad8: torch.Tensor, grad_scale: torch.Tensor, w8: torch.Tensor, w
     return out
 
 
-def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor) -> Optional[torch.Tensor]:
+def out_wgrad_fp8() -> bool:
+    """``DLRM_HSTU_FP8_BWD_OUT_WGRAD=1`` (with the FP8 backward on): the output
+    projection's weight gradient from the forward's e4m3 LN * U output and the
+    dgrad's e5m2 dout cast (``triton_hstu_linear.py:87-110``)."""
+    return enabled() and os.environ.get("DLRM_HSTU_FP8_BWD_OUT_WGRAD", "0") == "1"
+
+
+def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor, return_quantized: bool = False):
     """``dy = gradient @ weight^T`` in FP8 (gradient [M, N_out], weight
-    [K_in, N_out] as stored by the layer), or None to fall back to bf16."""
+    [K_in, N_out] as stored by the layer), or None to fall back to bf16.
+    With ``return_quantized``: (dy, gradient_fp8, its decode scale), for a
+    weight gradient that reuses the cast."""
     if not enabled() or not _has_stable_identity(weight):
         return None
     if gradient.dim() != 2 or gradient.shape[-1] % 128 or weight.shape[0] % 128:
@@ -273,13 +283,22 @@ def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor) -> Opt
         return None
     g8, gs = quantized
     w8, ws = quantize_weight(weight)
-    return fp8_dgrad(g8, gs, w8, ws, gradient.dtype if gradient.dtype == torch.bfloat16 else torch.bfloat16)
+    dy = fp8_dgrad(g8, gs, w8, ws, gradient.dtype if gradient.dtype == torch.bfloat16 else torch.bfloat16)
+    return (dy, g8, gs) if return_quantized else dy
 
 
 def uvqk_fp8_backward_enabled() -> bool:
     """``DLRM_HSTU_FP8_BWD_UVQK=1`` with the e5m2 gradient format."""
     return (os.environ.get("DLRM_HSTU_FP8_BWD_UVQK", "0") == "1"
             and grad_dtype_and_limit()[0] == E5M2)
+
+
+def uvqk_wgrad_fp8t() -> bool:
+    """``DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t`` (with the UVQK arm on): the UVQK
+    weight gradient from the forward's e4m3 LN output and the e5m2 gradient
+    (``uvqk_wgrad_fp8t``, ``ops/triton/bwd_fp8.py:1755-1762``)."""
+    return (uvqk_fp8_backward_enabled()
+            and os.environ.get("DLRM_HSTU_FP8_BWD_UVQK_WGRAD", "bf16").strip().lower() == "fp8t")
 
 
 def uvqk_projection_backward(
@@ -302,9 +321,11 @@ def uvqk_projection_backward(
     gradient is the bf16 product normed_x^T dz (the split-K wgrad kernel).
     ``per_layer`` keys the scale on the weight's storage (then it must be the
     leaf parameter).
-    ``normed_x`` may be None when ``recompute_normed_x`` is given.  The
-    token-major FP8 wgrad (``normed_x_fp8_t``) is not served: the wgrad stays
-    bf16 whatever ``DLRM_HSTU_FP8_BWD_UVQK_WGRAD`` says."""
+    ``normed_x`` may be None when ``recompute_normed_x`` is given.  With
+    ``uvqk_wgrad_fp8t()``, ``normed_x_fp8_t`` (the forward's e4m3 LN output,
+    here row-major [M, K] -- the kernel reads token rows directly, so no
+    token-major copy is made) and ``input_scale_value`` > 0, the weight
+    gradient is the FP8 product (x8 s_x)^T (dz8 s_dz) instead."""
     if not uvqk_fp8_backward_enabled():
         return None
     if per_layer and not _has_stable_identity(weight):
@@ -331,7 +352,14 @@ def uvqk_projection_backward(
     else:
         grad_scale = state.scale
     w8, w_scale = quantize_weight(weight)
-    xn = normed_x if normed_x is not None else recompute_normed_x()
-    d_w = token_wgrad(xn, dz)
+    use_tm = (uvqk_wgrad_fp8t() and normed_x_fp8_t is not None and input_scale_value is not None
+              and input_scale_value > 0.0 and normed_x_fp8_t.dtype == E4M3
+              and tuple(normed_x_fp8_t.shape) == (dz.shape[0], weight.shape[0]))
+    if use_tm:
+        sx = torch.full((1,), float(input_scale_value), dtype=torch.float32, device=dz.device)
+        d_w = fp8_wgrad(normed_x_fp8_t, dz8, sx, grad_scale)
+    else:
+        xn = normed_x if normed_x is not None else recompute_normed_x()
+        d_w = token_wgrad(xn, dz)
     d_x = fp8_dgrad(dz8, grad_scale, w8, w_scale)
     return d_x, d_w, colsum

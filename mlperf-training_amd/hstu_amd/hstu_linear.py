@@ -35,7 +35,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib, bwd_fp8
-from .wgrad import token_wgrad
+from .wgrad import fp8_wgrad, token_wgrad
 from .hstu_attention import HammerKernel
 from .pt_hstu_linear import pytorch_hstu_compute_output, pytorch_norm_mul_dropout
 
@@ -353,6 +353,10 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
             saved.append(y)
         if mask is not None:
             saved.append(mask)
+        # the e4m3 y feeds the FP8 output-projection weight gradient
+        ctx.y8_scale = sv if (use_fp8 and bwd_fp8.out_wgrad_fp8()) else None
+        if ctx.y8_scale is not None:
+            saved.append(y)
         ctx.save_for_backward(*saved)
         ctx.recompute = bool(recompute_y_in_backward)
         ctx.has_mask = mask is not None
@@ -371,19 +375,27 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
             y = ctx.saved_tensors[i]
             i += 1
         mask = ctx.saved_tensors[i] if ctx.has_mask else None
+        i += int(ctx.has_mask)
+        y8 = ctx.saved_tensors[i] if ctx.y8_scale is not None else None
         ratio, silu_u, concat_u, concat_x, act = ctx.cfg
         dout = dout.contiguous()
         # FP8 dgrad (DLRM_HSTU_FP8_BWD=1; triton_hstu_linear.py:5586-5588): None
         # while the gradient's scale warms up, then e5m2 dout . e4m3 W^T
-        dy = bwd_fp8.output_projection_dgrad(dout, output_weight) if bwd_fp8.enabled() else None
-        if dy is None:
-            dy = torch.mm(dout, output_weight.to(dout.dtype).t())
+        q = bwd_fp8.output_projection_dgrad(dout, output_weight, return_quantized=True) if bwd_fp8.enabled() else None
+        dy = q[0] if q is not None else torch.mm(dout, output_weight.to(dout.dtype).t())
+        # FP8 weight gradient (DLRM_HSTU_FP8_BWD_OUT_WGRAD=1) from the forward's
+        # e4m3 y and the dgrad's e5m2 dout: the bf16 y is then not recomputed
+        fp8_w = y8 is not None and q is not None
         dattn, du, dw, db, y_re = _ln_bwd(dy, attn, u, norm_weight, norm_bias, mean, rstd, ratio, mask, silu_u,
-                                          concat_u, concat_x, act, ctx.recompute, ctx.du_row_width)
-        if y is None:
-            y = y_re
-        # y^T dout over the tokens: the split-K wgrad kernel
-        d_out_w = token_wgrad(y, dout).to(output_weight.dtype)
+                                          concat_u, concat_x, act, ctx.recompute and not fp8_w, ctx.du_row_width)
+        if fp8_w:
+            sy = torch.full((1,), ctx.y8_scale, dtype=torch.float32, device=dout.device)
+            d_out_w = fp8_wgrad(y8, q[1], sy, q[2]).to(output_weight.dtype)
+        else:
+            if y is None:
+                y = y_re
+            # y^T dout over the tokens: the split-K wgrad kernel
+            d_out_w = token_wgrad(y, dout).to(output_weight.dtype)
         return (dattn, du, dout, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
                 None, None, None, None, None, None, None, None, None, None, None, None, None, None)
 

@@ -96,12 +96,16 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         attn = triton_hstu_attention_fwd(max_seq_len, attn_alpha, q, k, v, seq_offsets, num_targets, max_attn_len,
                                          contextual_seq_len, None, False, 0, qkv_scale, qkv_scale, qkv_scale,
                                          attn_bias=attn_bias)
+        # the e4m3 LN output feeds the FP8 UVQK weight gradient (fp8t switch)
+        keep_x8 = use_fp8 and bwd_fp8.uvqk_wgrad_fp8t()
         ctx.save_for_backward(x, norm_weight, norm_bias, mean, rstd, uvqk_weight, vqk, seq_offsets,
                               *([] if num_targets is None else [num_targets]),
                               *([] if attn_bias is None else [attn_bias]),
-                              *([] if u_pre is None else [u_pre]))
+                              *([] if u_pre is None else [u_pre]),
+                              *([x8] if keep_x8 else []))
         ctx.cfg = (norm_eps, H, Dq, Dv, max_seq_len, attn_alpha, max_attn_len, contextual_seq_len, qkv_scale,
                    defer_silu, num_targets is not None, attn_bias is not None, u_pre is not None)
+        ctx.x8_scale = sx if keep_x8 else None
         u = u.contiguous() if u.stride(1) != 1 else u
         setattr(u, DUVQK_WIDTH_ATTR, uvqk_weight.shape[1])
         return u, attn.view(T, H * Dv)
@@ -118,6 +122,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         attn_bias = saved[i] if has_bias else None
         i += int(has_bias)
         u_pre = saved[i] if has_upre else None
+        i += int(has_upre)
+        x8 = saved[i] if ctx.x8_scale is not None else None
         T = x.shape[0]
         nu = H * Dv
         width = W.shape[1]
@@ -144,7 +150,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         def recompute_normed_x() -> torch.Tensor:
             return _ln_fwd(x, None, nw, nb, eps, 0.0, False, False, False, False, "none", 0, False, 1.0)[0]
 
-        fp8_grads = bwd_fp8.uvqk_projection_backward(duvqk, None, None, W, recompute_normed_x=recompute_normed_x)
+        fp8_grads = bwd_fp8.uvqk_projection_backward(duvqk, None, ctx.x8_scale, W, normed_x_fp8_t=x8,
+                                                     recompute_normed_x=recompute_normed_x)
         if fp8_grads is not None:
             dxn, d_w, d_b = fp8_grads
         else:

@@ -18,7 +18,9 @@ attention backward on the e4m3 V/Q/K values (a straight-through estimator at
 each quantizer).  With ``grad_scales`` the output and / or UVQK projection's
 dgrad runs as the FP8 backward arm does (``ops/triton/bwd_fp8.py:1347-1395,
 2313-2520``): the incoming gradient cast to e5m2 at the given scale, the
-weight to per-tensor e4m3 (amax / 448), the wgrad and bias gradient exact.
+weight to per-tensor e4m3 (amax / 448), the wgrad and bias gradient exact --
+or, for the sites in ``fp8_wgrad``, the wgrad from the e4m3 activation and
+the e5m2 gradient (``fp8_wgrad``, ``ops/triton/fp8_wgrad.py:109-160``).
 Parity pins: those of the composed functions; the composition itself is
 checked for shapes, the residual gradient (= dY) and agreement with plain
 autograd when the quantizers are identities; the FP8 dgrad against
@@ -57,12 +59,14 @@ def _q_weight_cols(w_kn: torch.Tensor) -> torch.Tensor:
 
 class _Fp8DgradMatmul(torch.autograd.Function):
     """a @ w in the forward; in the backward d(a) = e5m2(g / s_g) s_g .
-    (e4m3(w / s_w) s_w)^T with s_w = amax(w) / 448, and d(w) = a^T g."""
+    (e4m3(w / s_w) s_w)^T with s_w = amax(w) / 448, and d(w) = a^T g -- or,
+    with an activation scale s_a, the FP8 weight gradient
+    (e4m3(a / s_a) s_a)^T (e5m2(g / s_g) s_g)."""
 
     @staticmethod
-    def forward(ctx, a, w, s_g):
+    def forward(ctx, a, w, s_g, s_a):
         ctx.save_for_backward(a, w)
-        ctx.s_g = s_g
+        ctx.s_g, ctx.s_a = s_g, s_a
         return a @ w
 
     @staticmethod
@@ -72,22 +76,29 @@ class _Fp8DgradMatmul(torch.autograd.Function):
         ws = float(BO.weight_scale(w))
         w8 = (w.detach() / ws).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
         d_a = BO.dgrad(g8, ctx.s_g, w8, ws)
-        return d_a, a.t() @ g, None
+        if ctx.s_a is None:
+            d_w = a.t() @ g
+        else:
+            a8 = (a.detach() / ctx.s_a).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+            d_w = BO.wgrad(a8, g8, ctx.s_a, ctx.s_g).to(g.dtype)
+        return d_a, d_w, None, None
 
 
-def fp8_dgrad_matmul(a: torch.Tensor, w: torch.Tensor, s_g: Optional[float]) -> torch.Tensor:
-    return a @ w if s_g is None else _Fp8DgradMatmul.apply(a, w, s_g)
+def fp8_dgrad_matmul(a: torch.Tensor, w: torch.Tensor, s_g: Optional[float],
+                     s_a: Optional[float] = None) -> torch.Tensor:
+    return a @ w if s_g is None else _Fp8DgradMatmul.apply(a, w, s_g, s_a)
 
 
 def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128, hidden_dim=128, eps=1e-6,
                    alpha=None, s_x=None, s_qkv=None, s_out=None, dropout_ratio=0.0, mask=None, attn_bias=None,
-                   quantize=True, grad_scales=None):
+                   quantize=True, grad_scales=None, fp8_wgrad=()):
     """Layer output [T, E] (float64, differentiable w.r.t. x and every
     parameter tensor in ``params``).  ``s_*`` = None with ``quantize`` keeps
     that stage in full precision; ``quantize=False`` disables every
     quantizer.  ``grad_scales``: {"output_projection": s, "uvqk_projection":
     s} -- the e5m2 gradient scale of each projection whose dgrad runs in
-    FP8."""
+    FP8; ``fp8_wgrad``: the sites among those whose weight gradient is the FP8
+    product of the e4m3 activation (at s_x / s_out) and the e5m2 gradient."""
     gs = grad_scales or {}
     H, Dq, Dv = num_heads, attn_dim, hidden_dim
     nu = H * Dv
@@ -95,7 +106,8 @@ def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128
     alpha = alpha if alpha is not None else 1.0 / Dq ** 0.5
     p = params
     xn = F.layer_norm(x, (x.shape[1],), p["input_norm_weight"], p["input_norm_bias"], eps)
-    uvqk_f = fp8_dgrad_matmul(xn, p["uvqk_weight"], gs.get("uvqk_projection")) + p["uvqk_bias"]
+    uvqk_f = fp8_dgrad_matmul(xn, p["uvqk_weight"], gs.get("uvqk_projection"),
+                              s_x if "uvqk_projection" in fp8_wgrad else None) + p["uvqk_bias"]
     if quantize and s_x is not None:
         xq = _q_tensor(xn, s_x)
         uvqk_q = xq @ _q_weight_cols(p["uvqk_weight"]) + p["uvqk_bias"].detach()
@@ -119,7 +131,7 @@ def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128
                                    dropout_ratio=dropout_ratio, mask=mask, silu_u=True, concat_u=True,
                                    concat_x=True, mul_u_activation_type="silu")
     W = p["output_weight"]
-    full = fp8_dgrad_matmul(y, W, gs.get("output_projection"))
+    full = fp8_dgrad_matmul(y, W, gs.get("output_projection"), s_out if "output_projection" in fp8_wgrad else None)
     if quantize and s_out is not None:
         val = _q_tensor(y, s_out) @ _q_weight_cols(W)
     else:

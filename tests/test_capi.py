@@ -248,7 +248,10 @@ def test_wgrad_rejects_before_launch():
     assert g(ldo=1024) == lib.HSTU_E_BAD_ARG
     assert g(T=-1) == lib.HSTU_E_BAD_ARG
     assert g(wsb=100) == lib.HSTU_E_BAD_ARG
-    assert g(adt=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_UNSUPPORTED
+    assert g(adt=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_UNSUPPORTED          # e4m3 x bf16
+    e4, e5 = lib.HSTU_DTYPE_FP8_E4M3, lib.HSTU_DTYPE_FP8_E5M2
+    assert g(adt=e5, bdt=e5) == lib.HSTU_E_UNSUPPORTED                     # A is e4m3 (the activation)
+    assert g(adt=e4, bdt=e5, lda=520, ldb=2048) == lib.HSTU_E_UNSUPPORTED   # fp8 rows in 16-byte pieces
     assert g(N1=384, lda=384) == lib.HSTU_E_UNSUPPORTED       # 256-wide tiles
     assert g(A=X + 2) == lib.HSTU_E_UNSUPPORTED
     assert g(odt=f32, out=W + 8) == lib.HSTU_E_UNSUPPORTED    # fp32 rows stored 16 bytes at a time

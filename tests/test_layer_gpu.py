@@ -79,7 +79,8 @@ def test_hstu_layer_fwd_bwd(hip_lib, monkeypatch, fp8, with_bias, dropout):
         assert e <= tol_grad, f"{name} rel L2 {e:.3e}"
 
 
-def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch):
+@pytest.mark.parametrize("uvqk_wgrad", ["bf16", "fp8t"])
+def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch, uvqk_wgrad):
     """The FP8 layer with both e5m2 dgrad arms engaged (output projection and
     UVQK, one warm-up call each): the second step against the oracle with the
     same gradient quantizers at the scales the sites published, at the FP8
@@ -91,6 +92,8 @@ def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch):
     monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
     monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
     monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK_WGRAD", uvqk_wgrad)
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_OUT_WGRAD", "1" if uvqk_wgrad == "fp8t" else "0")
     B.reset_sites()
     lengths = np.array([300, 77, 512, 129])
     T, N, E = int(lengths.sum()), 512, 512
@@ -115,7 +118,7 @@ def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch):
     pr = {k: v.double().requires_grad_(True) for k, v in params.items()}
     scales = {s: float(B._sites[f"{s}.L0"].scale) for s in ("output_projection", "uvqk_projection")}
     ref = LO.hstu_layer_ref(xr, pr, lengths, N, s_x=s_x, s_qkv=s_qkv, s_out=s_out, dropout_ratio=0.0, quantize=True,
-                            grad_scales=scales)
+                            grad_scales=scales, fp8_wgrad=("uvqk_projection", "output_projection") if uvqk_wgrad == "fp8t" else ())
     ref.backward(dy.double())
     e = _rel_l2(ref.detach(), out.detach().cpu())
     assert e <= 1.5e-2, f"out rel L2 {e:.3e}"

@@ -226,3 +226,23 @@ def test_layer_oracle_fp8_dgrad_matmul_is_dgrad_of_quantized_operands():
     rel = float((a.grad - dz @ w.detach().t()).norm() / (dz @ w.detach().t()).norm())
     assert 1e-3 < rel < 0.1                                                    # quantized, but close
     assert LO.fp8_dgrad_matmul(a, w, None).grad_fn is not None
+
+
+
+def test_layer_oracle_fp8_wgrad_matmul_is_wgrad_of_quantized_operands():
+    """With an activation scale the oracle's weight gradient is the bwd
+    oracle's wgrad of the e4m3 activation and the e5m2 gradient."""
+    from oracle import hstu_bwd_fp8_oracle as BO
+    from oracle import hstu_layer_oracle as LO
+
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(40, 64, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(64, 32, generator=g, dtype=torch.float64, requires_grad=True)
+    dz = torch.randn(40, 32, generator=g, dtype=torch.float64)
+    s_g, s_a = float(dz.abs().max()) * 8 / 57344, float(a.detach().abs().max()) / 448
+    LO.fp8_dgrad_matmul(a, w, s_g, s_a).backward(dz)
+    a8 = (a.detach() / s_a).to(torch.float8_e4m3fn)
+    g8 = (dz / s_g).to(torch.float8_e5m2)
+    assert torch.allclose(w.grad, BO.wgrad(a8, g8, s_a, s_g), rtol=1e-12, atol=0)
+    rel = float((w.grad - a.detach().t() @ dz).norm() / (a.detach().t() @ dz).norm())
+    assert 1e-3 < rel < 0.1

@@ -1,8 +1,10 @@
 """The split-K token-axis wgrad kernel (hstu_wgrad) against the float64
-oracle: a^T b of the same bf16 operands.
+oracle: a^T b of the same bf16 operands, and (sa a8)^T (sb b8) of the same
+fp8 operands (e4m3 x e5m2 / e4m3).
 
-Tolerances: fp32 output relative L2 <= 1e-5 (bf16 products are exact in fp32;
-only the fp32 summation order differs); bf16 output relative L2 <= 4e-3 and
+Tolerances: fp32 output relative L2 <= 1e-5 for bf16 operands (bf16 products
+are exact in fp32; only the fp32 summation order differs) and <= 1e-4 for fp8
+operands (the f8f6f4 MFMA's internal summation); bf16 output relative L2 <= 4e-3 and
 max |err| <= 2^-7 max |ref| (one bf16 rounding).  The fixed-order split
 reduction is checked bitwise: two calls give the same bytes."""
 
@@ -57,3 +59,31 @@ def test_wgrad_strided_operands_scales_and_empty(hip_lib):
     assert _rel(O.wgrad(a, b), token_wgrad(a, b)) <= 4e-3
     c = big_a[:, :300]
     assert _rel(O.wgrad(c, b), token_wgrad(c, b)) <= 4e-3
+
+
+@pytest.mark.parametrize("bdt", [torch.float8_e5m2, torch.float8_e4m3fn])
+@pytest.mark.parametrize("T,N1,N2,split", [(1000, 512, 2048, None), (3001, 1536, 512, None), (129, 256, 256, 1),
+                                           (5000, 512, 768, 5)])
+def test_fp8_wgrad_against_fp64(hip_lib, bdt, T, N1, N2, split):
+    """The fp32 output is within 1e-4 relative L2 of the float64 product of
+    the same fp8 values and scales: the f8f6f4 MFMA's own summation of its
+    128 products rounds more than a plain fp32 chain (1.2e-5 measured at
+    T = 1000, against 2e-6 for the bf16 MFMA)."""
+    from hstu_amd.wgrad import fp8_wgrad
+
+    g = torch.Generator(device="cuda").manual_seed(T + N2)
+    a8 = (torch.randn(T, N1, device="cuda", generator=g) * 40).to(torch.float8_e4m3fn)
+    # within each format's range (torch's e4m3 cast of |x| > 448 is NaN)
+    b8 = (torch.randn(T, N2, device="cuda", generator=g) * (300 if bdt == torch.float8_e5m2 else 40)).to(bdt)
+    sa = torch.tensor([0.01], device="cuda")
+    sb = torch.tensor([0.002], device="cuda")
+    ref = O.wgrad(a8, b8, 0.01, 0.002)
+    out32 = fp8_wgrad(a8, b8, sa, sb, out_dtype=torch.float32, split=split)
+    assert _rel(ref, out32) <= 1e-4
+    out16 = fp8_wgrad(a8, b8, sa, sb, split=split)
+    assert _rel(ref, out16) <= 4e-3
+    assert torch.equal(out16, fp8_wgrad(a8, b8, sa, sb, split=split))
+    # strided rows: column slices of wider fp8 buffers
+    big = (torch.randn(T, N1 + 256, device="cuda", generator=g) * 40).to(torch.float8_e4m3fn)
+    a_s = big[:, 256:]
+    assert _rel(O.wgrad(a_s, b8, 0.01, 0.002), fp8_wgrad(a_s, b8, sa, sb, out_dtype=torch.float32)) <= 1e-4
