@@ -220,7 +220,9 @@ int hstu_cast_fp8_amax_colsum(const void* x, int64_t ldx, int64_t rows, int64_t 
  * operands: out[n1][n2] = sa * sb * sum_{t < T} A[t][n1] * B[t][n2], fp32
  * accumulation, out bf16 (HSTU_DTYPE_BF16) or fp32 (HSTU_DTYPE_FP32) with row
  * stride ldo.  A [T, N1] (row stride lda elements), B [T, N2] (ldb): both
- * HSTU_DTYPE_BF16; N1, N2 multiples of 256; 16-byte aligned rows.  scale_a /
+ * HSTU_DTYPE_BF16, or A HSTU_DTYPE_FP8_E4M3 with B HSTU_DTYPE_FP8_E4M3 or
+ * HSTU_DTYPE_FP8_E5M2 (the FP8 backward's activation x gradient); N1, N2
+ * multiples of 256; rows 16-byte aligned.  scale_a /
  * scale_b: one fp32 on the device each, or NULL for 1.  The tokens are split
  * over `split` ranges (<= 0: about one workgroup per CU); the per-split fp32
  * partials go to workspace (hstu_wgrad_workspace_bytes bytes, 0 for one
@@ -228,8 +230,8 @@ int hstu_cast_fp8_amax_colsum(const void* x, int64_t ldx, int64_t rows, int64_t 
  * writes zeros.  hstu_wgrad_split gives the split actually used.
  * Replaces: dw = torch.mm(x.t(), dz) of triton_addmm_bwd,
  *           ops/triton/triton_addmm.py:1737-1750, and the output projection's
- *           torch.mm(y.t(), dout), ops/triton/triton_hstu_linear.py; the split-K
- *           scheme of fp8_wgrad, ops/triton/fp8_wgrad.py:27-160.
+ *           torch.mm(y.t(), dout), ops/triton/triton_hstu_linear.py; fp8_wgrad
+ *           (fp8 operands, the same split-K scheme), ops/triton/fp8_wgrad.py:27-160.
  */
 int hstu_wgrad_split(int64_t T, int N1, int N2, int split);
 int64_t hstu_wgrad_workspace_bytes(int64_t T, int N1, int N2, int split);
