@@ -251,6 +251,172 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
   }
 }
 
+// W-stationary persistent form for K <= 512 (the UVQK / VQK projections and
+// the K = 512 dgrad).  With K = 512 a 128 x 128 tile is only four k-steps, so
+// the tile-per-workgroup kernel above spends most of its time waiting for each
+// step's loads.  Here one workgroup per CU keeps its N tile's whole W panel
+// (128 x K bytes) in LDS and walks a stream of M tiles (m tile s, s + streams,
+// ...); the next tile's A rows are loaded into registers while the current
+// tile's MFMAs and epilogue run, so a memory round trip hides behind a whole
+// tile (two tiles ahead measured no faster).  8 waves as 4 (m) x 2 (n) of 32 x 64; the same operand-swapped MFMA,
+// 16-byte k-chunks {g, g+4} per lane group and epilogue as above (no residual).
+// With 8 | workgroups and tiles_n | workgroups / 8, the N tiles of one M
+// stream run on one XCD and share its L2 for the A rows.
+constexpr int kWsThreads = 512;
+constexpr int kWsMaxK = 512;
+constexpr int kWsPitch = kWsMaxK + 32;  // 544 = 32 mod 64: conflict-free b128 reads
+constexpr int kWsPanel = 128 * kWsPitch;
+constexpr int kWsLds = 2 * kWsPanel;    // W panel, A tile: 136 KiB
+constexpr int kWsCus = 256;
+
+template <bool E4M3_OUT, bool A_BF8>
+__global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p, int streams) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* const wl = smem;
+  uint8_t* const al = smem + kWsPanel;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 64;
+  int nt, s;
+  const int per_xcd = (int)gridDim.x / 8;
+  if ((int)gridDim.x % 8 == 0 && per_xcd % p.tiles_n == 0) {
+    const int xcd = (int)blockIdx.x % 8, slot = (int)blockIdx.x / 8;
+    nt = slot % p.tiles_n;
+    s = xcd * (per_xcd / p.tiles_n) + slot / p.tiles_n;
+  } else {
+    nt = (int)blockIdx.x % p.tiles_n;
+    s = (int)blockIdx.x / p.tiles_n;
+  }
+  const int n0 = nt * kBN;
+  const int K = p.K, cpr = K / 16, qn = 128 * cpr / kWsThreads;  // staged chunks per thread (<= 8)
+
+  // staging slots: chunk c = tid + 512 q of a 128-row x K-byte operand tile
+  uint32_t lo[8], vw[8], va[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int c = tid + kWsThreads * q, row = c / cpr, col = c - (c / cpr) * cpr;
+    lo[q] = row * kWsPitch + col * 16;
+    vw[q] = row * (uint32_t)p.ldw + col * 16;
+    va[q] = row * (uint32_t)p.lda + col * 16;
+  }
+  u32x4 st[8];
+  {
+    const BufRsrc wr = make_rsrc(p.W + (int64_t)n0 * p.ldw, (uint32_t)(127 * p.ldw + K));
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q < qn) st[q] = buf_ld128(wr, vw[q], 0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q < qn) *(u32x4*)(wl + lo[q]) = st[q];
+  }
+  auto load_a = [&](int mt) {
+    const int m0 = mt * kBM, mrows = min(kBM, p.M - m0);
+    const BufRsrc ar = make_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)((mrows - 1) * p.lda + K));
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q < qn) st[q] = buf_ld128(ar, va[q], 0);
+  };
+  auto store_a = [&]() {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q < qn) *(u32x4*)(al + lo[q]) = st[q];
+  };
+
+  // per-workgroup epilogue constants: lane's columns n0 + wn + 16 ns + 4 g .. +3
+  f32x4 swv[4], bv[4];
+  bool silu_any[4];
+#pragma unroll
+  for (int ns = 0; ns < 4; ++ns) {
+    const int n = n0 + wn + 16 * ns + 4 * g;
+    if (p.w_mode) swv[ns] = *(const f32x4*)(p.w_scale + n);
+    else swv[ns] = f32x4{p.w_scale[0], p.w_scale[0], p.w_scale[0], p.w_scale[0]};
+    if (p.bias) {
+      const u32x2 b = *(const u32x2*)(p.bias + n);
+      bv[ns] = f32x4{bf16_to_f32(b[0] & 0xffff), bf16_to_f32(b[0] >> 16), bf16_to_f32(b[1] & 0xffff),
+                     bf16_to_f32(b[1] >> 16)};
+    } else {
+      bv[ns] = zero4();
+    }
+    silu_any[ns] = n < p.silu_end && n + 4 > p.silu_begin;
+  }
+  const float out_s = E4M3_OUT ? p.out_scale[0] : 1.f;
+
+  int mt = s;
+  if (mt < p.tiles_m) {
+    load_a(mt);
+    store_a();
+  }
+  __syncthreads();
+  const int w_rd = (wn + li) * kWsPitch + 16 * g;
+  const int a_rd = (wm + li) * kWsPitch + 16 * g;
+  const int nk = K / kBK;
+  for (; mt < p.tiles_m; mt += streams) {
+    const int nxt = mt + streams;
+    if (nxt < p.tiles_m) load_a(nxt);
+    const int m0 = mt * kBM;
+    float sa[2];
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms) {
+      const int m = min(m0 + wm + 16 * ms + li, p.M - 1);
+      sa[ms] = p.a_mode ? p.a_scale[m] : p.a_scale[0];
+    }
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[a][0] = acc[a][1] = zero4();
+    for (int kk = 0; kk < nk; ++kk) {
+      i32x8 bop[2];
+#pragma unroll
+      for (int ms = 0; ms < 2; ++ms) {
+        const uint8_t* r = al + a_rd + ms * 16 * kWsPitch + kk * kBK;
+        bop[ms] = cat8(lds_ld128(r), lds_ld128(r + 64));
+      }
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        const uint8_t* r = wl + w_rd + ns * 16 * kWsPitch + kk * kBK;
+        const i32x8 aop = cat8(lds_ld128(r), lds_ld128(r + 64));
+#pragma unroll
+        for (int ms = 0; ms < 2; ++ms) {
+          if constexpr (A_BF8)
+            acc[ns][ms] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop, bop[ms], acc[ns][ms], 0, 1, 0, 0, 0, 0);
+          else
+            acc[ns][ms] = mfma_fp8(aop, bop[ms], acc[ns][ms]);
+        }
+      }
+    }
+    // epilogue: lane holds C[m = m0 + wm + 16 ms + li][n = n0 + wn + 16 ns + 4 g .. +3]
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms) {
+      const int m = m0 + wm + 16 * ms + li;
+      if (m >= p.M) continue;
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        const int n = n0 + wn + 16 * ns + 4 * g;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = acc[ns][ms][r] * (sa[ms] * swv[ns][r]) + bv[ns][r];
+        if (silu_any[ns]) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r >= p.silu_begin && n + r < p.silu_end)
+              v[r] = v[r] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * v[r]));
+        }
+        if constexpr (E4M3_OUT) {
+          float c[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) c[r] = __builtin_fminf(__builtin_fmaxf(v[r] / out_s, -448.f), 448.f);
+          int w = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+          w = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], w, true);
+          *(uint32_t*)((uint8_t*)p.C + (int64_t)m * p.ldc + n) = (uint32_t)w;
+        } else {
+          *(u32x2*)((uint16_t*)p.C + (int64_t)m * p.ldc + n) = u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with this tile's A rows
+    if (nxt < p.tiles_m) store_a();
+    __syncthreads();
+  }
+}
+
 // Per-group e4m3 quantization of bf16 rows: scale = amax/448 over each group
 // of `group` consecutive elements (1/448 for an all-zero group), out =
 // e4m3(clamp(x / scale, +-448)).  One wave per (row, group); group <= 4096 and
@@ -545,6 +711,32 @@ extern "C" int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void
   p.silu_end = silu_end;
   p.tiles_m = (M + kBM - 1) / kBM;
   p.tiles_n = N / kBN;
+  if (K <= kWsMaxK && !residual && p.tiles_n <= kWsCus) {
+    // W-stationary persistent form: about one workgroup per CU, streams of M tiles
+    const int streams = std::max(1, std::min(kWsCus / p.tiles_n, p.tiles_m));
+    void (*wk)(GemmParams, int);
+    if (a_dtype == HSTU_DTYPE_FP8_E5M2) {
+      if (out_dtype != HSTU_DTYPE_BF16) return HSTU_E_UNSUPPORTED;  // the dgrad form only
+      wk = fp8_gemm_ws_kernel<false, true>;
+    } else {
+      wk = out_dtype == HSTU_DTYPE_FP8_E4M3 ? fp8_gemm_ws_kernel<true, false> : fp8_gemm_ws_kernel<false, false>;
+    }
+    static std::mutex mu;
+    static bool lds_set[3] = {false, false, false};
+    const int which = wk == fp8_gemm_ws_kernel<false, true> ? 2 : wk == fp8_gemm_ws_kernel<true, false> ? 1 : 0;
+    {
+      std::lock_guard<std::mutex> lock(mu);
+      if (!lds_set[which]) {
+        hipError_t e = hipFuncSetAttribute((const void*)wk, hipFuncAttributeMaxDynamicSharedMemorySize, kWsLds);
+        if (e != hipSuccess) return (int)e;
+        lds_set[which] = true;
+      }
+    }
+    int sarg = streams;
+    void* args[] = {&p, &sarg};
+    return (int)hipLaunchKernel((const void*)wk, dim3(streams * p.tiles_n), dim3(kWsThreads), args, (size_t)kWsLds,
+                                stream);
+  }
   const int total = p.tiles_m * p.tiles_n;
   const int grid = (total + 7) / 8 * 8;
   void (*kern)(GemmParams);
