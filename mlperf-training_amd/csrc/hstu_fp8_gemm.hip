@@ -269,7 +269,12 @@ constexpr int kWsPanel = 128 * kWsPitch;
 constexpr int kWsLds = 2 * kWsPanel;    // W panel, A tile: 136 KiB
 constexpr int kWsCus = 256;
 
-template <bool E4M3_OUT, bool A_BF8>
+// NK = K / 128 k-steps (compile time, so the k-loop unrolls).  The output
+// leaves through LDS: after the tile's MFMAs each wave writes its 32 x 64
+// sub-tile into a private slice of the (then free) A buffer and stores it back
+// as whole 128-byte (bf16) or 64-byte (e4m3) row segments.
+constexpr int kWsSlicePitch = 144;  // 128-byte rows + 16
+template <bool E4M3_OUT, bool A_BF8, int NK>
 __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p, int streams) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* const wl = smem;
@@ -348,7 +353,7 @@ __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p
   __syncthreads();
   const int w_rd = (wn + li) * kWsPitch + 16 * g;
   const int a_rd = (wm + li) * kWsPitch + 16 * g;
-  const int nk = K / kBK;
+  uint8_t* const slice = al + wave * 32 * kWsSlicePitch;
   for (; mt < p.tiles_m; mt += streams) {
     const int nxt = mt + streams;
     if (nxt < p.tiles_m) load_a(nxt);
@@ -362,7 +367,8 @@ __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p
     f32x4 acc[4][2];
 #pragma unroll
     for (int a = 0; a < 4; ++a) acc[a][0] = acc[a][1] = zero4();
-    for (int kk = 0; kk < nk; ++kk) {
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
       i32x8 bop[2];
 #pragma unroll
       for (int ms = 0; ms < 2; ++ms) {
@@ -382,11 +388,12 @@ __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p
         }
       }
     }
-    // epilogue: lane holds C[m = m0 + wm + 16 ms + li][n = n0 + wn + 16 ns + 4 g .. +3]
+    __syncthreads();  // every wave is done with this tile's A rows: the slices are free
+    // epilogue: lane holds C[m = m0 + wm + 16 ms + li][n = n0 + wn + 16 ns + 4 g .. +3];
+    // slice row r = 16 ms + li, byte column (16 ns + 4 g) * element size
 #pragma unroll
     for (int ms = 0; ms < 2; ++ms) {
       const int m = m0 + wm + 16 * ms + li;
-      if (m >= p.M) continue;
 #pragma unroll
       for (int ns = 0; ns < 4; ++ns) {
         const int n = n0 + wn + 16 * ns + 4 * g;
@@ -405,13 +412,26 @@ __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p
           for (int r = 0; r < 4; ++r) c[r] = __builtin_fminf(__builtin_fmaxf(v[r] / out_s, -448.f), 448.f);
           int w = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
           w = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], w, true);
-          *(uint32_t*)((uint8_t*)p.C + (int64_t)m * p.ldc + n) = (uint32_t)w;
+          *(uint32_t*)(slice + (16 * ms + li) * kWsSlicePitch + (16 * ns + 4 * g)) = (uint32_t)w;
         } else {
-          *(u32x2*)((uint16_t*)p.C + (int64_t)m * p.ldc + n) = u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
+          *(u32x2*)(slice + (16 * ms + li) * kWsSlicePitch + (16 * ns + 4 * g) * 2) =
+              u32x2{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3])};
         }
+        (void)m;
       }
     }
-    __syncthreads();  // every wave is done with this tile's A rows
+    // the wave's own slice back as whole row segments (lane order: row-major 16-byte chunks)
+    {
+      constexpr int ES = E4M3_OUT ? 1 : 2, CPRW = 64 * ES / 16;  // chunks per 64-column row
+#pragma unroll
+      for (int i = 0; i < 32 * CPRW / 64; ++i) {
+        const int c = lane + 64 * i, r = c / CPRW, cc = c - r * CPRW;
+        const u32x4 d = *(const u32x4*)(slice + r * kWsSlicePitch + cc * 16);
+        const int m = m0 + wm + r;
+        if (m < p.M) *(u32x4*)((uint8_t*)p.C + ((int64_t)m * p.ldc + n0 + wn) * ES + cc * 16) = d;
+      }
+    }
+    __syncthreads();  // every wave has read its slice back
     if (nxt < p.tiles_m) store_a();
     __syncthreads();
   }
@@ -660,6 +680,32 @@ __global__ void __launch_bounds__(256) colsum_finish_kernel(const float* __restr
 
 inline int64_t cs_align(int64_t n) { return (n + 255) / 256 * 256; }
 
+template <bool E, bool B>
+const void* ws_kernel_nk(int nk) {
+  switch (nk) {
+    case 1: return (const void*)fp8_gemm_ws_kernel<E, B, 1>;
+    case 2: return (const void*)fp8_gemm_ws_kernel<E, B, 2>;
+    case 3: return (const void*)fp8_gemm_ws_kernel<E, B, 3>;
+    default: return (const void*)fp8_gemm_ws_kernel<E, B, 4>;
+  }
+}
+// form 0: bf16 out, 1: e4m3 out, 2: e5m2 A with bf16 out
+const void* ws_kernel(int form, int nk) {
+  return form == 2 ? ws_kernel_nk<false, true>(nk) : form == 1 ? ws_kernel_nk<true, false>(nk)
+                                                               : ws_kernel_nk<false, false>(nk);
+}
+
+hipError_t set_gemm_lds_size(const void* fn, int bytes) {
+  static std::mutex mu;
+  static std::vector<const void*> done;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const void* d : done)
+    if (d == fn) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.push_back(fn);
+  return e;
+}
+
 hipError_t set_gemm_lds(const void* fn) {
   static std::mutex mu;
   static std::vector<const void*> done;
@@ -714,28 +760,17 @@ extern "C" int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void
   if (K <= kWsMaxK && !residual && p.tiles_n <= kWsCus) {
     // W-stationary persistent form: about one workgroup per CU, streams of M tiles
     const int streams = std::max(1, std::min(kWsCus / p.tiles_n, p.tiles_m));
-    void (*wk)(GemmParams, int);
-    if (a_dtype == HSTU_DTYPE_FP8_E5M2) {
-      if (out_dtype != HSTU_DTYPE_BF16) return HSTU_E_UNSUPPORTED;  // the dgrad form only
-      wk = fp8_gemm_ws_kernel<false, true>;
-    } else {
-      wk = out_dtype == HSTU_DTYPE_FP8_E4M3 ? fp8_gemm_ws_kernel<true, false> : fp8_gemm_ws_kernel<false, false>;
-    }
-    static std::mutex mu;
-    static bool lds_set[3] = {false, false, false};
-    const int which = wk == fp8_gemm_ws_kernel<false, true> ? 2 : wk == fp8_gemm_ws_kernel<true, false> ? 1 : 0;
-    {
-      std::lock_guard<std::mutex> lock(mu);
-      if (!lds_set[which]) {
-        hipError_t e = hipFuncSetAttribute((const void*)wk, hipFuncAttributeMaxDynamicSharedMemorySize, kWsLds);
-        if (e != hipSuccess) return (int)e;
-        lds_set[which] = true;
-      }
-    }
+    if (a_dtype == HSTU_DTYPE_FP8_E5M2 && out_dtype != HSTU_DTYPE_BF16) return HSTU_E_UNSUPPORTED;  // dgrad form
+    if (out_dtype == HSTU_DTYPE_FP8_E4M3 && ldc % 16) return HSTU_E_UNSUPPORTED;  // 16-byte row segments
+    if (out_dtype == HSTU_DTYPE_BF16 && ldc % 8) return HSTU_E_UNSUPPORTED;
+    if ((uintptr_t)C % 16) return HSTU_E_UNSUPPORTED;
+    const int form = a_dtype == HSTU_DTYPE_FP8_E5M2 ? 2 : out_dtype == HSTU_DTYPE_FP8_E4M3 ? 1 : 0;
+    const void* wk = ws_kernel(form, K / kBK);
+    hipError_t e = set_gemm_lds_size(wk, kWsLds);
+    if (e != hipSuccess) return (int)e;
     int sarg = streams;
     void* args[] = {&p, &sarg};
-    return (int)hipLaunchKernel((const void*)wk, dim3(streams * p.tiles_n), dim3(kWsThreads), args, (size_t)kWsLds,
-                                stream);
+    return (int)hipLaunchKernel(wk, dim3(streams * p.tiles_n), dim3(kWsThreads), args, (size_t)kWsLds, stream);
   }
   const int total = p.tiles_m * p.tiles_n;
   const int grid = (total + 7) / 8 * 8;
