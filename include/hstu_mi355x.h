@@ -228,6 +228,9 @@ int hstu_cast_fp8_amax_colsum(const void* x, int64_t ldx, int64_t rows, int64_t 
  * partials go to workspace (hstu_wgrad_workspace_bytes bytes, 0 for one
  * split) and are summed in a fixed order (bitwise reproducible).  T = 0
  * writes zeros.  hstu_wgrad_split gives the split actually used.
+ * colsum_b (bf16 operands only; NULL to skip): fp32 [N2], 16-byte aligned,
+ * receives sum_t B[t][n2] (unscaled) -- the bias gradient of a projection
+ * whose output gradient is B -- from the same pass.
  * Replaces: dw = torch.mm(x.t(), dz) of triton_addmm_bwd,
  *           ops/triton/triton_addmm.py:1737-1750, and the output projection's
  *           torch.mm(y.t(), dout), ops/triton/triton_hstu_linear.py; fp8_wgrad
@@ -236,8 +239,8 @@ int hstu_cast_fp8_amax_colsum(const void* x, int64_t ldx, int64_t rows, int64_t 
 int hstu_wgrad_split(int64_t T, int N1, int N2, int split);
 int64_t hstu_wgrad_workspace_bytes(int64_t T, int N1, int N2, int split);
 int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, const void* B, int64_t ldb, int64_t T, int N1,
-               int N2, const float* scale_a, const float* scale_b, void* out, int64_t ldo, int out_dtype, int split,
-               void* workspace, int64_t workspace_bytes, hipStream_t stream);
+               int N2, const float* scale_a, const float* scale_b, void* out, int64_t ldo, int out_dtype,
+               float* colsum_b, int split, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * e4m3 quantization of bf16 rows in groups of `group` consecutive elements:

@@ -27,6 +27,9 @@
 // one XCD and share its L2.  With split > 1 every workgroup writes an fp32
 // partial tile; a second kernel sums the splits in a fixed order, applies
 // sa * sb and writes bf16 or fp32 (bitwise reproducible, no atomics).
+// Optionally (bf16) the workgroups of the first n1 tile also sum B's columns
+// from the registers they stage (the projection's bias gradient), so the
+// layer needs no separate pass over d(uvqk) for it.
 // The fp8 form (e4m3 A, e4m3 or e5m2 B: the reference's fp8_wgrad operands)
 // takes 128-token steps of 256-byte rows through the same LDS budget, reads
 // its fragments with ds_read_b64_tr_b8 (four 8-token reads per 32-byte
@@ -86,7 +89,9 @@ struct WgradParams {
   int64_t tps;  // tokens per split, a multiple of kKT
   int N1, N2;
   int split, tiles_n2, tiles;
-  float* ws;  // [split][N1][N2] fp32 partials when split > 1
+  float* ws;     // [split][N1][N2] fp32 partials when split > 1
+  float* cs_ws;  // [split][N2] column-sum partials when split > 1
+  float* colsum; // fp32 [N2]: sum over the tokens of B, or null (bf16 only)
   void* out;
   int64_t ldo;  // elements
   int out_f32;
@@ -139,11 +144,26 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_kernel(WgradParams p) {
       rb[q] = buf_ld128(br, vb[q], sb_off);
     }
   };
+  // column sums of B (the bias gradient of the layer's projection), taken
+  // from the staged registers by the workgroups of the first n1 tile: a
+  // thread's chunks all sit at byte column 16 (tid % 32) of the tile
+  const bool do_cs = !F8 && p.colsum != nullptr && t1 == 0;
+  float cs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   auto store = [&](uint8_t* st) {
 #pragma unroll
     for (int q = 0; q < kQ; ++q) {
       *(u32x4*)(st + lo[q]) = ra[q];
       *(u32x4*)(st + kWTile + lo[q]) = rb[q];
+    }
+    if (do_cs) {
+#pragma unroll
+      for (int q = 0; q < kQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = rb[q][e];
+          cs[2 * e] += __builtin_bit_cast(float, w << 16);
+          cs[2 * e + 1] += __builtin_bit_cast(float, w & 0xffff0000u);
+        }
     }
   };
 
@@ -207,6 +227,20 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_kernel(WgradParams p) {
     __syncthreads();
   }
 
+  if (do_cs) {
+    // fold the 16 row slots (tid / 32) of each column in LDS, in a fixed order
+    float* red = (float*)smem;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[(tid >> 5) * 256 + (tid & 31) * 8 + e] = cs[e];
+    __syncthreads();
+    if (tid < 256) {
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) t += red[k * 256 + tid];
+      if (p.split > 1) p.cs_ws[(int64_t)s * p.N2 + n20 + tid] = t;
+      else p.colsum[n20 + tid] = t;
+    }
+  }
   if (p.split > 1) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -232,14 +266,24 @@ __global__ void __launch_bounds__(kWThreads, 1) wgrad_kernel(WgradParams p) {
 }
 
 // out[n1][n2] = sa * sb * sum_{s < split} ws[s][n1][n2], summed in split order;
-// 4 consecutive n2 per thread.  split == 0 writes zeros (no tokens).
+// 4 consecutive n2 per thread; the threads past N1 * N2 / 4 do the same for
+// the column sums (colsum[n2] = sum_s cs_ws[s][n2], unscaled).  split == 0
+// writes zeros (no tokens).
 __global__ void __launch_bounds__(256) wgrad_reduce_kernel(const float* __restrict__ ws, int split, int N1, int N2,
                                                            const float* __restrict__ sa,
                                                            const float* __restrict__ sb, void* __restrict__ out,
-                                                           int64_t ldo, int out_f32) {
+                                                           int64_t ldo, int out_f32, const float* __restrict__ cs_ws,
+                                                           float* __restrict__ colsum) {
   const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   const int64_t numel = (int64_t)N1 * N2;
-  if (e >= numel) return;
+  if (e >= numel) {
+    const int64_t c = e - numel;
+    if (colsum == nullptr || c >= N2) return;
+    f32x4 t = zero4();
+    for (int s = 0; s < split; ++s) t += *(const f32x4*)(cs_ws + (int64_t)s * N2 + c);
+    *(f32x4*)(colsum + c) = t;
+    return;
+  }
   f32x4 acc = zero4();
   for (int s = 0; s < split; ++s) acc += *(const f32x4*)(ws + s * numel + e);
   acc *= (sa ? sa[0] : 1.f) * (sb ? sb[0] : 1.f);
@@ -288,12 +332,13 @@ extern "C" int hstu_wgrad_split(int64_t T, int N1, int N2, int split) {
 extern "C" int64_t hstu_wgrad_workspace_bytes(int64_t T, int N1, int N2, int split) {
   const int eff = hstu_wgrad_split(T, N1, N2, split);
   if (eff < 0) return -1;
-  return eff > 1 ? (int64_t)eff * N1 * N2 * 4 : 0;
+  return eff > 1 ? (int64_t)eff * (N1 + 1) * N2 * 4 : 0;  // product and column-sum partials
 }
 
 extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, const void* B, int64_t ldb, int64_t T,
                           int N1, int N2, const float* scale_a, const float* scale_b, void* out, int64_t ldo,
-                          int out_dtype, int split, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                          int out_dtype, float* colsum_b, int split, void* workspace, int64_t workspace_bytes,
+                          hipStream_t stream) {
   if (T < 0 || N1 <= 0 || N2 <= 0 || !out || (T > 0 && (!A || !B)) || lda < N1 || ldb < N2 || ldo < N2 ||
       (out_dtype != HSTU_DTYPE_BF16 && out_dtype != HSTU_DTYPE_FP32))
     return HSTU_E_BAD_ARG;
@@ -301,13 +346,14 @@ extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, 
   const bool f8 = a_dtype == HSTU_DTYPE_FP8_E4M3 && (b_dtype == HSTU_DTYPE_FP8_E4M3 || b_dtype == HSTU_DTYPE_FP8_E5M2);
   if (!bf16 && !f8) return HSTU_E_UNSUPPORTED;
   const int es = bf16 ? 2 : 1;
+  if (colsum_b && (!bf16 || (uintptr_t)colsum_b % 16)) return HSTU_E_UNSUPPORTED;
   if (N1 % kBN1 || N2 % kBN2 || (lda * es) % 16 || (ldb * es) % 16 || ((uintptr_t)A | (uintptr_t)B) % 16 ||
       (uintptr_t)out % (out_dtype == HSTU_DTYPE_FP32 ? 16 : 8) || ldo % 4)
     return HSTU_E_UNSUPPORTED;
   int64_t tps;
   int eff;
   plan(T, N1, N2, split, &tps, &eff);
-  const int64_t need = eff > 1 ? (int64_t)eff * N1 * N2 * 4 : 0;
+  const int64_t need = eff > 1 ? (int64_t)eff * (N1 + 1) * N2 * 4 : 0;
   if (workspace_bytes < need || (need > 0 && !workspace)) return HSTU_E_BAD_ARG;
   // one split's rows must stay within 32-bit buffer offsets
   if ((tps + kPlanKT) * std::max(lda, ldb) * es >= ((int64_t)1 << 32)) return HSTU_E_UNSUPPORTED;
@@ -327,6 +373,8 @@ extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, 
     p.tiles_n2 = N2 / kBN2;
     p.tiles = tiles;
     p.ws = (float*)workspace;
+    p.cs_ws = eff > 1 ? (float*)workspace + (int64_t)eff * N1 * N2 : nullptr;
+    p.colsum = colsum_b;
     p.out = out;
     p.ldo = ldo;
     p.out_f32 = out_f32;
@@ -345,9 +393,10 @@ extern "C" int hstu_wgrad(int a_dtype, const void* A, int64_t lda, int b_dtype, 
     if (e != hipSuccess) return (int)e;
   }
   if (eff != 1) {
-    const int64_t threads = (int64_t)N1 * N2 / 4;
+    const int64_t threads = (int64_t)N1 * N2 / 4 + (colsum_b ? N2 / 4 : 0);
+    const float* cs_ws = eff > 1 ? (const float*)workspace + (int64_t)eff * N1 * N2 : nullptr;
     hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                       (const float*)workspace, eff, N1, N2, scale_a, scale_b, out, ldo, out_f32);
+                       (const float*)workspace, eff, N1, N2, scale_a, scale_b, out, ldo, out_f32, cs_ws, colsum_b);
   }
   return (int)hipGetLastError();
 }

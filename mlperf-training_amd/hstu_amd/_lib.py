@@ -103,8 +103,8 @@ _SIGNATURES = {
     "hstu_cast_fp8_amax_colsum_workspace_bytes": (_i64, [_i64, _i64]),
     "hstu_wgrad_split": (_i32, [_i64, _i32, _i32, _i32]),
     "hstu_wgrad_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32]),
-    "hstu_wgrad": (_i32, [_i32, _vp, _i64, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _i32, _i32, _vp,
-                          _i64, _vp]),
+    "hstu_wgrad": (_i32, [_i32, _vp, _i64, _i32, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i64, _i32, _vp, _i32,
+                          _vp, _i64, _vp]),
     "hstu_cast_fp8_amax_colsum": (_i32, [_vp, _i64, _i64, _i64, _vp, _i32, _f32, _vp, _i64, _vp, _vp, _vp, _i64,
                                          _vp]),
     "hstu_quantize_e4m3_rows": (

@@ -156,8 +156,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
             dxn, d_w, d_b = fp8_grads
         else:
             xn = recompute_normed_x()
-            d_w = token_wgrad(xn, duvqk)
-            d_b = torch.sum(duvqk, 0, dtype=torch.float32)
+            # the wgrad kernel also sums d(uvqk)'s columns: the bias gradient
+            d_w, d_b = token_wgrad(xn, duvqk, with_colsum=True)
             dxn = torch.mm(duvqk, W.to(duvqk.dtype).t())
         d_w, d_b = d_w.to(W.dtype), d_b.to(W.dtype)
         dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False)

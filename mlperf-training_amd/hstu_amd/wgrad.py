@@ -51,11 +51,13 @@ def _rows(t: torch.Tensor) -> torch.Tensor:
 
 
 def wgrad(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.bfloat16, split: Optional[int] = None,
-          scale_a: Optional[torch.Tensor] = None, scale_b: Optional[torch.Tensor] = None) -> torch.Tensor:
+          scale_a: Optional[torch.Tensor] = None, scale_b: Optional[torch.Tensor] = None,
+          with_colsum: bool = False):
     """``(a * scale_a)^T @ (b * scale_b)`` [N1, N2] with fp32 accumulation, for
     a [T, N1] and b [T, N2] both bf16, or e4m3 and e4m3 / e5m2; the scales are
     one-element fp32 device tensors or None (1).  ``split``: token ranges
-    (None: about one workgroup per CU)."""
+    (None: about one workgroup per CU).  ``with_colsum`` (bf16): also the fp32
+    column sums of b from the same pass, returned as (out, colsum)."""
     if not supported(a, b):
         raise NotImplementedError("hstu_wgrad takes bf16 x bf16 or e4m3 x e4m3/e5m2 [T, N1], [T, N2] device "
                                   "operands, N1, N2 % 256 == 0")
@@ -71,12 +73,16 @@ def wgrad(a: torch.Tensor, b: torch.Tensor, out_dtype: torch.dtype = torch.bfloa
     sa = None if scale_a is None else scale_a.to(torch.float32).reshape(-1)[:1].contiguous()
     sb = None if scale_b is None else scale_b.to(torch.float32).reshape(-1)[:1].contiguous()
     code = _lib.HSTU_DTYPE_FP32 if out_dtype == torch.float32 else _lib.HSTU_DTYPE_BF16
+    if with_colsum and b.dtype != torch.bfloat16:
+        raise NotImplementedError("the fused column sum takes bf16 operands")
+    colsum = torch.empty(n2, dtype=torch.float32, device=a.device) if with_colsum else None
     st = _lib.fn("hstu_wgrad")(
         _CODES[a.dtype], a.data_ptr(), a.stride(0), _CODES[b.dtype], b.data_ptr(), b.stride(0), T, n1, n2,
         None if sa is None else sa.data_ptr(), None if sb is None else sb.data_ptr(), out.data_ptr(), out.stride(0),
-        code, sp, ws.data_ptr(), ws_bytes, torch.cuda.current_stream(a.device).cuda_stream)
+        code, None if colsum is None else colsum.data_ptr(), sp, ws.data_ptr(), ws_bytes,
+        torch.cuda.current_stream(a.device).cuda_stream)
     _lib.check(st, "hstu_wgrad")
-    return out
+    return (out, colsum) if with_colsum else out
 
 
 def fp8_wgrad(a_fp8: torch.Tensor, b_fp8: torch.Tensor, scale_a: torch.Tensor, scale_b: torch.Tensor,
@@ -89,9 +95,10 @@ def fp8_wgrad(a_fp8: torch.Tensor, b_fp8: torch.Tensor, scale_a: torch.Tensor, s
     return wgrad(a_fp8, b_fp8, out_dtype=out_dtype, split=split, scale_a=scale_a, scale_b=scale_b)
 
 
-def token_wgrad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+def token_wgrad(a: torch.Tensor, b: torch.Tensor, with_colsum: bool = False):
     """``a^T b`` in bf16: the split-K kernel where it serves the shapes, else
-    ``torch.mm``."""
+    ``torch.mm``.  ``with_colsum``: (a^T b, fp32 column sums of b)."""
     if supported(a, b) and a.dtype == torch.bfloat16:
-        return wgrad(a, b)
-    return torch.mm(a.t(), b)
+        return wgrad(a, b, with_colsum=with_colsum)
+    out = torch.mm(a.t(), b)
+    return (out, torch.sum(b, 0, dtype=torch.float32)) if with_colsum else out

@@ -231,7 +231,7 @@ def test_wgrad_rejects_before_launch():
     assert split(162251, 512, 2048, 0) == 16                 # 16 tiles -> one workgroup per CU
     assert split(1000, 512, 2048, 0) == 8                    # at least 4 k-steps of 32 tokens per split
     assert split(1000, 512, 2048, 1) == 1 and wsb(1000, 512, 2048, 1) == 0
-    assert wsb(162251, 512, 2048, 0) == 16 * 512 * 2048 * 4
+    assert wsb(162251, 512, 2048, 0) == 16 * (512 + 1) * 2048 * 4       # product and column-sum partials
     assert split(100, 300, 256, 0) == -1 and split(0, 256, 256, 0) == 0
     f = lib.fn("hstu_wgrad")
     X, W = 4096, 8192
@@ -239,7 +239,7 @@ def test_wgrad_rejects_before_launch():
 
     def g(**kw):
         a = dict(adt=bf, A=X, lda=512, bdt=bf, B=X, ldb=2048, T=1000, N1=512, N2=2048, sa=None, sb=None, out=W,
-                 ldo=2048, odt=bf, split=0, ws=W, wsb=wsb(1000, 512, 2048, 0), stream=None)
+                 ldo=2048, odt=bf, cs=None, split=0, ws=W, wsb=wsb(1000, 512, 2048, 0), stream=None)
         a.update(kw)
         return f(*a.values())
 
@@ -255,3 +255,5 @@ def test_wgrad_rejects_before_launch():
     assert g(N1=384, lda=384) == lib.HSTU_E_UNSUPPORTED       # 256-wide tiles
     assert g(A=X + 2) == lib.HSTU_E_UNSUPPORTED
     assert g(odt=f32, out=W + 8) == lib.HSTU_E_UNSUPPORTED    # fp32 rows stored 16 bytes at a time
+    assert g(adt=e4, bdt=e5, cs=W) == lib.HSTU_E_UNSUPPORTED     # the fused column sum is bf16 only
+    assert g(cs=W + 4) == lib.HSTU_E_UNSUPPORTED               # column sums stored 16 bytes at a time

@@ -38,6 +38,12 @@ def test_wgrad_against_fp64(hip_lib, T, N1, N2, split):
     assert float((out16.double().cpu() - ref).abs().max()) <= 2.0 ** -7 * float(ref.abs().max())
     again = wgrad(a, b, split=split)
     assert torch.equal(out16, again)
+    # the fused column sums of b: within the fp32 summation bound of the float64 sum
+    out_c, cs = wgrad(a, b, split=split, with_colsum=True)
+    assert torch.equal(out_c, out16)
+    ref_cs = b.double().cpu().sum(0)
+    bound = (T + 64) * 2.0 ** -24 * b.double().abs().cpu().sum(0) + 1e-30
+    assert bool(((cs.double().cpu() - ref_cs).abs() <= bound).all())
 
 
 def test_wgrad_strided_operands_scales_and_empty(hip_lib):
@@ -55,6 +61,10 @@ def test_wgrad_strided_operands_scales_and_empty(hip_lib):
     assert _rel(O.wgrad(a, b, 0.5, 3.0), out) <= 1e-5
     z = wgrad(a[:0], b[:0])
     assert z.shape == (512, 1024) and not bool(z.any())
+    z, zc = wgrad(a[:0], b[:0], with_colsum=True)
+    assert not bool(z.any()) and zc.shape == (1024,) and not bool(zc.any())
+    _, cs = wgrad(a, b, with_colsum=True)                                    # strided b
+    assert float((cs.double().cpu() - b.double().cpu().sum(0)).abs().max()) <= 1e-3
     # token_wgrad: the kernel for served shapes, torch.mm otherwise
     assert _rel(O.wgrad(a, b), token_wgrad(a, b)) <= 4e-3
     c = big_a[:, :300]
