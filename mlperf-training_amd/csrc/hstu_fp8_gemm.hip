@@ -757,13 +757,12 @@ extern "C" int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void
   p.silu_end = silu_end;
   p.tiles_m = (M + kBM - 1) / kBM;
   p.tiles_n = N / kBN;
-  if (K <= kWsMaxK && !residual && p.tiles_n <= kWsCus) {
-    // W-stationary persistent form: about one workgroup per CU, streams of M tiles
+  // W-stationary persistent form: about one workgroup per CU, streams of M
+  // tiles; its output leaves in 16-byte row segments (else the tile kernel)
+  const bool ws_rows = (uintptr_t)C % 16 == 0 && (out_dtype == HSTU_DTYPE_FP8_E4M3 ? ldc % 16 == 0 : ldc % 8 == 0);
+  if (K <= kWsMaxK && !residual && p.tiles_n <= kWsCus && ws_rows) {
     const int streams = std::max(1, std::min(kWsCus / p.tiles_n, p.tiles_m));
     if (a_dtype == HSTU_DTYPE_FP8_E5M2 && out_dtype != HSTU_DTYPE_BF16) return HSTU_E_UNSUPPORTED;  // dgrad form
-    if (out_dtype == HSTU_DTYPE_FP8_E4M3 && ldc % 16) return HSTU_E_UNSUPPORTED;  // 16-byte row segments
-    if (out_dtype == HSTU_DTYPE_BF16 && ldc % 8) return HSTU_E_UNSUPPORTED;
-    if ((uintptr_t)C % 16) return HSTU_E_UNSUPPORTED;
     const int form = a_dtype == HSTU_DTYPE_FP8_E5M2 ? 2 : out_dtype == HSTU_DTYPE_FP8_E4M3 ? 1 : 0;
     const void* wk = ws_kernel(form, K / kBK);
     hipError_t e = set_gemm_lds_size(wk, kWsLds);

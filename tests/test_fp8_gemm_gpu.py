@@ -168,3 +168,27 @@ def test_gemm_outproj_config4_full_size(hip_lib):
     got = out[rows.to(DEV)].double().cpu()
     assert orc.rel_l2(ref, got) <= 4e-3
     assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2
+
+
+def test_gemm_k512_both_kernels(hip_lib):
+    """K <= 512 runs the W-stationary kernel when the output rows allow
+    16-byte segments and the tile kernel otherwise (row stride N + 4): both
+    against the oracle."""
+    import hstu_amd._lib as lib
+
+    M, N, K = 777, 384, 512
+    a8, sa, w8t, sw = _operands(M, N, K, seed=9)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(10)) * 0.1).to(torch.bfloat16)
+    ref = orc.fp8_rowcol_gemm(a8, sa, w8t.t(), sw, bias=bias.float(), silu_cols=(0, 128))
+    A, W, SA, SW, B = (t.to(DEV).contiguous() for t in (a8, w8t, sa, sw, bias))
+    gemm = lib.fn("hstu_fp8_gemm_rowcol")
+    for ldc in (N, N + 4):
+        out = torch.zeros(M, ldc, dtype=torch.bfloat16, device=DEV)
+        st = gemm(A.data_ptr(), K, W.data_ptr(), K, SA.data_ptr(), 1, SW.data_ptr(), 1, B.data_ptr(), None, 0,
+                  out.data_ptr(), ldc, lib.HSTU_DTYPE_BF16, None, M, N, K, 0, 128,
+                  torch.cuda.current_stream().cuda_stream)
+        assert st == 0
+        torch.cuda.synchronize()
+        got = out[:, :N].double().cpu()
+        assert orc.rel_l2(ref, got) <= 4e-3, ldc
+        assert not bool(out[:, N:].any())                              # nothing written past N
