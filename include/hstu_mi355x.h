@@ -375,6 +375,18 @@ int hstu_quantize_do_e4m3_blk(int dtype, const void* dout, int64_t dout_row_stri
                               int B, int H, int D, int max_seq_len, void* dout_e4m3, void* e8,
                               hipStream_t stream);
 
+/*
+ * The inverse, for a backward that runs on the block-quantized dO:
+ * out[t, h, :] = bf16(dout_e4m3[t, h, :] * 2^(e8[t, h] - 127)), exact (an e4m3
+ * value times a power of two within 2^+-60 is a bf16).  dout_e4m3 [T, H, D]
+ * contiguous (8-byte aligned), e8 [T, H] uint8, out bf16 with row stride
+ * out_row_stride elements (16-byte aligned rows); D % 8 == 0.
+ * Replaces: the undoing of the block scales inside the full-FP8 backward's
+ *           out-gemm MFMAs (ops/flydsl/hstu_flydsl_mha.py:1330-1394, do_blk).
+ */
+int hstu_dequantize_do_e4m3_blk(const void* dout_e4m3, const void* e8, int64_t T, int H, int D, void* out,
+                                int64_t out_row_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

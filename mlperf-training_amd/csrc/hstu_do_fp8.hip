@@ -149,7 +149,43 @@ void launch_blk(bool f32, int grid, const void* x, int64_t rs, const int64_t* of
                        ntiles, (uint8_t*)y, (uint8_t*)e8);
 }
 
+// dO8 * 2^(E8 - 127) -> bf16, 8 elements of one (token, head) per thread.
+// Exact: an e4m3 value (3 mantissa bits) times 2^-e, |e| <= 60, is a bf16.
+__global__ void __launch_bounds__(256) do_dequant_kernel(const uint8_t* __restrict__ y,
+                                                         const uint8_t* __restrict__ e8, int64_t chunks, int H,
+                                                         int D, uint16_t* __restrict__ out, int64_t out_rs) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int cpr = H * D / 8;                  // 8-element chunks per token row
+  const int64_t t = i / cpr;
+  const int c = (int)(i - t * cpr), h = c * 8 / D;
+  const u32x2 w = *(const u32x2*)(y + (t * H * D + (int64_t)c * 8));
+  const float s = __builtin_bit_cast(float, (uint32_t)e8[t * H + h] << 23);  // 2^(E8 - 127)
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], false);
+    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[k], true);
+    o[2 * k] = pack_bf16(lo[0] * s, lo[1] * s);
+    o[2 * k + 1] = pack_bf16(hi[0] * s, hi[1] * s);
+  }
+  *(u32x4*)(out + t * out_rs + (int64_t)c * 8) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
 }  // namespace
+
+extern "C" int hstu_dequantize_do_e4m3_blk(const void* dout_e4m3, const void* e8, int64_t T, int H, int D,
+                                           void* out, int64_t out_row_stride, hipStream_t stream) {
+  if (T < 0 || H <= 0 || D <= 0 || (T > 0 && (!dout_e4m3 || !e8 || !out)) || out_row_stride < (int64_t)H * D)
+    return HSTU_E_BAD_ARG;
+  if (D % 8 || (uintptr_t)dout_e4m3 % 8 || (uintptr_t)out % 16 || out_row_stride % 8) return HSTU_E_UNSUPPORTED;
+  const int64_t chunks = T * (int64_t)H * D / 8;
+  if (chunks == 0) return 0;
+  if ((chunks + 255) / 256 >= ((int64_t)1 << 31)) return HSTU_E_UNSUPPORTED;
+  hipLaunchKernelGGL(do_dequant_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream,
+                     (const uint8_t*)dout_e4m3, (const uint8_t*)e8, chunks, H, D, (uint16_t*)out, out_row_stride);
+  return (int)hipGetLastError();
+}
 
 extern "C" int hstu_quantize_do_e4m3_blk(int dtype, const void* dout, int64_t dout_row_stride,
                                          const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,

@@ -32,4 +32,4 @@ from .hstu_preprocess import (  # noqa: F401
     triton_hstu_preprocess_and_attention,
 )
 from .hstu_delta import delta_hstu_mha, triton_cached_hstu_mha, triton_hstu_attention_delta_bwd  # noqa: F401
-from .hstu_do_fp8 import quantize_do_e4m3_blk  # noqa: F401
+from .hstu_do_fp8 import dequantize_do_e4m3_blk, quantize_do_e4m3_blk  # noqa: F401

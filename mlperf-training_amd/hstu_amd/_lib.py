@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "hstu_delta_attn_fwd",
     "hstu_delta_attn_bwd",
     "hstu_quantize_do_e4m3_blk",
+    "hstu_dequantize_do_e4m3_blk",
     "hstu_fp8_gemm",
     "hstu_cast_fp8_amax_partials",
     "hstu_cast_fp8_amax",
@@ -130,6 +131,7 @@ _SIGNATURES = {
          _i32, _f32, _vp, _i32, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
     ),
     "hstu_quantize_do_e4m3_blk": (_i32, [_i32, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp]),
+    "hstu_dequantize_do_e4m3_blk": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _i64, _vp]),
     "hstu_ln_mul_bwd": (
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,

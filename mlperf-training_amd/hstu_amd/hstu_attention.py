@@ -381,6 +381,17 @@ def triton_hstu_attention_bwd(
     if reason is not None:
         raise NotImplementedError(f"HIP HSTU attention backward: {reason}")
     fp8 = _is_fp8(q)
+    if fp8 and dout.numel() > 0:
+        from . import hstu_do_fp8
+
+        if hstu_do_fp8.bwd_full_fp8_enabled():
+            # DLRM_HSTU_FP8_BWD_FULL: the backward runs on the block-quantized dO
+            # (quantize_do_e4m3_blk; the reference undoes the scales in its MFMAs)
+            H, D = dout.shape[1], dout.shape[2]
+            if D in (64, 128) and H * D in (128, 256, 512):
+                dout = hstu_do_fp8.block_quantized_do(dout, seq_offsets, int(N))
+            else:
+                _log_once(f"full-FP8 dO quantizer: H*D = {H * D} not served, bf16 dO kept")
     _op_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, int(N), float(alpha), int(max_attn_len),
             int(contextual_seq_len),
             _scale_or_none(q_scale, q) if fp8 else None,

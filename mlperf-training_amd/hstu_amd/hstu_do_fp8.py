@@ -5,10 +5,18 @@ Drop-in for ``quantize_do_e4m3_blk`` (``ops/flydsl/hstu_do_fp8.py:95-121``,
 reference paths relative to ``recommendation_v4/hstu/generative_recommenders/``):
 one pow2 scale per (sequence, head, 32-token group), the groups being tokens
 p % 16 < 8 and p % 16 >= 8 of each 64-token tile of a sequence; no host sync.
+
+``bwd_full_fp8_enabled`` reads the reference's switch ``DLRM_HSTU_FP8_BWD_FULL``
+(``hstu_flydsl_mha.py:458-464``).  Under it the FP8 attention backward runs on
+the block-quantized dO: ``quantize_do_e4m3_blk`` then the exact
+``dequantize_do_e4m3_blk``, so its gradients are those of the reference's
+contract for the dO operand (the reference undoes the scales inside its
+MFMAs, :1330-1394).  The e4m3 P / dS operands of that backward are not built.
 """
 
 from __future__ import annotations
 
+import os
 from typing import Tuple
 
 import torch
@@ -42,3 +50,30 @@ def quantize_do_e4m3_blk(dout: torch.Tensor, seq_offsets: torch.Tensor, N: int) 
         torch.cuda.current_stream(dout.device).cuda_stream)
     _lib.check(st, "hstu_quantize_do_e4m3_blk")
     return y, e8
+
+
+def bwd_full_fp8_enabled() -> bool:
+    """``DLRM_HSTU_FP8_BWD_FULL`` in (1, true, on, yes)."""
+    return os.environ.get("DLRM_HSTU_FP8_BWD_FULL", "0").strip().lower() in ("1", "true", "on", "yes")
+
+
+def dequantize_do_e4m3_blk(dout8: torch.Tensor, e8: torch.Tensor) -> torch.Tensor:
+    """bf16 [T, H, D] = dout8 * 2^(E8 - 127), exact."""
+    if dout8.dim() != 3 or dout8.dtype != torch.float8_e4m3fn or e8.dtype != torch.uint8:
+        raise ValueError("expected dO8 e4m3 [T, H, D] and E8 uint8 [T, H]")
+    T, H, D = dout8.shape
+    y = dout8.contiguous()
+    e = e8.contiguous()
+    out = torch.empty((T, H, D), dtype=torch.bfloat16, device=dout8.device)
+    if T == 0:
+        return out
+    st = _lib.fn("hstu_dequantize_do_e4m3_blk")(y.data_ptr(), e.data_ptr(), T, H, D, out.data_ptr(), H * D,
+                                                torch.cuda.current_stream(dout8.device).cuda_stream)
+    _lib.check(st, "hstu_dequantize_do_e4m3_blk")
+    return out
+
+
+def block_quantized_do(dout: torch.Tensor, seq_offsets: torch.Tensor, N: int) -> torch.Tensor:
+    """dO as the full-FP8 backward sees it: dequantize(quantize(dO)), bf16."""
+    y, e8 = quantize_do_e4m3_blk(dout, seq_offsets, N)
+    return dequantize_do_e4m3_blk(y, e8)

@@ -19,6 +19,10 @@ Follows ``ops/flydsl/hstu_do_fp8.py`` (reference paths relative to
   e4m3(dO * 2^e) (torch's RNE float8_e4m3fn conversion, a library routine),
   E8 = 127 - e.  Pinned by the pieces above, the exact decode
   dO8 * 2^-e within half an e4m3 step of dO, and brute-force group maxima.
+* ``dequantize_do_e4m3_blk`` -- the undoing of the block scales
+  (``hstu_flydsl_mha.py:1330-1394``, inside the reference's MFMAs):
+  bf16(dO8 * 2^(E8 - 127)).  Pinned by exactness (the float64 product is a
+  bf16 value) and by the round trip staying within half an e4m3 step.
 """
 
 from __future__ import annotations
@@ -93,3 +97,10 @@ def quantize_do_e4m3_blk(dout: torch.Tensor, seq_offsets, max_seq_len: int):
                 y[rows] = q.view(torch.uint8)
                 e8[rows] = torch.as_tensor((127 - e).astype(np.uint8))[None, :].expand(len(rows), H)
     return y, e8
+
+
+def dequantize_do_e4m3_blk(y: torch.Tensor, e8: torch.Tensor) -> torch.Tensor:
+    """bf16 [T, H, D] = y (e4m3 bytes or float8) * 2^(E8 - 127)."""
+    yf = (y.view(torch.float8_e4m3fn) if y.dtype == torch.uint8 else y).cpu().double()
+    s = torch.pow(2.0, e8.cpu().double() - 127.0)[:, :, None]
+    return (yf * s).to(torch.bfloat16)

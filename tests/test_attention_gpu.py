@@ -336,3 +336,43 @@ def test_generic_masks_with_bias(hip_lib, mode):
     for name, got, r in (("dq", qd.grad, rq), ("dk", kd.grad, rk), ("dv", vd.grad, rv), ("dbias", bd.grad, rb)):
         err = orc.rel_l2(r, got.float().cpu())
         assert err <= 1e-2, f"{mode} bias {name}: rel L2 {err:.3e}"
+
+
+def test_fp8_bwd_full_fp8_block_quantized_dout(hip_lib, monkeypatch):
+    """DLRM_HSTU_FP8_BWD_FULL=1: the FP8 backward runs on the block-quantized
+    dO.  Its gradients are bitwise those of the plain backward given the
+    oracle's dequantize(quantize(dO)), and stay within the FP8 tolerance of
+    the float64 backward on the unquantized dO."""
+    from oracle import hstu_do_fp8_oracle as DO
+
+    ops = _ops()
+    H, D = 4, 128
+    lengths = [300, 77, 129]
+    N = max(lengths)
+    q, k, v, offs = _case(lengths, H, D, std=1.0, dtype=torch.float32)
+    (q8, sq), (k8, sk), (v8, sv) = _quantize(q), _quantize(k), _quantize(v)
+    qd, kd, vd = orc.dequantize(q8, sq), orc.dequantize(k8, sk), orc.dequantize(v8, sv)
+    alpha = 1.0 / D ** 0.5
+    dev = [t.to(DEV) for t in (q8, k8, v8, sq, sk, sv)]
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(19)).to(torch.bfloat16)
+    y, e8 = DO.quantize_do_e4m3_blk(dout, offs, N)
+    dout_q = DO.dequantize_do_e4m3_blk(y, e8)
+
+    def bwd(dO, full):
+        monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL", "1" if full else "0")
+        g = [torch.empty(q.shape, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        ops.triton_hstu_attention_bwd(dO.to(DEV), dev[0], dev[1], dev[2], *g, offs.to(DEV), None, N, alpha, 0, 0,
+                                      None, False, 0, dev[3], dev[4], dev[5])
+        torch.cuda.synchronize()
+        return [t.cpu() for t in g]
+
+    full = bwd(dout, True)
+    ref_q = bwd(dout_q, False)
+    plain = bwd(dout, False)
+    for a, b in zip(full, ref_q):
+        assert torch.equal(a, b)
+    assert any(not torch.equal(a, b) for a, b in zip(full, plain))
+    rq, rk, rv, _ = orc.hstu_mha_bwd(N, alpha, qd, kd, vd, offs, dout)
+    for name, got, r in (("dq", full[0], rq), ("dk", full[1], rk), ("dv", full[2], rv)):
+        err = orc.rel_l2(r, got.float())
+        assert err <= 3e-2, f"{name}: rel L2 {err:.3e}"

@@ -257,3 +257,15 @@ def test_wgrad_rejects_before_launch():
     assert g(odt=f32, out=W + 8) == lib.HSTU_E_UNSUPPORTED    # fp32 rows stored 16 bytes at a time
     assert g(adt=e4, bdt=e5, cs=W) == lib.HSTU_E_UNSUPPORTED     # the fused column sum is bf16 only
     assert g(cs=W + 4) == lib.HSTU_E_UNSUPPORTED               # column sums stored 16 bytes at a time
+
+
+def test_do_dequantizer_rejects_before_launch():
+    import hstu_amd._lib as lib
+
+    dq = lib.fn("hstu_dequantize_do_e4m3_blk")
+    X, W = 4096, 8192
+    assert dq(X, W, 10, 4, 128, X, 100, None) == lib.HSTU_E_BAD_ARG      # row stride below H * D
+    assert dq(X, W, -1, 4, 128, X, 512, None) == lib.HSTU_E_BAD_ARG
+    assert dq(X, W, 10, 4, 100, X, 400, None) == lib.HSTU_E_UNSUPPORTED  # D % 8
+    assert dq(X + 4, W, 10, 4, 128, X, 512, None) == lib.HSTU_E_UNSUPPORTED
+    assert dq(X, W, 0, 4, 128, X, 512, None) == 0

@@ -134,3 +134,36 @@ def test_do_blk_kernel_config3_strided(hip_lib):
         wy, we8 = Q.quantize_do_e4m3_blk(x[st:en].cpu(), so, 4096)
         assert torch.equal(e8[st:en].cpu(), we8)
         assert torch.equal(y[st:en].cpu().view(torch.uint8), wy)
+
+
+def test_oracle_dequantize_exact_and_round_trip():
+    from oracle import hstu_do_fp8_oracle as DO
+
+    g = torch.Generator().manual_seed(12)
+    lengths = [70, 5, 128]
+    T = sum(lengths)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]))
+    x = (torch.randn(T, 2, 128, generator=g) * torch.exp(torch.randn(T, 2, 1, generator=g) * 3)).to(torch.bfloat16)
+    y, e8 = DO.quantize_do_e4m3_blk(x, offs, 128)
+    d = DO.dequantize_do_e4m3_blk(y, e8)
+    exact = y.view(torch.float8_e4m3fn).double() * torch.pow(2.0, e8.double() - 127.0)[:, :, None]
+    assert torch.equal(d.double(), exact)                                   # no rounding in bf16
+    xf = x.double()
+    # half an e4m3 step: relative 2^-4 for normals, 2^-10 of the group's scale 2^-e for subnormals
+    step = torch.pow(2.0, e8.double() - 127.0)[:, :, None] * 2.0 ** -10
+    assert bool(((d.double() - xf).abs() <= xf.abs() * 2.0 ** -4 + step).all())
+
+
+@pytest.mark.gpu
+def test_dequantize_bit_exact(hip_lib):
+    import hstu_amd
+
+    lengths = [200, 64, 1, 333]
+    T = sum(lengths)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lengths)]))
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(T, 4, 128, generator=g) * torch.exp(torch.randn(T, 4, 1, generator=g) * 4)).to(torch.bfloat16)
+    y, e8 = hstu_amd.quantize_do_e4m3_blk(x.cuda(), offs.cuda(), 512)
+    d = hstu_amd.dequantize_do_e4m3_blk(y, e8)
+    want = Q.dequantize_do_e4m3_blk(y.cpu(), e8.cpu())
+    assert torch.equal(d.cpu().view(torch.int16), want.view(torch.int16))
