@@ -554,7 +554,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(multi-GPU sharding is designed, not built: see DESIGN.md)"}))
+                                   "(multi-GPU sharding is designed, not built)"}))
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()

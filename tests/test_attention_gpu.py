@@ -5,7 +5,7 @@ ops) and compares with ``oracle/hstu_oracle.py`` evaluated in float64 on the
 same (bf16- or e4m3-rounded) inputs.
 
 Tolerances (stated bar):
-* bf16: ``assert_close(rtol=1e-2, atol=1e-2)`` (the BASELINE bar) and, since
+* bf16: ``assert_close(rtol=1e-2, atol=1e-2)`` (the stated bf16 bar) and, since
   outputs are small, relative L2 <= 1e-2 as the discriminating check.
 * e4m3 inputs: against fp32/fp64 on the dequantized inputs, relative L2
   <= 1.5e-2 and max |err| <= 3e-2 * max |ref|.

@@ -1,6 +1,6 @@
 """Pins of the CPU oracle (oracle/hstu_oracle.py), independent of its own
 formulas: brute-force loops, closed forms, library routines (torch autograd /
-gradcheck, torch's e4m3fn conversion) and the BASELINE-documented generator
+gradcheck, torch's e4m3fn conversion) and the documented config generator
 outputs.  Each check is chosen so that a plausible slip (dropped 1/N, alpha
 applied twice, off-by-one in the mask diagonal, transposed operand) fails."""
 
@@ -26,7 +26,7 @@ def test_config_generators_match_baseline():
     L3 = orc.lengths_for_config(3)
     assert L3.sum() == 162251 and len(L3) == 128
     assert orc.causal_pairs(L3) == 300720505
-    # config 3 fwd+bwd FLOPs (BASELINE.md: 2.156 TFLOP; fwd 0.616, bwd 1.540)
+    # config 3 fwd+bwd FLOPs (2.156 TFLOP; fwd 0.616, bwd 1.540)
     assert abs(orc.attn_flops(L3, 4, 128) / 1e12 - 2.156) < 1e-3
     assert abs(orc.attn_flops(L3, 4, 128, bwd=False) / 1e12 - 0.616) < 1e-3
 
