@@ -97,3 +97,28 @@ def test_fp8_wgrad_against_fp64(hip_lib, bdt, T, N1, N2, split):
     big = (torch.randn(T, N1 + 256, device="cuda", generator=g) * 40).to(torch.float8_e4m3fn)
     a_s = big[:, 256:]
     assert _rel(O.wgrad(a_s, b8, 0.01, 0.002), fp8_wgrad(a_s, b8, sa, sb, out_dtype=torch.float32)) <= 1e-4
+
+
+@pytest.mark.parametrize("n1,n2", [(512, 2048), (1536, 512)])
+def test_wgrad_full_size_against_fp32_library_product(hip_lib, n1, n2):
+    """At the layer's full token count (config 3, T = 162 251, 16 or 21
+    splits): the bf16 and e4m3 x e5m2 products against torch's fp32 matmul of
+    the same values on the device (relative L2 1e-5 / 1e-4), and the fused
+    column sums against torch's fp32 sum."""
+    from hstu_amd.wgrad import fp8_wgrad, wgrad
+
+    T = 162251
+    g = torch.Generator(device="cuda").manual_seed(n1)
+    a = torch.randn(T, n1, device="cuda", generator=g).to(torch.bfloat16)
+    b = torch.randn(T, n2, device="cuda", generator=g).to(torch.bfloat16)
+    ref = torch.mm(a.float().t(), b.float())
+    out, cs = wgrad(a, b, out_dtype=torch.float32, with_colsum=True)
+    assert float((out - ref).norm() / ref.norm()) <= 1e-5
+    rcs = b.float().sum(0)
+    # two fp32 summations of the same values: within (T + 64) 2^-24 sum|b| of each other, per column
+    assert bool(((cs - rcs).abs() <= (T + 64) * 2.0 ** -24 * b.float().abs().sum(0)).all())
+    a8, b8 = a.to(torch.float8_e4m3fn), b.to(torch.float8_e5m2)
+    one = torch.ones(1, device="cuda")
+    ref8 = torch.mm(a8.float().t(), b8.float())
+    out8 = fp8_wgrad(a8, b8, one, one, out_dtype=torch.float32)
+    assert float((out8 - ref8).norm() / ref8.norm()) <= 1e-4
