@@ -292,8 +292,9 @@ def output_block_bench(torch, T, steps, warmup, flush):
     output for the FP8 out-projection) and its backward (dx, du, dweight,
     dbias, recomputed bf16 y): time and GB/s of algorithmic bytes."""
     import hstu_amd
+    import hstu_amd.hstu_linear as hl
 
-    os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
+    hl.set_mask16(True)
     D = 512
     g = torch.Generator(device="cuda").manual_seed(5)
     attn = torch.randn(T, D, device="cuda", generator=g).to(torch.bfloat16)
@@ -428,20 +429,17 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     config 3's shapes (T = 162 251, N = 4096, E = 512, H = 4, D = 128), with
     the relative bias and output dropout 0.3 (mask16).  Scales are calibrated
     once from the data (amax * 1.25 / 448) before timing.  fp8_dgrad: the
-    output and UVQK projections' dgrads in FP8 (e5m2 gradients,
-    DLRM_HSTU_FP8_BWD=1 and DLRM_HSTU_FP8_BWD_UVQK=1; the UVQK gradient's cast
-    also gives the bias gradient) and the UVQK weight gradient from the
-    forward's e4m3 LN output (DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t) and the output
-    projection's from the forward's e4m3 y (DLRM_HSTU_FP8_BWD_OUT_WGRAD=1), with enough
-    warm-up steps for their delayed scales to publish."""
+    output and UVQK projections' dgrads in FP8 (e5m2 gradients, the
+    reference's DLRM_HSTU_FP8_BWD=1 and DLRM_HSTU_FP8_BWD_UVQK=1, passed as an
+    explicit Fp8BackwardConfig; the UVQK gradient's cast also gives the bias
+    gradient) and the UVQK weight gradient from the forward's e4m3 LN output
+    (UVQK_WGRAD=fp8t) and the output projection's from the forward's e4m3 y
+    (OUT_WGRAD=1), with enough warm-up steps for their delayed scales to publish."""
     import hstu_amd
     import hstu_amd.bwd_fp8 as bwd_fp8
 
-    os.environ["DLRM_HSTU_FP8_MASK16"] = "1"
-    os.environ["DLRM_HSTU_FP8_BWD"] = "1" if fp8_dgrad else "0"
-    os.environ["DLRM_HSTU_FP8_BWD_UVQK"] = "1" if fp8_dgrad else "0"
-    os.environ["DLRM_HSTU_FP8_BWD_UVQK_WGRAD"] = "fp8t" if fp8_dgrad else "bf16"
-    os.environ["DLRM_HSTU_FP8_BWD_OUT_WGRAD"] = "1" if fp8_dgrad else "0"
+    cfg = bwd_fp8.Fp8BackwardConfig(enabled=fp8_dgrad, uvqk=fp8_dgrad, uvqk_wgrad_fp8t=fp8_dgrad,
+                                    out_wgrad_fp8=fp8_dgrad)
     bwd_fp8.reset_sites()
     if fp8_dgrad:
         warmup = max(warmup, 5)
@@ -467,7 +465,8 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
             t.grad = None
         if ev is not None:
             ev[0].record()
-        out = hstu_amd.hstu_layer(x, offs, N, p, dropout_ratio=0.3, training=True, attn_bias=bias, seed=7, **scales)
+        out = hstu_amd.hstu_layer(x, offs, N, p, dropout_ratio=0.3, training=True, attn_bias=bias, seed=7,
+                                  fp8_backward=cfg, dropout_mask16=True, **scales)
         if ev is not None:
             ev[1].record()
         out.backward(dy)
@@ -475,10 +474,6 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
             ev[2].record()
 
     tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
-    os.environ["DLRM_HSTU_FP8_BWD"] = "0"
-    os.environ["DLRM_HSTU_FP8_BWD_UVQK"] = "0"
-    os.environ["DLRM_HSTU_FP8_BWD_UVQK_WGRAD"] = "bf16"
-    os.environ["DLRM_HSTU_FP8_BWD_OUT_WGRAD"] = "0"
     bwd_fp8.reset_sites()
     m = float(np.median(tot))
     P = causal_pairs(lengths)

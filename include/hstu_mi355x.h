@@ -122,10 +122,13 @@ int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, in
  * The two halves of hstu_attn_bwd, same arguments: hstu_attn_bwd_dkdv writes
  * dk and dv only (dq may be NULL); hstu_attn_bwd_dq writes dq and dbias only
  * (dk, dv may be NULL).  Each writes its own parts of the shared workspace,
- * so run them in order on one stream.  The reference launches its backward in the same two parts when
- * the dq-split is armed: the fused dK/dV kernel, then dq from the stored ds
- * tiles (ops/flydsl/hstu_flydsl_mha.py:1707-1740, ops/flydsl/hstu_dq_split.py:348);
- * here dq recomputes the score tile instead of storing it.
+ * so run them in order on one stream, dkdv first.  The reference launches its
+ * backward in the same two parts when the dq-split is armed: the fused dK/dV
+ * kernel, then dq from the stored ds tiles (ops/flydsl/hstu_flydsl_mha.py:1707-1740,
+ * ops/flydsl/hstu_dq_split.py:348).  Here too, with the causal mask dq
+ * contracts the dS tiles that dkdv left in the workspace with K (it cannot
+ * run without them); only the generic masks (num_targets, window, contextual
+ * prefix) make dq recompute the score tiles itself.
  */
 int hstu_attn_bwd_dkdv(int dtype, const void* dout, int64_t dout_row_stride, const void* q, const void* k,
                        const void* v, int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
@@ -281,8 +284,11 @@ int hstu_dropout_mask(int rows, int D, int num_masks, int mask16, float dropout_
 
 /*
  * Forward.  y: bf16 or e4m3 (out_dtype) [rows, ncols * D] with row stride
- * ldy; e4m3 stores e4m3(clamp(value * inv_scale, +-448)).  With dropout the
- * keep mask is generated (as by hstu_dropout_mask) and written to `mask`.
+ * ldy; e4m3 stores e4m3(clamp(value * inv_scale, +-448)).  out_scale (device
+ * fp32, nullable): when given, the e4m3 output uses 1 / out_scale[0], read on
+ * the device, instead of inv_scale -- the layer's per-tensor dequantization
+ * scale never travels to the host.  With dropout the keep mask is generated
+ * (as by hstu_dropout_mask) and written to `mask`.
  * Replaces: triton_layer_norm_mul_dropout_fwd, triton_hstu_linear.py:3034-3146
  *           (kernels _ln_mul_dropout_fwd :1429-1563, _ln_mul_dropout_fwd_rng
  *           :529-700); triton_weighted_layer_norm_fwd,
@@ -293,7 +299,7 @@ int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_t ldu,
                     int mul_u_act, int silu_u, int concat_u, int concat_x,
                     int training, float dropout_ratio, uint64_t seed, int mask16,
                     void* mask, int64_t ldm,
-                    void* y, int64_t ldy, int out_dtype, float inv_scale,
+                    void* y, int64_t ldy, int out_dtype, float inv_scale, const float* out_scale,
                     float* mean, float* rstd, hipStream_t stream);
 
 /* Workspace of hstu_ln_mul_bwd (per-block dweight / dbias partials). */

@@ -210,6 +210,7 @@ struct FwdArgs {
   void* y;
   int64_t ldy;
   float inv_scale;
+  const float* out_scale;  // device scale (nullable): e4m3 output uses 1 / out_scale[0]
   float* mean;
   float* rstd;
 };
@@ -299,7 +300,9 @@ __global__ void __launch_bounds__(kThreads) ln_mul_fwd_kernel(FwdArgs a) {
   }
   const bool cu = HU && a.concat_u;
   const uint32_t bit_x = a.concat_x ? 2u : 0u, bit_u = cu ? (a.concat_x ? 4u : 2u) : 0u;
-  const float scale = E4M3 ? (DROP ? a.drop_scale * a.inv_scale : a.inv_scale) : a.drop_scale;
+  float inv_scale = a.inv_scale;
+  if (E4M3 && a.out_scale != nullptr) inv_scale = 1.0f / a.out_scale[0];
+  const float scale = E4M3 ? (DROP ? a.drop_scale * inv_scale : inv_scale) : a.drop_scale;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int rl = wave + 4 * k;
@@ -669,7 +672,8 @@ extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_
                                const float* bias, float eps, int rows, int D, int mul_u_act, int silu_u,
                                int concat_u, int concat_x, int training, float dropout_ratio, uint64_t seed,
                                int mask16, void* mask, int64_t ldm, void* y, int64_t ldy, int out_dtype,
-                               float inv_scale, float* mean, float* rstd, hipStream_t stream) {
+                               float inv_scale, const float* out_scale, float* mean, float* rstd,
+                               hipStream_t stream) {
   if (rows < 0 || D <= 0 || x == nullptr || ldx < D || (u != nullptr && ldu < D) || weight == nullptr ||
       bias == nullptr || mean == nullptr || rstd == nullptr || y == nullptr || mul_u_act < 0 || mul_u_act > 2 ||
       !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))
@@ -706,6 +710,7 @@ extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_
   a.y = y;
   a.ldy = ldy;
   a.inv_scale = inv_scale;
+  a.out_scale = out_scale;
   a.mean = mean;
   a.rstd = rstd;
   launch_fwd(D, u == nullptr ? kNoU : mul_u_act, dropout, out_dtype == HSTU_DTYPE_FP8_E4M3, a, stream);

@@ -33,3 +33,4 @@ from .hstu_preprocess import (  # noqa: F401
 )
 from .hstu_delta import delta_hstu_mha, triton_cached_hstu_mha, triton_hstu_attention_delta_bwd  # noqa: F401
 from .hstu_do_fp8 import dequantize_do_e4m3_blk, quantize_do_e4m3_blk  # noqa: F401
+from . import reference_ops  # noqa: F401,E402  (registers generative_recommenders::triton_hstu_attention_*)

@@ -116,7 +116,7 @@ _SIGNATURES = {
     "hstu_ln_mul_fwd": (
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _u64, _i32,
-         _vp, _i64, _vp, _i64, _i32, _f32, _vp, _vp, _vp],
+         _vp, _i64, _vp, _i64, _i32, _f32, _vp, _vp, _vp, _vp],
     ),
     "hstu_ln_mul_bwd_workspace_bytes": (_i64, [_i32, _i32]),
     "hstu_delta_attn_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32]),

@@ -20,15 +20,20 @@ Mirrors ``ops/triton/bwd_fp8.py`` (reference paths relative to
   wgrad or with ``DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t`` the e4m3 x e5m2 wgrad,
   the cast's column sum as the bias gradient)
 
-Switches (the reference's names): ``DLRM_HSTU_FP8_BWD=1`` enables the path;
-``DLRM_HSTU_FP8_BWD_MARGIN`` (8), ``_REFRESH_CALLS`` (200), ``_WARMUP_CALLS``
-(4), ``_GRAD_FORMAT`` (e5m2 | e4m3); ``DLRM_HSTU_FP8_BWD_UVQK=1`` (with the
-e5m2 format) enables the UVQK backward on its own, as in the reference.  They
-are read when a call needs them, so a process can switch the path on and off.
+Configuration is an explicit ``Fp8BackwardConfig`` passed by the caller
+(``config=``) or the process default (``default_config()``), which is read
+once from the reference's switch names -- ``DLRM_HSTU_FP8_BWD=1`` enables the
+path; ``DLRM_HSTU_FP8_BWD_MARGIN`` (8), ``_REFRESH_CALLS`` (200),
+``_WARMUP_CALLS`` (4), ``_GRAD_FORMAT`` (e5m2 | e4m3);
+``DLRM_HSTU_FP8_BWD_UVQK=1`` (with the e5m2 format) enables the UVQK backward
+on its own, as in the reference; ``_UVQK_WGRAD=fp8t`` and ``_OUT_WGRAD=1``
+the FP8 weight gradients -- and can be replaced with ``set_default_config``.
+No call reads the environment.
 """
 
 from __future__ import annotations
 
+import dataclasses
 import os
 from typing import Callable, Dict, Optional, Tuple
 
@@ -43,27 +48,83 @@ E4M3_MAX = 448.0
 E5M2_MAX = 57344.0
 
 
-def enabled() -> bool:
-    return os.environ.get("DLRM_HSTU_FP8_BWD", "0") == "1"
+@dataclasses.dataclass(frozen=True)
+class Fp8BackwardConfig:
+    """The FP8 backward arm's settings (the reference's switches, as values).
+
+    enabled: the output-projection e5m2 dgrad (``DLRM_HSTU_FP8_BWD``);
+    uvqk: the UVQK e5m2 dgrad (``DLRM_HSTU_FP8_BWD_UVQK``, e5m2 only);
+    out_wgrad_fp8 / uvqk_wgrad_fp8t: the FP8 weight gradients;
+    margin, warmup_calls, refresh_calls, grad_format: the delayed-scale policy.
+    """
+
+    enabled: bool = False
+    uvqk: bool = False
+    out_wgrad_fp8: bool = False
+    uvqk_wgrad_fp8t: bool = False
+    margin: float = 8.0
+    warmup_calls: int = 4
+    refresh_calls: int = 200
+    grad_format: str = "e5m2"
+
+    def __post_init__(self):
+        if self.grad_format not in ("e5m2", "e4m3"):
+            raise ValueError(f"grad_format {self.grad_format!r}: expected e5m2 | e4m3")
+        if self.warmup_calls < 1 or self.refresh_calls < 1:
+            raise ValueError("warmup_calls and refresh_calls must be >= 1")
+
+    @classmethod
+    def from_env(cls, env=None) -> "Fp8BackwardConfig":
+        """The reference's switch names (``ops/triton/bwd_fp8.py``), read once."""
+        env = os.environ if env is None else env
+        return cls(
+            enabled=env.get("DLRM_HSTU_FP8_BWD", "0") == "1",
+            uvqk=env.get("DLRM_HSTU_FP8_BWD_UVQK", "0") == "1",
+            out_wgrad_fp8=env.get("DLRM_HSTU_FP8_BWD_OUT_WGRAD", "0") == "1",
+            uvqk_wgrad_fp8t=env.get("DLRM_HSTU_FP8_BWD_UVQK_WGRAD", "bf16").strip().lower() == "fp8t",
+            margin=float(env.get("DLRM_HSTU_FP8_BWD_MARGIN", "8")),
+            warmup_calls=max(1, int(env.get("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "4"))),
+            refresh_calls=max(1, int(env.get("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "200"))),
+            grad_format=env.get("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e5m2").lower(),
+        )
+
+    @property
+    def grad_dtype(self) -> torch.dtype:
+        return E4M3 if self.grad_format == "e4m3" else E5M2
+
+    @property
+    def grad_limit(self) -> float:
+        return E4M3_MAX if self.grad_format == "e4m3" else E5M2_MAX
 
 
-def _margin() -> float:
-    return float(os.environ.get("DLRM_HSTU_FP8_BWD_MARGIN", "8"))
+_default: Optional[Fp8BackwardConfig] = None
 
 
-def _refresh_calls() -> int:
-    return max(1, int(os.environ.get("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "200")))
+def default_config() -> Fp8BackwardConfig:
+    """The process default: the environment's switches, read on first use."""
+    global _default
+    if _default is None:
+        _default = Fp8BackwardConfig.from_env()
+    return _default
 
 
-def _warmup_calls() -> int:
-    return max(1, int(os.environ.get("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "4")))
+def set_default_config(cfg: Optional[Fp8BackwardConfig]) -> None:
+    """Replace the process default (None: read the environment again on next use)."""
+    global _default
+    _default = cfg
 
 
-def grad_dtype_and_limit() -> Tuple[torch.dtype, float]:
-    fmt = os.environ.get("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e5m2").lower()
-    if fmt not in ("e5m2", "e4m3"):
-        raise ValueError(f"DLRM_HSTU_FP8_BWD_GRAD_FORMAT={fmt!r}")
-    return (E4M3, E4M3_MAX) if fmt == "e4m3" else (E5M2, E5M2_MAX)
+def _cfg(config: Optional[Fp8BackwardConfig]) -> Fp8BackwardConfig:
+    return default_config() if config is None else config
+
+
+def enabled(config: Optional[Fp8BackwardConfig] = None) -> bool:
+    return _cfg(config).enabled
+
+
+def grad_dtype_and_limit(config: Optional[Fp8BackwardConfig] = None) -> Tuple[torch.dtype, float]:
+    c = _cfg(config)
+    return c.grad_dtype, c.grad_limit
 
 
 def _code(dtype: torch.dtype) -> int:
@@ -74,7 +135,8 @@ def _code(dtype: torch.dtype) -> int:
 def quantize_row_major(value: torch.Tensor, inv_scale: torch.Tensor, dtype: Optional[torch.dtype] = None,
                        limit: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """(fp8(clamp(value * inv_scale, +-limit)), amax(|value|)) in one pass;
-    the amax is of the input, before scaling."""
+    the amax is of the input, before scaling.  dtype / limit default to the
+    process default's gradient format."""
     gdt, glim = grad_dtype_and_limit()
     dtype = gdt if dtype is None else dtype
     limit = glim if limit is None else limit
@@ -138,93 +200,136 @@ def quantize_amax_colsum(value: torch.Tensor, inv_scale: torch.Tensor, pad_to: i
     return out, amax, colsum
 
 
-class SiteScale:
-    """One backward tensor's scale, held and published on the device.
+class GradScaleSite:
+    """Delayed scaling of one backward tensor (one site of one layer).
 
-    ``scale`` dequantizes (fp8 value * scale = original), ``inv_scale`` is what
-    the cast multiplies by.  The window's amax accumulates in ``pending``.
+    All numbers live in one device tensor ``state`` = [scale, inverse scale,
+    peak of the current window, windows whose amax overflowed the format], so
+    publishing a scale is a device-side update with no host read.  ``scale``
+    and ``inv_scale`` are views of it: the dequantization scale (fp8 value *
+    scale = gradient) and what the cast multiplies by.  The host keeps only
+    the call count.
+
+    Policy (the reference's, ``ops/triton/bwd_fp8.py:869-1154``): the first
+    ``warmup_calls`` calls are not quantized (the caller runs bf16) and only
+    feed the window; then the window's peak times margin / format max becomes
+    the scale, and every ``refresh_calls``-th call publishes the window that
+    ends with it.
     """
 
-    def __init__(self, site: str, device: torch.device) -> None:
-        self.site = site
+    def __init__(self, device: torch.device) -> None:
+        self.state = torch.zeros(4, dtype=torch.float32, device=device)
         self.calls = 0
-        self.scale = torch.zeros(1, dtype=torch.float32, device=device)
-        self.inv_scale = torch.zeros(1, dtype=torch.float32, device=device)
-        self.pending = torch.zeros((), dtype=torch.float32, device=device)
-        self.clipped_windows = torch.zeros((), dtype=torch.int64, device=device)
-        self.published = False
+        self.live = False
 
-    def accumulate(self, amax: torch.Tensor) -> None:
-        torch.maximum(self.pending, amax, out=self.pending)
+    @property
+    def scale(self) -> torch.Tensor:
+        return self.state[0:1]
 
-    def publish(self) -> None:
-        """The window's amax becomes the next window's scale (clamped away
-        from zero so an all-zero window cannot publish an infinite inverse)."""
-        _, limit = grad_dtype_and_limit()
-        self.scale.copy_((self.pending.clamp_min(1.0e-30) * (_margin() / limit)).reshape(1))
-        self.inv_scale.copy_(1.0 / self.scale)
-        self.pending.zero_()
-        self.published = True
+    @property
+    def inv_scale(self) -> torch.Tensor:
+        return self.state[1:2]
 
-    def note_clipping(self, amax: torch.Tensor) -> None:
-        _, limit = grad_dtype_and_limit()
-        self.clipped_windows += (amax > self.scale.reshape(()) * limit).to(torch.int64)
+    @property
+    def overflow_windows(self) -> torch.Tensor:
+        return self.state[3]
+
+    def fold(self, amax: torch.Tensor, cfg: Fp8BackwardConfig) -> None:
+        """Add one call's max |gradient| to the window (and, once quantizing,
+        count the call if that amax overflowed the scale in use)."""
+        a = amax.reshape(1).to(torch.float32)
+        if self.live:
+            self.state[3:4].add_((a > self.state[0:1] * cfg.grad_limit).to(torch.float32))
+        torch.maximum(self.state[2:3], a, out=self.state[2:3])
+
+    def roll(self, cfg: Fp8BackwardConfig) -> None:
+        """Publish the window's scale and start a new window."""
+        s = self.state[2:3].clamp_min(1.0e-30) * (cfg.margin / cfg.grad_limit)
+        self.state[0:3].copy_(torch.cat([s, s.reciprocal(), torch.zeros_like(s)]))
+        self.live = True
+
+    def admit(self, cfg: Fp8BackwardConfig) -> Tuple[bool, bool]:
+        """Count this call: (quantize it?, does it end a window?)."""
+        self.calls += 1
+        if not self.live:
+            return False, self.calls >= cfg.warmup_calls
+        return True, self.calls % cfg.refresh_calls == 0
 
 
-_sites: Dict[str, SiteScale] = {}
-_layer_index: Dict[Tuple[str, int], int] = {}
+class _Registry:
+    """Sites by (name, layer).  A layer is numbered by the order in which its
+    discriminator (the weight's storage address) first appears for a site."""
+
+    def __init__(self) -> None:
+        self.sites: Dict[Tuple[str, int], GradScaleSite] = {}
+        self.layers: Dict[str, Dict[int, int]] = {}
+
+    def layer_of(self, site: str, discriminator: Optional[int]) -> int:
+        if discriminator is None:
+            return -1
+        seen = self.layers.setdefault(site, {})
+        return seen.setdefault(discriminator, len(seen))
+
+    def get(self, site: str, discriminator: Optional[int], device: torch.device) -> GradScaleSite:
+        key = (site, self.layer_of(site, discriminator))
+        found = self.sites.get(key)
+        if found is None:
+            found = self.sites[key] = GradScaleSite(device)
+        return found
+
+
+_registry = _Registry()
 
 
 def reset_sites() -> None:
     """Forget every site's state (tests, or a new run in the same process)."""
-    _sites.clear()
-    _layer_index.clear()
+    global _registry
+    _registry = _Registry()
 
 
 def site_name(site: str, discriminator: Optional[int]) -> str:
-    """One layer's instance of a site, indexed in order of first appearance."""
-    if discriminator is None:
-        return site
-    key = (site, discriminator)
-    if key not in _layer_index:
-        _layer_index[key] = sum(1 for k in _layer_index if k[0] == site)
-    return f"{site}.L{_layer_index[key]}"
+    """Printable name of one layer's instance of a site: ``site`` or ``site.L<n>``."""
+    layer = _registry.layer_of(site, discriminator)
+    return site if layer < 0 else f"{site}.L{layer}"
 
 
-def site_state(site: str, device: torch.device) -> SiteScale:
-    st = _sites.get(site)
-    if st is None:
-        st = _sites[site] = SiteScale(site, device)
-    return st
+def find_site(site: str, discriminator: Optional[int] = None, layer: Optional[int] = None) -> Optional[GradScaleSite]:
+    """The state of a site (by its discriminator, or by layer number), if it exists."""
+    if layer is None:
+        layer = -1 if discriminator is None else _registry.layers.get(site, {}).get(discriminator, -2)
+    return _registry.sites.get((site, layer))
 
 
 def quantize_gradient(site: str, gradient: torch.Tensor, discriminator: Optional[int] = None,
-                      snapshot_decode_scale: bool = False) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+                      snapshot_decode_scale: bool = False,
+                      config: Optional[Fp8BackwardConfig] = None) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
     """(fp8 gradient, dequantization scale) under the delayed-scale policy, or
     None while the site warms up (the caller's signal to run bf16).
 
-    As in the reference, the returned scale is the site's scale tensor, which
-    a refresh on this call has already updated in place; with
-    ``snapshot_decode_scale`` it is a copy of the scale the payload was cast
-    with, taken before the refresh."""
-    if not enabled():
+    On a call that ends a window the site publishes a new scale in place
+    after the cast.  The returned scale is then, as in the reference, the
+    live (already refreshed) scale tensor, unless ``snapshot_decode_scale``
+    asks for a copy of the scale the payload was cast with."""
+    cfg = _cfg(config)
+    if not cfg.enabled:
         return None
     if gradient.numel() == 0 or gradient.dtype not in (torch.bfloat16, torch.float32, torch.float16):
         return None
-    state = site_state(site_name(site, discriminator), gradient.device)
-    state.calls += 1
-    if not state.published:
-        state.accumulate(gradient.detach().abs().amax().float())
-        if state.calls >= _warmup_calls():
-            state.publish()
+    ctl = _registry.get(site, discriminator, gradient.device)
+    quantize, ends_window = ctl.admit(cfg)
+    if not quantize:
+        ctl.fold(gradient.detach().abs().amax(), cfg)
+        if ends_window:
+            ctl.roll(cfg)
         return None
-    q, amax = quantize_row_major(gradient, state.inv_scale)
-    state.note_clipping(amax)
-    state.accumulate(amax)
-    decode = state.scale.clone() if snapshot_decode_scale else state.scale
-    if state.calls % _refresh_calls() == 0:
-        state.publish()
-    return q, decode
+    payload, amax = quantize_row_major(gradient, ctl.inv_scale, cfg.grad_dtype, cfg.grad_limit)
+    ctl.fold(amax, cfg)
+    decode = ctl.scale
+    if ends_window:
+        if snapshot_decode_scale:
+            decode = decode.clone()
+        ctl.roll(cfg)
+    return payload, decode
 
 
 def quantize_weight(weight: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -262,23 +367,29 @@ def fp8_dgrad(grad8: torch.Tensor, grad_scale: torch.Tensor, w8: torch.Tensor, w
     return out
 
 
-def out_wgrad_fp8() -> bool:
-    """``DLRM_HSTU_FP8_BWD_OUT_WGRAD=1`` (with the FP8 backward on): the output
-    projection's weight gradient from the forward's e4m3 LN * U output and the
-    dgrad's e5m2 dout cast (``triton_hstu_linear.py:87-110``)."""
-    return enabled() and os.environ.get("DLRM_HSTU_FP8_BWD_OUT_WGRAD", "0") == "1"
+def out_wgrad_fp8(config: Optional[Fp8BackwardConfig] = None) -> bool:
+    """The output projection's weight gradient in FP8, from the forward's e4m3
+    LN * U output and the dgrad's e5m2 dout cast (``DLRM_HSTU_FP8_BWD_OUT_WGRAD``,
+    ``triton_hstu_linear.py:87-110``)."""
+    c = _cfg(config)
+    return c.enabled and c.out_wgrad_fp8
 
 
-def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor, return_quantized: bool = False):
+def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor, return_quantized: bool = False,
+                            config: Optional[Fp8BackwardConfig] = None):
     """``dy = gradient @ weight^T`` in FP8 (gradient [M, N_out], weight
     [K_in, N_out] as stored by the layer), or None to fall back to bf16.
     With ``return_quantized``: (dy, gradient_fp8, its decode scale), for a
-    weight gradient that reuses the cast."""
-    if not enabled() or not _has_stable_identity(weight):
+    weight gradient that reuses the cast; the decode scale is then the one
+    the payload was cast with even on a refresh call (the reference's
+    out-wgrad path snapshots it the same way, ``ops/triton/bwd_fp8.py:1472-1482``)."""
+    cfg = _cfg(config)
+    if not cfg.enabled or not _has_stable_identity(weight):
         return None
     if gradient.dim() != 2 or gradient.shape[-1] % 128 or weight.shape[0] % 128:
         return None
-    quantized = quantize_gradient("output_projection", gradient, discriminator=weight.data_ptr())
+    quantized = quantize_gradient("output_projection", gradient, discriminator=weight.data_ptr(),
+                                  snapshot_decode_scale=return_quantized, config=cfg)
     if quantized is None:
         return None
     g8, gs = quantized
@@ -287,29 +398,30 @@ def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor, return
     return (dy, g8, gs) if return_quantized else dy
 
 
-def uvqk_fp8_backward_enabled() -> bool:
-    """``DLRM_HSTU_FP8_BWD_UVQK=1`` with the e5m2 gradient format."""
-    return (os.environ.get("DLRM_HSTU_FP8_BWD_UVQK", "0") == "1"
-            and grad_dtype_and_limit()[0] == E5M2)
+def uvqk_fp8_backward_enabled(config: Optional[Fp8BackwardConfig] = None) -> bool:
+    """The UVQK e5m2 dgrad arm (``DLRM_HSTU_FP8_BWD_UVQK=1`` with the e5m2 format)."""
+    c = _cfg(config)
+    return c.uvqk and c.grad_dtype == E5M2
 
 
-def uvqk_wgrad_fp8t() -> bool:
-    """``DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t`` (with the UVQK arm on): the UVQK
-    weight gradient from the forward's e4m3 LN output and the e5m2 gradient
-    (``uvqk_wgrad_fp8t``, ``ops/triton/bwd_fp8.py:1755-1762``)."""
-    return (uvqk_fp8_backward_enabled()
-            and os.environ.get("DLRM_HSTU_FP8_BWD_UVQK_WGRAD", "bf16").strip().lower() == "fp8t")
+def uvqk_wgrad_fp8t(config: Optional[Fp8BackwardConfig] = None) -> bool:
+    """The UVQK weight gradient from the forward's e4m3 LN output and the e5m2
+    gradient (``DLRM_HSTU_FP8_BWD_UVQK_WGRAD=fp8t``, ``uvqk_wgrad_fp8t``,
+    ``ops/triton/bwd_fp8.py:1755-1762``)."""
+    c = _cfg(config)
+    return uvqk_fp8_backward_enabled(c) and c.uvqk_wgrad_fp8t
 
 
 def uvqk_projection_backward(
     dz: Optional[torch.Tensor],
     normed_x: Optional[torch.Tensor],
-    input_scale_value: Optional[float],
+    input_scale_value,
     weight: torch.Tensor,
     site: str = "uvqk_projection",
     per_layer: bool = True,
     normed_x_fp8_t: Optional[torch.Tensor] = None,
     recompute_normed_x: Optional[Callable[[], torch.Tensor]] = None,
+    config: Optional[Fp8BackwardConfig] = None,
 ) -> Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]]:
     """(d_normed_x, d_weight, d_bias fp32) of ``z = normed_x @ weight + b``
     with an FP8 dgrad, or None for the caller's bf16 path.
@@ -322,11 +434,13 @@ def uvqk_projection_backward(
     ``per_layer`` keys the scale on the weight's storage (then it must be the
     leaf parameter).
     ``normed_x`` may be None when ``recompute_normed_x`` is given.  With
-    ``uvqk_wgrad_fp8t()``, ``normed_x_fp8_t`` (the forward's e4m3 LN output,
+    ``uvqk_wgrad_fp8t``, ``normed_x_fp8_t`` (the forward's e4m3 LN output,
     here row-major [M, K] -- the kernel reads token rows directly, so no
-    token-major copy is made) and ``input_scale_value`` > 0, the weight
-    gradient is the FP8 product (x8 s_x)^T (dz8 s_dz) instead."""
-    if not uvqk_fp8_backward_enabled():
+    token-major copy is made) and ``input_scale_value`` (its dequantization
+    scale: a float > 0 or a device fp32 tensor), the weight gradient is the
+    FP8 product (x8 s_x)^T (dz8 s_dz) instead."""
+    cfg = _cfg(config)
+    if not uvqk_fp8_backward_enabled(cfg):
         return None
     if per_layer and not _has_stable_identity(weight):
         return None
@@ -335,28 +449,28 @@ def uvqk_projection_backward(
             or (normed_x is None and recompute_normed_x is None)
             or (normed_x is not None and tuple(normed_x.shape) != (dz.shape[0], weight.shape[0]))):
         return None
-    state = site_state(site_name(site, weight.data_ptr() if per_layer else None), dz.device)
-    state.calls += 1
-    if not state.published:
-        state.accumulate(dz.detach().abs().amax().float())
-        if state.calls >= _warmup_calls():
-            state.publish()
+    ctl = _registry.get(site, weight.data_ptr() if per_layer else None, dz.device)
+    quantize, ends_window = ctl.admit(cfg)
+    if not quantize:
+        ctl.fold(dz.detach().abs().amax(), cfg)
+        if ends_window:
+            ctl.roll(cfg)
         return None
-    dz8, amax, colsum = quantize_amax_colsum(dz, state.inv_scale, dtype=E5M2)
-    state.note_clipping(amax)
-    state.accumulate(amax)
-    # the payload was cast with the scale in use now; a refresh rewrites it in place
-    if state.calls % _refresh_calls() == 0:
-        grad_scale = state.scale.clone()
-        state.publish()
-    else:
-        grad_scale = state.scale
+    dz8, amax, colsum = quantize_amax_colsum(dz, ctl.inv_scale, dtype=E5M2)
+    ctl.fold(amax, cfg)
+    # decode with the scale the payload was cast with (a refresh rewrites the live one)
+    grad_scale = ctl.scale.clone() if ends_window else ctl.scale
+    if ends_window:
+        ctl.roll(cfg)
     w8, w_scale = quantize_weight(weight)
-    use_tm = (uvqk_wgrad_fp8t() and normed_x_fp8_t is not None and input_scale_value is not None
-              and input_scale_value > 0.0 and normed_x_fp8_t.dtype == E4M3
-              and tuple(normed_x_fp8_t.shape) == (dz.shape[0], weight.shape[0]))
-    if use_tm:
-        sx = torch.full((1,), float(input_scale_value), dtype=torch.float32, device=dz.device)
+    sx = None
+    if (uvqk_wgrad_fp8t(cfg) and normed_x_fp8_t is not None and normed_x_fp8_t.dtype == E4M3
+            and tuple(normed_x_fp8_t.shape) == (dz.shape[0], weight.shape[0])):
+        if torch.is_tensor(input_scale_value):
+            sx = input_scale_value.reshape(-1)[:1].to(torch.float32)
+        elif input_scale_value is not None and input_scale_value > 0.0:
+            sx = torch.full((1,), float(input_scale_value), dtype=torch.float32, device=dz.device)
+    if sx is not None:
         d_w = fp8_wgrad(normed_x_fp8_t, dz8, sx, grad_scale)
     else:
         xn = normed_x if normed_x is not None else recompute_normed_x()

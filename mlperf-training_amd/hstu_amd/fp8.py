@@ -7,6 +7,11 @@ relative to ``recommendation_v4/hstu/generative_recommenders/``):
 * ``quantize_with_scale`` (:760-781) / ``calibrated_scale`` (:396-413)
   -> ``quantize_with_scale`` / ``quantize_e4m3_rows`` (also per row and per
   (token, head) groups, which the reference does not have);
+* the per-layer FP8 scale state ``[scale, completed, amax history]``
+  (``fp8_scale_state_size`` :346-349, ``fp8_scale_tensor`` :352-355,
+  ``calibrate_scale_buffer`` :694-749, ``modules/stu.py:317-328``) ->
+  the same functions, plus ``scale_ready`` (is a scale usable now, known on the
+  host without a device read once the state is frozen);
 * ``scaled_addmm_fp8_preq`` (:1756) -> ``scaled_addmm_fp8_preq`` (bf16 out,
   bias or residual);
 * ``scaled_mm_fp8_out_preq`` (:2409) -> ``scaled_mm_fp8_out_preq`` (e4m3 out
@@ -18,7 +23,8 @@ pre-quantized ``(w8_nk, w_scale)`` pair from ``quantize_weight_e4m3``.
 
 from __future__ import annotations
 
-from typing import Optional, Tuple, Union
+import os
+from typing import Dict, Optional, Tuple, Union
 
 import torch
 
@@ -26,6 +32,9 @@ from . import _lib
 
 E4M3 = torch.float8_e4m3fn
 E4M3_MAX = 448.0
+# The reference's defaults (``triton_fp8.py:96-101``), read once at import as it does.
+ASCALE_MARGIN = float(os.environ.get("DLRM_HSTU_FP8_GEMM_ASCALE_MARGIN", "1.5"))
+CALIBRATION_STEPS = max(1, int(os.environ.get("DLRM_HSTU_FP8_CALIBRATION_STEPS", "4")))
 Weight = Union[torch.Tensor, Tuple[torch.Tensor, torch.Tensor]]
 
 
@@ -66,11 +75,112 @@ def quantize_with_scale(value: torch.Tensor, scale: torch.Tensor) -> torch.Tenso
     return out.view(value.shape)
 
 
-def calibrated_scale(value: torch.Tensor, *, margin: float = 1.0) -> torch.Tensor:
-    """Per-tensor scale amax*margin/448 as a (1, 1) fp32 tensor
-    (``calibrated_scale``, ``triton_fp8.py:396-413``)."""
+def calibrated_scale(value: torch.Tensor, *, margin: Optional[float] = None,
+                     fp8_max: float = E4M3_MAX) -> torch.Tensor:
+    """Per-tensor scale amax*margin/fp8_max as a (1, 1) fp32 tensor, margin
+    1.5 by default (``calibrated_scale``, ``triton_fp8.py:396-413``)."""
+    m = ASCALE_MARGIN if margin is None else margin
     amax = value.detach().abs().amax().float().clamp_min(1.0e-12)
-    return (amax * margin / E4M3_MAX).reshape(1, 1)
+    return (amax * m / fp8_max).reshape(1, 1)
+
+
+# ---------------------------------------------------------------------------
+# per-layer scale state: [scale, completed calibration steps, amax history]
+# ---------------------------------------------------------------------------
+def fp8_scale_state_size() -> int:
+    """Length of one scale state buffer: scale, completed count, history."""
+    return 2 + CALIBRATION_STEPS
+
+
+def fp8_scale_tensor(scale_state: torch.Tensor) -> torch.Tensor:
+    """The (1, 1) scale view of a state buffer (or of a plain scale)."""
+    if scale_state.numel() < 1:
+        raise ValueError("FP8 scale state cannot be empty")
+    return scale_state.reshape(-1)[:1].reshape(1, 1)
+
+
+# Host knowledge of each state buffer: storage address -> (version counter
+# when last seen, completed steps).  Buffers this module updates stay known
+# without reading the device; a buffer changed elsewhere (loaded from a
+# checkpoint, reset) is read once.
+_known: Dict[Tuple[int, int], Tuple[int, int]] = {}
+
+
+def _key(buf: torch.Tensor) -> Tuple[int, int]:
+    return buf.untyped_storage().data_ptr(), buf.storage_offset()
+
+
+def _completed(buf: torch.Tensor) -> int:
+    key = _key(buf)
+    seen = _known.get(key)
+    if seen is not None and seen[0] == buf._version:
+        return seen[1]
+    flat = buf.reshape(-1)
+    # one device read; a positive scale in a short buffer counts as complete
+    done = int(flat[1].item()) if flat.numel() >= 3 else (1 if float(flat[0].item()) > 0.0 else 0)
+    _known[key] = (buf._version, done)
+    return done
+
+
+def _remember(buf: torch.Tensor, done: int) -> None:
+    _known[_key(buf)] = (buf._version, done)
+
+
+def scale_ready(scale: Optional[torch.Tensor]) -> bool:
+    """Can the FP8 path use this scale now?  A one-element tensor is a plain
+    scale and always is (its value is not read); a state buffer is once its
+    calibration window is complete.  No device read for a buffer this module
+    calibrated, or any one-element scale."""
+    if scale is None:
+        return False
+    if scale.numel() == 1:
+        return True
+    if scale.numel() < 3:
+        raise ValueError("FP8 scale state must contain scale, count, and amax history")
+    return _completed(scale) >= scale.numel() - 2
+
+
+def calibrate_scale_buffer(scale_buffer: torch.Tensor, value: torch.Tensor, *, margin: Optional[float] = None,
+                           synchronize: bool = True) -> float:
+    """One calibration step of a scale state (``calibrate_scale_buffer``,
+    ``triton_fp8.py:694-749``): this call's amax joins the history; once the
+    history is full the scale is max(history) * margin / 448 and stays there
+    (the state is frozen).  A one-element buffer is simply set from this
+    call.  Returns the scale (0.0 while calibrating).  An all-zero value is
+    not a step.  With torch.distributed initialised (world > 1) the amax is
+    MAX-reduced across ranks first.  Bounded warm-up work: it reads the amax
+    on the host, as the reference does; a frozen state returns at once."""
+    m = ASCALE_MARGIN if margin is None else margin
+    flat = scale_buffer.reshape(-1)
+    if flat.numel() >= 3 and _completed(scale_buffer) >= flat.numel() - 2:
+        return float(flat[0].item())
+    amax = (value.detach().abs().amax().float() if value.numel()
+            else torch.zeros((), dtype=torch.float32, device=scale_buffer.device))
+    if (synchronize and torch.distributed.is_available() and torch.distributed.is_initialized()
+            and torch.distributed.get_world_size() > 1):
+        torch.distributed.all_reduce(amax, op=torch.distributed.ReduceOp.MAX)
+    a = float(amax.item())
+    if not a > 0.0:
+        return float(flat[0].item()) if flat.numel() else 0.0
+    a = max(a, 1.0e-12)
+    if flat.numel() == 1:
+        flat.fill_(a * m / E4M3_MAX)
+        _remember(scale_buffer, 1)
+        return float(flat[0].item())
+    if flat.numel() < 3:
+        raise ValueError("FP8 scale state must contain scale, count, and amax history")
+    steps = flat.numel() - 2
+    done = min(_completed(scale_buffer), steps)
+    flat[2 + done].fill_(a)
+    done += 1
+    flat[1].fill_(float(done))
+    if done < steps:
+        flat[0].zero_()
+        _remember(scale_buffer, done)
+        return 0.0
+    flat[0:1].copy_(flat[2:].amax().reshape(1) * (m / E4M3_MAX))
+    _remember(scale_buffer, done)
+    return float(flat[0].item())
 
 
 def quantize_weight_e4m3(w_kn: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:

@@ -198,9 +198,13 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
     q, k, v = _row_view(q), _row_view(k), _row_view(v)
     dout = _row_view(dout.to(torch.bfloat16))
     if fp8:
+        if q_scale is None or k_scale is None or v_scale is None:
+            raise ValueError("e4m3 inputs need q_scale, k_scale and v_scale")
         qs, srs, shs = _scale_tensor(q_scale, T, H, q.device)
-        ks, _, _ = _scale_tensor(k_scale, T, H, q.device)
-        vs, _, _ = _scale_tensor(v_scale, T, H, q.device)
+        ks, srs2, shs2 = _scale_tensor(k_scale, T, H, q.device)
+        vs, srs3, shs3 = _scale_tensor(v_scale, T, H, q.device)
+        if not (srs == srs2 == srs3 and shs == shs2 == shs3):
+            raise ValueError("q/k/v scales must share one layout (all scalars or all [T, H])")
     else:
         qs = ks = vs = None
         srs = shs = 0

@@ -17,7 +17,7 @@ MFMAs, :1330-1394).  The e4m3 P / dS operands of that backward are not built.
 from __future__ import annotations
 
 import os
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 
@@ -52,9 +52,22 @@ def quantize_do_e4m3_blk(dout: torch.Tensor, seq_offsets: torch.Tensor, N: int) 
     return y, e8
 
 
+_full: Optional[bool] = None
+
+
 def bwd_full_fp8_enabled() -> bool:
-    """``DLRM_HSTU_FP8_BWD_FULL`` in (1, true, on, yes)."""
-    return os.environ.get("DLRM_HSTU_FP8_BWD_FULL", "0").strip().lower() in ("1", "true", "on", "yes")
+    """The process default for the full-FP8 backward: ``DLRM_HSTU_FP8_BWD_FULL``
+    in (1, true, on, yes), read once."""
+    global _full
+    if _full is None:
+        _full = os.environ.get("DLRM_HSTU_FP8_BWD_FULL", "0").strip().lower() in ("1", "true", "on", "yes")
+    return _full
+
+
+def set_bwd_full_fp8(flag: Optional[bool]) -> None:
+    """Set the full-FP8 backward default (None: read the environment again on next use)."""
+    global _full
+    _full = flag
 
 
 def dequantize_do_e4m3_blk(dout8: torch.Tensor, e8: torch.Tensor) -> torch.Tensor:

@@ -18,9 +18,9 @@ Drop-in names (reference file:line, relative to
 Dropout follows the reference's separated-mask path (the one it runs on
 gfx950): an int8 mask [N, D] with one keep bit per concatenated block (bit 0 =
 y, then x, then u), drawn from Philox4x32-10 with the reference's counters,
-in the 32-bit scheme or, with ``DLRM_HSTU_FP8_MASK16=1`` (as
-``yambda_5b.gin`` sets), the 16-bit-half scheme -- the same bits for the same
-seed.  The mask is returned by the forward and reused by the backward.
+in the 32-bit scheme or, with ``set_mask16(True)`` (the process default
+comes from ``DLRM_HSTU_FP8_MASK16=1``, as ``yambda_5b.gin`` sets it), the
+16-bit-half scheme -- the same bits for the same seed.  The mask is returned by the forward and reused by the backward.
 
 Not served (raise ``NotImplementedError``): group norm, ``rng_row_indices``
 (compact last-layer rows), precomputed mean/rstd, the weighted LayerNorm
@@ -35,6 +35,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib, bwd_fp8
+from . import fp8 as _fp8
 from .wgrad import fp8_wgrad, token_wgrad
 from .hstu_attention import HammerKernel
 from .pt_hstu_linear import pytorch_hstu_compute_output, pytorch_norm_mul_dropout
@@ -48,9 +49,23 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+_mask16: Optional[bool] = None
+
+
 def _use_mask16() -> bool:
-    """16-bit-half keep decisions (``_use_mask16``, triton_hstu_linear.py:2358-2374)."""
-    return os.environ.get("DLRM_HSTU_FP8_MASK16", "0") == "1"
+    """16-bit-half keep decisions (``_use_mask16``, triton_hstu_linear.py:2358-2374):
+    the process default, read once from ``DLRM_HSTU_FP8_MASK16``."""
+    global _mask16
+    if _mask16 is None:
+        _mask16 = os.environ.get("DLRM_HSTU_FP8_MASK16", "0") == "1"
+    return _mask16
+
+
+def set_mask16(flag: Optional[bool]) -> None:
+    """Set the dropout mask scheme (True: 16-bit halves; None: read the
+    environment again on next use)."""
+    global _mask16
+    _mask16 = flag
 
 
 def _block_d(D: int) -> int:
@@ -95,14 +110,15 @@ def _ncols(concat_u: bool, concat_x: bool) -> int:
 
 
 def create_dropout_mask(N: int, D: int, concat_u: bool, concat_x: bool, dropout_ratio: float, seed: int,
-                        device) -> torch.Tensor:
+                        device, mask16: Optional[bool] = None) -> torch.Tensor:
     """int8 [N, D] keep mask, bit j = mask j (``_create_dropout_mask``,
-    triton_hstu_linear.py:2547-2600)."""
+    triton_hstu_linear.py:2547-2600); ``mask16`` None = the process default."""
+    mask16 = _use_mask16() if mask16 is None else bool(mask16)
     _check_d(D)
     mask = torch.empty((N, D), dtype=torch.int8, device=device)
     if N == 0:
         return mask
-    st = _lib.fn("hstu_dropout_mask")(N, D, _ncols(concat_u, concat_x), int(_use_mask16()), float(dropout_ratio),
+    st = _lib.fn("hstu_dropout_mask")(N, D, _ncols(concat_u, concat_x), int(mask16), float(dropout_ratio),
                                       int(seed) & 0xFFFFFFFFFFFFFFFF, mask.data_ptr(), D,
                                       torch.cuda.current_stream(device).cuda_stream)
     _lib.check(st, "hstu_dropout_mask")
@@ -113,7 +129,11 @@ def create_dropout_mask(N: int, D: int, concat_u: bool, concat_x: bool, dropout_
 # LayerNorm * U * dropout
 # ---------------------------------------------------------------------------
 def _ln_fwd(x, u, weight, bias, eps, dropout_ratio, training, silu_u, concat_u, concat_x, act, seed,
-            output_fp8, inv_scale):
+            output_fp8, inv_scale, out_scale: Optional[torch.Tensor] = None, mask16: Optional[bool] = None):
+    """The LN * U * dropout kernel.  An e4m3 output is scaled by ``inv_scale``
+    (host float) or, with ``out_scale`` (a device fp32 scale tensor), by
+    1 / out_scale[0] read on the device.  ``mask16`` None = the process default."""
+    mask16 = _use_mask16() if mask16 is None else bool(mask16)
     x = _rows(x)
     _check_bf16("x", x)
     N, D = x.shape
@@ -139,9 +159,9 @@ def _ln_fwd(x, u, weight, bias, eps, dropout_ratio, training, silu_u, concat_u, 
     st = _lib.fn("hstu_ln_mul_fwd")(
         x.data_ptr(), x.stride(0), _lib.ptr(u), 0 if u is None else u.stride(0), w.data_ptr(), b.data_ptr(),
         float(eps), N, D, _ACT[act], int(bool(silu_u)), int(cu), int(bool(concat_x)), int(dropout),
-        float(dropout_ratio), int(seed) & 0xFFFFFFFFFFFFFFFF, int(_use_mask16()), _lib.ptr(mask), D,
+        float(dropout_ratio), int(seed) & 0xFFFFFFFFFFFFFFFF, int(mask16), _lib.ptr(mask), D,
         y.data_ptr(), y.stride(0), _lib.HSTU_DTYPE_FP8_E4M3 if output_fp8 else _lib.HSTU_DTYPE_BF16,
-        float(inv_scale), mean.data_ptr(), rstd.data_ptr(), _stream(x))
+        float(inv_scale), _lib.ptr(out_scale), mean.data_ptr(), rstd.data_ptr(), _stream(x))
     _lib.check(st, "hstu_ln_mul_fwd")
     return y, mean, rstd, mask
 
@@ -311,10 +331,6 @@ def triton_norm_mul_dropout(
 # ---------------------------------------------------------------------------
 # output block: LN * U * dropout -> output projection + residual
 # ---------------------------------------------------------------------------
-def _fp8_scale_value(scale: torch.Tensor) -> float:
-    return float(scale.detach().reshape(-1)[0].item())
-
-
 class HSTUComputeOutputFunction(torch.autograd.Function):
     """``HSTUComputeOutputFunction`` (``triton_hstu_linear.py:5109-5900``),
     default (unfused-backward) contract: e4m3 LN output into the FP8 output
@@ -327,26 +343,32 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
     def forward(ctx, attn, u, x, norm_weight, norm_bias, output_weight, eps, dropout_ratio, training,
                 silu_u=False, concat_u=False, concat_x=False, mul_u_activation_type="none", group_norm=False,
                 num_heads=1, linear_dim=-1, seed=None, recompute_y_in_backward=False, rng_row_indices=None,
-                fp8_output_scale=None):
+                fp8_output_scale=None, fp8_backward=None, dropout_mask16=None):
         if group_norm:
             raise NotImplementedError("group norm is not served by this build")
         if rng_row_indices is not None:
             raise NotImplementedError("rng_row_indices (compact rows) is not served")
         if dropout_ratio == 0.0:
             training = False
-        use_fp8 = fp8_output_scale is not None and recompute_y_in_backward
+        # the scale is used once ready (a plain scale, or a calibrated state
+        # buffer); until then the call runs bf16 and calibrates the state
+        # (triton_hstu_linear.py:5260-5280).  It stays on the device.
+        ready = _fp8.scale_ready(fp8_output_scale)
+        use_fp8 = ready and recompute_y_in_backward
         seed = _seed(seed, training)
+        scale = None
         if use_fp8:
-            from .fp8 import scaled_addmm_fp8_preq
-
-            sv = _fp8_scale_value(fp8_output_scale)
+            scale = _fp8.fp8_scale_tensor(fp8_output_scale).reshape(1)
             y, mean, rstd, mask = _ln_fwd(attn, u, norm_weight, norm_bias, eps, dropout_ratio, training, silu_u,
-                                          concat_u, concat_x, mul_u_activation_type, seed, True, 1.0 / sv)
-            scale = torch.full((1,), sv, dtype=torch.float32, device=attn.device)
-            out = scaled_addmm_fp8_preq(y, scale, output_weight, x, out_dtype=x.dtype)
+                                          concat_u, concat_x, mul_u_activation_type, seed, True, 1.0, out_scale=scale,
+                                          mask16=dropout_mask16)
+            out = _fp8.scaled_addmm_fp8_preq(y, scale, output_weight, x, out_dtype=x.dtype)
         else:
             y, mean, rstd, mask = _ln_fwd(attn, u, norm_weight, norm_bias, eps, dropout_ratio, training, silu_u,
-                                          concat_u, concat_x, mul_u_activation_type, seed, False, 1.0)
+                                          concat_u, concat_x, mul_u_activation_type, seed, False, 1.0,
+                                          mask16=dropout_mask16)
+            if fp8_output_scale is not None and not ready:
+                _fp8.calibrate_scale_buffer(fp8_output_scale, y)
             out = torch.addmm(x, y, output_weight.to(y.dtype))
         saved = [attn, u, norm_weight, norm_bias, mean, rstd, output_weight]
         if not recompute_y_in_backward:
@@ -354,7 +376,8 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         if mask is not None:
             saved.append(mask)
         # the e4m3 y feeds the FP8 output-projection weight gradient
-        ctx.y8_scale = sv if (use_fp8 and bwd_fp8.out_wgrad_fp8()) else None
+        ctx.y8_scale = scale if (use_fp8 and bwd_fp8.out_wgrad_fp8(fp8_backward)) else None
+        ctx.fp8_backward = fp8_backward
         if ctx.y8_scale is not None:
             saved.append(y)
         ctx.save_for_backward(*saved)
@@ -381,7 +404,9 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         dout = dout.contiguous()
         # FP8 dgrad (DLRM_HSTU_FP8_BWD=1; triton_hstu_linear.py:5586-5588): None
         # while the gradient's scale warms up, then e5m2 dout . e4m3 W^T
-        q = bwd_fp8.output_projection_dgrad(dout, output_weight, return_quantized=True) if bwd_fp8.enabled() else None
+        cfg = ctx.fp8_backward
+        q = (bwd_fp8.output_projection_dgrad(dout, output_weight, return_quantized=True, config=cfg)
+             if bwd_fp8.enabled(cfg) else None)
         dy = q[0] if q is not None else torch.mm(dout, output_weight.to(dout.dtype).t())
         # FP8 weight gradient (DLRM_HSTU_FP8_BWD_OUT_WGRAD=1) from the forward's
         # e4m3 y and the dgrad's e5m2 dout: the bf16 y is then not recomputed
@@ -389,15 +414,14 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         dattn, du, dw, db, y_re = _ln_bwd(dy, attn, u, norm_weight, norm_bias, mean, rstd, ratio, mask, silu_u,
                                           concat_u, concat_x, act, ctx.recompute and not fp8_w, ctx.du_row_width)
         if fp8_w:
-            sy = torch.full((1,), ctx.y8_scale, dtype=torch.float32, device=dout.device)
-            d_out_w = fp8_wgrad(y8, q[1], sy, q[2]).to(output_weight.dtype)
+            d_out_w = fp8_wgrad(y8, q[1], ctx.y8_scale, q[2]).to(output_weight.dtype)
         else:
             if y is None:
                 y = y_re
             # y^T dout over the tokens: the split-K wgrad kernel
             d_out_w = token_wgrad(y, dout).to(output_weight.dtype)
         return (dattn, du, dout, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
-                None, None, None, None, None, None, None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None)
 
 
 def triton_hstu_compute_output(
@@ -421,13 +445,20 @@ def triton_hstu_compute_output(
     recompute_y_in_backward: bool = False,
     rng_row_indices: Optional[torch.Tensor] = None,
     fp8_output_scale: Optional[torch.Tensor] = None,
+    *,
+    fp8_backward: Optional[bwd_fp8.Fp8BackwardConfig] = None,
+    dropout_mask16: Optional[bool] = None,
 ) -> torch.Tensor:
     """x + dropout([u' | attn | m(u) * LN(attn)]) @ output_weight
-    (``triton_hstu_linear.py:6494-6572``)."""
+    (``triton_hstu_linear.py:6494-6572``).  ``fp8_output_scale``: a
+    one-element device scale, or the reference's [2 + steps] scale state
+    (calibrated by the bf16 calls until frozen).  ``fp8_backward``: the FP8
+    backward arm's settings, ``dropout_mask16`` the dropout mask scheme
+    (default for both: the process default)."""
     return HSTUComputeOutputFunction.apply(attn, u, x, norm_weight, norm_bias, output_weight, eps, dropout_ratio,
                                            training, silu_u, concat_u, concat_x, mul_u_activation_type, group_norm,
                                            num_heads, linear_dim, seed, recompute_y_in_backward, rng_row_indices,
-                                           fp8_output_scale)
+                                           fp8_output_scale, fp8_backward, dropout_mask16)
 
 
 def hstu_compute_output(

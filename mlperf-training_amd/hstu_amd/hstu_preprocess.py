@@ -38,10 +38,6 @@ from .wgrad import token_wgrad
 DUVQK_WIDTH_ATTR = "_hstu_duvqk_width"
 
 
-def _scale_value(s) -> float:
-    return float(s.detach().reshape(-1)[0].item()) if torch.is_tensor(s) else float(s)
-
-
 def _adopt_duvqk(du: Optional[torch.Tensor], T: int, width: int, like: torch.Tensor) -> torch.Tensor:
     """The d(uvqk) buffer: ``du`` itself when it is the leading columns of a
     [T, width] row-major buffer (the output block allocated it so), else a
@@ -61,23 +57,28 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias,
                 max_seq_len, seq_offsets, attn_alpha, num_targets, max_attn_len, contextual_seq_len,
-                fp8_input_scale, fp8_qkv_scale, defer_silu, attn_bias):
+                fp8_input_scale, fp8_qkv_scale, defer_silu, attn_bias, fp8_backward=None):
         T, E = x.shape
         H, Dq, Dv = num_heads, attn_dim, hidden_dim
         nu = H * Dv
-        use_fp8 = fp8_input_scale is not None
+        # A scale is used once it is ready: a plain scale tensor always, a
+        # [2 + steps] state buffer once calibrated; until then this call runs
+        # the bf16 path and is one calibration step (triton_hstu_preprocess_and_attention.py:1300-1350).
+        # Scales stay on the device: the kernels read them there.
+        use_fp8 = _fp8.scale_ready(fp8_input_scale)
+        use_fp8_qkv = use_fp8 and _fp8.scale_ready(fp8_qkv_scale)
+        calibrate_qkv = fp8_qkv_scale is not None and not use_fp8_qkv
+        sa = None
         if use_fp8:
-            sx = _scale_value(fp8_input_scale)
+            sa = _fp8.fp8_scale_tensor(fp8_input_scale).reshape(1)
             x8, mean, rstd, _ = _ln_fwd(x, None, norm_weight, norm_bias, norm_eps, 0.0, False, False, False, False,
-                                        "none", 0, True, 1.0 / sx)
-            sa = torch.full((1,), sx, dtype=torch.float32, device=x.device)
+                                        "none", 0, True, 1.0, out_scale=sa)
             u = _fp8.fp8_gemm(x8, sa, uvqk_weight[:, :nu], bias=uvqk_bias[:nu],
                               silu_cols=None if defer_silu else (0, nu))
-            if fp8_qkv_scale is not None:
-                sqkv = _scale_value(fp8_qkv_scale)
+            if use_fp8_qkv:
+                qkv_scale = _fp8.fp8_scale_tensor(fp8_qkv_scale).reshape(1)
                 vqk = _fp8.fp8_gemm(x8, sa, uvqk_weight[:, nu:], bias=uvqk_bias[nu:], out_dtype=_fp8.E4M3,
-                                    out_scale=torch.full((1,), sqkv, dtype=torch.float32, device=x.device))
-                qkv_scale = sqkv
+                                    out_scale=qkv_scale)
             else:
                 vqk = _fp8.fp8_gemm(x8, sa, uvqk_weight[:, nu:], bias=uvqk_bias[nu:])
                 qkv_scale = None
@@ -85,11 +86,15 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         else:
             xn, mean, rstd, _ = _ln_fwd(x, None, norm_weight, norm_bias, norm_eps, 0.0, False, False, False, False,
                                         "none", 0, False, 1.0)
+            if fp8_input_scale is not None:
+                _fp8.calibrate_scale_buffer(fp8_input_scale, xn)
             uvqk = torch.addmm(uvqk_bias.to(x.dtype), xn, uvqk_weight.to(x.dtype))
             u_pre = uvqk[:, :nu]
             u = u_pre if defer_silu else F.silu(u_pre)
             vqk = uvqk[:, nu:]
             qkv_scale = None
+        if calibrate_qkv:
+            _fp8.calibrate_scale_buffer(fp8_qkv_scale, vqk)
         v = vqk[:, :nu].view(T, H, Dv)
         q = vqk[:, nu:nu + H * Dq].view(T, H, Dq)
         k = vqk[:, nu + H * Dq:].view(T, H, Dq)
@@ -97,7 +102,7 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
                                          contextual_seq_len, None, False, 0, qkv_scale, qkv_scale, qkv_scale,
                                          attn_bias=attn_bias)
         # the e4m3 LN output feeds the FP8 UVQK weight gradient (fp8t switch)
-        keep_x8 = use_fp8 and bwd_fp8.uvqk_wgrad_fp8t()
+        keep_x8 = use_fp8 and bwd_fp8.uvqk_wgrad_fp8t(fp8_backward)
         ctx.save_for_backward(x, norm_weight, norm_bias, mean, rstd, uvqk_weight, vqk, seq_offsets,
                               *([] if num_targets is None else [num_targets]),
                               *([] if attn_bias is None else [attn_bias]),
@@ -105,7 +110,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
                               *([x8] if keep_x8 else []))
         ctx.cfg = (norm_eps, H, Dq, Dv, max_seq_len, attn_alpha, max_attn_len, contextual_seq_len, qkv_scale,
                    defer_silu, num_targets is not None, attn_bias is not None, u_pre is not None)
-        ctx.x8_scale = sx if keep_x8 else None
+        ctx.x8_scale = sa if keep_x8 else None
+        ctx.fp8_backward = fp8_backward
         u = u.contiguous() if u.stride(1) != 1 else u
         setattr(u, DUVQK_WIDTH_ATTR, uvqk_weight.shape[1])
         return u, attn.view(T, H * Dv)
@@ -151,7 +157,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
             return _ln_fwd(x, None, nw, nb, eps, 0.0, False, False, False, False, "none", 0, False, 1.0)[0]
 
         fp8_grads = bwd_fp8.uvqk_projection_backward(duvqk, None, ctx.x8_scale, W, normed_x_fp8_t=x8,
-                                                     recompute_normed_x=recompute_normed_x)
+                                                     recompute_normed_x=recompute_normed_x,
+                                                     config=ctx.fp8_backward)
         if fp8_grads is not None:
             dxn, d_w, d_b = fp8_grads
         else:
@@ -162,7 +169,7 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         d_w, d_b = d_w.to(W.dtype), d_b.to(W.dtype)
         dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False)
         return (dx, dnw.to(nw.dtype), dnb.to(nb.dtype), None, None, None, None, d_w, d_b, None, None, None, None,
-                None, None, None, None, None, None if dbias is None else dbias.to(attn_bias.dtype))
+                None, None, None, None, None, None if dbias is None else dbias.to(attn_bias.dtype), None)
 
 
 def triton_hstu_preprocess_and_attention(
@@ -192,10 +199,15 @@ def triton_hstu_preprocess_and_attention(
     return_residual_proxy: bool = False,
     *,
     attn_bias: Optional[torch.Tensor] = None,
+    fp8_backward: Optional[bwd_fp8.Fp8BackwardConfig] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """(u, attn [T, H*hidden_dim]); signature of
     ``triton_hstu_preprocess_and_attention`` (:3328-3393).  ``attn_bias`` is
-    this build's relative-position bias extension (default off)."""
+    this build's relative-position bias extension (default off);
+    ``fp8_backward`` the FP8 backward arm's settings (default: the process
+    default, ``bwd_fp8.default_config()``).  ``fp8_input_scale`` /
+    ``fp8_qkv_scale``: one-element device scales, or the reference's
+    [2 + steps] scale state buffers, calibrated by the bf16 calls until frozen."""
     if return_residual_proxy:
         raise NotImplementedError("the residual-proxy dropout fold is not served")
     if fp8_input_scale is None and fp8_qkv_scale is not None:
@@ -203,7 +215,7 @@ def triton_hstu_preprocess_and_attention(
     return _HSTUPreprocessAndAttentionFunction.apply(
         x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias, max_seq_len,
         seq_offsets, attn_alpha, num_targets, max_attn_len, contextual_seq_len, fp8_input_scale, fp8_qkv_scale,
-        defer_silu, attn_bias)
+        defer_silu, attn_bias, fp8_backward)
 
 
 def hstu_compute_uqvk(x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias,
@@ -262,13 +274,23 @@ def hstu_layer(
     attn_bias: Optional[torch.Tensor] = None,
     norm_eps: float = 1e-6,
     seed: Optional[int] = None,
+    fp8_backward: Optional[bwd_fp8.Fp8BackwardConfig] = None,
+    dropout_mask16: Optional[bool] = None,
 ) -> torch.Tensor:
     """One STU layer as ``modules/stu.py:567-651`` composes it with the
     production flags (defer_silu; output block with concat_u, concat_x and
     SiLU on u): preprocess + attention, then LN(attn) * U * dropout -> output
     projection + residual.  ``params``: input_norm_weight/bias [E],
     uvqk_weight [E, 2048], uvqk_bias [2048], output_norm_weight/bias
-    [H*hidden], output_weight [3*H*hidden, E]."""
+    [H*hidden], output_weight [3*H*hidden, E].
+
+    FP8 scales (``fp8_input_scale``, ``fp8_qkv_scale``, ``fp8_output_scale``)
+    are one-element device tensors or the reference's per-layer scale state
+    buffers ([2 + steps] fp32, ``fp8.fp8_scale_state_size()``), which the
+    first calls calibrate (bf16 math) until frozen; no scale is read on the
+    host.  ``fp8_backward`` sets the FP8 backward arm (default: the process
+    default); ``dropout_mask16`` the dropout mask scheme (default: the
+    process default, ``hstu_linear.set_mask16``)."""
     from .hstu_linear import triton_hstu_compute_output
 
     alpha = attn_alpha if attn_alpha is not None else 1.0 / attn_dim ** 0.5
@@ -276,11 +298,12 @@ def hstu_layer(
         x, params["input_norm_weight"], params["input_norm_bias"], norm_eps, num_heads, attn_dim, hidden_dim,
         params["uvqk_weight"], params["uvqk_bias"], max_seq_len, seq_offsets, alpha, None,
         recompute_uvqk_in_backward=True, recompute_normed_x_in_backward=True,
-        fp8_input_scale=fp8_input_scale, fp8_qkv_scale=fp8_qkv_scale, defer_silu=True, attn_bias=attn_bias)
+        fp8_input_scale=fp8_input_scale, fp8_qkv_scale=fp8_qkv_scale, defer_silu=True, attn_bias=attn_bias,
+        fp8_backward=fp8_backward)
     return triton_hstu_compute_output(
         attn, u, x, params["output_norm_weight"], params["output_norm_bias"], params["output_weight"], norm_eps,
         dropout_ratio, training, True, True, True, "silu", seed=seed, recompute_y_in_backward=True,
-        fp8_output_scale=fp8_output_scale)
+        fp8_output_scale=fp8_output_scale, fp8_backward=fp8_backward, dropout_mask16=dropout_mask16)
 
 
 __all__ = ["triton_hstu_preprocess_and_attention", "hstu_preprocess_and_attention", "hstu_compute_uqvk",

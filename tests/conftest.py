@@ -30,3 +30,21 @@ def hip_lib():
 
     lib = hstu_amd.load_library()
     return lib
+
+
+@pytest.fixture
+def fp8_bwd(monkeypatch):
+    """Set the FP8 backward arm's process default for one test, restored after:
+    fp8_bwd(enabled=True, uvqk=True, ...) takes Fp8BackwardConfig fields."""
+    import hstu_amd.bwd_fp8 as B
+
+    saved = B._default
+
+    def use(**fields):
+        cfg = B.Fp8BackwardConfig(**fields)
+        B.set_default_config(cfg)
+        return cfg
+
+    yield use
+    B.set_default_config(saved)
+    B.reset_sites()

@@ -359,7 +359,9 @@ def test_fp8_bwd_full_fp8_block_quantized_dout(hip_lib, monkeypatch):
     dout_q = DO.dequantize_do_e4m3_blk(y, e8)
 
     def bwd(dO, full):
-        monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL", "1" if full else "0")
+        import hstu_amd.hstu_do_fp8 as F
+
+        monkeypatch.setattr(F, "_full", bool(full))
         g = [torch.empty(q.shape, dtype=torch.bfloat16, device=DEV) for _ in range(3)]
         ops.triton_hstu_attention_bwd(dO.to(DEV), dev[0], dev[1], dev[2], *g, offs.to(DEV), None, N, alpha, 0, 0,
                                       None, False, 0, dev[3], dev[4], dev[5])
@@ -376,3 +378,36 @@ def test_fp8_bwd_full_fp8_block_quantized_dout(hip_lib, monkeypatch):
     for name, got, r in (("dq", full[0], rq), ("dk", full[1], rk), ("dv", full[2], rv)):
         err = orc.rel_l2(r, got.float())
         assert err <= 3e-2, f"{name}: rel L2 {err:.3e}"
+
+
+def test_reference_named_ops_on_gpu(hip_lib):
+    """torch.ops.generative_recommenders.triton_hstu_attention_{fwd,bwd} with
+    the reference's argument lists: bf16 results equal this build's own op
+    bitwise; e4m3 inputs at per-tensor float scales match the oracle."""
+    import hstu_amd
+
+    ns = torch.ops.generative_recommenders
+    H, D = 2, 128
+    lengths = [300, 77, 129]
+    N = max(lengths)
+    q, k, v, offs = _case(lengths, H, D)
+    qd, kd, vd, od = (t.to(DEV) for t in (q, k, v, offs))
+    out = ns.triton_hstu_attention_fwd(N, 0.1, qd, kd, vd, od, None, 0, 0, None, False, 0)
+    own = hstu_amd.triton_hstu_attention_fwd(N, 0.1, qd, kd, vd, od, None, 0, 0, None, False, 0)
+    assert out.dtype == torch.bfloat16 and torch.equal(out, own)
+    dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    g1 = [torch.empty_like(qd) for _ in range(3)]
+    g2 = [torch.empty_like(qd) for _ in range(3)]
+    ns.triton_hstu_attention_bwd(dout, qd, kd, vd, *g1, od, None, N, 0.1, 0, 0, None, False, 0)
+    hstu_amd.triton_hstu_attention_bwd(dout, qd, kd, vd, *g2, od, None, N, 0.1, 0, 0, None, False, 0)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+    # e4m3 with per-tensor float scales (the reference schema's q_scale/k_scale/v_scale)
+    qf, kf, vf, _ = _case(lengths, H, D, std=1.0, dtype=torch.float32)
+    s = 4.0 / 448
+    q8, k8, v8 = ((t / s).clamp(-448, 448).to(torch.float8_e4m3fn) for t in (qf, kf, vf))
+    o8 = ns.triton_hstu_attention_fwd(N, 0.1, q8.to(DEV), k8.to(DEV), v8.to(DEV), od, None, 0, 0, None, False, 0,
+                                      s, s, s)
+    ref = orc.hstu_mha_dense(N, 0.1, q8.double() * s, k8.double() * s, v8.double() * s, offs, dtype=torch.float64)
+    assert o8.dtype == torch.bfloat16
+    assert orc.rel_l2(ref, o8.float().cpu()) <= 1e-2

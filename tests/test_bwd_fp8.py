@@ -48,33 +48,50 @@ def test_controller_warmup_publish_refresh(monkeypatch):
     """The delayed-scale policy on CPU tensors (the cast is the oracle's)."""
     import hstu_amd.bwd_fp8 as B
 
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "2")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "3")
+    cfg = B.Fp8BackwardConfig(enabled=True, warmup_calls=2, refresh_calls=3)
     monkeypatch.setattr(B, "quantize_row_major",
                         lambda v, inv, dtype=None, limit=None: O.cast_amax(v, float(inv.reshape(-1)[0]),
                                                                             dtype or E5M2, limit or 57344.0))
     B.reset_sites()
     g = [torch.full((4, 128), float(a)) for a in (2.0, 3.0, 1.0, 9.0, 4.0, 1.0)]
-    assert B.quantize_gradient("site", g[0]) is None
-    assert B.quantize_gradient("site", g[1]) is None          # warm-up ends: publish max(2, 3)
-    st = B._sites["site"]
+    assert B.quantize_gradient("site", g[0], config=cfg) is None
+    assert B.quantize_gradient("site", g[1], config=cfg) is None      # warm-up ends: publish max(2, 3)
+    st = B.find_site("site")
     s0 = O.published_scale(3.0, 8.0, 57344.0)
-    assert st.published and float(st.scale) == pytest.approx(s0, rel=1e-6)
-    q, dec = B.quantize_gradient("site", g[2], snapshot_decode_scale=True)   # call 3: refresh
+    assert st.live and float(st.scale) == pytest.approx(s0, rel=1e-6)
+    q, dec = B.quantize_gradient("site", g[2], snapshot_decode_scale=True, config=cfg)   # call 3: refresh
     assert float(dec) == pytest.approx(s0, rel=1e-6)         # the scale it was cast with
     assert float(q.float()[0, 0]) * s0 == pytest.approx(1.0, rel=0.13)
     s1 = O.published_scale(1.0, 8.0, 57344.0)                 # window of call 3 only
     assert float(st.scale) == pytest.approx(s1, rel=1e-6)
-    q4, dec4 = B.quantize_gradient("site", g[3])              # 9.0 > s1 * 57344 = 8: clipped
-    assert int(st.clipped_windows) == 1
+    q4, dec4 = B.quantize_gradient("site", g[3], config=cfg)  # 9.0 > s1 * 57344 = 8: overflowed
+    assert int(st.overflow_windows) == 1
     assert float(dec4) == pytest.approx(s1, rel=1e-6)
-    _, dec5 = B.quantize_gradient("site", g[4])
-    q6, dec6 = B.quantize_gradient("site", g[5])              # call 6: refresh, default decode = new scale
+    _, dec5 = B.quantize_gradient("site", g[4], config=cfg)
+    q6, dec6 = B.quantize_gradient("site", g[5], config=cfg)  # call 6: refresh, default decode = new scale
     assert float(dec6) == pytest.approx(O.published_scale(9.0, 8.0, 57344.0), rel=1e-6)
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "0")
-    assert B.quantize_gradient("site", g[0]) is None
+    assert B.quantize_gradient("site", g[0], config=B.Fp8BackwardConfig(enabled=False)) is None
     B.reset_sites()
+
+
+def test_config_from_env_is_read_once(monkeypatch):
+    """The reference's switch names set the process default when it is first
+    used; later changes to the environment do not reach running calls."""
+    import hstu_amd.bwd_fp8 as B
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "7")
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e4m3")
+    B.set_default_config(None)
+    c = B.default_config()
+    assert c.enabled and c.warmup_calls == 7 and c.grad_dtype == E4M3 and c.grad_limit == 448.0
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "0")
+    assert B.enabled()                                          # unchanged until re-read
+    B.set_default_config(None)
+    assert not B.enabled()
+    with pytest.raises(ValueError):
+        B.Fp8BackwardConfig(grad_format="e3m4")
+    B.set_default_config(None)
 
 
 def test_site_names_per_layer():
@@ -125,10 +142,10 @@ def test_e5m2_gemm_against_fp64(hip_lib):
 
 
 @pytest.mark.gpu
-def test_output_projection_dgrad_warmup_then_fp8(hip_lib, monkeypatch):
+def test_output_projection_dgrad_warmup_then_fp8(hip_lib, fp8_bwd):
     import hstu_amd.bwd_fp8 as B
 
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    fp8_bwd(enabled=True)
     B.reset_sites()
     g = torch.Generator(device="cuda").manual_seed(7)
     w = (torch.randn(1536, 512, device="cuda", generator=g) / 40).requires_grad_(True)
@@ -147,7 +164,7 @@ def test_output_projection_dgrad_warmup_then_fp8(hip_lib, monkeypatch):
 
 
 @pytest.mark.gpu
-def test_output_block_backward_with_fp8_dgrad(hip_lib, monkeypatch):
+def test_output_block_backward_with_fp8_dgrad(hip_lib, fp8_bwd):
     import hstu_amd
     import hstu_amd.bwd_fp8 as B
 
@@ -169,9 +186,9 @@ def test_output_block_backward_with_fp8_dgrad(hip_lib, monkeypatch):
         out.backward(dout)
         return a.grad.float(), uu.grad.float()
 
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "0")
+    fp8_bwd(enabled=False)
     ref = grads()
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
+    fp8_bwd(enabled=True)
     B.reset_sites()
     for _ in range(4):
         warm = grads()                                        # warm-up: bf16, identical
@@ -221,19 +238,15 @@ def test_uvqk_controller_declines_and_snapshot(monkeypatch):
     W = torch.randn(128, 256).to(torch.bfloat16).requires_grad_(True)
     dz = torch.randn(64, 256).to(torch.bfloat16)
     xn = torch.randn(64, 128).to(torch.bfloat16)
-    monkeypatch.delenv("DLRM_HSTU_FP8_BWD_UVQK", raising=False)
-    assert B.uvqk_projection_backward(dz, xn, None, W) is None                 # off by default
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e4m3")
-    assert B.uvqk_projection_backward(dz, xn, None, W) is None                 # needs e5m2
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e5m2")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "2")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "3")
+    assert B.uvqk_projection_backward(dz, xn, None, W, config=B.Fp8BackwardConfig()) is None   # off by default
+    assert B.uvqk_projection_backward(dz, xn, None, W, config=B.Fp8BackwardConfig(
+        uvqk=True, grad_format="e4m3")) is None                                               # needs e5m2
+    cfg = B.Fp8BackwardConfig(uvqk=True, warmup_calls=2, refresh_calls=3)
     B.reset_sites()
-    assert B.uvqk_projection_backward(dz, xn, None, W.detach()) is None        # not the leaf parameter
-    assert B.uvqk_projection_backward(dz[:, :200].contiguous(), xn, None, W[:, :200]) is None  # N % 256
-    assert B.uvqk_projection_backward(dz, None, None, W) is None               # no normed_x at all
-    assert not B._sites                                                        # declines touch no state
+    assert B.uvqk_projection_backward(dz, xn, None, W.detach(), config=cfg) is None    # not the leaf parameter
+    assert B.uvqk_projection_backward(dz[:, :200].contiguous(), xn, None, W[:, :200], config=cfg) is None  # N % 256
+    assert B.uvqk_projection_backward(dz, None, None, W, config=cfg) is None           # no normed_x at all
+    assert not B._registry.sites                                               # declines touch no state
     seen = []
 
     def cast(v, inv, pad_to=1, out=None, dtype=None):
@@ -252,9 +265,9 @@ def test_uvqk_controller_declines_and_snapshot(monkeypatch):
     outs = []
     for a in amaxes:
         d = dz.float() / dz.float().abs().max() * a
-        outs.append(B.uvqk_projection_backward(d.to(torch.bfloat16), None, None, W, recompute_normed_x=lambda: xn))
+        outs.append(B.uvqk_projection_backward(d.to(torch.bfloat16), None, None, W, recompute_normed_x=lambda: xn,
+                                               config=cfg))
     assert outs[0] is None and outs[1] is None                                  # warm-up
-    st = B._sites["uvqk_projection.L0"]
     s0 = O.published_scale(3.0, 8.0, 57344.0)
     assert seen[0] == pytest.approx(s0, rel=1e-6)                              # call 3 decodes with the cast's scale
     assert seen[1] == pytest.approx(O.published_scale(1.0, 8.0, 57344.0), rel=1e-6)  # refreshed after call 3
@@ -291,10 +304,10 @@ def test_cast_amax_colsum_bit_exact(hip_lib, M, N, pad, ld, dst):
 
 
 @pytest.mark.gpu
-def test_uvqk_projection_backward_warmup_then_fp8(hip_lib, monkeypatch):
+def test_uvqk_projection_backward_warmup_then_fp8(hip_lib, fp8_bwd):
     import hstu_amd.bwd_fp8 as B
 
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
+    fp8_bwd(uvqk=True)
     B.reset_sites()
     g = torch.Generator(device="cuda").manual_seed(9)
     W = (torch.randn(512, 2048, device="cuda", generator=g) / 25).to(torch.bfloat16).requires_grad_(True)
@@ -304,7 +317,7 @@ def test_uvqk_projection_backward_warmup_then_fp8(hip_lib, monkeypatch):
         xn = torch.randn(1000, 512, device="cuda", generator=g).to(torch.bfloat16)
         res.append((dz, xn, B.uvqk_projection_backward(dz, xn, None, W)))
     assert all(r is None for _, _, r in res[:4])
-    st = B._sites["uvqk_projection.L0"]
+    st = B.find_site("uvqk_projection", layer=0)
     for dz, xn, r in res[4:]:
         d_x, d_w, d_b = r
         assert d_x.dtype == torch.bfloat16 and d_x.shape == (1000, 512)

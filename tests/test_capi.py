@@ -118,7 +118,7 @@ def test_ln_mul_entry_points_reject_before_launch():
     def f(**kw):
         a = dict(x=X, ldx=512, u=X, ldu=512, w=W, b=W, eps=1e-6, rows=64, D=512, act=1, silu_u=1, cu=1, cx=1,
                  training=0, ratio=0.0, seed=0, mask16=0, mask=None, ldm=0, y=X, ldy=1536, odt=0, inv=1.0,
-                 mean=W, rstd=W, stream=None)
+                 out_scale=None, mean=W, rstd=W, stream=None)
         a.update(kw)
         return fwd(*a.values())
 

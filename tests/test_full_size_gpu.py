@@ -20,6 +20,8 @@ import numpy as np
 import pytest
 import torch
 
+import hstu_amd.hstu_linear as L_mod
+
 from oracle import hstu_oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -159,7 +161,7 @@ def test_output_block_config3_tokens(hip_lib, monkeypatch):
     from oracle import hstu_ln_oracle as L
 
     ops = _ops()
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1")
+    monkeypatch.setattr(L_mod, "_mask16", True)
     T, D, p, eps, seed, inv = 162251, 512, 0.3, 1e-6, 2 ** 61 + 12345, 1.0 / 0.05
     assert int(np.sum(orc.lengths_for_config(3))) == T
     g = torch.Generator(device=DEV).manual_seed(0)

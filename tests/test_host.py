@@ -86,3 +86,97 @@ def test_bench_rejects_multi_gpu():
     r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stdout
+
+
+def test_reference_named_ops_registered_with_reference_schemas():
+    """generative_recommenders::triton_hstu_attention_{fwd,bwd,delta_bwd}
+    exist with the reference's argument names, defaults and mutation sets
+    (ops/triton/triton_hstu_attention.py:3166-3185, 3298-3319, 3413-3428)."""
+    import hstu_amd  # noqa: F401  (registers the ops)
+
+    ns = torch.ops.generative_recommenders
+    fwd = ns.triton_hstu_attention_fwd.default._schema
+    assert [a.name for a in fwd.arguments] == [
+        "N", "alpha", "q", "k", "v", "seq_offsets", "num_targets", "max_attn_len", "contextual_seq_len",
+        "sort_by_length_indices", "enable_tma", "num_softmax_heads", "q_scale", "k_scale", "v_scale"]
+    assert [a.default_value for a in fwd.arguments[-3:]] == [1.0, 1.0, 1.0]
+    bwd = ns.triton_hstu_attention_bwd.default._schema
+    assert [a.name for a in bwd.arguments] == [
+        "dout", "q", "k", "v", "dq", "dk", "dv", "seq_offsets", "num_targets", "N", "alpha", "max_attn_len",
+        "contextual_seq_len", "sort_by_length_indices", "enable_tma", "num_softmax_heads"]
+    assert [a.name for a in bwd.arguments if a.alias_info is not None and a.alias_info.is_write] == ["dq", "dk", "dv"]
+    dlt = ns.triton_hstu_attention_delta_bwd.default._schema
+    assert [a.name for a in dlt.arguments] == ["dout", "q", "k", "v", "dq", "dk", "dv", "seq_offsets", "N", "alpha",
+                                               "k_scale", "v_scale"]
+    assert [a.name for a in dlt.arguments if a.alias_info is not None and a.alias_info.is_write] == ["dq", "dk", "dv"]
+
+
+def test_reference_named_fwd_fake_output_dtype():
+    """The fake forward allocates [T, H, Dv] in bf16 for e4m3 inputs, else in
+    v's dtype (triton_hstu_attention.py:3508-3524)."""
+    import hstu_amd  # noqa: F401
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    op = torch.ops.generative_recommenders.triton_hstu_attention_fwd
+    with FakeTensorMode():
+        off = torch.empty(3, dtype=torch.int64)
+        q8 = torch.empty(10, 4, 128, dtype=torch.float8_e4m3fn)
+        o8 = op(64, 0.1, q8, q8, q8, off, None, 0, 0, None, False, 0)
+        q16 = torch.empty(10, 2, 64, dtype=torch.bfloat16)
+        v16 = torch.empty(10, 2, 32, dtype=torch.bfloat16)
+        o16 = op(64, 0.1, q16, q16, v16, off, None, 0, 0, None, False, 0)
+    assert o8.shape == (10, 4, 128) and o8.dtype == torch.bfloat16
+    assert o16.shape == (10, 2, 32) and o16.dtype == torch.bfloat16
+
+
+def test_backward_rejects_mixed_scale_layouts():
+    """One scale addressing serves q, k and v in the C ABI, so mixing a scalar
+    and per-(token, head) scales is refused before any launch."""
+    from hstu_amd import hstu_attention as A
+
+    T, H, D = 8, 2, 128
+    q = torch.zeros(T, H, D, dtype=torch.float8_e4m3fn)
+    g = [torch.zeros(T, H, D, dtype=torch.bfloat16) for _ in range(3)]
+    offs = torch.tensor([0, 8])
+    with pytest.raises(ValueError, match="one layout"):
+        A._launch_bwd(g[0], q, q, q, *g, offs, None, 16, 0.1, 0, 0, torch.ones(T, H), 1.0, torch.ones(T, H),
+                      None, None)
+
+
+def test_calibrate_scale_buffer_freeze_rule():
+    """The scale state [scale, completed, history]: zero while calibrating, then
+    max(history) * 1.5 / 448 and frozen (triton_fp8.py:694-749); an all-zero
+    value is not a step; a one-element buffer is set from each call."""
+    from hstu_amd import fp8 as F
+
+    steps = F.CALIBRATION_STEPS
+    buf = torch.zeros(F.fp8_scale_state_size())
+    amaxes = [2.0, 0.0, 5.0, 3.0, 1.0, 7.0][: steps + 2]
+    got = []
+    for a in amaxes:
+        got.append(F.calibrate_scale_buffer(buf, torch.full((4, 4), -a)))
+    nonzero = [a for a in amaxes if a > 0][:steps]
+    want = max(nonzero) * 1.5 / 448
+    k = [i for i, a in enumerate(amaxes) if a > 0][steps - 1]
+    assert all(v == 0.0 for v in got[:k])
+    assert got[k] == pytest.approx(want, rel=1e-6) and all(v == pytest.approx(want, rel=1e-6) for v in got[k:])
+    assert float(buf[1]) == steps and F.scale_ready(buf)
+    assert float(F.fp8_scale_tensor(buf).reshape(())) == pytest.approx(want, rel=1e-6)
+    one = torch.zeros(1)
+    assert F.calibrate_scale_buffer(one, torch.full((2,), 3.0), margin=1.0) == pytest.approx(3.0 / 448, rel=1e-6)
+    assert F.scale_ready(one) and not F.scale_ready(torch.zeros(F.fp8_scale_state_size()))
+    assert F.calibrated_scale(torch.tensor([-4.0, 2.0])).item() == pytest.approx(4.0 * 1.5 / 448, rel=1e-6)
+
+
+def test_scale_state_known_without_device_reads():
+    """A state this module froze is ready without reading it again; a write
+    from elsewhere (a checkpoint load) is noticed through the version counter."""
+    from hstu_amd import fp8 as F
+
+    buf = torch.zeros(F.fp8_scale_state_size())
+    for _ in range(F.CALIBRATION_STEPS):
+        F.calibrate_scale_buffer(buf, torch.ones(3))
+    v = buf._version
+    assert F.scale_ready(buf) and buf._version == v
+    buf.zero_()                                   # reset elsewhere
+    assert not F.scale_ready(buf)

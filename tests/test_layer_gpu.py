@@ -13,6 +13,8 @@ import numpy as np
 import pytest
 import torch
 
+import hstu_amd.hstu_linear as L_mod
+
 from oracle import hstu_layer_oracle as LO
 from oracle import hstu_ln_oracle as L
 from oracle import hstu_oracle as orc
@@ -41,7 +43,7 @@ def _calibrate(x, params):
 def test_hstu_layer_fwd_bwd(hip_lib, monkeypatch, fp8, with_bias, dropout):
     import hstu_amd
 
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1")
+    monkeypatch.setattr(L_mod, "_mask16", True)
     lengths = np.array([300, 77, 512, 129])
     T, N, E, seed = int(lengths.sum()), 512, 512, 77
     g = torch.Generator().manual_seed(3)
@@ -88,12 +90,9 @@ def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch, uvqk_wgrad):
     import hstu_amd
     import hstu_amd.bwd_fp8 as B
 
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD", "1")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK", "1")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "1")
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_UVQK_WGRAD", uvqk_wgrad)
-    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_OUT_WGRAD", "1" if uvqk_wgrad == "fp8t" else "0")
+    monkeypatch.setattr(L_mod, "_mask16", True)
+    cfg = B.Fp8BackwardConfig(enabled=True, uvqk=True, warmup_calls=1, uvqk_wgrad_fp8t=uvqk_wgrad == "fp8t",
+                              out_wgrad_fp8=uvqk_wgrad == "fp8t")
     B.reset_sites()
     lengths = np.array([300, 77, 512, 129])
     T, N, E = int(lengths.sum()), 512, 512
@@ -111,12 +110,13 @@ def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch, uvqk_wgrad):
             t.grad = None
         xd = x.to(DEV).requires_grad_(True)
         out = hstu_amd.hstu_layer(xd, offs, N, pd, dropout_ratio=0.0, training=True, fp8_input_scale=sc(s_x),
-                                  fp8_qkv_scale=sc(s_qkv), fp8_output_scale=sc(s_out))
+                                  fp8_qkv_scale=sc(s_qkv), fp8_output_scale=sc(s_out), fp8_backward=cfg)
         out.backward(dy.to(DEV))
-    assert B._sites["uvqk_projection.L0"].calls == 2 and B._sites["output_projection.L0"].calls == 2
+    sites = {s: B.find_site(s, layer=0) for s in ("output_projection", "uvqk_projection")}
+    assert all(st.calls == 2 for st in sites.values())
     xr = x.double().requires_grad_(True)
     pr = {k: v.double().requires_grad_(True) for k, v in params.items()}
-    scales = {s: float(B._sites[f"{s}.L0"].scale) for s in ("output_projection", "uvqk_projection")}
+    scales = {s: float(st.scale) for s, st in sites.items()}
     ref = LO.hstu_layer_ref(xr, pr, lengths, N, s_x=s_x, s_qkv=s_qkv, s_out=s_out, dropout_ratio=0.0, quantize=True,
                             grad_scales=scales, fp8_wgrad=("uvqk_projection", "output_projection") if uvqk_wgrad == "fp8t" else ())
     ref.backward(dy.double())
@@ -126,3 +126,61 @@ def test_hstu_layer_fp8_backward_arms(hip_lib, monkeypatch, uvqk_wgrad):
         e = _rel_l2(r, got.float().cpu())
         assert e <= 3e-2, f"{name} rel L2 {e:.3e}"
     B.reset_sites()
+
+
+def test_hstu_layer_calibrated_scale_states_no_host_sync(hip_lib, monkeypatch):
+    """The layer with the reference's per-layer scale state buffers
+    ([2 + steps] fp32, all zero): the first CALIBRATION_STEPS calls run bf16
+    and fill the amax histories; then the scales freeze at max(history) *
+    1.5 / 448 (their closed form, from the recorded histories), the layer
+    runs FP8, and a whole fwd + bwd step makes no host synchronisation
+    (torch.cuda.set_sync_debug_mode("error")).  The FP8 step matches the
+    float64 layer oracle at the frozen scales (output 1.5e-2, gradients 3e-2)."""
+    import hstu_amd
+    from hstu_amd import fp8 as F
+
+    monkeypatch.setattr(L_mod, "_mask16", True)
+    lengths = np.array([300, 77, 512, 129])
+    T, N, E = int(lengths.sum()), 512, 512
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    params = LO.make_layer_params(E, seed=6)
+    dy = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    offs = orc.offsets_from_lengths(lengths).to(DEV)
+    pd = {k: v.to(DEV).requires_grad_(True) for k, v in params.items()}
+    states = {n: torch.zeros(F.fp8_scale_state_size(), device=DEV) for n in ("in", "qkv", "out")}
+    x_dev, dy_dev = x.to(DEV), dy.to(DEV)   # inputs resident on the device before the checked step
+
+    def step():
+        for t in pd.values():
+            t.grad = None
+        xd = x_dev.detach().requires_grad_(True)
+        out = hstu_amd.hstu_layer(xd, offs, N, pd, dropout_ratio=0.0, training=True,
+                                  fp8_input_scale=states["in"], fp8_qkv_scale=states["qkv"],
+                                  fp8_output_scale=states["out"], fp8_backward=hstu_amd.bwd_fp8.Fp8BackwardConfig())
+        out.backward(dy_dev)
+        return xd, out
+
+    for _ in range(F.CALIBRATION_STEPS):
+        assert not F.scale_ready(states["in"])
+        step()
+    for n, st in states.items():
+        hist = st[2:].cpu()
+        assert F.scale_ready(st) and float(st[1]) == F.CALIBRATION_STEPS and bool((hist > 0).all()), n
+        assert float(st[0]) == pytest.approx(float(hist.max()) * 1.5 / 448, rel=1e-6), n
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        xd, out = step()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    s_x, s_qkv, s_out = (float(states[n][0]) for n in ("in", "qkv", "out"))
+    xr = x.double().requires_grad_(True)
+    pr = {k: v.double().requires_grad_(True) for k, v in params.items()}
+    ref = LO.hstu_layer_ref(xr, pr, lengths, N, s_x=s_x, s_qkv=s_qkv, s_out=s_out, dropout_ratio=0.0, quantize=True)
+    ref.backward(dy.double())
+    e = _rel_l2(ref.detach(), out.detach().cpu())
+    assert e <= 1.5e-2, f"out rel L2 {e:.3e}"
+    for name, r, got in [("dx", xr.grad, xd.grad)] + [(f"d{k}", pr[k].grad, pd[k].grad) for k in params]:
+        e = _rel_l2(r, got.float().cpu())
+        assert e <= 3e-2, f"{name} rel L2 {e:.3e}"

@@ -17,6 +17,8 @@ import numpy as np
 import pytest
 import torch
 
+import hstu_amd.hstu_linear as L_mod
+
 from oracle import hstu_ln_oracle as L
 
 pytestmark = pytest.mark.gpu
@@ -66,7 +68,7 @@ def _e4m3_close(got8, ref, inv_scale, what):
                                       (77, 512, 1, 0.5), (64, 256, 3, 1.0), (40, 512, 3, 0.0)])
 def test_dropout_mask_bitexact(hip_lib, mask16, N, D, nm, p, monkeypatch):
     ops = _ops()
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1" if mask16 else "0")
+    monkeypatch.setattr(L_mod, "_mask16", bool(mask16))
     seed = (123456789 << 20) + 987  # both key words non-zero
     got = ops.create_dropout_mask(N, D, nm == 3 or nm == 2, nm == 3, p, seed, torch.device(DEV))
     ref = L.dropout_mask(N, D, nm, p, seed, mask16)
@@ -93,7 +95,7 @@ def _oracle_fwd(x, u, w, b, eps, p, mask, act, silu_u, cu, cx):
 @pytest.mark.parametrize("act,silu_u,cu,cx,training,mask16,fp8,D", CASES)
 def test_ln_mul_dropout_fwd(hip_lib, monkeypatch, act, silu_u, cu, cx, training, mask16, fp8, D):
     ops = _ops()
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1" if mask16 else "0")
+    monkeypatch.setattr(L_mod, "_mask16", bool(mask16))
     N, p, eps, seed, inv = 1003, 0.3, 1e-6, 2 ** 40 + 17, 8.0
     x, u, w, b = _inputs(N, D, seed=1)
     y, mean, rstd, bd, nw, s, mask = ops.triton_layer_norm_mul_dropout_fwd(
@@ -121,7 +123,7 @@ def test_ln_mul_dropout_fwd(hip_lib, monkeypatch, act, silu_u, cu, cx, training,
 @pytest.mark.parametrize("act,silu_u,cu,cx,training,mask16,fp8,D", CASES)
 def test_ln_mul_dropout_bwd(hip_lib, monkeypatch, act, silu_u, cu, cx, training, mask16, fp8, D):
     ops = _ops()
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1" if mask16 else "0")
+    monkeypatch.setattr(L_mod, "_mask16", bool(mask16))
     N, p, eps, seed = 2051, 0.3, 1e-6, 99
     x, u, w, b = _inputs(N, D, seed=2)
     xd, ud, wd, bd_ = (t.to(DEV) for t in (x, u, w, b))
@@ -199,7 +201,7 @@ def test_hstu_compute_output_fwd_bwd(hip_lib, monkeypatch, fp8):
     from oracle import hstu_oracle as orc
 
     ops = _ops()
-    monkeypatch.setenv("DLRM_HSTU_FP8_MASK16", "1")
+    monkeypatch.setattr(L_mod, "_mask16", True)
     N, D, Dout, p, eps, seed, sc = 1500, 512, 512, 0.3, 1e-6, 4242, 0.05
     attn, u, nw, nb = _inputs(N, D, seed=9)
     g = torch.Generator().manual_seed(10)
