@@ -40,6 +40,7 @@ extern "C" {
 /* error codes beyond hipError_t (all negative) */
 #define HSTU_E_BAD_ARG (-1)
 #define HSTU_E_UNSUPPORTED (-2)
+#define HSTU_E_SCRATCH_TOO_SMALL (-3) /* the call needs more than an allocation-free entry point's scratch */
 
 /* Library version / self-description; host pointer to a static string. */
 const char* hstu_version(void);
@@ -75,6 +76,31 @@ int hstu_attn_fwd(int dtype,
  * take no workspace (ops/flydsl/hstu_flydsl_mha.py:2036-2046).
  */
 int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len);
+
+/*
+ * hstu_attn_fwd without a workspace, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  The same kernels and
+ * results as hstu_attn_fwd; the block schedule goes to a static device array
+ * of HSTU_ATTN_FWD_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends.  A call needs hstu_attn_fwd_workspace_bytes(...) of it, about
+ * 8 * B * (H + 1) bytes (B <= 6 500 sequences at H = 4); a larger call
+ * returns HSTU_E_SCRATCH_TOO_SMALL before any launch.  Calls no hipMalloc / hipFree.  All calls on one GPU share its
+ * array: calls that overlap on one GPU (concurrent streams) race, so
+ * serialise them.
+ */
+#define HSTU_ATTN_FWD_NOALLOC_SCRATCH_BYTES (256 * 1024)
+int hstu_attn_fwd_noalloc(int dtype,
+                          const void* q, const void* k, const void* v,
+                          int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                          const float* q_scale, const float* k_scale, const float* v_scale,
+                          int64_t scale_row_stride, int64_t scale_head_stride,
+                          const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                          float alpha,
+                          const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
+                          const float* attn_bias, int bias_R,
+                          void* out, int64_t out_row_stride,
+                          int64_t total_tokens, hipStream_t stream);
 
 /*
  * Backward of hstu_attn_fwd.  Writes dq, dk, dv (bf16, caller-owned, may be

@@ -1831,23 +1831,29 @@ extern "C" const char* hstu_version(void) {
   return "hstu-mi355x 0.1 (gfx950: bf16 16x16x32 / e4m3 16x16x128 MFMA)";
 }
 
-extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void* v, int64_t q_row_stride,
-                             int64_t k_row_stride, int64_t v_row_stride, const float* q_scale,
-                             const float* k_scale, const float* v_scale, int64_t scale_row_stride,
-                             int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
-                             int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len,
-                             int contextual_seq_len, const float* attn_bias, int bias_R, void* out,
-                             int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
-                             int64_t total_tokens, hipStream_t stream) {
+namespace {
+// Argument checks shared by both forward entry points (0 = launchable).
+int fwd_check(int dtype, const void* q, const void* k, const void* v, int64_t q_row_stride, int64_t k_row_stride,
+              int64_t v_row_stride, const float* q_scale, const float* k_scale, const float* v_scale, int B, int H,
+              int D, int max_seq_len, const float* attn_bias, int bias_R, int64_t total_tokens) {
   if (!check_common(dtype, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
-                    v_scale, bias_R, attn_bias))
+                    v_scale, bias_R, attn_bias) ||
+      total_tokens < 0)
     return HSTU_E_BAD_ARG;
   if (!(D == 128 || (D == 64 && dtype == HSTU_DTYPE_BF16))) return HSTU_E_UNSUPPORTED;
   if (!row_alignment_ok(dtype, q_row_stride, q) || !row_alignment_ok(dtype, k_row_stride, k) ||
       !row_alignment_ok(dtype, v_row_stride, v))
     return HSTU_E_UNSUPPORTED;
-  if (B == 0) return 0;
-  if (total_tokens < 0 || workspace == nullptr || workspace_bytes < fwd_workspace_bytes(B, H)) return HSTU_E_BAD_ARG;
+  return 0;
+}
+
+// The forward launches; `sched_ws` holds sched_ints(B, H) ints of device memory.
+int fwd_launch(int dtype, const void* q, const void* k, const void* v, int64_t q_row_stride, int64_t k_row_stride,
+               int64_t v_row_stride, const float* q_scale, const float* k_scale, const float* v_scale,
+               int64_t scale_row_stride, int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
+               int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
+               const float* attn_bias, int bias_R, void* out, int64_t out_row_stride, int* sched_ws,
+               hipStream_t stream) {
   AttnParams p{};
   p.q = (const uint8_t*)q;
   p.k = (const uint8_t*)k;
@@ -1876,7 +1882,7 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
   const int grid = sched_grid(B, H, max_seq_len);
   p.bias = attn_bias;
   p.bias_R = bias_R;
-  hipError_t e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)workspace, stream);
+  hipError_t e = schedule(p, seq_offsets, B, H, max_seq_len, sched_ws, stream);
   if (e != hipSuccess) return (int)e;
 #define HSTU_FWD(DD, F8, G, BB) launch(hstu_fwd_kernel<DD, F8, G, BB>, FwdCfg<DD, F8>::LDS, grid, p, stream)
 #define HSTU_FWD_B(DD, F8, G) (has_bias ? HSTU_FWD(DD, F8, G, true) : HSTU_FWD(DD, F8, G, false))
@@ -1894,6 +1900,84 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
   hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
                      p.out, p.o_rs, (uint16_t*)nullptr, (int64_t)0, (uint16_t*)nullptr, (int64_t)0);
   return (int)hipGetLastError();
+}
+}  // namespace
+
+extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void* v, int64_t q_row_stride,
+                             int64_t k_row_stride, int64_t v_row_stride, const float* q_scale,
+                             const float* k_scale, const float* v_scale, int64_t scale_row_stride,
+                             int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
+                             int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len,
+                             int contextual_seq_len, const float* attn_bias, int bias_R, void* out,
+                             int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                             int64_t total_tokens, hipStream_t stream) {
+  const int c = fwd_check(dtype, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale, B, H,
+                          D, max_seq_len, attn_bias, bias_R, total_tokens);
+  if (c != 0) return c;
+  if (B == 0) return 0;
+  if (workspace == nullptr || workspace_bytes < fwd_workspace_bytes(B, H)) return HSTU_E_BAD_ARG;
+  return fwd_launch(dtype, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale,
+                    scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, num_targets,
+                    max_attn_len, contextual_seq_len, attn_bias, bias_R, out, out_row_stride, (int*)workspace,
+                    stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward.  The block schedule goes to `scratch`, a
+// file-scope device array of HSTU_ATTN_FWD_NOALLOC_SCRATCH_BYTES that every
+// GPU the library runs on holds until the process ends.  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in):
+// the device address comes from hipGetSymbolAddress, looked up once per
+// device on the first call made with that device current, and kept per
+// device.  Every call on a GPU shares that GPU's array; the schedule kernel
+// writes every entry the attention kernel then reads, so nothing needs
+// clearing, and calls that overlap on one GPU (other streams) race.
+// ---------------------------------------------------------------------------
+static_assert(HSTU_ATTN_FWD_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) uint8_t scratch[HSTU_ATTN_FWD_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on first use).
+hipError_t scratch_address(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* a = nullptr;
+    e = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (a == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_addr[dev] = a;
+  }
+  *addr = g_scratch_addr[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+extern "C" int hstu_attn_fwd_noalloc(int dtype, const void* q, const void* k, const void* v, int64_t q_row_stride,
+                                     int64_t k_row_stride, int64_t v_row_stride, const float* q_scale,
+                                     const float* k_scale, const float* v_scale, int64_t scale_row_stride,
+                                     int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
+                                     int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len,
+                                     int contextual_seq_len, const float* attn_bias, int bias_R, void* out,
+                                     int64_t out_row_stride, int64_t total_tokens, hipStream_t stream) {
+  const int c = fwd_check(dtype, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale, B, H,
+                          D, max_seq_len, attn_bias, bias_R, total_tokens);
+  if (c != 0) return c;
+  if (B == 0) return 0;
+  if (fwd_workspace_bytes(B, H) > HSTU_ATTN_FWD_NOALLOC_SCRATCH_BYTES) return HSTU_E_SCRATCH_TOO_SMALL;
+  void* ws = nullptr;
+  const hipError_t e = scratch_address(&ws);
+  if (e != hipSuccess) return (int)e;
+  return fwd_launch(dtype, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale,
+                    scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, num_targets,
+                    max_attn_len, contextual_seq_len, attn_bias, bias_R, out, out_row_stride, (int*)ws, stream);
 }
 
 namespace {

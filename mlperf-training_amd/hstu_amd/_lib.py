@@ -24,6 +24,7 @@ HSTU_DTYPE_FP32 = 2
 HSTU_DTYPE_FP8_E5M2 = 3
 HSTU_E_BAD_ARG = -1
 HSTU_E_UNSUPPORTED = -2
+HSTU_E_SCRATCH_TOO_SMALL = -3
 
 # Every extern "C" symbol include/hstu_mi355x.h declares.
 EXPORTED_SYMBOLS = (
@@ -53,6 +54,7 @@ EXPORTED_SYMBOLS = (
     "hstu_wgrad_split",
     "hstu_wgrad_workspace_bytes",
     "hstu_wgrad",
+    "hstu_attn_fwd_noalloc",
 )
 
 
@@ -81,6 +83,11 @@ _SIGNATURES = {
          _f32, _vp, _i32, _i32, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp],
     ),
     "hstu_attn_fwd_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i32, _i32]),
+    "hstu_attn_fwd_noalloc": (
+        _i32,
+        [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
+         _f32, _vp, _i32, _i32, _vp, _i32, _vp, _i64, _i64, _vp],
+    ),
     "hstu_attn_bwd": (
         _i32,
         [_i32, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32,
@@ -177,7 +184,8 @@ def fn(name: str):
 
 def check(status: int, what: str) -> None:
     if status != 0:
-        msg = {HSTU_E_BAD_ARG: "bad argument", HSTU_E_UNSUPPORTED: "unsupported shape/layout"}.get(
+        msg = {HSTU_E_BAD_ARG: "bad argument", HSTU_E_UNSUPPORTED: "unsupported shape/layout",
+               HSTU_E_SCRATCH_TOO_SMALL: "needs more than the allocation-free entry point's scratch"}.get(
             status, f"hipError {status}")
         raise HstuKernelError(f"{what} failed: {msg}")
 

@@ -269,3 +269,27 @@ def test_do_dequantizer_rejects_before_launch():
     assert dq(X, W, 10, 4, 100, X, 400, None) == lib.HSTU_E_UNSUPPORTED  # D % 8
     assert dq(X + 4, W, 10, 4, 128, X, 512, None) == lib.HSTU_E_UNSUPPORTED
     assert dq(X, W, 0, 4, 128, X, 512, None) == 0
+
+
+def test_noalloc_forward_rejects_before_launch():
+    """The allocation-free forward refuses a call whose schedule would not
+    fit its static scratch, and bad arguments, before touching a device."""
+    import hstu_amd._lib as lib
+
+    f = lib.fn("hstu_attn_fwd_noalloc")
+    X = 4096  # fake device addresses: none of these calls may launch
+
+    def call(B, H, D=128, dtype=lib.HSTU_DTYPE_BF16, rs=None, T=1000):
+        rs = H * D if rs is None else rs
+        return f(dtype, X, X, X, rs, rs, rs, None, None, None, 0, 0, X, B, H, D, 4096, 0.1, None, 0, 0, None, 0,
+                 X, H * D, T, None)
+
+    limit = 256 * 1024
+    ws = lib.fn("hstu_attn_fwd_workspace_bytes")
+    assert ws(0, 1000, 8192, 4, 128, 4096) > limit and ws(0, 1000, 6000, 4, 128, 4096) <= limit
+    assert call(8192, 4) == lib.HSTU_E_SCRATCH_TOO_SMALL
+    assert call(100, 4, D=96) == lib.HSTU_E_UNSUPPORTED
+    assert call(100, 4, rs=100) == lib.HSTU_E_BAD_ARG                 # row stride < H * D
+    assert call(100, 4, dtype=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_BAD_ARG  # e4m3 without scales
+    assert call(100, 4, T=-1) == lib.HSTU_E_BAD_ARG
+    assert call(0, 4) == 0                                            # empty batch: nothing to do
