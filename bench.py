@@ -8,9 +8,12 @@ max_seq_len N=4096, H=4, D=128; q, k, v ~ N(0,1) quantized to OCP e4m3 with
 per-(token, head) fp32 scales amax/448; learned relative-position bias table
 [H, 2*1024-1] ~ N(0, 0.02) (offsets beyond 1023 clamped); upstream gradient
 N(0,1) bf16.  One step = forward + backward (dK/dV, dQ and the bias gradient)
-over the whole batch, inputs resident in HBM.  value = causal-effective FLOPs
-(14*D*H*P, P = sum L(L+1)/2) per second.  Also reported: the same step without
-the bias (the reference's attention has none) and on bf16 inputs, the output
+over the whole batch, inputs resident in HBM.  The backward is the reference's
+full-FP8 one (DLRM_HSTU_FP8_BWD_FULL: the bf16 dO block-quantized to e4m3 inside
+the step, e4m3 P and dS, five e4m3 products; --bf16-dout for the e4m3-input
+backward on the bf16 dO).  value = causal-effective FLOPs (14*D*H*P, P = sum
+L(L+1)/2) per second.  Also reported: the same step with the bf16-dO backward,
+without the bias (the reference's attention has none) and on bf16 inputs, the output
 block's LN * U * dropout kernels (GB/s against HBM), one whole HSTU layer
 forward + backward in FP8 at config 3's shapes, the
 targets-only delta-q attention, the full-FP8 backward's dO block quantizer and
@@ -76,6 +79,8 @@ def parse():
                     help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
                     help="how the caches are evicted before each timed call (see CacheFlush)")
+    ap.add_argument("--bf16-dout", action="store_true",
+                    help="headline with the e4m3-input backward on the bf16 dO instead of the full-FP8 backward")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the FP8-with-bias line (no no-bias / bf16 sub-results); for profiler runs")
     return ap.parse_args()
@@ -94,8 +99,9 @@ def causal_pairs(lengths) -> int:
 class Workload:
     """Device-resident inputs and the raw C-ABI argument tuples of one step."""
 
-    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True):
+    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True, full_fp8=False):
         self.torch = torch
+        self.full_fp8 = full_fp8 and dtype == "fp8"
         dev = "cuda"
         self.lengths = lengths
         self.H, self.D, self.N = H, D, N
@@ -153,23 +159,42 @@ class Workload:
         self.f_dkdv = lib.fn("hstu_attn_bwd_dkdv")
         self.f_dq = lib.fn("hstu_attn_bwd_dq")
         self.lib = lib
+        if self.full_fp8:
+            # the full-FP8 backward: the dO block quantizer, then e4m3 P / dS and five e4m3 products
+            del self.ws
+            self.dout8 = torch.empty(T, H, D, dtype=torch.float8_e4m3fn, device=dev)
+            self.e8 = torch.empty(T, H, dtype=torch.uint8, device=dev)
+            self.quant_args = (0, self.dout.data_ptr(), H * D, self.offs.data_ptr(), B, H, D, N,
+                               self.dout8.data_ptr(), self.e8.data_ptr(), stream)
+            ws8 = lib.fn("hstu_attn_bwd_fp8_workspace_bytes")(T, B, H, D, N, R)
+            self.ws = torch.empty(max(ws8, 1), dtype=torch.uint8, device=dev)
+            self.bwd_args = (self.dout8.data_ptr(), self.e8.data_ptr(), H * D, self.q.data_ptr(), self.k.data_ptr(),
+                             self.v.data_ptr(), H * D, H * D, H * D, sp(self.sq), sp(self.sk), sp(self.sv), srs,
+                             shs, self.offs.data_ptr(), B, H, D, N, self.alpha, sp(self.bias), R,
+                             self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), H * D, H * D, H * D,
+                             sp(self.dbias), self.ws.data_ptr(), ws8, T, stream)
+            self.f_quant = lib.fn("hstu_quantize_do_e4m3_blk")
+            self.f_dkdv = lib.fn("hstu_attn_bwd_fp8_dkdv")
+            self.f_dq = lib.fn("hstu_attn_bwd_fp8_dq")
 
     def flops(self, part):
         DHP = self.D * self.H * self.P
-        return {"fwd": 4 * DHP, "dkdv": 8 * DHP, "dq": 2 * DHP, "step": 14 * DHP}[part]
+        return {"fwd": 4 * DHP, "dkdv": 8 * DHP, "dq": 2 * DHP, "do_quant": 0, "step": 14 * DHP}[part]
+
+    def parts(self):
+        return ("fwd", "do_quant", "dkdv", "dq") if self.full_fp8 else ("fwd", "dkdv", "dq")
 
     def step(self, ev=None):
+        calls = [(self.f_fwd, self.fwd_args, "fwd")]
+        if self.full_fp8:
+            calls.append((self.f_quant, self.quant_args, "do_quant"))
+        calls += [(self.f_dkdv, self.bwd_args, "dkdv"), (self.f_dq, self.bwd_args, "dq")]
         if ev is not None:
             ev[0].record()
-        self.lib.check(self.f_fwd(*self.fwd_args), "fwd")
-        if ev is not None:
-            ev[1].record()
-        self.lib.check(self.f_dkdv(*self.bwd_args), "dkdv")
-        if ev is not None:
-            ev[2].record()
-        self.lib.check(self.f_dq(*self.bwd_args), "dq")
-        if ev is not None:
-            ev[3].record()
+        for i, (f, a, name) in enumerate(calls):
+            self.lib.check(f(*a), name)
+            if ev is not None:
+                ev[i + 1].record()
 
     def run(self, steps, warmup, flush):
         """Returns (back-to-back wall ms/step, cold-cache step stats, per-kernel medians).
@@ -186,17 +211,14 @@ class Workload:
             self.step()
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+        names = self.parts()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(steps)]
         for i in range(steps):
             flush()
             self.step(evs[i])
         torch.cuda.synchronize()
-        step = np.array([e[0].elapsed_time(e[3]) for e in evs])
-        parts = {
-            "fwd": float(np.median([e[0].elapsed_time(e[1]) for e in evs])),
-            "dkdv": float(np.median([e[1].elapsed_time(e[2]) for e in evs])),
-            "dq": float(np.median([e[2].elapsed_time(e[3]) for e in evs])),
-        }
+        step = np.array([e[0].elapsed_time(e[-1]) for e in evs])
+        parts = {n: float(np.median([e[j].elapsed_time(e[j + 1]) for e in evs])) for j, n in enumerate(names)}
         stats = {"median": float(np.median(step)), "p10": float(np.percentile(step, 10)),
                  "p90": float(np.percentile(step, 90))}
         return wall_ms, stats, parts
@@ -581,16 +603,17 @@ def main():
     if args.only == "wgrad":
         print(json.dumps(wgrad_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
         return
-    w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
+    w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True, full_fp8=not args.bf16_dout)
     wall_ms, st, parts = w8.run(args.steps, args.warmup, flush)
     total = w8.flops("step")
     value = total / (st["median"] * 1e-3) / 1e12
-    dom = max(parts, key=parts.get)
+    dom = max((k for k in parts if w8.flops(k) > 0), key=parts.get)
     achieved = w8.flops(dom) / (parts[dom] * 1e-3) / 1e12
+    prefix = "hstu_attn_fp8full_" if w8.full_fp8 else "hstu_attn_"
     traffic = None
     tfile = REPO / "profiles" / "hbm_traffic_cfg3.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get(f"hstu_attn_{dom}")
+        traffic = json.loads(tfile.read_text()).get(prefix + dom)
     res = {
         "metric": "HSTU jagged attn fwd+bwd TFLOP/s (FP8 e4m3 inputs) + % MFMA peak, 1xMI355X",
         "value": round(value, 2),
@@ -606,6 +629,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": "BASELINE config 3: jagged HSTU attention fwd+bwd (dq, dk, dv, dbias), e4m3 q/k/v "
                                "with per-token-per-head scales, relative-position bias [4, 2047], bf16 out/grads",
+                   "backward": ("full-FP8 (the reference's DLRM_HSTU_FP8_BWD_FULL contract: dO quantized to e4m3 "
+                                "in pow2 (sequence, head, 32-token) blocks inside the step, e4m3 P and dS, all five "
+                                "products on e4m3 MFMAs)" if w8.full_fp8 else "e4m3 inputs, bf16 dO and dS"),
                    "B": len(lengths), "T": w8.T, "max_seq_len": N, "H": H, "D": D,
                    "causal_pairs_per_head": w8.P, "attn_bias": True, "parallelism": "none (1 GPU)"},
         "timing": {"ms_per_step_median_cold": round(st["median"], 4), "p10": round(st["p10"], 4),
@@ -615,14 +641,25 @@ def main():
         "pct_fp8_peak": round(100 * value / PEAK_TFLOPS["fp8"], 2),
         "kernels_ms": {k: round(v, 4) for k, v in parts.items()},
         "kernels_tflops": {k: round(w8.flops(k) / (v * 1e-3) / 1e12, 1) for k, v in parts.items()},
-        "roofline": {"bound": "mfma", "kernel": f"hstu_attn_{dom}", "achieved": round(achieved, 1),
+        "roofline": {"bound": "mfma", "kernel": prefix + dom, "achieved": round(achieved, 1),
                      "peak": PEAK_TFLOPS["fp8"], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS["fp8"], 4), "traffic": traffic},
     }
     del w8
     torch.cuda.empty_cache()
+    if not args.headline_only and w8.full_fp8:
+        wd = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
+        wall_d, st_d, parts_d = wd.run(args.steps, max(args.warmup, 2), flush)
+        vd = wd.flops("step") / (st_d["median"] * 1e-3) / 1e12
+        res["fp8_bf16_dout"] = {"value": round(vd, 2), "unit": "TFLOP/s", "ms_per_step": round(st_d["median"], 4),
+                                "pct_fp8_peak": round(100 * vd / PEAK_TFLOPS["fp8"], 2),
+                                "kernels_ms": {k: round(v, 4) for k, v in parts_d.items()},
+                                "note": "the same step with the e4m3-input backward on the bf16 dO (bf16 dS tiles, "
+                                        "bf16 MFMAs for dV, dK, dQ)"}
+        del wd
+        torch.cuda.empty_cache()
     if not args.headline_only:
-        wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False)
+        wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=w8.full_fp8)
         wall_n, st_n, parts_n = wn.run(args.steps, max(args.warmup, 2), flush)
         vn = wn.flops("step") / (st_n["median"] * 1e-3) / 1e12
         res["no_bias"] = {"value": round(vn, 2), "unit": "TFLOP/s", "ms_per_step": round(st_n["median"], 4),

@@ -145,6 +145,63 @@ int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, in
                                       int bias_R);
 
 /*
+ * Full-FP8 backward (causal mask only; D = 128): e4m3 q, k, v as for
+ * hstu_attn_bwd, and the upstream gradient as the block quantizer leaves it
+ * -- dout8 e4m3 [T, H, D] (row stride dout_row_stride bytes, 16-byte aligned
+ * rows) and dout_e8 uint8 [T, H] = 127 - e with dO = dout8 * 2^-e per
+ * (sequence, head, 32-token group) (hstu_quantize_do_e4m3_blk).  All five
+ * products run on the e4m3 MFMA: P and dS are cast to e4m3 with the
+ * reference's N-relative power-of-two pre-scales (silu / N * 2^(c+3), dS *
+ * 2^(c-3), c = ceil(log2 N)), and the dO group scales are applied by the
+ * MFMA's E8M0 block-scale operands.  dS passes from the dK/dV kernel to the
+ * dQ kernel as e4m3 tiles in the workspace.  Writes dq, dk, dv (bf16) and,
+ * if dbias != NULL, the bias gradient (computed from the e4m3 dS).
+ * Replaces: flydsl_hstu_attention_bwd under DLRM_HSTU_FP8_BWD_FULL
+ *           (ops/flydsl/hstu_flydsl_mha.py:1330-1394 dO contract, :1351-1370
+ *           pre-scales, :1674-1741 dq split; ops/flydsl/hstu_bwd_dkdv.py:356-403).
+ */
+int64_t hstu_attn_bwd_fp8_workspace_bytes(int64_t total_tokens, int B, int H, int D, int max_seq_len,
+                                          int bias_R);
+int hstu_attn_bwd_fp8(const void* dout8, const void* dout_e8, int64_t dout_row_stride,
+                      const void* q, const void* k, const void* v,
+                      int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                      const float* q_scale, const float* k_scale, const float* v_scale,
+                      int64_t scale_row_stride, int64_t scale_head_stride,
+                      const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                      float alpha, const float* attn_bias, int bias_R,
+                      void* dq, void* dk, void* dv,
+                      int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
+                      float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
+                      hipStream_t stream);
+/*
+ * Its two halves, same arguments, run in order on one stream with one
+ * workspace: _dkdv writes dk, dv and leaves the e4m3 dS tiles (and the scale
+ * maxima) in the workspace; _dq reads them and writes dq and dbias.
+ */
+int hstu_attn_bwd_fp8_dkdv(const void* dout8, const void* dout_e8, int64_t dout_row_stride,
+                           const void* q, const void* k, const void* v,
+                           int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                           const float* q_scale, const float* k_scale, const float* v_scale,
+                           int64_t scale_row_stride, int64_t scale_head_stride,
+                           const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                           float alpha, const float* attn_bias, int bias_R,
+                           void* dq, void* dk, void* dv,
+                           int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
+                           float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
+                           hipStream_t stream);
+int hstu_attn_bwd_fp8_dq(const void* dout8, const void* dout_e8, int64_t dout_row_stride,
+                         const void* q, const void* k, const void* v,
+                         int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                         const float* q_scale, const float* k_scale, const float* v_scale,
+                         int64_t scale_row_stride, int64_t scale_head_stride,
+                         const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                         float alpha, const float* attn_bias, int bias_R,
+                         void* dq, void* dk, void* dv,
+                         int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
+                         float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
+                         hipStream_t stream);
+
+/*
  * The two halves of hstu_attn_bwd, same arguments: hstu_attn_bwd_dkdv writes
  * dk and dv only (dq may be NULL); hstu_attn_bwd_dq writes dq and dbias only
  * (dk, dv may be NULL).  Each writes its own parts of the shared workspace,

@@ -232,6 +232,12 @@ struct AttnParams {
   int blocks_per_seq;  // ceil(N / 128)
   uint8_t* ds_ws;           // workspace: bf16 dS tiles written by dK/dV, read by dQ (causal masks)
   const int64_t* ds_base;   // workspace: per-sequence exclusive prefix of ds_tiles(L) [B + 1]
+  // full-FP8 backward (hstu_attn_bwd_fp8)
+  const uint8_t* do8;       // e4m3 dO [T, H, D], row stride do_rs bytes
+  const uint8_t* e8;        // [T, H]: 127 - e of each token's dO group (dO8 = e4m3(dO * 2^e))
+  const unsigned* f8max;    // workspace: float bits of max q_scale, max k_scale
+  float p8_scale;           // e4m3 P = silu / N * p8_scale (a power of two times N-relative)
+  float ds8_scale;          // e4m3 dS = dS' * (scale normaliser) * ds8_scale
 };
 
 struct SeqCtx {
@@ -1553,6 +1559,542 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
   }
 }
 
+// =====================================================================
+// Full-FP8 backward (hstu_attn_bwd_fp8): e4m3 q, k, v and an e4m3 dO with
+// one power-of-two scale per (sequence, head, 32-token group) -- the input
+// contract of the reference's production backward (quantize_do_e4m3_blk,
+// ops/flydsl/hstu_do_fp8.py:16-38; ops/flydsl/hstu_flydsl_mha.py:1330-1394).
+// All five products are v_mfma_scale_f32_16x16x128_f8f6f4:
+//   S = Q.K^T, dP = dO8.V^T          e4m3 x e4m3, dP kept in dO8's scaled domain
+//   dV^T = dO8^T . P8                P8 = e4m3(silu / N * 2^(c+3)), c = ceil(log2 N);
+//                                    the dO group scales 2^-e ride the MFMA's
+//                                    E8M0 operand of the dO side
+//   dK^T = Q8^T . dS8k               dS8k = e4m3(dS' s_q 2^-Eq 2^(c-3)), E8M0 = dO group
+//   dQ^T = K8^T . dS8q^T             dS8q = e4m3(dS' s_k 2^-Ek 2^(c-3)), stored e4m3
+// where dS' = s_v dP silu'(x) / N (the dO scale still applied), 2^-Eq / 2^-Ek
+// the power-of-two normalisers of the largest q / k scale, and the P and dS
+// pre-scales the reference's N-relative ones (hstu_flydsl_mha.py:1351-1370).
+//
+// K-slot layout.  A 16x16x128 e4m3 operand lane (row, group g) holds K
+// indices 16g..16g+15 and 64+16g..+15, and K-block b (32 indices) takes its
+// E8M0 scale from lane group b.  In the dK/dV kernel the contraction index is
+// the query of a 128-query tile; the S fragment gives lane group g the
+// queries 16qs + 4g + r (qs = 0..7).  Two permlane16 swaps per 64 queries
+// turn those into runs of eight -- group 0: queries {0-7, 16-23}, 1: {32-39,
+// 48-55}, 2: {8-15, 24-31}, 3: {40-47, 56-63} (+64 for the high half) -- so
+// K-block b holds exactly the 32 tokens of one dO group (p / 64, (p % 16) / 8),
+// and the other operand reads the same tokens with ds_read_b64_tr_b8.
+// =====================================================================
+struct F8Bwd {
+  static constexpr int NT = 512;            // dK/dV: 8 waves, 16 keys each
+  static constexpr int BN = 128, BM = 128;  // keys per block, queries per tile
+  // dK/dV stage: Q and dO tiles of 128-byte e4m3 rows, unpadded (LDS DMA
+  // writes 1 KiB runs), data chunk c (bytes 16c .. 16c + 15) of row r at
+  // 16-byte slot c ^ kv_swz(r).  The swizzle spreads the 16 rows of a
+  // ds_read_b128 and the row groups 8 and 32 apart of a ds_read_b64_tr_b8
+  // over distinct banks; it is constant under r -> r + 16 (bits 1-3 and 5).
+  __host__ __device__ static constexpr int kv_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 5) & 1) << 2); }
+  __host__ __device__ static constexpr int kv_at(int r, int c) { return r * 128 + 16 * (c ^ kv_swz(r)); }
+  static constexpr int Q_OFF = 0;
+  static constexpr int DO_OFF = Q_OFF + BM * 128;
+  static constexpr int SQ_OFF = DO_OFF + BM * 128;  // 128 fp32 query scales
+  static constexpr int B_OFF = SQ_OFF + BM * 4;     // 256 fp32: pre-scaled bias of offsets m0-n0-127 ..
+  static constexpr int STAGE = B_OFF + 256 * 4;
+  static constexpr int LDS = 2 * STAGE;
+  // dQ: K tile [key][d] and dS tile [key][query], 128-byte rows at a pitch of
+  // 160 (== 32 mod 64: 16-row ds_read_b128 reads are conflict-free); rows of
+  // odd 16-row groups shifted by 16 bytes so the transposed reads of lane
+  // groups 16 rows apart use distinct banks.
+  static constexpr int PT = 160;
+  __host__ __device__ static constexpr int row16(int r) { return r * PT + 16 * ((r >> 4) & 1); }
+  static constexpr int TILE = BN * BM;      // one stored e4m3 dS tile (16 KiB)
+  // dQ: 4 waves, 32 queries each
+  static constexpr int QK_OFF = 0;
+  static constexpr int QDS_OFF = QK_OFF + BN * PT + 16;
+  static constexpr int QHIST_OFF = QDS_OFF + BN * PT + 16;
+  static int dq_lds(bool bias, int R) { return QHIST_OFF + (bias ? R * 4 : 0); }
+};
+
+// Stored dS tiles: for key block kb and query tile qt >= kb of a sequence
+// with nq = ceil(L / 128) tiles, (sequence, head) items hold nq (nq + 1) / 2
+// tiles, kb-major.  Inside a tile: [wave w][half hf][lane][16 bytes], the
+// 4 dwords qs = 0..3 of lane (li, g) being keys 16 w + li, queries
+// 64 hf + 16 qs + 4 g + (0..3).
+__host__ __device__ inline int64_t f8_tiles(int64_t L) {
+  const int64_t nq = (L + 127) / 128;
+  return nq * (nq + 1) / 2;
+}
+__device__ __forceinline__ uint8_t* f8_tile(const AttnParams& p, const SeqCtx& c, int kb, int qt) {
+  const int64_t nq = (c.L + 127) / 128;
+  const int64_t idx = p.ds_base[c.b] * p.H + (int64_t)c.h * f8_tiles(c.L) + (int64_t)kb * nq -
+                      (int64_t)kb * (kb - 1) / 2 + (qt - kb);
+  return p.ds_ws + idx * F8Bwd::TILE;
+}
+
+// 2^-E with E the frexp exponent of the largest scale: s * 2^-E in (0, 1).
+__device__ __forceinline__ float f8_norm(unsigned bits) {
+  int e = 0;
+  (void)frexpf(__uint_as_float(bits), &e);
+  return ldexpf(1.0f, -e);
+}
+
+__device__ __forceinline__ uint32_t buf_ldu8(BufRsrc r, uint32_t voff) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, 0, 0);
+}
+
+template <bool BIAS>
+__global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnParams p) {
+  using C = F8Bwd;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/false, sc)) return;
+  const int L = sc.L, h = sc.h;
+  const int n0 = sc.blk * C::BN;
+  if (n0 >= L) return;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, li = lane & 15,
+            g = lane >> 4;
+  const int kw0 = n0 + 16 * wave;
+  const int key = kw0 + li;
+  const bool key_ok = key < L;
+
+  // buffer resources over this (sequence, head): rows >= L read as zero
+  const uint32_t qrs = (uint32_t)p.q_rs, dors = (uint32_t)p.do_rs;
+  const BufRsrc q_rsrc = make_rsrc(p.q + sc.start * p.q_rs + (int64_t)h * 128, L > 0 ? (L - 1) * qrs + 128 : 0u);
+  const BufRsrc do_rsrc = make_rsrc(p.do8 + sc.start * p.do_rs + (int64_t)h * 128, L > 0 ? (L - 1) * dors + 128 : 0u);
+  const uint32_t s_step = (uint32_t)(p.s_rs * 4);
+  const BufRsrc sq_rsrc = make_rsrc(p.q_scale + sc.start * p.s_rs + h * p.s_hs, (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4));
+  const BufRsrc e8_rsrc = make_rsrc(p.e8 + sc.start * p.H + h, (uint32_t)(L * p.H));
+  const int ext_len = bias_ext_len(p.N);
+  const BufRsrc b_rsrc = make_rsrc(BIAS ? p.bias_ext + (int64_t)h * ext_len : nullptr, BIAS ? (uint32_t)(ext_len * 4) : 0u);
+
+  // this lane's key: e4m3 K and V rows (B operands of S and dP), its scales
+  i32x8 kf8 = {0, 0, 0, 0, 0, 0, 0, 0}, vf8 = {0, 0, 0, 0, 0, 0, 0, 0};
+  float sk = 0.f, sv = 0.f;
+  if (key_ok) {
+    const uint8_t* kr = p.k + (sc.start + key) * p.k_rs + (int64_t)h * 128;
+    const uint8_t* vr = p.v + (sc.start + key) * p.v_rs + (int64_t)h * 128;
+    kf8 = cat8(*(const u32x4*)(kr + 16 * g), *(const u32x4*)(kr + 64 + 16 * g));
+    vf8 = cat8(*(const u32x4*)(vr + 16 * g), *(const u32x4*)(vr + 64 + 16 * g));
+    sk = p.k_scale[(sc.start + key) * p.s_rs + h * p.s_hs];
+    sv = p.v_scale[(sc.start + key) * p.s_rs + h * p.s_hs];
+  }
+  const float nq = f8_norm(p.f8max[0]), nk = f8_norm(p.f8max[1]);
+  const float ck = -p.alpha * kLog2e * sk;                    // times s_q: exp2 argument factor
+  const float an = sv * nq * p.ds8_scale * p.inv_n;           // times s_q: dS8k factor
+  const float bn = sv * sk * nk * p.ds8_scale * p.inv_n;      // dS8q factor
+  const float kp = -kLn2 * p.p8_scale * p.inv_n;              // t * sigmoid -> e4m3 P
+
+  f32x4 dvt[8], dkt[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) dvt[dt] = dkt[dt] = zero4();
+
+  // one 128-query tile per stage, moved by LDS DMA: wave w takes rows
+  // 8 w + 64 i + (lane >> 3), i = 0, 1, of Q and dO (lane slot lane & 7
+  // holds data chunk (lane & 7) ^ kv_swz(row)), waves 0-1 the 128 query
+  // scales, waves 2-5 the 256 bias values
+  const int lrow = 8 * wave + (lane >> 3);
+  const uint32_t chunk = 16u * (uint32_t)((lane & 7) ^ C::kv_swz(lrow));
+  const uint32_t q_voff = lrow * qrs + chunk, d_voff = lrow * dors + chunk;
+  // E8M0 byte of the dO group K-block g covers: token m0 + 64 (g >> 1) + 8 (g & 1),
+  // loaded with its tile (complete at the tile's wait)
+  const uint32_t e8_tok = 64 * (g >> 1) + 8 * (g & 1);
+  int sc_next = 0;
+  auto load = [&](int m0, uint8_t* st) {
+    sc_next = (int)buf_ldu8(e8_rsrc, (uint32_t)(m0 + (int)e8_tok) * (uint32_t)p.H);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      buf_to_lds<16>(q_rsrc, st + C::Q_OFF + (8 * wave + 64 * i) * 128, q_voff, (uint32_t)(m0 + 64 * i) * qrs);
+      buf_to_lds<16>(do_rsrc, st + C::DO_OFF + (8 * wave + 64 * i) * 128, d_voff, (uint32_t)(m0 + 64 * i) * dors);
+    }
+    if (wave < 2) {
+      buf_to_lds<4>(sq_rsrc, st + C::SQ_OFF + 256 * wave, (uint32_t)lane * s_step, (uint32_t)(m0 + 64 * wave) * s_step);
+    } else if (BIAS && wave < 6) {
+      buf_to_lds<4>(b_rsrc, st + C::B_OFF + 256 * (wave - 2), (uint32_t)(64 * (wave - 2) + lane) * 4u,
+                    (uint32_t)(m0 - n0 + p.N) * 4u);
+    }
+  };
+
+  // S / dP A operands: row 64 hf + 16 qs + li, data chunks g and g + 4 at
+  // slots g ^ kv_swz(row) and that ^ 4, kv_swz(row) = (li >> 1) ^ 4 (qs >> 1)
+  const int ab0 = li * 128 + 16 * (g ^ (li >> 1)), ab1 = ab0 ^ 64;
+  // transposed (tr_b8) operand reads: lane group g takes the tokens
+  // base(g) + {0, 16} (low half) and + {64, 80} (high half), 8 each; the
+  // swizzle of its rows is that of base(g) + li / 2
+  const int tr_row = 32 * (g & 1) + 8 * (g >> 1) + (li >> 1);
+  const int tr_base = tr_row * 128 + 8 * (li & 1), tr_x = 16 * C::kv_swz(tr_row);
+  auto tr_frag = [&](const uint8_t* tile, int dt) {
+    const uint8_t* t = tile + tr_base + ((16 * dt) ^ tr_x);
+    const u32x2 r0 = lds_tr8(t), r1 = lds_tr8(t + 16 * 128);
+    const u32x2 r2 = lds_tr8(t + 64 * 128), r3 = lds_tr8(t + 80 * 128);
+    i32x8 f;  // read order: tokens +0..7, +16..23, +64..71, +80..87
+    f[0] = (int)r0[0]; f[1] = (int)r0[1]; f[2] = (int)r1[0]; f[3] = (int)r1[1];
+    f[4] = (int)r2[0]; f[5] = (int)r2[1]; f[6] = (int)r3[0]; f[7] = (int)r3[1];
+    return f;
+  };
+  const int R1 = p.bias_R - 1;
+  const int bias_lane = 127 + 4 * g - 16 * wave - li;  // + 64 hf + 16 qs + r
+  const int ntiles = (L - n0 + C::BM - 1) / C::BM;
+
+  // this block's stored dS tiles (query tiles blk, blk + 1, .. are consecutive)
+  uint8_t* const ds_dst = f8_tile(p, sc, sc.blk, sc.blk) + (size_t)((wave * 2) * 64 + lane) * 16;
+  load(n0, smem);
+  lds_dma_wait();
+  __syncthreads();
+
+  auto tile_body = [&](int t, auto masked_tag, auto bconst_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool BCONST = decltype(bconst_tag)::value;
+    const int m0 = n0 + t * C::BM;
+    const uint8_t* buf = smem + (t & 1) * C::STAGE;
+    const int sc_e = sc_next;
+    if (t + 1 < ntiles) load(m0 + C::BM, smem + ((t + 1) & 1) * C::STAGE);
+    uint8_t* dst = ds_dst + (size_t)t * C::TILE;
+    const float* bias_lds = (const float*)(buf + C::B_OFF);
+    const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
+    uint32_t pd[8], dk8[8];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      f32x4 s[4], dp[4];
+#pragma unroll
+      for (int qs = 0; qs < 4; ++qs) {
+        const int rb = (64 * hf + 16 * qs) * 128;
+        const int lo = rb + (qs < 2 ? ab0 : ab1), hi = rb + (qs < 2 ? ab1 : ab0);
+        const i32x8 aq = cat8(lds_ld128(buf + C::Q_OFF + lo), lds_ld128(buf + C::Q_OFF + hi));
+        const i32x8 ad = cat8(lds_ld128(buf + C::DO_OFF + lo), lds_ld128(buf + C::DO_OFF + hi));
+        s[qs] = mfma_fp8(aq, kf8, zero4());
+        dp[qs] = mfma_fp8(ad, vf8, zero4());
+      }
+      uint32_t dq8[4];
+#pragma unroll
+      for (int qs = 0; qs < 4; ++qs) {
+        const f32x4 sq4 = lds_ldf4(buf + C::SQ_OFF + (64 * hf + 16 * qs + 4 * g) * 4);
+        const float* bl = bias_lds + bias_lane + 64 * hf + 16 * qs;
+        float pv[4], dkv[4], dqv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float tt = s[qs][r] * (ck * sq4[r]);
+          if constexpr (BIAS) tt += BCONST ? bconst : bl[r];
+          const float sg = sig_of_t(tt);
+          const float pp = tt * sg;
+          float pval = pp * kp;
+          float dsv = dp[qs][r] * dsilu_factor(sg, pp);
+          if constexpr (MASKED) {
+            const bool ok = 64 * hf + 16 * qs + 4 * g + r >= 16 * wave + li;
+            pval = ok ? pval : 0.f;
+            dsv = ok ? dsv : 0.f;
+          }
+          pv[r] = __builtin_fminf(pval, 448.f);
+          dkv[r] = __builtin_amdgcn_fmed3f(dsv * (an * sq4[r]), -448.f, 448.f);
+          dqv[r] = __builtin_amdgcn_fmed3f(dsv * bn, -448.f, 448.f);
+        }
+        pd[4 * hf + qs] = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
+        dk8[4 * hf + qs] = pack_fp8x4(dkv[0], dkv[1], dkv[2], dkv[3]);
+        dq8[qs] = pack_fp8x4(dqv[0], dqv[1], dqv[2], dqv[3]);
+      }
+      // the dQ kernel's operand, streamed out (read once, much later)
+      __builtin_nontemporal_store(u32x4{dq8[0], dq8[1], dq8[2], dq8[3]}, (u32x4*)(dst + hf * 64 * 16));
+      // runs of eight queries per lane group (groups 0<->1 and 2<->3 trade qs 2,3 for qs 0,1)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const auto a = __builtin_amdgcn_permlane16_swap(pd[4 * hf + j], pd[4 * hf + j + 2], false, false);
+        pd[4 * hf + j] = a[0];
+        pd[4 * hf + j + 2] = a[1];
+        const auto b = __builtin_amdgcn_permlane16_swap(dk8[4 * hf + j], dk8[4 * hf + j + 2], false, false);
+        dk8[4 * hf + j] = b[0];
+        dk8[4 * hf + j + 2] = b[1];
+      }
+    }
+    // after the swaps pd[4 hf + j] holds queries base(g) + 64 hf + {0, 16, 4, 20}[j] + 0..3:
+    // B operand dwords in the A fragment's token order (+0..3, 4..7, 16..19, 20..23)
+    i32x8 bp, bk;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int src = (j & 4) | ((j & 1) << 1) | ((j >> 1) & 1);  // 0 2 1 3 4 6 5 7
+      bp[j] = (int)pd[src];
+      bk[j] = (int)dk8[src];
+    }
+    // dV^T += dO8^T . P8 (dO group scales on the dO side), dK^T += Q8^T . dS8k
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const i32x8 ado = tr_frag(buf + C::DO_OFF, dt);
+      dvt[dt] = mfma_fp8_scaled(ado, bp, dvt[dt], sc_e, 127);
+      const i32x8 aq = tr_frag(buf + C::Q_OFF, dt);
+      dkt[dt] = mfma_fp8_scaled(aq, bk, dkt[dt], 127, sc_e);
+      __builtin_amdgcn_sched_barrier(0);  // keep each step's operand reads next to its MFMAs
+    }
+    lds_dma_wait();  // the next stage's DMA (and this tile's dS stores) done
+    __syncthreads();
+  };
+
+  // tile 0 holds the diagonal; tiles whose smallest offset m0 - n0 - 127 is
+  // >= R - 1 see one clamped bias value
+  int t_const = ntiles;
+  if (BIAS) t_const = max(1, min(ntiles, (R1 + 127 + C::BM - 1) / C::BM));
+  tile_body(0, std::true_type{}, std::false_type{});
+  int t = 1;
+  for (; t < t_const; ++t) tile_body(t, std::false_type{}, std::false_type{});
+  if constexpr (BIAS) {
+    for (; t < ntiles; ++t) tile_body(t, std::false_type{}, std::true_type{});
+  }
+
+  if (!key_ok) return;
+  // lane (key, g) holds d = 16 dt + 4 g + r of its key
+  const float fin_v = 1.0f / p.p8_scale;
+  const float fin_k = p.alpha / (nq * p.ds8_scale);
+  uint16_t* dkr = p.dk + (sc.start + key) * p.dk_rs + (int64_t)h * 128 + 4 * g;
+  uint16_t* dvr = p.dv + (sc.start + key) * p.dv_rs + (int64_t)h * 128 + 4 * g;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    *(u32x2*)(dkr + 16 * dt) = u32x2{pack_bf16(dkt[dt][0] * fin_k, dkt[dt][1] * fin_k),
+                                     pack_bf16(dkt[dt][2] * fin_k, dkt[dt][3] * fin_k)};
+    *(u32x2*)(dvr + 16 * dt) = u32x2{pack_bf16(dvt[dt][0] * fin_v, dvt[dt][1] * fin_v),
+                                     pack_bf16(dvt[dt][2] * fin_v, dvt[dt][3] * fin_v)};
+  }
+}
+
+// dQ from the stored e4m3 dS tiles (and the bias gradient from the same
+// bytes).  Block = one 128-query tile qt of a (sequence, head); it walks the
+// key blocks kb = 0..qt.  Per step the K tile [key][d] and the dS tile
+// [key][query] are staged in LDS; dQ^T = K8^T . dS8q^T with both operands
+// read transposed (ds_read_b64_tr_b8), so a lane ends with 4 consecutive d
+// of one query.
+template <bool BIAS>
+__global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams p) {
+  using C = F8Bwd;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/true, sc)) return;
+  const int L = sc.L, h = sc.h;
+  const int qt = sc.blk;
+  const int m0 = qt * C::BM;
+  if (m0 >= L) return;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const uint32_t krs = (uint32_t)p.k_rs;
+  const BufRsrc k_rsrc = make_rsrc(p.k + sc.start * p.k_rs + (int64_t)h * 128, L > 0 ? (L - 1) * krs + 128 : 0u);
+  const BufRsrc e8_rsrc = make_rsrc(p.e8 + sc.start * p.H + h, (uint32_t)(L * p.H));
+  const uint32_t s_step = (uint32_t)(p.s_rs * 4);
+  const BufRsrc sk_rsrc = make_rsrc(p.k_scale + sc.start * p.s_rs + h * p.s_hs, (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4));
+  const float nk = f8_norm(p.f8max[1]);
+  const float unscale = 1.0f / (nk * p.ds8_scale);
+  const int R1 = p.bias_R - 1;
+  float* hist = (float*)(smem + C::QHIST_OFF);
+  if constexpr (BIAS) {
+    for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
+  }
+  // bias gradient: 2^(E8 - 127) of the dO group of this lane's query rows in half hf
+  float grp[2] = {1.f, 1.f};
+  if constexpr (BIAS) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint32_t b = buf_ldu8(e8_rsrc, (uint32_t)(m0 + 64 * hf + 8 * (g >> 1)) * (uint32_t)p.H);
+      grp[hf] = ldexpf(1.0f, (int)b - 127);
+    }
+  }
+
+  f32x4 acc[8][2];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt][0] = acc[dt][1] = zero4();
+
+  // staged registers of one key block: 4 K chunks, this lane's 4 dS pieces
+  // (waves 2 wave, 2 wave + 1 of the dK/dV kernel, halves 0, 1) and, for the
+  // bias gradient, 1 / s_k of its two keys
+  u32x4 kc[4], dsp[4];
+  float isk[2] = {0.f, 0.f};
+  auto load = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kThreads * i, row = c >> 3, ch = c & 7;
+      kc[i] = buf_ld128(k_rsrc, row * krs + 16 * ch, (uint32_t)(kb * C::BN) * krs);
+    }
+    const uint8_t* tile = f8_tile(p, sc, kb, qt);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = 2 * wave + (j >> 1), hf = j & 1;
+      dsp[j] = *(const u32x4*)(tile + (size_t)((w * 2 + hf) * 64 + lane) * 16);
+    }
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float s = buf_ldf(sk_rsrc, (uint32_t)(16 * (2 * wave + j) + li) * s_step, (uint32_t)(kb * C::BN) * s_step);
+        isk[j] = s > 0.f ? unscale / s : 0.f;
+      }
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + kThreads * i, row = c >> 3, ch = c & 7;
+      *(u32x4*)(smem + C::QK_OFF + C::row16(row) + 16 * ch) = kc[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = 2 * wave + (j >> 1), hf = j & 1;
+      uint8_t* row = smem + C::QDS_OFF + C::row16(16 * w + li) + 64 * hf + 4 * g;
+#pragma unroll
+      for (int qs = 0; qs < 4; ++qs) *(uint32_t*)(row + 16 * qs) = dsp[j][qs];
+    }
+  };
+  float dclamp = 0.f;
+  // bias gradient of the staged step: 32 x 32 sub-tiles (half hf, query pair
+  // qp) x (this wave's 32 keys), from the C-fragment layout the pieces have
+  auto bias_grad = [&](int kb, const u32x4 (&pcs)[4], const float (&iskv)[2]) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int qp = 0; qp < 2; ++qp) {
+        const int base = (m0 + 64 * hf + 32 * qp) - (kb * C::BN + 32 * wave);  // i - j of its (0, 0)
+        if (base + 31 < 0) continue;  // above the diagonal: zero
+        float v[2][2][4];             // [query sub-tile][key sub-tile][r]
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            const uint32_t w = pcs[2 * kt + hf][2 * qp + a];
+            const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+            const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+            const float c = iskv[kt] * grp[hf];
+            v[a][kt][0] = lo[0] * c;
+            v[a][kt][1] = lo[1] * c;
+            v[a][kt][2] = hi[0] * c;
+            v[a][kt][3] = hi[1] * c;
+          }
+        }
+        if (base - 31 >= R1) {  // every offset clamps
+#pragma unroll
+          for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) dclamp += v[a][kt][r];
+          continue;
+        }
+        float dacc[4] = {0.f, 0.f, 0.f, 0.f};
+        diag_accumulate<0>(dacc, v[0][0]);
+        diag_accumulate<0>(dacc, v[1][1]);
+        diag_accumulate<1>(dacc, v[0][1]);
+        diag_accumulate<-1>(dacc, v[1][0]);
+        const float dv = diag_reduce(dacc, lane);
+        const int off = base - (li + 16 - 16 * g);
+        if (off >= R1) dclamp += dv;
+        else if (off >= 0) atomicAdd(&hist[off], dv);
+      }
+    }
+  };
+
+  // operand reads: dS^T columns (queries c0 + li) and K^T rows (d c0 + li) of
+  // keys 16 g .. 16 g + 15 and 64 + 16 g .. +15
+  const int trk = C::row16(16 * g + (li >> 1)) + 8 * (li & 1);
+  auto frag = [&](const uint8_t* t) {
+    // rows +8, +64, +72 stay in the same 16-row parity: one swizzle offset
+    const u32x2 r0 = lds_tr8(t), r1 = lds_tr8(t + 8 * C::PT);
+    const u32x2 r2 = lds_tr8(t + 64 * C::PT), r3 = lds_tr8(t + 72 * C::PT);
+    i32x8 f;
+    f[0] = (int)r0[0]; f[1] = (int)r0[1]; f[2] = (int)r1[0]; f[3] = (int)r1[1];
+    f[4] = (int)r2[0]; f[5] = (int)r2[1]; f[6] = (int)r3[0]; f[7] = (int)r3[1];
+    return f;
+  };
+
+  const int nsteps = qt + 1;
+  load(0);
+  store();
+  __syncthreads();
+  for (int kb = 0; kb < nsteps; ++kb) {
+    u32x4 cur[4];
+    float cur_isk[2] = {isk[0], isk[1]};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cur[j] = dsp[j];
+    if (kb + 1 < nsteps) load(kb + 1);
+    i32x8 bq[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) bq[qs] = frag(smem + C::QDS_OFF + trk + 32 * wave + 16 * qs);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const i32x8 ak = frag(smem + C::QK_OFF + trk + 16 * dt);
+      acc[dt][0] = mfma_fp8(ak, bq[0], acc[dt][0]);
+      acc[dt][1] = mfma_fp8(ak, bq[1], acc[dt][1]);
+    }
+    if constexpr (BIAS) bias_grad(kb, cur, cur_isk);
+    __syncthreads();
+    if (kb + 1 < nsteps) {
+      store();
+      __syncthreads();
+    }
+  }
+
+  if constexpr (BIAS) {
+    if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
+    __syncthreads();
+    float* dst = p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1) + R1;
+    for (int i = tid; i < p.bias_R; i += kThreads) {
+      const float v = hist[i];
+      if (v != 0.f) atomicAdd(&dst[i], v);
+    }
+  }
+  // dQ_i = alpha 2^-e(i) / (nk ds8_scale) . acc
+  const float fin = p.alpha * unscale;
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    const int row = m0 + 32 * wave + 16 * qs + li;
+    if (row >= L) continue;
+    const uint32_t b = buf_ldu8(e8_rsrc, (uint32_t)row * (uint32_t)p.H);
+    const float f = fin * ldexpf(1.0f, (int)b - 127);
+    uint16_t* dst = p.dq + (sc.start + row) * p.dq_rs + (int64_t)h * 128 + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *(u32x2*)(dst + 16 * dt) = u32x2{pack_bf16(acc[dt][qs][0] * f, acc[dt][qs][1] * f),
+                                       pack_bf16(acc[dt][qs][2] * f, acc[dt][qs][3] * f)};
+  }
+}
+
+// base[b] = sum over sequences b' < b of f8_tiles(min(length, N)); base[B] =
+// the total; and the two scale maxima (f8max) reset for f8_scale_max.
+__global__ void __launch_bounds__(1024) f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base,
+                                                       unsigned* f8max) {
+  __shared__ int64_t part[1024];
+  const int tid = threadIdx.x, per = (B + 1023) / 1024, b0 = tid * per;
+  if (tid < 2) f8max[tid] = 0u;
+  auto tiles = [&](int b) { return f8_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); };
+  int64_t sum = 0;
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < B) sum += tiles(b0 + i);
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int64_t add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int64_t run = tid ? part[tid - 1] : 0;
+  for (int i = 0; i < per; ++i) {
+    if (b0 + i < B) {
+      base[b0 + i] = run;
+      run += tiles(b0 + i);
+    }
+  }
+  if (tid == 1023) base[B] = part[1023];
+}
+
+// f8max[0] / [1] = float bits of the largest q / k scale over [T, H] (or the scalar).
+__global__ void f8_scale_max(const float* qs, const float* ks, int64_t n, int H, int64_t srs, int64_t shs,
+                             unsigned* f8max) {
+  float mq = 0.f, mk = 0.f;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / H, hh = i - t * H, o = t * srs + hh * shs;
+    mq = fmaxf(mq, fabsf(qs[o]));
+    mk = fmaxf(mk, fabsf(ks[o]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    mq = fmaxf(mq, __shfl_xor(mq, off));
+    mk = fmaxf(mk, __shfl_xor(mk, off));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicMax(&f8max[0], __float_as_uint(mq));
+    atomicMax(&f8max[1], __float_as_uint(mk));
+  }
+}
+
 // e4m3 q rows -> exact bf16 copy [T, H, D] for the dK/dV kernel (scale 1).
 __global__ void convert_q8_bf16(const uint8_t* q8, int64_t q_rs, const int64_t* seq_offsets, int B, int H, int D,
                                 uint16_t* q16) {
@@ -1801,12 +2343,13 @@ hipError_t ensure_lds(const void* fn) {
   return e;
 }
 
-hipError_t launch(void (*kernel)(AttnParams), int lds, int grid, AttnParams p, hipStream_t stream) {
+hipError_t launch(void (*kernel)(AttnParams), int lds, int grid, AttnParams p, hipStream_t stream,
+                  int threads = kThreads) {
   if (lds > 160 * 1024) return hipErrorInvalidValue;
   hipError_t e = ensure_lds((const void*)kernel);
   if (e != hipSuccess) return e;
   void* args[] = {&p};
-  return hipLaunchKernel((const void*)kernel, dim3(grid), dim3(kThreads), args, (size_t)lds, stream);
+  return hipLaunchKernel((const void*)kernel, dim3(grid), dim3(threads), args, (size_t)lds, stream);
 }
 
 bool check_common(int dtype, int H, int D, int B, int N, int64_t rs_q, int64_t rs_k, int64_t rs_v,
@@ -2154,3 +2697,175 @@ extern "C" int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens
 extern "C" int hstu_attn_bwd(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdAll, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dkdv(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDkdv, HSTU_BWD_ARGS); }
 extern "C" int hstu_attn_bwd_dq(HSTU_BWD_PARAMS) { return attn_bwd_impl(kBwdDq, HSTU_BWD_ARGS); }
+
+// ---------------------------------------------------------------------------
+// Full-FP8 backward entry point.
+// ---------------------------------------------------------------------------
+namespace {
+// Workspace: [block schedule][pre-clamped bias rows][partial bias gradients]
+// [scale maxima][dS tile prefix][e4m3 dS tiles].  The tiles are sized by a
+// bound that needs no lengths: sum_b nq_b (nq_b + 1) / 2 <= (nq_max + 1) / 2 *
+// (ceil(T / 128) + B), nq_max = ceil(N / 128).
+struct F8Ws {
+  int64_t sched, bias_ext, part, maxv, base, tiles, total;
+};
+int64_t f8_tiles_bound(int64_t T, int B, int N) {
+  const int64_t nq = (N + 127) / 128;
+  return ((nq + 1) * ((T + 127) / 128 + B) + 1) / 2;
+}
+F8Ws f8_ws(int64_t T, int B, int H, int N, int R) {
+  F8Ws w;
+  int64_t o = 0;
+  w.sched = o;
+  o += sched_bytes(B, H);
+  w.bias_ext = o;
+  if (R > 0) o += bias_ext_bytes(H, N);
+  w.part = o;
+  if (R > 0) o += dbias_part_bytes(H, R);
+  w.maxv = o;
+  o += 256;
+  w.base = o;
+  o += align256(((int64_t)B + 1) * 8);
+  w.tiles = o;
+  o += f8_tiles_bound(T, B, N) * H * F8Bwd::TILE;
+  w.total = o;
+  return w;
+}
+int ceil_log2(int n) {
+  int c = 0;
+  while ((1 << c) < n) ++c;
+  return c;
+}
+}  // namespace
+
+extern "C" int64_t hstu_attn_bwd_fp8_workspace_bytes(int64_t total_tokens, int B, int H, int D, int max_seq_len,
+                                                     int bias_R) {
+  if (B < 0 || H <= 0 || D != 128 || total_tokens < 0 || max_seq_len <= 0 || bias_R < 0) return -1;
+  return f8_ws(total_tokens, B, H, max_seq_len, bias_R).total;
+}
+
+namespace {
+int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t dout_row_stride, const void* q,
+                      const void* k, const void* v, int64_t q_row_stride, int64_t k_row_stride,
+                      int64_t v_row_stride, const float* q_scale, const float* k_scale, const float* v_scale,
+                      int64_t scale_row_stride, int64_t scale_head_stride, const int64_t* seq_offsets, int B,
+                      int H, int D, int max_seq_len, float alpha, const float* attn_bias, int bias_R, void* dq,
+                      void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
+                      float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
+                      hipStream_t stream) {
+  if (!check_common(HSTU_DTYPE_FP8_E4M3, H, D, B, max_seq_len, q_row_stride, k_row_stride, v_row_stride, q_scale,
+                    k_scale, v_scale, bias_R, attn_bias) ||
+      (dbias != nullptr && attn_bias == nullptr) || dout8 == nullptr || dout_e8 == nullptr ||
+      dout_row_stride < (int64_t)H * D || total_tokens < 0 ||
+      ((parts & kBwdDq) && (dq == nullptr || dq_row_stride < (int64_t)H * D)) ||
+      ((parts & kBwdDkdv) && (dk == nullptr || dv == nullptr || dk_row_stride < (int64_t)H * D ||
+                              dv_row_stride < (int64_t)H * D)))
+    return HSTU_E_BAD_ARG;
+  if (D != 128) return HSTU_E_UNSUPPORTED;
+  if (!row_alignment_ok(HSTU_DTYPE_FP8_E4M3, q_row_stride, q) || !row_alignment_ok(HSTU_DTYPE_FP8_E4M3, k_row_stride, k) ||
+      !row_alignment_ok(HSTU_DTYPE_FP8_E4M3, v_row_stride, v) ||
+      !row_alignment_ok(HSTU_DTYPE_FP8_E4M3, dout_row_stride, dout8) ||
+      ((parts & kBwdDq) && !row_alignment_ok(HSTU_DTYPE_BF16, dq_row_stride, dq)) ||
+      ((parts & kBwdDkdv) && (!row_alignment_ok(HSTU_DTYPE_BF16, dk_row_stride, dk) ||
+                              !row_alignment_ok(HSTU_DTYPE_BF16, dv_row_stride, dv))))
+    return HSTU_E_UNSUPPORTED;
+  if (B == 0) return 0;
+  const bool has_bias = attn_bias != nullptr;
+  const F8Ws wl = f8_ws(total_tokens, B, H, max_seq_len, has_bias ? bias_R : 0);
+  if (workspace == nullptr || workspace_bytes < wl.total) return HSTU_E_BAD_ARG;
+  uint8_t* ws = (uint8_t*)workspace;
+  AttnParams p{};
+  p.q = (const uint8_t*)q;
+  p.k = (const uint8_t*)k;
+  p.v = (const uint8_t*)v;
+  p.do8 = (const uint8_t*)dout8;
+  p.e8 = (const uint8_t*)dout_e8;
+  p.q_rs = q_row_stride;
+  p.k_rs = k_row_stride;
+  p.v_rs = v_row_stride;
+  p.do_rs = dout_row_stride;
+  p.q_scale = q_scale;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.s_rs = scale_row_stride;
+  p.s_hs = scale_head_stride;
+  p.seq_offsets = seq_offsets;
+  p.dq = (uint16_t*)dq;
+  p.dk = (uint16_t*)dk;
+  p.dv = (uint16_t*)dv;
+  p.dq_rs = dq_row_stride;
+  p.dk_rs = dk_row_stride;
+  p.dv_rs = dv_row_stride;
+  p.B = B;
+  p.H = H;
+  p.N = max_seq_len;
+  p.alpha = alpha;
+  p.inv_n = 1.0f / (float)max_seq_len;
+  p.bias = attn_bias;
+  p.bias_R = bias_R;
+  p.dbias = dbias;
+  // N-relative pre-scales (hstu_flydsl_mha.py:1351-1370): silu / N * 2^(c+3) and
+  // dS * 2^(c-3) with c = ceil(log2 N)
+  const int c = ceil_log2(max_seq_len < 2 ? 2 : max_seq_len);
+  p.p8_scale = ldexpf(1.0f, c + 3);
+  p.ds8_scale = ldexpf(1.0f, c - 3);
+  p.f8max = (const unsigned*)(ws + wl.maxv);
+  p.ds_base = (const int64_t*)(ws + wl.base);
+  p.ds_ws = ws + wl.tiles;
+  const int grid = sched_grid(B, H, max_seq_len);
+  hipError_t e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)(ws + wl.sched), stream);
+  if (e != hipSuccess) return (int)e;
+  if (parts & kBwdDkdv) {
+    // tile prefix and scale maxima, read by both halves
+    hipLaunchKernelGGL(f8_tile_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
+                       (int64_t*)(ws + wl.base), (unsigned*)(ws + wl.maxv));
+    const int64_t nscale = (scale_row_stride || scale_head_stride) ? total_tokens * H : 1;
+    const int sgrid = (int)std::min<int64_t>((nscale + 255) / 256, 1024);
+    hipLaunchKernelGGL(f8_scale_max, dim3(sgrid > 0 ? sgrid : 1), dim3(256), 0, stream, q_scale, k_scale, nscale,
+                       H, scale_row_stride, scale_head_stride, (unsigned*)(ws + wl.maxv));
+    if (has_bias) {
+      p.bias_ext = (const float*)(ws + wl.bias_ext);
+      hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
+                         attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
+    }
+    e = has_bias ? launch(hstu_bwd_f8_dkdv_kernel<true>, F8Bwd::LDS, grid, p, stream, F8Bwd::NT)
+                 : launch(hstu_bwd_f8_dkdv_kernel<false>, F8Bwd::LDS, grid, p, stream, F8Bwd::NT);
+    if (e != hipSuccess) return (int)e;
+  }
+  if (parts & kBwdDq) {
+    if (has_bias) {
+      p.dbias_part = (float*)(ws + wl.part);
+      const int n = kDbiasCopies * H * (2 * bias_R - 1);
+      hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 0.f);
+    }
+    e = has_bias ? launch(hstu_bwd_f8_dq_kernel<true>, F8Bwd::dq_lds(true, bias_R), grid, p, stream)
+                 : launch(hstu_bwd_f8_dq_kernel<false>, F8Bwd::dq_lds(false, 0), grid, p, stream);
+    if (e != hipSuccess) return (int)e;
+    if (has_bias && dbias != nullptr) {
+      const int n = H * (2 * bias_R - 1);
+      hipLaunchKernelGGL(reduce_dbias, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 1.0f, dbias);
+    }
+  }
+  hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
+                     (parts & kBwdDq) ? p.dq : p.dk, (parts & kBwdDq) ? p.dq_rs : p.dk_rs,
+                     (parts & kBwdDkdv) ? p.dk : (uint16_t*)nullptr, p.dk_rs,
+                     (parts & kBwdDkdv) ? p.dv : (uint16_t*)nullptr, p.dv_rs);
+  return (int)hipGetLastError();
+}
+}  // namespace
+
+#define HSTU_BWD_FP8_PARAMS                                                                                       \
+  const void *dout8, const void *dout_e8, int64_t dout_row_stride, const void *q, const void *k, const void *v,  \
+      int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, const float *q_scale,                    \
+      const float *k_scale, const float *v_scale, int64_t scale_row_stride, int64_t scale_head_stride,           \
+      const int64_t *seq_offsets, int B, int H, int D, int max_seq_len, float alpha, const float *attn_bias,     \
+      int bias_R, void *dq, void *dk, void *dv, int64_t dq_row_stride, int64_t dk_row_stride,                    \
+      int64_t dv_row_stride, float *dbias, void *workspace, int64_t workspace_bytes, int64_t total_tokens,       \
+      hipStream_t stream
+#define HSTU_BWD_FP8_ARGS                                                                                        \
+  dout8, dout_e8, dout_row_stride, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale, \
+      scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, attn_bias, bias_R, dq, dk,  \
+      dv, dq_row_stride, dk_row_stride, dv_row_stride, dbias, workspace, workspace_bytes, total_tokens, stream
+extern "C" int hstu_attn_bwd_fp8(HSTU_BWD_FP8_PARAMS) { return attn_bwd_fp8_impl(kBwdAll, HSTU_BWD_FP8_ARGS); }
+extern "C" int hstu_attn_bwd_fp8_dkdv(HSTU_BWD_FP8_PARAMS) { return attn_bwd_fp8_impl(kBwdDkdv, HSTU_BWD_FP8_ARGS); }
+extern "C" int hstu_attn_bwd_fp8_dq(HSTU_BWD_FP8_PARAMS) { return attn_bwd_fp8_impl(kBwdDq, HSTU_BWD_FP8_ARGS); }

@@ -61,6 +61,22 @@ __device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t voff, uint32_t soff
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 
+// Buffer loads straight into LDS (gfx950 buffer_load_dword{,x4} ... lds):
+// lane l of the wave writes its BYTES bytes at lds + BYTES * l (`lds` must be
+// wave-uniform: it goes through M0); offsets past the range are written as
+// zero.  The write lands asynchronously: wait with lds_dma_wait() before a
+// barrier that publishes it.
+template <int BYTES>
+__device__ __forceinline__ void buf_to_lds(BufRsrc r, uint8_t* lds, uint32_t voff, uint32_t soff) {
+  static_assert(BYTES == 4 || BYTES == 16, "LDS DMA of 4 or 16 bytes per lane");
+  auto* l = (__attribute__((address_space(3))) void*)lds;
+  if constexpr (BYTES == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, voff, soff, 0, 0);
+  else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 4, voff, soff, 0, 0);
+}
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima 7, 15) as a real
+// instruction, so the compiler's own wait insertion counts it
+__device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Transposed LDS read (gfx950 ds_read_b64_tr_b16).  Within each 16-lane
 // group, lane j supplies the address of 4 consecutive bf16 M[j][0..3]; lane i
 // receives M[4r + i/4][i%4] for r = 0..3.  With lane j pointing at row
@@ -74,6 +90,34 @@ __device__ __forceinline__ u32x2 lds_tr16(const uint8_t* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)lp));
 }
 __device__ __forceinline__ u32x4 cat_tr(u32x2 a, u32x2 b) { return u32x4{a[0], a[1], b[0], b[1]}; }
+
+// ds_read_b64_tr_b8: within a 16-lane group, lane i receives byte i % 8 of
+// the 8-byte chunks addressed by lanes 2r + i / 8, r = 0..7.  With lane j
+// addressing token row t0 + j / 2 at byte column c0 + 8 (j % 2), lane i gets
+// column c0 + i of tokens t0 .. t0 + 7, one token per byte.
+__device__ __forceinline__ u32x2 lds_tr8(const uint8_t* p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(3))) v2i lds_v2i;
+  const lds_v2i* lp = (const lds_v2i*)(__attribute__((address_space(3))) const uint8_t*)(p);
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)lp));
+}
+
+// e4m3 x e4m3, K = 128, with E8M0 block scales: the K-block b (K indices
+// 32b .. 32b+31) of row i of A is scaled by 2^(byte - 127) of lane 16b + i's
+// sa, and of column j of B by lane 16b + j's sb (byte 0 of each).  A lane
+// (row i, group g) supplies K indices 16g .. 16g+15 (bytes 0-15) and
+// 64 + 16g .. 64 + 16g + 15 (bytes 16-31), so block b covers the low halves
+// of groups 2b, 2b+1 (b < 2) or the high halves of groups 2b-4, 2b-3.
+__device__ __forceinline__ f32x4 mfma_fp8_scaled(i32x8 a, i32x8 b, f32x4 c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+// Four floats -> four e4m3 bytes (RNE).  The conversion does not saturate
+// (out-of-range values become NaN): callers clamp to +-448 first.
+__device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+}
 
 // two e4m3 bytes (low or high half of w) -> two bf16, exact (scale 1.0)
 template <bool HI>

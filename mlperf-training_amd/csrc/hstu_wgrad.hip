@@ -70,16 +70,6 @@ struct WCfg {
 constexpr int kWLds = WCfg<false>::LDS;
 static_assert(WCfg<true>::LDS == kWLds, "one LDS size");
 
-// ds_read_b64_tr_b8: within a 16-lane group, lane i receives byte i % 8 of
-// the 8-byte chunks addressed by lanes 2r + i / 8, r = 0..7.  With lane j
-// addressing token row t0 + j / 2 at byte column c0 + 8 (j % 2), lane i gets
-// column c0 + i of tokens t0 .. t0 + 7, one token per byte.
-__device__ __forceinline__ u32x2 lds_tr8(const uint8_t* p) {
-  typedef int v2i __attribute__((ext_vector_type(2)));
-  typedef __attribute__((address_space(3))) v2i lds_v2i;
-  const lds_v2i* lp = (const lds_v2i*)(__attribute__((address_space(3))) const uint8_t*)(p);
-  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)lp));
-}
 
 struct WgradParams {
   const uint8_t* A;

@@ -55,6 +55,10 @@ EXPORTED_SYMBOLS = (
     "hstu_wgrad_workspace_bytes",
     "hstu_wgrad",
     "hstu_attn_fwd_noalloc",
+    "hstu_attn_bwd_fp8",
+    "hstu_attn_bwd_fp8_workspace_bytes",
+    "hstu_attn_bwd_fp8_dkdv",
+    "hstu_attn_bwd_fp8_dq",
 )
 
 
@@ -94,6 +98,14 @@ _SIGNATURES = {
          _i32, _f32, _vp, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp],
     ),
     "hstu_attn_bwd_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i32, _i32, _i32]),
+    "hstu_attn_bwd_fp8_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32, _i32, _i32]),
+    "hstu_attn_bwd_fp8": (
+        _i32,
+        [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
+         _f32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp],
+    ),
+    "hstu_attn_bwd_fp8_dkdv": "hstu_attn_bwd_fp8",
+    "hstu_attn_bwd_fp8_dq": "hstu_attn_bwd_fp8",
     "hstu_attn_bwd_dkdv": None,
     "hstu_attn_bwd_dq": None,
     "hstu_fp8_gemm_rowcol": (
@@ -175,7 +187,10 @@ def fn(name: str):
     f = _bound.get(name)
     if f is None:
         f = getattr(load_library(), name)
-        res, args = _SIGNATURES[name] or _SIGNATURES["hstu_attn_bwd"]
+        sig = _SIGNATURES[name] or _SIGNATURES["hstu_attn_bwd"]
+        if isinstance(sig, str):  # same argument list as another entry point
+            sig = _SIGNATURES[sig]
+        res, args = sig
         f.restype = res
         f.argtypes = args
         _bound[name] = f

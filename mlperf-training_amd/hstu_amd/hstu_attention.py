@@ -240,6 +240,61 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
             dst.copy_(src)
 
 
+def _launch_bwd_fp8(dout8, e8, q, k, v, dq, dk, dv, seq_offsets, N, alpha, q_scale, k_scale, v_scale,
+                    attn_bias, dbias) -> None:
+    """The full-FP8 backward (``hstu_attn_bwd_fp8``) on an e4m3 dO with its
+    block scales (``hstu_do_fp8.quantize_do_e4m3_blk``'s output)."""
+    T, H, D = q.shape
+    q, k, v = _row_view(q), _row_view(k), _row_view(v)
+    if dout8.dtype != _E4M3 or e8.dtype != torch.uint8 or tuple(e8.shape) != (T, H):
+        raise ValueError("expected dO8 e4m3 [T, H, D] and E8 uint8 [T, H]")
+    dout8 = _row_view(dout8)
+    e8 = e8.contiguous()
+    qs, srs, shs = _scale_tensor(q_scale, T, H, q.device)
+    ks, srs2, shs2 = _scale_tensor(k_scale, T, H, q.device)
+    vs, srs3, shs3 = _scale_tensor(v_scale, T, H, q.device)
+    if not (srs == srs2 == srs3 and shs == shs2 == shs3):
+        raise ValueError("q/k/v scales must share one layout (all scalars or all [T, H])")
+    targets = []
+    for g in (dq, dk, dv):
+        if g.dtype != torch.bfloat16:
+            raise ValueError("gradients are bf16")
+        ok = (g.stride(2) == 1 and g.stride(1) == D and (T <= 1 or g.stride(0) >= H * D)
+              and (g.stride(0) * 2) % 16 == 0 and g.data_ptr() % 16 == 0)
+        targets.append(g if ok else torch.empty((T, H, D), dtype=torch.bfloat16, device=q.device))
+    offs = _seq_offsets_i64(seq_offsets)
+    bias, R = _bias_args(attn_bias, H)
+    if dbias is not None:
+        if bias is None or dbias.shape != bias.shape or dbias.dtype != torch.float32 or not dbias.is_contiguous():
+            raise ValueError("dbias must be a contiguous fp32 tensor shaped like attn_bias")
+    B = offs.numel() - 1
+    ws = _workspace(_lib.fn("hstu_attn_bwd_fp8_workspace_bytes")(T, B, H, D, int(N), R), q.device)
+    st = _lib.fn("hstu_attn_bwd_fp8")(
+        dout8.data_ptr(), e8.data_ptr(), _row_stride(dout8),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _row_stride(q), _row_stride(k), _row_stride(v),
+        _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs), srs, shs,
+        offs.data_ptr(), B, H, D, int(N), float(alpha), _lib.ptr(bias), R,
+        targets[0].data_ptr(), targets[1].data_ptr(), targets[2].data_ptr(),
+        _row_stride(targets[0]), _row_stride(targets[1]), _row_stride(targets[2]),
+        _lib.ptr(dbias), ws.data_ptr(), ws.numel(), T, _stream(q.device))
+    _lib.check(st, "hstu_attn_bwd_fp8")
+    for dst, src in zip((dq, dk, dv), targets):
+        if dst is not src:
+            dst.copy_(src)
+
+
+def full_fp8_bwd_reason(q: torch.Tensor, num_targets, max_attn_len: int, contextual_seq_len: int) -> Optional[str]:
+    """None when the full-FP8 backward kernels serve this call (e4m3 inputs,
+    D = 128, the causal mask), else why not."""
+    if not _is_fp8(q):
+        return "inputs are not e4m3"
+    if q.shape[2] != 128:
+        return f"head dim {q.shape[2]}"
+    if num_targets is not None or max_attn_len > 0 or contextual_seq_len > 0:
+        return "num_targets / max_attn_len / contextual_seq_len masks"
+    return None
+
+
 # ---------------------------------------------------------------------------
 # custom ops (same argument lists and mutation contract as the reference)
 # ---------------------------------------------------------------------------
@@ -289,6 +344,7 @@ def _op_bwd(
     v_scale: Optional[torch.Tensor],
     attn_bias: Optional[torch.Tensor],
     dbias: Optional[torch.Tensor],
+    full_fp8: bool = False,
 ) -> None:
     if dout.shape[0] == 0:
         dq.zero_()
@@ -297,13 +353,21 @@ def _op_bwd(
         if dbias is not None:
             dbias.zero_()
         return
+    if full_fp8:
+        from . import hstu_do_fp8
+
+        # the reference's full-FP8 backward: dO quantized in pow2 blocks, then five e4m3 products
+        dout8, e8 = hstu_do_fp8.quantize_do_e4m3_blk(dout, seq_offsets, int(N))
+        _launch_bwd_fp8(dout8, e8, q, k, v, dq, dk, dv, seq_offsets, N, alpha, q_scale, k_scale, v_scale,
+                        attn_bias, dbias)
+        return
     _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, max_attn_len,
                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias)
 
 
 @_op_bwd.register_fake
 def _op_bwd_fake(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, max_attn_len,
-                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias):
+                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias, full_fp8=False):
     return None
 
 
@@ -375,33 +439,44 @@ def triton_hstu_attention_bwd(
     *,
     attn_bias: Optional[torch.Tensor] = None,
     dbias: Optional[torch.Tensor] = None,
+    full_fp8: Optional[bool] = None,
 ) -> None:
     """Backward op (``triton_hstu_attention.py:3298-3319``): writes dq, dk, dv
     in place (they may be strided views of a fused gradient buffer); an empty
     batch zeroes them.  With ``attn_bias``, ``dbias`` (fp32, same shape, if
-    given) is overwritten with the bias gradient."""
+    given) is overwritten with the bias gradient.
+
+    ``full_fp8`` (None: the process default, ``DLRM_HSTU_FP8_BWD_FULL``): for
+    e4m3 inputs, the reference's full-FP8 backward -- dO quantized to e4m3 in
+    power-of-two (sequence, head, 32-token) blocks, P and dS cast to e4m3,
+    all five products on the e4m3 MFMA (``hstu_attn_bwd_fp8``).  A call it
+    cannot serve (the targets / window / contextual masks) runs the e4m3-input
+    backward on the block-quantized dO instead, with the reason logged once."""
     del sort_by_length_indices, enable_tma
     reason = unsupported_shape_reason(q, k, v, num_softmax_heads)
     if reason is not None:
         raise NotImplementedError(f"HIP HSTU attention backward: {reason}")
     fp8 = _is_fp8(q)
+    use_full = False
     if fp8 and dout.numel() > 0:
         from . import hstu_do_fp8
 
-        if hstu_do_fp8.bwd_full_fp8_enabled():
-            # DLRM_HSTU_FP8_BWD_FULL: the backward runs on the block-quantized dO
-            # (quantize_do_e4m3_blk; the reference undoes the scales in its MFMAs)
+        if hstu_do_fp8.bwd_full_fp8_enabled() if full_fp8 is None else full_fp8:
+            why = full_fp8_bwd_reason(q, num_targets, int(max_attn_len), int(contextual_seq_len))
             H, D = dout.shape[1], dout.shape[2]
-            if D in (64, 128) and H * D in (128, 256, 512):
+            if why is None:
+                use_full = True
+            elif D in (64, 128) and H * D in (128, 256, 512):
+                _log_once(f"full-FP8 backward: {why}; the e4m3 backward runs on the block-quantized dO")
                 dout = hstu_do_fp8.block_quantized_do(dout, seq_offsets, int(N))
             else:
-                _log_once(f"full-FP8 dO quantizer: H*D = {H * D} not served, bf16 dO kept")
+                _log_once(f"full-FP8 backward: {why}; dO quantizer: H*D = {H * D} not served, bf16 dO kept")
     _op_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, int(N), float(alpha), int(max_attn_len),
             int(contextual_seq_len),
             _scale_or_none(q_scale, q) if fp8 else None,
             _scale_or_none(k_scale, q) if fp8 else None,
             _scale_or_none(v_scale, q) if fp8 else None,
-            attn_bias, dbias)
+            attn_bias, dbias, use_full)
 
 
 # ---------------------------------------------------------------------------
