@@ -271,6 +271,23 @@ int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void* W, int64_
                   int silu_begin, int silu_end, hipStream_t stream);
 
 /*
+ * bf16 projection GEMM on the same tile kernel: C[m][n] = epilogue(sum_k
+ * A[m][k] W[n][k]), A [M, K] and W [N, K] row-major bf16 (lda, ldw, ldc, ldr
+ * in elements), fp32 accumulate, epilogue as hstu_fp8_gemm without scales
+ * (+ bias[n], SiLU on [silu_begin, silu_end), + residual), bf16 C.
+ * N % 128 == 0, K % 64 == 0, 16-byte aligned A / W rows.  Each output row
+ * depends on its own A row only (no M-dependent split), so a row's result
+ * does not change with the batch it is computed in.
+ * Replaces: the layer's bf16 GEMMs on the host BLAS -- the projection dgrads
+ *           torch.mm(dout, output_weight.t()) (ops/triton/triton_hstu_linear.py:5588)
+ *           and the UVQK dgrad, and the bf16 UVQK projection
+ *           maybe_triton_addmm_fwd -> torch.addmm on ROCm (ops/triton/triton_addmm.py:1756-1767).
+ */
+int hstu_bf16_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const void* bias, const void* residual,
+                   int64_t ldr, void* C, int64_t ldc, int M, int N, int K, int silu_begin, int silu_end,
+                   hipStream_t stream);
+
+/*
  * One-pass FP8 cast with the input's amax: out[i] = fp8(clamp(x[i] *
  * inv_scale[0], +-limit)) (out_dtype e4m3 or e5m2, round to nearest even)
  * over n contiguous bf16 / fp32 elements (n % 32 == 0, 16-byte aligned), and

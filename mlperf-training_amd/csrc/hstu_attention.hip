@@ -1594,24 +1594,22 @@ struct F8Bwd {
   // ds_read_b128 and the row groups 8 and 32 apart of a ds_read_b64_tr_b8
   // over distinct banks; it is constant under r -> r + 16 (bits 1-3 and 5).
   __host__ __device__ static constexpr int kv_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 5) & 1) << 2); }
-  __host__ __device__ static constexpr int kv_at(int r, int c) { return r * 128 + 16 * (c ^ kv_swz(r)); }
   static constexpr int Q_OFF = 0;
   static constexpr int DO_OFF = Q_OFF + BM * 128;
   static constexpr int SQ_OFF = DO_OFF + BM * 128;  // 128 fp32 query scales
   static constexpr int B_OFF = SQ_OFF + BM * 4;     // 256 fp32: pre-scaled bias of offsets m0-n0-127 ..
   static constexpr int STAGE = B_OFF + 256 * 4;
   static constexpr int LDS = 2 * STAGE;
-  // dQ: K tile [key][d] and dS tile [key][query], 128-byte rows at a pitch of
-  // 160 (== 32 mod 64: 16-row ds_read_b128 reads are conflict-free); rows of
-  // odd 16-row groups shifted by 16 bytes so the transposed reads of lane
-  // groups 16 rows apart use distinct banks.
-  static constexpr int PT = 160;
-  __host__ __device__ static constexpr int row16(int r) { return r * PT + 16 * ((r >> 4) & 1); }
-  static constexpr int TILE = BN * BM;      // one stored e4m3 dS tile (16 KiB)
-  // dQ: 4 waves, 32 queries each
+  static constexpr int TILE = BN * BM;  // one stored e4m3 dS tile (16 KiB)
+  // dQ: K tile [key][d] and dS tile [key][query], unpadded 128-byte rows,
+  // data chunk c of row r at slot c ^ q_swz(r).  The transposed reads take
+  // rows 8 g + (li >> 1) + 32 m (lane group g, m = 0..3), on which q_swz does
+  // not depend on m; it spreads the two lane groups of each half-wave, the
+  // 16-row 4-byte dS stores and the 2-row 16-byte K stores over all banks.
+  __host__ __device__ static constexpr int q_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2); }
   static constexpr int QK_OFF = 0;
-  static constexpr int QDS_OFF = QK_OFF + BN * PT + 16;
-  static constexpr int QHIST_OFF = QDS_OFF + BN * PT + 16;
+  static constexpr int QDS_OFF = QK_OFF + BN * 128;
+  static constexpr int QHIST_OFF = QDS_OFF + BN * 128;
   static int dq_lds(bool bias, int R) { return QHIST_OFF + (bias ? R * 4 : 0); }
 };
 
@@ -1924,14 +1922,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + kThreads * i, row = c >> 3, ch = c & 7;
-      *(u32x4*)(smem + C::QK_OFF + C::row16(row) + 16 * ch) = kc[i];
+      *(u32x4*)(smem + C::QK_OFF + row * 128 + 16 * (ch ^ C::q_swz(row))) = kc[i];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int w = 2 * wave + (j >> 1), hf = j & 1;
-      uint8_t* row = smem + C::QDS_OFF + C::row16(16 * w + li) + 64 * hf + 4 * g;
+      const int r = 16 * w + li;
+      uint8_t* row = smem + C::QDS_OFF + r * 128 + 4 * g;
 #pragma unroll
-      for (int qs = 0; qs < 4; ++qs) *(uint32_t*)(row + 16 * qs) = dsp[j][qs];
+      for (int qs = 0; qs < 4; ++qs) *(uint32_t*)(row + 16 * ((4 * hf + qs) ^ C::q_swz(r))) = dsp[j][qs];
     }
   };
   float dclamp = 0.f;
@@ -1981,13 +1980,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
     }
   };
 
-  // operand reads: dS^T columns (queries c0 + li) and K^T rows (d c0 + li) of
-  // keys 16 g .. 16 g + 15 and 64 + 16 g .. +15
-  const int trk = C::row16(16 * g + (li >> 1)) + 8 * (li & 1);
-  auto frag = [&](const uint8_t* t) {
-    // rows +8, +64, +72 stay in the same 16-row parity: one swizzle offset
-    const u32x2 r0 = lds_tr8(t), r1 = lds_tr8(t + 8 * C::PT);
-    const u32x2 r2 = lds_tr8(t + 64 * C::PT), r3 = lds_tr8(t + 72 * C::PT);
+  // operand reads: dS^T columns (queries 16 chunk + li) and K^T rows (d =
+  // 16 chunk + li) over the keys 8 g + 32 m .. + 7, m = 0..3 (the contraction
+  // order is the same for both operands)
+  const int tr_row = 8 * g + (li >> 1);
+  const int trk = tr_row * 128 + 8 * (li & 1), trx = 16 * C::q_swz(tr_row);
+  auto frag = [&](const uint8_t* tile, int chunk) {
+    const uint8_t* t = tile + trk + ((16 * chunk) ^ trx);
+    const u32x2 r0 = lds_tr8(t), r1 = lds_tr8(t + 32 * 128);
+    const u32x2 r2 = lds_tr8(t + 64 * 128), r3 = lds_tr8(t + 96 * 128);
     i32x8 f;
     f[0] = (int)r0[0]; f[1] = (int)r0[1]; f[2] = (int)r1[0]; f[3] = (int)r1[1];
     f[4] = (int)r2[0]; f[5] = (int)r2[1]; f[6] = (int)r3[0]; f[7] = (int)r3[1];
@@ -2006,10 +2007,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
     if (kb + 1 < nsteps) load(kb + 1);
     i32x8 bq[2];
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) bq[qs] = frag(smem + C::QDS_OFF + trk + 32 * wave + 16 * qs);
+    for (int qs = 0; qs < 2; ++qs) bq[qs] = frag(smem + C::QDS_OFF, 2 * wave + qs);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
-      const i32x8 ak = frag(smem + C::QK_OFF + trk + 16 * dt);
+      const i32x8 ak = frag(smem + C::QK_OFF, dt);
       acc[dt][0] = mfma_fp8(ak, bq[0], acc[dt][0]);
       acc[dt][1] = mfma_fp8(ak, bq[1], acc[dt][1]);
     }

@@ -97,8 +97,14 @@ struct RegTile {
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
 
-// A_BF8: A holds e5m2 (the MFMA's B operand format 1, bf8).
-template <bool E4M3_OUT, bool RESID, bool A_BF8>
+// Operand formats of the tile kernel: A and W e4m3; A e5m2 (the MFMA's B
+// operand format 1, bf8) against e4m3 W; or A and W bf16, unscaled (a k-step
+// of 128 bytes is then 64 elements, two v_mfma_f32_16x16x32_bf16 per operand
+// pair: chunk g of a lane is elements 8g .. 8g+7 of the first 32, chunk g+4
+// the same of the second 32).
+enum GemmFmt { kE4M3 = 0, kE5M2A = 1, kBF16 = 2 };
+
+template <bool E4M3_OUT, bool RESID, int FMT>
 __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   // XCD-contiguous tile order: workgroup i runs on XCD i % 8.
@@ -134,12 +140,13 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
 #pragma unroll
   for (int ms = 0; ms < 4; ++ms) {
     const int m = min(m0 + wm + 16 * ms + li, p.M - 1);
-    sa[ms] = p.a_mode ? p.a_scale[m] : p.a_scale[0];
+    sa[ms] = FMT == kBF16 ? 1.f : p.a_mode ? p.a_scale[m] : p.a_scale[0];
   }
 #pragma unroll
   for (int ns = 0; ns < 4; ++ns) {
     const int n = n0 + wn + 16 * ns + 4 * g;
-    if (p.w_mode) sw[ns] = *(const f32x4*)(p.w_scale + n);
+    if (FMT == kBF16) sw[ns] = f32x4{1.f, 1.f, 1.f, 1.f};
+    else if (p.w_mode) sw[ns] = *(const f32x4*)(p.w_scale + n);
     else sw[ns] = f32x4{p.w_scale[0], p.w_scale[0], p.w_scale[0], p.w_scale[0]};
     bias[ns] = p.bias ? *(const u32x2*)(p.bias + n) : u32x2{0u, 0u};
   }
@@ -185,10 +192,17 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
       const i32x8 aop = cat8(lds_ld128(r), lds_ld128(r + 64));
 #pragma unroll
       for (int ms = 0; ms < 4; ++ms) {
-        if constexpr (A_BF8)  // W rows e4m3 (format 0), A rows e5m2 (format 1)
+        if constexpr (FMT == kE5M2A) {  // W rows e4m3 (format 0), A rows e5m2 (format 1)
           acc[ns][ms] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(aop, bop[ms], acc[ns][ms], 0, 1, 0, 0, 0, 0);
-        else
+        } else if constexpr (FMT == kBF16) {
+          const u32x4 alo = {(uint32_t)aop[0], (uint32_t)aop[1], (uint32_t)aop[2], (uint32_t)aop[3]};
+          const u32x4 ahi = {(uint32_t)aop[4], (uint32_t)aop[5], (uint32_t)aop[6], (uint32_t)aop[7]};
+          const u32x4 blo = {(uint32_t)bop[ms][0], (uint32_t)bop[ms][1], (uint32_t)bop[ms][2], (uint32_t)bop[ms][3]};
+          const u32x4 bhi = {(uint32_t)bop[ms][4], (uint32_t)bop[ms][5], (uint32_t)bop[ms][6], (uint32_t)bop[ms][7]};
+          acc[ns][ms] = mfma_bf16(ahi, bhi, mfma_bf16(alo, blo, acc[ns][ms]));
+        } else {
           acc[ns][ms] = mfma_fp8(aop, bop[ms], acc[ns][ms]);
+        }
       }
     }
 #if HSTU_GEMM_REGSTAGE
@@ -776,14 +790,52 @@ extern "C" int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void
   void (*kern)(GemmParams);
   if (a_dtype == HSTU_DTYPE_FP8_E5M2) {
     if (out_dtype != HSTU_DTYPE_BF16 || residual) return HSTU_E_UNSUPPORTED;  // the dgrad form only
-    kern = fp8_gemm_kernel<false, false, true>;
+    kern = fp8_gemm_kernel<false, false, kE5M2A>;
   } else if (out_dtype == HSTU_DTYPE_FP8_E4M3) {
-    kern = residual ? fp8_gemm_kernel<true, true, false> : fp8_gemm_kernel<true, false, false>;
+    kern = residual ? fp8_gemm_kernel<true, true, kE4M3> : fp8_gemm_kernel<true, false, kE4M3>;
   } else {
-    kern = residual ? fp8_gemm_kernel<false, true, false> : fp8_gemm_kernel<false, false, false>;
+    kern = residual ? fp8_gemm_kernel<false, true, kE4M3> : fp8_gemm_kernel<false, false, kE4M3>;
   }
   hipError_t e = set_gemm_lds((const void*)kern);
   if (e != hipSuccess) return (int)e;
+  void* args[] = {&p};
+  return (int)hipLaunchKernel((const void*)kern, dim3(grid), dim3(kThreads), args, (size_t)kGemmLds, stream);
+}
+
+extern "C" int hstu_bf16_gemm(const void* A, int64_t lda, const void* W, int64_t ldw, const void* bias,
+                              const void* residual, int64_t ldr, void* C, int64_t ldc, int M, int N, int K,
+                              int silu_begin, int silu_end, hipStream_t stream) {
+  // the tile kernel on bf16 rows: k counted in bytes (128-byte k-steps)
+  if (M < 0 || N <= 0 || K <= 0 || N % kBN != 0 || (2 * K) % kBK != 0 || !A || !W || !C) return HSTU_E_BAD_ARG;
+  if (lda < K || ldw < K || ldc < N || (residual && ldr < N)) return HSTU_E_BAD_ARG;
+  if (lda % 8 != 0 || ldw % 8 != 0 || ldc % 4 != 0 || (residual && ldr % 4 != 0) ||
+      ((uintptr_t)A | (uintptr_t)W) % 16 != 0 || (uintptr_t)C % 8 != 0 || (uintptr_t)residual % 8 != 0 ||
+      (uintptr_t)bias % 8 != 0)
+    return HSTU_E_UNSUPPORTED;
+  if ((int64_t)(kBM - 1) * 2 * lda + 2 * K > 0xffffffffLL || (int64_t)(kBN - 1) * 2 * ldw + 2 * K > 0xffffffffLL)
+    return HSTU_E_UNSUPPORTED;
+  if (M == 0) return 0;
+  GemmParams p{};
+  p.A = (const uint8_t*)A;
+  p.W = (const uint8_t*)W;
+  p.lda = 2 * lda;
+  p.ldw = 2 * ldw;
+  p.bias = (const uint16_t*)bias;
+  p.resid = (const uint16_t*)residual;
+  p.ldr = ldr;
+  p.C = C;
+  p.ldc = ldc;
+  p.M = M;
+  p.N = N;
+  p.K = 2 * K;
+  p.silu_begin = silu_begin;
+  p.silu_end = silu_end;
+  p.tiles_m = (M + kBM - 1) / kBM;
+  p.tiles_n = N / kBN;
+  void (*kern)(GemmParams) = residual ? fp8_gemm_kernel<false, true, kBF16> : fp8_gemm_kernel<false, false, kBF16>;
+  hipError_t e = set_gemm_lds((const void*)kern);
+  if (e != hipSuccess) return (int)e;
+  const int grid = (p.tiles_m * p.tiles_n + 7) / 8 * 8;
   void* args[] = {&p};
   return (int)hipLaunchKernel((const void*)kern, dim3(grid), dim3(kThreads), args, (size_t)kGemmLds, stream);
 }

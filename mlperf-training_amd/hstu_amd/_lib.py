@@ -47,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "hstu_quantize_do_e4m3_blk",
     "hstu_dequantize_do_e4m3_blk",
     "hstu_fp8_gemm",
+    "hstu_bf16_gemm",
     "hstu_cast_fp8_amax_partials",
     "hstu_cast_fp8_amax",
     "hstu_cast_fp8_amax_colsum_workspace_bytes",
@@ -118,6 +119,7 @@ _SIGNATURES = {
         [_i32, _vp, _i64, _vp, _i64, _vp, _i32, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i32, _vp,
          _i32, _i32, _i32, _i32, _i32, _vp],
     ),
+    "hstu_bf16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
     "hstu_cast_fp8_amax_partials": (_i64, [_i64]),
     "hstu_cast_fp8_amax": (_i32, [_i32, _vp, _i64, _vp, _i32, _f32, _vp, _vp, _i64, _vp]),
     "hstu_cast_fp8_amax_colsum_workspace_bytes": (_i64, [_i64, _i64]),

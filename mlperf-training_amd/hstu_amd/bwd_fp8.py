@@ -55,7 +55,9 @@ class Fp8BackwardConfig:
     enabled: the output-projection e5m2 dgrad (``DLRM_HSTU_FP8_BWD``);
     uvqk: the UVQK e5m2 dgrad (``DLRM_HSTU_FP8_BWD_UVQK``, e5m2 only);
     out_wgrad_fp8 / uvqk_wgrad_fp8t: the FP8 weight gradients;
-    margin, warmup_calls, refresh_calls, grad_format: the delayed-scale policy.
+    margin, warmup_calls, refresh_calls, grad_format: the delayed-scale policy;
+    attn_full_fp8: the attention's full-FP8 backward (``DLRM_HSTU_FP8_BWD_FULL``;
+    None: the attention op's process default).
     """
 
     enabled: bool = False
@@ -66,6 +68,7 @@ class Fp8BackwardConfig:
     warmup_calls: int = 4
     refresh_calls: int = 200
     grad_format: str = "e5m2"
+    attn_full_fp8: Optional[bool] = None
 
     def __post_init__(self):
         if self.grad_format not in ("e5m2", "e4m3"):
@@ -112,6 +115,11 @@ def set_default_config(cfg: Optional[Fp8BackwardConfig]) -> None:
     """Replace the process default (None: read the environment again on next use)."""
     global _default
     _default = cfg
+
+
+def resolve(config: Optional[Fp8BackwardConfig]) -> Fp8BackwardConfig:
+    """``config``, or the process default when None."""
+    return default_config() if config is None else config
 
 
 def _cfg(config: Optional[Fp8BackwardConfig]) -> Fp8BackwardConfig:

@@ -236,6 +236,56 @@ def fp8_gemm(a8: torch.Tensor, a_scale: torch.Tensor, weight: Weight, *, bias: O
     return out
 
 
+def bf16_gemm(a: torch.Tensor, w_nk: torch.Tensor, *, bias: Optional[torch.Tensor] = None,
+              residual: Optional[torch.Tensor] = None, silu_cols: Optional[Tuple[int, int]] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16 C = epilogue(a @ w_nk^T) on the HIP tile kernel (``hstu_bf16_gemm``):
+    a [M, K], w_nk [N, K] (the weight with the contraction index contiguous),
+    optional bf16 bias [N], residual [M, N], SiLU on a column range.  ``out``:
+    an [M, N] bf16 destination with unit column stride (e.g. columns of a
+    wider buffer)."""
+    if a.dtype != torch.bfloat16 or w_nk.dtype != torch.bfloat16:
+        raise TypeError(f"expected bf16 operands, got {a.dtype} and {w_nk.dtype}")
+    if a.stride(-1) != 1 or a.stride(0) % 8 != 0 or a.data_ptr() % 16 != 0:
+        a = a.contiguous()
+    if w_nk.stride(-1) != 1 or w_nk.stride(0) % 8 != 0 or w_nk.data_ptr() % 16 != 0:
+        w_nk = w_nk.contiguous()
+    M, K = a.shape
+    N = w_nk.shape[0]
+    if w_nk.shape[1] != K:
+        raise ValueError(f"K mismatch: a {tuple(a.shape)} w {tuple(w_nk.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    elif out.shape != (M, N) or out.dtype != torch.bfloat16 or out.stride(1) != 1:
+        raise ValueError("out must be a bf16 [M, N] view with unit column stride")
+    if M == 0:
+        return out
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    r = None if residual is None else residual.to(torch.bfloat16).contiguous()
+    c0, c1 = silu_cols if silu_cols is not None else (0, 0)
+    st = _lib.fn("hstu_bf16_gemm")(a.data_ptr(), a.stride(0), w_nk.data_ptr(), w_nk.stride(0), _lib.ptr(b),
+                                   _lib.ptr(r), N if r is not None else 0, out.data_ptr(), out.stride(0), M, N, K,
+                                   int(c0), int(c1), _stream(a))
+    _lib.check(st, "hstu_bf16_gemm")
+    return out
+
+
+def proj_mm(a: torch.Tensor, w_nk: torch.Tensor, *, bias: Optional[torch.Tensor] = None,
+            residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a @ w_nk^T (+ bias) (+ residual) for the layer's projections: the HIP
+    bf16 GEMM for bf16 operands at the shapes it serves (N % 128 == 0, K % 64
+    == 0), else the device BLAS (other dtypes: fp32 callers of the generic ops)."""
+    N, K = w_nk.shape
+    if a.dtype == torch.bfloat16 and a.is_cuda and N % 128 == 0 and K % 64 == 0:
+        return bf16_gemm(a, w_nk.to(torch.bfloat16), bias=bias, residual=residual)
+    out = a @ w_nk.to(a.dtype).t()
+    if bias is not None:
+        out = out + bias.to(out.dtype)
+    if residual is not None:
+        out = out + residual.to(out.dtype)
+    return out
+
+
 def scaled_addmm_fp8_preq(activation_fp8: torch.Tensor, scale_a: torch.Tensor, weight: Weight,
                           bias_or_residual: Optional[torch.Tensor], *, out_dtype: torch.dtype = torch.bfloat16,
                           silu_cols: Optional[Tuple[int, int]] = None) -> torch.Tensor:

@@ -369,7 +369,7 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
                                           mask16=dropout_mask16)
             if fp8_output_scale is not None and not ready:
                 _fp8.calibrate_scale_buffer(fp8_output_scale, y)
-            out = torch.addmm(x, y, output_weight.to(y.dtype))
+            out = _fp8.proj_mm(y, output_weight.to(y.dtype).t(), residual=x)
         saved = [attn, u, norm_weight, norm_bias, mean, rstd, output_weight]
         if not recompute_y_in_backward:
             saved.append(y)
@@ -407,7 +407,7 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         cfg = ctx.fp8_backward
         q = (bwd_fp8.output_projection_dgrad(dout, output_weight, return_quantized=True, config=cfg)
              if bwd_fp8.enabled(cfg) else None)
-        dy = q[0] if q is not None else torch.mm(dout, output_weight.to(dout.dtype).t())
+        dy = q[0] if q is not None else _fp8.proj_mm(dout, output_weight)
         # FP8 weight gradient (DLRM_HSTU_FP8_BWD_OUT_WGRAD=1) from the forward's
         # e4m3 y and the dgrad's e5m2 dout: the bf16 y is then not recomputed
         fp8_w = y8 is not None and q is not None

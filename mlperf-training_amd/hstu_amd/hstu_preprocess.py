@@ -88,7 +88,7 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
                                         "none", 0, False, 1.0)
             if fp8_input_scale is not None:
                 _fp8.calibrate_scale_buffer(fp8_input_scale, xn)
-            uvqk = torch.addmm(uvqk_bias.to(x.dtype), xn, uvqk_weight.to(x.dtype))
+            uvqk = _fp8.proj_mm(xn, uvqk_weight.to(x.dtype).t(), bias=uvqk_bias)
             u_pre = uvqk[:, :nu]
             u = u_pre if defer_silu else F.silu(u_pre)
             vqk = uvqk[:, nu:]
@@ -150,7 +150,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
             dbias = torch.empty(attn_bias.shape, dtype=torch.float32, device=x.device)
         triton_hstu_attention_bwd(dattn.contiguous().view(T, H, Dv), q, k, v, dq, dk, dv, seq_offsets, num_targets,
                                   N, alpha, max_attn_len, ctx_len, None, False, 0, qkv_scale, qkv_scale, qkv_scale,
-                                  attn_bias=attn_bias, dbias=dbias)
+                                  attn_bias=attn_bias, dbias=dbias,
+                                  full_fp8=bwd_fp8.resolve(ctx.fp8_backward).attn_full_fp8)
         # projection backward on the recomputed bf16 LN(x): the FP8 dgrad arm
         # (DLRM_HSTU_FP8_BWD_UVQK=1, after its warm-up), else bf16 GEMMs
         def recompute_normed_x() -> torch.Tensor:
@@ -165,7 +166,7 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
             xn = recompute_normed_x()
             # the wgrad kernel also sums d(uvqk)'s columns: the bias gradient
             d_w, d_b = token_wgrad(xn, duvqk, with_colsum=True)
-            dxn = torch.mm(duvqk, W.to(duvqk.dtype).t())
+            dxn = _fp8.proj_mm(duvqk, W)
         d_w, d_b = d_w.to(W.dtype), d_b.to(W.dtype)
         dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False)
         return (dx, dnw.to(nw.dtype), dnb.to(nb.dtype), None, None, None, None, d_w, d_b, None, None, None, None,

@@ -80,6 +80,7 @@ def full_fp8_bwd(
     e8: torch.Tensor,
     attn_bias: Optional[torch.Tensor] = None,
     quantize: bool = True,
+    max_scales: Optional[Tuple[float, float]] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """(dq, dk, dv, dbias) of the causal attention with the full-FP8 casts.
 
@@ -87,15 +88,18 @@ def full_fp8_bwd(
     (the dequantized value is q8 * sq); dout8 [T, H, D] with e8 uint8 [T, H]
     (dO = dout8 * 2^(e8 - 127)).  Gradients are with respect to the
     dequantized q, k, v and are float64.  ``quantize=False`` skips every cast
-    (the exact backward of the same inputs)."""
+    (the exact backward of the same inputs).  ``max_scales`` = (largest q
+    scale, largest k scale) of the whole batch when the rows given are a
+    sample of it (the normalisers come from the whole batch)."""
     T, H, D = q8.shape
     if dout8.dtype == torch.uint8:  # raw e4m3 bytes (the quantizer oracle's output)
         dout8 = dout8.view(torch.float8_e4m3fn)
     ssc, dsc = prescales(N) if quantize else (1.0, 1.0)
     cast = e4m3_sat if quantize else (lambda t: t)
     sq, sk, sv = (s.to(torch.float64).expand(T, H) if s.numel() == 1 else s.to(torch.float64) for s in (sq, sk, sv))
-    nq = pow2_norm(float(sq.abs().max())) if quantize else 1.0
-    nk = pow2_norm(float(sk.abs().max())) if quantize else 1.0
+    mq, mk = max_scales if max_scales is not None else (float(sq.abs().max()), float(sk.abs().max()))
+    nq = pow2_norm(mq) if quantize else 1.0
+    nk = pow2_norm(mk) if quantize else 1.0
     dq = torch.zeros(T, H, D, dtype=torch.float64)
     dk = torch.zeros(T, H, D, dtype=torch.float64)
     dv = torch.zeros(T, H, D, dtype=torch.float64)

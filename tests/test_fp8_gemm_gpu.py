@@ -192,3 +192,45 @@ def test_gemm_k512_both_kernels(hip_lib):
         got = out[:, :N].double().cpu()
         assert orc.rel_l2(ref, got) <= 4e-3, ldc
         assert not bool(out[:, N:].any())                              # nothing written past N
+
+
+@pytest.mark.parametrize("M,N,K,bias,resid,silu", [(1000, 512, 2048, False, False, False),
+                                                   (333, 1536, 512, False, False, False),
+                                                   (257, 2048, 512, True, False, True),
+                                                   (130, 512, 1536, False, True, False)])
+def test_bf16_gemm(hip_lib, M, N, K, bias, resid, silu):
+    """The bf16 mode of the tile kernel (``hstu_bf16_gemm``): against the
+    float64 product of the same bf16 operands with the same epilogue;
+    relative L2 <= 4e-3, max |err| <= 1e-2 * max |ref| (bf16 output)."""
+    fp8 = _fp8()
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    b = (0.1 * torch.randn(N, generator=g)).to(torch.bfloat16) if bias else None
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16) if resid else None
+    cols = (N // 4, N // 2) if silu else None
+    got = fp8.bf16_gemm(a.to(DEV), w.to(DEV), bias=None if b is None else b.to(DEV),
+                        residual=None if r is None else r.to(DEV), silu_cols=cols)
+    ref = a.double() @ w.double().t()
+    if b is not None:
+        ref = ref + b.double()
+    if cols is not None:
+        ref[:, cols[0]:cols[1]] = torch.nn.functional.silu(ref[:, cols[0]:cols[1]])
+    if r is not None:
+        ref = ref + r.double()
+    got = got.cpu().double()
+    assert orc.rel_l2(ref, got) <= 4e-3
+    assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2
+
+
+def test_bf16_gemm_rows_independent_of_batch(hip_lib):
+    """A row's result does not depend on the other rows of the batch: rows of
+    a 4096-row product equal the same rows computed in a 300-row batch."""
+    fp8 = _fp8()
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(512, 2048, generator=g) / 45).to(torch.bfloat16).to(DEV)
+    full = fp8.bf16_gemm(a, w)
+    part = fp8.bf16_gemm(a[1000:1300], w)
+    torch.cuda.synchronize()
+    assert torch.equal(full[1000:1300], part)

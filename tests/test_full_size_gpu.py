@@ -151,6 +151,182 @@ def test_config3_full_fp8_fwd_bwd(hip_lib):
     torch.testing.assert_close(full[4], first[4] + second[4], rtol=1e-4, atol=1e-6 * float(full[4].abs().max()))
 
 
+def test_config3_full_fp8_backward(hip_lib):
+    """Config 3 in full through the full-FP8 backward (dO quantized to e4m3 in
+    pow2 (sequence, head, 32-token) blocks inside the op, e4m3 P and dS, five
+    e4m3 MFMAs).  Sampled sequences incl. the longest (4096):
+
+    * the full batch's rows against the oracle with the same casts (and the
+      batch-wide q / k scale normalisers): relative L2 <= 1e-2;
+    * against the fp64 backward of the dequantized inputs on the unquantized
+      dO (the contract's own e4m3 error): relative L2 <= 6e-2, SNR >= 24 dB,
+      max |err| <= 0.2 max |ref|;
+    * a sub-batch of the sampled sequences (its own normalisers) with dbias
+      against the same-cast oracle, and dbias(full) against dbias(first
+      half) + dbias(second half) at relative L2 <= 1e-2 (the halves'
+      normalisers differ, so only up to e4m3 rounding)."""
+    from oracle import hstu_bwd_fp8full_oracle as FO
+    from oracle import hstu_do_fp8_oracle as DO
+
+    ops = _ops()
+    lengths, (q8, k8, v8), (sq, sk, sv), bias, dout = _cfg3_inputs()
+    N, alpha = 4096, 1.0 / 128 ** 0.5
+    offs = orc.offsets_from_lengths(lengths)
+
+    def run(lens, rows=None):
+        sel = (lambda t: t) if rows is None else (lambda t: t[rows])
+        o = orc.offsets_from_lengths(lens).to(DEV)
+        dev = [sel(t).to(DEV).contiguous() for t in (q8, k8, v8, sq, sk, sv)]
+        g = [torch.full(dev[0].shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        b = bias.to(DEV)
+        db = torch.empty_like(b)
+        print(f"config 3 full-FP8 bwd: {len(lens)} sequences, T={int(np.sum(lens))}", flush=True)
+        ops.triton_hstu_attention_bwd(sel(dout).to(DEV), *dev[:3], *g, o, None, N, alpha, 0, 0, None, False, 0,
+                                      *dev[3:], attn_bias=b, dbias=db, full_fp8=True)
+        torch.cuda.synchronize()
+        return [t.float().cpu() for t in g] + [db.cpu()]
+
+    full = run(lengths)
+    for name, t in zip(("dq", "dk", "dv", "dbias"), full):
+        assert torch.isfinite(t).all(), name
+
+    order = np.argsort(lengths)
+    sample = sorted({int(order[-1]), int(order[len(order) // 2]), int(order[0]), int(order[int(len(order) * 0.9)])})
+    assert int(max(lengths[sample])) == 4096
+    rows = torch.cat([torch.arange(int(offs[b]), int(offs[b + 1])) for b in sample])
+    sub_len = lengths[sample]
+    sub_offs = orc.offsets_from_lengths(sub_len)
+    y8, e8 = DO.quantize_do_e4m3_blk(dout[rows], sub_offs, N)
+    args = (N, alpha, q8[rows], k8[rows], v8[rows], sq[rows], sk[rows], sv[rows], sub_offs, y8, e8)
+    batch_max = (float(sq.abs().max()), float(sk.abs().max()))
+    want_full = FO.full_fp8_bwd(*args, attn_bias=bias, max_scales=batch_max)
+    exact = orc.hstu_mha_bwd_closed_form(N, alpha, *(orc.dequantize(x[rows], s[rows]) for x, s in
+                                                     ((q8, sq), (k8, sk), (v8, sv))),
+                                         sub_offs, dout[rows].double(), attn_bias=bias)
+    for name, gt, w, ex in zip(("dq", "dk", "dv"), full[:3], want_full[:3], exact[:3]):
+        gt = gt[rows]
+        e = orc.rel_l2(w, gt)
+        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+        e2, snr = orc.rel_l2(ex, gt), orc.snr_db(ex, gt)
+        m = float((gt.double() - ex).abs().max() / ex.abs().max())
+        assert e2 <= 6e-2 and snr >= 24.0 and m <= 0.2, (
+            f"{name}: rel L2 {e2:.3e}, SNR {snr:.1f} dB, max {m:.3e} vs the float64 backward")
+
+    sub = run(sub_len, rows)
+    want_sub = FO.full_fp8_bwd(*args, attn_bias=bias)
+    for name, gt, w in zip(("dq", "dk", "dv", "dbias"), sub, want_sub):
+        e = orc.rel_l2(w, gt)
+        assert e <= 1e-2, f"sub-batch {name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+    e2, snr = orc.rel_l2(exact[3], sub[3]), orc.snr_db(exact[3], sub[3])
+    assert e2 <= 6e-2 and snr >= 24.0, f"sub-batch dbias: rel L2 {e2:.3e}, SNR {snr:.1f} dB vs float64"
+
+    half = len(lengths) // 2
+    cut = int(offs[half])
+    first = run(lengths[:half], torch.arange(cut))
+    second = run(lengths[half:], torch.arange(cut, q8.shape[0]))
+    e = orc.rel_l2(full[3].double(), (first[3] + second[3]).double())
+    assert e <= 1e-2, f"dbias linearity: rel L2 {e:.3e}"
+
+
+def _layer_scales(x, params):
+    """(s_x, s_qkv) = amax * 1.25 / 448 of the LN output and of V|Q|K, from a
+    float64 pass over the whole batch (fixed scales: no per-call state)."""
+    p = {k: v.double() for k, v in params.items()}
+    xn = torch.nn.functional.layer_norm(x.double(), (x.shape[1],), p["input_norm_weight"], p["input_norm_bias"],
+                                        1e-6)
+    s_x = float(xn.abs().max()) * 1.25 / 448
+    s_qkv = float((xn @ p["uvqk_weight"][:, 512:] + p["uvqk_bias"][512:]).abs().max()) * 1.25 / 448
+    return s_x, s_qkv
+
+
+@pytest.mark.parametrize("attn_full_fp8", [False, True])
+def test_config5_layer_config3_shapes(hip_lib, attn_full_fp8):
+    """BASELINE config 5 (one HSTU layer fwd + bwd in FP8) at config 3's
+    shapes: T = 162 251 Zipf tokens, N = 4096, E = 512, H = 4, D = 128,
+    relative bias [4, 2047], dropout 0.3 with the 16-bit mask, fixed device
+    scales; attention backward bf16-dO or full-FP8.
+
+    * out and dx of sampled sequences (incl. the longest) against the float64
+      layer oracle run on those sequences with the full batch's mask rows:
+      relative L2 <= 1.5e-2 (out) and <= 3e-2 (dx; <= 6e-2 with the
+      full-FP8 attention backward, whose own e4m3 casts the oracle does not
+      model);
+    * bitwise sub-batch independence (dropout 0): the sampled sequences'
+      out and dx rows equal those of a run on the sub-batch alone;
+    * every parameter gradient is linear over the two halves of the batch
+      (dropout 0) to relative L2 <= 5e-3: the gradients of the bf16
+      parameters are bf16, so the batch's and the two halves' each carry a
+      2^-9 relative rounding."""
+    import hstu_amd
+    from hstu_amd import bwd_fp8
+    from oracle import hstu_layer_oracle as LO
+    from oracle import hstu_ln_oracle as L
+
+    lengths = orc.lengths_for_config(3)
+    T, N, E, seed = 162251, 4096, 512, 77
+    offs = orc.offsets_from_lengths(lengths)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    dy = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    params = LO.make_layer_params(E, seed=4)
+    bias = orc.make_bias(4, 1024)
+    s_x, s_qkv = _layer_scales(x, params)
+    s_out = 0.05
+    cfg = bwd_fp8.Fp8BackwardConfig(attn_full_fp8=attn_full_fp8)
+
+    def run(lens, rows, p):
+        print(f"config 5 layer: {len(lens)} sequences, T={int(np.sum(lens))}, dropout {p}, "
+              f"full-FP8 attention backward {attn_full_fp8}", flush=True)
+        sel = (lambda t: t) if rows is None else (lambda t: t[rows])
+        o = orc.offsets_from_lengths(lens).to(DEV)
+        xd = sel(x).to(DEV).requires_grad_(True)
+        pd = {k: v.to(DEV).requires_grad_(True) for k, v in params.items()}
+        bd = bias.to(DEV).requires_grad_(True)
+        sc = (lambda s: torch.full((1, 1), s, device=DEV))
+        out = hstu_amd.hstu_layer(xd, o, N, pd, dropout_ratio=p, training=True, fp8_input_scale=sc(s_x),
+                                  fp8_qkv_scale=sc(s_qkv), fp8_output_scale=sc(s_out), attn_bias=bd, seed=seed,
+                                  fp8_backward=cfg, dropout_mask16=True)
+        out.backward(sel(dy).to(DEV))
+        torch.cuda.synchronize()
+        grads = {k: v.grad.float().cpu() for k, v in pd.items()}
+        grads["attn_bias"] = bd.grad.float().cpu()
+        return out.detach().cpu(), xd.grad.cpu(), grads
+
+    out, dx, _ = run(lengths, None, 0.3)
+    assert torch.isfinite(out.float()).all() and torch.isfinite(dx.float()).all()
+
+    order = np.argsort(lengths)
+    sample = sorted({int(order[-1]), int(order[len(order) // 2]), int(order[0])})
+    assert int(max(lengths[sample])) == 4096
+    rows = torch.cat([torch.arange(int(offs[b]), int(offs[b + 1])) for b in sample])
+    sub_len = lengths[sample]
+    mask = L.dropout_mask_rows(rows.numpy(), 512, 3, 0.3, seed, True)
+    xr = x[rows].double().requires_grad_(True)
+    pr = {k: v.double().requires_grad_(True) for k, v in params.items()}
+    br = bias.double().requires_grad_(True)
+    ref = LO.hstu_layer_ref(xr, pr, sub_len, N, s_x=s_x, s_qkv=s_qkv, s_out=s_out, dropout_ratio=0.3, mask=mask,
+                            attn_bias=br, quantize=True)
+    ref.backward(dy[rows].double())
+    e_out = orc.rel_l2(ref.detach(), out[rows].double())
+    e_dx = orc.rel_l2(xr.grad, dx[rows].double())
+    print(f"sampled rows: out rel L2 {e_out:.3e}, dx rel L2 {e_dx:.3e}", flush=True)
+    assert e_out <= 1.5e-2, f"out rel L2 {e_out:.3e}"
+    assert e_dx <= (6e-2 if attn_full_fp8 else 3e-2), f"dx rel L2 {e_dx:.3e}"
+
+    out0, dx0, g0 = run(lengths, None, 0.0)
+    sub_out, sub_dx, _ = run(sub_len, rows, 0.0)
+    assert torch.equal(out0[rows], sub_out), "out: sub-batch rows differ from the full batch"
+    assert torch.equal(dx0[rows], sub_dx), "dx: sub-batch rows differ from the full batch"
+
+    half = len(lengths) // 2
+    cut = int(offs[half])
+    _, _, g1 = run(lengths[:half], torch.arange(cut), 0.0)
+    _, _, g2 = run(lengths[half:], torch.arange(cut, T), 0.0)
+    for k in g0:
+        e = orc.rel_l2(g0[k].double(), (g1[k] + g2[k]).double())
+        assert e <= 5e-3, f"d{k}: rel L2 {e:.3e} between the batch and the sum of its halves"
+
+
 def test_output_block_config3_tokens(hip_lib, monkeypatch):
     """The output block at config 3's token count (T = 162 251, D = 4*128 =
     512) with the production flags (silu, concat u and x, dropout 0.3 with the
