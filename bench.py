@@ -649,9 +649,10 @@ def main():
                      "peak": PEAK_TFLOPS["fp8"], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS["fp8"], 4), "traffic": traffic},
     }
+    full_fp8 = w8.full_fp8
     del w8
     torch.cuda.empty_cache()
-    if not args.headline_only and w8.full_fp8:
+    if not args.headline_only and full_fp8:
         wd = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
         wall_d, st_d, parts_d = wd.run(args.steps, max(args.warmup, 2), flush)
         vd = wd.flops("step") / (st_d["median"] * 1e-3) / 1e12
@@ -663,7 +664,7 @@ def main():
         del wd
         torch.cuda.empty_cache()
     if not args.headline_only:
-        wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=w8.full_fp8)
+        wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=full_fp8)
         wall_n, st_n, parts_n = wn.run(args.steps, max(args.warmup, 2), flush)
         vn = wn.flops("step") / (st_n["median"] * 1e-3) / 1e12
         res["no_bias"] = {"value": round(vn, 2), "unit": "TFLOP/s", "ms_per_step": round(st_n["median"], 4),

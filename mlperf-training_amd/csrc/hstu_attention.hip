@@ -1818,8 +1818,15 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
       dvt[dt] = mfma_fp8_scaled(ado, bp, dvt[dt], sc_e, 127);
       const i32x8 aq = tr_frag(buf + C::Q_OFF, dt);
       dkt[dt] = mfma_fp8_scaled(aq, bk, dkt[dt], 127, sc_e);
-      __builtin_amdgcn_sched_barrier(0);  // keep each step's operand reads next to its MFMAs
     }
+    // operand reads one step ahead of their MFMAs: {8 tr reads}, 7 x {2 MFMAs, 8 tr reads}, {2 MFMAs}
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
     lds_dma_wait();  // the next stage's DMA (and this tile's dS stores) done
     __syncthreads();
   };
