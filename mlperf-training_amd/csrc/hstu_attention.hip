@@ -472,7 +472,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
       }
     }
     if constexpr (FP8) {
-      if (tid < 128) ((float*)(buf + C::SC_OFF))[(tid & 63) * 2 + (tid >> 6)] = stg.sc;
+      // (sk, 1 / sv) per key: 1 / sv enters the sigmoid's denominator; a zero
+      // scale (rows past L, all-zero rows) has V = 0, so any finite factor does
+      float v = stg.sc;
+      if (tid >= 64) v = v > 0.f ? 1.0f / v : 1.0f;
+      if (tid < 128) ((float*)(buf + C::SC_OFF))[(tid & 63) * 2 + (tid >> 6)] = v;
     }
     if constexpr (BIAS) {
       if (tid < C::BM + C::BN - 1) ((float*)(buf + C::BIAS_OFF))[tid] = stg.bias;
@@ -545,8 +549,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
               float b = 0.f;
               if constexpr (BIAS) b = BCONST ? bconst : bias_lds[bias_rd + 16 * (qt - kt) - r];
               const float t = scaled_score<FP8, BIAS>(s[kt][qt][r], cq[qt], skv[r], b);
-              float val = t * sig_of_t(t);
-              if constexpr (FP8) val *= svv[r];
+              // e4m3: t sigmoid sv = t / (2^t / sv + 1 / sv), svv holding 1 / sv
+              float val;
+              if constexpr (FP8) val = t * __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(t), svv[r], svv[r]));
+              else val = t * sig_of_t(t);
               if constexpr (MASKED) {
                 const int i = mw0 + qt * 16 + li, j = n0 + kt * 16 + 4 * g + r;
                 const bool ok = GENERIC ? valid_generic(i, j, mc) : (j <= i);
@@ -566,7 +572,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
         if (bias_const) epilogue(std::false_type{}, std::true_type{});
         else epilogue(std::false_type{}, std::false_type{});
       }
-      // ---- O += P . V  (V rows read transposed by ds_read_b64_tr_b16)
+      // ---- O += P . V  (V rows read transposed by ds_read_b64_tr_b16); the
+      // raised wave priority lets this wave's MFMAs issue ahead of the other
+      // workgroup's epilogue VALU work on the same SIMD
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int c = 0; c < C::BN / 32; ++c) {
 #pragma unroll
@@ -577,6 +586,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
           o[1][dt] = mfma_bf16(pa[1][c], bv, o[1][dt]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
     }
 
     if (t + 1 < ntiles) store(smem + ((t + 1) & 1) * C::BUF);
@@ -2084,22 +2094,32 @@ __global__ void __launch_bounds__(1024) f8_tile_prefix(const int64_t* seq_offset
 }
 
 // f8max[0] / [1] = float bits of the largest q / k scale over [T, H] (or the scalar).
-__global__ void f8_scale_max(const float* qs, const float* ks, int64_t n, int H, int64_t srs, int64_t shs,
-                             unsigned* f8max) {
+__global__ void __launch_bounds__(256) f8_scale_max(const float* qs, const float* ks, int64_t ntok, int H,
+                                                    int64_t srs, int64_t shs, unsigned* f8max) {
+  __shared__ float red[2][4];
   float mq = 0.f, mk = 0.f;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t t = i / H, hh = i - t * H, o = t * srs + hh * shs;
-    mq = fmaxf(mq, fabsf(qs[o]));
-    mk = fmaxf(mk, fabsf(ks[o]));
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < ntok; t += (int64_t)gridDim.x * blockDim.x) {
+    for (int hh = 0; hh < H; ++hh) {
+      const int64_t o = t * srs + hh * shs;
+      mq = fmaxf(mq, fabsf(qs[o]));
+      mk = fmaxf(mk, fabsf(ks[o]));
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     mq = fmaxf(mq, __shfl_xor(mq, off));
     mk = fmaxf(mk, __shfl_xor(mk, off));
   }
+  const int wv = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
-    atomicMax(&f8max[0], __float_as_uint(mq));
-    atomicMax(&f8max[1], __float_as_uint(mk));
+    red[0][wv] = mq;
+    red[1][wv] = mk;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // one atomic per block and value (the maxima are non-negative: float bits order as unsigned)
+    atomicMax(&f8max[0], __float_as_uint(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]))));
+    atomicMax(&f8max[1], __float_as_uint(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]))));
   }
 }
 
@@ -2827,10 +2847,11 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
     // tile prefix and scale maxima, read by both halves
     hipLaunchKernelGGL(f8_tile_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
                        (int64_t*)(ws + wl.base), (unsigned*)(ws + wl.maxv));
-    const int64_t nscale = (scale_row_stride || scale_head_stride) ? total_tokens * H : 1;
-    const int sgrid = (int)std::min<int64_t>((nscale + 255) / 256, 1024);
-    hipLaunchKernelGGL(f8_scale_max, dim3(sgrid > 0 ? sgrid : 1), dim3(256), 0, stream, q_scale, k_scale, nscale,
-                       H, scale_row_stride, scale_head_stride, (unsigned*)(ws + wl.maxv));
+    const bool per_token = scale_row_stride || scale_head_stride;
+    const int64_t ntok = per_token ? total_tokens : 1;
+    const int sgrid = (int)std::min<int64_t>((ntok + 255) / 256, 256);
+    hipLaunchKernelGGL(f8_scale_max, dim3(sgrid > 0 ? sgrid : 1), dim3(256), 0, stream, q_scale, k_scale, ntok,
+                       per_token ? H : 1, scale_row_stride, scale_head_stride, (unsigned*)(ws + wl.maxv));
     if (has_bias) {
       p.bias_ext = (const float*)(ws + wl.bias_ext);
       hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
