@@ -311,13 +311,20 @@ __device__ __forceinline__ void wait_vm_le() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Unpadded 128-byte e4m3 tile rows: data chunk c (bytes 16c .. 16c + 15) of
+// row r sits at 16-byte slot c ^ swz128(r).  A ds_read_b128 of 16 consecutive
+// rows (one chunk each) then hits 16 distinct bank groups, as do the
+// transposed reads of row groups 8 and 32 apart; swz128 is constant under
+// r -> r + 16.
+__host__ __device__ constexpr int swz128(int r) { return ((r >> 1) & 7) ^ (((r >> 5) & 1) << 2); }
+
 template <int D, bool FP8>
 struct FwdCfg {
   static constexpr int BM = 128, BN = 64, KT = BN / 16, DT = D / 16, KS = D / 32;
   static constexpr int ES = FP8 ? 1 : 2;
-  // Row pitches of row bytes + 32 (== 32 mod 64): the pitch at which 16-row
-  // ds_read_b128 operand reads and ds_read_b64_tr_b16 reads run without bank
-  // conflicts on gfx950 (measured: 2x the b128 bandwidth of +16 or +48).
+  // bf16 rows at a pitch of row bytes + 32 (== 32 mod 64) for the 16-row
+  // ds_read_b128 operand reads and the ds_read_b64_tr_b16 V reads; the e4m3
+  // K tile uses unpadded swizzled rows (swz128) inside the same region.
   static constexpr int KP = D * ES + 32;
   static constexpr int VP = D * 2 + 32;
   static constexpr int K_OFF = 0;
@@ -328,7 +335,10 @@ struct FwdCfg {
   static constexpr int LDS = 2 * BUF;
   static constexpr int K_CPR = D * ES / 16;                 // 16-byte chunks per K row
   static constexpr int K_N = BN * K_CPR / kThreads;         // K chunks per thread
-  static constexpr int V_CPR = D * ES / 16;                 // 16-byte source chunks per V row
+  // V source pieces per row: 16 bytes (bf16), or 8 e4m3 bytes that become one
+  // 16-byte bf16 store, so that 16 lanes write one whole LDS row (256 bytes)
+  // and a store instruction's passes hit distinct banks
+  static constexpr int V_CPR = FP8 ? D / 8 : D * ES / 16;
   static constexpr int V_N = BN * V_CPR / kThreads;
 };
 
@@ -337,7 +347,7 @@ template <int D, bool FP8>
 struct FwdStage {
   using C = FwdCfg<D, FP8>;
   u32x4 k[C::K_N];
-  u32x4 v[C::V_N];
+  std::conditional_t<FP8, u32x2, u32x4> v[C::V_N];
   float sc;    // e4m3: sk (threads 0..63) or sv (threads 64..127) of one key
   float bias;  // threads 0..BM+BN-2: one bias value of the tile's offset band
 };
@@ -380,13 +390,13 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   for (int i = 0; i < C::K_N; ++i) {
     const int item = tid + kThreads * i, row = item / C::K_CPR, ch = item % C::K_CPR;
     k_voff[i] = row * krs + ch * 16;
-    k_loff[i] = C::K_OFF + row * C::KP + ch * 16;
+    k_loff[i] = FP8 ? C::K_OFF + row * 128 + 16 * (ch ^ swz128(row)) : C::K_OFF + row * C::KP + ch * 16;
   }
 #pragma unroll
   for (int i = 0; i < C::V_N; ++i) {
     const int item = tid + kThreads * i, row = item / C::V_CPR, ch = item % C::V_CPR;
-    v_voff[i] = row * vrs + ch * 16;
-    v_loff[i] = C::V_OFF + row * C::VP + ch * 16 * (FP8 ? 2 : 1);
+    v_voff[i] = row * vrs + ch * (FP8 ? 8 : 16);
+    v_loff[i] = C::V_OFF + row * C::VP + ch * 16;
   }
 
   // Q fragments (B operand of S^T = K.Q^T): lane holds query mw0+16qt+li.
@@ -433,7 +443,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < C::K_N; ++i) stg.k[i] = buf_ld128(krsrc, k_voff[i], n0 * krs);
 #pragma unroll
-    for (int i = 0; i < C::V_N; ++i) stg.v[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
+    for (int i = 0; i < C::V_N; ++i) {
+      if constexpr (FP8) stg.v[i] = buf_ld64(vrsrc, v_voff[i], n0 * vrs);
+      else stg.v[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
+    }
     if constexpr (FP8) {
       if (tid < 64) {
         stg.sc = buf_ldf(sk_rsrc, (uint32_t)tid * s_step, n0 * s_step);
@@ -456,17 +469,14 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
     for (int i = 0; i < C::V_N; ++i) {
       if constexpr (FP8) {
         // exact e4m3 -> bf16 (scale 1); the per-key V scale is folded into P
-        const u32x4 w = stg.v[i];
-        u32x4 lo, hi;
+        const u32x2 w = stg.v[i];
+        u32x4 b;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          lo[2 * e] = cvt_fp8x2_bf16<false>(w[e]);
-          lo[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e]);
-          hi[2 * e] = cvt_fp8x2_bf16<false>(w[e + 2]);
-          hi[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e + 2]);
+          b[2 * e] = cvt_fp8x2_bf16<false>(w[e]);
+          b[2 * e + 1] = cvt_fp8x2_bf16<true>(w[e]);
         }
-        *(u32x4*)(buf + v_loff[i]) = lo;
-        *(u32x4*)(buf + v_loff[i] + 16) = hi;
+        *(u32x4*)(buf + v_loff[i]) = b;
       } else {
         *(u32x4*)(buf + v_loff[i]) = stg.v[i];
       }
@@ -487,6 +497,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   // e4m3: lane group g holds the 16-byte k-chunks g and g+4 of a row (the
   // same order in both MFMA operands), so each b128 read is conflict-free.
   const int k_rd = C::K_OFF + li * C::KP + 16 * g;
+  // e4m3 (swizzled rows 16 kt + li): chunks g and g + 4 at slots g ^ swz128 and that ^ 4,
+  // swz128(16 kt + li) = (li >> 1) ^ 4 (kt >> 1)
+  const int ka0 = C::K_OFF + li * 128 + 16 * (g ^ (li >> 1)), ka1 = ka0 ^ 64;
   // tr16: lane j of group g addresses row 4g + j/4 (+16 for the second half), column 4*(j%4)
   const int v_rd = C::V_OFF + (4 * g + (li >> 2)) * C::VP + (li & 3) * 8;
   // bias index of element (qt, kt, r) = bias_rd + 16*(qt-kt) - r
@@ -508,7 +521,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
       for (int kt = 0; kt < C::KT; ++kt) {
         const uint8_t* krow = buf + k_rd + kt * 16 * C::KP;
         if constexpr (FP8) {
-          i32x8 a = cat8(lds_ld128(krow), lds_ld128(krow + 64));
+          const uint8_t* kb = buf + kt * 16 * 128;
+          i32x8 a = cat8(lds_ld128(kb + (kt < 2 ? ka0 : ka1)), lds_ld128(kb + (kt < 2 ? ka1 : ka0)));
           s[kt][0] = mfma_fp8(a, qf8[0], zero4());
           s[kt][1] = mfma_fp8(a, qf8[1], zero4());
         } else {
@@ -1603,7 +1617,7 @@ struct F8Bwd {
   // 16-byte slot c ^ kv_swz(r).  The swizzle spreads the 16 rows of a
   // ds_read_b128 and the row groups 8 and 32 apart of a ds_read_b64_tr_b8
   // over distinct banks; it is constant under r -> r + 16 (bits 1-3 and 5).
-  __host__ __device__ static constexpr int kv_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 5) & 1) << 2); }
+  __host__ __device__ static constexpr int kv_swz(int r) { return swz128(r); }
   static constexpr int Q_OFF = 0;
   static constexpr int DO_OFF = Q_OFF + BM * 128;
   static constexpr int SQ_OFF = DO_OFF + BM * 128;  // 128 fp32 query scales

@@ -57,6 +57,9 @@ __device__ __forceinline__ BufRsrc make_rsrc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ u32x4 buf_ld128(BufRsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
 }
+__device__ __forceinline__ u32x2 buf_ld64(BufRsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+}
 __device__ __forceinline__ float buf_ldf(BufRsrc r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
