@@ -365,7 +365,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
   if (m0 >= L) return;
   const MaskCtx mc = mask_ctx(p, sc);
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, li = lane & 15,
+            g = lane >> 4;
   const int mw0 = m0 + wave * 32;
   const bool wave_active = mw0 < L;
 
@@ -448,17 +449,19 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
       else stg.v[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
     }
     if constexpr (FP8) {
-      if (tid < 64) {
-        stg.sc = buf_ldf(sk_rsrc, (uint32_t)tid * s_step, n0 * s_step);
-      } else if (tid < 128) {
-        stg.sc = buf_ldf(sv_rsrc, (uint32_t)(tid - 64) * s_step, n0 * s_step);
+      // wave 0: the tile's key scales, wave 1: its value scales
+      if (wave == 0) {
+        stg.sc = buf_ldf(sk_rsrc, (uint32_t)lane * s_step, n0 * s_step);
+      } else if (wave == 1) {
+        stg.sc = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, n0 * s_step);
       }
     }
     if constexpr (BIAS) {
-      // offsets i-j of this tile span [m0-n0-(BN-1), m0-n0+BM-1]
+      // offsets i-j of this tile span [m0-n0-(BN-1), m0-n0+BM-1]; scaled at
+      // the LDS store, so that nothing waits for the loads before the tile's math
       if (tid < C::BM + C::BN - 1) {
         const int off = m0 - n0 - (C::BN - 1) + tid;
-        stg.bias = biasb[min(max(off, -R1), R1) + R1] * -kLog2e;
+        stg.bias = biasb[min(max(off, -R1), R1) + R1];
       }
     }
   };
@@ -489,7 +492,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
       if (tid < 128) ((float*)(buf + C::SC_OFF))[(tid & 63) * 2 + (tid >> 6)] = v;
     }
     if constexpr (BIAS) {
-      if (tid < C::BM + C::BN - 1) ((float*)(buf + C::BIAS_OFF))[tid] = stg.bias;
+      if (tid < C::BM + C::BN - 1) ((float*)(buf + C::BIAS_OFF))[tid] = stg.bias * -kLog2e;
     }
   };
 
@@ -1759,6 +1762,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
 
   // this block's stored dS tiles (query tiles blk, blk + 1, .. are consecutive)
   uint8_t* const ds_dst = f8_tile(p, sc, sc.blk, sc.blk) + (size_t)((wave * 2) * 64 + lane) * 16;
+  fp8_saturate_mode(true);
   load(n0, smem);
   lds_dma_wait();
   __syncthreads();
@@ -1805,9 +1809,10 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
             pval = ok ? pval : 0.f;
             dsv = ok ? dsv : 0.f;
           }
-          pv[r] = __builtin_fminf(pval, 448.f);
-          dkv[r] = __builtin_amdgcn_fmed3f(dsv * (an * sq4[r]), -448.f, 448.f);
-          dqv[r] = __builtin_amdgcn_fmed3f(dsv * bn, -448.f, 448.f);
+          // saturated to +-448 by the conversion (MODE.FP16_OVFL)
+          pv[r] = pval;
+          dkv[r] = dsv * (an * sq4[r]);
+          dqv[r] = dsv * bn;
         }
         pd[4 * hf + qs] = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
         dk8[4 * hf + qs] = pack_fp8x4(dkv[0], dkv[1], dkv[2], dkv[3]);
@@ -1866,6 +1871,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
     for (; t < ntiles; ++t) tile_body(t, std::false_type{}, std::true_type{});
   }
 
+  fp8_saturate_mode(false);
   if (!key_ok) return;
   // lane (key, g) holds d = 16 dt + 4 g + r of its key
   const float fin_v = 1.0f / p.p8_scale;
@@ -1942,11 +1948,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
       dsp[j] = *(const u32x4*)(tile + (size_t)((w * 2 + hf) * 64 + lane) * 16);
     }
     if constexpr (BIAS) {
+      // raw s_k; inverted when the step's operands are stored, so that
+      // nothing waits for these loads before the current step's math
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const float s = buf_ldf(sk_rsrc, (uint32_t)(16 * (2 * wave + j) + li) * s_step, (uint32_t)(kb * C::BN) * s_step);
-        isk[j] = s > 0.f ? unscale / s : 0.f;
-      }
+      for (int j = 0; j < 2; ++j)
+        isk[j] = buf_ldf(sk_rsrc, (uint32_t)(16 * (2 * wave + j) + li) * s_step, (uint32_t)(kb * C::BN) * s_step);
     }
   };
   auto store = [&]() {
@@ -2032,7 +2038,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   __syncthreads();
   for (int kb = 0; kb < nsteps; ++kb) {
     u32x4 cur[4];
-    float cur_isk[2] = {isk[0], isk[1]};
+    float cur_isk[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) cur_isk[j] = isk[j] > 0.f ? unscale / isk[j] : 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) cur[j] = dsp[j];
     if (kb + 1 < nsteps) load(kb + 1);

@@ -117,6 +117,18 @@ __device__ __forceinline__ f32x4 mfma_fp8_scaled(i32x8 a, i32x8 b, f32x4 c, int 
 
 // Four floats -> four e4m3 bytes (RNE).  The conversion does not saturate
 // (out-of-range values become NaN): callers clamp to +-448 first.
+// MODE.FP16_OVFL (MODE bit 23) of the wave.  Set, v_cvt_pk_fp8_f32 turns
+// every finite input beyond the e4m3 range into +-448 instead of NaN -- the
+// same byte as a clamp to +-448 followed by the conversion (probed on gfx950
+// over in-range, boundary, 1e30 and 3.39e38 inputs; +-inf and NaN still give
+// NaN) -- so a kernel whose values are finite can drop its clamps.  It also
+// makes v_cvt_pk_bf16_f32 return +-bf16 max instead of +-inf above that
+// range, so kernels clear it before their bf16 outputs.
+__device__ __forceinline__ void fp8_saturate_mode(bool on) {
+  if (on) asm volatile("s_setreg_imm32_b32 hwreg(HW_REG_MODE, 23, 1), 1\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  else asm volatile("s_setreg_imm32_b32 hwreg(HW_REG_MODE, 23, 1), 0\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
 __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
