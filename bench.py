@@ -81,9 +81,14 @@ def parse():
                     help="how the caches are evicted before each timed call (see CacheFlush)")
     ap.add_argument("--bf16-dout", action="store_true",
                     help="headline with the e4m3-input backward on the bf16 dO instead of the full-FP8 backward")
+    ap.add_argument("--bf16-p", action="store_true",
+                    help="headline with the bf16-P forward instead of the FP8 P.V forward")
     ap.add_argument("--headline-only", action="store_true",
                     help="only the FP8-with-bias line (no no-bias / bf16 sub-results); for profiler runs")
     return ap.parse_args()
+
+
+PV_SCALE = 10.04  # the reference's DLRM_HSTU_FP8_FWD_PV_SCALE default
 
 
 def lengths_cfg3():
@@ -99,9 +104,10 @@ def causal_pairs(lengths) -> int:
 class Workload:
     """Device-resident inputs and the raw C-ABI argument tuples of one step."""
 
-    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True, full_fp8=False):
+    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True, full_fp8=False, fp8_pv=False):
         self.torch = torch
         self.full_fp8 = full_fp8 and dtype == "fp8"
+        self.fp8_pv = fp8_pv and dtype == "fp8"
         dev = "cuda"
         self.lengths = lengths
         self.H, self.D, self.N = H, D, N
@@ -156,6 +162,13 @@ class Workload:
                          self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), H * D, H * D, H * D,
                          sp(self.dbias), self.ws.data_ptr(), ws_bytes, T, stream)
         self.f_fwd = lib.fn("hstu_attn_fwd")
+        if self.fp8_pv:
+            # the FP8 P.V forward at the reference's default static P scale
+            self.fwd_args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), H * D, H * D, H * D,
+                             sp(self.sq), sp(self.sk), sp(self.sv), srs, shs, self.offs.data_ptr(), B, H, D, N,
+                             self.alpha, None, 0, 0, sp(self.bias), R, PV_SCALE, self.out.data_ptr(), H * D,
+                             self.fws.data_ptr(), fws_bytes, T, stream)
+            self.f_fwd = lib.fn("hstu_attn_fwd_fp8_pv")
         self.f_dkdv = lib.fn("hstu_attn_bwd_dkdv")
         self.f_dq = lib.fn("hstu_attn_bwd_dq")
         self.lib = lib
@@ -485,6 +498,10 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
               for k in ("fp8_input_scale", "fp8_qkv_scale", "fp8_output_scale")}
     warmup = max(warmup, fp8_mod.CALIBRATION_STEPS + 1)
 
+    # the production forward: FP8 P.V (the reference's gin sets DLRM_HSTU_FP8_FWD_PV)
+    prev_pv = os.environ.get("DLRM_HSTU_FP8_FWD_PV")
+    os.environ["DLRM_HSTU_FP8_FWD_PV"] = "1"
+
     def step(ev):
         for t in [x, bias, *p.values()]:
             t.grad = None
@@ -498,14 +515,20 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
         if ev is not None:
             ev[2].record()
 
-    tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
+    try:
+        tot, (tf, tb) = _cold_events(torch, step, steps, warmup, flush, marks=2)
+    finally:
+        if prev_pv is None:
+            os.environ.pop("DLRM_HSTU_FP8_FWD_PV", None)
+        else:
+            os.environ["DLRM_HSTU_FP8_FWD_PV"] = prev_pv
     bwd_fp8.reset_sites()
     m = float(np.median(tot))
     P = causal_pairs(lengths)
     gemm_fwd = 2 * T * E * (2 * H * 2 * D) + 2 * T * (3 * H * D) * E
     flops = 3 * gemm_fwd + 14 * D * H * P
     return {"workload": "BASELINE config 5: HSTU layer fwd+bwd in FP8 (LN -> FP8 UVQK GEMM -> FP8 attention with "
-                        "bias and the full-FP8 attention backward -> LN(attn)*silu(u)*dropout -> FP8 out-proj + "
+                        "bias, the FP8 P.V forward and the full-FP8 attention backward -> LN(attn)*silu(u)*dropout -> FP8 out-proj + "
                         "residual; %s), "
                         "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj and UVQK dgrads, e4m3 x e5m2 wgrads" if fp8_dgrad
                                                     else "bf16 dgrad/wgrad"),
@@ -607,7 +630,8 @@ def main():
     if args.only == "wgrad":
         print(json.dumps(wgrad_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
         return
-    w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True, full_fp8=not args.bf16_dout)
+    w8 = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True, full_fp8=not args.bf16_dout,
+                  fp8_pv=not args.bf16_p)
     wall_ms, st, parts = w8.run(args.steps, args.warmup, flush)
     total = w8.flops("step")
     value = total / (st["median"] * 1e-3) / 1e12
@@ -633,6 +657,9 @@ def main():
         "data": "synthetic",
         "config": {"workload": "BASELINE config 3: jagged HSTU attention fwd+bwd (dq, dk, dv, dbias), e4m3 q/k/v "
                                "with per-token-per-head scales, relative-position bias [4, 2047], bf16 out/grads",
+                   "forward": ("FP8 P.V (the reference's DLRM_HSTU_FP8_FWD_PV contract: SiLU output rounded to "
+                               "e4m3 at the static scale %g, V raw e4m3, P.V on e4m3 MFMAs)" % PV_SCALE
+                               if w8.fp8_pv else "e4m3 inputs, bf16 P"),
                    "backward": ("full-FP8 (the reference's DLRM_HSTU_FP8_BWD_FULL contract: dO quantized to e4m3 "
                                 "in pow2 (sequence, head, 32-token) blocks inside the step, e4m3 P and dS, all five "
                                 "products on e4m3 MFMAs)" if w8.full_fp8 else "e4m3 inputs, bf16 dO and dS"),
@@ -649,22 +676,33 @@ def main():
                      "peak": PEAK_TFLOPS["fp8"], "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_TFLOPS["fp8"], 4), "traffic": traffic},
     }
-    full_fp8 = w8.full_fp8
+    full_fp8, fp8_pv = w8.full_fp8, w8.fp8_pv
     del w8
     torch.cuda.empty_cache()
-    if not args.headline_only and full_fp8:
+    if not args.headline_only and fp8_pv:
+        wp = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True, full_fp8=full_fp8)
+        wall_p, st_p, parts_p = wp.run(args.steps, max(args.warmup, 2), flush)
+        vp = wp.flops("step") / (st_p["median"] * 1e-3) / 1e12
+        res["fp8_bf16_p"] = {"value": round(vp, 2), "unit": "TFLOP/s", "ms_per_step": round(st_p["median"], 4),
+                             "pct_fp8_peak": round(100 * vp / PEAK_TFLOPS["fp8"], 2),
+                             "kernels_ms": {k: round(v, 4) for k, v in parts_p.items()},
+                             "note": "the same step with the bf16-P forward (P.V on bf16 MFMAs)"}
+        del wp
+        torch.cuda.empty_cache()
+    if not args.headline_only and (full_fp8 or fp8_pv):
         wd = Workload(torch, lib, lengths, H, D, N, "fp8", bias=True)
         wall_d, st_d, parts_d = wd.run(args.steps, max(args.warmup, 2), flush)
         vd = wd.flops("step") / (st_d["median"] * 1e-3) / 1e12
-        res["fp8_bf16_dout"] = {"value": round(vd, 2), "unit": "TFLOP/s", "ms_per_step": round(st_d["median"], 4),
-                                "pct_fp8_peak": round(100 * vd / PEAK_TFLOPS["fp8"], 2),
-                                "kernels_ms": {k: round(v, 4) for k, v in parts_d.items()},
-                                "note": "the same step with the e4m3-input backward on the bf16 dO (bf16 dS tiles, "
-                                        "bf16 MFMAs for dV, dK, dQ)"}
+        res["fp8_inputs_only"] = {"value": round(vd, 2), "unit": "TFLOP/s", "ms_per_step": round(st_d["median"], 4),
+                                  "pct_fp8_peak": round(100 * vd / PEAK_TFLOPS["fp8"], 2),
+                                  "kernels_ms": {k: round(v, 4) for k, v in parts_d.items()},
+                                  "note": "e4m3 inputs with no declared precision change: the bf16-P forward and the "
+                                          "e4m3-input backward on the bf16 dO (bf16 dS tiles, bf16 MFMAs for dV, "
+                                          "dK, dQ)"}
         del wd
         torch.cuda.empty_cache()
     if not args.headline_only:
-        wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=full_fp8)
+        wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=full_fp8, fp8_pv=fp8_pv)
         wall_n, st_n, parts_n = wn.run(args.steps, max(args.warmup, 2), flush)
         vn = wn.flops("step") / (st_n["median"] * 1e-3) / 1e12
         res["no_bias"] = {"value": round(vn, 2), "unit": "TFLOP/s", "ms_per_step": round(st_n["median"], 4),

@@ -78,6 +78,33 @@ int hstu_attn_fwd(int dtype,
 int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, int H, int D, int max_seq_len);
 
 /*
+ * FP8 P.V forward: hstu_attn_fwd on e4m3 q, k, v (D = 128, causal mask only:
+ * num_targets must be null, max_attn_len and contextual_seq_len 0, else
+ * HSTU_E_UNSUPPORTED) with the SiLU output rounded to e4m3 before P.V:
+ * P8 = e4m3(sat(P' * pv_scale * r_k)), P' = -log2(e) silu(score), and P.V
+ * on the e4m3 MFMA with V raw; out = sum_k P8 v8_k 2^E(k) * (-ln 2) /
+ * (pv_scale * max_seq_len) [* v_scale].  With one per-tensor scale (scale
+ * strides 0) r_k = 1 and v_scale rides on the output; with [T, H] scales
+ * r_k = v_scale(k) 2^-E(k), E(k) the frexp exponent of the largest V scale
+ * among the keys of k's group (64-key tiles from the sequence start, split by
+ * bit 4 of the key's index in the tile).  pv_scale in (0, 448); the
+ * reference's default is 10.04.  Workspace as hstu_attn_fwd (e4m3 dtype).
+ * Replaces: the FlyDSL e4m3 forward with pv="k128" (DLRM_HSTU_FP8_FWD_PV=1),
+ * ops/flydsl/hstu_flydsl_mha.py:2199-2330, ops/flydsl/hstu_fwd.py:253-283.
+ */
+int hstu_attn_fwd_fp8_pv(const void* q, const void* k, const void* v,
+                         int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride,
+                         const float* q_scale, const float* k_scale, const float* v_scale,
+                         int64_t scale_row_stride, int64_t scale_head_stride,
+                         const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
+                         float alpha,
+                         const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
+                         const float* attn_bias, int bias_R, float pv_scale,
+                         void* out, int64_t out_row_stride,
+                         void* workspace, int64_t workspace_bytes, int64_t total_tokens,
+                         hipStream_t stream);
+
+/*
  * hstu_attn_fwd without a workspace, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  The same kernels and

@@ -238,6 +238,9 @@ struct AttnParams {
   const unsigned* f8max;    // workspace: float bits of max q_scale, max k_scale
   float p8_scale;           // e4m3 P = silu / N * p8_scale (a power of two times N-relative)
   float ds8_scale;          // e4m3 dS = dS' * (scale normaliser) * ds8_scale
+  // FP8 P.V forward (hstu_attn_fwd_fp8_pv)
+  float pv_c;               // 2^-3 f32(2^3 / s): the sigmoid denominator factor of P' s
+  float pv_out;             // f32(1 / s): undoes the P scale on the output
 };
 
 struct SeqCtx {
@@ -622,6 +625,332 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_kernel(AttnParams p) {
 #pragma unroll
         for (int dt = 0; dt < C::DT; ++dt) dst[dt * 16] = to_bf16(o[qt][dt][r] * fin);
       }
+    }
+  }
+}
+
+// =====================================================================
+// FP8 P.V forward (hstu_attn_fwd_fp8_pv): the reference's production
+// forward contract DLRM_HSTU_FP8_FWD_PV=1 (ops/flydsl/hstu_flydsl_mha.py:
+// 2199-2330; the gin default, dlrm_v4/train/gin/yambda_5b.gin:3293-3319).
+// The SiLU output is rounded to e4m3 with a static scale s before P.V:
+//   P' = -log2(e) silu(x)    (the exp2-domain SiLU: x' = -log2(e) x,
+//                             P' = x' / (1 + 2^x'))
+//   P8 = e4m3_sat(P' s r_k), out = sum_k P8 v8_k 2^E(k) (-ln2 / (s N)) [s_v]
+// V stays raw e4m3 and P.V is an e4m3 MFMA.  With one per-tensor V scale
+// (the reference's qkv_scale) r_k = 1 and s_v rides on the output.  With
+// per-(token, head) V scales r_k = s_v(k) 2^-E(k), E(k) the frexp exponent
+// of the largest V scale among the 32 keys of the tile that share k's bit 4,
+// and 2^E(k) returns as the E8M0 block scale of the P.V MFMA.
+//
+// Block = 128 queries, 4 waves of 32; key tiles of 64.  All products are
+// 32x32x64 e4m3 MFMAs.  S = Q.K^T leaves a lane one key (column) and 16
+// queries, so the per-key scales and the sigmoid factor are lane scalars and
+// the 16 per-query factors stay in registers for the whole loop.  The e4m3 P
+// goes through a per-wave LDS region as P^T [key][query] (4-byte stores)
+// and comes back transposed (ds_read_b64_tr_b8) as the A operand of
+// O = P.V, with lane group g holding keys 32 g .. 32 g + 31; V's B operand
+// reads the same keys from the V tile, also transposed.  The S products of
+// the next 32-key sub-tile are issued before each sub-tile's epilogue, so the
+// matrix cores work through them while the wave runs the SiLU.
+// =====================================================================
+// The largest x over the 32 lanes of the wave that share bit 4 of the lane
+// index: DPP within each 16-lane row (lane ^ 1, ^ 2, then the mirrors that
+// pair quads and half-rows), then rows r and r + 2 through permlane32_swap.
+// All VALU: no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float max_lanes_same_bit4(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));   // quad_perm [1, 0, 3, 2]: lane ^ 1
+  x = fmaxf(x, dpp_f32<0x4E>(x));   // quad_perm [2, 3, 0, 1]: lane ^ 2
+  x = fmaxf(x, dpp_f32<0x141>(x));  // row_half_mirror: the other quad of 8
+  x = fmaxf(x, dpp_f32<0x140>(x));  // row_mirror: the other half of 16
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(x, __int_as_float((threadIdx.x & 32) ? sw[0] : sw[1]));
+}
+
+struct Pv8Cfg {
+  static constexpr int BM = 128, BN = 64;
+  // K ring of 3 tiles (tile t + 2 is staged while t and t + 1 are read),
+  // V ring of 2; 64 rows of 128 e4m3 bytes each, unpadded: chunk c of K row
+  // r at 16-byte slot c ^ swz128(r), of V row r at c ^ v_swz(r)
+  static constexpr int KT = BN * 128;
+  static constexpr int K_OFF = 0;
+  static constexpr int VS_OFF = 3 * KT;
+  // V stage: V rows, per key (s_k, c_k), 2 E8M0 bytes (as ints), BM + BN - 1 bias values
+  static constexpr int V_REL = 0, SC_REL = BN * 128, E8_REL = SC_REL + BN * 8, BIAS_REL = E8_REL + 16;
+  static constexpr int VSTAGE = BIAS_REL + (BM + BN) * 4;
+  static constexpr int P_OFF = VS_OFF + 2 * VSTAGE;  // per wave: P^T, 64 keys x 32 queries
+  static constexpr int LDS = P_OFF + 4 * BN * 32;
+  static_assert(VSTAGE % 16 == 0, "stage alignment");
+  __host__ __device__ static constexpr int v_swz(int r) { return r & 6; }
+};
+
+template <bool BIAS>
+__global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p) {
+  using C = Pv8Cfg;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  SeqCtx sc;
+  if (!seq_ctx(p, /*heavy_last=*/true, sc)) return;
+  const int L = sc.L, h = sc.h;
+  const int m0 = sc.blk * C::BM;
+  if (m0 >= L) return;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l32 = lane & 31, hg = lane >> 5, j16 = lane & 15, hi16 = (lane >> 4) & 1;
+  const int mw0 = m0 + 32 * wave;
+  const bool per_tensor = p.s_rs == 0;
+
+  const uint32_t krs = (uint32_t)p.k_rs, vrs = (uint32_t)p.v_rs;
+  const BufRsrc krsrc = make_rsrc(p.k + sc.start * p.k_rs + (int64_t)h * 128, L > 0 ? (L - 1) * krs + 128 : 0u);
+  const BufRsrc vrsrc = make_rsrc(p.v + sc.start * p.v_rs + (int64_t)h * 128, L > 0 ? (L - 1) * vrs + 128 : 0u);
+  const uint32_t s_step = (uint32_t)(p.s_rs * 4);
+  const uint32_t sbytes = (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4);
+  const BufRsrc sk_rsrc = make_rsrc(p.k_scale + sc.start * p.s_rs + h * p.s_hs, sbytes);
+  const BufRsrc sv_rsrc = make_rsrc(p.v_scale + sc.start * p.s_rs + h * p.s_hs, sbytes);
+  const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
+  const int R1 = p.bias_R - 1;
+
+  // staging: items tid and tid + 256 of each 64 x 8 chunk tile
+  uint32_t k_voff[2], v_voff[2], k_loff[2], v_loff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int item = tid + kThreads * i, row = item >> 3, ch = item & 7;
+    k_voff[i] = row * krs + 16 * ch;
+    v_voff[i] = row * vrs + 16 * ch;
+    k_loff[i] = row * 128 + 16 * (ch ^ swz128(row));
+    v_loff[i] = C::V_REL + row * 128 + 16 * (ch ^ C::v_swz(row));
+  }
+
+  // Q (A operand of S): query mw0 + l32, bytes 64 kk + 32 hg .. + 31 of its row
+  i32x8 qa[2];
+  float cq[16];  // -alpha log2(e) s_q of query 8 (j / 4) + 4 hg + j % 4
+  {
+    const int row = mw0 + l32;
+    const bool ok = row < L;
+    const uint8_t* src = p.q + (sc.start + row) * p.q_rs + (int64_t)h * 128 + 32 * hg;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      u32x4 lo = {0u, 0u, 0u, 0u}, hi = {0u, 0u, 0u, 0u};
+      if (ok) {
+        lo = *(const u32x4*)(src + 64 * kk);
+        hi = *(const u32x4*)(src + 64 * kk + 16);
+      }
+      qa[kk] = cat8(lo, hi);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int r = mw0 + 8 * (j >> 2) + 4 * hg + (j & 3);
+      const float s = r < L ? p.q_scale[(sc.start + r) * p.s_rs + h * p.s_hs] : 0.f;
+      cq[j] = -p.alpha * kLog2e * s;
+    }
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+
+  const int n_end = min(m0 + C::BM, L);
+  const int ntiles = (n_end + C::BN - 1) / C::BN;
+  // tiles this wave computes: key tile t is needed while 64 t <= mw0 + 31
+  const int wtiles = mw0 < L ? min(ntiles, (mw0 + 31) / C::BN + 1) : 0;
+
+  u32x4 stk[2], stv[2];
+  float st_sc = 0.f, st_bias = 0.f;
+  auto load_k = [&](int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) stk[i] = buf_ld128(krsrc, k_voff[i], n0 * krs);
+  };
+  auto load_v = [&](int n0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) stv[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
+    // wave 0: the tile's key scales, wave 1: its value scales (lane = key)
+    if (wave == 0) st_sc = buf_ldf(sk_rsrc, (uint32_t)lane * s_step, n0 * s_step);
+    else if (wave == 1) st_sc = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, n0 * s_step);
+    if constexpr (BIAS) {
+      // offsets i - j of the tile span [m0 - n0 - (BN - 1), m0 - n0 + BM - 1]
+      if (tid < C::BM + C::BN - 1) {
+        const int off = m0 - n0 - (C::BN - 1) + tid;
+        st_bias = biasb[min(max(off, -R1), R1) + R1];
+      }
+    }
+  };
+  auto store_k = [&](uint8_t* kbuf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *(u32x4*)(kbuf + k_loff[i]) = stk[i];
+  };
+  auto store_v = [&](uint8_t* vbuf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *(u32x4*)(vbuf + v_loff[i]) = stv[i];
+    float* scl = (float*)(vbuf + C::SC_REL);
+    if (wave == 0) {
+      scl[2 * lane] = st_sc;
+    } else if (wave == 1) {
+      // c_k = 1 / (s r_k), r_k = s_v 2^-E over the key's group (bit 4 of the key)
+      const float sv = st_sc;
+      float c = p.pv_c;
+      int e8 = 127;
+      if (!per_tensor) {
+        const float m = max_lanes_same_bit4(sv);
+        int e = 0;
+        if (m > 0.f) (void)frexpf(m, &e);
+        e8 = 127 + e;
+        if (sv > 0.f) c = ldexpf(p.pv_c * __builtin_amdgcn_rcpf(sv), e);
+      }
+      scl[2 * lane + 1] = c;
+      if ((lane & 47) == 0) ((int*)(vbuf + C::E8_REL))[lane >> 4] = e8;
+    }
+    if constexpr (BIAS) {
+      if (tid < C::BM + C::BN - 1) ((float*)(vbuf + C::BIAS_REL))[tid] = st_bias * -kLog2e;
+    }
+  };
+  auto kbuf = [&](int t) { return smem + C::K_OFF + (t % 3) * C::KT; };
+  auto vbuf = [&](int t) { return smem + C::VS_OFF + (t & 1) * C::VSTAGE; };
+
+  // K (B operand of S) reads: key 32 b + l32, chunks 4 kk + 2 hg + e at slots
+  // (4 kk + 2 hg + e) ^ swz128(32 b + l32) = ((2 hg + e) ^ swz128(l32)) ^ 4 (kk ^ b)
+  const int x0 = swz128(l32);
+  const int ka0 = l32 * 128 + 16 * ((2 * hg) ^ x0), ka1 = l32 * 128 + 16 * ((2 * hg + 1) ^ x0);
+  const int kx0 = ka0 ^ 64, kx1 = ka1 ^ 64;
+  // S of key sub-tile b (32 keys) of a K tile: lane key 32 b + l32, register j
+  // query 8 (j / 4) + 4 hg + j % 4
+  auto s_mfma = [&](const uint8_t* kt, int b) __attribute__((always_inline)) {
+    const uint8_t* kb = kt + 4096 * b;
+    const i32x8 k0 = cat8(lds_ld128(kb + (b ? kx0 : ka0)), lds_ld128(kb + (b ? kx1 : ka1)));
+    const i32x8 k1 = cat8(lds_ld128(kb + (b ? ka0 : kx0)), lds_ld128(kb + (b ? ka1 : kx1)));
+    f32x16 z;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) z[r] = 0.f;
+    return mfma32_fp8(qa[1], k1, mfma32_fp8(qa[0], k0, z));
+  };
+  // P^T stores: key row 32 b + l32 (32 bytes), dword (2 i + hg) ^ 2 ((l32 >> 3) & 3)
+  uint8_t* const pw = smem + C::P_OFF + 2048 * wave;
+  const int xp = (l32 >> 3) & 3;
+  int pst[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pst[i] = l32 * 32 + 4 * hg + 8 * (i ^ xp);
+  // bias index of (key sub-tile b, register j): bias_lo + 32 (1 - b) + 8 (j / 4) + j % 4
+  const int bias_lo = 32 * wave + 4 * hg - l32 + (C::BN - 1) - 32;
+  // SiLU epilogue of one key sub-tile into P^T (e4m3)
+  auto epilogue = [&](const f32x16& s, int b, int n0, const uint8_t* vb, auto masked_tag, auto bconst_tag) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool BCONST = decltype(bconst_tag)::value;
+    const float* bias_lds = (const float*)(vb + C::BIAS_REL);
+    const float* bias_lane = bias_lds + bias_lo;
+    const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
+    const f32x2 skc = *(const f32x2*)(vb + C::SC_REL + 8 * (32 * b + l32));
+    const int key = n0 + 32 * b + l32;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float pv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 4 * i + r;
+        float x = s[j] * (cq[j] * skc[0]);
+        if constexpr (BIAS) x += BCONST ? bconst : bias_lane[32 * (1 - b) + 8 * i + r];
+        // P' s r_k = x / ((2^x + 1) / (s r_k)), c_k = 1 / (s r_k)
+        float v = x * __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(x), skc[1], skc[1]));
+        if constexpr (MASKED) v = key <= mw0 + 8 * i + 4 * hg + r ? v : 0.f;
+        pv[r] = v;
+      }
+      *(uint32_t*)(pw + pst[i] + 1024 * b) = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
+    }
+  };
+  auto run_epilogue = [&](const f32x16& s, int b, int n0, const uint8_t* vb) __attribute__((always_inline)) {
+    const bool masked = n0 + 32 * b + 31 > mw0;
+    const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
+    if (masked) {
+      if (bias_const) epilogue(s, b, n0, vb, std::true_type{}, std::true_type{});
+      else epilogue(s, b, n0, vb, std::true_type{}, std::false_type{});
+    } else {
+      if (bias_const) epilogue(s, b, n0, vb, std::false_type{}, std::true_type{});
+      else epilogue(s, b, n0, vb, std::false_type{}, std::false_type{});
+    }
+  };
+  // P (A operand of P.V) reads, u = 0..3: key rows 32 hg + 8 u + j16 / 2,
+  // byte column 16 hi16 + 8 (j16 & 1) -> dword w ^ 2 u
+  int pld[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    pld[u] = (32 * hg + 8 * u + (j16 >> 1)) * 32 + 4 * ((4 * hi16 + 2 * (j16 & 1)) ^ (2 * u));
+  // V (B operand of P.V) reads for d block db: key rows 32 hg + 8 u + j16 / 2,
+  // chunk 2 db + hi16 at slot (2 db + hi16) ^ v_swz(row) (v_swz(row) = (j16 >> 1) & 6)
+  const int vsw = (j16 >> 1) & 6;
+  int vld[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+    vld[db] = C::V_REL + (32 * hg + (j16 >> 1)) * 128 + 16 * ((2 * db + hi16) ^ vsw) + 8 * (j16 & 1);
+
+  // prologue: K tiles 0 and 1, V tile 0, S of sub-tile (0, 0)
+  fp8_saturate_mode(true);
+  load_k(0);
+  load_v(0);
+  store_k(kbuf(0));
+  store_v(vbuf(0));
+  if (ntiles > 1) {
+    load_k(C::BN);
+    store_k(kbuf(1));
+  }
+  __syncthreads();
+  f32x16 s0, s1;
+  if (wtiles > 0) s0 = s_mfma(kbuf(0), 0);
+
+  // tile t: S(t, 1) runs on the matrix cores during the epilogue of (t, 0),
+  // S(t + 1, 0) during that of (t, 1); K is staged two tiles ahead, V one
+  for (int t = 0; t < ntiles; ++t) {
+    const int n0 = t * C::BN;
+    if (t + 2 < ntiles) load_k(n0 + 2 * C::BN);
+    if (t + 1 < ntiles) load_v(n0 + C::BN);
+    const uint8_t* vb = vbuf(t);
+    if (t < wtiles) {
+      s1 = s_mfma(kbuf(t), 1);
+      run_epilogue(s0, 0, n0, vb);
+      if (t + 1 < wtiles) s0 = s_mfma(kbuf(t + 1), 0);
+      run_epilogue(s1, 1, n0, vb);
+      // the wave's own P^T stores precede its transposed reads (LDS keeps a
+      // wave's operations in order); this only stops the compiler reordering
+      asm volatile("" ::: "memory");
+      i32x8 pa;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const u32x2 w = lds_tr8(pw + pld[u]);
+        pa[2 * u] = (int)w[0];
+        pa[2 * u + 1] = (int)w[1];
+      }
+      const int e8v = ((const int*)(vb + C::E8_REL))[hg];
+      // ---- O += P.V, V's group scales as the B operand's E8M0
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        i32x8 bv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const u32x2 w = lds_tr8(vb + vld[db] + 1024 * u);
+          bv[2 * u] = (int)w[0];
+          bv[2 * u + 1] = (int)w[1];
+        }
+        o[db] = mfma32_fp8_scaled(pa, bv, o[db], 127, e8v);
+      }
+    }
+    if (t + 2 < ntiles) store_k(kbuf(t + 2));
+    if (t + 1 < ntiles) store_v(vbuf(t + 1));
+    __syncthreads();
+  }
+  fp8_saturate_mode(false);
+
+  if (mw0 >= L) return;
+  float fin = -kLn2 * p.inv_n * p.pv_out;
+  if (per_tensor) fin *= p.v_scale[0];
+  // lane: d = 32 db + l32, register j: query 8 (j / 4) + 4 hg + j % 4
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int row = mw0 + 8 * (j >> 2) + 4 * hg + (j & 3);
+    if (row < L) {
+      uint16_t* dst = p.out + (sc.start + row) * p.o_rs + (int64_t)h * 128 + l32;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) dst[32 * db] = to_bf16(o[db][j] * fin);
     }
   }
 }
@@ -2446,7 +2775,7 @@ int fwd_launch(int dtype, const void* q, const void* k, const void* v, int64_t q
                int64_t scale_row_stride, int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
                int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len, int contextual_seq_len,
                const float* attn_bias, int bias_R, void* out, int64_t out_row_stride, int* sched_ws,
-               hipStream_t stream) {
+               hipStream_t stream, float pv_scale = 0.f) {
   AttnParams p{};
   p.q = (const uint8_t*)q;
   p.k = (const uint8_t*)k;
@@ -2480,7 +2809,15 @@ int fwd_launch(int dtype, const void* q, const void* k, const void* v, int64_t q
 #define HSTU_FWD(DD, F8, G, BB) launch(hstu_fwd_kernel<DD, F8, G, BB>, FwdCfg<DD, F8>::LDS, grid, p, stream)
 #define HSTU_FWD_B(DD, F8, G) (has_bias ? HSTU_FWD(DD, F8, G, true) : HSTU_FWD(DD, F8, G, false))
   const bool has_bias = attn_bias != nullptr;
-  if (dtype == HSTU_DTYPE_FP8_E4M3) {
+  if (pv_scale > 0.f) {
+    // FP8 P.V: P8 = e4m3(P' s); pv_c = 2^-3 f32(2^3 / s) is f32(1 / s) up to
+    // its last bit, and makes P' s the product the reference's cast divides
+    // by 2^-3 (hstu_fwd.py pv_s)
+    p.pv_c = (float)(8.0f / pv_scale) * 0.125f;
+    p.pv_out = 1.0f / pv_scale;
+    e = has_bias ? launch(hstu_fwd_pv8_kernel<true>, Pv8Cfg::LDS, grid, p, stream)
+                 : launch(hstu_fwd_pv8_kernel<false>, Pv8Cfg::LDS, grid, p, stream);
+  } else if (dtype == HSTU_DTYPE_FP8_E4M3) {
     e = generic ? HSTU_FWD_B(128, true, true) : HSTU_FWD_B(128, true, false);
   } else if (D == 128) {
     e = generic ? HSTU_FWD_B(128, false, true) : HSTU_FWD_B(128, false, false);
@@ -2513,6 +2850,27 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
                     scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, num_targets,
                     max_attn_len, contextual_seq_len, attn_bias, bias_R, out, out_row_stride, (int*)workspace,
                     stream);
+}
+
+extern "C" int hstu_attn_fwd_fp8_pv(const void* q, const void* k, const void* v, int64_t q_row_stride,
+                                    int64_t k_row_stride, int64_t v_row_stride, const float* q_scale,
+                                    const float* k_scale, const float* v_scale, int64_t scale_row_stride,
+                                    int64_t scale_head_stride, const int64_t* seq_offsets, int B, int H, int D,
+                                    int max_seq_len, float alpha, const int32_t* num_targets, int max_attn_len,
+                                    int contextual_seq_len, const float* attn_bias, int bias_R, float pv_scale,
+                                    void* out, int64_t out_row_stride, void* workspace, int64_t workspace_bytes,
+                                    int64_t total_tokens, hipStream_t stream) {
+  const int c = fwd_check(HSTU_DTYPE_FP8_E4M3, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
+                          v_scale, B, H, D, max_seq_len, attn_bias, bias_R, total_tokens);
+  if (c != 0) return c;
+  if (!(pv_scale > 0.f) || !(pv_scale < 448.f)) return HSTU_E_BAD_ARG;
+  // the causal mask only (the reference arms FP8 P.V on its causal config)
+  if (num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0) return HSTU_E_UNSUPPORTED;
+  if (B == 0) return 0;
+  if (workspace == nullptr || workspace_bytes < fwd_workspace_bytes(B, H)) return HSTU_E_BAD_ARG;
+  return fwd_launch(HSTU_DTYPE_FP8_E4M3, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
+                    v_scale, scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, nullptr, 0,
+                    0, attn_bias, bias_R, out, out_row_stride, (int*)workspace, stream, pv_scale);
 }
 
 // ---------------------------------------------------------------------------

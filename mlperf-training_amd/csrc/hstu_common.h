@@ -16,6 +16,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -30,6 +31,19 @@ __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
 // v_mfma_f32_16x16x128_f8f6f4).
 __device__ __forceinline__ f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// e4m3 x e4m3, 32x32x64.  Lane l: row (A) / column (B) l % 32, K group
+// l / 32 (32 bytes); byte j of group g pairs with byte j of group g of the
+// other operand.  The accumulator: lane l, register r holds row
+// 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32 (probed on gfx950).
+__device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+// The same with E8M0 block scales: bytes 16 b .. 16 b + 15 of both K groups
+// of row (column) i are scaled by 2^(byte - 127) of lane 32 b + i's sa (sb)
+// (probed on gfx950).
+__device__ __forceinline__ f32x16 mfma32_fp8_scaled(i32x8 a, i32x8 b, f32x16 c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
 }
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   f32x2 v = {lo, hi};
@@ -115,8 +129,6 @@ __device__ __forceinline__ f32x4 mfma_fp8_scaled(i32x8 a, i32x8 b, f32x4 c, int 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
 }
 
-// Four floats -> four e4m3 bytes (RNE).  The conversion does not saturate
-// (out-of-range values become NaN): callers clamp to +-448 first.
 // MODE.FP16_OVFL (MODE bit 23) of the wave.  Set, v_cvt_pk_fp8_f32 turns
 // every finite input beyond the e4m3 range into +-448 instead of NaN -- the
 // same byte as a clamp to +-448 followed by the conversion (probed on gfx950
@@ -129,8 +141,13 @@ __device__ __forceinline__ void fp8_saturate_mode(bool on) {
   else asm volatile("s_setreg_imm32_b32 hwreg(HW_REG_MODE, 23, 1), 0\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+// Four floats -> four e4m3 bytes (RNE).  By default the conversion does not
+// saturate (out-of-range values become NaN): callers clamp to +-448 first or
+// run under fp8_saturate_mode(true).
 __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c, float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // the first conversion writes the low half and keeps the high half of its
+  // old operand, which the second one overwrites: any register will do
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, c), false);
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
 }
 

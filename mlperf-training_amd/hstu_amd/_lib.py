@@ -30,6 +30,7 @@ HSTU_E_SCRATCH_TOO_SMALL = -3
 EXPORTED_SYMBOLS = (
     "hstu_version",
     "hstu_attn_fwd",
+    "hstu_attn_fwd_fp8_pv",
     "hstu_attn_bwd",
     "hstu_attn_fwd_workspace_bytes",
     "hstu_attn_bwd_workspace_bytes",
@@ -86,6 +87,11 @@ _SIGNATURES = {
         _i32,
         [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
          _f32, _vp, _i32, _i32, _vp, _i32, _vp, _i64, _vp, _i64, _i64, _vp],
+    ),
+    "hstu_attn_fwd_fp8_pv": (
+        _i32,
+        [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
+         _f32, _vp, _i32, _i32, _vp, _i32, _f32, _vp, _i64, _vp, _i64, _i64, _vp],
     ),
     "hstu_attn_fwd_workspace_bytes": (_i64, [_i32, _i64, _i32, _i32, _i32, _i32]),
     "hstu_attn_fwd_noalloc": (

@@ -28,6 +28,7 @@ the kernel ops raise -- there is no silent fallback to another backend.
 from __future__ import annotations
 
 import logging
+import os
 from enum import Enum, unique
 from typing import Optional, Tuple, Union
 
@@ -152,7 +153,7 @@ def _stream(device) -> int:
 # raw launches
 # ---------------------------------------------------------------------------
 def _launch_fwd(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len, contextual_seq_len,
-                q_scale, k_scale, v_scale, attn_bias) -> torch.Tensor:
+                q_scale, k_scale, v_scale, attn_bias, pv_scale: float = 0.0) -> torch.Tensor:
     T, H, D = q.shape
     out = torch.empty((T, H, D), dtype=torch.bfloat16, device=q.device)
     if T == 0:
@@ -179,6 +180,18 @@ def _launch_fwd(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len, conte
     dt = _lib.HSTU_DTYPE_FP8_E4M3 if fp8 else _lib.HSTU_DTYPE_BF16
     B = offs.numel() - 1
     ws = _workspace(_lib.fn("hstu_attn_fwd_workspace_bytes")(dt, T, B, H, D, int(N)), q.device)
+    if pv_scale > 0.0:
+        if not fp8:
+            raise ValueError("the FP8 P.V forward takes e4m3 inputs")
+        st = _lib.fn("hstu_attn_fwd_fp8_pv")(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), _row_stride(q), _row_stride(k), _row_stride(v),
+            _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs), srs, shs,
+            offs.data_ptr(), B, H, D, int(N), float(alpha),
+            _lib.ptr(nt), int(max_attn_len), int(contextual_seq_len),
+            _lib.ptr(bias), R, float(pv_scale),
+            out.data_ptr(), H * D, ws.data_ptr(), ws.numel(), T, _stream(q.device))
+        _lib.check(st, "hstu_attn_fwd_fp8_pv")
+        return out
     st = _lib.fn("hstu_attn_fwd")(
         dt,
         q.data_ptr(), k.data_ptr(), v.data_ptr(), _row_stride(q), _row_stride(k), _row_stride(v),
@@ -283,6 +296,54 @@ def _launch_bwd_fp8(dout8, e8, q, k, v, dq, dk, dv, seq_offsets, N, alpha, q_sca
             dst.copy_(src)
 
 
+# FP8 P.V forward switch and scale: the reference's DLRM_HSTU_FP8_FWD_PV and
+# DLRM_HSTU_FP8_FWD_PV_SCALE (ops/flydsl/hstu_flydsl_mha.py:2199-2264), read per call.
+FP8_FWD_PV_SCALE_DEFAULT = 10.04
+FP8_FWD_PV_POW2 = 8.0  # 2^pv_k, pv_k = 3
+_FP8_FWD_PV_SCALE_RANGE = (4.0, 32.0)
+
+
+def fp8_fwd_pv_enabled() -> bool:
+    """``DLRM_HSTU_FP8_FWD_PV=1`` (exactly "1"; anything else is off)."""
+    return os.environ.get("DLRM_HSTU_FP8_FWD_PV", "0") == "1"
+
+
+def fp8_fwd_pv_scale() -> float:
+    """The static P scale s of the FP8 P.V forward: ``DLRM_HSTU_FP8_FWD_PV_SCALE``
+    unset or empty = 10.04; ``pow2`` or ``0`` = 2^3; otherwise a float in
+    [4, 32], rounded to 6 decimals.  Anything else raises ValueError (a typo
+    must not silently change the cast)."""
+    raw = os.environ.get("DLRM_HSTU_FP8_FWD_PV_SCALE", "")
+    v = raw.strip().lower()
+    if v == "":
+        return FP8_FWD_PV_SCALE_DEFAULT
+    if v == "pow2":
+        return FP8_FWD_PV_POW2
+    try:
+        x = float(v)
+    except ValueError:
+        x = float("nan")
+    if x == 0.0:
+        return FP8_FWD_PV_POW2
+    lo, hi = _FP8_FWD_PV_SCALE_RANGE
+    if not (lo <= x <= hi):  # also rejects nan / inf
+        raise ValueError(f"DLRM_HSTU_FP8_FWD_PV_SCALE={raw!r}: use unset (10.04), 'pow2', '0' or a float in "
+                         f"[{lo:g}, {hi:g}]")
+    return round(x, 6)
+
+
+def fp8_pv_fwd_reason(q: torch.Tensor, num_targets, max_attn_len: int, contextual_seq_len: int) -> Optional[str]:
+    """None when the FP8 P.V forward kernel serves this call (e4m3 inputs,
+    D = 128, the causal mask), else why not."""
+    if not _is_fp8(q):
+        return "inputs are not e4m3"
+    if q.shape[2] != 128:
+        return f"head dim {q.shape[2]}"
+    if num_targets is not None or max_attn_len > 0 or contextual_seq_len > 0:
+        return "num_targets / max_attn_len / contextual_seq_len masks"
+    return None
+
+
 def full_fp8_bwd_reason(q: torch.Tensor, num_targets, max_attn_len: int, contextual_seq_len: int) -> Optional[str]:
     """None when the full-FP8 backward kernels serve this call (e4m3 inputs,
     D = 128, the causal mask), else why not."""
@@ -313,14 +374,15 @@ def _op_fwd(
     k_scale: Optional[torch.Tensor],
     v_scale: Optional[torch.Tensor],
     attn_bias: Optional[torch.Tensor],
+    pv_scale: float = 0.0,
 ) -> torch.Tensor:
     return _launch_fwd(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len, contextual_seq_len,
-                       q_scale, k_scale, v_scale, attn_bias)
+                       q_scale, k_scale, v_scale, attn_bias, pv_scale)
 
 
 @_op_fwd.register_fake
 def _op_fwd_fake(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len, contextual_seq_len,
-                 q_scale, k_scale, v_scale, attn_bias):
+                 q_scale, k_scale, v_scale, attn_bias, pv_scale=0.0):
     return q.new_empty((q.shape[0], q.shape[1], v.shape[2]), dtype=torch.bfloat16)
 
 
@@ -397,23 +459,38 @@ def triton_hstu_attention_fwd(
     v_scale: ScaleArg = 1.0,
     *,
     attn_bias: Optional[torch.Tensor] = None,
+    fp8_pv: Optional[bool] = None,
 ) -> torch.Tensor:
     """Forward op with the reference's argument list
     (``triton_hstu_attention.py:3166-3185``).  Allocates and returns the
     [T, H, D] bf16 output.  ``sort_by_length_indices`` and ``enable_tma`` are
     scheduling hints of the reference kernel and do not change results: the HIP
-    grid already issues the longest blocks first."""
+    grid already issues the longest blocks first.
+
+    ``fp8_pv`` (None: ``DLRM_HSTU_FP8_FWD_PV``): for e4m3 inputs, the
+    reference's FP8 P.V forward -- the SiLU output rounded to e4m3 with the
+    static scale of ``DLRM_HSTU_FP8_FWD_PV_SCALE`` and P.V on the e4m3 MFMA
+    (``hstu_attn_fwd_fp8_pv``), a declared precision change.  A call it does
+    not serve (the targets / window / contextual masks) runs the bf16-P
+    forward, with the reason logged once, as the reference declines."""
     del sort_by_length_indices, enable_tma
     reason = unsupported_shape_reason(q, k, v, num_softmax_heads)
     if reason is not None:
         raise NotImplementedError(f"HIP HSTU attention forward: {reason}")
     fp8 = _is_fp8(q)
+    pv_scale = 0.0
+    if fp8 and (fp8_fwd_pv_enabled() if fp8_pv is None else fp8_pv):
+        why = fp8_pv_fwd_reason(q, num_targets, int(max_attn_len), int(contextual_seq_len))
+        if why is None:
+            pv_scale = fp8_fwd_pv_scale()
+        else:
+            _log_once(f"FP8 P.V forward: {why}; the bf16-P forward runs")
     return _op_fwd(int(N), float(alpha), q, k, v, seq_offsets, num_targets, int(max_attn_len),
                    int(contextual_seq_len),
                    _scale_or_none(q_scale, q) if fp8 else None,
                    _scale_or_none(k_scale, q) if fp8 else None,
                    _scale_or_none(v_scale, q) if fp8 else None,
-                   attn_bias)
+                   attn_bias, pv_scale)
 
 
 def triton_hstu_attention_bwd(
@@ -494,7 +571,7 @@ def _log_once(reason: str) -> None:
 def try_hstu_attention_fwd(
     *, q, k, v, seq_offsets, num_targets, N, alpha, max_attn_len, contextual_seq_len,
     num_softmax_heads=0, q_scale: ScaleArg = None, k_scale: ScaleArg = None, v_scale: ScaleArg = None,
-    attn_bias=None,
+    attn_bias=None, fp8_pv: Optional[bool] = None,
 ) -> Optional[torch.Tensor]:
     """The HIP forward, or None (reason logged once) when the shape is outside
     the kernels' specialisation.  Host problems raise."""
@@ -504,7 +581,7 @@ def try_hstu_attention_fwd(
         return None
     return triton_hstu_attention_fwd(N, alpha, q, k, v, seq_offsets, num_targets, max_attn_len,
                                      contextual_seq_len, None, False, num_softmax_heads,
-                                     q_scale, k_scale, v_scale, attn_bias=attn_bias)
+                                     q_scale, k_scale, v_scale, attn_bias=attn_bias, fp8_pv=fp8_pv)
 
 
 def try_hstu_attention_bwd(

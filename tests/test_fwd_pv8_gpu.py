@@ -1,0 +1,159 @@
+"""GPU parity of the FP8 P.V forward (``hstu_attn_fwd_fp8_pv``, the
+reference's DLRM_HSTU_FP8_FWD_PV=1 contract) against the CPU oracle.
+
+Tolerances (stated bar):
+* against ``oracle/hstu_fwd_pv8_oracle.fwd_pv8`` -- the same e4m3 cast of P
+  evaluated in float64: relative L2 <= 5e-3 and max |err| <= 5e-2 max |ref|
+  (a P byte rounds the other way where the kernel's fp32 P' s r sits within
+  fp32 rounding of an e4m3 midpoint);
+* against the unquantized float64 forward on the dequantized inputs (the
+  contract's own e4m3 error of P, 2.6 % relative L2 in the oracle): relative
+  L2 <= 3.5e-2 and SNR >= 28 dB.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hstu_fwd_pv8_oracle as PV
+from oracle import hstu_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _ops():
+    import hstu_amd
+
+    return hstu_amd
+
+
+def _case(lengths, H=2, D=128, seed=0, per_tensor=False, std=1.0):
+    q, k, v = orc.make_qkv(lengths, H, D, std, seed=seed)
+    offs = orc.offsets_from_lengths(lengths)
+    if per_tensor:
+        outs = []
+        for t in (q, k, v):
+            x8, s = orc.quantize_e4m3_per_tensor(t)
+            outs.append((x8, s.reshape(1).float()))
+    else:
+        outs = [orc.quantize_e4m3_rows(t, dim=-1) for t in (q, k, v)]
+    (q8, sq), (k8, sk), (v8, sv) = outs
+    return q8, k8, v8, sq, sk, sv, offs
+
+
+def _check(got, want, exact, what):
+    got = got.float().cpu().double()
+    e = orc.rel_l2(want, got)
+    mx = float((got - want).abs().max() / want.abs().max())
+    assert e <= 5e-3 and mx <= 5e-2, f"{what}: rel L2 {e:.3e}, max {mx:.3e} vs the same-cast oracle"
+    e2, snr = orc.rel_l2(exact, got), orc.snr_db(exact, got)
+    assert e2 <= 3.5e-2 and snr >= 28.0, f"{what}: rel L2 {e2:.3e}, SNR {snr:.1f} dB vs the unquantized forward"
+
+
+def _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias, **kw):
+    dev = [t.to(DEV) for t in (q8, k8, v8)]
+    sc = [s.to(DEV) for s in (sq, sk, sv)]
+    out = ops.triton_hstu_attention_fwd(N, alpha, *dev, offs.to(DEV), kw.pop("num_targets", None), 0, 0, None,
+                                        False, 0, *sc, attn_bias=None if bias is None else bias.to(DEV), **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+LENGTH_CASES = [
+    [1],
+    [5, 17, 64],
+    [221, 169, 139, 81, 90, 25, 34, 19],
+    [128, 256, 1, 300, 0, 77],
+    [600, 1000, 63, 65],
+]
+
+
+@pytest.mark.parametrize("lengths", LENGTH_CASES)
+@pytest.mark.parametrize("per_tensor", [False, True])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fwd_pv8(hip_lib, lengths, per_tensor, with_bias):
+    ops = _ops()
+    N = max(max(lengths), 1)
+    alpha = 1.0 / 128 ** 0.5
+    q8, k8, v8, sq, sk, sv, offs = _case(lengths, per_tensor=per_tensor, seed=len(lengths))
+    bias = orc.make_bias(2, 512) if with_bias else None
+    print(f"FP8 P.V fwd: lengths={lengths} per_tensor={per_tensor} bias={with_bias}", flush=True)
+    out = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias, fp8_pv=True)
+    want = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias)
+    exact = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias, quantize=False)
+    assert torch.isfinite(out.float()).all()
+    if sum(lengths) > 1:
+        _check(out, want, exact, f"lengths={lengths}")
+
+
+def test_fwd_pv8_env_switch_and_scale(hip_lib, monkeypatch):
+    """DLRM_HSTU_FP8_FWD_PV=1 arms it with the scale of
+    DLRM_HSTU_FP8_FWD_PV_SCALE (here 16 and pow2 = 8), matching the oracle at
+    that scale; without the switch the bf16-P forward runs, bitwise equal to
+    fp8_pv=False."""
+    ops = _ops()
+    lengths = [300, 77, 129]
+    N = 300
+    alpha = 1.0 / 128 ** 0.5
+    q8, k8, v8, sq, sk, sv, offs = _case(lengths, seed=11)
+    bias = orc.make_bias(2, 256)
+    exact = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias, quantize=False)
+    monkeypatch.setenv("DLRM_HSTU_FP8_FWD_PV", "1")
+    for raw, s in (("16", 16.0), ("pow2", 8.0)):
+        monkeypatch.setenv("DLRM_HSTU_FP8_FWD_PV_SCALE", raw)
+        out = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias)
+        want = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias, pv_scale=s)
+        _check(out, want, exact, f"scale {raw}")
+    monkeypatch.delenv("DLRM_HSTU_FP8_FWD_PV_SCALE")
+    monkeypatch.delenv("DLRM_HSTU_FP8_FWD_PV")
+    off = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias)
+    bf16p = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias, fp8_pv=False)
+    assert torch.equal(off, bf16p)
+
+
+def test_fwd_pv8_declines_generic_masks(hip_lib):
+    """With num_targets the FP8 P.V kernel does not serve the call: the
+    bf16-P forward runs (logged), bitwise equal to fp8_pv=False."""
+    ops = _ops()
+    lengths = [200, 64, 130]
+    N = 200
+    alpha = 1.0 / 128 ** 0.5
+    q8, k8, v8, sq, sk, sv, offs = _case(lengths, seed=2)
+    nt = torch.tensor([5, 0, 17], dtype=torch.int64, device=DEV)
+    a = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, None, num_targets=nt, fp8_pv=True)
+    b = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, None, num_targets=nt, fp8_pv=False)
+    assert torch.equal(a, b)
+
+
+def test_fwd_pv8_config3(hip_lib):
+    """Config 3 in full (B=128, N=4096, per-(token, head) scales, bias
+    [4, 2047]) through the FP8 P.V forward: sampled sequences incl. the
+    longest against the oracle, and a sub-batch bitwise equal to the same rows
+    of the full batch (the V scale groups are per sequence)."""
+    ops = _ops()
+    lengths = orc.lengths_for_config(3)
+    H, D, N = 4, 128, 4096
+    q, k, v = orc.make_qkv(lengths, H, D, 1.0, seed=0)
+    (q8, sq), (k8, sk), (v8, sv) = (orc.quantize_e4m3_rows(x, dim=-1) for x in (q, k, v))
+    bias = orc.make_bias(H, 1024)
+    offs = orc.offsets_from_lengths(lengths)
+    alpha = 1.0 / D ** 0.5
+    print("config 3 FP8 P.V fwd: full batch", flush=True)
+    full = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias, fp8_pv=True).cpu()
+    assert torch.isfinite(full.float()).all()
+    order = np.argsort(lengths)
+    sample = sorted({int(order[-1]), int(order[len(order) // 2]), int(order[0]), int(order[int(len(order) * 0.9)])})
+    assert int(max(lengths[sample])) == 4096
+    rows = torch.cat([torch.arange(int(offs[b]), int(offs[b + 1])) for b in sample])
+    sub_len = lengths[sample]
+    sub_offs = orc.offsets_from_lengths(sub_len)
+    args = (N, alpha, q8[rows], k8[rows], v8[rows], sq[rows], sk[rows], sv[rows], sub_offs)
+    want = PV.fwd_pv8(*args, attn_bias=bias)
+    exact = PV.fwd_pv8(*args, attn_bias=bias, quantize=False)
+    _check(full[rows], want, exact, "config 3 sampled sequences")
+    print("config 3 FP8 P.V fwd: sub-batch", flush=True)
+    sub = _run(ops, N, alpha, q8[rows], k8[rows], v8[rows], sq[rows], sk[rows], sv[rows], sub_offs, bias,
+               fp8_pv=True).cpu()
+    assert torch.equal(sub, full[rows])
