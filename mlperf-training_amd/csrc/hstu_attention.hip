@@ -1086,8 +1086,24 @@ __device__ __forceinline__ void diag_accumulate(float (&a)[4], const float (&v)[
   a[LO] += dpp_row<0x11D>(v[3]);
 }
 
-__device__ __forceinline__ float bperm(int src_lane, float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src_lane << 2, __builtin_bit_cast(int, x)));
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_rows(float old, float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, x), CTRL, ROWS, 0xF, false));
+}
+// lane (g, p) of row g <- lane (g, (p + 4 g) mod 16): row_ror by 16 - 4 g on rows 1..3
+__device__ __forceinline__ float skew_undo(float x) {
+  float y = dpp_rows<0x12C, 0x2>(x, x);
+  y = dpp_rows<0x128, 0x4>(y, x);
+  return dpp_rows<0x124, 0x8>(y, x);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? s[0] : s[1]);
+}
+__device__ __forceinline__ float lane_xor16(float x) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? s[0] : s[1]);
 }
 
 // Sum over the wave of diagonal p + 16(1-g) for lane 16g+p (g = 3, p = 0 is
@@ -1095,18 +1111,18 @@ __device__ __forceinline__ float bperm(int src_lane, float x) {
 __device__ __forceinline__ float diag_reduce(const float (&a)[4], int lane) {
   const int g = lane >> 4, p = lane & 15;
   // undo the 4g skew: lane (g, p) reads lane (g, p + 4g mod 16); wrapped
-  // reads land one bucket (16 diagonals) lower
+  // reads land one bucket (16 diagonals) lower.  DPP and permlane swaps
+  // only: no LDS round trip
   const bool wrap = p + 4 * g >= 16;
-  const int src = 16 * g + ((p + 4 * g) & 15);
-  const float g0 = bperm(src, a[0]), g1 = bperm(src, a[1]), g2 = bperm(src, a[2]), g3 = bperm(src, a[3]);
+  const float g0 = skew_undo(a[0]), g1 = skew_undo(a[1]), g2 = skew_undo(a[2]), g3 = skew_undo(a[3]);
   const float b0 = wrap ? 0.f : g0, b1 = wrap ? g0 : g1, b2 = wrap ? g1 : g2, b3 = wrap ? g2 : g3;
   // reduce-scatter over the four rows: row g keeps bucket g
   const bool upper = lane >= 32, odd = (g & 1) != 0;
   float ka = upper ? b2 : b0, kb = upper ? b3 : b1;
   const float sa = upper ? b0 : b2, sb = upper ? b1 : b3;
-  ka += bperm(lane ^ 32, sa);
-  kb += bperm(lane ^ 32, sb);
-  return (odd ? kb : ka) + bperm(lane ^ 16, odd ? ka : kb);
+  ka += lane_xor32(sa);
+  kb += lane_xor32(sb);
+  return (odd ? kb : ka) + lane_xor16(odd ? ka : kb);
 }
 
 template <int D, bool FP8, bool GENERIC, bool BIAS>
