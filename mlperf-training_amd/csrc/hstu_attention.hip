@@ -2201,7 +2201,9 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    lds_dma_wait();  // the next stage's DMA (and this tile's dS stores) done
+    // the next stage's DMA done; this tile's two dS stores, the last vector
+    // memory operations issued, may stay in flight
+    wait_vm_le<2>();
     __syncthreads();
   };
 
