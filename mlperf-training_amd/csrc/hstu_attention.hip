@@ -826,12 +826,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     for (int r = 0; r < 16; ++r) z[r] = 0.f;
     return mfma32_fp8(qa[1], k1, mfma32_fp8(qa[0], k0, z));
   };
-  // P^T stores: key row 32 b + l32 (32 bytes), dword (2 i + hg) ^ 2 ((l32 >> 3) & 3)
+  // P^T: key row 32 b + l32 (32 bytes); byte 16 hg + 4 i + r holds query
+  // 8 i + 4 hg + r, so a lane stores its 16 bytes at once, in 16-byte chunk
+  // hg ^ ((row >> 3) & 1) (16 consecutive rows of a store on distinct banks)
   uint8_t* const pw = smem + C::P_OFF + 2048 * wave;
-  const int xp = (l32 >> 3) & 3;
-  int pst[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pst[i] = l32 * 32 + 4 * hg + 8 * (i ^ xp);
+  const int pst = l32 * 32 + 16 * (hg ^ ((l32 >> 3) & 1));
   // bias index of (key sub-tile b, register j): bias_lo + 32 (1 - b) + 8 (j / 4) + j % 4
   const int bias_lo = 32 * wave + 4 * hg - l32 + (C::BN - 1) - 32;
   // SiLU epilogue of one key sub-tile into P^T (e4m3)
@@ -843,6 +842,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
     const f32x2 skc = *(const f32x2*)(vb + C::SC_REL + 8 * (32 * b + l32));
     const int key = n0 + 32 * b + l32;
+    u32x4 pk;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float pv[4];
@@ -856,8 +856,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
         if constexpr (MASKED) v = key <= mw0 + 8 * i + 4 * hg + r ? v : 0.f;
         pv[r] = v;
       }
-      *(uint32_t*)(pw + pst[i] + 1024 * b) = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
+      pk[i] = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
     }
+    *(u32x4*)(pw + pst + 1024 * b) = pk;
   };
   auto run_epilogue = [&](const f32x16& s, int b, int n0, const uint8_t* vb) __attribute__((always_inline)) {
     const bool masked = n0 + 32 * b + 31 > mw0;
@@ -871,11 +872,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     }
   };
   // P (A operand of P.V) reads, u = 0..3: key rows 32 hg + 8 u + j16 / 2,
-  // byte column 16 hi16 + 8 (j16 & 1) -> dword w ^ 2 u
+  // byte column 16 hi16 + 8 (j16 & 1), in chunk hi16 ^ (u & 1); lane l32 of
+  // the operand then holds query 8 ((l32 & 15) >> 2) + 4 (l32 >> 4) + (l32 & 3)
   int pld[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u)
-    pld[u] = (32 * hg + 8 * u + (j16 >> 1)) * 32 + 4 * ((4 * hi16 + 2 * (j16 & 1)) ^ (2 * u));
+    pld[u] = (32 * hg + 8 * u + (j16 >> 1)) * 32 + 16 * (hi16 ^ (u & 1)) + 8 * (j16 & 1);
   // V (B operand of P.V) reads for d block db: key rows 32 hg + 8 u + j16 / 2,
   // chunk 2 db + hi16 at slot (2 db + hi16) ^ v_swz(row) (v_swz(row) = (j16 >> 1) & 6)
   const int vsw = (j16 >> 1) & 6;
@@ -943,10 +945,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   if (mw0 >= L) return;
   float fin = -kLn2 * p.inv_n * p.pv_out;
   if (per_tensor) fin *= p.v_scale[0];
-  // lane: d = 32 db + l32, register j: query 8 (j / 4) + 4 hg + j % 4
+  // lane: d = 32 db + l32, register j: operand row 8 i + 4 hg + r (i = j / 4,
+  // r = j % 4), which is query 16 (i & 1) + 8 hg + 4 (i >> 1) + r (the P^T byte order)
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    const int row = mw0 + 8 * (j >> 2) + 4 * hg + (j & 3);
+    const int i = j >> 2;
+    const int row = mw0 + 16 * (i & 1) + 8 * hg + 4 * (i >> 1) + (j & 3);
     if (row < L) {
       uint16_t* dst = p.out + (sc.start + row) * p.o_rs + (int64_t)h * 128 + l32;
 #pragma unroll
