@@ -828,9 +828,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   };
   // P^T: key row 32 b + l32 (32 bytes); byte 16 hg + 4 i + r holds query
   // 8 i + 4 hg + r, so a lane stores its 16 bytes at once, in 16-byte chunk
-  // hg ^ ((row >> 3) & 1) (16 consecutive rows of a store on distinct banks)
+  // hg ^ ((row >> 2) & 1): a store's 8-lane passes (8 rows) then cover all
+  // 32 banks, and so do the transposed reads' 16-lane passes
   uint8_t* const pw = smem + C::P_OFF + 2048 * wave;
-  const int pst = l32 * 32 + 16 * (hg ^ ((l32 >> 3) & 1));
+  const int pst = l32 * 32 + 16 * (hg ^ ((l32 >> 2) & 1));
   // bias index of (key sub-tile b, register j): bias_lo + 32 (1 - b) + 8 (j / 4) + j % 4
   const int bias_lo = 32 * wave + 4 * hg - l32 + (C::BN - 1) - 32;
   // SiLU epilogue of one key sub-tile into P^T (e4m3)
@@ -872,12 +873,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     }
   };
   // P (A operand of P.V) reads, u = 0..3: key rows 32 hg + 8 u + j16 / 2,
-  // byte column 16 hi16 + 8 (j16 & 1), in chunk hi16 ^ (u & 1); lane l32 of
-  // the operand then holds query 8 ((l32 & 15) >> 2) + 4 (l32 >> 4) + (l32 & 3)
+  // byte column 16 hi16 + 8 (j16 & 1), in chunk hi16 ^ (j16 >> 3); lane l32
+  // of the operand then holds query 8 ((l32 & 15) >> 2) + 4 (l32 >> 4) + (l32 & 3)
   int pld[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u)
-    pld[u] = (32 * hg + 8 * u + (j16 >> 1)) * 32 + 16 * (hi16 ^ (u & 1)) + 8 * (j16 & 1);
+    pld[u] = (32 * hg + 8 * u + (j16 >> 1)) * 32 + 16 * (hi16 ^ (j16 >> 3)) + 8 * (j16 & 1);
   // V (B operand of P.V) reads for d block db: key rows 32 hg + 8 u + j16 / 2,
   // chunk 2 db + hi16 at slot (2 db + hi16) ^ v_swz(row) (v_swz(row) = (j16 >> 1) & 6)
   const int vsw = (j16 >> 1) & 6;
@@ -1977,12 +1978,16 @@ struct F8Bwd {
   static constexpr int STAGE = B_OFF + 256 * 4;
   static constexpr int LDS = 2 * STAGE;
   static constexpr int TILE = BN * BM;  // one stored e4m3 dS tile (16 KiB)
-  // dQ: K tile [key][d] and dS tile [key][query], unpadded 128-byte rows,
-  // data chunk c of row r at slot c ^ q_swz(r).  The transposed reads take
-  // rows 8 g + (li >> 1) + 32 m (lane group g, m = 0..3), on which q_swz does
-  // not depend on m; it spreads the two lane groups of each half-wave, the
-  // 16-row 4-byte dS stores and the 2-row 16-byte K stores over all banks.
-  __host__ __device__ static constexpr int q_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 4) & 1) << 2); }
+  // dQ: K tile [key][d] and dS tile [key][query] (queries permuted so that
+  // a stored piece is one 16-byte chunk), unpadded 128-byte rows, data chunk
+  // c of row r at slot c ^ q_swz(r).  16-byte stores go 8 lanes per pass
+  // with banks repeating every 128 bytes: the dS stores (8 aligned rows, one
+  // chunk each) and the K stores (one row's 8 chunks) hit distinct banks.
+  // The transposed 8-byte reads go 32 lanes per pass over 256 bytes of banks
+  // (rows 8 g + (li >> 1) + 32 m, two lane groups g): 16 aligned rows, two
+  // lanes a row, are spread when the slots of the even rows, and of the odd
+  // rows, differ (bit 3 of the row flips the slot's bit 0).
+  __host__ __device__ static constexpr int q_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
   static constexpr int QK_OFF = 0;
   static constexpr int QDS_OFF = QK_OFF + BN * 128;
   static constexpr int QHIST_OFF = QDS_OFF + BN * 128;
@@ -2312,13 +2317,13 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
       const int c = tid + kThreads * i, row = c >> 3, ch = c & 7;
       *(u32x4*)(smem + C::QK_OFF + row * 128 + 16 * (ch ^ C::q_swz(row))) = kc[i];
     }
+    // a piece holds queries 64 hf + 16 qs + 4 g + (0..3), qs = 0..3: it goes
+    // whole into 16-byte chunk 4 hf + g of its key row (query-permuted rows)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int w = 2 * wave + (j >> 1), hf = j & 1;
       const int r = 16 * w + li;
-      uint8_t* row = smem + C::QDS_OFF + r * 128 + 4 * g;
-#pragma unroll
-      for (int qs = 0; qs < 4; ++qs) *(uint32_t*)(row + 16 * ((4 * hf + qs) ^ C::q_swz(r))) = dsp[j][qs];
+      *(u32x4*)(smem + C::QDS_OFF + r * 128 + 16 * ((4 * hf + g) ^ C::q_swz(r))) = dsp[j];
     }
   };
   float dclamp = 0.f;
@@ -2368,9 +2373,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
     }
   };
 
-  // operand reads: dS^T columns (queries 16 chunk + li) and K^T rows (d =
-  // 16 chunk + li) over the keys 8 g + 32 m .. + 7, m = 0..3 (the contraction
-  // order is the same for both operands)
+  // operand reads: dS^T columns (byte 16 chunk + li of the permuted rows:
+  // query 64 (chunk >> 2) + 4 (chunk & 3) + 16 (li >> 2) + (li & 3)) and K^T
+  // rows (d = 16 chunk + li) over the keys 8 g + 32 m .. + 7, m = 0..3 (the
+  // contraction order is the same for both operands)
   const int tr_row = 8 * g + (li >> 1);
   const int trk = tr_row * 128 + 8 * (li & 1), trx = 16 * C::q_swz(tr_row);
   auto frag = [&](const uint8_t* tile, int chunk) {
@@ -2425,7 +2431,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   const float fin = p.alpha * unscale;
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs) {
-    const int row = m0 + 32 * wave + 16 * qs + li;
+    const int chunk = 2 * wave + qs;
+    const int row = m0 + 64 * (chunk >> 2) + 4 * (chunk & 3) + 16 * (li >> 2) + (li & 3);
     if (row >= L) continue;
     const uint32_t b = buf_ldu8(e8_rsrc, (uint32_t)row * (uint32_t)p.H);
     const float f = fin * ldexpf(1.0f, (int)b - 127);
