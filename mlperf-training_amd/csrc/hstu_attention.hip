@@ -679,8 +679,8 @@ struct Pv8Cfg {
   static constexpr int KT = BN * 128;
   static constexpr int K_OFF = 0;
   static constexpr int VS_OFF = 3 * KT;
-  // V stage: V rows, per key (s_k, c_k), 2 E8M0 bytes (as ints), BM + BN - 1 bias values
-  static constexpr int V_REL = 0, SC_REL = BN * 128, E8_REL = SC_REL + BN * 8, BIAS_REL = E8_REL + 16;
+  // V stage: V rows, per key c_k, 2 E8M0 bytes (as ints), BM + BN - 1 bias values
+  static constexpr int V_REL = 0, SC_REL = BN * 128, E8_REL = SC_REL + BN * 4, BIAS_REL = E8_REL + 16;
   static constexpr int VSTAGE = BIAS_REL + (BM + BN) * 4;
   static constexpr int P_OFF = VS_OFF + 2 * VSTAGE;  // per wave: P^T, 64 keys x 32 queries
   static constexpr int LDS = P_OFF + 4 * BN * 32;
@@ -725,7 +725,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 
   // Q (A operand of S): query mw0 + l32, bytes 64 kk + 32 hg .. + 31 of its row
   i32x8 qa[2];
-  float cq[16];  // -alpha log2(e) s_q of query 8 (j / 4) + 4 hg + j % 4
+  // -alpha log2(e) s_q of query mw0 + l32 in the half-wave hg = b, 0 in the
+  // other: the A operand of the outer product that scales key sub-tile b
+  float cqa[2];
   {
     const int row = mw0 + l32;
     const bool ok = row < L;
@@ -739,12 +741,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
       }
       qa[kk] = cat8(lo, hi);
     }
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = mw0 + 8 * (j >> 2) + 4 * hg + (j & 3);
-      const float s = r < L ? p.q_scale[(sc.start + r) * p.s_rs + h * p.s_hs] : 0.f;
-      cq[j] = -p.alpha * kLog2e * s;
-    }
+    const float cq = ok ? -p.alpha * kLog2e * p.q_scale[(sc.start + row) * p.s_rs + h * p.s_hs] : 0.f;
+    cqa[0] = hg ? 0.f : cq;
+    cqa[1] = hg ? cq : 0.f;
   }
 
   f32x16 o[4];
@@ -764,12 +763,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 #pragma unroll
     for (int i = 0; i < 2; ++i) stk[i] = buf_ld128(krsrc, k_voff[i], n0 * krs);
   };
+  // key scales of the tile at n0, lane = key (every wave loads its own)
+  auto load_sk = [&](int n0) __attribute__((always_inline)) {
+    return buf_ldf(sk_rsrc, (uint32_t)lane * s_step, n0 * s_step);
+  };
   auto load_v = [&](int n0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) stv[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
-    // wave 0: the tile's key scales, wave 1: its value scales (lane = key)
-    if (wave == 0) st_sc = buf_ldf(sk_rsrc, (uint32_t)lane * s_step, n0 * s_step);
-    else if (wave == 1) st_sc = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, n0 * s_step);
+    // wave 1: the tile's value scales (lane = key)
+    if (wave == 1) st_sc = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, n0 * s_step);
     if constexpr (BIAS) {
       // offsets i - j of the tile span [m0 - n0 - (BN - 1), m0 - n0 + BM - 1]
       if (tid < C::BM + C::BN - 1) {
@@ -786,9 +788,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 #pragma unroll
     for (int i = 0; i < 2; ++i) *(u32x4*)(vbuf + v_loff[i]) = stv[i];
     float* scl = (float*)(vbuf + C::SC_REL);
-    if (wave == 0) {
-      scl[2 * lane] = st_sc;
-    } else if (wave == 1) {
+    if (wave == 1) {
       // c_k = 1 / (s r_k), r_k = s_v 2^-E over the key's group (bit 4 of the key)
       const float sv = st_sc;
       float c = p.pv_c;
@@ -800,7 +800,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
         e8 = 127 + e;
         if (sv > 0.f) c = ldexpf(p.pv_c * __builtin_amdgcn_rcpf(sv), e);
       }
-      scl[2 * lane + 1] = c;
+      scl[lane] = c;
       if ((lane & 47) == 0) ((int*)(vbuf + C::E8_REL))[lane >> 4] = e8;
     }
     if constexpr (BIAS) {
@@ -809,6 +809,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   };
   auto kbuf = [&](int t) { return smem + C::K_OFF + (t % 3) * C::KT; };
   auto vbuf = [&](int t) { return smem + C::VS_OFF + (t & 1) * C::VSTAGE; };
+  // the K stage of tile t as a wave-uniform byte offset: one add per read address
+  auto kstage = [&](int t) { return (uint32_t)__builtin_amdgcn_readfirstlane((t % 3) * C::KT); };
 
   // K (B operand of S) reads: key 32 b + l32, chunks 4 kk + 2 hg + e at slots
   // (4 kk + 2 hg + e) ^ swz128(32 b + l32) = ((2 hg + e) ^ swz128(l32)) ^ 4 (kk ^ b)
@@ -817,8 +819,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   const int kx0 = ka0 ^ 64, kx1 = ka1 ^ 64;
   // S of key sub-tile b (32 keys) of a K tile: lane key 32 b + l32, register j
   // query 8 (j / 4) + 4 hg + j % 4
-  auto s_mfma = [&](const uint8_t* kt, int b) __attribute__((always_inline)) {
-    const uint8_t* kb = kt + 4096 * b;
+  auto s_mfma = [&](uint32_t kst, int b) __attribute__((always_inline)) {
+    const uint8_t* kb = smem + C::K_OFF + kst + 4096 * b;
     const i32x8 k0 = cat8(lds_ld128(kb + (b ? kx0 : ka0)), lds_ld128(kb + (b ? kx1 : ka1)));
     const i32x8 k1 = cat8(lds_ld128(kb + (b ? ka0 : kx0)), lds_ld128(kb + (b ? ka1 : kx1)));
     f32x16 z;
@@ -834,14 +836,21 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   const int pst = l32 * 32 + 16 * (hg ^ ((l32 >> 2) & 1));
   // bias index of (key sub-tile b, register j): bias_lo + 32 (1 - b) + 8 (j / 4) + j % 4
   const int bias_lo = 32 * wave + 4 * hg - l32 + (C::BN - 1) - 32;
-  // SiLU epilogue of one key sub-tile into P^T (e4m3)
-  auto epilogue = [&](const f32x16& s, int b, int n0, const uint8_t* vb, auto masked_tag, auto bconst_tag) __attribute__((always_inline)) {
+  // SiLU epilogue of one key sub-tile into P^T (e4m3); sc holds the score
+  // scales c_q s_k of the sub-tile's elements (the outer product)
+  auto epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb, auto masked_tag,
+                      auto bconst_tag) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool BCONST = decltype(bconst_tag)::value;
     const float* bias_lds = (const float*)(vb + C::BIAS_REL);
-    const float* bias_lane = bias_lds + bias_lo;
     const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
-    const f32x2 skc = *(const f32x2*)(vb + C::SC_REL + 8 * (32 * b + l32));
+    // the lane's bias window as an opaque LDS address, so that its 16 reads
+    // share one base register and differ in the instructions' offsets
+    uint32_t baddr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(vb + C::BIAS_REL) +
+                     4 * (bias_lo + 32 * (1 - b));
+    if constexpr (BIAS && !BCONST) asm volatile("" : "+v"(baddr));
+    const __attribute__((address_space(3))) float* bias_lane = (const __attribute__((address_space(3))) float*)(uintptr_t)baddr;
+    const float ck = *(const float*)(vb + C::SC_REL + 4 * (32 * b + l32));
     const int key = n0 + 32 * b + l32;
     u32x4 pk;
 #pragma unroll
@@ -850,10 +859,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 4 * i + r;
-        float x = s[j] * (cq[j] * skc[0]);
-        if constexpr (BIAS) x += BCONST ? bconst : bias_lane[32 * (1 - b) + 8 * i + r];
+        float x;
+        if constexpr (BIAS) x = __builtin_fmaf(s[j], scl[j], BCONST ? bconst : bias_lane[8 * i + r]);
+        else x = s[j] * scl[j];
         // P' s r_k = x / ((2^x + 1) / (s r_k)), c_k = 1 / (s r_k)
-        float v = x * __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(x), skc[1], skc[1]));
+        float v = x * __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(x), ck, ck));
         if constexpr (MASKED) v = key <= mw0 + 8 * i + 4 * hg + r ? v : 0.f;
         pv[r] = v;
       }
@@ -861,15 +871,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     }
     *(u32x4*)(pw + pst + 1024 * b) = pk;
   };
-  auto run_epilogue = [&](const f32x16& s, int b, int n0, const uint8_t* vb) __attribute__((always_inline)) {
+  auto run_epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb) __attribute__((always_inline)) {
     const bool masked = n0 + 32 * b + 31 > mw0;
     const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
     if (masked) {
-      if (bias_const) epilogue(s, b, n0, vb, std::true_type{}, std::true_type{});
-      else epilogue(s, b, n0, vb, std::true_type{}, std::false_type{});
+      if (bias_const) epilogue(s, scl, b, n0, vb, std::true_type{}, std::true_type{});
+      else epilogue(s, scl, b, n0, vb, std::true_type{}, std::false_type{});
     } else {
-      if (bias_const) epilogue(s, b, n0, vb, std::false_type{}, std::true_type{});
-      else epilogue(s, b, n0, vb, std::false_type{}, std::false_type{});
+      if (bias_const) epilogue(s, scl, b, n0, vb, std::false_type{}, std::true_type{});
+      else epilogue(s, scl, b, n0, vb, std::false_type{}, std::false_type{});
     }
   };
   // P (A operand of P.V) reads, u = 0..3: key rows 32 hg + 8 u + j16 / 2,
@@ -889,6 +899,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 
   // prologue: K tiles 0 and 1, V tile 0, S of sub-tile (0, 0)
   fp8_saturate_mode(true);
+  float sk_cur = load_sk(0), sk_next = 0.f;
   load_k(0);
   load_v(0);
   store_k(kbuf(0));
@@ -898,21 +909,32 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     store_k(kbuf(1));
   }
   __syncthreads();
-  f32x16 s0, s1;
-  if (wtiles > 0) s0 = s_mfma(kbuf(0), 0);
+  f32x16 s0, s1, sc0, sc1;
+  if (wtiles > 0) {
+    s0 = s_mfma(kstage(0), 0);
+    sc0 = mfma32_outer(cqa[0], sk_cur);
+  }
 
-  // tile t: S(t, 1) runs on the matrix cores during the epilogue of (t, 0),
-  // S(t + 1, 0) during that of (t, 1); K is staged two tiles ahead, V one
+  // tile t: S(t, 1) and the score scales of sub-tile (t, 1) run on the
+  // matrix cores during the epilogue of (t, 0), S(t + 1, 0) and its scales
+  // during that of (t, 1); K is staged two tiles ahead, V one.  The key
+  // scales of tile t + 1 are loaded first, so that waiting for them does not
+  // wait for the K/V loads
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * C::BN;
+    if (t + 1 < wtiles) sk_next = load_sk(n0 + C::BN);
     if (t + 2 < ntiles) load_k(n0 + 2 * C::BN);
     if (t + 1 < ntiles) load_v(n0 + C::BN);
     const uint8_t* vb = vbuf(t);
     if (t < wtiles) {
-      s1 = s_mfma(kbuf(t), 1);
-      run_epilogue(s0, 0, n0, vb);
-      if (t + 1 < wtiles) s0 = s_mfma(kbuf(t + 1), 0);
-      run_epilogue(s1, 1, n0, vb);
+      s1 = s_mfma(kstage(t), 1);
+      sc1 = mfma32_outer(cqa[1], sk_cur);
+      run_epilogue(s0, sc0, 0, n0, vb);
+      if (t + 1 < wtiles) {
+        s0 = s_mfma(kstage(t + 1), 0);
+        sc0 = mfma32_outer(cqa[0], sk_next);
+      }
+      run_epilogue(s1, sc1, 1, n0, vb);
       // the wave's own P^T stores precede its transposed reads (LDS keeps a
       // wave's operations in order); this only stops the compiler reordering
       asm volatile("" ::: "memory");
@@ -939,6 +961,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     }
     if (t + 2 < ntiles) store_k(kbuf(t + 2));
     if (t + 1 < ntiles) store_v(vbuf(t + 1));
+    sk_cur = sk_next;
     __syncthreads();
   }
   fp8_saturate_mode(false);
