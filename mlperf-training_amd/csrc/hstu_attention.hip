@@ -819,14 +819,19 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   const int kx0 = ka0 ^ 64, kx1 = ka1 ^ 64;
   // S of key sub-tile b (32 keys) of a K tile: lane key 32 b + l32, register j
   // query 8 (j / 4) + 4 hg + j % 4
-  auto s_mfma = [&](uint32_t kst, int b) __attribute__((always_inline)) {
+  // (the operands k[0], k[1] pair with qa[0], qa[1])
+  auto k_read = [&](uint32_t kst, int b, i32x8 (&k)[2]) __attribute__((always_inline)) {
     const uint8_t* kb = smem + C::K_OFF + kst + 4096 * b;
-    const i32x8 k0 = cat8(lds_ld128(kb + (b ? kx0 : ka0)), lds_ld128(kb + (b ? kx1 : ka1)));
-    const i32x8 k1 = cat8(lds_ld128(kb + (b ? ka0 : kx0)), lds_ld128(kb + (b ? ka1 : kx1)));
+    k[0] = cat8(lds_ld128(kb + (b ? kx0 : ka0)), lds_ld128(kb + (b ? kx1 : ka1)));
+    k[1] = cat8(lds_ld128(kb + (b ? ka0 : kx0)), lds_ld128(kb + (b ? ka1 : kx1)));
+  };
+  auto s_mfma = [&](uint32_t kst, int b) __attribute__((always_inline)) {
+    i32x8 k[2];
+    k_read(kst, b, k);
     f32x16 z;
 #pragma unroll
     for (int r = 0; r < 16; ++r) z[r] = 0.f;
-    return mfma32_fp8(qa[1], k1, mfma32_fp8(qa[0], k0, z));
+    return mfma32_fp8(qa[1], k[1], mfma32_fp8(qa[0], k[0], z));
   };
   // P^T: key row 32 b + l32 (32 bytes); byte 16 hg + 4 i + r holds query
   // 8 i + 4 hg + r, so a lane stores its 16 bytes at once, in 16-byte chunk
@@ -836,10 +841,14 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   const int pst = l32 * 32 + 16 * (hg ^ ((l32 >> 2) & 1));
   // bias index of (key sub-tile b, register j): bias_lo + 32 (1 - b) + 8 (j / 4) + j % 4
   const int bias_lo = 32 * wave + 4 * hg - l32 + (C::BN - 1) - 32;
-  // SiLU epilogue of one key sub-tile into P^T (e4m3); sc holds the score
-  // scales c_q s_k of the sub-tile's elements (the outer product)
+  // SiLU epilogue of one key sub-tile into P^T (e4m3); scl holds the score
+  // scales c_q s_k of the sub-tile's elements (the outer product).  hook(g),
+  // g = 0..2, issues one of the caller's MFMAs; the scheduling groups at the
+  // end place them one at a time between pieces of this wave's VALU work
+  // instead of back to back (a wave does not issue past an MFMA that waits
+  // for the matrix core)
   auto epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb, auto masked_tag,
-                      auto bconst_tag) __attribute__((always_inline)) {
+                      auto bconst_tag, auto&& hook) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool BCONST = decltype(bconst_tag)::value;
     const float* bias_lds = (const float*)(vb + C::BIAS_REL);
@@ -852,15 +861,19 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     const __attribute__((address_space(3))) float* bias_lane = (const __attribute__((address_space(3))) float*)(uintptr_t)baddr;
     const float ck = *(const float*)(vb + C::SC_REL + 4 * (32 * b + l32));
     const int key = n0 + 32 * b + l32;
+    float bj[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) bj[j] = BIAS ? (BCONST ? bconst : bias_lane[8 * (j >> 2) + (j & 3)]) : 0.f;
     u32x4 pk;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      if (i > 0) hook(i - 1);
       float pv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 4 * i + r;
         float x;
-        if constexpr (BIAS) x = __builtin_fmaf(s[j], scl[j], BCONST ? bconst : bias_lane[8 * i + r]);
+        if constexpr (BIAS) x = __builtin_fmaf(s[j], scl[j], bj[j]);
         else x = s[j] * scl[j];
         // P' s r_k = x / ((2^x + 1) / (s r_k)), c_k = 1 / (s r_k)
         float v = x * __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(x), ck, ck));
@@ -870,16 +883,22 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
       pk[i] = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
     }
     *(u32x4*)(pw + pst + 1024 * b) = pk;
+    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);  // the LDS reads
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x402, 24, 0);  // VALU incl. transcendental
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+    }
   };
-  auto run_epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb) __attribute__((always_inline)) {
+  auto run_epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb, auto&& hook) __attribute__((always_inline)) {
     const bool masked = n0 + 32 * b + 31 > mw0;
     const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
     if (masked) {
-      if (bias_const) epilogue(s, scl, b, n0, vb, std::true_type{}, std::true_type{});
-      else epilogue(s, scl, b, n0, vb, std::true_type{}, std::false_type{});
+      if (bias_const) epilogue(s, scl, b, n0, vb, std::true_type{}, std::true_type{}, hook);
+      else epilogue(s, scl, b, n0, vb, std::true_type{}, std::false_type{}, hook);
     } else {
-      if (bias_const) epilogue(s, scl, b, n0, vb, std::false_type{}, std::true_type{});
-      else epilogue(s, scl, b, n0, vb, std::false_type{}, std::false_type{});
+      if (bias_const) epilogue(s, scl, b, n0, vb, std::false_type{}, std::true_type{}, hook);
+      else epilogue(s, scl, b, n0, vb, std::false_type{}, std::false_type{}, hook);
     }
   };
   // P (A operand of P.V) reads, u = 0..3: key rows 32 hg + 8 u + j16 / 2,
@@ -927,14 +946,36 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
     if (t + 1 < ntiles) load_v(n0 + C::BN);
     const uint8_t* vb = vbuf(t);
     if (t < wtiles) {
-      s1 = s_mfma(kstage(t), 1);
-      sc1 = mfma32_outer(cqa[1], sk_cur);
-      run_epilogue(s0, sc0, 0, n0, vb);
-      if (t + 1 < wtiles) {
-        s0 = s_mfma(kstage(t + 1), 0);
-        sc0 = mfma32_outer(cqa[0], sk_next);
-      }
-      run_epilogue(s1, sc1, 1, n0, vb);
+      // S(t, 1) and its scales during the epilogue of (t, 0); S(t + 1, 0)
+      // and its scales during that of (t, 1) (computed, unused, past the
+      // wave's last tile: the K stage and the key scales are in bounds)
+      i32x8 kr[2];
+      k_read(kstage(t), 1, kr);
+      run_epilogue(s0, sc0, 0, n0, vb, [&](int g) __attribute__((always_inline)) {
+        if (g == 0) {
+          f32x16 z;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) z[r] = 0.f;
+          s1 = mfma32_fp8(qa[0], kr[0], z);
+        } else if (g == 1) {
+          s1 = mfma32_fp8(qa[1], kr[1], s1);
+        } else {
+          sc1 = mfma32_outer(cqa[1], sk_cur);
+        }
+      });
+      k_read(kstage(t + 1), 0, kr);
+      run_epilogue(s1, sc1, 1, n0, vb, [&](int g) __attribute__((always_inline)) {
+        if (g == 0) {
+          f32x16 z;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) z[r] = 0.f;
+          s0 = mfma32_fp8(qa[0], kr[0], z);
+        } else if (g == 1) {
+          s0 = mfma32_fp8(qa[1], kr[1], s0);
+        } else {
+          sc0 = mfma32_outer(cqa[0], sk_next);
+        }
+      });
       // the wave's own P^T stores precede its transposed reads (LDS keeps a
       // wave's operations in order); this only stops the compiler reordering
       asm volatile("" ::: "memory");
