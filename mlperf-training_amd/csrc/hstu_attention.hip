@@ -712,15 +712,16 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
   const int R1 = p.bias_R - 1;
 
-  // staging: items tid and tid + 256 of each 64 x 8 chunk tile
-  uint32_t k_voff[2], v_voff[2], k_loff[2], v_loff[2];
+  // K/V staging by LDS DMA: wave w's load i writes the 1 KiB of rows
+  // 8 w + 32 i .. + 7 of the tile; lane l lands in slot l % 8 of row
+  // 8 w + 32 i + l / 8 and so loads the data chunk that slot holds,
+  // (l % 8) ^ swizzle(row)
+  uint32_t k_voff[2], v_voff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int item = tid + kThreads * i, row = item >> 3, ch = item & 7;
-    k_voff[i] = row * krs + 16 * ch;
-    v_voff[i] = row * vrs + 16 * ch;
-    k_loff[i] = row * 128 + 16 * (ch ^ swz128(row));
-    v_loff[i] = C::V_REL + row * 128 + 16 * (ch ^ C::v_swz(row));
+    const int row = 8 * wave + 32 * i + (lane >> 3), slot = lane & 7;
+    k_voff[i] = row * krs + 16 * (slot ^ swz128(row));
+    v_voff[i] = row * vrs + 16 * (slot ^ C::v_swz(row));
   }
 
   // Q (A operand of S): query mw0 + l32, bytes 64 kk + 32 hg .. + 31 of its row
@@ -757,19 +758,19 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   // tiles this wave computes: key tile t is needed while 64 t <= mw0 + 31
   const int wtiles = mw0 < L ? min(ntiles, (mw0 + 31) / C::BN + 1) : 0;
 
-  u32x4 stk[2], stv[2];
   float st_sc = 0.f, st_bias = 0.f;
-  auto load_k = [&](int n0) __attribute__((always_inline)) {
+  auto load_k = [&](int n0, uint8_t* kbuf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) stk[i] = buf_ld128(krsrc, k_voff[i], n0 * krs);
+    for (int i = 0; i < 2; ++i) buf_to_lds<16>(krsrc, kbuf + (8 * wave + 32 * i) * 128, k_voff[i], n0 * krs);
   };
   // key scales of the tile at n0, lane = key (every wave loads its own)
   auto load_sk = [&](int n0) __attribute__((always_inline)) {
     return buf_ldf(sk_rsrc, (uint32_t)lane * s_step, n0 * s_step);
   };
-  auto load_v = [&](int n0) __attribute__((always_inline)) {
+  auto load_v = [&](int n0, uint8_t* vbuf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) stv[i] = buf_ld128(vrsrc, v_voff[i], n0 * vrs);
+    for (int i = 0; i < 2; ++i)
+      buf_to_lds<16>(vrsrc, vbuf + C::V_REL + (8 * wave + 32 * i) * 128, v_voff[i], n0 * vrs);
     // wave 1: the tile's value scales (lane = key)
     if (wave == 1) st_sc = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, n0 * s_step);
     if constexpr (BIAS) {
@@ -780,13 +781,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
       }
     }
   };
-  auto store_k = [&](uint8_t* kbuf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) *(u32x4*)(kbuf + k_loff[i]) = stk[i];
-  };
+  // the V stage's per-key factors, E8M0 bytes and bias window
   auto store_v = [&](uint8_t* vbuf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) *(u32x4*)(vbuf + v_loff[i]) = stv[i];
     float* scl = (float*)(vbuf + C::SC_REL);
     if (wave == 1) {
       // c_k = 1 / (s r_k), r_k = s_v 2^-E over the key's group (bit 4 of the key)
@@ -919,14 +915,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   // prologue: K tiles 0 and 1, V tile 0, S of sub-tile (0, 0)
   fp8_saturate_mode(true);
   float sk_cur = load_sk(0), sk_next = 0.f;
-  load_k(0);
-  load_v(0);
-  store_k(kbuf(0));
+  load_k(0, kbuf(0));
+  load_v(0, vbuf(0));
+  if (ntiles > 1) load_k(C::BN, kbuf(1));
   store_v(vbuf(0));
-  if (ntiles > 1) {
-    load_k(C::BN);
-    store_k(kbuf(1));
-  }
+  lds_dma_wait();
   __syncthreads();
   f32x16 s0, s1, sc0, sc1;
   if (wtiles > 0) {
@@ -936,14 +929,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 
   // tile t: S(t, 1) and the score scales of sub-tile (t, 1) run on the
   // matrix cores during the epilogue of (t, 0), S(t + 1, 0) and its scales
-  // during that of (t, 1); K is staged two tiles ahead, V one.  The key
+  // during that of (t, 1); K is staged two tiles ahead, V one (the DMA into
+  // a stage starts a barrier after the stage's last reads).  The key
   // scales of tile t + 1 are loaded first, so that waiting for them does not
   // wait for the K/V loads
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * C::BN;
     if (t + 1 < wtiles) sk_next = load_sk(n0 + C::BN);
-    if (t + 2 < ntiles) load_k(n0 + 2 * C::BN);
-    if (t + 1 < ntiles) load_v(n0 + C::BN);
+    if (t + 2 < ntiles) load_k(n0 + 2 * C::BN, kbuf(t + 2));
+    if (t + 1 < ntiles) load_v(n0 + C::BN, vbuf(t + 1));
     const uint8_t* vb = vbuf(t);
     if (t < wtiles) {
       // S(t, 1) and its scales during the epilogue of (t, 0); S(t + 1, 0)
@@ -1000,9 +994,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
         o[db] = mfma32_fp8_scaled(pa, bv, o[db], 127, e8v);
       }
     }
-    if (t + 2 < ntiles) store_k(kbuf(t + 2));
     if (t + 1 < ntiles) store_v(vbuf(t + 1));
     sk_cur = sk_next;
+    // this wave's LDS DMA of tiles t + 1 (V) and t + 2 (K) has landed; the
+    // barrier publishes all four waves'
+    lds_dma_wait();
     __syncthreads();
   }
   fp8_saturate_mode(false);
