@@ -2118,10 +2118,14 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
     sv = p.v_scale[(sc.start + key) * p.s_rs + h * p.s_hs];
   }
   const float nq = f8_norm(p.f8max[0]), nk = f8_norm(p.f8max[1]);
+  // P8 = e4m3(t sigma kp) is computed as t sigma' with sigma' = kp sigma =
+  // 1 / ((1 + 2^t) / kp); then silu'(x) kp = fma(P, fma(sigma', ln2 / kp, -ln2), sigma'),
+  // and the 1 / kp goes into the dS factors
+  const float kp = -kLn2 * p.p8_scale * p.inv_n;
+  const float ikp = 1.0f / kp, ln2_kp = kLn2 * ikp;
   const float ck = -p.alpha * kLog2e * sk;                    // times s_q: exp2 argument factor
-  const float an = sv * nq * p.ds8_scale * p.inv_n;           // times s_q: dS8k factor
-  const float bn = sv * sk * nk * p.ds8_scale * p.inv_n;      // dS8q factor
-  const float kp = -kLn2 * p.p8_scale * p.inv_n;              // t * sigmoid -> e4m3 P
+  const float an = sv * nq * p.ds8_scale * p.inv_n * ikp;     // times s_q: dS8k factor
+  const float bn = sv * sk * nk * p.ds8_scale * p.inv_n * ikp;  // dS8q factor
 
   f32x4 dvt[8], dkt[8];
 #pragma unroll
@@ -2214,10 +2218,9 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
         for (int r = 0; r < 4; ++r) {
           float tt = s[qs][r] * (ck * sq4[r]);
           if constexpr (BIAS) tt += BCONST ? bconst : bl[r];
-          const float sg = sig_of_t(tt);
-          const float pp = tt * sg;
-          float pval = pp * kp;
-          float dsv = dp[qs][r] * dsilu_factor(sg, pp);
+          const float sgk = __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(tt), ikp, ikp));
+          float pval = tt * sgk;
+          float dsv = dp[qs][r] * __builtin_fmaf(pval, __builtin_fmaf(sgk, ln2_kp, -kLn2), sgk);
           if constexpr (MASKED) {
             const bool ok = 64 * hf + 16 * qs + 4 * g + r >= 16 * wave + li;
             pval = ok ? pval : 0.f;
