@@ -252,8 +252,11 @@ struct SeqCtx {
 // (i / 8)-th block of that XCD's list.  heavy_last: the block with the most
 // key tiles is the last one of its sequence (forward, dQ) rather than the
 // first (dK/dV); each item's blocks run heaviest first.  False = no work.
-__device__ __forceinline__ bool seq_ctx(const AttnParams& p, bool heavy_last, SeqCtx& c) {
-  const int x = blockIdx.x & 7, k = blockIdx.x >> 3;
+// With half != nullptr two workgroups share each block (i = 16 k + 8 h + x:
+// half h of the k-th block), on the same XCD one after the other.
+__device__ __forceinline__ bool seq_ctx(const AttnParams& p, bool heavy_last, SeqCtx& c, int* half = nullptr) {
+  const int x = blockIdx.x & 7, k = half ? blockIdx.x >> 4 : blockIdx.x >> 3;
+  if (half) *half = (blockIdx.x >> 3) & 1;
   const int n = p.sched_count[x];
   const int* st = p.sched_start + x * (p.sched_cap + 1);
   if (k >= st[n]) return false;
@@ -2023,7 +2026,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
 // and the other operand reads the same tokens with ds_read_b64_tr_b8.
 // =====================================================================
 struct F8Bwd {
-  static constexpr int NT = 512;            // dK/dV: 8 waves, 16 keys each
+  // dK/dV: a 128-key block is two workgroups of 4 waves (64 keys), 16 keys
+  // a wave; two such workgroups share a CU, so the two waves of a SIMD
+  // belong to different workgroups and do not meet at the same barriers
+  static constexpr int NT = 256;
   static constexpr int BN = 128, BM = 128;  // keys per block, queries per tile
   // dK/dV stage: Q and dO tiles of 128-byte e4m3 rows, unpadded (LDS DMA
   // writes 1 KiB runs), data chunk c (bytes 16c .. 16c + 15) of row r at
@@ -2082,17 +2088,19 @@ __device__ __forceinline__ uint32_t buf_ldu8(BufRsrc r, uint32_t voff) {
 }
 
 template <bool BIAS>
-__global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnParams p) {
+__global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnParams p) {
   using C = F8Bwd;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   SeqCtx sc;
-  if (!seq_ctx(p, /*heavy_last=*/false, sc)) return;
+  int half = 0;
+  if (!seq_ctx(p, /*heavy_last=*/false, sc, &half)) return;
   const int L = sc.L, h = sc.h;
   const int n0 = sc.blk * C::BN;
   if (n0 >= L) return;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, li = lane & 15,
             g = lane >> 4;
-  const int kw0 = n0 + 16 * wave;
+  const int wv = 4 * half + wave;  // the wave's 16 keys within the 128-key block
+  const int kw0 = n0 + 16 * wv;
   const int key = kw0 + li;
   const bool key_ok = key < L;
 
@@ -2132,12 +2140,18 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
   for (int dt = 0; dt < 8; ++dt) dvt[dt] = dkt[dt] = zero4();
 
   // one 128-query tile per stage, moved by LDS DMA: wave w takes rows
-  // 8 w + 64 i + (lane >> 3), i = 0, 1, of Q and dO (lane slot lane & 7
-  // holds data chunk (lane & 7) ^ kv_swz(row)), waves 0-1 the 128 query
-  // scales, waves 2-5 the 256 bias values
+  // 8 w + 32 i + (lane >> 3), i = 0..3, of Q and dO (lane slot lane & 7
+  // holds data chunk (lane & 7) ^ kv_swz(row), which depends on i through
+  // bit 5 of the row), waves 0-1 the 128 query scales, wave w bias values
+  // 64 w .. 64 w + 63
   const int lrow = 8 * wave + (lane >> 3);
-  const uint32_t chunk = 16u * (uint32_t)((lane & 7) ^ C::kv_swz(lrow));
-  const uint32_t q_voff = lrow * qrs + chunk, d_voff = lrow * dors + chunk;
+  uint32_t q_voff[2], d_voff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t chunk = 16u * (uint32_t)((lane & 7) ^ C::kv_swz(lrow + 32 * j));
+    q_voff[j] = lrow * qrs + chunk;
+    d_voff[j] = lrow * dors + chunk;
+  }
   // E8M0 byte of the dO group K-block g covers: token m0 + 64 (g >> 1) + 8 (g & 1),
   // loaded with its tile (complete at the tile's wait)
   const uint32_t e8_tok = 64 * (g >> 1) + 8 * (g & 1);
@@ -2145,14 +2159,15 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
   auto load = [&](int m0, uint8_t* st) {
     sc_next = (int)buf_ldu8(e8_rsrc, (uint32_t)(m0 + (int)e8_tok) * (uint32_t)p.H);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      buf_to_lds<16>(q_rsrc, st + C::Q_OFF + (8 * wave + 64 * i) * 128, q_voff, (uint32_t)(m0 + 64 * i) * qrs);
-      buf_to_lds<16>(do_rsrc, st + C::DO_OFF + (8 * wave + 64 * i) * 128, d_voff, (uint32_t)(m0 + 64 * i) * dors);
+    for (int i = 0; i < 4; ++i) {
+      buf_to_lds<16>(q_rsrc, st + C::Q_OFF + (8 * wave + 32 * i) * 128, q_voff[i & 1], (uint32_t)(m0 + 32 * i) * qrs);
+      buf_to_lds<16>(do_rsrc, st + C::DO_OFF + (8 * wave + 32 * i) * 128, d_voff[i & 1],
+                     (uint32_t)(m0 + 32 * i) * dors);
     }
-    if (wave < 2) {
+    if (wave < 2)
       buf_to_lds<4>(sq_rsrc, st + C::SQ_OFF + 256 * wave, (uint32_t)lane * s_step, (uint32_t)(m0 + 64 * wave) * s_step);
-    } else if (BIAS && wave < 6) {
-      buf_to_lds<4>(b_rsrc, st + C::B_OFF + 256 * (wave - 2), (uint32_t)(64 * (wave - 2) + lane) * 4u,
+    if (BIAS) {
+      buf_to_lds<4>(b_rsrc, st + C::B_OFF + 256 * wave, (uint32_t)(64 * wave + lane) * 4u,
                     (uint32_t)(m0 - n0 + p.N) * 4u);
     }
   };
@@ -2175,11 +2190,11 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
     return f;
   };
   const int R1 = p.bias_R - 1;
-  const int bias_lane = 127 + 4 * g - 16 * wave - li;  // + 64 hf + 16 qs + r
+  const int bias_lane = 127 + 4 * g - 16 * wv - li;  // + 64 hf + 16 qs + r
   const int ntiles = (L - n0 + C::BM - 1) / C::BM;
 
   // this block's stored dS tiles (query tiles blk, blk + 1, .. are consecutive)
-  uint8_t* const ds_dst = f8_tile(p, sc, sc.blk, sc.blk) + (size_t)((wave * 2) * 64 + lane) * 16;
+  uint8_t* const ds_dst = f8_tile(p, sc, sc.blk, sc.blk) + (size_t)((wv * 2) * 64 + lane) * 16;
   fp8_saturate_mode(true);
   load(n0, smem);
   lds_dma_wait();
@@ -2222,7 +2237,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 1) hstu_bwd_f8_dkdv_kernel(AttnPara
           float pval = tt * sgk;
           float dsv = dp[qs][r] * __builtin_fmaf(pval, __builtin_fmaf(sgk, ln2_kp, -kLn2), sgk);
           if constexpr (MASKED) {
-            const bool ok = 64 * hf + 16 * qs + 4 * g + r >= 16 * wave + li;
+            const bool ok = 64 * hf + 16 * qs + 4 * g + r >= 16 * wv + li;
             pval = ok ? pval : 0.f;
             dsv = ok ? dsv : 0.f;
           }
@@ -3329,8 +3344,8 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
       hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
                          attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
     }
-    e = has_bias ? launch(hstu_bwd_f8_dkdv_kernel<true>, F8Bwd::LDS, grid, p, stream, F8Bwd::NT)
-                 : launch(hstu_bwd_f8_dkdv_kernel<false>, F8Bwd::LDS, grid, p, stream, F8Bwd::NT);
+    e = has_bias ? launch(hstu_bwd_f8_dkdv_kernel<true>, F8Bwd::LDS, 2 * grid, p, stream, F8Bwd::NT)
+                 : launch(hstu_bwd_f8_dkdv_kernel<false>, F8Bwd::LDS, 2 * grid, p, stream, F8Bwd::NT);
     if (e != hipSuccess) return (int)e;
   }
   if (parts & kBwdDq) {
