@@ -682,11 +682,16 @@ struct Pv8Cfg {
   static constexpr int KT = BN * 128;
   static constexpr int K_OFF = 0;
   static constexpr int VS_OFF = 3 * KT;
-  // V stage: V rows, per key c_k, 2 E8M0 bytes (as ints), BM + BN - 1 bias values
-  static constexpr int V_REL = 0, SC_REL = BN * 128, E8_REL = SC_REL + BN * 4, BIAS_REL = E8_REL + 16;
+  // V stage: V rows, BM + BN - 1 bias values
+  static constexpr int V_REL = 0, BIAS_REL = BN * 128;
   static constexpr int VSTAGE = BIAS_REL + (BM + BN) * 4;
   static constexpr int P_OFF = VS_OFF + 2 * VSTAGE;  // per wave: P^T, 64 keys x 32 queries
-  static constexpr int LDS = P_OFF + 4 * BN * 32;
+  // the block's table: two E8M0 bytes (as ints) per key tile, then c_k per key
+  static constexpr int TAB_OFF = P_OFF + 4 * BN * 32;
+  static int lds(int N) {
+    const int nt = (N + BN - 1) / BN;
+    return TAB_OFF + 8 * nt + 4 * BN * nt;
+  }
   static_assert(VSTAGE % 16 == 0, "stage alignment");
   __host__ __device__ static constexpr int v_swz(int r) { return r & 6; }
 };
@@ -760,8 +765,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   const int ntiles = (n_end + C::BN - 1) / C::BN;
   // tiles this wave computes: key tile t is needed while 64 t <= mw0 + 31
   const int wtiles = mw0 < L ? min(ntiles, (mw0 + 31) / C::BN + 1) : 0;
+  // the block's table of E8M0 bytes (two per key tile) and per-key c_k
+  int* const e8t = (int*)(smem + C::TAB_OFF);
+  float* const ckt = (float*)(smem + C::TAB_OFF + 8 * ((p.N + C::BN - 1) / C::BN));
 
-  float st_sc = 0.f, st_bias = 0.f;
+  float st_bias = 0.f;
   auto load_k = [&](int n0, uint8_t* kbuf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) buf_to_lds<16>(krsrc, kbuf + (8 * wave + 32 * i) * 128, k_voff[i], n0 * krs);
@@ -774,34 +782,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       buf_to_lds<16>(vrsrc, vbuf + C::V_REL + (8 * wave + 32 * i) * 128, v_voff[i], n0 * vrs);
-    // wave 1: the tile's value scales (lane = key)
-    if (wave == 1) st_sc = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, n0 * s_step);
     if constexpr (BIAS) {
       // offsets i - j of the tile span [m0 - n0 - (BN - 1), m0 - n0 + BM - 1]
-      if (tid < C::BM + C::BN - 1) {
-        const int off = m0 - n0 - (C::BN - 1) + tid;
-        st_bias = biasb[min(max(off, -R1), R1) + R1];
-      }
+      // (threads tid < BM + BN - 1 store theirs)
+      const int off = m0 - n0 - (C::BN - 1) + tid;
+      st_bias = biasb[min(max(off, -R1), R1) + R1];
     }
   };
-  // the V stage's per-key factors, E8M0 bytes and bias window
+  // the V stage's bias window
   auto store_v = [&](uint8_t* vbuf) __attribute__((always_inline)) {
-    float* scl = (float*)(vbuf + C::SC_REL);
-    if (wave == 1) {
-      // c_k = 1 / (s r_k), r_k = s_v 2^-E over the key's group (bit 4 of the key)
-      const float sv = st_sc;
-      float c = p.pv_c;
-      int e8 = 127;
-      if (!per_tensor) {
-        const float m = max_lanes_same_bit4(sv);
-        int e = 0;
-        if (m > 0.f) (void)frexpf(m, &e);
-        e8 = 127 + e;
-        if (sv > 0.f) c = ldexpf(p.pv_c * __builtin_amdgcn_rcpf(sv), e);
-      }
-      scl[lane] = c;
-      if ((lane & 47) == 0) ((int*)(vbuf + C::E8_REL))[lane >> 4] = e8;
-    }
     if constexpr (BIAS) {
       if (tid < C::BM + C::BN - 1) ((float*)(vbuf + C::BIAS_REL))[tid] = st_bias * -kLog2e;
     }
@@ -858,7 +847,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
                      4 * (bias_lo + 32 * (1 - b));
     if constexpr (BIAS && !BCONST) asm volatile("" : "+v"(baddr));
     const __attribute__((address_space(3))) float* bias_lane = (const __attribute__((address_space(3))) float*)(uintptr_t)baddr;
-    const float ck = *(const float*)(vb + C::SC_REL + 4 * (32 * b + l32));
+    const float ck = ckt[n0 + 32 * b + l32];
     const int key = n0 + 32 * b + l32;
     float bj[16];
 #pragma unroll
@@ -915,12 +904,39 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   for (int db = 0; db < 4; ++db)
     vld[db] = C::V_REL + (32 * hg + (j16 >> 1)) * 128 + 16 * ((2 * db + hi16) ^ vsw) + 8 * (j16 & 1);
 
+  // per-key factors c_k = 1 / (s r_k), r_k = s_v 2^-E over the key's group
+  // (the keys of its 64-key tile with the same bit 4), and the group's
+  // E8M0 byte 127 + E, for all of the block's key tiles: wave w takes tiles
+  // w, w + 4, .. (lane = key), four value-scale loads at a time
+  for (int T0 = wave; T0 < ntiles; T0 += 16) {
+    float svs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) svs[u] = buf_ldf(sv_rsrc, (uint32_t)lane * s_step, (uint32_t)(64 * (T0 + 4 * u)) * s_step);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int T = T0 + 4 * u;
+      if (T >= ntiles) break;
+      const float sv = svs[u];
+      float c = p.pv_c;
+      int e8 = 127;
+      if (!per_tensor) {
+        const float m = max_lanes_same_bit4(sv);
+        int e = 0;
+        if (m > 0.f) (void)frexpf(m, &e);
+        e8 = 127 + e;
+        if (sv > 0.f) c = ldexpf(p.pv_c * __builtin_amdgcn_rcpf(sv), e);
+      }
+      ckt[64 * T + lane] = c;
+      if ((lane & 47) == 0) e8t[2 * T + (lane >> 4)] = e8;
+    }
+  }
+
   // prologue: K tiles 0 and 1, V tile 0, S of sub-tile (0, 0)
   fp8_saturate_mode(true);
   float sk_cur = load_sk(0), sk_next = 0.f;
   load_k(0, kbuf(0));
   load_v(0, vbuf(0));
-  if (ntiles > 1) load_k(C::BN, kbuf(1));
+  load_k(C::BN, kbuf(1));
   store_v(vbuf(0));
   lds_dma_wait();
   __syncthreads();
@@ -935,12 +951,16 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   // during that of (t, 1); K is staged two tiles ahead, V one (the DMA into
   // a stage starts a barrier after the stage's last reads).  The key
   // scales of tile t + 1 are loaded first, so that waiting for them does not
-  // wait for the K/V loads
+  // wait for the K/V loads; every load is issued on every tile (past the
+  // sequence the buffer range check returns zeros into a stage nobody reads,
+  // the bias index is clamped), so the wait counts the compiler derives are
+  // exact instead of falling back to waiting for all loads
   for (int t = 0; t < ntiles; ++t) {
     const int n0 = t * C::BN;
-    if (t + 1 < wtiles) sk_next = load_sk(n0 + C::BN);
-    if (t + 2 < ntiles) load_k(n0 + 2 * C::BN, kbuf(t + 2));
-    if (t + 1 < ntiles) load_v(n0 + C::BN, vbuf(t + 1));
+    sk_next = load_sk(n0 + C::BN);
+    __builtin_amdgcn_sched_barrier(0);  // issued before the tile loads
+    load_k(n0 + 2 * C::BN, kbuf(t + 2));
+    load_v(n0 + C::BN, vbuf(t + 1));
     const uint8_t* vb = vbuf(t);
     if (t < wtiles) {
       // S(t, 1) and its scales during the epilogue of (t, 0); S(t + 1, 0)
@@ -983,7 +1003,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
         pa[2 * u] = (int)w[0];
         pa[2 * u + 1] = (int)w[1];
       }
-      const int e8v = ((const int*)(vb + C::E8_REL))[hg];
+      const int e8v = e8t[2 * t + hg];
       // ---- O += P.V, V's group scales as the B operand's E8M0
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -997,7 +1017,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
         o[db] = mfma32_fp8_scaled(pa, bv, o[db], 127, e8v);
       }
     }
-    if (t + 1 < ntiles) store_v(vbuf(t + 1));
+    store_v(vbuf(t + 1));
     sk_cur = sk_next;
     // this wave's LDS DMA of tiles t + 1 (V) and t + 2 (K) has landed; the
     // barrier publishes all four waves'
@@ -2922,8 +2942,8 @@ int fwd_launch(int dtype, const void* q, const void* k, const void* v, int64_t q
     // by 2^-3 (hstu_fwd.py pv_s)
     p.pv_c = (float)(8.0f / pv_scale) * 0.125f;
     p.pv_out = 1.0f / pv_scale;
-    e = has_bias ? launch(hstu_fwd_pv8_kernel<true>, Pv8Cfg::LDS, grid, p, stream)
-                 : launch(hstu_fwd_pv8_kernel<false>, Pv8Cfg::LDS, grid, p, stream);
+    e = has_bias ? launch(hstu_fwd_pv8_kernel<true>, Pv8Cfg::lds(max_seq_len), grid, p, stream)
+                 : launch(hstu_fwd_pv8_kernel<false>, Pv8Cfg::lds(max_seq_len), grid, p, stream);
   } else if (dtype == HSTU_DTYPE_FP8_E4M3) {
     e = generic ? HSTU_FWD_B(128, true, true) : HSTU_FWD_B(128, true, false);
   } else if (D == 128) {
