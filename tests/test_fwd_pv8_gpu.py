@@ -157,3 +157,22 @@ def test_fwd_pv8_config3(hip_lib):
     sub = _run(ops, N, alpha, q8[rows], k8[rows], v8[rows], sq[rows], sk[rows], sv[rows], sub_offs, bias,
                fp8_pv=True).cpu()
     assert torch.equal(sub, full[rows])
+
+
+def test_fwd_pv8_long_n(hip_lib):
+    """max_seq_len 8192: the per-block table of per-key factors (4 bytes per
+    key, 8 per key tile of N) no longer leaves room for two blocks per CU, so
+    the kernel runs one block per CU; sequences of 8192 and 5000 tokens (128
+    and 79 key tiles) against the oracle, with bias."""
+    ops = _ops()
+    lengths = [8192, 5000, 3]
+    N = 8192
+    alpha = 1.0 / 128 ** 0.5
+    q8, k8, v8, sq, sk, sv, offs = _case(lengths, H=1, seed=13)
+    bias = orc.make_bias(1, 3000)
+    print(f"FP8 P.V fwd: lengths={lengths} N={N}", flush=True)
+    out = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias, fp8_pv=True)
+    want = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias)
+    exact = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias, quantize=False)
+    assert torch.isfinite(out.float()).all()
+    _check(out, want, exact, f"lengths={lengths} N={N}")
