@@ -477,3 +477,32 @@ def test_full_fp8_backward(hip_lib, per_tensor, with_bias):
         m = float((gt.double() - ex).abs().max() / ex.abs().max())
         assert e2 <= 6e-2 and snr >= 24.0 and m <= 0.2, (
             f"{name}: rel L2 {e2:.3e}, SNR {snr:.1f} dB, max {m:.3e} vs the float64 backward")
+
+
+def test_full_fp8_backward_long_n(hip_lib):
+    """The full-FP8 backward at max_seq_len 8192 (64 key blocks of 128, each
+    run as two workgroups, and 64 query tiles in the dQ walk) against the
+    oracle with the same casts: relative L2 <= 1e-2 for dq, dk, dv, dbias."""
+    from oracle import hstu_bwd_fp8full_oracle as FO
+
+    ops = _ops()
+    H, D = 1, 128
+    lengths = [8192, 2500, 1]
+    N = 8192
+    alpha = 1.0 / D ** 0.5
+    q8, k8, v8, sq, sk, sv, offs, dout, y8, e8 = _full_fp8_case(lengths, H, D, 5, False)
+    bias = orc.make_bias(H, 3000)
+    dev = [t.to(DEV) for t in (q8, k8, v8)]
+    scales = [s.to(DEV).contiguous() for s in (sq, sk, sv)]
+    g = [torch.full(q8.shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+    db = torch.empty(bias.shape, dtype=torch.float32, device=DEV)
+    print(f"full-FP8 bwd: lengths={lengths} N={N}", flush=True)
+    ops.triton_hstu_attention_bwd(dout.to(DEV), *dev, *g, offs.to(DEV), None, N, alpha, 0, 0, None, False, 0,
+                                  *scales, attn_bias=bias.to(DEV), dbias=db, full_fp8=True)
+    torch.cuda.synchronize()
+    got = [t.float().cpu() for t in g] + [db.cpu()]
+    want = FO.full_fp8_bwd(N, alpha, q8, k8, v8, sq, sk, sv, offs, y8, e8, attn_bias=bias)
+    for name, gt, w in zip(("dq", "dk", "dv", "dbias"), got, want):
+        assert not torch.isnan(gt).any(), name
+        e = orc.rel_l2(w, gt)
+        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
