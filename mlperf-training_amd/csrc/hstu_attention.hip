@@ -835,23 +835,24 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   // end place them one at a time between pieces of this wave's VALU work
   // instead of back to back (a wave does not issue past an MFMA that waits
   // for the matrix core)
-  auto epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb, auto masked_tag,
-                      auto bconst_tag, auto&& hook) __attribute__((always_inline)) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
-    constexpr bool BCONST = decltype(bconst_tag)::value;
-    const float* bias_lds = (const float*)(vb + C::BIAS_REL);
-    const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
+  // the lane's 16 bias values (the window holds clamped values, so tiles
+  // past the bias range read their constant) and c_k of key sub-tile b,
+  // read ahead of the epilogue that uses them
+  auto load_bias = [&](const uint8_t* vb, int n0, int b, float (&bj)[16], float& ck) __attribute__((always_inline)) {
     // the lane's bias window as an opaque LDS address, so that its 16 reads
     // share one base register and differ in the instructions' offsets
     uint32_t baddr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(vb + C::BIAS_REL) +
                      4 * (bias_lo + 32 * (1 - b));
-    if constexpr (BIAS && !BCONST) asm volatile("" : "+v"(baddr));
+    if constexpr (BIAS) asm volatile("" : "+v"(baddr));
     const __attribute__((address_space(3))) float* bias_lane = (const __attribute__((address_space(3))) float*)(uintptr_t)baddr;
-    const float ck = ckt[n0 + 32 * b + l32];
-    const int key = n0 + 32 * b + l32;
-    float bj[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) bj[j] = BIAS ? (BCONST ? bconst : bias_lane[8 * (j >> 2) + (j & 3)]) : 0.f;
+    for (int j = 0; j < 16; ++j) bj[j] = BIAS ? bias_lane[8 * (j >> 2) + (j & 3)] : 0.f;
+    ck = ckt[n0 + 32 * b + l32];
+  };
+  auto epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const float (&bj)[16], float ck,
+                      auto masked_tag, auto&& hook) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    const int key = n0 + 32 * b + l32;
     u32x4 pk;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -871,23 +872,16 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
       pk[i] = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
     }
     *(u32x4*)(pw + pst + 1024 * b) = pk;
-    __builtin_amdgcn_sched_group_barrier(0x100, 9, 0);  // the LDS reads
 #pragma unroll
     for (int g = 0; g < 3; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x402, 24, 0);  // VALU incl. transcendental
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
     }
   };
-  auto run_epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const uint8_t* vb, auto&& hook) __attribute__((always_inline)) {
-    const bool masked = n0 + 32 * b + 31 > mw0;
-    const bool bias_const = BIAS && (m0 - n0 - (C::BN - 1) >= R1);
-    if (masked) {
-      if (bias_const) epilogue(s, scl, b, n0, vb, std::true_type{}, std::true_type{}, hook);
-      else epilogue(s, scl, b, n0, vb, std::true_type{}, std::false_type{}, hook);
-    } else {
-      if (bias_const) epilogue(s, scl, b, n0, vb, std::false_type{}, std::true_type{}, hook);
-      else epilogue(s, scl, b, n0, vb, std::false_type{}, std::false_type{}, hook);
-    }
+  auto run_epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const float (&bj)[16], float ck,
+                          auto&& hook) __attribute__((always_inline)) {
+    if (n0 + 32 * b + 31 > mw0) epilogue(s, scl, b, n0, bj, ck, std::true_type{}, hook);
+    else epilogue(s, scl, b, n0, bj, ck, std::false_type{}, hook);
   };
   // P (A operand of P.V) reads, u = 0..3: key rows 32 hg + 8 u + j16 / 2,
   // byte column 16 hi16 + 8 (j16 & 1), in chunk hi16 ^ (j16 >> 3); lane l32
@@ -968,7 +962,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
       // wave's last tile: the K stage and the key scales are in bounds)
       i32x8 kr[2];
       k_read(kstage(t), 1, kr);
-      run_epilogue(s0, sc0, 0, n0, vb, [&](int g) __attribute__((always_inline)) {
+      // both sub-tiles' bias values and c_k now: sub-tile 1's arrive during
+      // the epilogue of sub-tile 0
+      float bj0[16], bj1[16], ck0, ck1;
+      load_bias(vb, n0, 0, bj0, ck0);
+      load_bias(vb, n0, 1, bj1, ck1);
+      run_epilogue(s0, sc0, 0, n0, bj0, ck0, [&](int g) __attribute__((always_inline)) {
         if (g == 0) {
           f32x16 z;
 #pragma unroll
@@ -981,7 +980,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
         }
       });
       k_read(kstage(t + 1), 0, kr);
-      run_epilogue(s1, sc1, 1, n0, vb, [&](int g) __attribute__((always_inline)) {
+      run_epilogue(s1, sc1, 1, n0, bj1, ck1, [&](int g) __attribute__((always_inline)) {
         if (g == 0) {
           f32x16 z;
 #pragma unroll
