@@ -74,7 +74,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--only", choices=("output_block", "layer", "layer_fp8_dgrad", "delta", "do_quant", "gemm", "wgrad"),
+    ap.add_argument("--only", choices=("output_block", "layer", "layer_bf16_dgrad", "delta", "do_quant", "gemm", "wgrad"),
                     default=None,
                     help="run just one secondary measurement and print its JSON (for profiling)")
     ap.add_argument("--flush", choices=("read", "write"), default="read",
@@ -459,23 +459,26 @@ def layer_params(torch, E=512, H=4, D=128, seed=0):
     return {k: v.to(torch.bfloat16).requires_grad_(True) for k, v in p.items()}
 
 
-def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
+def layer_bench(torch, lengths, N, steps, warmup, flush, bf16_dgrad=False):
     """one whole HSTU layer in FP8, forward + backward, at
     config 3's shapes (T = 162 251, N = 4096, E = 512, H = 4, D = 128), with
     the relative bias and output dropout 0.3 (mask16).  The FP8 scales are
     the reference's scale-state buffers, calibrated by the first (untimed,
-    bf16) calls and frozen before timing.  fp8_dgrad: the
-    output and UVQK projections' dgrads in FP8 (e5m2 gradients, the
-    reference's DLRM_HSTU_FP8_BWD=1 and DLRM_HSTU_FP8_BWD_UVQK=1, passed as an
-    explicit Fp8BackwardConfig; the UVQK gradient's cast also gives the bias
-    gradient) and the UVQK weight gradient from the forward's e4m3 LN output
+    bf16) calls and frozen before timing.  By default the backward runs the
+    reference's production FP8 arms (yambda_5b.gin:229, 1115, 1188-1189):
+    the output and UVQK projections' dgrads in FP8 (e5m2 gradients,
+    DLRM_HSTU_FP8_BWD=1 and DLRM_HSTU_FP8_BWD_UVQK=1, passed as an explicit
+    Fp8BackwardConfig; the UVQK gradient's cast also gives the bias
+    gradient), the UVQK weight gradient from the forward's e4m3 LN output
     (UVQK_WGRAD=fp8t) and the output projection's from the forward's e4m3 y
-    (OUT_WGRAD=1), with enough warm-up steps for their delayed scales to publish.
-    The attention backward is the full-FP8 one (DLRM_HSTU_FP8_BWD_FULL) in
-    both forms, as in the headline."""
+    (OUT_WGRAD=1), with enough warm-up steps for their delayed scales to
+    publish.  bf16_dgrad: those four GEMMs in bf16 instead.  The attention
+    backward is the full-FP8 one (DLRM_HSTU_FP8_BWD_FULL) in both forms, as in
+    the headline."""
     import hstu_amd
     import hstu_amd.bwd_fp8 as bwd_fp8
 
+    fp8_dgrad = not bf16_dgrad
     cfg = bwd_fp8.Fp8BackwardConfig(enabled=fp8_dgrad, uvqk=fp8_dgrad, uvqk_wgrad_fp8t=fp8_dgrad,
                                     out_wgrad_fp8=fp8_dgrad, attn_full_fp8=True)
     bwd_fp8.reset_sites()
@@ -530,7 +533,8 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, fp8_dgrad=False):
     return {"workload": "BASELINE config 5: HSTU layer fwd+bwd in FP8 (LN -> FP8 UVQK GEMM -> FP8 attention with "
                         "bias, the FP8 P.V forward and the full-FP8 attention backward -> LN(attn)*silu(u)*dropout -> FP8 out-proj + "
                         "residual; %s), "
-                        "config 3 shapes, E=512" % ("e5m2 x e4m3 out-proj and UVQK dgrads, e4m3 x e5m2 wgrads" if fp8_dgrad
+                        "config 3 shapes, E=512" % ("the reference's production FP8 backward arms: e5m2 x e4m3 "
+                                                    "out-proj and UVQK dgrads, e4m3 x e5m2 wgrads" if fp8_dgrad
                                                     else "bf16 dgrad/wgrad"),
             "T": T, "ms_per_step": round(m, 4), "fwd_ms": round(float(np.median(tf)), 4),
             "bwd_ms": round(float(np.median(tb)), 4),
@@ -614,9 +618,9 @@ def main():
     if args.only == "output_block":
         print(json.dumps(output_block_bench(torch, int(np.sum(lengths)), args.steps, args.warmup, flush)), flush=True)
         return
-    if args.only in ("layer", "layer_fp8_dgrad"):
+    if args.only in ("layer", "layer_bf16_dgrad"):
         print(json.dumps(layer_bench(torch, lengths, N, args.steps, args.warmup, flush,
-                                     fp8_dgrad=args.only == "layer_fp8_dgrad")), flush=True)
+                                     bf16_dgrad=args.only == "layer_bf16_dgrad")), flush=True)
         return
     if args.only == "delta":
         print(json.dumps(delta_bench(torch, lengths, N, args.steps, args.warmup, flush)), flush=True)
@@ -724,7 +728,7 @@ def main():
         res["output_block"] = output_block_bench(torch, int(np.sum(lengths)), max(args.steps // 2, 5), 2, flush)
         torch.cuda.empty_cache()
         res["layer"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush)
-        res["layer_fp8_dgrad"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush, fp8_dgrad=True)
+        res["layer_bf16_dgrad"] = layer_bench(torch, lengths, N, max(args.steps // 2, 5), 2, flush, bf16_dgrad=True)
         torch.cuda.empty_cache()
         res["delta"] = delta_bench(torch, lengths, N, args.steps, 3, flush)
         res["do_quant"] = do_quant_bench(torch, lengths, N, args.steps, 3, flush)
