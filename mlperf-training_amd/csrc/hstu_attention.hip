@@ -1159,18 +1159,21 @@ __device__ __forceinline__ float dpp_row(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
+// folds a fragment into the bucket pair (hi, lo) = diagonals p - 4g, p - 4g - 16
+__device__ __forceinline__ void diag_accumulate_to(float& hi, float& lo, const float (&v)[4]) {
+  // lane p takes column p + r of register r (row_shl:r): diagonal p - 4g
+  hi += v[0];
+  hi += dpp_row<0x101>(v[1]);
+  hi += dpp_row<0x102>(v[2]);
+  hi += dpp_row<0x103>(v[3]);
+  // ... and column p + r - 16 (row_shr:16-r): diagonal p - 4g - 16
+  lo += dpp_row<0x11F>(v[1]);
+  lo += dpp_row<0x11E>(v[2]);
+  lo += dpp_row<0x11D>(v[3]);
+}
 template <int S>
 __device__ __forceinline__ void diag_accumulate(float (&a)[4], const float (&v)[4]) {
-  constexpr int HI = 1 - S, LO = 2 - S;
-  // lane p takes column p + r of register r (row_shl:r): diagonal p - 4g
-  a[HI] += v[0];
-  a[HI] += dpp_row<0x101>(v[1]);
-  a[HI] += dpp_row<0x102>(v[2]);
-  a[HI] += dpp_row<0x103>(v[3]);
-  // ... and column p + r - 16 (row_shr:16-r): diagonal p - 4g - 16
-  a[LO] += dpp_row<0x11F>(v[1]);
-  a[LO] += dpp_row<0x11E>(v[2]);
-  a[LO] += dpp_row<0x11D>(v[3]);
+  diag_accumulate_to(a[1 - S], a[2 - S], v);
 }
 
 template <int CTRL, int ROWS>
@@ -1193,23 +1196,27 @@ __device__ __forceinline__ float lane_xor16(float x) {
   return __builtin_bit_cast(float, (threadIdx.x & 16) ? s[0] : s[1]);
 }
 
-// Sum over the wave of diagonal p + 16(1-g) for lane 16g+p (g = 3, p = 0 is
-// diagonal -32, always 0).
-__device__ __forceinline__ float diag_reduce(const float (&a)[4], int lane) {
-  const int g = lane >> 4, p = lane & 15;
-  // undo the 4g skew: lane (g, p) reads lane (g, p + 4g mod 16); wrapped
-  // reads land one bucket (16 diagonals) lower.  DPP and permlane swaps
-  // only: no LDS round trip
-  const bool wrap = p + 4 * g >= 16;
-  const float g0 = skew_undo(a[0]), g1 = skew_undo(a[1]), g2 = skew_undo(a[2]), g3 = skew_undo(a[3]);
-  const float b0 = wrap ? 0.f : g0, b1 = wrap ? g0 : g1, b2 = wrap ? g1 : g2, b3 = wrap ? g2 : g3;
-  // reduce-scatter over the four rows: row g keeps bucket g
-  const bool upper = lane >= 32, odd = (g & 1) != 0;
+// Reduce-scatter over the four rows of unskewed buckets b0..b3 (lane p of
+// every row holds the same diagonal of a bucket): lane 16g+p gets the sum over
+// the rows of bucket g at p.  DPP and permlane swaps only: no LDS round trip.
+__device__ __forceinline__ float diag_scatter(float b0, float b1, float b2, float b3, int lane) {
+  const bool upper = lane >= 32, odd = ((lane >> 4) & 1) != 0;
   float ka = upper ? b2 : b0, kb = upper ? b3 : b1;
   const float sa = upper ? b0 : b2, sb = upper ? b1 : b3;
   ka += lane_xor32(sa);
   kb += lane_xor32(sb);
   return (odd ? kb : ka) + lane_xor16(odd ? ka : kb);
+}
+
+// Sum over the wave of diagonal p + 16(1-g) for lane 16g+p (g = 3, p = 0 is
+// diagonal -32, always 0).
+__device__ __forceinline__ float diag_reduce(const float (&a)[4], int lane) {
+  const int g = lane >> 4, p = lane & 15;
+  // undo the 4g skew: lane (g, p) reads lane (g, p + 4g mod 16); wrapped
+  // reads land one bucket (16 diagonals) lower
+  const bool wrap = p + 4 * g >= 16;
+  const float g0 = skew_undo(a[0]), g1 = skew_undo(a[1]), g2 = skew_undo(a[2]), g3 = skew_undo(a[3]);
+  return diag_scatter(wrap ? 0.f : g0, wrap ? g0 : g1, wrap ? g1 : g2, wrap ? g2 : g3, lane);
 }
 
 template <int D, bool FP8, bool GENERIC, bool BIAS>
@@ -2424,50 +2431,83 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
     }
   };
   float dclamp = 0.f;
-  // bias gradient of the staged step: 32 x 32 sub-tiles (half hf, query pair
-  // qp) x (this wave's 32 keys), from the C-fragment layout the pieces have
+  // bias gradient of the staged step, as per-lane diagonal sums in buckets
+  // of 16 offsets.  Bucket v (bk[v + 1], v = -1..8) holds in lane (g, li) the
+  // offset i - j = base0 + 16 v - (li - 4 g), base0 = m0 - kb BN - 32 wave
+  // (i - j of this wave's first query and key); the 32 x 32 sub-tile of
+  // query rows 32 s .. 32 s + 31 (s = 2 hf + qp) folds into buckets
+  // 2 s - 1 .. 2 s + 2.  Unskewed, bucket w holds base0 + 16 w - li in every
+  // row.  The next step's buckets 7, 8 are this step's -1, 0, so a step
+  // completes the offsets base0 + 17 .. base0 + 144 (unskewed buckets 2..9,
+  // bucket 9 the previous step's 1) and carries buckets -1, 0 and unskewed 1.
+  float cr_m1 = 0.f, cr_0 = 0.f, cr_g1 = 0.f;
+  const bool wrap = li + 4 * g >= 16;
+  // unskewed buckets t0..t3 = w, w + 1, w + 2, w + 3: lane (g, li) sums
+  // offset xw - li + 16 g, xw = base0 + 16 w
+  auto flush = [&](float t0, float t1, float t2, float t3, int xw) {
+    const float dv = diag_scatter(t0, t1, t2, t3, lane);
+    const int off = xw + 16 * g - li;
+    if (off >= R1) dclamp += dv;
+    else if (off >= 0) atomicAdd(&hist[off], dv);
+  };
+  // the 16 scores of sub-tile s, query sub-tile a, key sub-tile kt
+  auto piece = [&](const u32x4 (&pcs)[4], const float (&iskv)[2], int s, int a, int kt, float (&v)[4]) {
+    const int hf = s >> 1, qp = s & 1;
+    const uint32_t w = pcs[2 * kt + hf][2 * qp + a];
+    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
+    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
+    const float c = iskv[kt] * grp[hf];
+    v[0] = lo[0] * c;
+    v[1] = lo[1] * c;
+    v[2] = hi[0] * c;
+    v[3] = hi[1] * c;
+  };
   auto bias_grad = [&](int kb, const u32x4 (&pcs)[4], const float (&iskv)[2]) {
+    const int base0 = m0 - kb * C::BN - 32 * wave;
+    if (base0 - 31 >= R1) {  // every offset clamps
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int qp = 0; qp < 2; ++qp) {
-        const int base = (m0 + 64 * hf + 32 * qp) - (kb * C::BN + 32 * wave);  // i - j of its (0, 0)
-        if (base + 31 < 0) continue;  // above the diagonal: zero
-        float v[2][2][4];             // [query sub-tile][key sub-tile][r]
-#pragma unroll
-        for (int a = 0; a < 2; ++a) {
+        for (int a = 0; a < 2; ++a)
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt) {
-            const uint32_t w = pcs[2 * kt + hf][2 * qp + a];
-            const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-            const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-            const float c = iskv[kt] * grp[hf];
-            v[a][kt][0] = lo[0] * c;
-            v[a][kt][1] = lo[1] * c;
-            v[a][kt][2] = hi[0] * c;
-            v[a][kt][3] = hi[1] * c;
+            float v[4];
+            piece(pcs, iskv, s, a, kt, v);
+            dclamp += (v[0] + v[1]) + (v[2] + v[3]);
           }
-        }
-        if (base - 31 >= R1) {  // every offset clamps
-#pragma unroll
-          for (int a = 0; a < 2; ++a)
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-              for (int r = 0; r < 4; ++r) dclamp += v[a][kt][r];
-          continue;
-        }
-        float dacc[4] = {0.f, 0.f, 0.f, 0.f};
-        diag_accumulate<0>(dacc, v[0][0]);
-        diag_accumulate<0>(dacc, v[1][1]);
-        diag_accumulate<1>(dacc, v[0][1]);
-        diag_accumulate<-1>(dacc, v[1][0]);
-        const float dv = diag_reduce(dacc, lane);
-        const int off = base - (li + 16 - 16 * g);
-        if (off >= R1) dclamp += dv;
-        else if (off >= 0) atomicAdd(&hist[off], dv);
-      }
+      cr_m1 = cr_0 = cr_g1 = 0.f;
+      return;
     }
+    float bk[10];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bk[i] = 0.f;
+    bk[8] = cr_m1;
+    bk[9] = cr_0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      // rows = queries (16 a + 4 g + r), cols = keys (16 kt + li): shift kt - a
+      float v00[4], v11[4], v01[4], v10[4];
+      piece(pcs, iskv, s, 0, 0, v00);
+      piece(pcs, iskv, s, 1, 1, v11);
+      piece(pcs, iskv, s, 0, 1, v01);
+      piece(pcs, iskv, s, 1, 0, v10);
+      diag_accumulate_to(bk[2 * s + 1], bk[2 * s + 2], v00);
+      diag_accumulate_to(bk[2 * s + 1], bk[2 * s + 2], v11);
+      diag_accumulate_to(bk[2 * s], bk[2 * s + 1], v01);
+      diag_accumulate_to(bk[2 * s + 2], bk[2 * s + 3], v10);
+    }
+    float gu[10];  // unskewed bucket w = 1..9
+#pragma unroll
+    for (int w = 1; w < 9; ++w) gu[w] = skew_undo(bk[w + 1]);
+    gu[9] = cr_g1;
+    float t[10];  // bucket w: offsets base0 + 16 w - li (wrapped lanes read bucket w - 1)
+#pragma unroll
+    for (int w = 2; w < 10; ++w) t[w] = wrap ? gu[w - 1] : gu[w];
+    flush(t[2], t[3], t[4], t[5], base0 + 32);
+    flush(t[6], t[7], t[8], t[9], base0 + 96);
+    cr_m1 = bk[0];
+    cr_0 = bk[1];
+    cr_g1 = gu[1];
   };
 
   // operand reads: dS^T columns (byte 16 chunk + li of the permuted rows:
@@ -2516,6 +2556,13 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   }
 
   if constexpr (BIAS) {
+    // the carried buckets: unskewed 7, 8, 9 of a step past the last (its
+    // buckets 1..6 are empty), offsets down to the last step's base0 - 47
+    const int base_v = m0 - nsteps * C::BN - 32 * wave;
+    if (base_v + 144 >= 0) {
+      const float g7 = skew_undo(cr_m1), g8 = skew_undo(cr_0);
+      flush(0.f, wrap ? 0.f : g7, wrap ? g7 : g8, wrap ? g8 : cr_g1, base_v + 96);
+    }
     if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
     __syncthreads();
     float* dst = p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1) + R1;
