@@ -452,6 +452,30 @@ int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
                     float* dweight, float* dbias, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
 
+/* Workspace of hstu_outproj_ln_bwd (per-workgroup dweight / dbias partials). */
+int64_t hstu_outproj_ln_bwd_workspace_bytes(int rows);
+
+/*
+ * The output projection's FP8 dgrad fused with the LN * U * dropout backward
+ * of the [u' | x | y] concat (D = 512, W [1536, 512]): dy = bf16(g8 . w8^T *
+ * g_scale * w_scale) is formed 64 rows at a time on chip and consumed by the
+ * row backward, never stored.  g8: e5m2 [rows, 512] (ldg bytes); w8: e4m3
+ * [1536, 512] (ldw bytes); g_scale, w_scale: fp32 device scalars.  The other
+ * arguments and outputs are hstu_ln_mul_bwd's (concat_u = concat_x = 1, no
+ * recomputed y): dx and du equal the unfused hstu_fp8_gemm (e5m2 dgrad) +
+ * hstu_ln_mul_bwd bit for bit; dweight / dbias are deterministic (fixed
+ * summation order, a different one than the unfused path's).
+ * Replaces: l11_outproj_lnmd_bwd_launch,
+ *           ops/hip/l11_outproj_lnmd.cu:906-910 (host finalize of its
+ *           partials: triton_hstu_linear.py:5410-5470).
+ */
+int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_scale, const void* w8, int64_t ldw,
+                        const float* w_scale, const void* x, int64_t ldx, const void* u, int64_t ldu,
+                        const float* weight, const float* bias, const float* mean, const float* rstd,
+                        int rows, int D, int mul_u_act, int silu_u, float dropout_ratio, const void* mask,
+                        int64_t ldm, void* dx, int64_t lddx, void* du, int64_t lddu, float* dweight,
+                        float* dbias, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 /*
  * Delta-q ("cached" / targets-only) attention: DS compact query rows per
  * sequence (delta_q [B*DS, H, D]) at positions L-DS .. L-1 of each sequence,

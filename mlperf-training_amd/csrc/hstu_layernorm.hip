@@ -11,7 +11,9 @@
 // D = 512); mean and variance are exact two-pass sums over the wave.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "hstu_common.h"
@@ -407,6 +409,106 @@ __device__ __forceinline__ float keep_scaled(float v, float s, uint32_t mw, uint
   return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v * s) & m);
 }
 
+// Raw inputs of one row for a lane's EPT columns c0 .. c0 + EPT - 1.
+template <int EPT>
+struct LnBwdRowIn {
+  RawT<EPT> x, gy, gx, gu, u;
+  MaskRawT<EPT> m;
+  float mean, rstd;
+};
+
+// The per-row backward of LN * U * dropout for a lane's EPT columns: du, the
+// recomputed y (Y), dx, and the lane's dweight / dbias sums.  Shared by the
+// standalone backward and the out-projection-fused one, so that both compute
+// a row with the same operations in the same order.
+template <int EPT, int ACT, bool DROP, bool Y>
+__device__ __forceinline__ void ln_bwd_row(const BwdArgs& a, int64_t row, int c0, const LnBwdRowIn<EPT>& in,
+                                           const float (&w)[EPT], const float (&bb)[EPT], float (&dw)[EPT],
+                                           float (&db)[EPT]) {
+  constexpr int D = 64 * EPT;
+  constexpr bool HU = ACT != kNoU;
+  const bool cu = HU && a.concat_u, cx = a.concat_x;
+  const int col_u = 0, col_x = cu ? 1 : 0, col_z = (cu ? 1 : 0) + (cx ? 1 : 0);
+  const uint32_t pos_x = 1, pos_u = cx ? 2 : 1;  // bit of x / u in a mask byte
+  const float mean = in.mean, rstd = in.rstd;
+  float x[EPT], gy[EPT], gx[EPT], gu[EPT], u[EPT];
+  unpack_bf16<EPT>(in.x, x);
+  unpack_bf16<EPT>(in.gy, gy);
+  unpack_bf16<EPT>(in.gx, gx);
+  unpack_bf16<EPT>(in.gu, gu);
+  if constexpr (HU) unpack_bf16<EPT>(in.u, u);
+  uint32_t mw[EPT / 4];
+  if constexpr (DROP) {
+#pragma unroll
+    for (int q = 0; q < EPT / 4; ++q) mw[q] = in.m[q];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const uint32_t b0 = 8 * (i % 4);
+      gy[i] = keep_scaled(gy[i], a.drop_scale, mw[i / 4], b0);
+      gx[i] = keep_scaled(gx[i], a.drop_scale, mw[i / 4], b0 + pos_x);
+      gu[i] = keep_scaled(gu[i], a.drop_scale, mw[i / 4], b0 + pos_u);
+    }
+  }
+  // du and the recomputed y first, so that u, ln and m(u) die before the
+  // row reductions; xh, g and gx stay live for dx.
+  float xh[EPT], g[EPT], s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    xh[i] = (x[i] - mean) * rstd;
+    const float ln = xh[i] * w[i] + bb[i];
+    float mul = 1.f;
+    if constexpr (HU) {
+      const float sg = sigmoidf(u[i]);
+      const float silu = u[i] * sg;
+      const float dsilu = sg + silu * (1.f - sg);
+      float dm;
+      if constexpr (ACT == kActSilu) {
+        mul = silu;
+        dm = dsilu;
+      } else if constexpr (ACT == kActSigmoid) {
+        mul = sg;
+        dm = sg * (1.f - sg);
+      } else {
+        mul = u[i];
+        dm = 1.f;
+      }
+      gu[i] = gy[i] * ln * dm + (a.silu_u ? gu[i] * dsilu : gu[i]);
+      if (a.silu_u) u[i] = silu;  // the concatenated u, for the recomputed y
+    }
+    g[i] = gy[i] * mul;  // gradient at ln
+    gy[i] = ln * mul;    // y before dropout (gy is dead from here)
+  }
+  if constexpr (HU) store_bf16<EPT>(a.du + row * a.lddu + c0, gu);
+  if constexpr (Y) {
+    if constexpr (DROP) {
+#pragma unroll
+      for (int i = 0; i < EPT; ++i) {
+        const uint32_t b0 = 8 * (i % 4);
+        gy[i] = keep_scaled(gy[i], a.drop_scale, mw[i / 4], b0);
+        x[i] = keep_scaled(x[i], a.drop_scale, mw[i / 4], b0 + pos_x);
+        if constexpr (HU) u[i] = keep_scaled(u[i], a.drop_scale, mw[i / 4], b0 + pos_u);
+      }
+    }
+    uint16_t* yr = a.y + row * a.ldy + c0;
+    if (cu) store_bf16<EPT>(yr + col_u * D, u);
+    if (cx) store_bf16<EPT>(yr + col_x * D, x);
+    store_bf16<EPT>(yr + col_z * D, gy);
+  }
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) {
+    const float wg = w[i] * g[i];
+    s1 += xh[i] * wg;
+    s2 += wg;
+    dw[i] += g[i] * xh[i];
+    db[i] += g[i];
+  }
+  const float c1 = wave_sum(s1) * a.inv_d, c2 = wave_sum(s2) * a.inv_d;
+  float dx[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; ++i) dx[i] = gx[i] + (w[i] * g[i] - (xh[i] * c1 + c2)) * rstd;
+  store_bf16<EPT>(a.dx + row * a.lddx + c0, dx);
+}
+
 // Wave i handles rows i, i + nwaves, ... in order; each block then sums its
 // four waves' dweight / dbias in a fixed order, so the result is deterministic.
 // ACT: kActNone / kActSilu / kActSigmoid, or kNoU (no u: weighted LayerNorm).
@@ -427,15 +529,9 @@ __global__ void __launch_bounds__(kThreads) ln_mul_bwd_kernel(BwdArgs a) {
   }
   const bool cu = HU && a.concat_u, cx = a.concat_x;
   const int col_u = 0, col_x = cu ? 1 : 0, col_z = (cu ? 1 : 0) + (cx ? 1 : 0);
-  const uint32_t pos_x = 1, pos_u = cx ? 2 : 1;  // bit of x / u in a mask byte
   // Software pipeline: the next row's loads are in flight while this row is
   // computed (rows are independent).
-  struct RowIn {
-    RawT<EPT> x, gy, gx, gu, u;
-    MaskRawT<EPT> m;
-    float mean, rstd;
-  };
-  auto fetch = [&](int64_t row, RowIn& r) {
+  auto fetch = [&](int64_t row, LnBwdRowIn<EPT>& r) {
     const uint16_t* dyr = a.dy + row * a.lddy + c0;
     r.x = load_raw<EPT>(a.x + row * a.ldx + c0);
     r.gy = load_raw<EPT>(dyr + col_z * D);
@@ -447,88 +543,12 @@ __global__ void __launch_bounds__(kThreads) ln_mul_bwd_kernel(BwdArgs a) {
     r.rstd = a.rstd[row];
   };
   int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  RowIn cur;
+  LnBwdRowIn<EPT> cur;
   if (row < a.rows) fetch(row, cur);
   for (; row < a.rows; row += nw) {
-    RowIn nxt;
+    LnBwdRowIn<EPT> nxt;
     if (row + nw < a.rows) fetch(row + nw, nxt);
-    const float mean = cur.mean, rstd = cur.rstd;
-    float x[EPT], gy[EPT], gx[EPT], gu[EPT], u[EPT];
-    unpack_bf16<EPT>(cur.x, x);
-    unpack_bf16<EPT>(cur.gy, gy);
-    unpack_bf16<EPT>(cur.gx, gx);
-    unpack_bf16<EPT>(cur.gu, gu);
-    if constexpr (HU) unpack_bf16<EPT>(cur.u, u);
-    uint32_t mw[EPT / 4];
-    if constexpr (DROP) {
-#pragma unroll
-      for (int q = 0; q < EPT / 4; ++q) mw[q] = cur.m[q];
-#pragma unroll
-      for (int i = 0; i < EPT; ++i) {
-        const uint32_t b0 = 8 * (i % 4);
-        gy[i] = keep_scaled(gy[i], a.drop_scale, mw[i / 4], b0);
-        gx[i] = keep_scaled(gx[i], a.drop_scale, mw[i / 4], b0 + pos_x);
-        gu[i] = keep_scaled(gu[i], a.drop_scale, mw[i / 4], b0 + pos_u);
-      }
-    }
-    // du and the recomputed y first, so that u, ln and m(u) die before the
-    // row reductions; xh, g and gx stay live for dx.
-    float xh[EPT], g[EPT], s1 = 0.f, s2 = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      xh[i] = (x[i] - mean) * rstd;
-      const float ln = xh[i] * w[i] + bb[i];
-      float mul = 1.f;
-      if constexpr (HU) {
-        const float sg = sigmoidf(u[i]);
-        const float silu = u[i] * sg;
-        const float dsilu = sg + silu * (1.f - sg);
-        float dm;
-        if constexpr (ACT == kActSilu) {
-          mul = silu;
-          dm = dsilu;
-        } else if constexpr (ACT == kActSigmoid) {
-          mul = sg;
-          dm = sg * (1.f - sg);
-        } else {
-          mul = u[i];
-          dm = 1.f;
-        }
-        gu[i] = gy[i] * ln * dm + (a.silu_u ? gu[i] * dsilu : gu[i]);
-        if (a.silu_u) u[i] = silu;  // the concatenated u, for the recomputed y
-      }
-      g[i] = gy[i] * mul;  // gradient at ln
-      gy[i] = ln * mul;    // y before dropout (gy is dead from here)
-    }
-    if constexpr (HU) store_bf16<EPT>(a.du + row * a.lddu + c0, gu);
-    if constexpr (Y) {
-      if constexpr (DROP) {
-#pragma unroll
-        for (int i = 0; i < EPT; ++i) {
-          const uint32_t b0 = 8 * (i % 4);
-          gy[i] = keep_scaled(gy[i], a.drop_scale, mw[i / 4], b0);
-          x[i] = keep_scaled(x[i], a.drop_scale, mw[i / 4], b0 + pos_x);
-          if constexpr (HU) u[i] = keep_scaled(u[i], a.drop_scale, mw[i / 4], b0 + pos_u);
-        }
-      }
-      uint16_t* yr = a.y + row * a.ldy + c0;
-      if (cu) store_bf16<EPT>(yr + col_u * D, u);
-      if (cx) store_bf16<EPT>(yr + col_x * D, x);
-      store_bf16<EPT>(yr + col_z * D, gy);
-    }
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-      const float wg = w[i] * g[i];
-      s1 += xh[i] * wg;
-      s2 += wg;
-      dw[i] += g[i] * xh[i];
-      db[i] += g[i];
-    }
-    const float c1 = wave_sum(s1) * a.inv_d, c2 = wave_sum(s2) * a.inv_d;
-    float dx[EPT];
-#pragma unroll
-    for (int i = 0; i < EPT; ++i) dx[i] = gx[i] + (w[i] * g[i] - (xh[i] * c1 + c2)) * rstd;
-    store_bf16<EPT>(a.dx + row * a.lddx + c0, dx);
+    ln_bwd_row<EPT, ACT, DROP, Y>(a, row, c0, cur, w, bb, dw, db);
     cur = nxt;
   }
 #pragma unroll
@@ -564,6 +584,225 @@ __global__ void __launch_bounds__(kThreads) ln_reduce_partials(const float* part
     if (c < D) dweight[c] = t;
     else dbias[c - D] = t;
   }
+}
+
+// ------------------------------------------------- fused out-projection backward
+// The output projection's FP8 dgrad fused with the LN * U * dropout backward
+// (the reference's DLRM_HSTU_FP8_BWD_OUTPROJ_LNMD_FUSED kernel,
+// ops/hip/l11_outproj_lnmd.cu:1-6): dy = bf16(g8 . w8^T * (s_g s_w) + 0),
+// [rows, 1536] = the [u' | x | y] gradient, exactly as the e5m2 dgrad GEMM
+// computes it (same MFMA, operand bytes, k order and epilogue), but it never
+// leaves the chip: the LN backward consumes it row by row.
+//
+// One persistent workgroup per CU (8 waves) walks blocks of 64 rows.  GEMM
+// phase: the block's e5m2 rows sit in LDS (64 x 512 bytes, 544-byte pitch);
+// wave w owns columns 32 w .. 32 w + 31 of each of the six 256-column tiles
+// for all 64 rows, and loads its W fragments straight from L2 into registers
+// two (tile, k-step) chunks ahead -- no W staging, so the phase has no
+// barrier.  After a tile's fourth k-step the wave's 32 results per lane are
+// rounded to bf16 and kept packed (96 registers for the six tiles).
+// Consumer phase: two groups of 32 rows; every wave writes its columns of the
+// group into an LDS row buffer (3088-byte pitch), then runs four of its rows
+// through ln_bwd_row (the standalone backward's row code), the x / u / mask
+// loads of its next two rows in flight.
+struct OutBwdArgs {
+  BwdArgs ln;        // dy, y unused
+  const uint8_t* g8;  // e5m2 [rows, 512]
+  int64_t ldg;        // bytes
+  const uint8_t* w8;  // e4m3 [1536, 512]
+  int64_t ldw;        // bytes
+  const float* g_scale;
+  const float* w_scale;
+  int nblk;
+};
+constexpr int kObThreads = 512, kObRows = 64, kObN = 1536, kObK = 512, kObD = 512, kObTileN = 256;
+constexpr int kObApitch = kObK + 32;      // 544: conflict-free b128 fragment reads
+constexpr int kObRpitch = 2 * kObN + 16;  // 3088
+constexpr int kObGroup = 32;              // rows per consumer group
+constexpr int kObA = kObRows * kObApitch;                       // 34816
+constexpr int kObLnOff = kObA + kObGroup * kObRpitch;           // LN weight, bias: fp32 [2][512]
+constexpr int kObSumOff = kObLnOff + 2 * kObD * 4;              // the workgroup's dweight, dbias sums
+constexpr int kObLds = kObSumOff + 2 * kObD * 4;                // 141824
+constexpr int kObTiles = kObN / kObTileN, kObSteps = kObK / 128, kObChunks = kObTiles * kObSteps;  // 6, 4, 24
+constexpr int kObGrid = 256;
+
+template <int ACT, bool DROP>
+__global__ void __launch_bounds__(kObThreads, 1) outproj_ln_bwd_kernel(OutBwdArgs p) {
+  constexpr int EPT = 8;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* const al = smem;
+  uint8_t* const rl = smem + kObA;
+  float* const lnwb = (float*)(smem + kObLnOff);
+  float* const wsum = (float*)(smem + kObSumOff);
+  const BwdArgs& a = p.ln;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
+  lnwb[tid] = a.w[tid];
+  lnwb[kObD + tid] = a.b[tid];  // published by the first block's prologue barrier
+  wsum[tid] = wsum[kObD + tid] = 0.f;  // thread t alone adds to entries t and 512 + t
+  const int c0 = lane * EPT;
+  const float scale = p.g_scale[0] * p.w_scale[0];
+  const uint32_t ldw = (uint32_t)p.ldw, ldg = (uint32_t)p.ldg;
+  const BufRsrc wr = make_rsrc(p.w8, (kObN - 1) * ldw + kObK);
+  // W fragment (tile nt, k-step kk, column sub-tile cf): row 256 nt + 32 wave
+  // + 16 cf + li, bytes 128 kk + 16 g and + 64 (the chunk part in soffset)
+  const uint32_t w_voff = (uint32_t)(32 * wave + li) * ldw + 16 * g;
+  auto load_w = [&](int c, i32x8 (&f)[2]) {
+    const uint32_t soff = (uint32_t)((c >> 2) * kObTileN) * ldw + 128 * (c & 3);
+#pragma unroll
+    for (int cf = 0; cf < 2; ++cf) {
+      const uint32_t v = w_voff + (uint32_t)(16 * cf) * ldw;
+      f[cf] = cat8(buf_ld128(wr, v, soff), buf_ld128(wr, v + 64, soff));
+    }
+  };
+
+  // the consumer's global inputs of one row (dy comes from LDS)
+  auto fetch = [&](int64_t row, LnBwdRowIn<EPT>& r) {
+    r.x = load_raw<EPT>(a.x + row * a.ldx + c0);
+    r.u = load_raw<EPT>(a.u + row * a.ldu + c0);
+    if constexpr (DROP) r.m = *(const MaskRawT<EPT>*)(a.mask + row * a.ldm + c0);
+    r.mean = a.mean[row];
+    r.rstd = a.rstd[row];
+  };
+
+  const int a_rd = li * kObApitch + 16 * g;
+  for (int blk = blockIdx.x; blk < p.nblk; blk += gridDim.x) {
+    const int64_t m0 = (int64_t)blk * kObRows;
+    const int mrows = (int)min((int64_t)kObRows, (int64_t)a.rows - m0);
+    i32x8 wf[2][2];
+    {
+      // the block's e5m2 rows (rows past the end read as zero); W chunks 0, 1
+      const BufRsrc ar = make_rsrc(p.g8 + m0 * p.ldg, (uint32_t)(mrows - 1) * ldg + kObK);
+      u32x4 ast[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + kObThreads * i;
+        ast[i] = buf_ld128(ar, (uint32_t)(e >> 5) * ldg + 16 * (e & 31), 0);
+      }
+      load_w(0, wf[0]);
+      load_w(1, wf[1]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = tid + kObThreads * i;
+        *(u32x4*)(al + (e >> 5) * kObApitch + 16 * (e & 31)) = ast[i];
+      }
+    }
+    __syncthreads();
+    uint32_t dyp[kObTiles][2][4][2];  // [tile][column sub-tile][row sub-tile][pair]
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int c = 0; c < kObChunks; ++c) {
+      const int nt = c >> 2, kk = c & 3;
+      if (kk == 0) {
+#pragma unroll
+        for (int cf = 0; cf < 2; ++cf)
+#pragma unroll
+          for (int rf = 0; rf < 4; ++rf) acc[cf][rf] = zero4();
+      }
+#pragma unroll
+      for (int rf = 0; rf < 4; ++rf) {
+        const uint8_t* r = al + a_rd + rf * 16 * kObApitch + kk * 128;
+        const i32x8 bop = cat8(lds_ld128(r), lds_ld128(r + 64));
+#pragma unroll
+        for (int cf = 0; cf < 2; ++cf)
+          acc[cf][rf] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(wf[c & 1][cf], bop, acc[cf][rf], 0, 1, 0, 0,
+                                                                        0, 0);
+      }
+      if (c + 2 < kObChunks) load_w(c + 2, wf[c & 1]);
+      if (kk == 3) {
+        // lane: row 16 rf + li, columns 256 nt + 32 wave + 16 cf + 4 g .. + 3
+#pragma unroll
+        for (int cf = 0; cf < 2; ++cf)
+#pragma unroll
+          for (int rf = 0; rf < 4; ++rf) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = acc[cf][rf][r] * scale + 0.f;
+            dyp[nt][cf][rf][0] = pack_bf16(v[0], v[1]);
+            dyp[nt][cf][rf][1] = pack_bf16(v[2], v[3]);
+          }
+      }
+      // no scheduling across chunks: hoisted reads and MFMAs of later chunks
+      // would keep several chunks' operands live
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // consumer: group G = rows 32 G .. 32 G + 31 of the block (row sub-tiles
+    // 2 G, 2 G + 1); wave w then takes rows w, w + 8, w + 16, w + 24 of it,
+    // two rows' loads in flight
+    float dw[EPT], db[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) dw[i] = db[i] = 0.f;
+    auto put = [&](int G) {
+      uint8_t* dst = rl + li * kObRpitch + 2 * (32 * wave + 4 * g);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int nt = 0; nt < kObTiles; ++nt)
+#pragma unroll
+          for (int cf = 0; cf < 2; ++cf)
+            *(u32x2*)(dst + 16 * h * kObRpitch + 2 * (nt * kObTileN + 16 * cf)) =
+                u32x2{dyp[nt][cf][2 * G + h][0], dyp[nt][cf][2 * G + h][1]};
+    };
+#pragma unroll 1
+    for (int G = 0; G < 2; ++G) {
+      LnBwdRowIn<EPT> in[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int rr = kObGroup * G + 8 * k + wave;
+        if (rr < mrows) fetch(m0 + rr, in[k]);
+      }
+      if (G == 0) put(0);
+      else put(1);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int rr = kObGroup * G + 8 * k + wave;
+        LnBwdRowIn<EPT>& cur = in[k & 1];
+        if (rr < mrows) {
+          const uint8_t* src = rl + (8 * k + wave) * kObRpitch + 16 * lane;
+          cur.gu = *(const u32x4*)src;
+          cur.gx = *(const u32x4*)(src + 2 * kObD);
+          cur.gy = *(const u32x4*)(src + 4 * kObD);
+          // the LN weight and bias, read per row so that they hold no
+          // registers across the phases
+          float w[EPT], bb[EPT];
+          const f32x4 w0 = *(const f32x4*)(lnwb + c0), w1 = *(const f32x4*)(lnwb + c0 + 4);
+          const f32x4 b0 = *(const f32x4*)(lnwb + kObD + c0), b1 = *(const f32x4*)(lnwb + kObD + c0 + 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            w[i] = w0[i];
+            w[i + 4] = w1[i];
+            bb[i] = b0[i];
+            bb[i + 4] = b1[i];
+          }
+          ln_bwd_row<EPT, ACT, DROP, false>(a, m0 + rr, c0, cur, w, bb, dw, db);
+        }
+        if (k + 2 < 4 && rr + 16 < mrows) fetch(m0 + rr + 16, cur);
+      }
+      __syncthreads();
+    }
+    // the block's dweight / dbias: its 8 waves summed in a fixed order (the
+    // A tile's LDS is free until the next block's prologue), added to the
+    // workgroup's sums
+    float* red = (float*)smem;  // [8][2][512]
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      red[(wave * 2 + 0) * kObD + c0 + i] = dw[i];
+      red[(wave * 2 + 1) * kObD + c0 + i] = db[i];
+    }
+    __syncthreads();
+    for (int c = tid; c < 2 * kObD; c += kObThreads) {
+      const int k = c / kObD, cc = c - k * kObD;
+      float t = red[k * kObD + cc];
+#pragma unroll
+      for (int v = 1; v < 8; ++v) t += red[(v * 2 + k) * kObD + cc];
+      wsum[c] += t;
+    }
+    __syncthreads();
+  }
+  // the workgroup's sums over its blocks (in block order)
+  float* dst = a.partial + (int64_t)blockIdx.x * 2 * kObD;
+  for (int c = tid; c < 2 * kObD; c += kObThreads) dst[c] = wsum[c];
 }
 
 // ------------------------------------------------------------------ host
@@ -772,5 +1011,87 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   launch_bwd(D, u == nullptr ? kNoU : mul_u_act, mask != nullptr, y != nullptr, a, stream);
   hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial,
                      u == nullptr ? kBwdBlocksMax : kBwdBlocksU, D, dweight, dbias);
+  return (int)hipGetLastError();
+}
+
+extern "C" int64_t hstu_outproj_ln_bwd_workspace_bytes(int rows) {
+  if (rows < 0) return -1;
+  return (int64_t)kObGrid * 2 * kObD * 4;
+}
+
+extern "C" int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_scale, const void* w8, int64_t ldw,
+                                   const float* w_scale, const void* x, int64_t ldx, const void* u, int64_t ldu,
+                                   const float* weight, const float* bias, const float* mean, const float* rstd,
+                                   int rows, int D, int mul_u_act, int silu_u, float dropout_ratio, const void* mask,
+                                   int64_t ldm, void* dx, int64_t lddx, void* du, int64_t lddu, float* dweight,
+                                   float* dbias, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (rows < 0 || g8 == nullptr || w8 == nullptr || g_scale == nullptr || w_scale == nullptr || x == nullptr ||
+      u == nullptr || dx == nullptr || du == nullptr || weight == nullptr || bias == nullptr || mean == nullptr ||
+      rstd == nullptr || dweight == nullptr || dbias == nullptr || mul_u_act < 0 || mul_u_act > 2 ||
+      ldg < kObK || ldw < kObK || ldx < D || ldu < D || lddx < D || lddu < D ||
+      (mask != nullptr && (ldm < D || !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))))
+    return HSTU_E_BAD_ARG;
+  if (D != kObD) return HSTU_E_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < hstu_outproj_ln_bwd_workspace_bytes(rows)) return HSTU_E_BAD_ARG;
+  auto al16 = [](const void* p, int64_t ld, int esz) { return aligned(p, 16) && (ld * esz) % 16 == 0; };
+  if (!al16(g8, ldg, 1) || !al16(w8, ldw, 1) || !al16(x, ldx, 2) || !al16(u, ldu, 2) || !al16(dx, lddx, 2) ||
+      !al16(du, lddu, 2) || (mask != nullptr && (!aligned(mask, 8) || ldm % 8 != 0)))
+    return HSTU_E_UNSUPPORTED;
+  if ((int64_t)(kObN - 1) * ldw + kObK > 0xffffffffLL || (int64_t)(kObRows - 1) * ldg + kObK > 0xffffffffLL)
+    return HSTU_E_UNSUPPORTED;
+  if (rows == 0) {
+    // no rows: zero weight gradients, like the standalone backward
+    hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream,
+                       (const float*)workspace, 0, D, dweight, dbias);
+    return (int)hipGetLastError();
+  }
+  OutBwdArgs p{};
+  BwdArgs& a = p.ln;
+  a.x = (const uint16_t*)x;
+  a.ldx = ldx;
+  a.u = (const uint16_t*)u;
+  a.ldu = ldu;
+  a.w = weight;
+  a.b = bias;
+  a.mean = mean;
+  a.rstd = rstd;
+  a.inv_d = 1.f / (float)D;
+  a.rows = rows;
+  a.silu_u = silu_u;
+  a.concat_u = 1;
+  a.concat_x = 1;
+  a.mask = (const uint8_t*)mask;
+  a.ldm = ldm;
+  a.drop_scale = 1.f / (1.f - dropout_ratio);
+  a.dx = (uint16_t*)dx;
+  a.lddx = lddx;
+  a.du = (uint16_t*)du;
+  a.lddu = lddu;
+  a.partial = (float*)workspace;
+  p.g8 = (const uint8_t*)g8;
+  p.ldg = ldg;
+  p.w8 = (const uint8_t*)w8;
+  p.ldw = ldw;
+  p.g_scale = g_scale;
+  p.w_scale = w_scale;
+  p.nblk = (int)(((int64_t)rows + kObRows - 1) / kObRows);
+  const int grid = std::min(p.nblk, kObGrid);
+  const void* fn;
+  const bool drop = mask != nullptr;
+  switch (mul_u_act) {
+    case kActNone: fn = drop ? (const void*)outproj_ln_bwd_kernel<kActNone, true> : (const void*)outproj_ln_bwd_kernel<kActNone, false>; break;
+    case kActSilu: fn = drop ? (const void*)outproj_ln_bwd_kernel<kActSilu, true> : (const void*)outproj_ln_bwd_kernel<kActSilu, false>; break;
+    default: fn = drop ? (const void*)outproj_ln_bwd_kernel<kActSigmoid, true> : (const void*)outproj_ln_bwd_kernel<kActSigmoid, false>; break;
+  }
+  static std::once_flag once[6];
+  static hipError_t set_err[6];
+  const int slot = 2 * mul_u_act + (drop ? 1 : 0);
+  std::call_once(once[slot], [&] { set_err[slot] = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kObLds); });
+  if (set_err[slot] != hipSuccess) return (int)set_err[slot];
+  void* args[] = {&p};
+  hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(kObThreads), args, (size_t)kObLds, stream);
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial, grid, D,
+                     dweight, dbias);
   return (int)hipGetLastError();
 }

@@ -42,6 +42,8 @@ EXPORTED_SYMBOLS = (
     "hstu_ln_mul_fwd",
     "hstu_ln_mul_bwd_workspace_bytes",
     "hstu_ln_mul_bwd",
+    "hstu_outproj_ln_bwd_workspace_bytes",
+    "hstu_outproj_ln_bwd",
     "hstu_delta_attn_workspace_bytes",
     "hstu_delta_attn_fwd",
     "hstu_delta_attn_bwd",
@@ -163,6 +165,12 @@ _SIGNATURES = {
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
          _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
+    ),
+    "hstu_outproj_ln_bwd_workspace_bytes": (_i64, [_i32]),
+    "hstu_outproj_ln_bwd": (
+        _i32,
+        [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32,
+         _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
     ),
 }
 

@@ -57,7 +57,10 @@ class Fp8BackwardConfig:
     out_wgrad_fp8 / uvqk_wgrad_fp8t: the FP8 weight gradients;
     margin, warmup_calls, refresh_calls, grad_format: the delayed-scale policy;
     attn_full_fp8: the attention's full-FP8 backward (``DLRM_HSTU_FP8_BWD_FULL``;
-    None: the attention op's process default).
+    None: the attention op's process default);
+    outproj_lnmd_fused: the output projection's e5m2 dgrad and the LN * U *
+    dropout backward as one kernel when the FP8 weight gradient is on
+    (``DLRM_HSTU_FP8_BWD_OUTPROJ_LNMD_FUSED``, ``triton_hstu_linear.py:5410-5470``).
     """
 
     enabled: bool = False
@@ -69,6 +72,7 @@ class Fp8BackwardConfig:
     refresh_calls: int = 200
     grad_format: str = "e5m2"
     attn_full_fp8: Optional[bool] = None
+    outproj_lnmd_fused: bool = False
 
     def __post_init__(self):
         if self.grad_format not in ("e5m2", "e4m3"):
@@ -89,6 +93,7 @@ class Fp8BackwardConfig:
             warmup_calls=max(1, int(env.get("DLRM_HSTU_FP8_BWD_WARMUP_CALLS", "4"))),
             refresh_calls=max(1, int(env.get("DLRM_HSTU_FP8_BWD_REFRESH_CALLS", "200"))),
             grad_format=env.get("DLRM_HSTU_FP8_BWD_GRAD_FORMAT", "e5m2").lower(),
+            outproj_lnmd_fused=env.get("DLRM_HSTU_FP8_BWD_OUTPROJ_LNMD_FUSED", "0") == "1",
         )
 
     @property
@@ -391,19 +396,33 @@ def output_projection_dgrad(gradient: torch.Tensor, weight: torch.Tensor, return
     weight gradient that reuses the cast; the decode scale is then the one
     the payload was cast with even on a refresh call (the reference's
     out-wgrad path snapshots it the same way, ``ops/triton/bwd_fp8.py:1472-1482``)."""
+    ops = output_projection_dgrad_operands(gradient, weight, snapshot_decode_scale=return_quantized, config=config)
+    if ops is None:
+        return None
+    g8, gs, w8, ws = ops
+    dy = fp8_dgrad(g8, gs, w8, ws, gradient.dtype if gradient.dtype == torch.bfloat16 else torch.bfloat16)
+    return (dy, g8, gs) if return_quantized else dy
+
+
+def output_projection_dgrad_operands(gradient: torch.Tensor, weight: torch.Tensor, snapshot_decode_scale: bool = True,
+                                     config: Optional[Fp8BackwardConfig] = None):
+    """The FP8 dgrad's operands (gradient e5m2 [M, N_out], its decode scale,
+    weight^T e4m3 [K_in, N_out] as [N, K] rows, its scale), or None while the
+    gradient's scale warms up (``output_projection_dgrad_operands``,
+    ``ops/triton/bwd_fp8.py:1431``): the output projection dgrad runs on them, or
+    the fused dgrad + LN * U * dropout backward does."""
     cfg = _cfg(config)
     if not cfg.enabled or not _has_stable_identity(weight):
         return None
     if gradient.dim() != 2 or gradient.shape[-1] % 128 or weight.shape[0] % 128:
         return None
     quantized = quantize_gradient("output_projection", gradient, discriminator=weight.data_ptr(),
-                                  snapshot_decode_scale=return_quantized, config=cfg)
+                                  snapshot_decode_scale=snapshot_decode_scale, config=cfg)
     if quantized is None:
         return None
     g8, gs = quantized
     w8, ws = quantize_weight(weight)
-    dy = fp8_dgrad(g8, gs, w8, ws, gradient.dtype if gradient.dtype == torch.bfloat16 else torch.bfloat16)
-    return (dy, g8, gs) if return_quantized else dy
+    return g8, gs, w8, ws
 
 
 def uvqk_fp8_backward_enabled(config: Optional[Fp8BackwardConfig] = None) -> bool:

@@ -237,6 +237,42 @@ def _ln_bwd(dy, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, con
     return dx, du, dw, db, y
 
 
+def _outproj_ln_bwd(g8, g_scale, w8, w_scale, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, act,
+                    du_row_width=0):
+    """The output projection's FP8 dgrad fused with the LN * U * dropout
+    backward ([u' | x | y] concat, D = 512): dy = g8 . w8^T * (s_g s_w) never
+    leaves the kernel.  Returns (dx, du, dweight fp32, dbias fp32); dx and du
+    equal the unfused dgrad + ``_ln_bwd`` bit for bit."""
+    x = _rows(x)
+    u = _rows(u)
+    N, D = x.shape
+    if D != 512 or tuple(w8.shape) != (3 * D, 512) or tuple(g8.shape) != (N, 512):
+        raise ValueError(f"fused output-projection backward: x {tuple(x.shape)}, g8 {tuple(g8.shape)}, "
+                         f"w8 {tuple(w8.shape)}")
+    dx = torch.empty((N, D), dtype=x.dtype, device=x.device)
+    du = _alloc_du(u, du_row_width)
+    dw = torch.empty((D,), dtype=torch.float32, device=x.device)
+    db = torch.empty((D,), dtype=torch.float32, device=x.device)
+    w = _param(weight, D, 1.0, x.device)
+    b = _param(bias, D, 0.0, x.device)
+    if mask is not None:
+        mask = _rows(mask)
+    g8 = g8.contiguous()
+    w8 = w8.contiguous()
+    gs = g_scale.to(torch.float32).reshape(-1)[:1].contiguous()
+    ws_ = w_scale.to(torch.float32).reshape(-1)[:1].contiguous()
+    nbytes = int(_lib.fn("hstu_outproj_ln_bwd_workspace_bytes")(N))
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
+    st = _lib.fn("hstu_outproj_ln_bwd")(
+        g8.data_ptr(), g8.stride(0), gs.data_ptr(), w8.data_ptr(), w8.stride(0), ws_.data_ptr(), x.data_ptr(),
+        x.stride(0), u.data_ptr(), u.stride(0), w.data_ptr(), b.data_ptr(), mean.contiguous().data_ptr(),
+        rstd.contiguous().data_ptr(), N, D, _ACT[act], int(bool(silu_u)), float(dropout_ratio), _lib.ptr(mask),
+        0 if mask is None else mask.stride(0), dx.data_ptr(), dx.stride(0), du.data_ptr(), du.stride(0),
+        dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nbytes, _stream(x))
+    _lib.check(st, "hstu_outproj_ln_bwd")
+    return dx, du, dw, db
+
+
 def triton_layer_norm_mul_dropout_bwd(
     dy: torch.Tensor,
     x: torch.Tensor,
@@ -405,8 +441,26 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         # FP8 dgrad (DLRM_HSTU_FP8_BWD=1; triton_hstu_linear.py:5586-5588): None
         # while the gradient's scale warms up, then e5m2 dout . e4m3 W^T
         cfg = ctx.fp8_backward
-        q = (bwd_fp8.output_projection_dgrad(dout, output_weight, return_quantized=True, config=cfg)
-             if bwd_fp8.enabled(cfg) else None)
+        # the fused FP8 dgrad + LN * U * dropout backward (dy never in HBM) when
+        # the FP8 weight gradient needs no recomputed y and the shapes are the
+        # kernel's ([u' | x | y] concat, D = 512)
+        if (y8 is not None and bwd_fp8.enabled(cfg) and bwd_fp8.resolve(cfg).outproj_lnmd_fused and concat_u
+                and concat_x and attn.shape[-1] == 512 and tuple(output_weight.shape) == (1536, 512)):
+            ops = bwd_fp8.output_projection_dgrad_operands(dout, output_weight, snapshot_decode_scale=True,
+                                                           config=cfg)
+            if ops is not None:
+                g8, gs, w8, ws = ops
+                dattn, du, dw, db = _outproj_ln_bwd(g8, gs, w8, ws, attn, u, norm_weight, norm_bias, mean, rstd,
+                                                    ratio, mask, silu_u, act, ctx.du_row_width)
+                d_out_w = fp8_wgrad(y8, g8, ctx.y8_scale, gs).to(output_weight.dtype)
+                return (dattn, du, dout, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
+                        None, None, None, None, None, None, None, None, None, None, None, None, None, None, None,
+                        None)
+            # the gradient's scale warms up (this call is counted): bf16 dgrad
+            q = None
+        else:
+            q = (bwd_fp8.output_projection_dgrad(dout, output_weight, return_quantized=True, config=cfg)
+                 if bwd_fp8.enabled(cfg) else None)
         dy = q[0] if q is not None else _fp8.proj_mm(dout, output_weight)
         # FP8 weight gradient (DLRM_HSTU_FP8_BWD_OUT_WGRAD=1) from the forward's
         # e4m3 y and the dgrad's e5m2 dout: the bf16 y is then not recomputed

@@ -184,3 +184,45 @@ def test_hstu_layer_calibrated_scale_states_no_host_sync(hip_lib, monkeypatch):
     for name, r, got in [("dx", xr.grad, xd.grad)] + [(f"d{k}", pr[k].grad, pd[k].grad) for k in params]:
         e = _rel_l2(r, got.float().cpu())
         assert e <= 3e-2, f"{name} rel L2 {e:.3e}"
+
+
+def test_hstu_layer_fused_outproj_backward(hip_lib, monkeypatch):
+    """The production FP8 arms with the output projection's dgrad fused into
+    the LN * U * dropout backward (``outproj_lnmd_fused``) against the same
+    layer unfused, with dropout: every gradient bit-equal except the output
+    LayerNorm's weight and bias (fp32 sums in another fixed order: rtol 1e-5),
+    which feed nothing upstream."""
+    import hstu_amd
+    import hstu_amd.bwd_fp8 as B
+
+    monkeypatch.setattr(L_mod, "_mask16", True)
+    lengths = np.array([300, 77, 512, 129])
+    T, N, E = int(lengths.sum()), 512, 512
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    params = LO.make_layer_params(E, seed=6)
+    s_x, s_qkv = _calibrate(x, params)
+    dy = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    offs = orc.offsets_from_lengths(lengths).to(DEV)
+    sc = (lambda s: torch.full((1, 1), s, device=DEV))
+    grads = {}
+    for fused in (False, True):
+        cfg = B.Fp8BackwardConfig(enabled=True, uvqk=True, warmup_calls=1, uvqk_wgrad_fp8t=True,
+                                  out_wgrad_fp8=True, outproj_lnmd_fused=fused)
+        B.reset_sites()
+        pd = {k: v.to(DEV).requires_grad_(True) for k, v in params.items()}
+        for _ in range(2):                  # step 1 publishes the scales (bf16), step 2 runs FP8
+            for t in pd.values():
+                t.grad = None
+            xd = x.to(DEV).requires_grad_(True)
+            out = hstu_amd.hstu_layer(xd, offs, N, pd, dropout_ratio=0.3, training=True, fp8_input_scale=sc(s_x),
+                                      fp8_qkv_scale=sc(s_qkv), fp8_output_scale=sc(0.05), fp8_backward=cfg, seed=5)
+            out.backward(dy.to(DEV))
+        grads[fused] = {"out": out.detach(), "dx": xd.grad, **{k: t.grad for k, t in pd.items()}}
+    for name, ref in grads[False].items():
+        got = grads[True][name]
+        if name.startswith("output_norm"):
+            torch.testing.assert_close(got.float(), ref.float(), rtol=1e-5, atol=1e-6 * float(ref.abs().max()),
+                                       msg=name)
+        else:
+            assert torch.equal(got, ref), name
