@@ -471,8 +471,10 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, bf16_dgrad=False):
     Fp8BackwardConfig; the UVQK gradient's cast also gives the bias
     gradient), the UVQK weight gradient from the forward's e4m3 LN output
     (UVQK_WGRAD=fp8t) and the output projection's from the forward's e4m3 y
-    (OUT_WGRAD=1), with enough warm-up steps for their delayed scales to
-    publish.  bf16_dgrad: those four GEMMs in bf16 instead.  The attention
+    (OUT_WGRAD=1), the output projection's dgrad fused into the LN * U *
+    dropout backward (OUTPROJ_LNMD_FUSED, yambda_5b.gin:2104), with enough
+    warm-up steps for their delayed scales to publish.  bf16_dgrad: those
+    four GEMMs in bf16 instead.  The attention
     backward is the full-FP8 one (DLRM_HSTU_FP8_BWD_FULL) in both forms, as in
     the headline."""
     import hstu_amd
@@ -480,7 +482,7 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, bf16_dgrad=False):
 
     fp8_dgrad = not bf16_dgrad
     cfg = bwd_fp8.Fp8BackwardConfig(enabled=fp8_dgrad, uvqk=fp8_dgrad, uvqk_wgrad_fp8t=fp8_dgrad,
-                                    out_wgrad_fp8=fp8_dgrad, attn_full_fp8=True)
+                                    out_wgrad_fp8=fp8_dgrad, outproj_lnmd_fused=fp8_dgrad, attn_full_fp8=True)
     bwd_fp8.reset_sites()
     if fp8_dgrad:
         warmup = max(warmup, 5)
@@ -534,7 +536,8 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, bf16_dgrad=False):
                         "bias, the FP8 P.V forward and the full-FP8 attention backward -> LN(attn)*silu(u)*dropout -> FP8 out-proj + "
                         "residual; %s), "
                         "config 3 shapes, E=512" % ("the reference's production FP8 backward arms: e5m2 x e4m3 "
-                                                    "out-proj and UVQK dgrads, e4m3 x e5m2 wgrads" if fp8_dgrad
+                                                    "out-proj and UVQK dgrads (the out-proj one fused with the "
+                                                    "LN*U*dropout backward), e4m3 x e5m2 wgrads" if fp8_dgrad
                                                     else "bf16 dgrad/wgrad"),
             "T": T, "ms_per_step": round(m, 4), "fwd_ms": round(float(np.median(tf)), 4),
             "bwd_ms": round(float(np.median(tb)), 4),
