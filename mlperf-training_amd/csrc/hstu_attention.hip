@@ -43,6 +43,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <climits>
 #include <mutex>
 #include <type_traits>
 #include <vector>
@@ -1578,6 +1579,18 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_ws_kernel(AttnParams 
   const int trk = (4 * g + (li >> 2)) * C::P + (li & 3) * 8;   // K tile
   const int trs = (4 * g + (li >> 2)) * C::PS + (li & 3) * 8;  // dS rows
   float dclamp = 0.f;
+  // the bias gradient's carried buckets (see the step body) and the
+  // reduce-scatter of four unskewed buckets w .. w + 3: lane (g, li) sums
+  // offset xw - li + 16 g, xw = base0 + 16 w
+  float cr_m3 = 0.f, cr_m2 = 0.f, cr_g = 0.f;
+  int base_last = INT_MIN;
+  const bool bwrap = li + 4 * g >= 16;
+  auto bias_flush = [&](float t0, float t1, float t2, float t3, int xw) {
+    const float dv = diag_scatter(t0, t1, t2, t3, lane);
+    const int off = xw + 16 * g - li;
+    if (off >= R1) dclamp += dv;
+    else if (off >= 0) atomicAdd(&hist[off], dv);
+  };
 
   load(0);
   store();
@@ -1590,44 +1603,64 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_ws_kernel(AttnParams 
     if (step + 1 < nsteps) load(step + 1);
     if (wave_active && k0 <= qw0 + 31) {
       if constexpr (BIAS) {
-        // bias gradient from the held dS: 32x32 sub-tile per w' (keys k0 + 32wl ..)
+        // bias gradient from the held dS, as per-lane diagonal sums in
+        // buckets of 16 offsets: bucket v (bk[v + 3], v = -3..2) holds in lane
+        // (g, li) the offset i - j = base0 + 16 v - (li - 4 g), base0 = qw0 -
+        // k0; the 32 x 32 sub-tile of keys k0 + 32 wl .. folds into buckets
+        // -2 wl - 1 .. -2 wl + 2.  Unskewed, bucket w holds base0 + 16 w - li.
+        // The next step's buckets 1, 2 are this step's -3, -2, so a step
+        // completes the offsets base0 - 15 .. base0 + 48 (unskewed buckets
+        // 0..3, bucket 3 the previous step's -1) and carries -3, -2 and
+        // unskewed -1.
+        const int base0 = qw0 - k0;
+        auto piece = [&](int wl, int qs, int kt, float (&v)[4]) {
+          const u32x4 w = cur[2 * wl + kt];
+          v[0] = __builtin_bit_cast(float, w[2 * qs] << 16) * inv_db[qs][0];
+          v[1] = __builtin_bit_cast(float, w[2 * qs] & 0xffff0000u) * inv_db[qs][1];
+          v[2] = __builtin_bit_cast(float, w[2 * qs + 1] << 16) * inv_db[qs][2];
+          v[3] = __builtin_bit_cast(float, w[2 * qs + 1] & 0xffff0000u) * inv_db[qs][3];
+        };
+        if (base0 - 63 >= R1) {  // every offset clamps
 #pragma unroll
-        for (int wl = 0; wl < 2; ++wl) {
-          const int base = qw0 - (k0 + 32 * wl);  // i - j of (query 0, key 0) of the sub-tile
-          if (base + 31 < 0) continue;           // entirely above the diagonal (all zero)
-          float v[2][2][4];                      // [qs][kt][r]
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
-            const u32x4 w = cur[2 * wl + kt];
-#pragma unroll
-            for (int qs = 0; qs < 2; ++qs) {
-              v[qs][kt][0] = __builtin_bit_cast(float, w[2 * qs] << 16) * inv_db[qs][0];
-              v[qs][kt][1] = __builtin_bit_cast(float, w[2 * qs] & 0xffff0000u) * inv_db[qs][1];
-              v[qs][kt][2] = __builtin_bit_cast(float, w[2 * qs + 1] << 16) * inv_db[qs][2];
-              v[qs][kt][3] = __builtin_bit_cast(float, w[2 * qs + 1] & 0xffff0000u) * inv_db[qs][3];
-            }
-          }
-          if (base - 31 >= R1) {  // every offset clamps
+          for (int wl = 0; wl < 2; ++wl)
 #pragma unroll
             for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
-              for (int kt = 0; kt < 2; ++kt)
+              for (int kt = 0; kt < 2; ++kt) {
+                float v[4];
+                piece(wl, qs, kt, v);
+                dclamp += (v[0] + v[1]) + (v[2] + v[3]);
+              }
+          cr_m3 = cr_m2 = cr_g = 0.f;
+        } else {
+          float bk[6] = {0.f, 0.f, 0.f, 0.f, cr_m3, cr_m2};
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dclamp += v[qs][kt][r];
-            continue;
+          for (int wl = 0; wl < 2; ++wl) {
+            // rows = queries (16 qs + 4g + r), cols = keys (16 kt + li): shift kt - qs
+            float v00[4], v11[4], v01[4], v10[4];
+            piece(wl, 0, 0, v00);
+            piece(wl, 1, 1, v11);
+            piece(wl, 0, 1, v01);
+            piece(wl, 1, 0, v10);
+            const int o = 3 - 2 * wl;  // bucket index of v = -2 wl
+            diag_accumulate_to(bk[o], bk[o + 1], v00);
+            diag_accumulate_to(bk[o], bk[o + 1], v11);
+            diag_accumulate_to(bk[o - 1], bk[o], v01);
+            diag_accumulate_to(bk[o + 1], bk[o + 2], v10);
           }
-          float dacc[4] = {0.f, 0.f, 0.f, 0.f};
-          // rows = queries (16 qs + 4g + r), cols = keys (16 kt + li): shift kt - qs
-          diag_accumulate<0>(dacc, v[0][0]);
-          diag_accumulate<0>(dacc, v[1][1]);
-          diag_accumulate<1>(dacc, v[0][1]);
-          diag_accumulate<-1>(dacc, v[1][0]);
-          const float dv = diag_reduce(dacc, lane);
-          // this lane's diagonal col - row = li + 16 - 16g, i.e. offset i - j = base - that
-          const int off = base - (li + 16 - 16 * g);
-          if (off >= R1) dclamp += dv;
-          else if (off >= 0) atomicAdd(&hist[off], dv);
+          float gu[5];  // unskewed bucket w = -1..3 (gu[w + 1])
+#pragma unroll
+          for (int w = 0; w < 4; ++w) gu[w] = skew_undo(bk[w + 2]);
+          gu[4] = cr_g;
+          float t[4];  // bucket w = 0..3 (wrapped lanes read bucket w - 1)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) t[w] = bwrap ? gu[w] : gu[w + 1];
+          bias_flush(t[0], t[1], t[2], t[3], base0);
+          cr_m3 = bk[0];
+          cr_m2 = bk[1];
+          cr_g = gu[0];
         }
+        base_last = base0;
       }
       const uint8_t* kb = smem + C::K_OFF;
       const uint8_t* dsb = smem + C::DS_OFF + wave * C::DS_WAVE;
@@ -1657,6 +1690,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_ws_kernel(AttnParams 
   }
 
   if constexpr (BIAS) {
+    // the carried buckets: unskewed 1, 2, 3 of a step past the wave's last
+    // (its buckets -3..0 are empty), offsets down to that step's base0 - 63
+    if (wave_active && base_last != INT_MIN && base_last - 64 + 48 >= 0) {
+      const float g1 = skew_undo(cr_m3), g2 = skew_undo(cr_m2);
+      bias_flush(0.f, bwrap ? 0.f : g1, bwrap ? g1 : g2, bwrap ? g2 : cr_g, base_last - 64);
+    }
     if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
     __syncthreads();
     float* dst = dbias_copy + R1;
