@@ -257,7 +257,7 @@ def _outproj_ln_bwd(g8, g_scale, w8, w_scale, x, u, weight, bias, mean, rstd, dr
     b = _param(bias, D, 0.0, x.device)
     if mask is not None:
         mask = _rows(mask)
-    g8 = g8.contiguous()
+    g8 = _rows(g8)  # column slices stay in place (row stride = ldg)
     w8 = w8.contiguous()
     gs = g_scale.to(torch.float32).reshape(-1)[:1].contiguous()
     ws_ = w_scale.to(torch.float32).reshape(-1)[:1].contiguous()

@@ -293,3 +293,32 @@ def test_noalloc_forward_rejects_before_launch():
     assert call(100, 4, dtype=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_BAD_ARG  # e4m3 without scales
     assert call(100, 4, T=-1) == lib.HSTU_E_BAD_ARG
     assert call(0, 4) == 0                                            # empty batch: nothing to do
+
+
+def test_outproj_ln_bwd_rejects_before_launch():
+    """The fused output-projection backward's argument checks, on the CPU:
+    every call below returns before any HIP call."""
+    import hstu_amd._lib as lib
+
+    ws = lib.fn("hstu_outproj_ln_bwd_workspace_bytes")
+    assert ws(162251) == 256 * 2 * 512 * 4 and ws(-1) == -1
+    f = lib.fn("hstu_outproj_ln_bwd")
+    X, W = 4096, 8192  # fake device addresses: none of these calls may launch
+
+    def g(**kw):
+        a = dict(g8=X, ldg=512, gs=W, w8=X, ldw=512, ws_=W, x=X, ldx=512, u=X, ldu=512, w=W, b=W, mean=W, rstd=W,
+                 rows=64, D=512, act=1, silu_u=1, ratio=0.3, mask=X, ldm=512, dx=X, lddx=512, du=X, lddu=2048,
+                 dw=W, db=W, ws=W, wsb=ws(64), stream=None)
+        a.update(kw)
+        return f(*a.values())
+
+    assert g(wsb=100) == lib.HSTU_E_BAD_ARG
+    assert g(u=None) == lib.HSTU_E_BAD_ARG  # the [u' | x | y] concat needs u
+    assert g(gs=None) == lib.HSTU_E_BAD_ARG
+    assert g(ldg=256) == lib.HSTU_E_BAD_ARG  # a gradient row is 512 bytes
+    assert g(act=3) == lib.HSTU_E_BAD_ARG
+    assert g(ratio=1.5) == lib.HSTU_E_BAD_ARG
+    assert g(rows=-1) == lib.HSTU_E_BAD_ARG
+    assert g(D=256, ldx=256, ldu=256, lddx=256, lddu=256, ldm=256) == lib.HSTU_E_UNSUPPORTED
+    assert g(x=X + 2) == lib.HSTU_E_UNSUPPORTED  # rows not 16-byte aligned
+    assert g(ldg=520) == lib.HSTU_E_UNSUPPORTED  # gradient rows not 16-byte aligned

@@ -120,3 +120,23 @@ def test_fused_config3_rows(hip_lib):
     """Config 3's 162 251 tokens: bit-equal to the unfused pair."""
     print("fused out-proj backward: config 3 rows", flush=True)
     _check_equal(_case(162251, seed=1), "config 3 rows")
+
+
+def test_fused_strided_operands(hip_lib):
+    """Column slices of wider buffers (as the layer hands them over): x from
+    [N, 1024], u from [N, 2048], the e5m2 gradient from [N, 1024] bytes; bit-equal
+    to the unfused pair on the same views."""
+    N = 1500
+    c = _case(N, seed=12)
+    xs = torch.zeros(N, 1024, dtype=torch.bfloat16, device=DEV)
+    us = torch.zeros(N, 2048, dtype=torch.bfloat16, device=DEV)
+    gs8 = torch.zeros(N, 1024, dtype=torch.float8_e5m2, device=DEV)
+    xs[:, 256:768] = c["x"]
+    us[:, 1024:1536] = c["u"]
+    gs8[:, 512:] = c["g8"]
+    c.update(x=xs[:, 256:768], u=us[:, 1024:1536], g8=gs8[:, 512:])
+    assert c["x"].stride(0) == 1024 and c["u"].stride(0) == 2048 and c["g8"].stride(0) == 1024
+    ref = _unfused(c)
+    got = _fused(c)
+    torch.cuda.synchronize()
+    assert torch.equal(got[0], ref[1]) and torch.equal(got[1], ref[2])
