@@ -437,7 +437,9 @@ int64_t hstu_ln_mul_bwd_workspace_bytes(int rows, int D);
  * order); mask as written by the forward (NULL: no dropout).  Writes dx, du
  * (bf16, du only with u), dweight and dbias (fp32 [D], deterministic: fixed
  * summation order) and, when y != NULL, the bf16 forward output recomputed
- * (for the output projection's weight gradient).
+ * (for the output projection's weight gradient).  dres (NULL: none): a bf16
+ * [rows, D] gradient from a residual branch of x, added to dx before its
+ * rounding (not with concat_x or a mask).
  * Replaces: triton_layer_norm_mul_dropout_bwd, triton_hstu_linear.py:3689-3747
  *           (kernel _ln_mul_dropout_bwd_dx_du_rng :1566-1760, finalize
  *           _lnmd_bwd_finalize :3402-3431); triton_weighted_layer_norm_bwd,
@@ -449,6 +451,7 @@ int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
                     int mul_u_act, int silu_u, int concat_u, int concat_x,
                     float dropout_ratio, const void* mask, int64_t ldm,
                     void* dx, int64_t lddx, void* du, int64_t lddu, void* y, int64_t ldy,
+                    const void* dres, int64_t lddres,
                     float* dweight, float* dbias, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
 

@@ -399,6 +399,8 @@ struct BwdArgs {
   int64_t lddu;
   uint16_t* y;  // recomputed bf16 forward output (null: not wanted)
   int64_t ldy;
+  const uint16_t* dres;  // bf16 gradient added to dx (null: none; never with concat_x)
+  int64_t lddres;
   float* partial;  // [gridDim.x, 2, D]: per-block dweight, dbias sums
 };
 
@@ -535,7 +537,8 @@ __global__ void __launch_bounds__(kThreads) ln_mul_bwd_kernel(BwdArgs a) {
     const uint16_t* dyr = a.dy + row * a.lddy + c0;
     r.x = load_raw<EPT>(a.x + row * a.ldx + c0);
     r.gy = load_raw<EPT>(dyr + col_z * D);
-    r.gx = cx ? load_raw<EPT>(dyr + col_x * D) : RawT<EPT>{};
+    // without an x block, a residual branch's gradient takes gx's place: dx = gx + the LN backward
+    r.gx = cx ? load_raw<EPT>(dyr + col_x * D) : a.dres ? load_raw<EPT>(a.dres + row * a.lddres + c0) : RawT<EPT>{};
     r.gu = cu ? load_raw<EPT>(dyr + col_u * D) : RawT<EPT>{};
     if constexpr (HU) r.u = load_raw<EPT>(a.u + row * a.ldu + c0);
     if constexpr (DROP) r.m = *(const MaskRawT<EPT>*)(a.mask + row * a.ldm + c0);
@@ -965,8 +968,9 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
                                int64_t ldu, const float* weight, const float* bias, const float* mean,
                                const float* rstd, int rows, int D, int mul_u_act, int silu_u, int concat_u,
                                int concat_x, float dropout_ratio, const void* mask, int64_t ldm, void* dx,
-                               int64_t lddx, void* du, int64_t lddu, void* y, int64_t ldy, float* dweight,
-                               float* dbias, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                               int64_t lddx, void* du, int64_t lddu, void* y, int64_t ldy, const void* dres,
+                               int64_t lddres, float* dweight, float* dbias, void* workspace,
+                               int64_t workspace_bytes, hipStream_t stream) {
   if (rows < 0 || D <= 0 || dy == nullptr || x == nullptr || ldx < D || dx == nullptr || lddx < D ||
       (u != nullptr && (ldu < D || du == nullptr || lddu < D)) || weight == nullptr || bias == nullptr ||
       mean == nullptr || rstd == nullptr || dweight == nullptr || dbias == nullptr || mul_u_act < 0 ||
@@ -974,13 +978,14 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
     return HSTU_E_BAD_ARG;
   const int ncols = ncols_of(u, concat_u, concat_x);
   if (lddy < (int64_t)ncols * D || (y != nullptr && ldy < (int64_t)ncols * D)) return HSTU_E_BAD_ARG;
+  if (dres != nullptr && (concat_x || mask != nullptr || lddres < D)) return HSTU_E_BAD_ARG;
   if (!d_served(D)) return HSTU_E_UNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < hstu_ln_mul_bwd_workspace_bytes(rows, D)) return HSTU_E_BAD_ARG;
   const int ept = D / 64;
   auto ok = [&](const void* p, int64_t ld, int esz) { return aligned(p, esz * ept) && ld % ept == 0; };
   if (!ok(dy, lddy, 2) || !ok(x, ldx, 2) || !ok(dx, lddx, 2) ||
       (u != nullptr && (!ok(u, ldu, 2) || !ok(du, lddu, 2))) || (y != nullptr && !ok(y, ldy, 2)) ||
-      (mask != nullptr && !ok(mask, ldm, 1)))
+      (mask != nullptr && !ok(mask, ldm, 1)) || (dres != nullptr && !ok(dres, lddres, 2)))
     return HSTU_E_UNSUPPORTED;
   BwdArgs a{};
   a.dy = (const uint16_t*)dy;
@@ -1007,6 +1012,8 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   a.lddu = lddu;
   a.y = (uint16_t*)y;
   a.ldy = ldy;
+  a.dres = (const uint16_t*)dres;
+  a.lddres = lddres;
   a.partial = (float*)workspace;
   launch_bwd(D, u == nullptr ? kNoU : mul_u_act, mask != nullptr, y != nullptr, a, stream);
   hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial,

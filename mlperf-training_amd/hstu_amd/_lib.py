@@ -164,7 +164,7 @@ _SIGNATURES = {
     "hstu_ln_mul_bwd": (
         _i32,
         [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
-         _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
+         _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
     ),
     "hstu_outproj_ln_bwd_workspace_bytes": (_i64, [_i32]),
     "hstu_outproj_ln_bwd": (

@@ -203,7 +203,9 @@ def _alloc_du(u: torch.Tensor, du_row_width: int) -> torch.Tensor:
 
 
 def _ln_bwd(dy, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, concat_u, concat_x, act,
-            compute_y, du_row_width=0):
+            compute_y, du_row_width=0, dres=None):
+    """The LN * U * dropout backward.  ``dres``: a residual branch's bf16
+    gradient of x, added to dx inside the kernel (no x block, no mask)."""
     x = _rows(x)
     dy = _rows(dy)
     _check_bf16("dy", dy)
@@ -224,6 +226,11 @@ def _ln_bwd(dy, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, con
     b = _param(bias, D, 0.0, x.device)
     if mask is not None:
         mask = _rows(mask)
+    if dres is not None:
+        dres = _rows(dres)
+        _check_bf16("dres", dres)
+        if dres.shape != (N, D):
+            raise ValueError(f"dres {tuple(dres.shape)}; expected {(N, D)}")
     nbytes = int(_lib.fn("hstu_ln_mul_bwd_workspace_bytes")(N, D))
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     st = _lib.fn("hstu_ln_mul_bwd")(
@@ -231,8 +238,8 @@ def _ln_bwd(dy, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, con
         w.data_ptr(), b.data_ptr(), mean.contiguous().data_ptr(), rstd.contiguous().data_ptr(), N, D, _ACT[act],
         int(bool(silu_u)), int(cu), int(bool(concat_x)), float(dropout_ratio), _lib.ptr(mask),
         0 if mask is None else mask.stride(0), dx.data_ptr(), dx.stride(0), _lib.ptr(du),
-        0 if du is None else du.stride(0), _lib.ptr(y), 0 if y is None else y.stride(0), dw.data_ptr(),
-        db.data_ptr(), ws.data_ptr(), nbytes, _stream(x))
+        0 if du is None else du.stride(0), _lib.ptr(y), 0 if y is None else y.stride(0), _lib.ptr(dres),
+        0 if dres is None else dres.stride(0), dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nbytes, _stream(x))
     _lib.check(st, "hstu_ln_mul_bwd")
     return dx, du, dw, db, y
 
@@ -367,6 +374,21 @@ def triton_norm_mul_dropout(
 # ---------------------------------------------------------------------------
 # output block: LN * U * dropout -> output projection + residual
 # ---------------------------------------------------------------------------
+class ResidualLink:
+    """Hands the output block's residual gradient of the layer input x to the
+    preprocess backward of the same layer, which adds it inside its LayerNorm
+    backward (dx = dres + LN backward, one rounding) instead of autograd adding
+    the two bf16 gradients in a separate kernel.  The output block's backward
+    runs first (its inputs are the preprocess outputs); it stores the gradient
+    and returns None for x."""
+
+    def __init__(self) -> None:
+        self.grad: Optional[torch.Tensor] = None
+
+    def take(self) -> Optional[torch.Tensor]:
+        g, self.grad = self.grad, None
+        return g
+
 class HSTUComputeOutputFunction(torch.autograd.Function):
     """``HSTUComputeOutputFunction`` (``triton_hstu_linear.py:5109-5900``),
     default (unfused-backward) contract: e4m3 LN output into the FP8 output
@@ -379,7 +401,7 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
     def forward(ctx, attn, u, x, norm_weight, norm_bias, output_weight, eps, dropout_ratio, training,
                 silu_u=False, concat_u=False, concat_x=False, mul_u_activation_type="none", group_norm=False,
                 num_heads=1, linear_dim=-1, seed=None, recompute_y_in_backward=False, rng_row_indices=None,
-                fp8_output_scale=None, fp8_backward=None, dropout_mask16=None):
+                fp8_output_scale=None, fp8_backward=None, dropout_mask16=None, residual_link=None):
         if group_norm:
             raise NotImplementedError("group norm is not served by this build")
         if rng_row_indices is not None:
@@ -423,6 +445,7 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         # written as the leading columns of that buffer (triton_hstu_linear.py:5347-5350)
         ctx.du_row_width = int(getattr(u, "_hstu_duvqk_width", 0))
         ctx.cfg = (dropout_ratio, silu_u, concat_u, concat_x, mul_u_activation_type)
+        ctx.residual_link = residual_link
         return out
 
     @staticmethod
@@ -438,6 +461,12 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         y8 = ctx.saved_tensors[i] if ctx.y8_scale is not None else None
         ratio, silu_u, concat_u, concat_x, act = ctx.cfg
         dout = dout.contiguous()
+        # the residual gradient of x: to the same layer's preprocess backward
+        # when linked, else returned here
+        dres_x = dout
+        if ctx.residual_link is not None and ctx.needs_input_grad[2]:
+            ctx.residual_link.grad = dout
+            dres_x = None
         # FP8 dgrad (DLRM_HSTU_FP8_BWD=1; triton_hstu_linear.py:5586-5588): None
         # while the gradient's scale warms up, then e5m2 dout . e4m3 W^T
         cfg = ctx.fp8_backward
@@ -453,9 +482,9 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
                 dattn, du, dw, db = _outproj_ln_bwd(g8, gs, w8, ws, attn, u, norm_weight, norm_bias, mean, rstd,
                                                     ratio, mask, silu_u, act, ctx.du_row_width)
                 d_out_w = fp8_wgrad(y8, g8, ctx.y8_scale, gs).to(output_weight.dtype)
-                return (dattn, du, dout, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
+                return (dattn, du, dres_x, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
                         None, None, None, None, None, None, None, None, None, None, None, None, None, None, None,
-                        None)
+                        None, None)
             # the gradient's scale warms up (this call is counted): bf16 dgrad
             q = None
         else:
@@ -474,8 +503,8 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
                 y = y_re
             # y^T dout over the tokens: the split-K wgrad kernel
             d_out_w = token_wgrad(y, dout).to(output_weight.dtype)
-        return (dattn, du, dout, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
-                None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None)
+        return (dattn, du, dres_x, dw.to(norm_weight.dtype), db.to(norm_bias.dtype), d_out_w,
+                None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None)
 
 
 def triton_hstu_compute_output(
@@ -502,17 +531,19 @@ def triton_hstu_compute_output(
     *,
     fp8_backward: Optional[bwd_fp8.Fp8BackwardConfig] = None,
     dropout_mask16: Optional[bool] = None,
+    residual_link: Optional[ResidualLink] = None,
 ) -> torch.Tensor:
     """x + dropout([u' | attn | m(u) * LN(attn)]) @ output_weight
     (``triton_hstu_linear.py:6494-6572``).  ``fp8_output_scale``: a
     one-element device scale, or the reference's [2 + steps] scale state
     (calibrated by the bf16 calls until frozen).  ``fp8_backward``: the FP8
     backward arm's settings, ``dropout_mask16`` the dropout mask scheme
-    (default for both: the process default)."""
+    (default for both: the process default); ``residual_link`` hands x's
+    residual gradient to the same layer's preprocess backward."""
     return HSTUComputeOutputFunction.apply(attn, u, x, norm_weight, norm_bias, output_weight, eps, dropout_ratio,
                                            training, silu_u, concat_u, concat_x, mul_u_activation_type, group_norm,
                                            num_heads, linear_dim, seed, recompute_y_in_backward, rng_row_indices,
-                                           fp8_output_scale, fp8_backward, dropout_mask16)
+                                           fp8_output_scale, fp8_backward, dropout_mask16, residual_link)
 
 
 def hstu_compute_output(

@@ -57,7 +57,7 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias,
                 max_seq_len, seq_offsets, attn_alpha, num_targets, max_attn_len, contextual_seq_len,
-                fp8_input_scale, fp8_qkv_scale, defer_silu, attn_bias, fp8_backward=None):
+                fp8_input_scale, fp8_qkv_scale, defer_silu, attn_bias, fp8_backward=None, residual_link=None):
         T, E = x.shape
         H, Dq, Dv = num_heads, attn_dim, hidden_dim
         nu = H * Dv
@@ -112,6 +112,7 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
                    defer_silu, num_targets is not None, attn_bias is not None, u_pre is not None)
         ctx.x8_scale = sa if keep_x8 else None
         ctx.fp8_backward = fp8_backward
+        ctx.residual_link = residual_link
         u = u.contiguous() if u.stride(1) != 1 else u
         setattr(u, DUVQK_WIDTH_ATTR, uvqk_weight.shape[1])
         return u, attn.view(T, H * Dv)
@@ -168,9 +169,13 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
             d_w, d_b = token_wgrad(xn, duvqk, with_colsum=True)
             dxn = _fp8.proj_mm(duvqk, W)
         d_w, d_b = d_w.to(W.dtype), d_b.to(W.dtype)
-        dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False)
+        # the output block's residual gradient of x, when the layer linked it,
+        # is added inside the LayerNorm backward
+        dres = None if ctx.residual_link is None else ctx.residual_link.take()
+        dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False,
+                                     dres=dres)
         return (dx, dnw.to(nw.dtype), dnb.to(nb.dtype), None, None, None, None, d_w, d_b, None, None, None, None,
-                None, None, None, None, None, None if dbias is None else dbias.to(attn_bias.dtype), None)
+                None, None, None, None, None, None if dbias is None else dbias.to(attn_bias.dtype), None, None)
 
 
 def triton_hstu_preprocess_and_attention(
@@ -201,12 +206,15 @@ def triton_hstu_preprocess_and_attention(
     *,
     attn_bias: Optional[torch.Tensor] = None,
     fp8_backward: Optional[bwd_fp8.Fp8BackwardConfig] = None,
+    residual_link=None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """(u, attn [T, H*hidden_dim]); signature of
     ``triton_hstu_preprocess_and_attention`` (:3328-3393).  ``attn_bias`` is
     this build's relative-position bias extension (default off);
     ``fp8_backward`` the FP8 backward arm's settings (default: the process
-    default, ``bwd_fp8.default_config()``).  ``fp8_input_scale`` /
+    default, ``bwd_fp8.default_config()``); ``residual_link``
+    (``hstu_linear.ResidualLink``): the same layer's output block hands its
+    residual gradient of x over it.  ``fp8_input_scale`` /
     ``fp8_qkv_scale``: one-element device scales, or the reference's
     [2 + steps] scale state buffers, calibrated by the bf16 calls until frozen."""
     if return_residual_proxy:
@@ -216,7 +224,7 @@ def triton_hstu_preprocess_and_attention(
     return _HSTUPreprocessAndAttentionFunction.apply(
         x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias, max_seq_len,
         seq_offsets, attn_alpha, num_targets, max_attn_len, contextual_seq_len, fp8_input_scale, fp8_qkv_scale,
-        defer_silu, attn_bias, fp8_backward)
+        defer_silu, attn_bias, fp8_backward, residual_link)
 
 
 def hstu_compute_uqvk(x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias,
@@ -292,19 +300,22 @@ def hstu_layer(
     host.  ``fp8_backward`` sets the FP8 backward arm (default: the process
     default); ``dropout_mask16`` the dropout mask scheme (default: the
     process default, ``hstu_linear.set_mask16``)."""
-    from .hstu_linear import triton_hstu_compute_output
+    from .hstu_linear import ResidualLink, triton_hstu_compute_output
 
+    # x's residual gradient joins its LayerNorm backward's dx in one kernel
+    link = ResidualLink()
     alpha = attn_alpha if attn_alpha is not None else 1.0 / attn_dim ** 0.5
     u, attn = triton_hstu_preprocess_and_attention(
         x, params["input_norm_weight"], params["input_norm_bias"], norm_eps, num_heads, attn_dim, hidden_dim,
         params["uvqk_weight"], params["uvqk_bias"], max_seq_len, seq_offsets, alpha, None,
         recompute_uvqk_in_backward=True, recompute_normed_x_in_backward=True,
         fp8_input_scale=fp8_input_scale, fp8_qkv_scale=fp8_qkv_scale, defer_silu=True, attn_bias=attn_bias,
-        fp8_backward=fp8_backward)
+        fp8_backward=fp8_backward, residual_link=link)
     return triton_hstu_compute_output(
         attn, u, x, params["output_norm_weight"], params["output_norm_bias"], params["output_weight"], norm_eps,
         dropout_ratio, training, True, True, True, "silu", seed=seed, recompute_y_in_backward=True,
-        fp8_output_scale=fp8_output_scale, fp8_backward=fp8_backward, dropout_mask16=dropout_mask16)
+        fp8_output_scale=fp8_output_scale, fp8_backward=fp8_backward, dropout_mask16=dropout_mask16,
+        residual_link=link)
 
 
 __all__ = ["triton_hstu_preprocess_and_attention", "hstu_preprocess_and_attention", "hstu_compute_uqvk",

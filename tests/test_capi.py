@@ -138,7 +138,7 @@ def test_ln_mul_entry_points_reject_before_launch():
     def g(**kw):
         a = dict(dy=X, lddy=1536, x=X, ldx=512, u=X, ldu=512, w=W, b=W, mean=W, rstd=W, rows=64, D=512, act=1,
                  silu_u=1, cu=1, cx=1, ratio=0.0, mask=None, ldm=0, dx=X, lddx=512, du=X, lddu=512, y=None, ldy=0,
-                 dw=W, db=W, ws=W, wsb=ws(64, 512), stream=None)
+                 dres=None, lddres=0, dw=W, db=W, ws=W, wsb=ws(64, 512), stream=None)
         a.update(kw)
         return bwd(*a.values())
 
@@ -147,6 +147,8 @@ def test_ln_mul_entry_points_reject_before_launch():
     assert g(lddy=1024) == lib.HSTU_E_BAD_ARG
     assert g(y=X, ldy=512) == lib.HSTU_E_BAD_ARG
     assert g(D=128, ldx=128, ldu=128, lddx=128, lddu=128, lddy=384) == lib.HSTU_E_UNSUPPORTED
+    assert g(dres=X, lddres=512) == lib.HSTU_E_BAD_ARG  # a residual gradient only without an x block
+    assert g(cx=0, lddy=1024, dres=X, lddres=256) == lib.HSTU_E_BAD_ARG
 
 
 def test_delta_entry_points_reject_before_launch():

@@ -247,3 +247,27 @@ def test_hstu_compute_output_dispatch(hip_lib):
     a = ops.hstu_compute_output(attn, u, x, nw, nb, kernel=ops.HammerKernel.TRITON, **kw)
     b = ops.hstu_compute_output(attn, u, x, nw, nb, kernel=ops.HammerKernel.PYTORCH, **kw)
     torch.testing.assert_close(a.float(), b.float(), rtol=1e-2, atol=2e-2)
+
+
+def test_ln_bwd_residual_gradient(hip_lib):
+    """A residual branch's gradient of x folded into the plain LayerNorm's
+    backward (``dres``, as the layer passes the output block's): dx =
+    the LN backward + dres with one rounding, against float64 at the bf16 bar;
+    dweight / dbias unchanged bit for bit."""
+    N, D, eps = 1031, 512, 1e-6
+    x, _, w, b = _inputs(N, D, seed=8)
+    g = torch.Generator().manual_seed(9)
+    dxn = torch.randn(N, D, generator=g).to(torch.bfloat16)
+    dres = (4.0 * torch.randn(N, D, generator=g)).to(torch.bfloat16)
+    xd, wd, bd = (t.to(DEV) for t in (x, w, b))
+    _, mean, rstd, _ = L_mod._ln_fwd(xd, None, wd, bd, eps, 0.0, False, False, False, False, "none", 0, False, 1.0)
+    args = (dxn.to(DEV), xd, None, wd, bd, mean, rstd, 0.0, None, False, False, False, "none", False)
+    dx0, _, dw0, db0, _ = L_mod._ln_bwd(*args)
+    dx, _, dw, db, _ = L_mod._ln_bwd(*args, dres=dres.to(DEV))
+    rdx, _, _, _ = L.ln_mul_dropout_bwd(dxn.double(), x.double(), None, w.double(), b.double(), eps)
+    _bf16_close(dx, rdx + dres.double(), "dx with the residual gradient")
+    assert torch.equal(dw, dw0) and torch.equal(db, db0)
+    # dx rounds the fp32 sum once, dx0 was rounded before the sum: each within
+    # half a bf16 step (2^-8 relative) of its exact value
+    d = (dx.float() - (dx0.float() + dres.to(DEV).float())).abs()
+    assert float((d <= 2.0 ** -7 * (dx.float().abs() + dx0.float().abs()) + 1e-6).float().mean()) == 1.0
