@@ -89,6 +89,9 @@ def parse():
 
 
 PV_SCALE = 10.04  # the reference's DLRM_HSTU_FP8_FWD_PV_SCALE default
+# the full-FP8 backward's e4m3 P / dS pre-scales 2^(ceil(log2 N) + K): the
+# reference's SSC_K default and the production gin's DSC_K (yambda_5b.gin:3799)
+PROD_SSC_K, PROD_DSC_K = 3, -5
 
 
 def lengths_cfg3():
@@ -181,9 +184,12 @@ class Workload:
                                self.dout8.data_ptr(), self.e8.data_ptr(), stream)
             ws8 = lib.fn("hstu_attn_bwd_fp8_workspace_bytes")(T, B, H, D, N, R)
             self.ws = torch.empty(max(ws8, 1), dtype=torch.uint8, device=dev)
+            # the production pre-scales of e4m3 P and dS (SSC_K = 3, DSC_K = -5)
+            from hstu_amd.hstu_do_fp8 import full_fp8_prescale_log2
+            e_p, e_ds = full_fp8_prescale_log2(N, ssc_k=PROD_SSC_K, dsc_k=PROD_DSC_K)
             self.bwd_args = (self.dout8.data_ptr(), self.e8.data_ptr(), H * D, self.q.data_ptr(), self.k.data_ptr(),
                              self.v.data_ptr(), H * D, H * D, H * D, sp(self.sq), sp(self.sk), sp(self.sv), srs,
-                             shs, self.offs.data_ptr(), B, H, D, N, self.alpha, sp(self.bias), R,
+                             shs, self.offs.data_ptr(), B, H, D, N, self.alpha, e_p, e_ds, sp(self.bias), R,
                              self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), H * D, H * D, H * D,
                              sp(self.dbias), self.ws.data_ptr(), ws8, T, stream)
             self.f_quant = lib.fn("hstu_quantize_do_e4m3_blk")
@@ -482,7 +488,8 @@ def layer_bench(torch, lengths, N, steps, warmup, flush, bf16_dgrad=False):
 
     fp8_dgrad = not bf16_dgrad
     cfg = bwd_fp8.Fp8BackwardConfig(enabled=fp8_dgrad, uvqk=fp8_dgrad, uvqk_wgrad_fp8t=fp8_dgrad,
-                                    out_wgrad_fp8=fp8_dgrad, outproj_lnmd_fused=fp8_dgrad, attn_full_fp8=True)
+                                    out_wgrad_fp8=fp8_dgrad, outproj_lnmd_fused=fp8_dgrad, attn_full_fp8=True,
+                                    attn_ssc_k=PROD_SSC_K, attn_dsc_k=PROD_DSC_K)
     bwd_fp8.reset_sites()
     if fp8_dgrad:
         warmup = max(warmup, 5)

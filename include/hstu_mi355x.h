@@ -89,6 +89,8 @@ int64_t hstu_attn_fwd_workspace_bytes(int dtype, int64_t total_tokens, int B, in
  * among the keys of k's group (64-key tiles from the sequence start, split by
  * bit 4 of the key's index in the tile).  pv_scale in (0, 448); the
  * reference's default is 10.04.  Workspace as hstu_attn_fwd (e4m3 dtype).
+ * max_seq_len above hstu_attn_fwd_fp8_pv_max_seq_len() (a per-key table in
+ * LDS outgrows the CU's 160 KiB) returns HSTU_E_UNSUPPORTED before any launch.
  * Replaces: the FlyDSL e4m3 forward with pv="k128" (DLRM_HSTU_FP8_FWD_PV=1),
  * ops/flydsl/hstu_flydsl_mha.py:2199-2330, ops/flydsl/hstu_fwd.py:253-283.
  */
@@ -103,6 +105,12 @@ int hstu_attn_fwd_fp8_pv(const void* q, const void* k, const void* v,
                          void* out, int64_t out_row_stride,
                          void* workspace, int64_t workspace_bytes, int64_t total_tokens,
                          hipStream_t stream);
+/*
+ * The largest max_seq_len hstu_attn_fwd_fp8_pv serves (a multiple of 64).
+ * Replaces: the reference's shape gate that declines a call with a reason
+ * before any launch, ops/flydsl/hstu_flydsl_mha.py:311-354.
+ */
+int hstu_attn_fwd_fp8_pv_max_seq_len(void);
 
 /*
  * hstu_attn_fwd without a workspace, for callers that cannot allocate device
@@ -134,7 +142,12 @@ int hstu_attn_fwd_noalloc(int dtype,
  * strided views) completely -- no accumulation into existing contents, so no
  * zero-fill is needed -- and, if dbias != NULL, overwrites dbias (fp32
  * [H, 2R-1]) with the bias gradient.  Gradients are with respect to the
- * dequantized q, k, v.  Deterministic: no atomics on dq/dk/dv.
+ * dequantized q, k, v.  Deterministic, bias gradient included: no atomics;
+ * each 128-query dQ block writes its own row of bias-gradient sums and the
+ * rows are summed in a fixed order.  With a bias, the dQ kernels keep one
+ * histogram per wave in LDS: 16 R bytes (causal mask) or 16 (2R - 1) bytes
+ * (other masks) beyond their tiles; a bias_R past the CU's 160 KiB returns
+ * HSTU_E_UNSUPPORTED before any launch.
  * Replaces: triton_hstu_attention_bwd, ops/triton/triton_hstu_attention.py:3298-3410
  *           (mutates_args dq/dk/dv), and the FlyDSL backward launch
  *           fn(q, k, v, dout, dk, dv, dq_slot, cu, batch, n_blocks, 1/N, qkv_scale)
@@ -158,9 +171,10 @@ int hstu_attn_bwd(int dtype,
 
 /*
  * Device workspace the backward needs (bytes): the block schedule; with a
- * bias (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows and 64
- * partial copies of the bias gradient; for e4m3 inputs an exact bf16 copy of
- * q; the dS tiles (8 KiB per 128-key x 32-query tile, bounded by
+ * bias (bias_R > 0; 0 = no bias) a pre-clamped copy of the bias rows, one
+ * bias-gradient row of 2R - 1 floats per dQ block (ceil(T/128) + B per head)
+ * and 64 chunk sums of them; the per-sequence dQ block prefix; for e4m3
+ * inputs an exact bf16 copy of q; the dS tiles (8 KiB per 128-key x 32-query tile, bounded by
  * 2 (ceil(N/128) + 1) (ceil(T/128) + B) H tiles).  total_tokens = T = seq_offsets[B].  Returns -1 for bad sizes.  The
  * caller allocates it (the reference's FlyDSL backward likewise takes its
  * dq-split workspace from the caller, ops/flydsl/hstu_flydsl_mha.py:1674-1741).
@@ -177,15 +191,23 @@ int64_t hstu_attn_bwd_workspace_bytes(int dtype, int64_t total_tokens, int B, in
  * -- dout8 e4m3 [T, H, D] (row stride dout_row_stride bytes, 16-byte aligned
  * rows) and dout_e8 uint8 [T, H] = 127 - e with dO = dout8 * 2^-e per
  * (sequence, head, 32-token group) (hstu_quantize_do_e4m3_blk).  All five
- * products run on the e4m3 MFMA: P and dS are cast to e4m3 with the
- * reference's N-relative power-of-two pre-scales (silu / N * 2^(c+3), dS *
- * 2^(c-3), c = ceil(log2 N)), and the dO group scales are applied by the
- * MFMA's E8M0 block-scale operands.  dS passes from the dK/dV kernel to the
+ * products run on the e4m3 MFMA: P and dS are cast to e4m3 with
+ * power-of-two pre-scales, e4m3(silu / N * 2^p8_scale_log2) and
+ * e4m3(dS * 2^ds8_scale_log2), and the dO group scales are applied by the
+ * MFMA's E8M0 block-scale operands.  The reference's pre-scales are
+ * N-relative: p8_scale_log2 = ceil(log2 N) + K_SSC (K_SSC = 3,
+ * DLRM_HSTU_FP8_BWD_FULL_SSC_K) and ds8_scale_log2 = ceil(log2 N) + K_DSC
+ * (K_DSC = -3 by default, DLRM_HSTU_FP8_BWD_FULL_DSC_K; -5 in the
+ * production gin), or an absolute *_LOG2; both within [-64, 64] and
+ * p8_scale_log2 <= ceil(log2 N) + 9 (the SiLU's upper-only clamp), else
+ * HSTU_E_BAD_ARG.  dS passes from the dK/dV kernel to the
  * dQ kernel as e4m3 tiles in the workspace.  Writes dq, dk, dv (bf16) and,
- * if dbias != NULL, the bias gradient (computed from the e4m3 dS).
+ * if dbias != NULL, the bias gradient (computed from the e4m3 dS); every
+ * output is bitwise deterministic (the bias gradient as hstu_attn_bwd's).
  * Replaces: flydsl_hstu_attention_bwd under DLRM_HSTU_FP8_BWD_FULL
  *           (ops/flydsl/hstu_flydsl_mha.py:1330-1394 dO contract, :1351-1370
- *           pre-scales, :1674-1741 dq split; ops/flydsl/hstu_bwd_dkdv.py:356-403).
+ *           pre-scales, :1674-1741 dq split; ops/flydsl/hstu_bwd_dkdv.py:356-403;
+ *           dlrm_v4/train/gin/yambda_5b.gin:3764-3799 for K_DSC = -5).
  */
 int64_t hstu_attn_bwd_fp8_workspace_bytes(int64_t total_tokens, int B, int H, int D, int max_seq_len,
                                           int bias_R);
@@ -195,7 +217,8 @@ int hstu_attn_bwd_fp8(const void* dout8, const void* dout_e8, int64_t dout_row_s
                       const float* q_scale, const float* k_scale, const float* v_scale,
                       int64_t scale_row_stride, int64_t scale_head_stride,
                       const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
-                      float alpha, const float* attn_bias, int bias_R,
+                      float alpha, int p8_scale_log2, int ds8_scale_log2,
+                      const float* attn_bias, int bias_R,
                       void* dq, void* dk, void* dv,
                       int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
                       float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
@@ -211,7 +234,8 @@ int hstu_attn_bwd_fp8_dkdv(const void* dout8, const void* dout_e8, int64_t dout_
                            const float* q_scale, const float* k_scale, const float* v_scale,
                            int64_t scale_row_stride, int64_t scale_head_stride,
                            const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
-                           float alpha, const float* attn_bias, int bias_R,
+                           float alpha, int p8_scale_log2, int ds8_scale_log2,
+                           const float* attn_bias, int bias_R,
                            void* dq, void* dk, void* dv,
                            int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
                            float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
@@ -222,7 +246,8 @@ int hstu_attn_bwd_fp8_dq(const void* dout8, const void* dout_e8, int64_t dout_ro
                          const float* q_scale, const float* k_scale, const float* v_scale,
                          int64_t scale_row_stride, int64_t scale_head_stride,
                          const int64_t* seq_offsets, int B, int H, int D, int max_seq_len,
-                         float alpha, const float* attn_bias, int bias_R,
+                         float alpha, int p8_scale_log2, int ds8_scale_log2,
+                         const float* attn_bias, int bias_R,
                          void* dq, void* dk, void* dv,
                          int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
                          float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,

@@ -193,7 +193,10 @@ struct ScaleTile {
 
 
 // ---------------------------------------------------------------- params
-constexpr int kDbiasCopies = 64;
+// Bias gradient: every dQ block (sequence, head, 128-query block) writes its
+// own row of partial sums to the workspace; kDbiasChunks fixed-order partial
+// sums of the rows, then their fixed-order sum, give dbias (no atomics).
+constexpr int kDbiasChunks = 64;
 
 // Length of one head's row of the pre-clamped bias table (build_bias_ext):
 // entry off + N + 127 holds the bias of relative offset off, for every off a
@@ -225,7 +228,9 @@ struct AttnParams {
   float* dbias;       // bias gradient, same shape (backward)
   const float* bias_ext;  // workspace: pre-clamped, pre-scaled bias rows [H, 2N+192]
   const uint8_t* q16;     // workspace: bf16 copy of e4m3 q, [T, H, D]
-  float* dbias_part;      // workspace: kDbiasCopies partial bias gradients [copies, H, 2R-1]
+  float* dbias_part;      // workspace: one bias-gradient row per dQ block [blocks, H, dbias_w]
+  const int64_t* dq_base;  // workspace: per-sequence exclusive prefix of 128-query blocks [B + 1]
+  int dbias_w;            // floats per row: offsets 0 .. R-1 (causal), -(R-1) .. R-1 (generic masks)
   const int* sched_items;  // block schedule (build_schedule): [8][sched_cap] (sequence*H + head)
   const int* sched_start;  // [8][sched_cap + 1] first block position of each item on its XCD
   const int* sched_count;  // [8] items per XCD
@@ -243,6 +248,42 @@ struct AttnParams {
   float pv_c;               // 2^-3 f32(2^3 / s): the sigmoid denominator factor of P' s
   float pv_out;             // f32(1 / s): undoes the P scale on the output
 };
+
+// ---------------------------------------------------------------- bias gradient rows
+// A dQ block keeps one LDS histogram of dbias_w floats per wave.  A wave adds
+// into its own histogram only, in program order, and the 64 lanes of one
+// add hit distinct offsets, so every sum has one fixed order.  At the end
+// the block adds its waves' histograms in wave order and stores the row of
+// its slot (dq_base[b] + block) * H + h.
+
+// The 64 lanes' sum, as lane 0 holds it after a fixed butterfly.
+__device__ __forceinline__ float wave_sum_fixed(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// Adds a wave's per-lane clamped-offset sums into its histogram entry `at`
+// (lane 0 after the fixed-order lane sum); call with the whole wave.
+__device__ __forceinline__ void hist_add_clamped(float* hist_w, int at, float v, int lane) {
+  const float s = wave_sum_fixed(v);
+  if (lane == 0) hist_w[at] += s;
+}
+
+// Waits for every wave, then writes this block's row: the sum of the NW
+// wave histograms (hist, NW x W floats) in wave order.
+template <int NW>
+__device__ __forceinline__ void dbias_store_row(const AttnParams& p, const float* hist, int b, int blk, int h) {
+  __syncthreads();
+  const int W = p.dbias_w;
+  float* dst = p.dbias_part + ((p.dq_base[b] + blk) * p.H + h) * (int64_t)W;
+  for (int i = threadIdx.x; i < W; i += NW * 64) {
+    float v = hist[i];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += hist[w * W + i];
+    dst[i] = v;
+  }
+}
 
 struct SeqCtx {
   int64_t start;
@@ -1137,8 +1178,8 @@ struct DqCfg {
   static constexpr int SC_OFF = V_OFF + BN * P;  // (sk, sv) per key
   static constexpr int BIAS_OFF = SC_OFF + BN * 8;
   static constexpr int BUF = BIAS_OFF + (BM + BN) * 4;
-  static constexpr int HIST_OFF = 2 * BUF;  // bias-gradient histogram, R floats
-  static int lds(bool bias, int R) { return HIST_OFF + (bias ? R * 4 : 0); }
+  static constexpr int HIST_OFF = 2 * BUF;  // bias-gradient histograms, 2R - 1 floats per wave
+  static int lds(bool bias, int R) { return HIST_OFF + (bias ? 4 * (2 * R - 1) * 4 : 0); }
 };
 
 // ---------------------------------------------------------------------------
@@ -1248,13 +1289,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
   const BufRsrc sv_rsrc = make_rsrc(FP8 ? p.v_scale + sc.start * p.s_rs + h * p.s_hs : nullptr, sbytes);
   const float* biasb = BIAS ? p.bias + (int64_t)h * (2 * p.bias_R - 1) : nullptr;
   const int R1 = p.bias_R - 1;
-  float* hist = (float*)(smem + C::HIST_OFF);
-  // This block's partial bias gradient: one of kDbiasCopies copies, so that
-  // the flushing atomics of different blocks rarely meet on one address.
-  float* dbias_copy = BIAS ? p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1)
-                           : nullptr;
+  // the wave's bias-gradient histogram: offset o at entry o + R - 1, o = -(R-1) .. R-1
+  float* hist0 = (float*)(smem + C::HIST_OFF);
+  float* hist = hist0 + wave * (2 * p.bias_R - 1);
   if constexpr (BIAS) {
-    for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
+    for (int i = tid; i < 4 * (2 * p.bias_R - 1); i += kThreads) hist0[i] = 0.f;
   }
 
   // Q and dO fragments (B operands): lane holds query mw0+16qt+li.
@@ -1317,7 +1356,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
   const int v_rd = C::V_OFF + li * C::P + 16 * g;
   const int kt_rd = C::K_OFF + (4 * g + (li >> 2)) * C::P + (li & 3) * 8;  // tr16
   const int bias_rd = 32 * wave + (C::BN - 1) + li - 4 * g;
-  float dclamp = 0.f;  // bias gradient of elements in the clamped region
+  float dclamp = 0.f, dclampn = 0.f;  // bias gradient of elements in the clamped regions (+, -)
 
   load(0);
   store(smem);
@@ -1403,8 +1442,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
             const float dv = diag_reduce(dacc, lane);
             const int off = (mw0 - n0 - 32 * c) + li + 16 - 16 * g;
             if (off >= R1) dclamp += dv;
-            else if (off >= 0) atomicAdd(&hist[off], dv);
-            else if (GENERIC && dv != 0.f) atomicAdd(&dbias_copy[max(off, -R1) + R1], dv);
+            else if (off > -R1) atomicAdd(&hist[off + R1], dv);
+            else dclampn += dv;
           }
         };
         if (need_mask) {
@@ -1430,13 +1469,9 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_kernel(AttnParams p) 
   }
 
   if constexpr (BIAS) {
-    if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
-    __syncthreads();
-    float* dst = dbias_copy + R1;
-    for (int i = tid; i < p.bias_R; i += kThreads) {
-      const float v = hist[i];
-      if (v != 0.f) atomicAdd(&dst[i], v);
-    }
+    hist_add_clamped(hist, 2 * R1, dclamp, lane);
+    hist_add_clamped(hist, 0, dclampn, lane);
+    dbias_store_row<4>(p, hist0, sc.b, sc.blk, h);
   }
 
   if (!wave_active) return;
@@ -1473,8 +1508,8 @@ struct DqWsCfg {
   static constexpr int K_OFF = 0;
   static constexpr int DS_OFF = K_OFF + BNK * P;
   static constexpr int DS_WAVE = BNK * PS;
-  static constexpr int HIST_OFF = DS_OFF + 4 * DS_WAVE;
-  static int lds(bool bias, int R) { return HIST_OFF + (bias ? R * 4 : 0); }
+  static constexpr int HIST_OFF = DS_OFF + 4 * DS_WAVE;  // bias-gradient histograms, R floats per wave
+  static int lds(bool bias, int R) { return HIST_OFF + (bias ? 4 * R * 4 : 0); }
 };
 
 template <int D, bool FP8, bool BIAS>
@@ -1502,11 +1537,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_ws_kernel(AttnParams 
   const BufRsrc krsrc = make_rsrc(p.k + (sc.start * p.k_rs + (int64_t)h * D) * ES,
                                   (uint32_t)(L > 0 ? (L - 1) * krs + D * ES : 0));
   const int R1 = p.bias_R - 1;
-  float* hist = (float*)(smem + C::HIST_OFF);
-  float* dbias_copy = BIAS ? p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1)
-                           : nullptr;
+  // the wave's bias-gradient histogram, offsets 0 .. R - 1
+  float* hist0 = (float*)(smem + C::HIST_OFF);
+  float* hist = hist0 + wave * p.bias_R;
   if constexpr (BIAS) {
-    for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
+    for (int i = tid; i < 4 * p.bias_R; i += kThreads) hist0[i] = 0.f;
   }
   // 1 / q_scale of the lane's queries: for the dQ store (query qs*16 + li) and
   // for the bias gradient (queries qs*16 + 4g + r of the dS fragments)
@@ -1696,13 +1731,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dq_ws_kernel(AttnParams 
       const float g1 = skew_undo(cr_m3), g2 = skew_undo(cr_m2);
       bias_flush(0.f, bwrap ? 0.f : g1, bwrap ? g1 : g2, bwrap ? g2 : cr_g, base_last - 64);
     }
-    if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
-    __syncthreads();
-    float* dst = dbias_copy + R1;
-    for (int i = tid; i < p.bias_R; i += kThreads) {
-      const float v = hist[i];
-      if (v != 0.f) atomicAdd(&dst[i], v);
-    }
+    hist_add_clamped(hist, R1, dclamp, lane);
+    dbias_store_row<4>(p, hist0, sc.b, sc.blk, h);
   }
 
   if (!wave_active) return;
@@ -2122,7 +2152,7 @@ struct F8Bwd {
   static constexpr int QK_OFF = 0;
   static constexpr int QDS_OFF = QK_OFF + BN * 128;
   static constexpr int QHIST_OFF = QDS_OFF + BN * 128;
-  static int dq_lds(bool bias, int R) { return QHIST_OFF + (bias ? R * 4 : 0); }
+  static int dq_lds(bool bias, int R) { return QHIST_OFF + (bias ? 4 * R * 4 : 0); }  // a histogram per wave
 };
 
 // Stored dS tiles: for key block kb and query tile qt >= kb of a sequence
@@ -2411,9 +2441,11 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   const float nk = f8_norm(p.f8max[1]);
   const float unscale = 1.0f / (nk * p.ds8_scale);
   const int R1 = p.bias_R - 1;
-  float* hist = (float*)(smem + C::QHIST_OFF);
+  // the wave's bias-gradient histogram, offsets 0 .. R - 1
+  float* hist0 = (float*)(smem + C::QHIST_OFF);
+  float* hist = hist0 + wave * p.bias_R;
   if constexpr (BIAS) {
-    for (int i = tid; i < p.bias_R; i += kThreads) hist[i] = 0.f;
+    for (int i = tid; i < 4 * p.bias_R; i += kThreads) hist0[i] = 0.f;
   }
   // bias gradient: 2^(E8 - 127) of the dO group of this lane's query rows in half hf
   float grp[2] = {1.f, 1.f};
@@ -2602,13 +2634,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
       const float g7 = skew_undo(cr_m1), g8 = skew_undo(cr_0);
       flush(0.f, wrap ? 0.f : g7, wrap ? g7 : g8, wrap ? g8 : cr_g1, base_v + 96);
     }
-    if (dclamp != 0.f) atomicAdd(&hist[R1], dclamp);
-    __syncthreads();
-    float* dst = p.dbias_part + ((int64_t)(blockIdx.x % kDbiasCopies) * p.H + h) * (2 * p.bias_R - 1) + R1;
-    for (int i = tid; i < p.bias_R; i += kThreads) {
-      const float v = hist[i];
-      if (v != 0.f) atomicAdd(&dst[i], v);
-    }
+    hist_add_clamped(hist, R1, dclamp, lane);
+    dbias_store_row<4>(p, hist0, sc.b, qt, h);
   }
   // dQ_i = alpha 2^-e(i) / (nk ds8_scale) . acc
   const float fin = p.alpha * unscale;
@@ -2627,17 +2654,14 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   }
 }
 
-// base[b] = sum over sequences b' < b of f8_tiles(min(length, N)); base[B] =
-// the total; and the two scale maxima (f8max) reset for f8_scale_max.
-__global__ void __launch_bounds__(1024) f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base,
-                                                       unsigned* f8max) {
-  __shared__ int64_t part[1024];
+// out[b] = sum over sequences b' < b of count(b), out[B] = the total, by
+// one 1024-thread block; part: 1024 int64 of shared memory.
+template <class F>
+__device__ void seq_exclusive_scan(int B, F count, int64_t* part, int64_t* out) {
   const int tid = threadIdx.x, per = (B + 1023) / 1024, b0 = tid * per;
-  if (tid < 2) f8max[tid] = 0u;
-  auto tiles = [&](int b) { return f8_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); };
   int64_t sum = 0;
   for (int i = 0; i < per; ++i)
-    if (b0 + i < B) sum += tiles(b0 + i);
+    if (b0 + i < B) sum += count(b0 + i);
   part[tid] = sum;
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
@@ -2649,11 +2673,29 @@ __global__ void __launch_bounds__(1024) f8_tile_prefix(const int64_t* seq_offset
   int64_t run = tid ? part[tid - 1] : 0;
   for (int i = 0; i < per; ++i) {
     if (b0 + i < B) {
-      base[b0 + i] = run;
-      run += tiles(b0 + i);
+      out[b0 + i] = run;
+      run += count(b0 + i);
     }
   }
-  if (tid == 1023) base[B] = part[1023];
+  if (tid == 1023) out[B] = part[1023];
+  __syncthreads();
+}
+
+// 128-query dQ blocks of a sequence: ceil(min(length, N) / 128).
+__device__ __forceinline__ int64_t dq_blocks(const int64_t* seq_offsets, int b, int N) {
+  return (min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N) + 127) / 128;
+}
+
+// base[b] = sum over sequences b' < b of f8_tiles(min(length, N)); base[B] =
+// the total; dq_base the same prefix of 128-query blocks (the bias-gradient
+// rows); and the two scale maxima (f8max) reset for f8_scale_max.
+__global__ void __launch_bounds__(1024) f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base,
+                                                       int64_t* dq_base, unsigned* f8max) {
+  __shared__ int64_t part[1024];
+  if (threadIdx.x < 2) f8max[threadIdx.x] = 0u;
+  seq_exclusive_scan(B, [&](int b) { return f8_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); },
+                     part, base);
+  seq_exclusive_scan(B, [&](int b) { return dq_blocks(seq_offsets, b, N); }, part, dq_base);
 }
 
 // f8max[0] / [1] = float bits of the largest q / k scale over [T, H] (or the scalar).
@@ -2829,17 +2871,22 @@ int sched_grid(int B, int H, int N) { return 8 * sched_cap(B, H) * ((N + 127) / 
 
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 int64_t bias_ext_bytes(int H, int N) { return align256((int64_t)H * bias_ext_len(N) * 4); }
-int64_t dbias_part_bytes(int H, int R) { return align256((int64_t)kDbiasCopies * H * (2 * R - 1) * 4); }
+// Bias-gradient rows: one per dQ block and head, at most ceil(T/128) + B
+// blocks per head, of up to 2R - 1 floats; then the chunk sums.
+int64_t dbias_rows_bytes(int64_t T, int B, int H, int R) {
+  return align256(((T + 127) / 128 + B) * H * (int64_t)(2 * R - 1) * 4);
+}
+int64_t dbias_chunks_bytes(int H, int R) { return align256((int64_t)kDbiasChunks * H * (2 * R - 1) * 4); }
 int64_t sched_bytes(int B, int H) { return align256(sched_ints(B, H) * 4); }
 // Forward workspace: the block schedule.
 int64_t fwd_workspace_bytes(int B, int H) { return sched_bytes(B, H); }
 // Backward workspace: [block schedule][pre-clamped bias rows][bf16 copy of
-// e4m3 q][partial bias gradients][dS tile prefix][dS tiles]; byte offsets of
-// each part.  The dS tiles are sized by a bound that needs no lengths:
+// e4m3 q][bias-gradient rows][their chunk sums][dQ block prefix][dS tile
+// prefix][dS tiles]; byte offsets of each part.  The dS tiles are sized by a bound that needs no lengths:
 // ds_tiles(L) <= 2 nb (nb + 1) with nb = ceil(L / 128) <= ceil(N / 128), so
 // the sum over sequences is at most 2 (ceil(N/128) + 1) (ceil(T/128) + B).
 struct BwdWs {
-  int64_t sched, bias_ext, q16, part, ds_base, ds, total;
+  int64_t sched, bias_ext, q16, part, chunks, dq_base, ds_base, ds, total;
 };
 int64_t ds_tiles_bound(int64_t T, int B, int N) { return 2 * ((N + 127) / 128 + 1) * ((T + 127) / 128 + B); }
 BwdWs bwd_ws(int dtype, int64_t T, int B, int H, int D, int N, int R) {
@@ -2852,7 +2899,11 @@ BwdWs bwd_ws(int dtype, int64_t T, int B, int H, int D, int N, int R) {
   w.q16 = o;
   if (dtype == HSTU_DTYPE_FP8_E4M3) o += align256(T * H * D * 2);
   w.part = o;
-  if (R > 0) o += dbias_part_bytes(H, R);
+  if (R > 0) o += dbias_rows_bytes(T, B, H, R);
+  w.chunks = o;
+  if (R > 0) o += dbias_chunks_bytes(H, R);
+  w.dq_base = o;
+  o += align256(((int64_t)B + 1) * 8);
   w.ds_base = o;
   o += align256(((int64_t)B + 1) * 8);
   w.ds = o;
@@ -2862,44 +2913,55 @@ BwdWs bwd_ws(int dtype, int64_t T, int B, int H, int D, int N, int R) {
 }
 
 
-// base[b] = sum over sequences b' < b of ds_tiles(min(length, N)); base[B] = the total.
-__global__ void __launch_bounds__(1024) ds_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base) {
+// base[b] = sum over sequences b' < b of ds_tiles(min(length, N)); base[B] =
+// the total; dq_base (if not null) the same prefix of 128-query blocks.
+__global__ void __launch_bounds__(1024) ds_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base,
+                                                       int64_t* dq_base) {
   __shared__ int64_t part[1024];
-  const int tid = threadIdx.x, per = (B + 1023) / 1024, b0 = tid * per;
-  auto tiles = [&](int b) { return ds_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); };
-  int64_t sum = 0;
-  for (int i = 0; i < per; ++i)
-    if (b0 + i < B) sum += tiles(b0 + i);
-  part[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int64_t add = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += add;
-    __syncthreads();
-  }
-  int64_t run = tid ? part[tid - 1] : 0;
-  for (int i = 0; i < per; ++i) {
-    if (b0 + i < B) {
-      base[b0 + i] = run;
-      run += tiles(b0 + i);
-    }
-  }
-  if (tid == 1023) base[B] = part[1023];
+  seq_exclusive_scan(B, [&](int b) { return ds_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); },
+                     part, base);
+  if (dq_base != nullptr) seq_exclusive_scan(B, [&](int b) { return dq_blocks(seq_offsets, b, N); }, part, dq_base);
 }
 
-// dbias = inv_n * sum of the kDbiasCopies partial copies.
-__global__ void reduce_dbias(const float* part, int n, float inv_n, float* dbias) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+// dq_base alone (the recomputing dQ kernel's bias-gradient rows).
+__global__ void __launch_bounds__(1024) dq_block_prefix(const int64_t* seq_offsets, int B, int N, int64_t* dq_base) {
+  __shared__ int64_t part[1024];
+  seq_exclusive_scan(B, [&](int b) { return dq_blocks(seq_offsets, b, N); }, part, dq_base);
+}
+
+// Chunk c of head h's bias-gradient rows: the sum of rows c * per ..
+// min((c + 1) * per, n) - 1 in row order, n = dq_base[B] rows per head.
+__global__ void dbias_chunk_sum(const float* rows, const int64_t* dq_base, int B, int H, int W, float* chunks) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y, c = blockIdx.z;
+  if (i >= W) return;
+  const int64_t n = dq_base[B], per = (n + kDbiasChunks - 1) / kDbiasChunks;
+  const int64_t r0 = c * per, r1 = min(n, r0 + per);
   float s = 0.f;
-  for (int c = 0; c < kDbiasCopies; ++c) s += part[(int64_t)c * n + i];
-  dbias[i] = s * inv_n;
+  for (int64_t r = r0; r < r1; ++r) s += rows[(r * H + h) * W + i];
+  chunks[((int64_t)c * H + h) * W + i] = s;
 }
 
-__global__ void fill_f32(float* p, int n, float v) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
+// dbias [H, 2R - 1] = scale * the chunks summed in chunk order.  A row of W
+// floats holds the offsets R - W .. R - 1; dbias entries below are zero.
+__global__ void dbias_finish(const float* chunks, int H, int W, int R, float scale, float* dbias) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y, n = 2 * R - 1;
+  if (j >= n) return;
+  const int i = j - (n - W);
+  float s = 0.f;
+  if (i >= 0)
+    for (int c = 0; c < kDbiasChunks; ++c) s += chunks[((int64_t)c * H + h) * W + i];
+  dbias[(int64_t)h * n + j] = s * scale;
+}
+
+// The bias gradient from the dQ blocks' rows (p.dbias_part, p.dq_base,
+// p.dbias_w): chunk sums, then dbias, both in a fixed order.
+hipError_t dbias_reduce(const AttnParams& p, float* chunks, float scale, float* dbias, hipStream_t stream) {
+  const int W = p.dbias_w;
+  hipLaunchKernelGGL(dbias_chunk_sum, dim3((W + 255) / 256, p.H, kDbiasChunks), dim3(256), 0, stream,
+                     p.dbias_part, p.dq_base, p.B, p.H, W, chunks);
+  hipLaunchKernelGGL(dbias_finish, dim3((2 * p.bias_R - 1 + 255) / 256, p.H), dim3(256), 0, stream, chunks, p.H, W,
+                     p.bias_R, scale, dbias);
+  return hipGetLastError();
 }
 
 // Rows of a sequence beyond max_seq_len are not computed by the kernels (the
@@ -2920,6 +2982,8 @@ __global__ void zero_rows_beyond_n(const int64_t* seq_offsets, int N, int width,
 }
 
 // ---------------------------------------------------------------- launch
+constexpr int kMaxLdsBytes = 160 * 1024;  // LDS of one gfx950 CU
+
 // Raise each kernel's dynamic-LDS limit to the CU's 160 KiB once; the actual
 // allocation is the launch's size (the forward uses ~72 KiB, so two
 // workgroups share a CU).
@@ -2929,14 +2993,14 @@ hipError_t ensure_lds(const void* fn) {
   std::lock_guard<std::mutex> lock(mu);
   for (const void* d : done)
     if (d == fn) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes);
   if (e == hipSuccess) done.push_back(fn);
   return e;
 }
 
 hipError_t launch(void (*kernel)(AttnParams), int lds, int grid, AttnParams p, hipStream_t stream,
                   int threads = kThreads) {
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
   hipError_t e = ensure_lds((const void*)kernel);
   if (e != hipSuccess) return e;
   void* args[] = {&p};
@@ -3064,6 +3128,12 @@ extern "C" int hstu_attn_fwd(int dtype, const void* q, const void* k, const void
                     stream);
 }
 
+extern "C" int hstu_attn_fwd_fp8_pv_max_seq_len(void) {
+  int n = 64;
+  while (Pv8Cfg::lds(n + 64) <= kMaxLdsBytes) n += 64;
+  return n;
+}
+
 extern "C" int hstu_attn_fwd_fp8_pv(const void* q, const void* k, const void* v, int64_t q_row_stride,
                                     int64_t k_row_stride, int64_t v_row_stride, const float* q_scale,
                                     const float* k_scale, const float* v_scale, int64_t scale_row_stride,
@@ -3078,6 +3148,9 @@ extern "C" int hstu_attn_fwd_fp8_pv(const void* q, const void* k, const void* v,
   if (!(pv_scale > 0.f) || !(pv_scale < 448.f)) return HSTU_E_BAD_ARG;
   // the causal mask only (the reference arms FP8 P.V on its causal config)
   if (num_targets != nullptr || max_attn_len > 0 || contextual_seq_len > 0) return HSTU_E_UNSUPPORTED;
+  // the block's per-key table grows with N: refused before any launch past
+  // the CU's 160 KiB of LDS
+  if (max_seq_len > hstu_attn_fwd_fp8_pv_max_seq_len()) return HSTU_E_UNSUPPORTED;
   if (B == 0) return 0;
   if (workspace == nullptr || workspace_bytes < fwd_workspace_bytes(B, H)) return HSTU_E_BAD_ARG;
   return fwd_launch(HSTU_DTYPE_FP8_E4M3, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale,
@@ -3206,8 +3279,13 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   hipError_t e;
   const BwdWs wl = bwd_ws(dtype, total_tokens, B, H, D, max_seq_len, has_bias ? bias_R : 0);
   if (total_tokens < 0 || workspace_bytes < wl.total || workspace == nullptr) return HSTU_E_BAD_ARG;
+  // the dQ kernels' per-wave bias-gradient histograms must fit the CU's LDS
+  if (has_bias && (parts & kBwdDq)) {
+    const int lds = generic ? (D == 128 ? DqCfg<128>::lds(true, bias_R) : DqCfg<64>::lds(true, bias_R))
+                            : (D == 128 ? DqWsCfg<128>::lds(true, bias_R) : DqWsCfg<64>::lds(true, bias_R));
+    if (lds > kMaxLdsBytes) return HSTU_E_UNSUPPORTED;
+  }
   uint8_t* ws = (uint8_t*)workspace;
-  uint8_t* ws_part = has_bias ? ws + wl.part : nullptr;
   e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)(ws + wl.sched), stream);
   if (e != hipSuccess) return (int)e;
   if (!generic) {
@@ -3215,7 +3293,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
     p.ds_base = (const int64_t*)(ws + wl.ds_base);
     p.ds_ws = ws + wl.ds;
     hipLaunchKernelGGL(ds_tile_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
-                       (int64_t*)(ws + wl.ds_base));
+                       (int64_t*)(ws + wl.ds_base), has_bias ? (int64_t*)(ws + wl.dq_base) : (int64_t*)nullptr);
   }
   if (parts & kBwdDkdv) {
     if (has_bias) {
@@ -3244,9 +3322,14 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
   }
   if (parts & kBwdDq) {
     if (has_bias) {
-      p.dbias_part = (float*)ws_part;
-      const int n = kDbiasCopies * H * (2 * bias_R - 1);
-      hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 0.f);
+      // one bias-gradient row per dQ block: offsets 0 .. R-1, or -(R-1) .. R-1
+      // for the masks that admit keys after the query
+      p.dbias_part = (float*)(ws + wl.part);
+      p.dq_base = (const int64_t*)(ws + wl.dq_base);
+      p.dbias_w = generic ? 2 * bias_R - 1 : bias_R;
+      if (generic)
+        hipLaunchKernelGGL(dq_block_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
+                           (int64_t*)(ws + wl.dq_base));
     }
     // dQ (+ bias gradient): 128-query blocks, longest key range first.  With
     // the causal mask, from the dS tiles the dK/dV kernel stored.
@@ -3273,9 +3356,8 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
     }
     if (e != hipSuccess) return (int)e;
     if (has_bias && dbias != nullptr) {
-      const int n = H * (2 * bias_R - 1);
-      hipLaunchKernelGGL(reduce_dbias, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, p.inv_n,
-                         dbias);
+      e = dbias_reduce(p, (float*)(ws + wl.chunks), p.inv_n, dbias, stream);
+      if (e != hipSuccess) return (int)e;
     }
   }
   hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
@@ -3327,7 +3409,7 @@ namespace {
 // bound that needs no lengths: sum_b nq_b (nq_b + 1) / 2 <= (nq_max + 1) / 2 *
 // (ceil(T / 128) + B), nq_max = ceil(N / 128).
 struct F8Ws {
-  int64_t sched, bias_ext, part, maxv, base, tiles, total;
+  int64_t sched, bias_ext, part, chunks, dq_base, maxv, base, tiles, total;
 };
 int64_t f8_tiles_bound(int64_t T, int B, int N) {
   const int64_t nq = (N + 127) / 128;
@@ -3341,7 +3423,11 @@ F8Ws f8_ws(int64_t T, int B, int H, int N, int R) {
   w.bias_ext = o;
   if (R > 0) o += bias_ext_bytes(H, N);
   w.part = o;
-  if (R > 0) o += dbias_part_bytes(H, R);
+  if (R > 0) o += dbias_rows_bytes(T, B, H, R);
+  w.chunks = o;
+  if (R > 0) o += dbias_chunks_bytes(H, R);
+  w.dq_base = o;
+  o += align256(((int64_t)B + 1) * 8);
   w.maxv = o;
   o += 256;
   w.base = o;
@@ -3369,7 +3455,8 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
                       const void* k, const void* v, int64_t q_row_stride, int64_t k_row_stride,
                       int64_t v_row_stride, const float* q_scale, const float* k_scale, const float* v_scale,
                       int64_t scale_row_stride, int64_t scale_head_stride, const int64_t* seq_offsets, int B,
-                      int H, int D, int max_seq_len, float alpha, const float* attn_bias, int bias_R, void* dq,
+                      int H, int D, int max_seq_len, float alpha, int p8_scale_log2, int ds8_scale_log2,
+                      const float* attn_bias, int bias_R, void* dq,
                       void* dk, void* dv, int64_t dq_row_stride, int64_t dk_row_stride, int64_t dv_row_stride,
                       float* dbias, void* workspace, int64_t workspace_bytes, int64_t total_tokens,
                       hipStream_t stream) {
@@ -3389,6 +3476,13 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
       ((parts & kBwdDkdv) && (!row_alignment_ok(HSTU_DTYPE_BF16, dk_row_stride, dk) ||
                               !row_alignment_ok(HSTU_DTYPE_BF16, dv_row_stride, dv))))
     return HSTU_E_UNSUPPORTED;
+  // silu * N >= -0.279 is clamped from above only, exact while the P
+  // pre-scale stays <= 2^(ceil(log2 N) + 9) (hstu_flydsl_mha.py:1371-1374)
+  if (p8_scale_log2 < -64 || p8_scale_log2 > 64 || ds8_scale_log2 < -64 || ds8_scale_log2 > 64 ||
+      p8_scale_log2 > ceil_log2(max_seq_len < 2 ? 2 : max_seq_len) + 9)
+    return HSTU_E_BAD_ARG;
+  // the dQ kernel's per-wave bias-gradient histograms must fit the CU's LDS
+  if (attn_bias != nullptr && F8Bwd::dq_lds(true, bias_R) > kMaxLdsBytes) return HSTU_E_UNSUPPORTED;
   if (B == 0) return 0;
   const bool has_bias = attn_bias != nullptr;
   const F8Ws wl = f8_ws(total_tokens, B, H, max_seq_len, has_bias ? bias_R : 0);
@@ -3424,11 +3518,10 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
   p.bias = attn_bias;
   p.bias_R = bias_R;
   p.dbias = dbias;
-  // N-relative pre-scales (hstu_flydsl_mha.py:1351-1370): silu / N * 2^(c+3) and
-  // dS * 2^(c-3) with c = ceil(log2 N)
-  const int c = ceil_log2(max_seq_len < 2 ? 2 : max_seq_len);
-  p.p8_scale = ldexpf(1.0f, c + 3);
-  p.ds8_scale = ldexpf(1.0f, c - 3);
+  // power-of-two pre-scales of the e4m3 P and dS (hstu_flydsl_mha.py:1351-1370:
+  // 2^(ceil(log2 N) + K), K = 3 and -3 by default, -5 for dS in production)
+  p.p8_scale = ldexpf(1.0f, p8_scale_log2);
+  p.ds8_scale = ldexpf(1.0f, ds8_scale_log2);
   p.f8max = (const unsigned*)(ws + wl.maxv);
   p.ds_base = (const int64_t*)(ws + wl.base);
   p.ds_ws = ws + wl.tiles;
@@ -3438,7 +3531,7 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
   if (parts & kBwdDkdv) {
     // tile prefix and scale maxima, read by both halves
     hipLaunchKernelGGL(f8_tile_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
-                       (int64_t*)(ws + wl.base), (unsigned*)(ws + wl.maxv));
+                       (int64_t*)(ws + wl.base), (int64_t*)(ws + wl.dq_base), (unsigned*)(ws + wl.maxv));
     const bool per_token = scale_row_stride || scale_head_stride;
     const int64_t ntok = per_token ? total_tokens : 1;
     const int sgrid = (int)std::min<int64_t>((ntok + 255) / 256, 256);
@@ -3456,15 +3549,15 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
   if (parts & kBwdDq) {
     if (has_bias) {
       p.dbias_part = (float*)(ws + wl.part);
-      const int n = kDbiasCopies * H * (2 * bias_R - 1);
-      hipLaunchKernelGGL(fill_f32, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 0.f);
+      p.dq_base = (const int64_t*)(ws + wl.dq_base);
+      p.dbias_w = bias_R;
     }
     e = has_bias ? launch(hstu_bwd_f8_dq_kernel<true>, F8Bwd::dq_lds(true, bias_R), grid, p, stream)
                  : launch(hstu_bwd_f8_dq_kernel<false>, F8Bwd::dq_lds(false, 0), grid, p, stream);
     if (e != hipSuccess) return (int)e;
     if (has_bias && dbias != nullptr) {
-      const int n = H * (2 * bias_R - 1);
-      hipLaunchKernelGGL(reduce_dbias, dim3((n + 255) / 256), dim3(256), 0, stream, p.dbias_part, n, 1.0f, dbias);
+      e = dbias_reduce(p, (float*)(ws + wl.chunks), 1.0f, dbias, stream);
+      if (e != hipSuccess) return (int)e;
     }
   }
   hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
@@ -3479,13 +3572,15 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
   const void *dout8, const void *dout_e8, int64_t dout_row_stride, const void *q, const void *k, const void *v,  \
       int64_t q_row_stride, int64_t k_row_stride, int64_t v_row_stride, const float *q_scale,                    \
       const float *k_scale, const float *v_scale, int64_t scale_row_stride, int64_t scale_head_stride,           \
-      const int64_t *seq_offsets, int B, int H, int D, int max_seq_len, float alpha, const float *attn_bias,     \
-      int bias_R, void *dq, void *dk, void *dv, int64_t dq_row_stride, int64_t dk_row_stride,                    \
+      const int64_t *seq_offsets, int B, int H, int D, int max_seq_len, float alpha, int p8_scale_log2,          \
+      int ds8_scale_log2, const float *attn_bias, int bias_R, void *dq, void *dk, void *dv,                      \
+      int64_t dq_row_stride, int64_t dk_row_stride,                                                              \
       int64_t dv_row_stride, float *dbias, void *workspace, int64_t workspace_bytes, int64_t total_tokens,       \
       hipStream_t stream
 #define HSTU_BWD_FP8_ARGS                                                                                        \
   dout8, dout_e8, dout_row_stride, q, k, v, q_row_stride, k_row_stride, v_row_stride, q_scale, k_scale, v_scale, \
-      scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, attn_bias, bias_R, dq, dk,  \
+      scale_row_stride, scale_head_stride, seq_offsets, B, H, D, max_seq_len, alpha, p8_scale_log2,             \
+      ds8_scale_log2, attn_bias, bias_R, dq, dk,                                                                 \
       dv, dq_row_stride, dk_row_stride, dv_row_stride, dbias, workspace, workspace_bytes, total_tokens, stream
 extern "C" int hstu_attn_bwd_fp8(HSTU_BWD_FP8_PARAMS) { return attn_bwd_fp8_impl(kBwdAll, HSTU_BWD_FP8_ARGS); }
 extern "C" int hstu_attn_bwd_fp8_dkdv(HSTU_BWD_FP8_PARAMS) { return attn_bwd_fp8_impl(kBwdDkdv, HSTU_BWD_FP8_ARGS); }

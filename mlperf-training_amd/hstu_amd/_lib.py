@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "hstu_version",
     "hstu_attn_fwd",
     "hstu_attn_fwd_fp8_pv",
+    "hstu_attn_fwd_fp8_pv_max_seq_len",
     "hstu_attn_bwd",
     "hstu_attn_fwd_workspace_bytes",
     "hstu_attn_bwd_workspace_bytes",
@@ -85,6 +86,7 @@ _u64 = ctypes.c_uint64
 
 _SIGNATURES = {
     "hstu_version": (ctypes.c_char_p, []),
+    "hstu_attn_fwd_fp8_pv_max_seq_len": (ctypes.c_int32, []),
     "hstu_attn_fwd": (
         _i32,
         [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
@@ -111,7 +113,7 @@ _SIGNATURES = {
     "hstu_attn_bwd_fp8": (
         _i32,
         [_vp, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _i32, _i32, _i32,
-         _f32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp],
+         _f32, _i32, _i32, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp],
     ),
     "hstu_attn_bwd_fp8_dkdv": "hstu_attn_bwd_fp8",
     "hstu_attn_bwd_fp8_dq": "hstu_attn_bwd_fp8",

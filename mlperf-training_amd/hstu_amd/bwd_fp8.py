@@ -60,7 +60,12 @@ class Fp8BackwardConfig:
     None: the attention op's process default);
     outproj_lnmd_fused: the output projection's e5m2 dgrad and the LN * U *
     dropout backward as one kernel when the FP8 weight gradient is on
-    (``DLRM_HSTU_FP8_BWD_OUTPROJ_LNMD_FUSED``, ``triton_hstu_linear.py:5410-5470``).
+    (``DLRM_HSTU_FP8_BWD_OUTPROJ_LNMD_FUSED``, ``triton_hstu_linear.py:5410-5470``);
+    attn_ssc_k / attn_dsc_k: the full-FP8 attention backward's P and dS
+    pre-scale exponents relative to ceil(log2 N)
+    (``DLRM_HSTU_FP8_BWD_FULL_SSC_K`` / ``_DSC_K``, ``hstu_flydsl_mha.py:1351-1370``;
+    None: the environment, read per call as the reference does; the
+    production gin sets DSC_K = -5, ``yambda_5b.gin:3764-3799``).
     """
 
     enabled: bool = False
@@ -73,6 +78,8 @@ class Fp8BackwardConfig:
     grad_format: str = "e5m2"
     attn_full_fp8: Optional[bool] = None
     outproj_lnmd_fused: bool = False
+    attn_ssc_k: Optional[int] = None
+    attn_dsc_k: Optional[int] = None
 
     def __post_init__(self):
         if self.grad_format not in ("e5m2", "e4m3"):

@@ -23,7 +23,9 @@ pre-quantized ``(w8_nk, w_scale)`` pair from ``quantize_weight_e4m3``.
 
 from __future__ import annotations
 
+import math
 import os
+import weakref
 from typing import Dict, Optional, Tuple, Union
 
 import torch
@@ -99,11 +101,12 @@ def fp8_scale_tensor(scale_state: torch.Tensor) -> torch.Tensor:
     return scale_state.reshape(-1)[:1].reshape(1, 1)
 
 
-# Host knowledge of each state buffer: storage address -> (version counter
-# when last seen, completed steps).  Buffers this module updates stay known
-# without reading the device; a buffer changed elsewhere (loaded from a
-# checkpoint, reset) is read once.
-_known: Dict[Tuple[int, int], Tuple[int, int]] = {}
+# Host knowledge of each scale tensor: storage address -> (version counter
+# when last seen, completed steps, the tensor itself as a weak reference).
+# Tensors this module updates stay known without reading the device; a
+# tensor changed elsewhere (loaded from a checkpoint, reset), or a new tensor
+# on a recycled address, is read once.
+_known: Dict[Tuple[int, int], Tuple[int, int, "weakref.ref"]] = {}
 
 
 def _key(buf: torch.Tensor) -> Tuple[int, int]:
@@ -111,30 +114,38 @@ def _key(buf: torch.Tensor) -> Tuple[int, int]:
 
 
 def _completed(buf: torch.Tensor) -> int:
+    """Completed calibration steps of a state buffer; for a one-element scale
+    1 once its value is finite and positive (the reference's
+    ``activation_scale_value``, ``triton_fp8.py:429-442``), else 0."""
     key = _key(buf)
     seen = _known.get(key)
-    if seen is not None and seen[0] == buf._version:
+    if seen is not None and seen[0] == buf._version and seen[2]() is buf:
         return seen[1]
     flat = buf.reshape(-1)
-    # one device read; a positive scale in a short buffer counts as complete
-    done = int(flat[1].item()) if flat.numel() >= 3 else (1 if float(flat[0].item()) > 0.0 else 0)
-    _known[key] = (buf._version, done)
+    if flat.numel() >= 3:
+        done = int(flat[1].item())
+    else:
+        v = float(flat[0].item())
+        done = 1 if math.isfinite(v) and v > 0.0 else 0
+    _remember(buf, done)
     return done
 
 
 def _remember(buf: torch.Tensor, done: int) -> None:
-    _known[_key(buf)] = (buf._version, done)
+    _known[_key(buf)] = (buf._version, done, weakref.ref(buf))
 
 
 def scale_ready(scale: Optional[torch.Tensor]) -> bool:
     """Can the FP8 path use this scale now?  A one-element tensor is a plain
-    scale and always is (its value is not read); a state buffer is once its
-    calibration window is complete.  No device read for a buffer this module
-    calibrated, or any one-element scale."""
+    scale, usable once its value is finite and positive (read once per
+    tensor and version: a zero or non-finite scale runs bf16 and is
+    calibrated, as the reference's ``activation_scale_value`` returns None
+    for it); a state buffer is usable once its calibration window is
+    complete.  No device read for a tensor this module calibrated."""
     if scale is None:
         return False
     if scale.numel() == 1:
-        return True
+        return _completed(scale) >= 1
     if scale.numel() < 3:
         raise ValueError("FP8 scale state must contain scale, count, and amax history")
     return _completed(scale) >= scale.numel() - 2
@@ -146,8 +157,10 @@ def calibrate_scale_buffer(scale_buffer: torch.Tensor, value: torch.Tensor, *, m
     ``triton_fp8.py:694-749``): this call's amax joins the history; once the
     history is full the scale is max(history) * margin / 448 and stays there
     (the state is frozen).  A one-element buffer is simply set from this
-    call.  Returns the scale (0.0 while calibrating).  An all-zero value is
-    not a step.  With torch.distributed initialised (world > 1) the amax is
+    call.  Both scales are the reference's device expression
+    ``amax * margin / 448`` in its operation order, so they match its bits.
+    Returns the scale (0.0 while calibrating).  An all-zero value is not a
+    step.  With torch.distributed initialised (world > 1) the amax is
     MAX-reduced across ranks first.  Bounded warm-up work: it reads the amax
     on the host, as the reference does; a frozen state returns at once."""
     m = ASCALE_MARGIN if margin is None else margin
@@ -159,26 +172,25 @@ def calibrate_scale_buffer(scale_buffer: torch.Tensor, value: torch.Tensor, *, m
     if (synchronize and torch.distributed.is_available() and torch.distributed.is_initialized()
             and torch.distributed.get_world_size() > 1):
         torch.distributed.all_reduce(amax, op=torch.distributed.ReduceOp.MAX)
-    a = float(amax.item())
-    if not a > 0.0:
+    if not float(amax.item()) > 0.0:
         return float(flat[0].item()) if flat.numel() else 0.0
-    a = max(a, 1.0e-12)
+    amax = amax.to(scale_buffer.device).clamp_min(1.0e-12)
     if flat.numel() == 1:
-        flat.fill_(a * m / E4M3_MAX)
+        flat[:1].copy_((amax * m / E4M3_MAX).reshape(1))
         _remember(scale_buffer, 1)
         return float(flat[0].item())
     if flat.numel() < 3:
         raise ValueError("FP8 scale state must contain scale, count, and amax history")
     steps = flat.numel() - 2
     done = min(_completed(scale_buffer), steps)
-    flat[2 + done].fill_(a)
+    flat[2 + done].copy_(amax)
     done += 1
     flat[1].fill_(float(done))
     if done < steps:
         flat[0].zero_()
         _remember(scale_buffer, done)
         return 0.0
-    flat[0:1].copy_(flat[2:].amax().reshape(1) * (m / E4M3_MAX))
+    flat[0].copy_(flat[2:2 + done].amax() * m / E4M3_MAX)
     _remember(scale_buffer, done)
     return float(flat[0].item())
 

@@ -254,9 +254,10 @@ def _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, m
 
 
 def _launch_bwd_fp8(dout8, e8, q, k, v, dq, dk, dv, seq_offsets, N, alpha, q_scale, k_scale, v_scale,
-                    attn_bias, dbias) -> None:
+                    attn_bias, dbias, prescale_log2: Tuple[int, int]) -> None:
     """The full-FP8 backward (``hstu_attn_bwd_fp8``) on an e4m3 dO with its
-    block scales (``hstu_do_fp8.quantize_do_e4m3_blk``'s output)."""
+    block scales (``hstu_do_fp8.quantize_do_e4m3_blk``'s output), P and dS
+    cast at 2^prescale_log2[0] and 2^prescale_log2[1]."""
     T, H, D = q.shape
     q, k, v = _row_view(q), _row_view(k), _row_view(v)
     if dout8.dtype != _E4M3 or e8.dtype != torch.uint8 or tuple(e8.shape) != (T, H):
@@ -286,8 +287,8 @@ def _launch_bwd_fp8(dout8, e8, q, k, v, dq, dk, dv, seq_offsets, N, alpha, q_sca
         dout8.data_ptr(), e8.data_ptr(), _row_stride(dout8),
         q.data_ptr(), k.data_ptr(), v.data_ptr(), _row_stride(q), _row_stride(k), _row_stride(v),
         _lib.ptr(qs), _lib.ptr(ks), _lib.ptr(vs), srs, shs,
-        offs.data_ptr(), B, H, D, int(N), float(alpha), _lib.ptr(bias), R,
-        targets[0].data_ptr(), targets[1].data_ptr(), targets[2].data_ptr(),
+        offs.data_ptr(), B, H, D, int(N), float(alpha), int(prescale_log2[0]), int(prescale_log2[1]),
+        _lib.ptr(bias), R, targets[0].data_ptr(), targets[1].data_ptr(), targets[2].data_ptr(),
         _row_stride(targets[0]), _row_stride(targets[1]), _row_stride(targets[2]),
         _lib.ptr(dbias), ws.data_ptr(), ws.numel(), T, _stream(q.device))
     _lib.check(st, "hstu_attn_bwd_fp8")
@@ -332,15 +333,21 @@ def fp8_fwd_pv_scale() -> float:
     return round(x, 6)
 
 
-def fp8_pv_fwd_reason(q: torch.Tensor, num_targets, max_attn_len: int, contextual_seq_len: int) -> Optional[str]:
+def fp8_pv_fwd_reason(q: torch.Tensor, num_targets, max_attn_len: int, contextual_seq_len: int,
+                      N: Optional[int] = None) -> Optional[str]:
     """None when the FP8 P.V forward kernel serves this call (e4m3 inputs,
-    D = 128, the causal mask), else why not."""
+    D = 128, the causal mask, max_seq_len ``N`` within the kernel's LDS
+    table), else why not."""
     if not _is_fp8(q):
         return "inputs are not e4m3"
     if q.shape[2] != 128:
         return f"head dim {q.shape[2]}"
     if num_targets is not None or max_attn_len > 0 or contextual_seq_len > 0:
         return "num_targets / max_attn_len / contextual_seq_len masks"
+    if N is not None:
+        n_max = int(_lib.fn("hstu_attn_fwd_fp8_pv_max_seq_len")())
+        if int(N) > n_max:
+            return f"max_seq_len {int(N)} above {n_max} (the kernel's per-key LDS table)"
     return None
 
 
@@ -407,6 +414,8 @@ def _op_bwd(
     attn_bias: Optional[torch.Tensor],
     dbias: Optional[torch.Tensor],
     full_fp8: bool = False,
+    p8_log2: int = 0,
+    ds8_log2: int = 0,
 ) -> None:
     if dout.shape[0] == 0:
         dq.zero_()
@@ -421,7 +430,7 @@ def _op_bwd(
         # the reference's full-FP8 backward: dO quantized in pow2 blocks, then five e4m3 products
         dout8, e8 = hstu_do_fp8.quantize_do_e4m3_blk(dout, seq_offsets, int(N))
         _launch_bwd_fp8(dout8, e8, q, k, v, dq, dk, dv, seq_offsets, N, alpha, q_scale, k_scale, v_scale,
-                        attn_bias, dbias)
+                        attn_bias, dbias, (p8_log2, ds8_log2))
         return
     _launch_bwd(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, max_attn_len,
                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias)
@@ -429,7 +438,8 @@ def _op_bwd(
 
 @_op_bwd.register_fake
 def _op_bwd_fake(dout, q, k, v, dq, dk, dv, seq_offsets, num_targets, N, alpha, max_attn_len,
-                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias, full_fp8=False):
+                 contextual_seq_len, q_scale, k_scale, v_scale, attn_bias, dbias, full_fp8=False, p8_log2=0,
+                 ds8_log2=0):
     return None
 
 
@@ -480,7 +490,7 @@ def triton_hstu_attention_fwd(
     fp8 = _is_fp8(q)
     pv_scale = 0.0
     if fp8 and (fp8_fwd_pv_enabled() if fp8_pv is None else fp8_pv):
-        why = fp8_pv_fwd_reason(q, num_targets, int(max_attn_len), int(contextual_seq_len))
+        why = fp8_pv_fwd_reason(q, num_targets, int(max_attn_len), int(contextual_seq_len), int(N))
         if why is None:
             pv_scale = fp8_fwd_pv_scale()
         else:
@@ -517,6 +527,8 @@ def triton_hstu_attention_bwd(
     attn_bias: Optional[torch.Tensor] = None,
     dbias: Optional[torch.Tensor] = None,
     full_fp8: Optional[bool] = None,
+    ssc_k: Optional[int] = None,
+    dsc_k: Optional[int] = None,
 ) -> None:
     """Backward op (``triton_hstu_attention.py:3298-3319``): writes dq, dk, dv
     in place (they may be strided views of a fused gradient buffer); an empty
@@ -528,13 +540,17 @@ def triton_hstu_attention_bwd(
     power-of-two (sequence, head, 32-token) blocks, P and dS cast to e4m3,
     all five products on the e4m3 MFMA (``hstu_attn_bwd_fp8``).  A call it
     cannot serve (the targets / window / contextual masks) runs the e4m3-input
-    backward on the block-quantized dO instead, with the reason logged once."""
+    backward on the block-quantized dO instead, with the reason logged once.
+    ``ssc_k`` / ``dsc_k``: the P and dS pre-scale exponents relative to
+    ceil(log2 N) (None: the reference's environment, read per call,
+    ``hstu_do_fp8.full_fp8_prescale_log2``)."""
     del sort_by_length_indices, enable_tma
     reason = unsupported_shape_reason(q, k, v, num_softmax_heads)
     if reason is not None:
         raise NotImplementedError(f"HIP HSTU attention backward: {reason}")
     fp8 = _is_fp8(q)
     use_full = False
+    prescale = (0, 0)
     if fp8 and dout.numel() > 0:
         from . import hstu_do_fp8
 
@@ -543,6 +559,7 @@ def triton_hstu_attention_bwd(
             H, D = dout.shape[1], dout.shape[2]
             if why is None:
                 use_full = True
+                prescale = hstu_do_fp8.full_fp8_prescale_log2(int(N), ssc_k=ssc_k, dsc_k=dsc_k)
             elif D in (64, 128) and H * D in (128, 256, 512):
                 _log_once(f"full-FP8 backward: {why}; the e4m3 backward runs on the block-quantized dO")
                 dout = hstu_do_fp8.block_quantized_do(dout, seq_offsets, int(N))
@@ -553,7 +570,7 @@ def triton_hstu_attention_bwd(
             _scale_or_none(q_scale, q) if fp8 else None,
             _scale_or_none(k_scale, q) if fp8 else None,
             _scale_or_none(v_scale, q) if fp8 else None,
-            attn_bias, dbias, use_full)
+            attn_bias, dbias, use_full, prescale[0], prescale[1])
 
 
 # ---------------------------------------------------------------------------

@@ -7,15 +7,16 @@ one pow2 scale per (sequence, head, 32-token group), the groups being tokens
 p % 16 < 8 and p % 16 >= 8 of each 64-token tile of a sequence; no host sync.
 
 ``bwd_full_fp8_enabled`` reads the reference's switch ``DLRM_HSTU_FP8_BWD_FULL``
-(``hstu_flydsl_mha.py:458-464``).  Under it the FP8 attention backward runs on
-the block-quantized dO: ``quantize_do_e4m3_blk`` then the exact
-``dequantize_do_e4m3_blk``, so its gradients are those of the reference's
-contract for the dO operand (the reference undoes the scales inside its
-MFMAs, :1330-1394).  The e4m3 P / dS operands of that backward are not built.
+(``hstu_flydsl_mha.py:458-464``).  Under it the FP8 attention backward runs
+the full-FP8 kernels on ``quantize_do_e4m3_blk``'s output, with the e4m3 P
+and dS pre-scales of ``full_fp8_prescale_log2``; for the masks those kernels
+do not serve it runs the e4m3-input backward on the exact
+``dequantize_do_e4m3_blk`` of the quantized dO.
 """
 
 from __future__ import annotations
 
+import math
 import os
 from typing import Optional, Tuple
 
@@ -68,6 +69,37 @@ def set_bwd_full_fp8(flag: Optional[bool]) -> None:
     """Set the full-FP8 backward default (None: read the environment again on next use)."""
     global _full
     _full = flag
+
+
+SSC_K_DEFAULT = 3
+DSC_K_DEFAULT = -3
+
+
+def full_fp8_prescale_log2(N: int, *, ssc_k: Optional[int] = None, dsc_k: Optional[int] = None) -> Tuple[int, int]:
+    """(P, dS) e4m3 pre-scale exponents of the full-FP8 backward, as the
+    reference resolves them per call (``hstu_flydsl_mha.py:1351-1374``): with
+    c = ceil(log2 max(N, 2)), ``DLRM_HSTU_FP8_BWD_FULL_{SSC,DSC}_LOG2`` (an
+    absolute exponent) if set, else c + ``DLRM_HSTU_FP8_BWD_FULL_{SSC,DSC}_K``
+    (defaults 3 and -3; the production gin sets DSC_K = -5,
+    ``yambda_5b.gin:3799``).  ``ssc_k`` / ``dsc_k`` given (the layer's
+    ``Fp8BackwardConfig``) replace the environment.  The P exponent may not
+    exceed c + 9 (the SiLU's upper-only clamp stays exact below it)."""
+    c = int(math.ceil(math.log2(max(int(N), 2))))
+
+    def one(name: str, k: Optional[int], k_default: int) -> int:
+        if k is not None:
+            return c + int(k)
+        ab = os.environ.get(f"DLRM_HSTU_FP8_BWD_FULL_{name}_LOG2")
+        if ab not in (None, ""):
+            return int(ab)
+        return c + int(os.environ.get(f"DLRM_HSTU_FP8_BWD_FULL_{name}_K", str(k_default)))
+
+    e_p, e_ds = one("SSC", ssc_k, SSC_K_DEFAULT), one("DSC", dsc_k, DSC_K_DEFAULT)
+    if e_p > c + 9:
+        raise ValueError(f"full-FP8 backward: P pre-scale 2^{e_p} above 2^(ceil(log2 N) + 9) = 2^{c + 9}")
+    if not (-64 <= e_p <= 64 and -64 <= e_ds <= 64):
+        raise ValueError(f"full-FP8 backward: pre-scale exponents ({e_p}, {e_ds}) outside [-64, 64]")
+    return e_p, e_ds
 
 
 def dequantize_do_e4m3_blk(dout8: torch.Tensor, e8: torch.Tensor) -> torch.Tensor:

@@ -30,6 +30,7 @@ backward's residual / dropout-mask folds, D other than 256 or 512.
 from __future__ import annotations
 
 import os
+import weakref
 from typing import Optional, Tuple
 
 import torch
@@ -380,14 +381,28 @@ class ResidualLink:
     backward (dx = dres + LN backward, one rounding) instead of autograd adding
     the two bf16 gradients in a separate kernel.  The output block's backward
     runs first (its inputs are the preprocess outputs); it stores the gradient
-    and returns None for x."""
+    and returns None for x.
+
+    The preprocess forward binds its x (``bind``); the output block uses the
+    link only when its own residual input is that same tensor at the same
+    version (``bound_to``), else it returns the residual gradient itself."""
 
     def __init__(self) -> None:
         self.grad: Optional[torch.Tensor] = None
+        self._x: Optional["weakref.ref"] = None
+        self._x_version = -1
+
+    def bind(self, x: torch.Tensor) -> None:
+        self._x = weakref.ref(x)
+        self._x_version = x._version
+
+    def bound_to(self, x: torch.Tensor) -> bool:
+        return self._x is not None and self._x() is x and x._version == self._x_version
 
     def take(self) -> Optional[torch.Tensor]:
         g, self.grad = self.grad, None
         return g
+
 
 class HSTUComputeOutputFunction(torch.autograd.Function):
     """``HSTUComputeOutputFunction`` (``triton_hstu_linear.py:5109-5900``),
@@ -445,7 +460,8 @@ class HSTUComputeOutputFunction(torch.autograd.Function):
         # written as the leading columns of that buffer (triton_hstu_linear.py:5347-5350)
         ctx.du_row_width = int(getattr(u, "_hstu_duvqk_width", 0))
         ctx.cfg = (dropout_ratio, silu_u, concat_u, concat_x, mul_u_activation_type)
-        ctx.residual_link = residual_link
+        # the link is used only for the x its preprocess forward was given
+        ctx.residual_link = residual_link if residual_link is not None and residual_link.bound_to(x) else None
         return out
 
     @staticmethod

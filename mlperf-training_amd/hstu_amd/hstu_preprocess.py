@@ -24,6 +24,7 @@ and the LayerNorm backward.
 
 from __future__ import annotations
 
+import logging
 from typing import Optional, Tuple
 
 import torch
@@ -36,6 +37,7 @@ from .hstu_linear import _ln_bwd, _ln_fwd, hstu_compute_output
 from .wgrad import token_wgrad
 
 DUVQK_WIDTH_ATTR = "_hstu_duvqk_width"
+logger = logging.getLogger(__name__)
 
 
 def _adopt_duvqk(du: Optional[torch.Tensor], T: int, width: int, like: torch.Tensor) -> torch.Tensor:
@@ -113,6 +115,8 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         ctx.x8_scale = sa if keep_x8 else None
         ctx.fp8_backward = fp8_backward
         ctx.residual_link = residual_link
+        if residual_link is not None:
+            residual_link.bind(x)
         u = u.contiguous() if u.stride(1) != 1 else u
         setattr(u, DUVQK_WIDTH_ATTR, uvqk_weight.shape[1])
         return u, attn.view(T, H * Dv)
@@ -149,10 +153,11 @@ class _HSTUPreprocessAndAttentionFunction(torch.autograd.Function):
         dbias = None
         if attn_bias is not None:
             dbias = torch.empty(attn_bias.shape, dtype=torch.float32, device=x.device)
+        bcfg = bwd_fp8.resolve(ctx.fp8_backward)
         triton_hstu_attention_bwd(dattn.contiguous().view(T, H, Dv), q, k, v, dq, dk, dv, seq_offsets, num_targets,
                                   N, alpha, max_attn_len, ctx_len, None, False, 0, qkv_scale, qkv_scale, qkv_scale,
                                   attn_bias=attn_bias, dbias=dbias,
-                                  full_fp8=bwd_fp8.resolve(ctx.fp8_backward).attn_full_fp8)
+                                  full_fp8=bcfg.attn_full_fp8, ssc_k=bcfg.attn_ssc_k, dsc_k=bcfg.attn_dsc_k)
         # projection backward on the recomputed bf16 LN(x): the FP8 dgrad arm
         # (DLRM_HSTU_FP8_BWD_UVQK=1, after its warm-up), else bf16 GEMMs
         def recompute_normed_x() -> torch.Tensor:
@@ -227,12 +232,75 @@ def triton_hstu_preprocess_and_attention(
         defer_silu, attn_bias, fp8_backward, residual_link)
 
 
+class _NormProjFunction(torch.autograd.Function):
+    """``LN(x) . W + b`` on this build's kernels: the LayerNorm kernel and the
+    bf16 GEMM (``ops/hstu_compute.py:108-127`` with a Triton/HIP ``kernel``).
+    Backward: the token-axis weight gradient with the bias column sum in the
+    same pass, the bf16 dgrad ``d(uvqk) . W^T`` and the LayerNorm backward
+    on the saved mean / rstd."""
+
+    @staticmethod
+    def forward(ctx, x, norm_weight, norm_bias, norm_eps, uvqk_weight, uvqk_bias):
+        xn, mean, rstd, _ = _ln_fwd(x, None, norm_weight, norm_bias, norm_eps, 0.0, False, False, False, False,
+                                    "none", 0, False, 1.0)
+        w = uvqk_weight.to(x.dtype)
+        uvqk = _fp8.bf16_gemm(xn, w.t(), bias=uvqk_bias)
+        ctx.save_for_backward(x, norm_weight, norm_bias, mean, rstd, w, xn)
+        ctx.dtypes = (uvqk_weight.dtype, uvqk_bias.dtype)
+        return uvqk
+
+    @staticmethod
+    def backward(ctx, duvqk):
+        x, nw, nb, mean, rstd, w, xn = ctx.saved_tensors
+        w_dtype, b_dtype = ctx.dtypes
+        duvqk = duvqk.to(x.dtype).contiguous()
+        d_w, d_b = token_wgrad(xn, duvqk, with_colsum=True)
+        dxn = _fp8.bf16_gemm(duvqk, w)
+        dx, _, dnw, dnb, _ = _ln_bwd(dxn, x, None, nw, nb, mean, rstd, 0.0, None, False, False, False, "none", False)
+        return dx, dnw.to(nw.dtype), dnb.to(nb.dtype), None, d_w.to(w_dtype), d_b.to(b_dtype)
+
+
+def uqvk_kernel_reason(x: torch.Tensor, norm_weight, norm_bias, uvqk_weight: torch.Tensor,
+                       uvqk_bias) -> Optional[str]:
+    """Why ``hstu_compute_uqvk`` cannot run on the LayerNorm kernel and the
+    bf16 GEMM (None: it can): bf16 device rows, LayerNorm width in
+    ``SERVED_D``, projection width a multiple of 256 (the weight gradient's
+    tile), both LayerNorm parameters and the bias given."""
+    from .hstu_linear import SERVED_D
+
+    if not x.is_cuda or x.dtype != torch.bfloat16 or x.dim() != 2:
+        return f"x must be a 2-D bf16 device tensor (got {x.dtype}, {tuple(x.shape)})"
+    if x.shape[1] not in SERVED_D:
+        return f"LayerNorm width {x.shape[1]} not served (D in {SERVED_D})"
+    if norm_weight is None or norm_bias is None or uvqk_bias is None:
+        return "the kernel path takes the LayerNorm weight and bias and the projection bias"
+    if uvqk_weight.dim() != 2 or uvqk_weight.shape[0] != x.shape[1] or uvqk_weight.shape[1] % 256 != 0:
+        return f"uvqk_weight {tuple(uvqk_weight.shape)} not served (K = {x.shape[1]}, N % 256 == 0)"
+    return None
+
+
+_UQVK_LOGGED: set = set()
+
+
 def hstu_compute_uqvk(x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim, uvqk_weight, uvqk_bias,
                       kernel: HammerKernel = HammerKernel.PYTORCH):
-    """LN -> addmm -> split u|v|q|k -> silu(u) (``ops/hstu_compute.py:86-144``),
-    in torch ops (differentiable)."""
-    xn = F.layer_norm(x, (x.shape[-1],), norm_weight, norm_bias, norm_eps)
-    uvqk = torch.addmm(uvqk_bias, xn, uvqk_weight)
+    """LN -> addmm -> split u|v|q|k -> silu(u) (``ops/hstu_compute.py:86-144``).
+    ``kernel=PYTORCH``: torch ops (``F.layer_norm`` + ``torch.addmm``), as the
+    reference's PyTorch path.  ``TRITON`` / ``HIP``: this build's LayerNorm
+    kernel and bf16 GEMM (``_NormProjFunction``); a shape those kernels do
+    not serve takes the torch ops, with the reason logged once.  Returns
+    (u, q, k, v), q/k/v as [T, H, D] views of the projection."""
+    uvqk = None
+    if kernel in (HammerKernel.TRITON, HammerKernel.HIP):
+        why = uqvk_kernel_reason(x, norm_weight, norm_bias, uvqk_weight, uvqk_bias)
+        if why is None:
+            uvqk = _NormProjFunction.apply(x, norm_weight, norm_bias, norm_eps, uvqk_weight, uvqk_bias)
+        elif why not in _UQVK_LOGGED:
+            _UQVK_LOGGED.add(why)
+            logger.warning("hstu_compute_uqvk: %s; the torch ops run", why)
+    if uvqk is None:
+        xn = F.layer_norm(x, (x.shape[-1],), norm_weight, norm_bias, norm_eps)
+        uvqk = torch.addmm(uvqk_bias, xn, uvqk_weight)
     u, v, q, k = torch.split(uvqk, [hidden_dim * num_heads, hidden_dim * num_heads, attn_dim * num_heads,
                                     attn_dim * num_heads], dim=1)
     return (F.silu(u), q.reshape(-1, num_heads, attn_dim), k.reshape(-1, num_heads, attn_dim),
@@ -260,8 +328,8 @@ def hstu_preprocess_and_attention(
     u, q, k, v = hstu_compute_uqvk(x, norm_weight, norm_bias, norm_eps, num_heads, attn_dim, hidden_dim,
                                    uvqk_weight, uvqk_bias, kernel)
     attn = hstu_mha(max_seq_len, attn_alpha, q, k, v, seq_offsets, True, 0.0, False, num_targets,
-                    max_attn_len=max_attn_len, contextual_seq_len=contextual_seq_len,
-                    kernel=HammerKernel.PYTORCH).view(-1, hidden_dim * num_heads)
+                    max_attn_len=max_attn_len, contextual_seq_len=contextual_seq_len, sort_by_length=sort_by_length,
+                    kernel=kernel).view(-1, hidden_dim * num_heads)
     return u, attn, k, v
 
 

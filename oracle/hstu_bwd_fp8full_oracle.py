@@ -10,8 +10,10 @@ What the reference's production backward does under DLRM_HSTU_FP8_BWD_FULL
   ``hstu_do_fp8_oracle``); dP = dO8 . V^T stays in that scaled domain and
   the group scales are undone inside the dV / dK / dQ products;
 * ``:1351-1370`` -- silu and dS carry the kernel's 1 / N, so their e4m3
-  pre-scales are N-relative: P8 = e4m3_sat(silu / N * 2^(c+3)) and dS8 =
-  e4m3_sat(dS * 2^(c-3)), c = ceil(log2 N) (``prescales``);
+  pre-scales are N-relative: P8 = e4m3_sat(silu / N * 2^(c+K_SSC)) and dS8 =
+  e4m3_sat(dS * 2^(c+K_DSC)), c = ceil(log2 N), K_SSC = 3, K_DSC = -3 by
+  default and -5 in the production gin (``yambda_5b.gin:3764-3799``)
+  (``prescales``);
 * ``ops/flydsl/hstu_bwd_dkdv.py:356-403`` -- all five products on e4m3
   operands: dV = P8^T dO8, dK = dS8^T q8, dQ = dS8 k8 with the dO group
   scale on the dO side.
@@ -20,12 +22,12 @@ This build extends the reference's per-tensor ``qkv_scale`` to per-(token,
 head) scales: the query scale is folded into the dK operand and the key
 scale into the dQ operand before their casts, times the power-of-two
 normaliser 2^-E of the largest scale (``pow2_norm``):
-dS8k = e4m3_sat(dS' s_q 2^-Eq 2^(c-3)), dS8q = e4m3_sat(dS' s_k 2^-Ek 2^(c-3)).
+dS8k = e4m3_sat(dS' s_q 2^-Eq 2^(c+K_DSC)), dS8q = e4m3_sat(dS' s_k 2^-Ek 2^(c+K_DSC)).
 The bias gradient is read back from dS8q.
 
 Functions and what pins them (``tests/test_bwd_fp8full_oracle.py``):
 
-* ``prescales`` -- closed forms at N = 4096, 1000, 2.
+* ``prescales`` -- closed forms at N = 4096, 1000, 2 and at K_DSC = -5.
 * ``pow2_norm`` -- s * norm in [1/2, 1) for the largest s, a power of two.
 * ``e4m3_sat`` -- torch's RNE float8_e4m3fn conversion (a library routine)
   after a clamp to +-448.
@@ -47,10 +49,12 @@ from . import hstu_oracle as orc
 E4M3_MAX = 448.0
 
 
-def prescales(N: int) -> Tuple[float, float]:
-    """(P pre-scale 2^(c+3), dS pre-scale 2^(c-3)) with c = ceil(log2 max(N, 2))."""
+def prescales(N: int, ssc_k: int = 3, dsc_k: int = -3) -> Tuple[float, float]:
+    """(P pre-scale 2^(c+ssc_k), dS pre-scale 2^(c+dsc_k)) with
+    c = ceil(log2 max(N, 2)) (``hstu_flydsl_mha.py:1351-1370``: K = 3 and -3
+    by default; the production gin's DSC_K = -5, ``yambda_5b.gin:3799``)."""
     c = max(1, math.ceil(math.log2(max(int(N), 2))))
-    return 2.0 ** (c + 3), 2.0 ** (c - 3)
+    return 2.0 ** (c + ssc_k), 2.0 ** (c + dsc_k)
 
 
 def pow2_norm(max_scale: float) -> float:
@@ -81,6 +85,8 @@ def full_fp8_bwd(
     attn_bias: Optional[torch.Tensor] = None,
     quantize: bool = True,
     max_scales: Optional[Tuple[float, float]] = None,
+    ssc_k: int = 3,
+    dsc_k: int = -3,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """(dq, dk, dv, dbias) of the causal attention with the full-FP8 casts.
 
@@ -90,11 +96,12 @@ def full_fp8_bwd(
     dequantized q, k, v and are float64.  ``quantize=False`` skips every cast
     (the exact backward of the same inputs).  ``max_scales`` = (largest q
     scale, largest k scale) of the whole batch when the rows given are a
-    sample of it (the normalisers come from the whole batch)."""
+    sample of it (the normalisers come from the whole batch).  ``ssc_k`` /
+    ``dsc_k``: the pre-scale exponents relative to ceil(log2 N)."""
     T, H, D = q8.shape
     if dout8.dtype == torch.uint8:  # raw e4m3 bytes (the quantizer oracle's output)
         dout8 = dout8.view(torch.float8_e4m3fn)
-    ssc, dsc = prescales(N) if quantize else (1.0, 1.0)
+    ssc, dsc = prescales(N, ssc_k, dsc_k) if quantize else (1.0, 1.0)
     cast = e4m3_sat if quantize else (lambda t: t)
     sq, sk, sv = (s.to(torch.float64).expand(T, H) if s.numel() == 1 else s.to(torch.float64) for s in (sq, sk, sv))
     mq, mk = max_scales if max_scales is not None else (float(sq.abs().max()), float(sk.abs().max()))

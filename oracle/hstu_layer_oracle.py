@@ -21,10 +21,20 @@ dgrad runs as the FP8 backward arm does (``ops/triton/bwd_fp8.py:1347-1395,
 weight to per-tensor e4m3 (amax / 448), the wgrad and bias gradient exact --
 or, for the sites in ``fp8_wgrad``, the wgrad from the e4m3 activation and
 the e5m2 gradient (``fp8_wgrad``, ``ops/triton/fp8_wgrad.py:109-160``).
+With ``attention="production"`` the attention step is the reference's
+production FP8 pair (``DLRM_HSTU_FP8_FWD_PV=1`` and ``DLRM_HSTU_FP8_BWD_FULL=1``,
+``dlrm_v4/train/gin/yambda_5b.gin:3293-3319``): the forward is the FP8 P.V
+forward of ``hstu_fwd_pv8_oracle.fwd_pv8`` on the e4m3 V/Q/K at the
+per-tensor scale s_qkv, and the backward is ``hstu_bwd_fp8full_oracle.full_fp8_bwd``
+on the attention output's gradient rounded to bf16 and block-quantized by
+``hstu_do_fp8_oracle.quantize_do_e4m3_blk`` (``ops/flydsl/hstu_flydsl_mha.py:1330-1394``),
+with the P / dS pre-scale exponents ``ssc_k`` / ``dsc_k``.
 Parity pins: those of the composed functions; the composition itself is
 checked for shapes, the residual gradient (= dY) and agreement with plain
 autograd when the quantizers are identities; the FP8 dgrad against
-``hstu_bwd_fp8_oracle.dgrad`` of the same quantized operands.
+``hstu_bwd_fp8_oracle.dgrad`` of the same quantized operands; the production
+attention step, with its casts off, against the autograd of the dense
+attention (``tests/test_layer_oracle.py``).
 """
 
 from __future__ import annotations
@@ -36,6 +46,9 @@ import torch
 import torch.nn.functional as F
 
 from oracle import hstu_bwd_fp8_oracle as BO
+from oracle import hstu_bwd_fp8full_oracle as FO
+from oracle import hstu_do_fp8_oracle as DO
+from oracle import hstu_fwd_pv8_oracle as PV
 from oracle import hstu_ln_oracle as L
 from oracle import hstu_oracle as orc
 
@@ -84,6 +97,48 @@ class _Fp8DgradMatmul(torch.autograd.Function):
         return d_a, d_w, None, None
 
 
+class _ProductionAttention(torch.autograd.Function):
+    """The production FP8 attention on dequantized q, k, v [T, H, D] whose
+    values are e4m3 codes times the per-tensor scale s.  Forward: the FP8
+    P.V forward; backward: the full-FP8 backward on e4m3(bf16(dO)) in pow2
+    blocks.  ``quantize=False`` turns every cast off (the dO passes
+    unquantized at unit group scale): the exact attention and its gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, N, alpha, s, offs, pv_scale, ssc_k, dsc_k, quantize):
+        codes = [(t.detach() / s) for t in (q, k, v)]
+        if quantize:  # exact e4m3 codes (the straight-through sum can be off by an ulp)
+            codes = [c.to(torch.float8_e4m3fn).double() for c in codes]
+        st = torch.tensor([s], dtype=torch.float64)
+        b = None if bias is None else bias.detach()
+        out = PV.fwd_pv8(N, alpha, *codes, st, st, st, offs, attn_bias=b, pv_scale=pv_scale, quantize=quantize)
+        ctx.save_for_backward(*codes, *([] if b is None else [b]))
+        ctx.cfg = (N, alpha, s, offs, ssc_k, dsc_k, quantize, b is not None)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        N, alpha, s, offs, ssc_k, dsc_k, quantize, has_b = ctx.cfg
+        q8, k8, v8 = ctx.saved_tensors[:3]
+        b = ctx.saved_tensors[3] if has_b else None
+        if quantize:
+            y8, e8 = DO.quantize_do_e4m3_blk(dout.to(torch.bfloat16), offs, N)
+        else:
+            y8, e8 = dout, torch.full(dout.shape[:2], 127, dtype=torch.uint8)
+        st = torch.tensor([s], dtype=torch.float64)
+        dq, dk, dv, db = FO.full_fp8_bwd(N, alpha, q8, k8, v8, st, st, st, offs, y8, e8, attn_bias=b,
+                                         quantize=quantize, ssc_k=ssc_k, dsc_k=dsc_k)
+        return dq, dk, dv, db, None, None, None, None, None, None, None, None
+
+
+def production_attention(q, k, v, s, offs, N, alpha, attn_bias=None, pv_scale=10.04, ssc_k=3, dsc_k=-3,
+                         quantize=True):
+    """[T, H, D] float64 output of the production FP8 attention (see
+    ``_ProductionAttention``), differentiable in q, k, v and the bias."""
+    return _ProductionAttention.apply(q, k, v, attn_bias, N, alpha, float(s), offs, pv_scale, ssc_k, dsc_k,
+                                      quantize)
+
+
 def fp8_dgrad_matmul(a: torch.Tensor, w: torch.Tensor, s_g: Optional[float],
                      s_a: Optional[float] = None) -> torch.Tensor:
     return a @ w if s_g is None else _Fp8DgradMatmul.apply(a, w, s_g, s_a)
@@ -91,14 +146,19 @@ def fp8_dgrad_matmul(a: torch.Tensor, w: torch.Tensor, s_g: Optional[float],
 
 def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128, hidden_dim=128, eps=1e-6,
                    alpha=None, s_x=None, s_qkv=None, s_out=None, dropout_ratio=0.0, mask=None, attn_bias=None,
-                   quantize=True, grad_scales=None, fp8_wgrad=()):
+                   quantize=True, grad_scales=None, fp8_wgrad=(), attention="dense", pv_scale=10.04, ssc_k=3,
+                   dsc_k=-3):
     """Layer output [T, E] (float64, differentiable w.r.t. x and every
     parameter tensor in ``params``).  ``s_*`` = None with ``quantize`` keeps
     that stage in full precision; ``quantize=False`` disables every
     quantizer.  ``grad_scales``: {"output_projection": s, "uvqk_projection":
     s} -- the e5m2 gradient scale of each projection whose dgrad runs in
     FP8; ``fp8_wgrad``: the sites among those whose weight gradient is the FP8
-    product of the e4m3 activation (at s_x / s_out) and the e5m2 gradient."""
+    product of the e4m3 activation (at s_x / s_out) and the e5m2 gradient;
+    ``attention``: "dense" (the float64 attention and its exact gradient on
+    the quantized V/Q/K) or "production" (the FP8 P.V forward at
+    ``pv_scale`` and the full-FP8 backward at ``ssc_k`` / ``dsc_k``; needs
+    ``s_qkv``)."""
     gs = grad_scales or {}
     H, Dq, Dv = num_heads, attn_dim, hidden_dim
     nu = H * Dv
@@ -124,8 +184,16 @@ def hstu_layer_ref(x, params, lengths, max_seq_len, *, num_heads=4, attn_dim=128
     q = vqk[:, nu:nu + H * Dq].reshape(T, H, Dq)
     k = vqk[:, nu + H * Dq:].reshape(T, H, Dq)
     offs = orc.offsets_from_lengths(lengths)
-    attn = orc.hstu_mha_dense(max_seq_len, alpha, q, k, v, offs, attn_bias=attn_bias,
-                              dtype=torch.float64).reshape(T, H * Dv)
+    if attention == "production":
+        if not (quantize and s_qkv is not None):
+            raise ValueError("the production attention runs on e4m3 V/Q/K: give s_qkv with quantize=True")
+        attn = production_attention(q, k, v, s_qkv, offs, max_seq_len, alpha, attn_bias=attn_bias,
+                                    pv_scale=pv_scale, ssc_k=ssc_k, dsc_k=dsc_k).reshape(T, H * Dv)
+    elif attention == "dense":
+        attn = orc.hstu_mha_dense(max_seq_len, alpha, q, k, v, offs, attn_bias=attn_bias,
+                                  dtype=torch.float64).reshape(T, H * Dv)
+    else:
+        raise ValueError(f"attention {attention!r}: dense | production")
     attn = _ste(attn, bf(attn.detach()))
     y, _, _ = L.ln_mul_dropout_fwd(attn, u, p["output_norm_weight"], p["output_norm_bias"], eps,
                                    dropout_ratio=dropout_ratio, mask=mask, silu_u=True, concat_u=True,

@@ -86,18 +86,27 @@ def test_bwd_bf16(hip_lib, lengths, D):
         _check_bf16(got.float().cpu() / scale, ref / scale, f"{name} bf16 D={D} L={lengths}")
 
 
-def test_bwd_deterministic(hip_lib):
+@pytest.mark.parametrize("mode", ["causal", "bias", "targets_bias", "contextual_bias"])
+def test_bwd_deterministic(hip_lib, mode):
+    """Two backward calls give bitwise-equal dq, dk, dv and bias gradient:
+    no atomics anywhere (the bias gradient's per-block rows are summed in a
+    fixed order), with the causal mask and the generic ones."""
     ops = _ops()
-    lengths = [300, 129, 64]
-    H, D, N = 2, 128, 300
+    lengths = [300, 129, 64, 1, 700]
+    H, D, N = 2, 128, 700
     q, k, v, offs = _case(lengths, H, D)
     dout = torch.randn(q.shape, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    bias = None if mode == "causal" else orc.make_bias(H, 512, seed=2, std=0.3).to(DEV)
+    nt = torch.tensor([5, 1, 3, 1, 40], device=DEV) if mode == "targets_bias" else None
+    ctx = 7 if mode == "contextual_bias" else 0
     res = []
+    print(f"bwd determinism: {mode}", flush=True)
     for _ in range(2):
         dq, dk, dv = (torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3))
-        ops.triton_hstu_attention_bwd(dout, q.to(DEV), k.to(DEV), v.to(DEV), dq, dk, dv, offs.to(DEV), None,
-                                      N, 0.1, 0, 0, None, False, 0)
-        res.append((dq, dk, dv))
+        db = None if bias is None else torch.full(bias.shape, float("nan"), device=DEV)
+        ops.triton_hstu_attention_bwd(dout, q.to(DEV), k.to(DEV), v.to(DEV), dq, dk, dv, offs.to(DEV), nt,
+                                      N, 0.1, 0, ctx, None, False, 0, attn_bias=bias, dbias=db)
+        res.append((dq, dk, dv) + (() if db is None else (db,)))
     torch.cuda.synchronize()
     for a, b in zip(*res):
         assert not torch.isnan(a).any()
@@ -506,3 +515,44 @@ def test_full_fp8_backward_long_n(hip_lib):
         assert not torch.isnan(gt).any(), name
         e = orc.rel_l2(w, gt)
         assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+
+
+@pytest.mark.parametrize("dsc_k,ssc_k", [(-5, 3), (-3, 6), (-7, 1)])
+def test_full_fp8_backward_prescales(hip_lib, monkeypatch, dsc_k, ssc_k):
+    """Other P / dS pre-scale exponents (``DLRM_HSTU_FP8_BWD_FULL_{SSC,DSC}_K``;
+    production runs DSC_K = -5): against the oracle with the same casts,
+    relative L2 <= 1e-2, on inputs where the default dS scale (K = -3)
+    clamps some dS to +-448 in the oracle; the environment's K gives the
+    same bytes as the explicit argument."""
+    from oracle import hstu_bwd_fp8full_oracle as FO
+
+    ops = _ops()
+    H, D = 2, 128
+    lengths = [300, 77, 512, 129, 1, 64]
+    N = 600
+    alpha = 1.0 / D ** 0.5
+    q8, k8, v8, sq, sk, sv, offs, dout, y8, e8 = _full_fp8_case(lengths, H, D, 11, False)
+    bias = orc.make_bias(H, 256)
+    dev = [t.to(DEV) for t in (q8, k8, v8)]
+    scales = [s.to(DEV).contiguous() for s in (sq, sk, sv)]
+
+    def run(**kw):
+        g = [torch.full(q8.shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        db = torch.empty(bias.shape, dtype=torch.float32, device=DEV)
+        ops.triton_hstu_attention_bwd(dout.to(DEV), *dev, *g, offs.to(DEV), None, N, alpha, 0, 0, None, False,
+                                      0, *scales, attn_bias=bias.to(DEV), dbias=db, full_fp8=True, **kw)
+        torch.cuda.synchronize()
+        return [t.float().cpu() for t in g] + [db.cpu()]
+
+    print(f"full-FP8 bwd prescales: dsc_k={dsc_k} ssc_k={ssc_k}", flush=True)
+    got = run(ssc_k=ssc_k, dsc_k=dsc_k)
+    want = FO.full_fp8_bwd(N, alpha, q8, k8, v8, sq, sk, sv, offs, y8, e8, attn_bias=bias, ssc_k=ssc_k,
+                           dsc_k=dsc_k)
+    for name, gt, w in zip(("dq", "dk", "dv", "dbias"), got, want):
+        assert not torch.isnan(gt).any(), name
+        e = orc.rel_l2(w, gt)
+        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle at K = ({ssc_k}, {dsc_k})"
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL_SSC_K", str(ssc_k))
+    monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL_DSC_K", str(dsc_k))
+    for a, b in zip(got, run()):
+        assert torch.equal(a, b)

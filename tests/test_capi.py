@@ -53,11 +53,14 @@ def test_workspace_size():
     # dS tiles (8 KiB each) for the dQ kernel: 2 (ceil(N/128) + 1) (ceil(T/128) + B) per head, plus the
     # per-sequence tile prefix (int64 [B + 1])
     ds = a256((B + 1) * 8) + 2 * (4096 // 128 + 1) * ((1000 + 127) // 128 + B) * H * 8192
-    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 0) == sched + ds
-    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096, 0) == sched + 1000 * 4 * 128 * 2 + ds
+    dqb = a256((B + 1) * 8)  # the per-sequence dQ block prefix
+    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 0) == sched + dqb + ds
+    assert f(lib.HSTU_DTYPE_FP8_E4M3, 1000, B, H, 128, 4096, 0) == sched + 1000 * 4 * 128 * 2 + dqb + ds
     ext = a256(4 * (2 * 4096 + 256) * 4)  # pre-clamped bias rows, 2N+256 per head
-    part = a256(64 * 4 * (2 * 1024 - 1) * 4)
-    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 1024) == sched + ext + part + ds
+    # bias-gradient rows (one per 128-query dQ block and head, 2R - 1 floats), their 64 chunk sums
+    part = a256(((1000 + 127) // 128 + B) * H * (2 * 1024 - 1) * 4) + a256(64 * H * (2 * 1024 - 1) * 4)
+    dq_base = a256((B + 1) * 8)
+    assert f(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096, 1024) == sched + ext + part + dq_base + ds
     assert f(lib.HSTU_DTYPE_BF16, -1, B, H, 128, 4096, 0) == -1
     g = lib.fn("hstu_attn_fwd_workspace_bytes")
     assert g(lib.HSTU_DTYPE_BF16, 1000, B, H, 128, 4096) == sched
@@ -324,3 +327,30 @@ def test_outproj_ln_bwd_rejects_before_launch():
     assert g(D=256, ldx=256, ldu=256, lddx=256, lddu=256, ldm=256) == lib.HSTU_E_UNSUPPORTED
     assert g(x=X + 2) == lib.HSTU_E_UNSUPPORTED  # rows not 16-byte aligned
     assert g(ldg=520) == lib.HSTU_E_UNSUPPORTED  # gradient rows not 16-byte aligned
+
+
+def test_fp8_pv_forward_declines_long_sequences_before_launch():
+    """The FP8 P.V forward keeps a per-key table in LDS: past the N it can
+    hold (hstu_attn_fwd_fp8_pv_max_seq_len) it returns HSTU_E_UNSUPPORTED
+    before any device call, and the host's reason names it, so the op takes
+    the bf16-P forward instead of failing."""
+    import torch
+
+    import hstu_amd._lib as lib
+    from hstu_amd.hstu_attention import fp8_pv_fwd_reason
+
+    n_max = lib.fn("hstu_attn_fwd_fp8_pv_max_seq_len")()
+    assert 8192 <= n_max < 32768 and n_max % 64 == 0
+    f = lib.fn("hstu_attn_fwd_fp8_pv")
+    X = 4096  # fake device addresses: none of these calls may launch
+
+    def call(N, B=10):
+        return f(X, X, X, 512, 512, 512, X, X, X, 0, 0, X, B, 4, 128, N, 0.1, None, 0, 0, None, 0, 10.04,
+                 X, 512, None, 0, 1000, None)
+
+    assert call(n_max + 1) == lib.HSTU_E_UNSUPPORTED
+    assert call(n_max + 1, B=0) == lib.HSTU_E_UNSUPPORTED
+    assert call(n_max, B=0) == 0
+    q = torch.zeros(4, 4, 128, dtype=torch.float8_e4m3fn)
+    assert "LDS" in fp8_pv_fwd_reason(q, None, 0, 0, n_max + 64)
+    assert fp8_pv_fwd_reason(q, None, 0, 0, n_max) is None

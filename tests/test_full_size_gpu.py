@@ -151,8 +151,11 @@ def test_config3_full_fp8_fwd_bwd(hip_lib):
     torch.testing.assert_close(full[4], first[4] + second[4], rtol=1e-4, atol=1e-6 * float(full[4].abs().max()))
 
 
-def test_config3_full_fp8_backward(hip_lib):
-    """Config 3 in full through the full-FP8 backward (dO quantized to e4m3 in
+@pytest.mark.parametrize("dsc_k", [-3, -5])
+def test_config3_full_fp8_backward(hip_lib, dsc_k):
+    """Config 3 in full through the full-FP8 backward, at the reference's
+    default dS pre-scale (K_DSC = -3) and its production one (-5,
+    ``yambda_5b.gin:3799``) (dO quantized to e4m3 in
     pow2 (sequence, head, 32-token) blocks inside the op, e4m3 P and dS, five
     e4m3 MFMAs).  Sampled sequences incl. the longest (4096):
 
@@ -182,7 +185,7 @@ def test_config3_full_fp8_backward(hip_lib):
         db = torch.empty_like(b)
         print(f"config 3 full-FP8 bwd: {len(lens)} sequences, T={int(np.sum(lens))}", flush=True)
         ops.triton_hstu_attention_bwd(sel(dout).to(DEV), *dev[:3], *g, o, None, N, alpha, 0, 0, None, False, 0,
-                                      *dev[3:], attn_bias=b, dbias=db, full_fp8=True)
+                                      *dev[3:], attn_bias=b, dbias=db, full_fp8=True, dsc_k=dsc_k)
         torch.cuda.synchronize()
         return [t.float().cpu() for t in g] + [db.cpu()]
 
@@ -199,7 +202,7 @@ def test_config3_full_fp8_backward(hip_lib):
     y8, e8 = DO.quantize_do_e4m3_blk(dout[rows], sub_offs, N)
     args = (N, alpha, q8[rows], k8[rows], v8[rows], sq[rows], sk[rows], sv[rows], sub_offs, y8, e8)
     batch_max = (float(sq.abs().max()), float(sk.abs().max()))
-    want_full = FO.full_fp8_bwd(*args, attn_bias=bias, max_scales=batch_max)
+    want_full = FO.full_fp8_bwd(*args, attn_bias=bias, max_scales=batch_max, dsc_k=dsc_k)
     exact = orc.hstu_mha_bwd_closed_form(N, alpha, *(orc.dequantize(x[rows], s[rows]) for x, s in
                                                      ((q8, sq), (k8, sk), (v8, sv))),
                                          sub_offs, dout[rows].double(), attn_bias=bias)
@@ -213,7 +216,7 @@ def test_config3_full_fp8_backward(hip_lib):
             f"{name}: rel L2 {e2:.3e}, SNR {snr:.1f} dB, max {m:.3e} vs the float64 backward")
 
     sub = run(sub_len, rows)
-    want_sub = FO.full_fp8_bwd(*args, attn_bias=bias)
+    want_sub = FO.full_fp8_bwd(*args, attn_bias=bias, dsc_k=dsc_k)
     for name, gt, w in zip(("dq", "dk", "dv", "dbias"), sub, want_sub):
         e = orc.rel_l2(w, gt)
         assert e <= 1e-2, f"sub-batch {name}: rel L2 {e:.3e} vs the full-FP8 oracle"
@@ -379,3 +382,126 @@ def test_output_block_config3_tokens(hip_lib, monkeypatch):
     for k, full in ((2, dw), (3, db)):
         two = halves[0][k] + halves[1][k]
         torch.testing.assert_close(full, two, rtol=1e-4, atol=1e-5 * float(full.abs().max()))
+
+
+def test_config3_full_fp8_backward_deterministic(hip_lib):
+    """The production backward at config 3 (dO block quantizer, full-FP8
+    dK/dV and dQ with the bias gradient, DSC_K = -5) run twice on the same
+    inputs: dq, dk, dv and dbias bitwise equal."""
+    ops = _ops()
+    lengths, (q8, k8, v8), (sq, sk, sv), bias, dout = _cfg3_inputs()
+    N, alpha = 4096, 1.0 / 128 ** 0.5
+    offs = orc.offsets_from_lengths(lengths).to(DEV)
+    dev = [t.to(DEV).contiguous() for t in (q8, k8, v8, sq, sk, sv)]
+    b, do = bias.to(DEV), dout.to(DEV)
+    res = []
+    for i in range(2):
+        print(f"config 3 full-FP8 bwd determinism: call {i}", flush=True)
+        g = [torch.full(q8.shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        db = torch.full_like(b, float("nan"))
+        ops.triton_hstu_attention_bwd(do, *dev[:3], *g, offs, None, N, alpha, 0, 0, None, False, 0, *dev[3:],
+                                      attn_bias=b, dbias=db, full_fp8=True, dsc_k=-5)
+        res.append(g + [db])
+    torch.cuda.synchronize()
+    for name, x, y in zip(("dq", "dk", "dv", "dbias"), *res):
+        assert torch.isfinite(x).all(), name
+        assert torch.equal(x, y), f"{name} differs between two calls"
+
+
+def test_config5_production_layer_as_benched(hip_lib, monkeypatch):
+    """BASELINE config 5 at config 3 shapes exactly as ``bench.py``'s layer line
+    runs it (the reference's production configuration, yambda_5b.gin:221-268,
+    2104, 3293-3319, 3799): the FP8 P.V forward (DLRM_HSTU_FP8_FWD_PV=1), the
+    full-FP8 attention backward at DSC_K = -5, e5m2 dgrads, FP8 wgrads, the
+    output projection's dgrad fused into the LN * U * dropout backward,
+    calibrated per-layer scale states, dropout 0.3 with the 16-bit mask, the
+    relative-position bias.  After the bench's warm-up calls (the scale
+    calibration and the gradient sites' warm-up):
+
+    * the full batch's step: sampled sequences incl. the longest against the
+      layer oracle with the same casts (``attention="production"``, the
+      frozen activation scales, the published gradient scales): out <= 1.5e-2,
+      dx <= 3e-2 relative L2;
+    * a step on the sampled sequences alone: out, dx, every parameter
+      gradient and the bias gradient against the same oracle: <= 1.5e-2 /
+      3e-2."""
+    import hstu_amd
+    from hstu_amd import bwd_fp8
+    from hstu_amd import fp8 as F
+    from oracle import hstu_layer_oracle as LO
+    from oracle import hstu_ln_oracle as L
+
+    monkeypatch.setenv("DLRM_HSTU_FP8_FWD_PV", "1")
+    lengths = orc.lengths_for_config(3)
+    T, N, E, seed, p = 162251, 4096, 512, 7, 0.3
+    offs = orc.offsets_from_lengths(lengths)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    dy = torch.randn(T, E, generator=g).to(torch.bfloat16)
+    params = LO.make_layer_params(E, seed=4)
+    bias = orc.make_bias(4, 1024)
+    cfg = bwd_fp8.Fp8BackwardConfig(enabled=True, uvqk=True, uvqk_wgrad_fp8t=True, out_wgrad_fp8=True,
+                                    outproj_lnmd_fused=True, attn_full_fp8=True, attn_ssc_k=3, attn_dsc_k=-5)
+    bwd_fp8.reset_sites()
+    states = {n: torch.zeros(F.fp8_scale_state_size(), device=DEV) for n in ("in", "qkv", "out")}
+    pd = {k: v.to(DEV).requires_grad_(True) for k, v in params.items()}
+    bd = bias.to(DEV).requires_grad_(True)
+
+    def run(lens, rows, tag):
+        print(f"production layer: {tag}, {len(lens)} sequences, T={int(np.sum(lens))}", flush=True)
+        sel = (lambda t: t) if rows is None else (lambda t: t[rows])
+        for t in [*pd.values(), bd]:
+            t.grad = None
+        xd = sel(x).to(DEV).requires_grad_(True)
+        out = hstu_amd.hstu_layer(xd, orc.offsets_from_lengths(lens).to(DEV), N, pd, dropout_ratio=p,
+                                  training=True, attn_bias=bd, seed=seed, fp8_backward=cfg, dropout_mask16=True,
+                                  fp8_input_scale=states["in"], fp8_qkv_scale=states["qkv"],
+                                  fp8_output_scale=states["out"])
+        out.backward(sel(dy).to(DEV))
+        torch.cuda.synchronize()
+        grads = {k: v.grad.float().cpu() for k, v in pd.items()}
+        grads["attn_bias"] = bd.grad.float().cpu()
+        return out.detach().cpu(), xd.grad.cpu(), grads
+
+    try:
+        for i in range(F.CALIBRATION_STEPS + 1):       # the bench's warm-up calls
+            run(lengths, None, f"warm-up {i}")
+        assert all(F.scale_ready(st) for st in states.values())
+        out, dx, _ = run(lengths, None, "production step")
+        sites = {s: bwd_fp8.find_site(s, layer=0) for s in ("output_projection", "uvqk_projection")}
+        scales = {s: float(st.scale) for s, st in sites.items()}
+        assert all(v > 0 for v in scales.values()), scales
+        order = np.argsort(lengths)
+        sample = sorted({int(order[-1]), int(order[len(order) // 2]), int(order[0])})
+        assert int(max(lengths[sample])) == 4096
+        rows = torch.cat([torch.arange(int(offs[b]), int(offs[b + 1])) for b in sample])
+        sub_len = lengths[sample]
+        sub_out, sub_dx, sub_g = run(sub_len, rows, "sampled sequences alone")
+        assert all(float(sites[s].scale) == v for s, v in scales.items())
+    finally:
+        bwd_fp8.reset_sites()
+    s_x, s_qkv, s_out = (float(states[n][0]) for n in ("in", "qkv", "out"))
+
+    def oracle(mask):
+        xr = x[rows].double().requires_grad_(True)
+        pr = {k: v.double().requires_grad_(True) for k, v in params.items()}
+        br = bias.double().requires_grad_(True)
+        ref = LO.hstu_layer_ref(xr, pr, sub_len, N, s_x=s_x, s_qkv=s_qkv, s_out=s_out, dropout_ratio=p, mask=mask,
+                                attn_bias=br, quantize=True, grad_scales=scales,
+                                fp8_wgrad=("uvqk_projection", "output_projection"), attention="production",
+                                pv_scale=10.04, ssc_k=3, dsc_k=-5)
+        ref.backward(dy[rows].double())
+        return ref.detach(), xr.grad, {**{k: t.grad for k, t in pr.items()}, "attn_bias": br.grad}
+
+    # the full batch's step: the sampled rows carry their global dropout rows
+    ref, ref_dx, _ = oracle(L.dropout_mask_rows(rows.numpy(), 512, 3, p, seed, True))
+    e_out, e_dx = orc.rel_l2(ref, out[rows].double()), orc.rel_l2(ref_dx, dx[rows].double())
+    print(f"full batch, sampled rows: out rel L2 {e_out:.3e}, dx rel L2 {e_dx:.3e}", flush=True)
+    assert e_out <= 1.5e-2 and e_dx <= 3e-2, (e_out, e_dx)
+    # the sub-batch's step: its rows are 0 .. T_sub - 1 for the dropout mask
+    ref, ref_dx, ref_g = oracle(L.dropout_mask(int(np.sum(sub_len)), 512, 3, p, seed, True))
+    errs = {"out": orc.rel_l2(ref, sub_out.double()), "dx": orc.rel_l2(ref_dx, sub_dx.double())}
+    errs.update({f"d{k}": orc.rel_l2(r, sub_g[k].double()) for k, r in ref_g.items()})
+    print("sub-batch: " + ", ".join(f"{k} {v:.3e}" for k, v in errs.items()), flush=True)
+    assert errs["out"] <= 1.5e-2, errs
+    assert all(v <= 3e-2 for k, v in errs.items() if k != "out"), errs

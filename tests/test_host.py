@@ -180,3 +180,86 @@ def test_scale_state_known_without_device_reads():
     assert F.scale_ready(buf) and buf._version == v
     buf.zero_()                                   # reset elsewhere
     assert not F.scale_ready(buf)
+
+
+@pytest.mark.parametrize("bad", [0.0, -1.0, float("inf"), float("nan")])
+def test_one_element_scale_needs_finite_positive_value(bad):
+    """A one-element scale is usable only once finite and > 0 (the reference's
+    activation_scale_value, triton_fp8.py:429-442): a zero buffer runs bf16
+    and is calibrated, then ready; the value is read once per version."""
+    from hstu_amd import fp8 as F
+
+    s = torch.full((1,), bad)
+    assert not F.scale_ready(s)
+    F.calibrate_scale_buffer(s, torch.tensor([-2.0, 1.0]))
+    assert F.scale_ready(s) and float(s[0]) > 0
+    assert F.scale_ready(torch.full((1, 1), 0.25))
+    assert not F.scale_ready(torch.zeros(1, 1))
+
+
+def test_scale_record_is_per_tensor_object():
+    """A new tensor on a recycled storage address does not inherit another
+    tensor's record: the record holds the tensor as a weak reference."""
+    from hstu_amd import fp8 as F
+
+    a = torch.full((1,), 0.5)
+    assert F.scale_ready(a)
+    F._known[F._key(a)] = (a._version, 1, __import__("weakref").ref(torch.zeros(1)))
+    a.zero_()
+    assert not F.scale_ready(a)
+
+
+@pytest.mark.parametrize("amaxes,margin", [([2.0, 3.3, 0.7, 1.1], 1.5), ([1e-3, 7.77, 5.0, 1.0], 1.25),
+                                           ([0.123456, 0.2, 0.3, 0.1], 1.5)])
+def test_frozen_scale_bits_follow_reference_expression(amaxes, margin):
+    """The frozen scale is the reference's fp32 expression
+    ``history.amax() * margin / 448`` (triton_fp8.py:737-739) bit for bit,
+    and a one-element scale ``amax * margin / 448`` (:724-727)."""
+    from hstu_amd import fp8 as F
+
+    buf = torch.zeros(F.fp8_scale_state_size())
+    for a in amaxes[: F.CALIBRATION_STEPS]:
+        F.calibrate_scale_buffer(buf, torch.tensor([a, -a / 2]), margin=margin)
+    hist = torch.tensor(amaxes[: F.CALIBRATION_STEPS], dtype=torch.float32)
+    want = hist.amax() * margin / 448.0
+    assert torch.equal(buf[0], want)
+    one = torch.zeros(1)
+    F.calibrate_scale_buffer(one, torch.tensor([amaxes[1]]), margin=margin)
+    assert torch.equal(one[0], torch.tensor(amaxes[1], dtype=torch.float32) * margin / 448.0)
+
+
+def test_uqvk_kernel_reason_and_torch_path():
+    """hstu_compute_uqvk(kernel=TRITON) declines what the LayerNorm kernel and
+    the bf16 GEMM do not serve (host tensors here) and runs the torch ops,
+    equal to the reference's PyTorch composition."""
+    import torch.nn.functional as TF
+
+    from hstu_amd import HammerKernel
+    from hstu_amd.hstu_preprocess import hstu_compute_uqvk, uqvk_kernel_reason
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 512, generator=g)
+    nw, nb = torch.randn(512, generator=g), torch.randn(512, generator=g)
+    W, b = torch.randn(512, 2048, generator=g) * 0.05, torch.randn(2048, generator=g)
+    assert "device" in uqvk_kernel_reason(x, nw, nb, W, b)
+    u, q, k, v = hstu_compute_uqvk(x, nw, nb, 1e-6, 4, 128, 128, W, b, kernel=HammerKernel.TRITON)
+    uvqk = torch.addmm(b, TF.layer_norm(x, (512,), nw, nb, 1e-6), W)
+    assert torch.equal(u, TF.silu(uvqk[:, :512])) and torch.equal(v.reshape(5, 512), uvqk[:, 512:1024])
+    assert torch.equal(q.reshape(5, 512), uvqk[:, 1024:1536]) and torch.equal(k.reshape(5, 512), uvqk[:, 1536:])
+
+
+def test_residual_link_binds_the_preprocess_input():
+    """The output block uses a ResidualLink only for the x its preprocess
+    forward bound: another tensor, or the same one written in place since,
+    gets its residual gradient returned the ordinary way."""
+    from hstu_amd.hstu_linear import ResidualLink
+
+    x = torch.zeros(4, 8)
+    link = ResidualLink()
+    assert not link.bound_to(x)
+    link.bind(x)
+    assert link.bound_to(x) and not link.bound_to(x.clone()) and not link.bound_to(x.view(8, 4))
+    x.add_(1.0)
+    assert not link.bound_to(x)
+    link.grad = torch.ones(1)
+    assert link.take() is not None and link.take() is None
