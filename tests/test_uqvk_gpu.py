@@ -6,8 +6,10 @@ gradient and the LayerNorm backward (reference ``ops/hstu_compute.py:86-144,
 
 Small sizes: against the float64 composition ``F.layer_norm`` -> ``addmm``
 -> split -> ``silu`` (the reference's PyTorch path) on the same bf16 inputs,
-forward and backward, ``assert_close(rtol=1e-2, atol=1e-2)`` and relative L2
-<= 1e-2.  Config 2 and config 3 token counts: against the same composition
+forward and backward: relative L2 <= 1e-2 for every output and gradient,
+``assert_close(rtol=1e-2, atol=1e-2)`` for the row-wise ones (u, q, k, v,
+dx), and max|err| <= 2e-2 max|ref| for the parameter gradients (sums over
+the tokens of bf16 products).  Config 2 and config 3 token counts: against the same composition
 in float32 on the device, relative L2 <= 1e-2 for u, q, k, v and every
 gradient.
 """
@@ -65,9 +67,13 @@ def test_uqvk_small_vs_oracle(hip_lib, T):
     ref_o, ref_g = _run(_ref_uqvk, *(t.double() for t in (x, nw, nb, W, b)), [t.double() for t in douts])
     for name, r, g in zip(("u", "q", "k", "v", "dx", "dnorm_w", "dnorm_b", "dW", "db"), ref_o + ref_g,
                           got_o + got_g):
-        torch.testing.assert_close(g.double().cpu(), r, rtol=1e-2, atol=1e-2, msg=name)
+        g = g.double().cpu()
+        if name in ("u", "q", "k", "v", "dx"):
+            torch.testing.assert_close(g, r, rtol=1e-2, atol=1e-2, msg=name)
+        else:  # sums over the tokens of bf16 products: relative to the largest entry
+            assert float((g - r).abs().max()) <= 2e-2 * float(r.abs().max()), name
         if r.norm() > 0:
-            assert _rel_l2(r, g.cpu()) <= 1e-2, name
+            assert _rel_l2(r, g) <= 1e-2, name
 
 
 @pytest.mark.parametrize("cfg", [2, 3])
