@@ -107,7 +107,8 @@ def causal_pairs(lengths) -> int:
 class Workload:
     """Device-resident inputs and the raw C-ABI argument tuples of one step."""
 
-    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True, full_fp8=False, fp8_pv=False):
+    def __init__(self, torch, lib, lengths, H, D, N, dtype, seed=0, bias=True, full_fp8=False, fp8_pv=False,
+                 per_tensor=False):
         self.torch = torch
         self.full_fp8 = full_fp8 and dtype == "fp8"
         self.fp8_pv = fp8_pv and dtype == "fp8"
@@ -128,7 +129,13 @@ class Workload:
                 amax = x.abs().amax(dim=-1, keepdim=True)
                 s = torch.where(amax > 0, amax / 448.0, torch.full_like(amax, 1 / 448.0))
                 return (x / s).clamp(-448, 448).to(torch.float8_e4m3fn), s.squeeze(-1).contiguous()
-            (self.q, self.sq), (self.k, self.sk), (self.v, self.sv) = quant(q), quant(k), quant(v)
+            if per_tensor:
+                # the reference's qkv_scale: one scale for q, k and v
+                s = (torch.stack([x.abs().amax() for x in (q, k, v)]).amax() / 448.0).reshape(1)
+                (self.q, self.k, self.v) = ((x / s).clamp(-448, 448).to(torch.float8_e4m3fn) for x in (q, k, v))
+                self.sq = self.sk = self.sv = s.contiguous()
+            else:
+                (self.q, self.sq), (self.k, self.sk), (self.v, self.sv) = quant(q), quant(k), quant(v)
         else:
             self.q, self.k, self.v = (x.to(torch.bfloat16) for x in (q, k, v))
             self.sq = self.sk = self.sv = None
@@ -150,7 +157,7 @@ class Workload:
         stream = torch.cuda.current_stream().cuda_stream
         dt = 1 if self.fp8 else 0
         sp = lambda t: None if t is None else t.data_ptr()  # noqa: E731
-        srs, shs = (H, 1) if self.fp8 else (0, 0)
+        srs, shs = (H, 1) if self.fp8 and not per_tensor else (0, 0)
         fws_bytes = lib.fn("hstu_attn_fwd_workspace_bytes")(dt, T, B, H, D, N)
         self.fws = torch.empty(max(fws_bytes, 1), dtype=torch.uint8, device=dev)
         self.fwd_args = (dt, self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), H * D, H * D, H * D,
@@ -714,6 +721,18 @@ def main():
                                           "e4m3-input backward on the bf16 dO (bf16 dS tiles, bf16 MFMAs for dV, "
                                           "dK, dQ)"}
         del wd
+        torch.cuda.empty_cache()
+    if not args.headline_only and full_fp8:
+        wt = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=True, fp8_pv=fp8_pv, per_tensor=True)
+        wall_t, st_t, parts_t = wt.run(args.steps, max(args.warmup, 2), flush)
+        vt = wt.flops("step") / (st_t["median"] * 1e-3) / 1e12
+        res["per_tensor_no_bias"] = {
+            "value": round(vt, 2), "unit": "TFLOP/s", "ms_per_step": round(st_t["median"], 4),
+            "pct_fp8_peak": round(100 * vt / PEAK_TFLOPS["fp8"], 2),
+            "kernels_ms": {k: round(v, 4) for k, v in parts_t.items()},
+            "note": "the reference's production call exactly: one per-tensor qkv_scale for q, k and v "
+                    "(hstu_flydsl_mha.py:2392-2395), no bias, the headline's FP8 P.V forward and full-FP8 backward"}
+        del wt
         torch.cuda.empty_cache()
     if not args.headline_only:
         wn = Workload(torch, lib, lengths, H, D, N, "fp8", bias=False, full_fp8=full_fp8, fp8_pv=fp8_pv)

@@ -2182,8 +2182,17 @@ __device__ __forceinline__ uint32_t buf_ldu8(BufRsrc r, uint32_t voff) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, voff, 0, 0);
 }
 
-template <bool BIAS>
+// Scale modes: kScalesPerToken ([T, H] scales), kScalesPerTensor (one scale
+// per tensor: the query scale, and so the score's exp2 factor and dS8k's
+// factor, is a per-block constant and no query scales are staged),
+// kScalesShared (one scale tensor for q, k and v, the reference's qkv_scale:
+// also the dK and dQ casts of dS are the same bytes, so each score is cast
+// twice (P8, dS8) instead of three times).
+enum ScaleMode { kScalesPerToken = 0, kScalesPerTensor = 1, kScalesShared = 2 };
+
+template <bool BIAS, int SM>
 __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnParams p) {
+  constexpr bool PT = SM != kScalesPerToken;
   using C = F8Bwd;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   SeqCtx sc;
@@ -2228,7 +2237,10 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
   const float ikp = 1.0f / kp, ln2_kp = kLn2 * ikp;
   const float ck = -p.alpha * kLog2e * sk;                    // times s_q: exp2 argument factor
   const float an = sv * nq * p.ds8_scale * p.inv_n * ikp;     // times s_q: dS8k factor
-  const float bn = sv * sk * nk * p.ds8_scale * p.inv_n * ikp;  // dS8q factor
+  const float bn = sv * sk * nk * p.ds8_scale * p.inv_n * ikp;  // dS8q factor (with PT also dS8k's)
+  // one query scale: the exp2 argument and dS8k factors are constants
+  const float sq_pt = PT ? p.q_scale[0] : 0.f;
+  const float ck_pt = PT ? ck * sq_pt : 0.f, an_pt = PT ? an * sq_pt : 0.f;
 
   f32x4 dvt[8], dkt[8];
 #pragma unroll
@@ -2259,7 +2271,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
       buf_to_lds<16>(do_rsrc, st + C::DO_OFF + (8 * wave + 32 * i) * 128, d_voff[i & 1],
                      (uint32_t)(m0 + 32 * i) * dors);
     }
-    if (wave < 2)
+    if (!PT && wave < 2)
       buf_to_lds<4>(sq_rsrc, st + C::SQ_OFF + 256 * wave, (uint32_t)lane * s_step, (uint32_t)(m0 + 64 * wave) * s_step);
     if (BIAS) {
       buf_to_lds<4>(b_rsrc, st + C::B_OFF + 256 * wave, (uint32_t)(64 * wave + lane) * 4u,
@@ -2321,12 +2333,12 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
       uint32_t dq8[4];
 #pragma unroll
       for (int qs = 0; qs < 4; ++qs) {
-        const f32x4 sq4 = lds_ldf4(buf + C::SQ_OFF + (64 * hf + 16 * qs + 4 * g) * 4);
+        const f32x4 sq4 = PT ? f32x4{0.f, 0.f, 0.f, 0.f} : lds_ldf4(buf + C::SQ_OFF + (64 * hf + 16 * qs + 4 * g) * 4);
         const float* bl = bias_lds + bias_lane + 64 * hf + 16 * qs;
         float pv[4], dkv[4], dqv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float tt = s[qs][r] * (ck * sq4[r]);
+          float tt = PT ? s[qs][r] * ck_pt : s[qs][r] * (ck * sq4[r]);
           if constexpr (BIAS) tt += BCONST ? bconst : bl[r];
           const float sgk = __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(tt), ikp, ikp));
           float pval = tt * sgk;
@@ -2338,12 +2350,13 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
           }
           // saturated to +-448 by the conversion (MODE.FP16_OVFL)
           pv[r] = pval;
-          dkv[r] = dsv * (an * sq4[r]);
           dqv[r] = dsv * bn;
+          // shared scale: an s_q = bn (s_q = s_k, the same normaliser)
+          dkv[r] = SM == kScalesShared ? dqv[r] : dsv * (PT ? an_pt : an * sq4[r]);
         }
         pd[4 * hf + qs] = pack_fp8x4(pv[0], pv[1], pv[2], pv[3]);
-        dk8[4 * hf + qs] = pack_fp8x4(dkv[0], dkv[1], dkv[2], dkv[3]);
         dq8[qs] = pack_fp8x4(dqv[0], dqv[1], dqv[2], dqv[3]);
+        dk8[4 * hf + qs] = SM == kScalesShared ? dq8[qs] : pack_fp8x4(dkv[0], dkv[1], dkv[2], dkv[3]);
       }
       // the dQ kernel's operand, streamed out (read once, much later)
       __builtin_nontemporal_store(u32x4{dq8[0], dq8[1], dq8[2], dq8[3]}, (u32x4*)(dst + hf * 64 * 16));
@@ -3542,8 +3555,14 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
       hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
                          attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
     }
-    e = has_bias ? launch(hstu_bwd_f8_dkdv_kernel<true>, F8Bwd::LDS, 2 * grid, p, stream, F8Bwd::NT)
-                 : launch(hstu_bwd_f8_dkdv_kernel<false>, F8Bwd::LDS, 2 * grid, p, stream, F8Bwd::NT);
+    // one scale tensor for q and k (the same device address): the shared mode
+    const int sm = per_token ? kScalesPerToken : (q_scale == k_scale ? kScalesShared : kScalesPerTensor);
+#define HSTU_F8_DKDV(BB, SS) launch(hstu_bwd_f8_dkdv_kernel<BB, SS>, F8Bwd::LDS, 2 * grid, p, stream, F8Bwd::NT)
+#define HSTU_F8_DKDV_B(SS) (has_bias ? HSTU_F8_DKDV(true, SS) : HSTU_F8_DKDV(false, SS))
+    e = sm == kScalesPerToken ? HSTU_F8_DKDV_B(kScalesPerToken)
+                              : (sm == kScalesShared ? HSTU_F8_DKDV_B(kScalesShared) : HSTU_F8_DKDV_B(kScalesPerTensor));
+#undef HSTU_F8_DKDV_B
+#undef HSTU_F8_DKDV
     if (e != hipSuccess) return (int)e;
   }
   if (parts & kBwdDq) {

@@ -443,7 +443,7 @@ def _full_fp8_case(lengths, H, D, seed, per_tensor):
     return q8, k8, v8, sq, sk, sv, offs, dout, y.view(torch.float8_e4m3fn), e8
 
 
-@pytest.mark.parametrize("per_tensor", [False, True])
+@pytest.mark.parametrize("per_tensor", [False, True, "shared"])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_full_fp8_backward(hip_lib, per_tensor, with_bias):
     """The full-FP8 backward (e4m3 dO in pow2 blocks, e4m3 P and dS, five
@@ -463,7 +463,11 @@ def test_full_fp8_backward(hip_lib, per_tensor, with_bias):
     q8, k8, v8, sq, sk, sv, offs, dout, y8, e8 = _full_fp8_case(lengths, H, D, 7, per_tensor)
     bias = orc.make_bias(H, 256) if with_bias else None
     dev = [t.to(DEV) for t in (q8, k8, v8)]
-    if per_tensor:
+    if per_tensor == "shared":  # one scale tensor for q, k and v (the reference's qkv_scale)
+        one = torch.tensor([float(sq[0, 0])], device=DEV)
+        scales = [one, one, one]
+        sq = sk = sv = torch.full_like(sq, float(sq[0, 0]))
+    elif per_tensor:
         scales = [torch.tensor([float(s[0, 0])], device=DEV) for s in (sq, sk, sv)]
     else:
         scales = [s.to(DEV).contiguous() for s in (sq, sk, sv)]
