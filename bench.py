@@ -69,6 +69,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup-seconds", type=float, default=0.5,
+                    help="untimed warm-up also lasts at least this long (GPU clocks reach their steady state "
+                         "after ~0.2 s of continuous work; a step timed before that runs ~5-10%% slower)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-bf16", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
@@ -96,6 +99,24 @@ PROD_SSC_K, PROD_DSC_K = 3, -5
 
 def lengths_cfg3():
     return np.random.default_rng(0).zipf(1.2, 128).clip(32, 4096)
+
+
+# minimum seconds of untimed warm-up before each timed region (set from --warmup-seconds)
+WARMUP_SECONDS = 0.5
+
+
+def warm(torch, fn, steps):
+    """``steps`` untimed calls of fn(), continued until at least
+    WARMUP_SECONDS have passed on the host clock with the GPU busy."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < steps or time.perf_counter() - t0 < WARMUP_SECONDS:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 
 
 def causal_pairs(lengths) -> int:
@@ -229,9 +250,7 @@ class Workload:
         256 MB MALL, then HIP events on the launch stream bracket the step and
         each of its three entry points."""
         torch = self.torch
-        for _ in range(warmup):
-            self.step()
-        torch.cuda.synchronize()
+        warm(torch, self.step, warmup)
         t0 = time.perf_counter()
         for _ in range(steps):
             self.step()
@@ -254,9 +273,7 @@ def _cold_events(torch, fn, steps, warmup, flush, marks=1):
     """Median / p10 / p90 ms of fn() with HIP events on the current stream,
     each call after ``flush()`` has evicted the caches (fn may record
     ``marks`` intermediate events through the list it is given)."""
-    for _ in range(warmup):
-        fn(None)
-    torch.cuda.synchronize()
+    warm(torch, lambda: fn(None), warmup)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(marks + 1)] for _ in range(steps)]
     for i in range(steps):
         flush()
@@ -616,7 +633,9 @@ def copy_calibration():
 
 
 def main():
+    global WARMUP_SECONDS
     args = parse()
+    WARMUP_SECONDS = max(0.0, args.warmup_seconds)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is designed, not built)"}))
@@ -688,8 +707,10 @@ def main():
                    "causal_pairs_per_head": w8.P, "attn_bias": True, "parallelism": "none (1 GPU)"},
         "timing": {"ms_per_step_median_cold": round(st["median"], 4), "p10": round(st["p10"], 4),
                    "p90": round(st["p90"], 4), "ms_per_step_back_to_back": round(wall_ms, 4),
+                   "warmup_seconds": WARMUP_SECONDS,
                    "method": "HIP events per step after a 512 MiB cache-evicting %s (CacheFlush); value uses the "
-                             "median" % args.flush},
+                             "median; each timed region follows >= warmup steps and >= warmup_seconds of untimed "
+                             "steps" % args.flush},
         "pct_fp8_peak": round(100 * value / PEAK_TFLOPS["fp8"], 2),
         "kernels_ms": {k: round(v, 4) for k, v in parts.items()},
         "kernels_tflops": {k: round(w8.flops(k) / (v * 1e-3) / 1e12, 1) for k, v in parts.items()},

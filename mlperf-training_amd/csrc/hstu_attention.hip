@@ -3014,8 +3014,12 @@ hipError_t ensure_lds(const void* fn) {
 hipError_t launch(void (*kernel)(AttnParams), int lds, int grid, AttnParams p, hipStream_t stream,
                   int threads = kThreads) {
   if (lds > kMaxLdsBytes) return hipErrorInvalidValue;
-  hipError_t e = ensure_lds((const void*)kernel);
-  if (e != hipSuccess) return e;
+  // a kernel with static LDS only (lds == 0) needs no dynamic limit; raising
+  // it to the whole CU would exceed what its static part leaves
+  if (lds > 0) {
+    hipError_t e = ensure_lds((const void*)kernel);
+    if (e != hipSuccess) return e;
+  }
   void* args[] = {&p};
   return hipLaunchKernel((const void*)kernel, dim3(grid), dim3(threads), args, (size_t)lds, stream);
 }
