@@ -104,6 +104,13 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __builtin_bit_
 // the same of the second 32).
 enum GemmFmt { kE4M3 = 0, kE5M2A = 1, kBF16 = 2 };
 
+// acc * s + b rounded after the multiply and after the add (no FMA), the
+// e4m3-output epilogue's order (k512_fp8_gemm.cu:13-17: "MUL THEN ADD").
+__device__ __forceinline__ float mul_then_add(float acc, float s, float b) {
+#pragma clang fp contract(off)
+  return acc * s + b;
+}
+
 template <bool E4M3_OUT, bool RESID, int FMT>
 __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -228,14 +235,15 @@ __global__ void __launch_bounds__(kThreads, 2) fp8_gemm_kernel(GemmParams p) {
     for (int ns = 0; ns < 4; ++ns) {
       const int n = n0 + wn + 16 * ns + 4 * g;
       float v[4];
+      {
+        const u32x2 b = p.bias ? bias[ns] : u32x2{0u, 0u};
+        const float bb[4] = {bf16_to_f32(b[0] & 0xffff), bf16_to_f32(b[0] >> 16), bf16_to_f32(b[1] & 0xffff),
+                             bf16_to_f32(b[1] >> 16)};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[ns][ms][r] * (sa[ms] * sw[ns][r]);
-      if (p.bias) {
-        const u32x2 b = bias[ns];
-        v[0] += bf16_to_f32(b[0] & 0xffff);
-        v[1] += bf16_to_f32(b[0] >> 16);
-        v[2] += bf16_to_f32(b[1] & 0xffff);
-        v[3] += bf16_to_f32(b[1] >> 16);
+        for (int r = 0; r < 4; ++r) {
+          const float sc = sa[ms] * sw[ns][r];
+          v[r] = E4M3_OUT ? mul_then_add(acc[ns][ms][r], sc, bb[r]) : acc[ns][ms][r] * sc + bb[r];
+        }
       }
       if (n < p.silu_end && n + 4 > p.silu_begin) {
 #pragma unroll
@@ -413,7 +421,10 @@ __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p
         const int n = n0 + wn + 16 * ns + 4 * g;
         float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = acc[ns][ms][r] * (sa[ms] * swv[ns][r]) + bv[ns][r];
+        for (int r = 0; r < 4; ++r) {
+          const float sc = sa[ms] * swv[ns][r];
+          v[r] = E4M3_OUT ? mul_then_add(acc[ns][ms][r], sc, bv[ns][r]) : acc[ns][ms][r] * sc + bv[ns][r];
+        }
         if (silu_any[ns]) {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
