@@ -66,6 +66,9 @@ struct GemmParams {
 #ifndef HSTU_GEMM_REGSTAGE
 #define HSTU_GEMM_REGSTAGE 1
 #endif
+#ifndef HSTU_GEMM_WIDE
+#define HSTU_GEMM_WIDE 1
+#endif
 constexpr int kBM = 128, kBN = 128, kBK = 128;
 constexpr int kPitch = kBK + 32;  // 160: conflict-free operand reads
 using GTile = DirectTile<128, kBK, kPitch>;  // 20 load instructions, 5 per wave
@@ -462,6 +465,279 @@ __global__ void __launch_bounds__(kWsThreads, 1) fp8_gemm_ws_kernel(GemmParams p
   }
 }
 
+// Persistent producer/consumer form, for N % 256 == 0, K % 256 == 0 and a
+// 64-column aligned SiLU range (every FP8 projection of the layer).  At
+// K = 512 the output dominates the HBM traffic, so the kernel is built to
+// keep the stores streaming under the MFMAs (the epilogue's VALU work itself
+// still runs between k-steps: its 128 accumulators per lane leave no
+// registers for a second tile).  On gfx9 a wave's loads and stores share one in-order counter
+// (vmcnt): a wave that stores a tile's output and then waits for a later
+// load waits for those stores to drain first.  So the waves that store never
+// load from global memory:
+//  * one workgroup per CU, 5 waves: a loader wave and 4 MFMA waves.  The
+//    loader only issues global -> LDS loads (buffer_load ... lds) into a
+//    3-stage ring, two k-steps ahead, and stages each tile's column scales,
+//    bias and row scales.  The MFMA waves only read LDS, issue MFMAs and run
+//    the epilogue; their stores are never waited for.  One s_barrier per
+//    k-step: the loader arrives once the step's loads have landed, the MFMA
+//    waves once they have read the previous stage.
+//  * workgroup tile 128 (M) x 256 (N); MFMA wave w owns all 128 rows and the
+//    64 columns [64 w, 64 w + 64): per 128-byte k-step 12 operand reads (24
+//    ds_read_b128) feed 32 v_mfma_f32_16x16x128_f8f6f4, issued
+//    operand-swapped (W rows as the A operand) so a lane's accumulators are
+//    output columns of one row.
+//  * W rows are placed in LDS in a permuted order (free: it is the source
+//    offset of each lane's load) so that the 16 accumulators a lane holds for
+//    one output row are whole 16-byte stores: bf16 columns 8 g .. 8 g + 7 and
+//    32 + 8 g .. 32 + 8 g + 7 of the wave's 64 (one store instruction writes
+//    64 contiguous bytes of each of 16 rows), e4m3 columns 16 g .. 16 g + 15.
+//  * XCD x walks the tile range [x * per_xcd, (x + 1) * per_xcd), numbered
+//    M-panel-major, so the N tiles of one A panel run close in time on one
+//    XCD and share its L2.
+// An LDS operand tile is R rows x 128 bytes with the 16-byte chunk c of row r
+// at position c ^ swz(r), swz(r) = ((r >> 1) & 7) ^ (((r >> 5) & 1) << 2): a
+// ds_read_b128 of 16 consecutive rows (one chunk each) hits 16 distinct bank
+// groups (measured conflict-free; (r & 7) ^ ((r >> 3) & 1) is not).  swz is
+// constant under r -> r + 64 and flips bit 2 under r -> r + 32, so the
+// operand rows 16 i + li read chunk g at (g ^ ((li >> 1) & 7)) ^ 4 ((i >> 1) & 1):
+// for odd i >> 1 the chunks g and g + 4 trade places.
+constexpr int kWideBN = 256;
+constexpr int kPcThreads = 320;  // 4 MFMA waves + the loader
+constexpr int kPcStages = 3;
+constexpr int kPcA = 128 * 128;          // A item: 128 rows x 128 bytes
+constexpr int kPcStage = kPcA + 256 * 128;  // + W item: 256 rows x 128 bytes = 48 KiB
+
+__device__ __forceinline__ int wide_swz(int r) { return ((r >> 1) & 7) ^ (((r >> 5) & 1) << 2); }
+
+// Column (within the wave's 64) of accumulator element e = 4 ns + r of lane
+// group g.
+template <bool E4M3_OUT>
+__device__ __forceinline__ int wide_col(int g, int e) {
+  if constexpr (E4M3_OUT) return 16 * g + e;
+  else return e < 8 ? 8 * g + e : 32 + 8 * g + (e - 8);
+}
+
+// v / s rounded to fp32 exactly as the division, from y = 1 / s (correctly
+// rounded): q0 = v y, r = v - q0 s (exact with the FMA), q = q0 + r y
+// (Markstein's correction, Handbook of Floating-Point Arithmetic sec. 4.7).
+// Non-finite q0 (v infinite or NaN, or v y overflowing) is kept as is.
+__device__ __forceinline__ float div_by(float v, float s, float y) {
+  const float q0 = v * y;
+  const float q = __builtin_fmaf(__builtin_fmaf(-q0, s, v), y, q0);
+  return __builtin_fabsf(q0) < __builtin_huge_valf() ? q : q0;
+}
+
+// Barriers without a memory fence (a fence would make the MFMA waves wait
+// for their own stores): the MFMA waves wait for their LDS reads only, the
+// loader for its loads up to the last VM outstanding ones.
+__device__ __forceinline__ void pc_barrier_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+template <int VM>
+__device__ __forceinline__ void pc_barrier_vm() {
+  static_assert(VM == 0 || VM == 48, "loader wait counts");
+  if constexpr (VM == 48) asm volatile("s_waitcnt vmcnt(48) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <bool E4M3_OUT, bool RESID, bool A_BF8>
+__global__ void __launch_bounds__(kPcThreads, 1) fp8_gemm_pc_kernel(GemmParams p, int per_xcd) {
+  __shared__ __attribute__((aligned(1024))) uint8_t stage[kPcStages][kPcStage];
+  // the current tile's column scales, bias and row scales
+  __shared__ __attribute__((aligned(16))) float col_sw[kWideBN];
+  __shared__ __attribute__((aligned(16))) uint16_t col_b[kWideBN];
+  __shared__ __attribute__((aligned(16))) float row_sa[kBM];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int xcd = (int)blockIdx.x & 7, gx = (int)gridDim.x >> 3;
+  const int total = p.tiles_m * p.tiles_n;
+  const int t0 = xcd * per_xcd + ((int)blockIdx.x >> 3);
+  const int t_end = min((xcd + 1) * per_xcd, total);
+  const int ntiles = t0 < t_end ? (t_end - t0 + gx - 1) / gx : 0;
+  const int nk = p.K >> 7;  // even, >= 2
+  const int S = ntiles * nk;  // k-steps of this workgroup
+  if (S == 0) return;
+
+  if (wave == 4) {
+    // ---------------- loader: LDS slot q = 64 i + lane of an item is row
+    // q >> 3, position q & 7, which holds chunk (q & 7) ^ swz(row)
+    uint32_t av[16], wv[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int q = 64 * i + lane, r = q >> 3;
+      av[i] = (uint32_t)r * (uint32_t)p.lda + (((q & 7) ^ wide_swz(r)) * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const int q = 64 * i + lane, j = q >> 3, jj = j & 15;
+      const int col = 64 * (j >> 6) + wide_col<E4M3_OUT>(jj >> 2, 4 * ((j >> 4) & 3) + (jj & 3));
+      wv[i] = (uint32_t)col * (uint32_t)p.ldw + (((q & 7) ^ wide_swz(j)) * 16);
+    }
+    const BufRsrc wrs = make_rsrc(p.W, (uint32_t)((int64_t)(p.N - 1) * p.ldw + p.K));
+    auto issue = [&](int s) {
+      const int t = t0 + (s / nk) * gx, kk = s - (s / nk) * nk;
+      const int mt = t / p.tiles_n, nt = t - mt * p.tiles_n;
+      const int m0 = mt * kBM, mrows = min(kBM, p.M - m0);
+      // rows past M read as zero (the range check covers the vector offset)
+      const BufRsrc ars = make_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)((mrows - 1) * p.lda + p.K));
+      uint8_t* st = stage[s % kPcStages];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) buf_to_lds<16>(ars, st + 1024 * i, av[i], kk * 128);
+      const uint32_t wso = (uint32_t)(nt * kWideBN) * (uint32_t)p.ldw + kk * 128;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) buf_to_lds<16>(wrs, st + kPcA + 1024 * i, wv[i], wso);
+    };
+    issue(0);
+    if (S > 1) {
+      issue(1);
+      pc_barrier_vm<48>();
+    } else {
+      pc_barrier_vm<0>();
+    }
+    // The tile's constants, also as LDS loads (the loader's only memory
+    // operations are LDS loads, so its waits count them exactly): column
+    // scales (replicated for a per-tensor scale), bias (zero without one) and
+    // row scales, read in the tile's epilogue, after barrier s + 1.
+    const BufRsrc swr = make_rsrc(p.w_scale, p.w_mode ? (uint32_t)p.N * 4u : 4u);
+    const BufRsrc bsr = make_rsrc(p.bias, p.bias ? (uint32_t)p.N * 2u : 0u);
+    const BufRsrc sar = make_rsrc(p.a_scale, p.a_mode ? (uint32_t)p.M * 4u : 4u);
+    for (int s = 0; s < S; ++s) {
+      // after barrier s: step s is readable, the stage of step s - 1 is free
+      const int tile_i = s / nk, kk = s - tile_i * nk;
+      if (kk == 0) {
+        const int t = t0 + tile_i * gx, mt = t / p.tiles_n, nt = t - mt * p.tiles_n;
+        const int n0 = nt * kWideBN, m0 = mt * kBM;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          buf_to_lds<4>(swr, (uint8_t*)col_sw + 256 * i, p.w_mode ? (uint32_t)(n0 + 64 * i + lane) * 4u : 0u, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) buf_to_lds<4>(bsr, (uint8_t*)col_b + 256 * i, (uint32_t)(n0 + 128 * i + 2 * lane) * 2u, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          buf_to_lds<4>(sar, (uint8_t*)row_sa + 256 * i, p.a_mode ? (uint32_t)min(m0 + 64 * i + lane, p.M - 1) * 4u : 0u, 0);
+      }
+      if (s + 2 < S) {
+        issue(s + 2);
+        pc_barrier_vm<48>();  // all but step s + 2's loads: step s + 1 and the constants
+      } else if (s + 1 < S) {
+        pc_barrier_vm<0>();
+      }
+    }
+    return;
+  }
+
+  // ---------------- MFMA waves
+  const int li = lane & 15, g = lane >> 4;
+  // chunks g and g + 4 of operand row li (rows 16 i + li with (i >> 1) even;
+  // odd: the two trade places)
+  const uint32_t a_rd0 = li * 128 + ((g ^ wide_swz(li)) * 16);
+  const uint32_t a_rd1 = li * 128 + (((g + 4) ^ wide_swz(li)) * 16);
+  const uint32_t w_rd0 = kPcA + 64 * wave * 128 + a_rd0, w_rd1 = kPcA + 64 * wave * 128 + a_rd1;
+
+  f32x4 acc[8][4];
+  // epilogue: lane holds C[m0 + 16 ms + li][n0 + 64 wave + wide_col(g, e)],
+  // e = 4 ns + r: the runs c0 + (0..7) (e < 8) and c1 + (0..7) (e >= 8).
+  // Stores (and residual loads) go through buffer resources bounded at the
+  // tile's valid rows: rows past M are dropped by the range check.
+  auto epilogue = [&](int m0, int n0) {
+    constexpr int ES = E4M3_OUT ? 1 : 2;
+    const int vrows = min(kBM, p.M - m0);
+    const BufRsrc crs = make_rsrc((uint8_t*)p.C + (int64_t)m0 * p.ldc * ES, (uint32_t)(vrows * p.ldc * ES));
+    const BufRsrc rrs = make_rsrc(RESID ? (const void*)(p.resid + (int64_t)m0 * p.ldr) : p.C,
+                                  RESID ? (uint32_t)(vrows * p.ldr * 2) : 0u);
+    const float os = E4M3_OUT ? p.out_scale[0] : 1.f;
+    const float oy = E4M3_OUT ? 1.f / os : 1.f;
+    const int cl0 = 64 * wave + (E4M3_OUT ? 16 * g : 8 * g);
+    const int cl1 = cl0 + (E4M3_OUT ? 8 : 32);
+    // SiLU on the wave's 64 columns or on none of them: the host takes this
+    // form only for a 64-column aligned [silu_begin, silu_end) (the U slice)
+    const int wc0 = n0 + 64 * wave;
+    const bool silu = wc0 >= p.silu_begin && wc0 < p.silu_end;
+#pragma unroll
+    for (int ms = 0; ms < 8; ++ms) {
+      const int r = 16 * ms + li;  // row within the tile
+      const float sa = row_sa[r];
+      float v[16];
+#pragma unroll
+      for (int run = 0; run < 2; ++run) {
+        const int cl = run ? cl1 : cl0, c = n0 + cl;
+        const f32x4 x0 = *(const f32x4*)(col_sw + cl), x1 = *(const f32x4*)(col_sw + cl + 4);
+        const u32x4 b = *(const u32x4*)(col_b + cl);
+        const float sw[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        float* o = v + 8 * run;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float bb = bf16_to_f32(e & 1 ? (uint16_t)(b[e >> 1] >> 16) : (uint16_t)(b[e >> 1] & 0xffff));
+          const float a = acc[ms][2 * run + (e >> 2)][e & 3];
+          o[e] = E4M3_OUT ? mul_then_add(a, sa * sw[e], bb) : a * (sa * sw[e]) + bb;
+        }
+        if (silu) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = o[e] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * o[e]));
+        }
+        if constexpr (RESID) {
+          const u32x4 rv = buf_ld128(rrs, (uint32_t)(r * p.ldr + c) * 2, 0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            o[2 * j] += bf16_to_f32(rv[j] & 0xffff);
+            o[2 * j + 1] += bf16_to_f32(rv[j] >> 16);
+          }
+        }
+        if constexpr (!E4M3_OUT) {
+          __builtin_amdgcn_raw_buffer_store_b128(
+              u32x4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])}, crs,
+              (uint32_t)(r * p.ldc + c) * 2, 0, 0);
+        }
+      }
+      if constexpr (E4M3_OUT) {  // the lane's 16 columns are contiguous: one 16-byte store
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float q[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            q[k] = __builtin_fminf(__builtin_fmaxf(os == 1.f ? v[4 * j + k] : div_by(v[4 * j + k], os, oy), -448.f),
+                                   448.f);
+          w[j] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], __builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0, false),
+                                                           true);
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, crs, (uint32_t)(r * p.ldc + n0 + cl0), 0, 0);
+      }
+    }
+  };
+
+  for (int s = 0; s < S; ++s) {
+    const int tile_i = s / nk, kk = s - tile_i * nk;
+    pc_barrier_lds();  // step s has landed; every wave is done with step s - 1
+    if (kk == 0) {
+#pragma unroll
+      for (int ms = 0; ms < 8; ++ms)
+#pragma unroll
+        for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = zero4();
+    }
+    const uint8_t* st = stage[s % kPcStages];
+    i32x8 w[4];
+#pragma unroll
+    for (int ns = 0; ns < 4; ++ns) {
+      const uint32_t lo = ns & 2 ? w_rd1 : w_rd0, hi = ns & 2 ? w_rd0 : w_rd1;
+      w[ns] = cat8(lds_ld128(st + lo + 2048 * ns), lds_ld128(st + hi + 2048 * ns));
+    }
+#pragma unroll
+    for (int ms = 0; ms < 8; ++ms) {
+      const uint32_t lo = ms & 2 ? a_rd1 : a_rd0, hi = ms & 2 ? a_rd0 : a_rd1;
+      const i32x8 b = cat8(lds_ld128(st + lo + 2048 * ms), lds_ld128(st + hi + 2048 * ms));
+#pragma unroll
+      for (int ns = 0; ns < 4; ++ns) {
+        if constexpr (A_BF8)  // W e4m3 (format 0), A e5m2 (format 1)
+          acc[ms][ns] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w[ns], b, acc[ms][ns], 0, 1, 0, 0, 0, 0);
+        else
+          acc[ms][ns] = mfma_fp8(w[ns], b, acc[ms][ns]);
+      }
+    }
+    if (kk == nk - 1) {
+      const int t = t0 + tile_i * gx, mt = t / p.tiles_n;
+      epilogue(mt * kBM, (t - mt * p.tiles_n) * kWideBN);
+    }
+  }
+}
+
 // Per-group e4m3 quantization of bf16 rows: scale = amax/448 over each group
 // of `group` consecutive elements (1/448 for an all-zero group), out =
 // e4m3(clamp(x / scale, +-448)).  One wave per (row, group); group <= 4096 and
@@ -731,6 +1007,21 @@ hipError_t set_gemm_lds_size(const void* fn, int bytes) {
   return e;
 }
 
+// compute units of the current device (cached per device)
+int device_cus() {
+  static std::mutex mu;
+  static std::vector<int> cus;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)cus.size() <= dev) cus.resize(dev + 1, 0);
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
 hipError_t set_gemm_lds(const void* fn) {
   static std::mutex mu;
   static std::vector<const void*> done;
@@ -781,6 +1072,28 @@ extern "C" int hstu_fp8_gemm(int a_dtype, const void* A, int64_t lda, const void
   p.silu_begin = silu_begin;
   p.silu_end = silu_end;
   p.tiles_m = (M + kBM - 1) / kBM;
+  // producer/consumer form: N % 256, K % 256, 16-byte aligned epilogue rows
+  const bool out8 = out_dtype == HSTU_DTYPE_FP8_E4M3;
+  const bool wide_ok =
+      HSTU_GEMM_WIDE && N % kWideBN == 0 && K % 256 == 0 && (uintptr_t)C % 16 == 0 && ldc % (out8 ? 16 : 8) == 0 &&
+      (uintptr_t)bias % 4 == 0 && (silu_begin >= silu_end || (silu_begin % 64 == 0 && silu_end % 64 == 0)) &&
+      (int64_t)kBM * ldc * (out8 ? 1 : 2) <= 0xffffffffLL && (int64_t)kBM * ldr * 2 <= 0xffffffffLL &&
+      (int64_t)M * 4 <= 0xffffffffLL &&
+      (!residual || ((uintptr_t)residual % 16 == 0 && ldr % 8 == 0)) && (int64_t)(N - 1) * ldw + K <= 0xffffffffLL &&
+      (a_dtype == HSTU_DTYPE_FP8_E4M3 || (!out8 && !residual));
+  if (wide_ok) {
+    p.tiles_n = N / kWideBN;
+    const int total = p.tiles_m * p.tiles_n;
+    const int per_xcd = (total + 7) / 8;
+    const int gx = std::max(1, std::min(device_cus() / 8, per_xcd));  // one workgroup per CU
+    void (*kern)(GemmParams, int);
+    if (a_dtype == HSTU_DTYPE_FP8_E5M2) kern = fp8_gemm_pc_kernel<false, false, true>;
+    else if (out8) kern = residual ? fp8_gemm_pc_kernel<true, true, false> : fp8_gemm_pc_kernel<true, false, false>;
+    else kern = residual ? fp8_gemm_pc_kernel<false, true, false> : fp8_gemm_pc_kernel<false, false, false>;
+    int parg = per_xcd;
+    void* args[] = {&p, &parg};
+    return (int)hipLaunchKernel((const void*)kern, dim3(8 * gx), dim3(kPcThreads), args, 0, stream);
+  }
   p.tiles_n = N / kBN;
   // W-stationary persistent form: about one workgroup per CU, streams of M
   // tiles; its output leaves in 16-byte row segments (else the tile kernel)

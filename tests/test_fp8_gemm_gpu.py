@@ -170,6 +170,48 @@ def test_gemm_outproj_config4_full_size(hip_lib):
     assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2
 
 
+def test_gemm_proj512_config4_full_size(hip_lib):
+    """Config 4's second shape at full size: X [262 144, 512] e4m3 (per-row
+    scales) times W [512, 512] e4m3 (per-column scales) with a bf16 bias,
+    bf16 out, no SiLU; 1024 sampled rows (incl. the first and last) against
+    the float64 oracle, to the bar of test_gemm_bf16."""
+    fp8 = _fp8()
+    M, N, K = 262144, 512, 512
+    a8, sa, w8t, sw = _operands(M, N, K, seed=21)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(22)) * 0.1).to(torch.bfloat16)
+    out = fp8.fp8_gemm(a8.to(DEV), sa.to(DEV), (w8t.to(DEV), sw.to(DEV)), bias=bias.to(DEV))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.tensor([0, M - 1]),
+                      torch.randint(1, M - 1, (1022,), generator=torch.Generator().manual_seed(23))])
+    ref = orc.fp8_rowcol_gemm(a8[rows], sa[rows], w8t.t(), sw, bias=bias.float())
+    got = out[rows.to(DEV)].double().cpu()
+    assert orc.rel_l2(ref, got) <= 4e-3
+    assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2
+
+
+@pytest.mark.parametrize("M,N,K", [(162251, 512, 2048), (162251, 1536, 512), (257, 512, 2048)])
+def test_dgrad_e5m2_full_size(hip_lib, M, N, K):
+    """The FP8 backward's dgrad form (``bwd_fp8.fp8_dgrad``): e5m2 dY [M, K]
+    times the e4m3 weight [N, K]^T with per-tensor scales, bf16 out, at the
+    layer's shapes (the out-projection dgrad K = 2048 -> 512 and the UVQK
+    dgrad K = 512 -> 1536 at config 3's T) and a ragged M; sampled rows
+    against the float64 product."""
+    from hstu_amd import bwd_fp8
+
+    g = torch.Generator().manual_seed(M + N)
+    dy8 = (torch.randn(M, K, generator=g) * 8).to(torch.float8_e5m2)
+    w8 = (torch.randn(N, K, generator=g) * 40).clamp(-448, 448).to(torch.float8_e4m3fn)
+    sg, sw = torch.tensor([0.02]), torch.tensor([0.003])
+    out = bwd_fp8.fp8_dgrad(dy8.to(DEV), sg.to(DEV), w8.to(DEV), sw.to(DEV))
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.tensor([0, M - 1]),
+                      torch.randint(1, M - 1, (min(M, 1024) - 2,), generator=torch.Generator().manual_seed(3))])
+    ref = (dy8[rows].double() * 0.02) @ (w8.double() * 0.003).t()
+    got = out[rows.to(DEV)].double().cpu()
+    assert orc.rel_l2(ref, got) <= 4e-3
+    assert float((got - ref).abs().max() / ref.abs().max()) <= 1e-2
+
+
 def test_gemm_k512_both_kernels(hip_lib):
     """K <= 512 runs the W-stationary kernel when the output rows allow
     16-byte segments and the tile kernel otherwise (row stride N + 4): both
@@ -192,6 +234,39 @@ def test_gemm_k512_both_kernels(hip_lib):
         got = out[:, :N].double().cpu()
         assert orc.rel_l2(ref, got) <= 4e-3, ldc
         assert not bool(out[:, N:].any())                              # nothing written past N
+
+
+@pytest.mark.parametrize("out8", [False, True])
+def test_gemm_pc_kernel_bounds(hip_lib, out8):
+    """The producer/consumer kernel (N % 256, K % 256, 64-aligned SiLU) on a
+    ragged M with a padded row stride: every valid element against the
+    oracle, and nothing written past N in a row nor past row M (its stores
+    are bounded by buffer resources at the tile's valid rows)."""
+    import hstu_amd._lib as lib
+
+    M, N, K = 777, 512, 1024
+    a8, sa, w8t, sw = _operands(M, N, K, seed=31)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(32)) * 0.1).to(torch.bfloat16)
+    ref = orc.fp8_rowcol_gemm(a8, sa, w8t.t(), sw, bias=bias.float(), silu_cols=(64, 192))
+    A, W, SA, SW, B = (t.to(DEV).contiguous() for t in (a8, w8t, sa, sw, bias))
+    os_ = torch.tensor([0.05], device=DEV)
+    ldc = N + 16
+    out = torch.zeros(M + 200, ldc, dtype=torch.uint8 if out8 else torch.bfloat16, device=DEV)
+    st = lib.fn("hstu_fp8_gemm_rowcol")(A.data_ptr(), K, W.data_ptr(), K, SA.data_ptr(), 1, SW.data_ptr(), 1,
+                                        B.data_ptr(), None, 0, out.data_ptr(), ldc,
+                                        lib.HSTU_DTYPE_FP8_E4M3 if out8 else lib.HSTU_DTYPE_BF16, os_.data_ptr(),
+                                        M, N, K, 64, 192, torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    if out8:  # the bar of test_gemm_e4m3_out, in units of the output scale
+        got = out[:M, :N].view(torch.float8_e4m3fn).double().cpu()
+        want = (ref / 0.05).clamp(-448, 448)
+        tol = want.abs() * 2.0 ** -4 + 2.5e-5 * float(want.abs().max())
+        assert float(((got - want).abs() - tol).max()) <= 0
+    else:
+        got = out[:M, :N].double().cpu()
+        assert orc.rel_l2(ref, got) <= 4e-3
+    assert not bool(out[:, N:].any()) and not bool(out[M:].any())
 
 
 @pytest.mark.parametrize("M,N,K,bias,resid,silu", [(1000, 512, 2048, False, False, False),
