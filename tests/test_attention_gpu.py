@@ -20,6 +20,12 @@ from oracle import hstu_oracle as orc
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
+# Full-FP8 backward against the oracle that repeats its casts: the kernels'
+# fp32 exp2 / rcp differ from float64 in the last bits, so a P or dS byte near
+# an e4m3 rounding midpoint can round the other way (one e4m3 step on that
+# element).  Measured on these tests and at config 3: dq, dk, dv 1.8e-3 ..
+# 2.3e-3 relative L2, dbias 7.3e-4 .. 9.5e-4; bars at about twice that.
+SAME_CAST_BAR = {"dq": 4e-3, "dk": 4e-3, "dv": 4e-3, "dbias": 2e-3}
 
 
 def _ops():
@@ -447,7 +453,8 @@ def _full_fp8_case(lengths, H, D, seed, per_tensor):
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_full_fp8_backward(hip_lib, per_tensor, with_bias):
     """The full-FP8 backward (e4m3 dO in pow2 blocks, e4m3 P and dS, five
-    e4m3 MFMAs): against the oracle with the same casts, relative L2 <= 1e-2
+    e4m3 MFMAs): against the oracle with the same casts, relative L2 within
+    SAME_CAST_BAR (4e-3 for dq, dk, dv; 2e-3 for dbias)
     for dq, dk, dv (and dbias); against the float64 backward of the
     dequantized inputs on the unquantized dO (the e4m3 error of the
     contract itself, which the oracle shows at 3.8-5 % relative L2, 26-28.5
@@ -485,7 +492,8 @@ def test_full_fp8_backward(hip_lib, per_tensor, with_bias):
     for name, gt, w, ex in zip(("dq", "dk", "dv", "dbias"), got, want, exact):
         assert not torch.isnan(gt).any(), name
         e = orc.rel_l2(w, gt)
-        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+        print(f"same-cast full-FP8 {name}: {e:.3e}", flush=True)
+        assert e <= SAME_CAST_BAR[name], f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
         e2, snr = orc.rel_l2(ex, gt), orc.snr_db(ex, gt)
         m = float((gt.double() - ex).abs().max() / ex.abs().max())
         assert e2 <= 6e-2 and snr >= 24.0 and m <= 0.2, (
@@ -495,7 +503,7 @@ def test_full_fp8_backward(hip_lib, per_tensor, with_bias):
 def test_full_fp8_backward_long_n(hip_lib):
     """The full-FP8 backward at max_seq_len 8192 (64 key blocks of 128, each
     run as two workgroups, and 64 query tiles in the dQ walk) against the
-    oracle with the same casts: relative L2 <= 1e-2 for dq, dk, dv, dbias."""
+    oracle with the same casts: relative L2 within SAME_CAST_BAR."""
     from oracle import hstu_bwd_fp8full_oracle as FO
 
     ops = _ops()
@@ -518,14 +526,15 @@ def test_full_fp8_backward_long_n(hip_lib):
     for name, gt, w in zip(("dq", "dk", "dv", "dbias"), got, want):
         assert not torch.isnan(gt).any(), name
         e = orc.rel_l2(w, gt)
-        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+        print(f"same-cast full-FP8 {name}: {e:.3e}", flush=True)
+        assert e <= SAME_CAST_BAR[name], f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
 
 
 @pytest.mark.parametrize("dsc_k,ssc_k", [(-5, 3), (-3, 6), (-7, 1)])
 def test_full_fp8_backward_prescales(hip_lib, monkeypatch, dsc_k, ssc_k):
     """Other P / dS pre-scale exponents (``DLRM_HSTU_FP8_BWD_FULL_{SSC,DSC}_K``;
     production runs DSC_K = -5): against the oracle with the same casts,
-    relative L2 <= 1e-2, on inputs where the default dS scale (K = -3)
+    relative L2 within SAME_CAST_BAR, on inputs where the default dS scale (K = -3)
     clamps some dS to +-448 in the oracle; the environment's K gives the
     same bytes as the explicit argument."""
     from oracle import hstu_bwd_fp8full_oracle as FO
@@ -555,7 +564,8 @@ def test_full_fp8_backward_prescales(hip_lib, monkeypatch, dsc_k, ssc_k):
     for name, gt, w in zip(("dq", "dk", "dv", "dbias"), got, want):
         assert not torch.isnan(gt).any(), name
         e = orc.rel_l2(w, gt)
-        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle at K = ({ssc_k}, {dsc_k})"
+        print(f"same-cast full-FP8 K=({ssc_k},{dsc_k}) {name}: {e:.3e}", flush=True)
+        assert e <= SAME_CAST_BAR[name], f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle at K = ({ssc_k}, {dsc_k})"
     monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL_SSC_K", str(ssc_k))
     monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL_DSC_K", str(dsc_k))
     for a, b in zip(got, run()):

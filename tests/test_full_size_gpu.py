@@ -160,7 +160,9 @@ def test_config3_full_fp8_backward(hip_lib, dsc_k):
     e4m3 MFMAs).  Sampled sequences incl. the longest (4096):
 
     * the full batch's rows against the oracle with the same casts (and the
-      batch-wide q / k scale normalisers): relative L2 <= 1e-2;
+      batch-wide q / k scale normalisers): relative L2 <= 4e-3 (measured
+      1.9e-3: P / dS bytes near an e4m3 midpoint round the other way where
+      the kernels' fp32 exp2 / rcp differ from float64);
     * against the fp64 backward of the dequantized inputs on the unquantized
       dO (the contract's own e4m3 error): relative L2 <= 6e-2, SNR >= 24 dB,
       max |err| <= 0.2 max |ref|;
@@ -209,7 +211,8 @@ def test_config3_full_fp8_backward(hip_lib, dsc_k):
     for name, gt, w, ex in zip(("dq", "dk", "dv"), full[:3], want_full[:3], exact[:3]):
         gt = gt[rows]
         e = orc.rel_l2(w, gt)
-        assert e <= 1e-2, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+        print(f"same-cast full-FP8 config3 {name}: {e:.3e}", flush=True)
+        assert e <= 4e-3, f"{name}: rel L2 {e:.3e} vs the full-FP8 oracle"
         e2, snr = orc.rel_l2(ex, gt), orc.snr_db(ex, gt)
         m = float((gt.double() - ex).abs().max() / ex.abs().max())
         assert e2 <= 6e-2 and snr >= 24.0 and m <= 0.2, (
@@ -219,7 +222,8 @@ def test_config3_full_fp8_backward(hip_lib, dsc_k):
     want_sub = FO.full_fp8_bwd(*args, attn_bias=bias, dsc_k=dsc_k)
     for name, gt, w in zip(("dq", "dk", "dv", "dbias"), sub, want_sub):
         e = orc.rel_l2(w, gt)
-        assert e <= 1e-2, f"sub-batch {name}: rel L2 {e:.3e} vs the full-FP8 oracle"
+        print(f"same-cast full-FP8 config3 sub-batch {name}: {e:.3e}", flush=True)
+        assert e <= (2e-3 if name == "dbias" else 4e-3), f"sub-batch {name}: rel L2 {e:.3e} vs the full-FP8 oracle"
     e2, snr = orc.rel_l2(exact[3], sub[3]), orc.snr_db(exact[3], sub[3])
     assert e2 <= 6e-2 and snr >= 24.0, f"sub-batch dbias: rel L2 {e2:.3e}, SNR {snr:.1f} dB vs float64"
 

@@ -5,7 +5,9 @@ Tolerances (stated bar):
 * against ``oracle/hstu_fwd_pv8_oracle.fwd_pv8`` -- the same e4m3 cast of P
   evaluated in float64: relative L2 <= 5e-3 and max |err| <= 5e-2 max |ref|
   (a P byte rounds the other way where the kernel's fp32 P' s r sits within
-  fp32 rounding of an e4m3 midpoint);
+  fp32 rounding of an e4m3 midpoint; measured 1.7e-3 .. 2.1e-3 relative L2
+  and up to 1.3e-2 max on these tests and config 3, 4.5e-3 / 1.9e-2 on the
+  shortest sequences, whose few elements make one flipped byte weigh more);
 * against the unquantized float64 forward on the dequantized inputs (the
   contract's own e4m3 error of P, 2.6 % relative L2 in the oracle): relative
   L2 <= 3.5e-2 and SNR >= 28 dB.
@@ -47,6 +49,7 @@ def _check(got, want, exact, what):
     got = got.float().cpu().double()
     e = orc.rel_l2(want, got)
     mx = float((got - want).abs().max() / want.abs().max())
+    print(f"same-cast fwd_pv8 {what}: rel L2 {e:.3e} max {mx:.3e}", flush=True)
     assert e <= 5e-3 and mx <= 5e-2, f"{what}: rel L2 {e:.3e}, max {mx:.3e} vs the same-cast oracle"
     e2, snr = orc.rel_l2(exact, got), orc.snr_db(exact, got)
     assert e2 <= 3.5e-2 and snr >= 28.0, f"{what}: rel L2 {e2:.3e}, SNR {snr:.1f} dB vs the unquantized forward"
