@@ -2122,8 +2122,10 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_dkdv_kernel(AttnParams p
 // =====================================================================
 struct F8Bwd {
   // dK/dV: a 128-key block is two workgroups of 4 waves (64 keys), 16 keys
-  // a wave; two such workgroups share a CU, so the two waves of a SIMD
-  // belong to different workgroups and do not meet at the same barriers
+  // a wave; three such workgroups share a CU (one LDS stage each, at most 168
+  // VGPRs), so the three waves of a SIMD belong to different workgroups and
+  // do not meet at the same barriers: while one workgroup waits for its next
+  // tile's loads, the others compute
   static constexpr int NT = 256;
   static constexpr int BN = 128, BM = 128;  // keys per block, queries per tile
   // dK/dV stage: Q and dO tiles of 128-byte e4m3 rows, unpadded (LDS DMA
@@ -2137,7 +2139,7 @@ struct F8Bwd {
   static constexpr int SQ_OFF = DO_OFF + BM * 128;  // 128 fp32 query scales
   static constexpr int B_OFF = SQ_OFF + BM * 4;     // 256 fp32: pre-scaled bias of offsets m0-n0-127 ..
   static constexpr int STAGE = B_OFF + 256 * 4;
-  static constexpr int LDS = 2 * STAGE;
+  static constexpr int LDS = STAGE;
   static constexpr int TILE = BN * BM;  // one stored e4m3 dS tile (16 KiB)
   // dQ: K tile [key][d] and dS tile [key][query] (queries permuted so that
   // a stored piece is one 16-byte chunk), unpadded 128-byte rows, data chunk
@@ -2191,7 +2193,7 @@ __device__ __forceinline__ uint32_t buf_ldu8(BufRsrc r, uint32_t voff) {
 enum ScaleMode { kScalesPerToken = 0, kScalesPerTensor = 1, kScalesShared = 2 };
 
 template <bool BIAS, int SM>
-__global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnParams p) {
+__global__ void __launch_bounds__(F8Bwd::NT, 3) hstu_bwd_f8_dkdv_kernel(AttnParams p) {
   constexpr bool PT = SM != kScalesPerToken;
   using C = F8Bwd;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -2246,7 +2248,9 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) dvt[dt] = dkt[dt] = zero4();
 
-  // one 128-query tile per stage, moved by LDS DMA: wave w takes rows
+  // one 128-query tile in the workgroup's one stage, loaded by LDS DMA after
+  // the previous tile's barrier (the other two workgroups of the CU compute
+  // meanwhile): wave w takes rows
   // 8 w + 32 i + (lane >> 3), i = 0..3, of Q and dO (lane slot lane & 7
   // holds data chunk (lane & 7) ^ kv_swz(row), which depends on i through
   // bit 5 of the row), waves 0-1 the 128 query scales, wave w bias values
@@ -2311,11 +2315,23 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool BCONST = decltype(bconst_tag)::value;
     const int m0 = n0 + t * C::BM;
-    const uint8_t* buf = smem + (t & 1) * C::STAGE;
+    if (t > 0) {  // after the previous tile's barrier every wave is done with the stage
+      load(m0, smem);
+      wait_vm_le<0>();
+      __syncthreads();
+    }
+    const uint8_t* buf = smem;
     const int sc_e = sc_next;
-    if (t + 1 < ntiles) load(m0 + C::BM, smem + ((t + 1) & 1) * C::STAGE);
     uint8_t* dst = ds_dst + (size_t)t * C::TILE;
     const float* bias_lds = (const float*)(buf + C::B_OFF);
+    // the lane's bias values through one opaque LDS base register: the 32
+    // reads of a tile then differ only in the instructions' offsets (with a
+    // plain pointer the compiler kept 16 addresses live across tiles and
+    // spilled them at 168 VGPRs)
+    uint32_t bbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(buf + C::B_OFF) +
+                     4u * (uint32_t)bias_lane;
+    if constexpr (BIAS) asm volatile("" : "+v"(bbase));
+    const __attribute__((address_space(3))) float* blane = (const __attribute__((address_space(3))) float*)(uintptr_t)bbase;
     const float bconst = (BIAS && BCONST) ? bias_lds[0] : 0.f;
     uint32_t pd[8], dk8[8];
 #pragma unroll
@@ -2334,12 +2350,11 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
 #pragma unroll
       for (int qs = 0; qs < 4; ++qs) {
         const f32x4 sq4 = PT ? f32x4{0.f, 0.f, 0.f, 0.f} : lds_ldf4(buf + C::SQ_OFF + (64 * hf + 16 * qs + 4 * g) * 4);
-        const float* bl = bias_lds + bias_lane + 64 * hf + 16 * qs;
         float pv[4], dkv[4], dqv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float tt = PT ? s[qs][r] * ck_pt : s[qs][r] * (ck * sq4[r]);
-          if constexpr (BIAS) tt += BCONST ? bconst : bl[r];
+          if constexpr (BIAS) tt += BCONST ? bconst : blane[64 * hf + 16 * qs + r];
           const float sgk = __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_amdgcn_exp2f(tt), ikp, ikp));
           float pval = tt * sgk;
           float dsv = dp[qs][r] * __builtin_fmaf(pval, __builtin_fmaf(sgk, ln2_kp, -kLn2), sgk);
@@ -2358,6 +2373,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
         dq8[qs] = pack_fp8x4(dqv[0], dqv[1], dqv[2], dqv[3]);
         dk8[4 * hf + qs] = SM == kScalesShared ? dq8[qs] : pack_fp8x4(dkv[0], dkv[1], dkv[2], dkv[3]);
       }
+      __builtin_amdgcn_sched_barrier(0);  // bounds the live ranges at 168 VGPRs
       // the dQ kernel's operand, streamed out (read once, much later)
       __builtin_nontemporal_store(u32x4{dq8[0], dq8[1], dq8[2], dq8[3]}, (u32x4*)(dst + hf * 64 * 16));
       // runs of eight queries per lane group (groups 0<->1 and 2<->3 trade qs 2,3 for qs 0,1)
@@ -2371,6 +2387,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
         dk8[4 * hf + j + 2] = b[1];
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // phase B's operand reads stay in phase B
     // after the swaps pd[4 hf + j] holds queries base(g) + 64 hf + {0, 16, 4, 20}[j] + 0..3:
     // B operand dwords in the A fragment's token order (+0..3, 4..7, 16..19, 20..23)
     i32x8 bp, bk;
@@ -2396,10 +2413,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 2) hstu_bwd_f8_dkdv_kernel(AttnPara
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    // the next stage's DMA done; this tile's two dS stores, the last vector
-    // memory operations issued, may stay in flight
-    wait_vm_le<2>();
-    __syncthreads();
+    __syncthreads();  // every wave is done with the stage
   };
 
   // tile 0 holds the diagonal; tiles whose smallest offset m0 - n0 - 127 is
