@@ -724,9 +724,15 @@ struct Pv8Cfg {
   static constexpr int KT = BN * 128;
   static constexpr int K_OFF = 0;
   static constexpr int VS_OFF = 3 * KT;
-  // V stage: V rows, BM + BN - 1 bias values
+  // V stage: V rows, then the BM + BN - 1 bias values of the tile in four
+  // copies, copy c shifted by c floats (copy_c[y] = window[y - c]), so that
+  // every lane reads its runs of four with 16-byte aligned ds_read_b128s from
+  // the copy that aligns them.  The copies start at dwords 0, 204, 412, 620
+  // (0, 12, 28, 44 mod 64): the 16 lanes of a read pass, four of each copy,
+  // then cover the 64 banks once.
   static constexpr int V_REL = 0, BIAS_REL = BN * 128;
-  static constexpr int VSTAGE = BIAS_REL + (BM + BN) * 4;
+  __host__ __device__ static constexpr int bias_copy(int c) { return c == 0 ? 0 : c == 1 ? 204 : c == 2 ? 412 : 620; }
+  static constexpr int VSTAGE = BIAS_REL + (620 + 200) * 4;
   static constexpr int P_OFF = VS_OFF + 2 * VSTAGE;  // per wave: P^T, 64 keys x 32 queries
   // the block's table: two E8M0 bytes (as ints) per key tile, then c_k per key
   static constexpr int TAB_OFF = P_OFF + 4 * BN * 32;
@@ -834,7 +840,12 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   // the V stage's bias window
   auto store_v = [&](uint8_t* vbuf) __attribute__((always_inline)) {
     if constexpr (BIAS) {
-      if (tid < C::BM + C::BN - 1) ((float*)(vbuf + C::BIAS_REL))[tid] = st_bias * -kLog2e;
+      if (tid < C::BM + C::BN - 1) {
+        float* w = (float*)(vbuf + C::BIAS_REL);
+        const float x = st_bias * -kLog2e;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) w[C::bias_copy(c) + tid + c] = x;
+      }
     }
   };
   auto kbuf = [&](int t) { return smem + C::K_OFF + (t % 3) * C::KT; };
@@ -880,15 +891,24 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_fwd_pv8_kernel(AttnParams p)
   // the lane's 16 bias values (the window holds clamped values, so tiles
   // past the bias range read their constant) and c_k of key sub-tile b,
   // read ahead of the epilogue that uses them
+  // the lane's runs start at window index bias_lo + 32 (1 - b) + 8 i, which
+  // is 3 - l32 mod 4: copy (l32 + 1) & 3 holds them 16-byte aligned
+  const int bias_c = (l32 + 1) & 3;
+  const int bias_at = 4 * (C::bias_copy(bias_c) + bias_lo + bias_c);
   auto load_bias = [&](const uint8_t* vb, int n0, int b, float (&bj)[16], float& ck) __attribute__((always_inline)) {
-    // the lane's bias window as an opaque LDS address, so that its 16 reads
-    // share one base register and differ in the instructions' offsets
-    uint32_t baddr = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(vb + C::BIAS_REL) +
-                     4 * (bias_lo + 32 * (1 - b));
+    // the lane's base as an opaque LDS address, so that its four reads share
+    // one base register and differ in the instructions' offsets
+    uint32_t baddr =
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)(vb + C::BIAS_REL) + bias_at;
     if constexpr (BIAS) asm volatile("" : "+v"(baddr));
-    const __attribute__((address_space(3))) float* bias_lane = (const __attribute__((address_space(3))) float*)(uintptr_t)baddr;
+    const __attribute__((address_space(3))) f32x4* bias_lane =
+        (const __attribute__((address_space(3))) f32x4*)(uintptr_t)(baddr + 128 * (1 - b));
 #pragma unroll
-    for (int j = 0; j < 16; ++j) bj[j] = BIAS ? bias_lane[8 * (j >> 2) + (j & 3)] : 0.f;
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 v = BIAS ? bias_lane[2 * i] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bj[4 * i + r] = v[r];
+    }
     ck = ckt[n0 + 32 * b + l32];
   };
   auto epilogue = [&](const f32x16& s, const f32x16& scl, int b, int n0, const float (&bj)[16], float ck,
