@@ -353,6 +353,33 @@ int hstu_cast_fp8_amax(int in_dtype, const void* x, int64_t n, const float* inv_
                        void* out, float* partial_amax, int64_t partial_count, hipStream_t stream);
 
 /*
+ * e4m3 at unit margin with the scale derived on the device (two launches):
+ * scale_out[0] = max(amax |x|, 1e-30) * fp32(1 / 448), out = e4m3(clamp(x *
+ * (1 / scale), +-448)), 1 / scale correctly rounded; x bf16 / fp32 (in_dtype),
+ * n > 0, n % 32 == 0, 16-byte aligned; partial: hstu_cast_fp8_amax_partials(n)
+ * fp32 of scratch.  Bitwise equal to the torch expression it replaces.
+ * Replaces: quantize_weight, ops/triton/bwd_fp8.py:1157-1175 (the
+ *           DLRM_HSTU_FP8_BWD_HELPERS_FUSED form :1178-1190 is likewise one
+ *           amax launch + one cast launch).
+ */
+int hstu_quantize_e4m3_unit(int in_dtype, const void* x, int64_t n, void* out, float* scale_out, float* partial,
+                            int64_t partial_count, hipStream_t stream);
+
+/*
+ * One call's update of a delayed-scale gradient site in one launch; state
+ * (device fp32 [4]) = [scale, 1 / scale, window peak, overflowed calls].
+ * a = max of amax_values[0 .. count) (a cast's partials, or one amax; NaN
+ * propagates); when live, state[3] += (a > state[0] * limit); state[2] =
+ * max(state[2], a); snapshot (nullable) <- state[0]; when roll, state[0] =
+ * max(state[2], 1e-30) * factor, state[1] = 1 / state[0], state[2] = 0.
+ * Replaces: the partial-amax reduce, note_clipping, accumulate, the decode
+ *           scale snapshot and the publish of the reference's _SiteScale,
+ *           ops/triton/bwd_fp8.py:869-1154 (fused as in :1178-1190).
+ */
+int hstu_fp8_site_update(const float* amax_values, int count, float* state, float limit, int live, int roll,
+                         float factor, float* snapshot, hipStream_t stream);
+
+/*
  * One read of a row-major bf16 gradient x [rows, cols] (row stride ldx,
  * cols % 256 == 0) -> out [rows_out, cols] contiguous fp8 (out_dtype e4m3 or
  * e5m2) = fp8(clamp(x * inv_scale[0], +-limit)), RNE, with rows in
@@ -414,7 +441,10 @@ int hstu_quantize_e4m3_rows(const void* x, int64_t ldx, int rows, int cols, int 
 /*
  * LayerNorm * U * dropout of the output block, and the weighted LayerNorm.
  * Rows of x, u: bf16 [rows, D] with row strides (elements); D = 256 or 512.
- * weight, bias: fp32 [D].  mean, rstd: fp32 [rows] (written by the forward).
+ * weight, bias: [D], fp32 (param_dtype HSTU_DTYPE_FP32) or bf16
+ * (HSTU_DTYPE_BF16, the parameters' own dtype, converted exactly on load),
+ * 16-byte aligned.
+ * mean, rstd: fp32 [rows] (written by the forward).
  * mul_u_act: 0 none (ln * u), 1 silu (ln * silu(u)), 2 sigmoid.
  * u == NULL: plain weighted LayerNorm, y = ln (concat_u, mul_u_act, silu_u
  * ignored).
@@ -447,7 +477,7 @@ int hstu_dropout_mask(int rows, int D, int num_masks, int mask16, float dropout_
  *           ops/triton/triton_layer_norm.py:1668-1740 (u == NULL).
  */
 int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_t ldu,
-                    const float* weight, const float* bias, float eps, int rows, int D,
+                    const void* weight, const void* bias, int param_dtype, float eps, int rows, int D,
                     int mul_u_act, int silu_u, int concat_u, int concat_x,
                     int training, float dropout_ratio, uint64_t seed, int mask16,
                     void* mask, int64_t ldm,
@@ -471,7 +501,7 @@ int64_t hstu_ln_mul_bwd_workspace_bytes(int rows, int D);
  *           ops/triton/triton_layer_norm.py:3574-3640 (u == NULL, no residual).
  */
 int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx,
-                    const void* u, int64_t ldu, const float* weight, const float* bias,
+                    const void* u, int64_t ldu, const void* weight, const void* bias, int param_dtype,
                     const float* mean, const float* rstd, int rows, int D,
                     int mul_u_act, int silu_u, int concat_u, int concat_x,
                     float dropout_ratio, const void* mask, int64_t ldm,
@@ -499,8 +529,9 @@ int64_t hstu_outproj_ln_bwd_workspace_bytes(int rows);
  */
 int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_scale, const void* w8, int64_t ldw,
                         const float* w_scale, const void* x, int64_t ldx, const void* u, int64_t ldu,
-                        const float* weight, const float* bias, const float* mean, const float* rstd,
-                        int rows, int D, int mul_u_act, int silu_u, float dropout_ratio, const void* mask,
+                        const void* weight, const void* bias, int param_dtype, const float* mean,
+                        const float* rstd, int rows, int D, int mul_u_act, int silu_u, float dropout_ratio,
+                        const void* mask,
                         int64_t ldm, void* dx, int64_t lddx, void* du, int64_t lddu, float* dweight,
                         float* dbias, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 

@@ -863,6 +863,133 @@ __global__ void __launch_bounds__(256) cast_fp8_amax_kernel(const uint8_t* __res
   if (tid == 0) partial[blockIdx.x] = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
 }
 
+// max(a, b) that returns NaN when either is NaN (torch.maximum / amax).
+__device__ __forceinline__ float max_nan(float a, float b) { return a != a ? a : (b != b || b > a ? b : a); }
+
+// The 32 elements a thread of the 8192-element cast blocks handles, as fp32.
+// (The loads go into an array first: a const vector local initialised by
+// the conditional load compiled, for fp32, to one dword load per chunk whose
+// value filled all four lanes.)
+template <bool IN_F32>
+__device__ __forceinline__ void load32(const uint8_t* __restrict__ x, int64_t n, int64_t e0, float (&v)[32]) {
+  constexpr int ES = IN_F32 ? 4 : 2, NL = 32 * ES / 16;
+  u32x4 w[NL];
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t e = e0 + i * (16 / ES);
+    w[i] = e < n ? *(const u32x4*)(x + e * ES) : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u = w[i][j];
+      if constexpr (IN_F32) {
+        v[4 * i + j] = __builtin_bit_cast(float, u);
+      } else {
+        v[8 * i + 2 * j] = __builtin_bit_cast(float, u << 16);
+        v[8 * i + 2 * j + 1] = __builtin_bit_cast(float, u & 0xffff0000u);
+      }
+    }
+  }
+}
+
+// Unit-margin e4m3 quantization of a whole tensor (the dgrad's weight):
+// scale = max(amax |x|, 1e-30) * fp32(1 / 448) (torch divides a tensor by a
+// host scalar as a product with the scalar's fp32 reciprocal), out =
+// e4m3(clamp(x * (1 / scale), +-448)) with 1 / scale correctly rounded (its
+// reciprocal kernel).  Pass 1: per 8192-element block the max |x| (NaN
+// propagates, as torch.amax) into partial[block].
+template <bool IN_F32>
+__global__ void __launch_bounds__(256) absmax_partials_kernel(const uint8_t* __restrict__ x, int64_t n,
+                                                              float* __restrict__ partial) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  float v[32];
+  load32<IN_F32>(x, n, (int64_t)blockIdx.x * kCastBlock + (int64_t)tid * 32, v);
+  float m = 0.f;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) m = max_nan(m, __builtin_fabsf(v[k]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) partial[blockIdx.x] = max_nan(max_nan(red[0], red[1]), max_nan(red[2], red[3]));
+}
+// Pass 2: every block folds the partials in the same way, derives the scale
+// and casts its 8192 elements; block 0 writes the scale.
+template <bool IN_F32>
+__global__ void __launch_bounds__(256) cast_unit_e4m3_kernel(const uint8_t* __restrict__ x, int64_t n,
+                                                             const float* __restrict__ partial, int parts,
+                                                             uint8_t* __restrict__ out, float* __restrict__ scale_out) {
+  __shared__ float inv_sh;
+  const int tid = threadIdx.x;
+  if (tid < 64) {
+    float m = 0.f;
+    for (int i = tid; i < parts; i += 64) m = max_nan(m, partial[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off));
+    if (tid == 0) {
+      const float c = m != m ? m : __builtin_fmaxf(m, 1.0e-30f);
+      const float scale = c * (1.0f / 448.0f);
+      inv_sh = 1.0f / scale;
+      if (blockIdx.x == 0) scale_out[0] = scale;
+    }
+  }
+  __syncthreads();
+  const float s = inv_sh;
+  const int64_t e0 = (int64_t)blockIdx.x * kCastBlock + (int64_t)tid * 32;
+  if (e0 >= n) return;
+  float v[32];
+  load32<IN_F32>(x, n, e0, v);
+  uint32_t o[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    float c[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) c[r] = __builtin_fminf(__builtin_fmaxf(v[4 * q + r] * s, -448.f), 448.f);
+    int t = __builtin_amdgcn_cvt_pk_fp8_f32(c[0], c[1], 0, false);
+    t = __builtin_amdgcn_cvt_pk_fp8_f32(c[2], c[3], t, true);
+    o[q] = (uint32_t)t;
+  }
+  *(u32x4*)(out + e0) = u32x4{o[0], o[1], o[2], o[3]};
+  *(u32x4*)(out + e0 + 16) = u32x4{o[4], o[5], o[6], o[7]};
+}
+
+// One call's update of a delayed-scale site, state = [scale, 1 / scale,
+// window peak, overflowed calls]: a = max of the call's amax values (NaN
+// propagates); when live, count the call if a > scale * limit; peak =
+// max(peak, a); snapshot (nullable) <- the scale the call was cast with;
+// when rolling, scale = max(peak, 1e-30) * factor, 1 / scale, peak = 0.
+// One block of 256 threads (a cast of config 3's gradients leaves ~10 000
+// partials); the arithmetic is the host policy's, operation for operation.
+__global__ void __launch_bounds__(256) site_update_kernel(const float* __restrict__ vals, int count,
+                                                          float* __restrict__ st, float limit, int live, int roll,
+                                                          float factor, float* __restrict__ snapshot) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  float m = 0.f;
+  for (int i = tid; i < count; i += 256) m = max_nan(m, vals[i]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  if (tid != 0) return;
+  m = max_nan(max_nan(red[0], red[1]), max_nan(red[2], red[3]));
+  const float scale = st[0];
+  if (live) st[3] = st[3] + (m > scale * limit ? 1.f : 0.f);
+  const float peak = max_nan(st[2], m);
+  st[2] = peak;
+  if (snapshot != nullptr) snapshot[0] = scale;
+  if (roll) {
+    const float c = peak != peak ? peak : __builtin_fmaxf(peak, 1.0e-30f);
+    const float s = c * factor;
+    st[0] = s;
+    st[1] = 1.0f / s;
+    st[2] = 0.f;
+  }
+}
+
 // One read of a row-major bf16 gradient [rows, cols] -> its FP8 copy
 // [rows_out, cols] (fp8(clamp(x * inv_scale, +-limit)), rows >= rows zero),
 // the max |x| and the fp32 column sums of the unquantized input (the bias
@@ -1209,6 +1336,36 @@ extern "C" int hstu_cast_fp8_amax(int in_dtype, const void* x, int64_t n, const 
   else if (f32) hipLaunchKernelGGL((cast_fp8_amax_kernel<true, false>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
   else if (bf8) hipLaunchKernelGGL((cast_fp8_amax_kernel<false, true>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
   else hipLaunchKernelGGL((cast_fp8_amax_kernel<false, false>), dim3(grid), dim3(256), 0, stream, xp, n, inv_scale, limit, op, partial_amax);
+  return (int)hipGetLastError();
+}
+
+extern "C" int hstu_quantize_e4m3_unit(int in_dtype, const void* x, int64_t n, void* out, float* scale_out,
+                                       float* partial, int64_t partial_count, hipStream_t stream) {
+  if ((in_dtype != HSTU_DTYPE_BF16 && in_dtype != HSTU_DTYPE_FP32) || n <= 0 || !x || !out || !scale_out ||
+      !partial)
+    return HSTU_E_BAD_ARG;
+  const int64_t grid = hstu_cast_fp8_amax_partials(n);
+  if (partial_count < grid) return HSTU_E_BAD_ARG;
+  if (n % 32 != 0 || (uintptr_t)x % 16 || (uintptr_t)out % 16 || grid >= ((int64_t)1 << 31)) return HSTU_E_UNSUPPORTED;
+  auto* xp = (const uint8_t*)x;
+  auto* op = (uint8_t*)out;
+  if (in_dtype == HSTU_DTYPE_FP32) {
+    hipLaunchKernelGGL(absmax_partials_kernel<true>, dim3(grid), dim3(256), 0, stream, xp, n, partial);
+    hipLaunchKernelGGL(cast_unit_e4m3_kernel<true>, dim3(grid), dim3(256), 0, stream, xp, n, partial, (int)grid, op,
+                       scale_out);
+  } else {
+    hipLaunchKernelGGL(absmax_partials_kernel<false>, dim3(grid), dim3(256), 0, stream, xp, n, partial);
+    hipLaunchKernelGGL(cast_unit_e4m3_kernel<false>, dim3(grid), dim3(256), 0, stream, xp, n, partial, (int)grid, op,
+                       scale_out);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int hstu_fp8_site_update(const float* amax_values, int count, float* state, float limit, int live,
+                                    int roll, float factor, float* snapshot, hipStream_t stream) {
+  if (!amax_values || count <= 0 || !state || !(limit > 0.f)) return HSTU_E_BAD_ARG;
+  hipLaunchKernelGGL(site_update_kernel, dim3(1), dim3(256), 0, stream, amax_values, count, state, limit, live, roll,
+                     factor, snapshot);
   return (int)hipGetLastError();
 }
 

@@ -195,13 +195,52 @@ __device__ __forceinline__ void store_bytes(uint8_t* dst, const uint32_t (&b)[EP
 }
 
 // ------------------------------------------------------------------ forward
+// Element i of a LayerNorm parameter vector, fp32 or bf16 (converted exactly).
+__device__ __forceinline__ float ln_param(const void* v, int i, int bf16) {
+  return bf16 ? __builtin_bit_cast(float, (uint32_t)((const uint16_t*)v)[i] << 16) : ((const float*)v)[i];
+}
+// A lane's EPT consecutive weight and bias values from column c0, fp32 or
+// bf16 (a kernel-uniform branch; vector loads, 16-byte aligned vectors).
+template <int EPT>
+__device__ __forceinline__ void ln_params(const void* w, const void* b, int bf16, int c0, float (&wv)[EPT],
+                                          float (&bv)[EPT]) {
+  static_assert(EPT == 4 || EPT == 8, "4 or 8 columns a lane");
+  if (bf16) {
+    uint32_t x[EPT / 2], y[EPT / 2];
+    if constexpr (EPT == 8) {
+      const u32x4 p = *(const u32x4*)((const uint16_t*)w + c0), q = *(const u32x4*)((const uint16_t*)b + c0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = p[i], y[i] = q[i];
+    } else {
+      const u32x2 p = *(const u32x2*)((const uint16_t*)w + c0), q = *(const u32x2*)((const uint16_t*)b + c0);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) x[i] = p[i], y[i] = q[i];
+    }
+#pragma unroll
+    for (int i = 0; i < EPT / 2; ++i) {
+      wv[2 * i] = __builtin_bit_cast(float, x[i] << 16);
+      wv[2 * i + 1] = __builtin_bit_cast(float, x[i] & 0xffff0000u);
+      bv[2 * i] = __builtin_bit_cast(float, y[i] << 16);
+      bv[2 * i + 1] = __builtin_bit_cast(float, y[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPT / 4; ++i) {
+      const f32x4 p = *(const f32x4*)((const float*)w + c0 + 4 * i), q = *(const f32x4*)((const float*)b + c0 + 4 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[4 * i + j] = p[j], bv[4 * i + j] = q[j];
+    }
+  }
+}
+
 struct FwdArgs {
   const uint16_t* x;
   int64_t ldx;
   const uint16_t* u;  // null: weighted LayerNorm only
   int64_t ldu;
-  const float* w;
-  const float* b;
+  const void* w;  // LayerNorm weight and bias, fp32 or bf16 (w_bf16)
+  const void* b;
+  int w_bf16;
   float eps, inv_d;
   int rows;
   int silu_u, concat_u, concat_x;
@@ -286,11 +325,7 @@ __global__ void __launch_bounds__(kThreads) ln_mul_fwd_kernel(FwdArgs a) {
     if constexpr (HU) ur[k] = load_raw<EPT>(a.u + row * a.ldu + c0);
   }
   float w[EPT], bb[EPT];
-#pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    w[i] = a.w[c0 + i];
-    bb[i] = a.b[c0 + i];
-  }
+  ln_params<EPT>(a.w, a.b, a.w_bf16, c0, w, bb);
   if constexpr (DROP) {
     for (int col = threadIdx.x; col < D; col += kThreads) {
       uint32_t bits[8];
@@ -383,8 +418,9 @@ struct BwdArgs {
   int64_t ldx;
   const uint16_t* u;
   int64_t ldu;
-  const float* w;
-  const float* b;
+  const void* w;  // LayerNorm weight and bias, fp32 or bf16 (w_bf16)
+  const void* b;
+  int w_bf16;
   const float* mean;
   const float* rstd;
   float inv_d;
@@ -523,12 +559,9 @@ __global__ void __launch_bounds__(kThreads) ln_mul_bwd_kernel(BwdArgs a) {
   const int nw = gridDim.x * 4;
   const int c0 = lane * EPT;
   float w[EPT], bb[EPT], dw[EPT], db[EPT];
+  ln_params<EPT>(a.w, a.b, a.w_bf16, c0, w, bb);
 #pragma unroll
-  for (int i = 0; i < EPT; ++i) {
-    w[i] = a.w[c0 + i];
-    bb[i] = a.b[c0 + i];
-    dw[i] = db[i] = 0.f;
-  }
+  for (int i = 0; i < EPT; ++i) dw[i] = db[i] = 0.f;
   const bool cu = HU && a.concat_u, cx = a.concat_x;
   const int col_u = 0, col_x = cu ? 1 : 0, col_z = (cu ? 1 : 0) + (cx ? 1 : 0);
   // Software pipeline: the next row's loads are in flight while this row is
@@ -639,8 +672,8 @@ __global__ void __launch_bounds__(kObThreads, 1) outproj_ln_bwd_kernel(OutBwdArg
   float* const wsum = (float*)(smem + kObSumOff);
   const BwdArgs& a = p.ln;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 15, g = lane >> 4;
-  lnwb[tid] = a.w[tid];
-  lnwb[kObD + tid] = a.b[tid];  // published by the first block's prologue barrier
+  lnwb[tid] = ln_param(a.w, tid, a.w_bf16);
+  lnwb[kObD + tid] = ln_param(a.b, tid, a.w_bf16);  // published by the first block's prologue barrier
   wsum[tid] = wsum[kObD + tid] = 0.f;  // thread t alone adds to entries t and 512 + t
   const int c0 = lane * EPT;
   const float scale = p.g_scale[0] * p.w_scale[0];
@@ -910,15 +943,21 @@ extern "C" int hstu_dropout_mask(int rows, int D, int num_masks, int mask16, flo
   return (int)hipGetLastError();
 }
 
-extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_t ldu, const float* weight,
-                               const float* bias, float eps, int rows, int D, int mul_u_act, int silu_u,
+// LayerNorm weight / bias: fp32, or bf16 read as is (the parameters' own
+// dtype, so a caller needs no conversion per call).
+static bool param_dtype_ok(int t) { return t == HSTU_DTYPE_FP32 || t == HSTU_DTYPE_BF16; }
+// the kernels read a lane's parameters as 16-byte vectors (8 bytes for bf16 at D = 256)
+static bool params_aligned(const void* w, const void* b) { return aligned(w, 16) && aligned(b, 16); }
+
+extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_t ldu, const void* weight,
+                               const void* bias, int param_dtype, float eps, int rows, int D, int mul_u_act, int silu_u,
                                int concat_u, int concat_x, int training, float dropout_ratio, uint64_t seed,
                                int mask16, void* mask, int64_t ldm, void* y, int64_t ldy, int out_dtype,
                                float inv_scale, const float* out_scale, float* mean, float* rstd,
                                hipStream_t stream) {
   if (rows < 0 || D <= 0 || x == nullptr || ldx < D || (u != nullptr && ldu < D) || weight == nullptr ||
       bias == nullptr || mean == nullptr || rstd == nullptr || y == nullptr || mul_u_act < 0 || mul_u_act > 2 ||
-      !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))
+      !(dropout_ratio >= 0.f && dropout_ratio <= 1.f) || !param_dtype_ok(param_dtype))
     return HSTU_E_BAD_ARG;
   if (out_dtype != HSTU_DTYPE_BF16 && out_dtype != HSTU_DTYPE_FP8_E4M3) return HSTU_E_BAD_ARG;
   const int ncols = ncols_of(u, concat_u, concat_x);
@@ -929,7 +968,8 @@ extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_
   const int ept = D / 64;
   const int ysz = out_dtype == HSTU_DTYPE_BF16 ? 2 : 1;
   if (!aligned(x, 2 * ept) || ldx % ept || (u != nullptr && (!aligned(u, 2 * ept) || ldu % ept)) ||
-      !aligned(y, ysz * ept) || ldy % ept || (dropout && (!aligned(mask, ept) || ldm % ept)))
+      !aligned(y, ysz * ept) || ldy % ept || (dropout && (!aligned(mask, ept) || ldm % ept)) ||
+      !params_aligned(weight, bias))
     return HSTU_E_UNSUPPORTED;
   if (rows == 0) return 0;
   FwdArgs a{};
@@ -939,6 +979,7 @@ extern "C" int hstu_ln_mul_fwd(const void* x, int64_t ldx, const void* u, int64_
   a.ldu = ldu;
   a.w = weight;
   a.b = bias;
+  a.w_bf16 = param_dtype == HSTU_DTYPE_BF16;
   a.eps = eps;
   a.inv_d = 1.f / (float)D;
   a.rows = rows;
@@ -965,7 +1006,7 @@ extern "C" int64_t hstu_ln_mul_bwd_workspace_bytes(int rows, int D) {
 }
 
 extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int64_t ldx, const void* u,
-                               int64_t ldu, const float* weight, const float* bias, const float* mean,
+                               int64_t ldu, const void* weight, const void* bias, int param_dtype, const float* mean,
                                const float* rstd, int rows, int D, int mul_u_act, int silu_u, int concat_u,
                                int concat_x, float dropout_ratio, const void* mask, int64_t ldm, void* dx,
                                int64_t lddx, void* du, int64_t lddu, void* y, int64_t ldy, const void* dres,
@@ -974,7 +1015,8 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   if (rows < 0 || D <= 0 || dy == nullptr || x == nullptr || ldx < D || dx == nullptr || lddx < D ||
       (u != nullptr && (ldu < D || du == nullptr || lddu < D)) || weight == nullptr || bias == nullptr ||
       mean == nullptr || rstd == nullptr || dweight == nullptr || dbias == nullptr || mul_u_act < 0 ||
-      mul_u_act > 2 || (mask != nullptr && (ldm < D || !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))))
+      mul_u_act > 2 || (mask != nullptr && (ldm < D || !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))) ||
+      !param_dtype_ok(param_dtype))
     return HSTU_E_BAD_ARG;
   const int ncols = ncols_of(u, concat_u, concat_x);
   if (lddy < (int64_t)ncols * D || (y != nullptr && ldy < (int64_t)ncols * D)) return HSTU_E_BAD_ARG;
@@ -985,7 +1027,8 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   auto ok = [&](const void* p, int64_t ld, int esz) { return aligned(p, esz * ept) && ld % ept == 0; };
   if (!ok(dy, lddy, 2) || !ok(x, ldx, 2) || !ok(dx, lddx, 2) ||
       (u != nullptr && (!ok(u, ldu, 2) || !ok(du, lddu, 2))) || (y != nullptr && !ok(y, ldy, 2)) ||
-      (mask != nullptr && !ok(mask, ldm, 1)) || (dres != nullptr && !ok(dres, lddres, 2)))
+      (mask != nullptr && !ok(mask, ldm, 1)) || (dres != nullptr && !ok(dres, lddres, 2)) ||
+      !params_aligned(weight, bias))
     return HSTU_E_UNSUPPORTED;
   BwdArgs a{};
   a.dy = (const uint16_t*)dy;
@@ -996,6 +1039,7 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   a.ldu = ldu;
   a.w = weight;
   a.b = bias;
+  a.w_bf16 = param_dtype == HSTU_DTYPE_BF16;
   a.mean = mean;
   a.rstd = rstd;
   a.inv_d = 1.f / (float)D;
@@ -1028,15 +1072,17 @@ extern "C" int64_t hstu_outproj_ln_bwd_workspace_bytes(int rows) {
 
 extern "C" int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_scale, const void* w8, int64_t ldw,
                                    const float* w_scale, const void* x, int64_t ldx, const void* u, int64_t ldu,
-                                   const float* weight, const float* bias, const float* mean, const float* rstd,
-                                   int rows, int D, int mul_u_act, int silu_u, float dropout_ratio, const void* mask,
+                                   const void* weight, const void* bias, int param_dtype, const float* mean,
+                                   const float* rstd, int rows, int D, int mul_u_act, int silu_u, float dropout_ratio,
+                                   const void* mask,
                                    int64_t ldm, void* dx, int64_t lddx, void* du, int64_t lddu, float* dweight,
                                    float* dbias, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   if (rows < 0 || g8 == nullptr || w8 == nullptr || g_scale == nullptr || w_scale == nullptr || x == nullptr ||
       u == nullptr || dx == nullptr || du == nullptr || weight == nullptr || bias == nullptr || mean == nullptr ||
       rstd == nullptr || dweight == nullptr || dbias == nullptr || mul_u_act < 0 || mul_u_act > 2 ||
       ldg < kObK || ldw < kObK || ldx < D || ldu < D || lddx < D || lddu < D ||
-      (mask != nullptr && (ldm < D || !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))))
+      (mask != nullptr && (ldm < D || !(dropout_ratio >= 0.f && dropout_ratio <= 1.f))) ||
+      !param_dtype_ok(param_dtype))
     return HSTU_E_BAD_ARG;
   if (D != kObD) return HSTU_E_UNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < hstu_outproj_ln_bwd_workspace_bytes(rows)) return HSTU_E_BAD_ARG;
@@ -1060,6 +1106,7 @@ extern "C" int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_s
   a.ldu = ldu;
   a.w = weight;
   a.b = bias;
+  a.w_bf16 = param_dtype == HSTU_DTYPE_BF16;
   a.mean = mean;
   a.rstd = rstd;
   a.inv_d = 1.f / (float)D;

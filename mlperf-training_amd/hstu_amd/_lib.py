@@ -54,6 +54,8 @@ EXPORTED_SYMBOLS = (
     "hstu_bf16_gemm",
     "hstu_cast_fp8_amax_partials",
     "hstu_cast_fp8_amax",
+    "hstu_quantize_e4m3_unit",
+    "hstu_fp8_site_update",
     "hstu_cast_fp8_amax_colsum_workspace_bytes",
     "hstu_cast_fp8_amax_colsum",
     "hstu_wgrad_split",
@@ -132,6 +134,8 @@ _SIGNATURES = {
     "hstu_bf16_gemm": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _vp]),
     "hstu_cast_fp8_amax_partials": (_i64, [_i64]),
     "hstu_cast_fp8_amax": (_i32, [_i32, _vp, _i64, _vp, _i32, _f32, _vp, _vp, _i64, _vp]),
+    "hstu_quantize_e4m3_unit": (_i32, [_i32, _vp, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "hstu_fp8_site_update": (_i32, [_vp, _i32, _vp, _f32, _i32, _i32, _f32, _vp, _vp]),
     "hstu_cast_fp8_amax_colsum_workspace_bytes": (_i64, [_i64, _i64]),
     "hstu_wgrad_split": (_i32, [_i64, _i32, _i32, _i32]),
     "hstu_wgrad_workspace_bytes": (_i64, [_i64, _i32, _i32, _i32]),
@@ -146,7 +150,7 @@ _SIGNATURES = {
     "hstu_dropout_mask": (_i32, [_i32, _i32, _i32, _i32, _f32, _u64, _vp, _i64, _vp]),
     "hstu_ln_mul_fwd": (
         _i32,
-        [_vp, _i64, _vp, _i64, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _u64, _i32,
+        [_vp, _i64, _vp, _i64, _vp, _vp, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _u64, _i32,
          _vp, _i64, _vp, _i64, _i32, _f32, _vp, _vp, _vp, _vp],
     ),
     "hstu_ln_mul_bwd_workspace_bytes": (_i64, [_i32, _i32]),
@@ -165,14 +169,14 @@ _SIGNATURES = {
     "hstu_dequantize_do_e4m3_blk": (_i32, [_vp, _vp, _i64, _i32, _i32, _vp, _i64, _vp]),
     "hstu_ln_mul_bwd": (
         _i32,
-        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+        [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
          _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
     ),
     "hstu_outproj_ln_bwd_workspace_bytes": (_i64, [_i32]),
     "hstu_outproj_ln_bwd": (
         _i32,
-        [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _f32,
-         _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
+        [_vp, _i64, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32,
+         _f32, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp],
     ),
 }
 

@@ -153,10 +153,11 @@ def _code(dtype: torch.dtype) -> int:
 
 
 def quantize_row_major(value: torch.Tensor, inv_scale: torch.Tensor, dtype: Optional[torch.dtype] = None,
-                       limit: Optional[float] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                       limit: Optional[float] = None, partials: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
     """(fp8(clamp(value * inv_scale, +-limit)), amax(|value|)) in one pass;
-    the amax is of the input, before scaling.  dtype / limit default to the
-    process default's gradient format."""
+    the amax is of the input, before scaling (with ``partials``, its
+    per-8192-element block maxima instead, for ``GradScaleSite.update``).
+    dtype / limit default to the process default's gradient format."""
     gdt, glim = grad_dtype_and_limit()
     dtype = gdt if dtype is None else dtype
     limit = glim if limit is None else limit
@@ -172,13 +173,13 @@ def quantize_row_major(value: torch.Tensor, inv_scale: torch.Tensor, dtype: Opti
     parts = int(_lib.fn("hstu_cast_fp8_amax_partials")(n))
     partial = torch.empty(max(parts, 1), dtype=torch.float32, device=src.device)
     if n == 0:
-        return out, torch.zeros((), dtype=torch.float32, device=src.device)
+        return out, torch.zeros(1 if partials else (), dtype=torch.float32, device=src.device)
     inv = inv_scale.to(torch.float32).reshape(-1)[:1].contiguous()
     st = _lib.fn("hstu_cast_fp8_amax")(
         _code(src.dtype), src.data_ptr(), n, inv.data_ptr(), _code(dtype), float(limit), out.data_ptr(),
         partial.data_ptr(), parts, torch.cuda.current_stream(src.device).cuda_stream)
     _lib.check(st, "hstu_cast_fp8_amax")
-    return out, partial[:parts].amax()
+    return out, (partial[:parts] if partials else partial[:parts].amax())
 
 
 def quantize_amax_colsum(value: torch.Tensor, inv_scale: torch.Tensor, pad_to: int = 1,
@@ -268,6 +269,30 @@ class GradScaleSite:
         self.state[0:3].copy_(torch.cat([s, s.reciprocal(), torch.zeros_like(s)]))
         self.live = True
 
+    def update(self, amax_values: torch.Tensor, cfg: Fp8BackwardConfig, roll: bool,
+               snapshot: bool = False) -> Optional[torch.Tensor]:
+        """``fold`` of the max of ``amax_values`` (a cast's per-block partials
+        or one amax), then, with ``snapshot``, a copy of the scale in use, then
+        ``roll`` when ``roll`` -- in one device launch (``hstu_fp8_site_update``),
+        the same arithmetic as those methods.  Returns the snapshot."""
+        vals = amax_values.reshape(-1)
+        if not self.state.is_cuda:  # host tensors (the policy's CPU tests): the same steps in torch
+            self.fold(vals.amax(), cfg)
+            snap = self.scale.clone() if snapshot else None
+            if roll:
+                self.roll(cfg)
+            return snap
+        if vals.dtype != torch.float32 or not vals.is_contiguous():
+            vals = vals.to(torch.float32).contiguous()
+        snap = torch.empty(1, dtype=torch.float32, device=self.state.device) if snapshot else None
+        st = _lib.fn("hstu_fp8_site_update")(
+            vals.data_ptr(), vals.numel(), self.state.data_ptr(), float(cfg.grad_limit), int(self.live), int(roll),
+            float(cfg.margin / cfg.grad_limit), _lib.ptr(snap), torch.cuda.current_stream(vals.device).cuda_stream)
+        _lib.check(st, "hstu_fp8_site_update")
+        if roll:
+            self.live = True
+        return snap
+
     def admit(self, cfg: Fp8BackwardConfig) -> Tuple[bool, bool]:
         """Count this call: (quantize it?, does it end a window?)."""
         self.calls += 1
@@ -338,25 +363,38 @@ def quantize_gradient(site: str, gradient: torch.Tensor, discriminator: Optional
     ctl = _registry.get(site, discriminator, gradient.device)
     quantize, ends_window = ctl.admit(cfg)
     if not quantize:
-        ctl.fold(gradient.detach().abs().amax(), cfg)
-        if ends_window:
-            ctl.roll(cfg)
+        ctl.update(gradient.detach().abs().amax(), cfg, roll=ends_window)
         return None
-    payload, amax = quantize_row_major(gradient, ctl.inv_scale, cfg.grad_dtype, cfg.grad_limit)
-    ctl.fold(amax, cfg)
-    decode = ctl.scale
-    if ends_window:
-        if snapshot_decode_scale:
-            decode = decode.clone()
-        ctl.roll(cfg)
-    return payload, decode
+    payload, partial = quantize_row_major(gradient, ctl.inv_scale, cfg.grad_dtype, cfg.grad_limit, partials=True)
+    snap = ctl.update(partial, cfg, roll=ends_window, snapshot=ends_window and snapshot_decode_scale)
+    return payload, (snap if snap is not None else ctl.scale)
 
 
 def quantize_weight(weight: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """e4m3 at unit margin: scale = amax / 448 on the device, cast at 1 / scale."""
-    amax = weight.detach().abs().amax().float().clamp_min(1.0e-30)
-    scale = (amax / E4M3_MAX).reshape(1)
-    q, _ = quantize_row_major(weight, 1.0 / scale, dtype=E4M3, limit=E4M3_MAX)
+    """e4m3 at unit margin: scale = max(amax, 1e-30) / 448 on the device, cast
+    at 1 / scale (``quantize_weight``, ``ops/triton/bwd_fp8.py:1157-1175``), in
+    two launches (``hstu_quantize_e4m3_unit``; bitwise equal to the torch
+    expression ``weight.abs().amax().float().clamp_min(1e-30) / 448``, which
+    multiplies by fp32(1 / 448), and the cast at its reciprocal)."""
+    src = weight.detach()
+    if src.dtype not in (torch.bfloat16, torch.float32):
+        src = src.float()
+    if not src.is_contiguous() or src.data_ptr() % 16:
+        src = src.contiguous()
+    n = src.numel()
+    if n == 0 or n % 32:
+        amax = src.abs().amax().float().clamp_min(1.0e-30)
+        scale = (amax / E4M3_MAX).reshape(1)
+        q, _ = quantize_row_major(weight, 1.0 / scale, dtype=E4M3, limit=E4M3_MAX)
+        return q, scale
+    q = torch.empty(src.shape, dtype=E4M3, device=src.device)
+    scale = torch.empty(1, dtype=torch.float32, device=src.device)
+    parts = int(_lib.fn("hstu_cast_fp8_amax_partials")(n))
+    partial = torch.empty(parts, dtype=torch.float32, device=src.device)
+    st = _lib.fn("hstu_quantize_e4m3_unit")(
+        _code(src.dtype), src.data_ptr(), n, q.data_ptr(), scale.data_ptr(), partial.data_ptr(), parts,
+        torch.cuda.current_stream(src.device).cuda_stream)
+    _lib.check(st, "hstu_quantize_e4m3_unit")
     return q, scale
 
 
@@ -486,16 +524,12 @@ def uvqk_projection_backward(
     ctl = _registry.get(site, weight.data_ptr() if per_layer else None, dz.device)
     quantize, ends_window = ctl.admit(cfg)
     if not quantize:
-        ctl.fold(dz.detach().abs().amax(), cfg)
-        if ends_window:
-            ctl.roll(cfg)
+        ctl.update(dz.detach().abs().amax(), cfg, roll=ends_window)
         return None
     dz8, amax, colsum = quantize_amax_colsum(dz, ctl.inv_scale, dtype=E5M2)
-    ctl.fold(amax, cfg)
     # decode with the scale the payload was cast with (a refresh rewrites the live one)
-    grad_scale = ctl.scale.clone() if ends_window else ctl.scale
-    if ends_window:
-        ctl.roll(cfg)
+    snap = ctl.update(amax, cfg, roll=ends_window, snapshot=ends_window)
+    grad_scale = snap if snap is not None else ctl.scale
     w8, w_scale = quantize_weight(weight)
     sx = None
     if (uvqk_wgrad_fp8t(cfg) and normed_x_fp8_t is not None and normed_x_fp8_t.dtype == E4M3

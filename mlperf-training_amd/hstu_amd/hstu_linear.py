@@ -94,10 +94,20 @@ def _check_d(D: int) -> None:
         raise NotImplementedError(f"feature dim {D} not served (D in {SERVED_D})")
 
 
-def _param(t: Optional[torch.Tensor], D: int, fill: float, device) -> torch.Tensor:
-    if t is None:
-        return torch.full((D,), fill, dtype=torch.float32, device=device)
-    return t.detach().to(torch.float32).contiguous()
+def _params(weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], D: int, device):
+    """(weight, bias, param dtype code) for the LayerNorm kernels: bf16 or fp32
+    parameters go as they are (no conversion kernel per call); anything else,
+    or a mix of the two, as fp32 copies."""
+    w = torch.ones((D,), dtype=torch.float32, device=device) if weight is None else weight.detach()
+    b = torch.zeros((D,), dtype=torch.float32, device=device) if bias is None else bias.detach()
+    if w.dtype == b.dtype and w.dtype in (torch.bfloat16, torch.float32):
+        w, b = w.contiguous(), b.contiguous()
+    else:
+        w, b = w.to(torch.float32).contiguous(), b.to(torch.float32).contiguous()
+    # the kernels read them as 16-byte vectors
+    w = w if w.data_ptr() % 16 == 0 else w.clone()
+    b = b if b.data_ptr() % 16 == 0 else b.clone()
+    return w, b, _lib.HSTU_DTYPE_BF16 if w.dtype == torch.bfloat16 else _lib.HSTU_DTYPE_FP32
 
 
 def _seed(seed: Optional[int], training: bool) -> int:
@@ -155,10 +165,9 @@ def _ln_fwd(x, u, weight, bias, eps, dropout_ratio, training, silu_u, concat_u, 
     mask = torch.empty((N, D), dtype=torch.int8, device=x.device) if dropout else None
     if N == 0:
         return y, mean, rstd, mask
-    w = _param(weight, D, 1.0, x.device)
-    b = _param(bias, D, 0.0, x.device)
+    w, b, pd = _params(weight, bias, D, x.device)
     st = _lib.fn("hstu_ln_mul_fwd")(
-        x.data_ptr(), x.stride(0), _lib.ptr(u), 0 if u is None else u.stride(0), w.data_ptr(), b.data_ptr(),
+        x.data_ptr(), x.stride(0), _lib.ptr(u), 0 if u is None else u.stride(0), w.data_ptr(), b.data_ptr(), pd,
         float(eps), N, D, _ACT[act], int(bool(silu_u)), int(cu), int(bool(concat_x)), int(dropout),
         float(dropout_ratio), int(seed) & 0xFFFFFFFFFFFFFFFF, int(mask16), _lib.ptr(mask), D,
         y.data_ptr(), y.stride(0), _lib.HSTU_DTYPE_FP8_E4M3 if output_fp8 else _lib.HSTU_DTYPE_BF16,
@@ -223,8 +232,7 @@ def _ln_bwd(dy, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, con
     y = torch.empty((N, ncols * D), dtype=x.dtype, device=x.device) if compute_y else None
     dw = torch.empty((D,), dtype=torch.float32, device=x.device)
     db = torch.empty((D,), dtype=torch.float32, device=x.device)
-    w = _param(weight, D, 1.0, x.device)
-    b = _param(bias, D, 0.0, x.device)
+    w, b, pd = _params(weight, bias, D, x.device)
     if mask is not None:
         mask = _rows(mask)
     if dres is not None:
@@ -236,7 +244,7 @@ def _ln_bwd(dy, x, u, weight, bias, mean, rstd, dropout_ratio, mask, silu_u, con
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     st = _lib.fn("hstu_ln_mul_bwd")(
         dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), _lib.ptr(u), 0 if u is None else u.stride(0),
-        w.data_ptr(), b.data_ptr(), mean.contiguous().data_ptr(), rstd.contiguous().data_ptr(), N, D, _ACT[act],
+        w.data_ptr(), b.data_ptr(), pd, mean.contiguous().data_ptr(), rstd.contiguous().data_ptr(), N, D, _ACT[act],
         int(bool(silu_u)), int(cu), int(bool(concat_x)), float(dropout_ratio), _lib.ptr(mask),
         0 if mask is None else mask.stride(0), dx.data_ptr(), dx.stride(0), _lib.ptr(du),
         0 if du is None else du.stride(0), _lib.ptr(y), 0 if y is None else y.stride(0), _lib.ptr(dres),
@@ -261,8 +269,7 @@ def _outproj_ln_bwd(g8, g_scale, w8, w_scale, x, u, weight, bias, mean, rstd, dr
     du = _alloc_du(u, du_row_width)
     dw = torch.empty((D,), dtype=torch.float32, device=x.device)
     db = torch.empty((D,), dtype=torch.float32, device=x.device)
-    w = _param(weight, D, 1.0, x.device)
-    b = _param(bias, D, 0.0, x.device)
+    w, b, pd = _params(weight, bias, D, x.device)
     if mask is not None:
         mask = _rows(mask)
     g8 = _rows(g8)  # column slices stay in place (row stride = ldg)
@@ -273,7 +280,7 @@ def _outproj_ln_bwd(g8, g_scale, w8, w_scale, x, u, weight, bias, mean, rstd, dr
     ws = torch.empty((nbytes,), dtype=torch.uint8, device=x.device)
     st = _lib.fn("hstu_outproj_ln_bwd")(
         g8.data_ptr(), g8.stride(0), gs.data_ptr(), w8.data_ptr(), w8.stride(0), ws_.data_ptr(), x.data_ptr(),
-        x.stride(0), u.data_ptr(), u.stride(0), w.data_ptr(), b.data_ptr(), mean.contiguous().data_ptr(),
+        x.stride(0), u.data_ptr(), u.stride(0), w.data_ptr(), b.data_ptr(), pd, mean.contiguous().data_ptr(),
         rstd.contiguous().data_ptr(), N, D, _ACT[act], int(bool(silu_u)), float(dropout_ratio), _lib.ptr(mask),
         0 if mask is None else mask.stride(0), dx.data_ptr(), dx.stride(0), du.data_ptr(), du.stride(0),
         dw.data_ptr(), db.data_ptr(), ws.data_ptr(), nbytes, _stream(x))

@@ -50,8 +50,8 @@ def test_controller_warmup_publish_refresh(monkeypatch):
 
     cfg = B.Fp8BackwardConfig(enabled=True, warmup_calls=2, refresh_calls=3)
     monkeypatch.setattr(B, "quantize_row_major",
-                        lambda v, inv, dtype=None, limit=None: O.cast_amax(v, float(inv.reshape(-1)[0]),
-                                                                            dtype or E5M2, limit or 57344.0))
+                        lambda v, inv, dtype=None, limit=None, partials=False: O.cast_amax(
+                            v, float(inv.reshape(-1)[0]), dtype or E5M2, limit or 57344.0))
     B.reset_sites()
     g = [torch.full((4, 128), float(a)) for a in (2.0, 3.0, 1.0, 9.0, 4.0, 1.0)]
     assert B.quantize_gradient("site", g[0], config=cfg) is None
@@ -341,3 +341,51 @@ def test_oracle_wgrad_closed_forms():
     hot = torch.zeros(50, 5)
     hot[torch.arange(5) * 3, torch.arange(5)] = 1.0                        # token 3c -> column c
     assert torch.allclose(O.wgrad(a, hot, 2.0, 0.5), a.double()[torch.arange(5) * 3].t())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,dtype,zero", [((1536, 512), torch.bfloat16, False), ((512, 2048), torch.bfloat16, False),
+                                              ((256, 96), torch.float32, False), ((128, 64), torch.bfloat16, True)])
+def test_quantize_weight_two_launches_bitwise(hip_lib, shape, dtype, zero):
+    """hstu_quantize_e4m3_unit (block maxima, then scale + cast in one
+    launch) equals the torch expression it replaces bit for bit: scale =
+    amax.clamp_min(1e-30) / 448 and the cast at 1 / scale (an all-zero weight
+    takes the clamp)."""
+    import hstu_amd.bwd_fp8 as B
+
+    g = torch.Generator(device="cuda").manual_seed(sum(shape))
+    w = (torch.randn(shape, device="cuda", generator=g) * 0.05).to(dtype)
+    if zero:
+        w.zero_()
+    q, s = B.quantize_weight(w)
+    amax = w.abs().amax().float().clamp_min(1.0e-30)
+    s_ref = (amax / B.E4M3_MAX).reshape(1)
+    q_ref, _ = B.quantize_row_major(w, 1.0 / s_ref, dtype=E4M3, limit=B.E4M3_MAX)
+    assert torch.equal(s, s_ref)
+    assert torch.equal(q.view(torch.uint8), q_ref.view(torch.uint8))
+
+
+@pytest.mark.gpu
+def test_site_update_matches_the_policy_steps(hip_lib):
+    """hstu_fp8_site_update (one launch) against GradScaleSite's own torch
+    steps (fold, snapshot, roll) on a copy of the state, over a sequence of
+    calls: warm-up, publish, overflow, refresh with and without a snapshot;
+    states and snapshots bitwise equal."""
+    import hstu_amd.bwd_fp8 as B
+
+    cfg = B.Fp8BackwardConfig(enabled=True)
+    a = B.GradScaleSite(torch.device("cuda"))
+    b = B.GradScaleSite(torch.device("cuda"))
+    g = torch.Generator(device="cuda").manual_seed(5)
+    seq = [(0.5, False, False), (3.0, True, False), (1.0, False, True), (1e6, False, False), (0.25, True, True),
+           (7.0, False, False), (0.0, True, False)]
+    for peak, roll, snap in seq:
+        parts = torch.rand(37, device="cuda", generator=g) * peak
+        got = a.update(parts, cfg, roll=roll, snapshot=snap)
+        b.fold(parts.amax(), cfg)
+        want = b.scale.clone() if snap else None
+        if roll:
+            b.roll(cfg)
+        assert torch.equal(a.state, b.state) and a.live == b.live
+        assert (got is None) == (want is None) and (got is None or torch.equal(got, want))
+    assert int(a.overflow_windows) >= 1

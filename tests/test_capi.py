@@ -119,7 +119,8 @@ def test_ln_mul_entry_points_reject_before_launch():
     X, W = 4096, 8192  # fake device addresses: none of these calls may launch
 
     def f(**kw):
-        a = dict(x=X, ldx=512, u=X, ldu=512, w=W, b=W, eps=1e-6, rows=64, D=512, act=1, silu_u=1, cu=1, cx=1,
+        a = dict(x=X, ldx=512, u=X, ldu=512, w=W, b=W, pdt=lib.HSTU_DTYPE_BF16, eps=1e-6, rows=64, D=512, act=1,
+                 silu_u=1, cu=1, cx=1,
                  training=0, ratio=0.0, seed=0, mask16=0, mask=None, ldm=0, y=X, ldy=1536, odt=0, inv=1.0,
                  out_scale=None, mean=W, rstd=W, stream=None)
         a.update(kw)
@@ -133,13 +134,16 @@ def test_ln_mul_entry_points_reject_before_launch():
     assert f(training=1, ratio=1.5, mask=X, ldm=512) == lib.HSTU_E_BAD_ARG
     assert f(x=X + 2) == lib.HSTU_E_UNSUPPORTED  # rows not 16-byte aligned
     assert f(rows=-1) == lib.HSTU_E_BAD_ARG
+    assert f(pdt=lib.HSTU_DTYPE_FP8_E4M3) == lib.HSTU_E_BAD_ARG  # LayerNorm parameters are fp32 or bf16
+    assert f(w=W + 8) == lib.HSTU_E_UNSUPPORTED  # parameters are read as 16-byte vectors
     mask = lib.fn("hstu_dropout_mask")
     assert mask(64, 512, 4, 0, 0.3, 1, X, 512, None) == lib.HSTU_E_BAD_ARG
     assert mask(64, 320, 1, 0, 0.3, 1, X, 320, None) == lib.HSTU_E_UNSUPPORTED
     bwd = lib.fn("hstu_ln_mul_bwd")
 
     def g(**kw):
-        a = dict(dy=X, lddy=1536, x=X, ldx=512, u=X, ldu=512, w=W, b=W, mean=W, rstd=W, rows=64, D=512, act=1,
+        a = dict(dy=X, lddy=1536, x=X, ldx=512, u=X, ldu=512, w=W, b=W, pdt=lib.HSTU_DTYPE_FP32, mean=W, rstd=W,
+                 rows=64, D=512, act=1,
                  silu_u=1, cu=1, cx=1, ratio=0.0, mask=None, ldm=0, dx=X, lddx=512, du=X, lddu=512, y=None, ldy=0,
                  dres=None, lddres=0, dw=W, db=W, ws=W, wsb=ws(64, 512), stream=None)
         a.update(kw)
@@ -152,6 +156,7 @@ def test_ln_mul_entry_points_reject_before_launch():
     assert g(D=128, ldx=128, ldu=128, lddx=128, lddu=128, lddy=384) == lib.HSTU_E_UNSUPPORTED
     assert g(dres=X, lddres=512) == lib.HSTU_E_BAD_ARG  # a residual gradient only without an x block
     assert g(cx=0, lddy=1024, dres=X, lddres=256) == lib.HSTU_E_BAD_ARG
+    assert g(pdt=7) == lib.HSTU_E_BAD_ARG
 
 
 def test_delta_entry_points_reject_before_launch():
@@ -311,7 +316,8 @@ def test_outproj_ln_bwd_rejects_before_launch():
     X, W = 4096, 8192  # fake device addresses: none of these calls may launch
 
     def g(**kw):
-        a = dict(g8=X, ldg=512, gs=W, w8=X, ldw=512, ws_=W, x=X, ldx=512, u=X, ldu=512, w=W, b=W, mean=W, rstd=W,
+        a = dict(g8=X, ldg=512, gs=W, w8=X, ldw=512, ws_=W, x=X, ldx=512, u=X, ldu=512, w=W, b=W,
+                 pdt=lib.HSTU_DTYPE_BF16, mean=W, rstd=W,
                  rows=64, D=512, act=1, silu_u=1, ratio=0.3, mask=X, ldm=512, dx=X, lddx=512, du=X, lddu=2048,
                  dw=W, db=W, ws=W, wsb=ws(64), stream=None)
         a.update(kw)
@@ -327,6 +333,7 @@ def test_outproj_ln_bwd_rejects_before_launch():
     assert g(D=256, ldx=256, ldu=256, lddx=256, lddu=256, ldm=256) == lib.HSTU_E_UNSUPPORTED
     assert g(x=X + 2) == lib.HSTU_E_UNSUPPORTED  # rows not 16-byte aligned
     assert g(ldg=520) == lib.HSTU_E_UNSUPPORTED  # gradient rows not 16-byte aligned
+    assert g(pdt=lib.HSTU_DTYPE_FP8_E5M2) == lib.HSTU_E_BAD_ARG
 
 
 def test_fp8_pv_forward_declines_long_sequences_before_launch():

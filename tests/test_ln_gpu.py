@@ -271,3 +271,25 @@ def test_ln_bwd_residual_gradient(hip_lib):
     # half a bf16 step (2^-8 relative) of its exact value
     d = (dx.float() - (dx0.float() + dres.to(DEV).float())).abs()
     assert float((d <= 2.0 ** -7 * (dx.float().abs() + dx0.float().abs()) + 1e-6).float().mean()) == 1.0
+
+
+def test_ln_params_bf16_and_fp32_agree(hip_lib):
+    """The LayerNorm kernels read bf16 parameters as they are (param_dtype
+    bf16) and fp32 ones as fp32: the same values give bitwise-equal outputs
+    and gradients (the parameter gradients come back in each parameter's
+    dtype, so they are compared in the first call's), and a mix of the two
+    goes as fp32."""
+    ops = _ops()
+    N, D = 1001, 512
+    x, u, w, b = (t.to(DEV) for t in _inputs(N, D, seed=6))
+    outs = []
+    for ww, bb in ((w, b), (w.float(), b.float()), (w, b.float())):
+        y, mean, rstd, BD, nw, s, mask = ops.triton_layer_norm_mul_dropout_fwd(
+            x, u, ww, bb, 1e-6, 0.3, True, True, True, True, "silu", 5)
+        dy = torch.randn(y.shape, device=DEV, generator=torch.Generator(device=DEV).manual_seed(3)).to(torch.bfloat16)
+        r = ops.triton_layer_norm_mul_dropout_bwd(dy, x, u, ww, bb, mean, rstd, BD, nw, 1e-6, True, 0.3, s, True,
+                                                  True, True, "silu", random_mask=mask)
+        outs.append((y, mean, rstd) + tuple(r[:4]))
+    for other in outs[1:]:
+        for a, c in zip(outs[0], other):
+            assert torch.equal(a, c.to(a.dtype))
