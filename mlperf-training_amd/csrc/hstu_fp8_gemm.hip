@@ -867,9 +867,8 @@ __global__ void __launch_bounds__(256) cast_fp8_amax_kernel(const uint8_t* __res
 __device__ __forceinline__ float max_nan(float a, float b) { return a != a ? a : (b != b || b > a ? b : a); }
 
 // The 32 elements a thread of the 8192-element cast blocks handles, as fp32.
-// (The loads go into an array first: a const vector local initialised by
-// the conditional load compiled, for fp32, to one dword load per chunk whose
-// value filled all four lanes.)
+// Vector elements go through a scalar before __builtin_bit_cast: bit-casting
+// an ext-vector element lvalue reads element 0 whatever the index.
 template <bool IN_F32>
 __device__ __forceinline__ void load32(const uint8_t* __restrict__ x, int64_t n, int64_t e0, float (&v)[32]) {
   constexpr int ES = IN_F32 ? 4 : 2, NL = 32 * ES / 16;
