@@ -225,8 +225,9 @@ int hstu_attn_bwd_fp8(const void* dout8, const void* dout_e8, int64_t dout_row_s
                       hipStream_t stream);
 /*
  * Its two halves, same arguments, run in order on one stream with one
- * workspace: _dkdv writes dk, dv and leaves the e4m3 dS tiles (and the scale
- * maxima) in the workspace; _dq reads them and writes dq and dbias.
+ * workspace: _dkdv writes dk, dv and leaves the e4m3 dS tiles (and the block
+ * schedule, tile prefixes, pre-clamped bias rows and scale maxima) in the
+ * workspace; _dq reads them and writes dq and dbias.
  */
 int hstu_attn_bwd_fp8_dkdv(const void* dout8, const void* dout_e8, int64_t dout_row_stride,
                            const void* q, const void* k, const void* v,

@@ -231,7 +231,7 @@ struct AttnParams {
   float* dbias_part;      // workspace: one bias-gradient row per dQ block [blocks, H, dbias_w]
   const int64_t* dq_base;  // workspace: per-sequence exclusive prefix of 128-query blocks [B + 1]
   int dbias_w;            // floats per row: offsets 0 .. R-1 (causal), -(R-1) .. R-1 (generic masks)
-  const int* sched_items;  // block schedule (build_schedule): [8][sched_cap] (sequence*H + head)
+  const int* sched_items;  // block schedule (schedule_block): [8][sched_cap] (sequence*H + head)
   const int* sched_start;  // [8][sched_cap + 1] first block position of each item on its XCD
   const int* sched_count;  // [8] items per XCD
   int sched_cap;
@@ -290,7 +290,7 @@ struct SeqCtx {
   int L, b, h, blk;
 };
 // Workgroup -> (sequence, head, 128-row block), from the schedule that
-// build_schedule wrote: workgroup i runs on XCD x = i % 8 and takes the
+// schedule_block wrote: workgroup i runs on XCD x = i % 8 and takes the
 // (i / 8)-th block of that XCD's list.  heavy_last: the block with the most
 // key tiles is the last one of its sequence (forward, dQ) rather than the
 // first (dK/dV); each item's blocks run heaviest first.  False = no work.
@@ -2736,8 +2736,8 @@ __device__ __forceinline__ int64_t dq_blocks(const int64_t* seq_offsets, int b, 
 // base[b] = sum over sequences b' < b of f8_tiles(min(length, N)); base[B] =
 // the total; dq_base the same prefix of 128-query blocks (the bias-gradient
 // rows); and the two scale maxima (f8max) reset for f8_scale_max.
-__global__ void __launch_bounds__(1024) f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base,
-                                                       int64_t* dq_base, unsigned* f8max) {
+__device__ void f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base, int64_t* dq_base,
+                               unsigned* f8max) {
   __shared__ int64_t part[1024];
   if (threadIdx.x < 2) f8max[threadIdx.x] = 0u;
   seq_exclusive_scan(B, [&](int b) { return f8_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); },
@@ -2799,12 +2799,12 @@ __global__ void convert_q8_bf16(const uint8_t* q8, int64_t q_rs, const int64_t* 
   }
 }
 
-// bias table [H, 2R-1] -> [H, bias_ext_len(N)] with entry off+N+127 = bias(clamp(off)) * -log2(e)
-__global__ void build_bias_ext(const float* bias, int H, int R, int N, float* ext) {
+// bias table [H, 2R-1] -> [H, bias_ext_len(N)] with entry off+N+127 =
+// bias(clamp(off)) * -log2(e): block bx of nbx of head h
+__device__ void build_bias_ext(const float* bias, int R, int N, float* ext, int h, int bx, int nbx) {
   const int len = bias_ext_len(N);
-  const int h = blockIdx.y;
   const int R1 = R - 1;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < len; i += gridDim.x * blockDim.x) {
+  for (int i = bx * blockDim.x + threadIdx.x; i < len; i += nbx * blockDim.x) {
     const int off = i - N - 127;
     ext[(int64_t)h * len + i] = bias[(int64_t)h * (2 * R - 1) + min(max(off, -R1), R1) + R1] * -kLog2e;
   }
@@ -2832,7 +2832,7 @@ inline int64_t sched_ints(int B, int H) {
   return 8 * cap + 8 * (cap + 1) + 8 + 2 * (int64_t)B;
 }
 
-__global__ void __launch_bounds__(1024) build_schedule(const int64_t* seq_offsets, int B, int H, int N, int* ws) {
+__device__ void schedule_block(const int64_t* seq_offsets, int B, int H, int N, int* ws) {
   const int cap = sched_cap(B, H);
   int* items = ws;
   int* start = items + 8 * cap;
@@ -2904,14 +2904,12 @@ __global__ void __launch_bounds__(1024) build_schedule(const int64_t* seq_offset
   }
 }
 
-// Launch build_schedule into ws (sched_ints(B, H) ints) and point p at it.
-hipError_t schedule(AttnParams& p, const int64_t* seq_offsets, int B, int H, int N, int* ws, hipStream_t stream) {
-  hipLaunchKernelGGL(build_schedule, dim3(1), dim3(kSchedBins), 0, stream, seq_offsets, B, H, N, ws);
+// Point p at the block schedule in ws (sched_ints(B, H) ints).
+void use_schedule(AttnParams& p, int B, int H, int* ws) {
   p.sched_cap = sched_cap(B, H);
   p.sched_items = ws;
   p.sched_start = ws + 8 * p.sched_cap;
   p.sched_count = p.sched_start + 8 * (p.sched_cap + 1);
-  return hipGetLastError();
 }
 // grid covering every XCD's longest possible list
 int sched_grid(int B, int H, int N) { return 8 * sched_cap(B, H) * ((N + 127) / 128); }
@@ -3014,18 +3012,86 @@ hipError_t dbias_reduce(const AttnParams& p, float* chunks, float scale, float* 
 // Rows of a sequence beyond max_seq_len are not computed by the kernels (the
 // reference's padded path drops them, so their output is zero); zero them so
 // every output element is written.  Exits at once when every L <= N.
-__global__ void zero_rows_beyond_n(const int64_t* seq_offsets, int N, int width, uint16_t* a, int64_t a_rs,
-                                   uint16_t* b, int64_t b_rs, uint16_t* c, int64_t c_rs) {
-  const int s = blockIdx.y;
+// Block bx of nbx of sequence s.
+__device__ void zero_rows_beyond_n(const int64_t* seq_offsets, int N, int width, uint16_t* a, int64_t a_rs,
+                                   uint16_t* b, int64_t b_rs, uint16_t* c, int64_t c_rs, int s, int bx, int nbx) {
   const int64_t start = seq_offsets[s];
   const int L = (int)(seq_offsets[s + 1] - start);
-  for (int row = N + blockIdx.x; row < L; row += gridDim.x) {
+  for (int row = N + bx; row < L; row += nbx) {
     for (int col = threadIdx.x; col < width; col += blockDim.x) {
       a[(start + row) * a_rs + col] = 0;
       if (b) b[(start + row) * b_rs + col] = 0;
       if (c) c[(start + row) * c_rs + col] = 0;
     }
   }
+}
+
+// The small set-up work of an attention call in one launch of 1024-thread
+// blocks, by block role (each block takes one role, so every barrier inside
+// a role is block-uniform): the block schedule (one block, if sched); the FP8
+// backward's tile and dQ-block prefixes and the scale-maximum reset (one
+// block, if tile_base); the pre-clamped bias rows (bias_bx blocks per head,
+// if bias_ext); rows past N zeroed in up to three outputs (kPrepZero blocks
+// per sequence, if z[0]).  The roles touch disjoint memory.
+constexpr int kPrepZero = 4;
+struct PrepArgs {
+  const int64_t* seq_offsets;
+  int B, H, N;
+  int* sched;  // null: no schedule block
+  int64_t* tile_base;
+  int64_t* dq_base;
+  unsigned* f8max;  // tile_base null: no prefix block
+  const float* bias;
+  float* bias_ext;  // null: no bias blocks
+  int R, bias_bx;
+  int width;
+  uint16_t* z[3];  // z[0] null: no zeroing blocks
+  int64_t zrs[3];
+};
+int prep_blocks(const PrepArgs& a) {
+  return (a.sched ? 1 : 0) + (a.tile_base ? 1 : 0) + (a.bias_ext ? a.H * a.bias_bx : 0) +
+         (a.z[0] ? kPrepZero * a.B : 0);
+}
+__global__ void __launch_bounds__(1024) attn_prep(PrepArgs a) {
+  int blk = (int)blockIdx.x;
+  if (a.sched) {
+    if (blk == 0) {
+      schedule_block(a.seq_offsets, a.B, a.H, a.N, a.sched);
+      return;
+    }
+    blk -= 1;
+  }
+  if (a.tile_base) {
+    if (blk == 0) {
+      f8_tile_prefix(a.seq_offsets, a.B, a.N, a.tile_base, a.dq_base, a.f8max);
+      return;
+    }
+    blk -= 1;
+  }
+  if (a.bias_ext) {
+    const int nb = a.H * a.bias_bx;
+    if (blk < nb) {
+      build_bias_ext(a.bias, a.R, a.N, a.bias_ext, blk / a.bias_bx, blk % a.bias_bx, a.bias_bx);
+      return;
+    }
+    blk -= nb;
+  }
+  if (a.z[0] && blk < kPrepZero * a.B)
+    zero_rows_beyond_n(a.seq_offsets, a.N, a.width, a.z[0], a.zrs[0], a.z[1], a.zrs[1], a.z[2], a.zrs[2],
+                       blk / kPrepZero, blk % kPrepZero, kPrepZero);
+}
+hipError_t launch_prep(const PrepArgs& a, hipStream_t stream) {
+  const int n = prep_blocks(a);
+  if (n > 0) hipLaunchKernelGGL(attn_prep, dim3(n), dim3(1024), 0, stream, a);
+  return hipGetLastError();
+}
+PrepArgs prep_args(const int64_t* seq_offsets, int B, int H, int N) {
+  PrepArgs a{};
+  a.seq_offsets = seq_offsets;
+  a.B = B;
+  a.H = H;
+  a.N = N;
+  return a;
 }
 
 // ---------------------------------------------------------------- launch
@@ -3131,8 +3197,15 @@ int fwd_launch(int dtype, const void* q, const void* k, const void* v, int64_t q
   const int grid = sched_grid(B, H, max_seq_len);
   p.bias = attn_bias;
   p.bias_R = bias_R;
-  hipError_t e = schedule(p, seq_offsets, B, H, max_seq_len, sched_ws, stream);
+  // the block schedule, and the rows past max_seq_len zeroed, in one launch
+  PrepArgs pa = prep_args(seq_offsets, B, H, max_seq_len);
+  pa.sched = sched_ws;
+  pa.width = H * D;
+  pa.z[0] = p.out;
+  pa.zrs[0] = p.o_rs;
+  hipError_t e = launch_prep(pa, stream);
   if (e != hipSuccess) return (int)e;
+  use_schedule(p, B, H, sched_ws);
 #define HSTU_FWD(DD, F8, G, BB) launch(hstu_fwd_kernel<DD, F8, G, BB>, FwdCfg<DD, F8>::LDS, grid, p, stream)
 #define HSTU_FWD_B(DD, F8, G) (has_bias ? HSTU_FWD(DD, F8, G, true) : HSTU_FWD(DD, F8, G, false))
   const bool has_bias = attn_bias != nullptr;
@@ -3154,8 +3227,6 @@ int fwd_launch(int dtype, const void* q, const void* k, const void* v, int64_t q
 #undef HSTU_FWD_B
 #undef HSTU_FWD
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
-                     p.out, p.o_rs, (uint16_t*)nullptr, (int64_t)0, (uint16_t*)nullptr, (int64_t)0);
   return (int)hipGetLastError();
 }
 }  // namespace
@@ -3337,8 +3408,26 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
     if (lds > kMaxLdsBytes) return HSTU_E_UNSUPPORTED;
   }
   uint8_t* ws = (uint8_t*)workspace;
-  e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)(ws + wl.sched), stream);
+  // the block schedule, the pre-clamped bias rows (dK/dV) and the rows past
+  // max_seq_len of this half's outputs zeroed, in one launch
+  PrepArgs pa = prep_args(seq_offsets, B, H, max_seq_len);
+  pa.sched = (int*)(ws + wl.sched);
+  if ((parts & kBwdDkdv) && has_bias) {
+    pa.bias = attn_bias;
+    pa.R = bias_R;
+    pa.bias_ext = (float*)(ws + wl.bias_ext);
+    pa.bias_bx = (bias_ext_len(max_seq_len) + 1023) / 1024;
+  }
+  pa.width = H * D;
+  pa.z[0] = (parts & kBwdDq) ? p.dq : p.dk;
+  pa.zrs[0] = (parts & kBwdDq) ? p.dq_rs : p.dk_rs;
+  pa.z[1] = (parts & kBwdDkdv) ? p.dk : (uint16_t*)nullptr;
+  pa.zrs[1] = p.dk_rs;
+  pa.z[2] = (parts & kBwdDkdv) ? p.dv : (uint16_t*)nullptr;
+  pa.zrs[2] = p.dv_rs;
+  e = launch_prep(pa, stream);
   if (e != hipSuccess) return (int)e;
+  use_schedule(p, B, H, (int*)(ws + wl.sched));
   if (!generic) {
     // dS tiles pass from the dK/dV kernel to the dQ kernel through the workspace
     p.ds_base = (const int64_t*)(ws + wl.ds_base);
@@ -3347,11 +3436,7 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
                        (int64_t*)(ws + wl.ds_base), has_bias ? (int64_t*)(ws + wl.dq_base) : (int64_t*)nullptr);
   }
   if (parts & kBwdDkdv) {
-    if (has_bias) {
-      p.bias_ext = (const float*)(ws + wl.bias_ext);
-      hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
-                         attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
-    }
+    if (has_bias) p.bias_ext = (const float*)(ws + wl.bias_ext);
     if (dtype == HSTU_DTYPE_FP8_E4M3) {
       p.q16 = ws + wl.q16;
       hipLaunchKernelGGL(convert_q8_bf16, dim3(1024), dim3(256), 0, stream, (const uint8_t*)q, q_row_stride,
@@ -3411,10 +3496,6 @@ int attn_bwd_impl(int parts, int dtype, const void* dout, int64_t dout_row_strid
       if (e != hipSuccess) return (int)e;
     }
   }
-  hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
-                     (parts & kBwdDq) ? p.dq : p.dk, (parts & kBwdDq) ? p.dq_rs : p.dk_rs,
-                     (parts & kBwdDkdv) ? p.dk : (uint16_t*)nullptr, p.dk_rs,
-                     (parts & kBwdDkdv) ? p.dv : (uint16_t*)nullptr, p.dv_rs);
   return (int)hipGetLastError();
 }
 }  // namespace
@@ -3577,22 +3658,42 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
   p.ds_base = (const int64_t*)(ws + wl.base);
   p.ds_ws = ws + wl.tiles;
   const int grid = sched_grid(B, H, max_seq_len);
-  hipError_t e = schedule(p, seq_offsets, B, H, max_seq_len, (int*)(ws + wl.sched), stream);
-  if (e != hipSuccess) return (int)e;
+  // One launch for the set-up: with the dK/dV half, the block schedule, the
+  // tile and dQ-block prefixes (and the scale-maximum reset) and the
+  // pre-clamped bias rows, all read by both halves (the dQ half, which runs
+  // after it on the same workspace, builds none of them); and the rows past
+  // max_seq_len of this half's outputs zeroed.
+  PrepArgs pa = prep_args(seq_offsets, B, H, max_seq_len);
   if (parts & kBwdDkdv) {
-    // tile prefix and scale maxima, read by both halves
-    hipLaunchKernelGGL(f8_tile_prefix, dim3(1), dim3(1024), 0, stream, seq_offsets, B, max_seq_len,
-                       (int64_t*)(ws + wl.base), (int64_t*)(ws + wl.dq_base), (unsigned*)(ws + wl.maxv));
+    pa.sched = (int*)(ws + wl.sched);
+    pa.tile_base = (int64_t*)(ws + wl.base);
+    pa.dq_base = (int64_t*)(ws + wl.dq_base);
+    pa.f8max = (unsigned*)(ws + wl.maxv);
+    if (has_bias) {
+      pa.bias = attn_bias;
+      pa.R = bias_R;
+      pa.bias_ext = (float*)(ws + wl.bias_ext);
+      pa.bias_bx = (bias_ext_len(max_seq_len) + 1023) / 1024;
+    }
+  }
+  pa.width = H * D;
+  pa.z[0] = (parts & kBwdDq) ? p.dq : p.dk;
+  pa.zrs[0] = (parts & kBwdDq) ? p.dq_rs : p.dk_rs;
+  pa.z[1] = (parts & kBwdDkdv) ? p.dk : (uint16_t*)nullptr;
+  pa.zrs[1] = p.dk_rs;
+  pa.z[2] = (parts & kBwdDkdv) ? p.dv : (uint16_t*)nullptr;
+  pa.zrs[2] = p.dv_rs;
+  hipError_t e = launch_prep(pa, stream);
+  if (e != hipSuccess) return (int)e;
+  use_schedule(p, B, H, (int*)(ws + wl.sched));
+  if (parts & kBwdDkdv) {
+    // the scale maxima, after the prep launch's reset
     const bool per_token = scale_row_stride || scale_head_stride;
     const int64_t ntok = per_token ? total_tokens : 1;
     const int sgrid = (int)std::min<int64_t>((ntok + 255) / 256, 256);
     hipLaunchKernelGGL(f8_scale_max, dim3(sgrid > 0 ? sgrid : 1), dim3(256), 0, stream, q_scale, k_scale, ntok,
                        per_token ? H : 1, scale_row_stride, scale_head_stride, (unsigned*)(ws + wl.maxv));
-    if (has_bias) {
-      p.bias_ext = (const float*)(ws + wl.bias_ext);
-      hipLaunchKernelGGL(build_bias_ext, dim3((bias_ext_len(max_seq_len) + 255) / 256, H), dim3(256), 0, stream,
-                         attn_bias, H, bias_R, max_seq_len, (float*)(ws + wl.bias_ext));
-    }
+    if (has_bias) p.bias_ext = (const float*)(ws + wl.bias_ext);
     // one scale tensor for q and k (the same device address): the shared mode
     const int sm = per_token ? kScalesPerToken : (q_scale == k_scale ? kScalesShared : kScalesPerTensor);
 #define HSTU_F8_DKDV(BB, SS) launch(hstu_bwd_f8_dkdv_kernel<BB, SS>, F8Bwd::LDS, 2 * grid, p, stream, F8Bwd::NT)
@@ -3617,10 +3718,6 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
       if (e != hipSuccess) return (int)e;
     }
   }
-  hipLaunchKernelGGL(zero_rows_beyond_n, dim3(16, B), dim3(256), 0, stream, seq_offsets, max_seq_len, H * D,
-                     (parts & kBwdDq) ? p.dq : p.dk, (parts & kBwdDq) ? p.dq_rs : p.dk_rs,
-                     (parts & kBwdDkdv) ? p.dk : (uint16_t*)nullptr, p.dk_rs,
-                     (parts & kBwdDkdv) ? p.dv : (uint16_t*)nullptr, p.dv_rs);
   return (int)hipGetLastError();
 }
 }  // namespace
