@@ -15,6 +15,8 @@
 // the tile in registers between the max and the conversion.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "hstu_common.h"
 #include "hstu_mi355x.h"
 
@@ -53,20 +55,16 @@ __device__ __forceinline__ float group_max(float v) {
 // HD = H * D elements per token row (128 .. 512), D = 64 or 128; F32 input
 // rows are fp32, else bf16.  8-element pieces: PPR per token row, each thread
 // owns piece column c = tid % PPR (so one head) of tokens tid / PPR + i * 256 / PPR.
+// One 64-token tile (tokens p0 .. p0 + 63 of the sequence at st, length L)
+// by a 256-thread block; amax_lds: the block's [H][2] group maxima.
 template <int HD, int D, bool F32>
-__global__ void __launch_bounds__(256) do_blk_kernel(const uint8_t* __restrict__ x, int64_t x_rs,
-                                                      const int64_t* __restrict__ seq_offsets, int ntiles,
-                                                      uint8_t* __restrict__ y, uint8_t* __restrict__ e8) {
+__device__ __forceinline__ void do_tile(const uint8_t* __restrict__ x, int64_t x_rs, int64_t st, int L, int p0,
+                                        uint8_t* __restrict__ y, uint8_t* __restrict__ e8,
+                                        uint32_t (&amax_lds)[HD / D][2]) {
   constexpr int H = HD / D, PPR = HD / 8, TPI = 256 / PPR, NP = kTile / TPI, LPH = D / 8;
   constexpr int ES = F32 ? 4 : 2;
   static_assert(256 % PPR == 0 && kTile % TPI == 0 && (LPH == 8 || LPH == 16), "piece layout");
-  __shared__ uint32_t amax_lds[H][2];
   const int tid = threadIdx.x;
-  const int b = blockIdx.x / ntiles, t = blockIdx.x - b * ntiles;
-  const int64_t st = seq_offsets[b];
-  const int L = (int)(seq_offsets[b + 1] - st);
-  const int p0 = t * kTile;
-  if (p0 >= L) return;
   if (tid < 2 * H) amax_lds[tid >> 1][tid & 1] = 0u;
   const int c = tid % PPR, tok0 = tid / PPR, h = c / LPH;
   // all loads first; rows past the sequence are zero (they take no part in the max)
@@ -138,15 +136,102 @@ __global__ void __launch_bounds__(256) do_blk_kernel(const uint8_t* __restrict__
   }
 }
 
+// Block (b, t) of the B x ntiles grid: tile t of sequence b, if it has tokens.
+template <int HD, int D, bool F32>
+__global__ void __launch_bounds__(256) do_blk_kernel(const uint8_t* __restrict__ x, int64_t x_rs,
+                                                      const int64_t* __restrict__ seq_offsets, int ntiles,
+                                                      uint8_t* __restrict__ y, uint8_t* __restrict__ e8) {
+  __shared__ uint32_t amax_lds[HD / D][2];
+  const int b = blockIdx.x / ntiles, t = blockIdx.x - b * ntiles;
+  const int64_t st = seq_offsets[b];
+  const int L = (int)(seq_offsets[b + 1] - st);
+  if (t * kTile >= L) return;
+  do_tile<HD, D, F32>(x, x_rs, st, L, t * kTile, y, e8, amax_lds);
+}
+
+// The same tiles, only those that hold tokens, walked by a persistent grid:
+// each block first builds the tile prefix of the sequences in LDS (tiles of
+// sequence b = ceil(min(L_b, 64 ntiles) / 64)), then takes tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ..., finding each tile's sequence by binary search.
+// Blocks therefore start their next tile's loads while others still store,
+// and no block is spent on the padding of short sequences.  B <= kPersistMaxB.
+constexpr int kPersistMaxB = 4096;
+template <int HD, int D, bool F32>
+__global__ void __launch_bounds__(256) do_blk_persistent(const uint8_t* __restrict__ x, int64_t x_rs,
+                                                          const int64_t* __restrict__ seq_offsets, int B,
+                                                          int ntiles, uint8_t* __restrict__ y,
+                                                          uint8_t* __restrict__ e8) {
+  __shared__ uint32_t amax_lds[HD / D][2];
+  __shared__ int pre[kPersistMaxB + 1];
+  __shared__ int part[256];
+  const int tid = threadIdx.x;
+  const int64_t cap = (int64_t)ntiles * kTile;
+  auto tiles = [&](int b) {
+    const int64_t L = min(seq_offsets[b + 1] - seq_offsets[b], cap);
+    return (int)((max(L, (int64_t)0) + kTile - 1) / kTile);
+  };
+  // exclusive prefix: thread tid sums sequences [tid per, tid per + per)
+  const int per = (B + 255) / 256, b0 = tid * per;
+  int sum = 0;
+  for (int i = 0; i < per; ++i)
+    if (b0 + i < B) sum += tiles(b0 + i);
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int run = tid ? part[tid - 1] : 0;
+  for (int i = 0; i < per; ++i) {
+    if (b0 + i < B) {
+      pre[b0 + i] = run;
+      run += tiles(b0 + i);
+    }
+  }
+  if (tid == 255) pre[B] = part[255];
+  __syncthreads();
+  const int total = pre[B];
+  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+    // the last b with pre[b] <= tile (sequences without tiles share their
+    // successor's prefix and are skipped by taking the last)
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pre[mid] <= tile) lo = mid;
+      else hi = mid - 1;
+    }
+    const int64_t st = seq_offsets[lo];
+    const int L = (int)(seq_offsets[lo + 1] - st);
+    do_tile<HD, D, F32>(x, x_rs, st, L, (tile - pre[lo]) * kTile, y, e8, amax_lds);
+    __syncthreads();  // the tile's E8 reads of amax_lds are done before the next tile resets it
+  }
+}
+
+// Persistent grid: about eight blocks per CU (the kernel's occupancy), never
+// more than the B x ntiles tiles there can be.
+constexpr int kPersistBlocks = 2048;
 template <int HD, int D>
-void launch_blk(bool f32, int grid, const void* x, int64_t rs, const int64_t* offs, int ntiles, void* y, void* e8,
+void launch_blk(bool f32, int B, int ntiles, const void* x, int64_t rs, const int64_t* offs, void* y, void* e8,
                 hipStream_t s) {
+  const int64_t all = (int64_t)B * ntiles;
+  if (B <= kPersistMaxB) {
+    const int grid = (int)std::min<int64_t>(all, kPersistBlocks);
+    if (f32)
+      hipLaunchKernelGGL((do_blk_persistent<HD, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)x, rs, offs,
+                         B, ntiles, (uint8_t*)y, (uint8_t*)e8);
+    else
+      hipLaunchKernelGGL((do_blk_persistent<HD, D, false>), dim3(grid), dim3(256), 0, s, (const uint8_t*)x, rs, offs,
+                         B, ntiles, (uint8_t*)y, (uint8_t*)e8);
+    return;
+  }
   if (f32)
-    hipLaunchKernelGGL((do_blk_kernel<HD, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)x, rs, offs, ntiles,
-                       (uint8_t*)y, (uint8_t*)e8);
-  else
-    hipLaunchKernelGGL((do_blk_kernel<HD, D, false>), dim3(grid), dim3(256), 0, s, (const uint8_t*)x, rs, offs,
+    hipLaunchKernelGGL((do_blk_kernel<HD, D, true>), dim3((unsigned)all), dim3(256), 0, s, (const uint8_t*)x, rs, offs,
                        ntiles, (uint8_t*)y, (uint8_t*)e8);
+  else
+    hipLaunchKernelGGL((do_blk_kernel<HD, D, false>), dim3((unsigned)all), dim3(256), 0, s, (const uint8_t*)x, rs,
+                       offs, ntiles, (uint8_t*)y, (uint8_t*)e8);
 }
 
 // dO8 * 2^(E8 - 127) -> bf16, 8 elements of one (token, head) per thread.
@@ -201,13 +286,12 @@ extern "C" int hstu_quantize_do_e4m3_blk(int dtype, const void* dout, int64_t do
   if (B == 0) return 0;
   const int ntiles = (max_seq_len + kTile - 1) / kTile;
   if ((int64_t)B * ntiles >= (int64_t)1 << 31) return HSTU_E_UNSUPPORTED;
-  const int grid = B * ntiles;
   const bool f32 = dtype == HSTU_DTYPE_FP32;
-  if (D == 128 && HD == 512) launch_blk<512, 128>(f32, grid, dout, dout_row_stride, seq_offsets, ntiles, dout_e4m3, e8, stream);
-  else if (D == 128 && HD == 256) launch_blk<256, 128>(f32, grid, dout, dout_row_stride, seq_offsets, ntiles, dout_e4m3, e8, stream);
-  else if (D == 128) launch_blk<128, 128>(f32, grid, dout, dout_row_stride, seq_offsets, ntiles, dout_e4m3, e8, stream);
-  else if (HD == 512) launch_blk<512, 64>(f32, grid, dout, dout_row_stride, seq_offsets, ntiles, dout_e4m3, e8, stream);
-  else if (HD == 256) launch_blk<256, 64>(f32, grid, dout, dout_row_stride, seq_offsets, ntiles, dout_e4m3, e8, stream);
-  else launch_blk<128, 64>(f32, grid, dout, dout_row_stride, seq_offsets, ntiles, dout_e4m3, e8, stream);
+  if (D == 128 && HD == 512) launch_blk<512, 128>(f32, B, ntiles, dout, dout_row_stride, seq_offsets, dout_e4m3, e8, stream);
+  else if (D == 128 && HD == 256) launch_blk<256, 128>(f32, B, ntiles, dout, dout_row_stride, seq_offsets, dout_e4m3, e8, stream);
+  else if (D == 128) launch_blk<128, 128>(f32, B, ntiles, dout, dout_row_stride, seq_offsets, dout_e4m3, e8, stream);
+  else if (HD == 512) launch_blk<512, 64>(f32, B, ntiles, dout, dout_row_stride, seq_offsets, dout_e4m3, e8, stream);
+  else if (HD == 256) launch_blk<256, 64>(f32, B, ntiles, dout, dout_row_stride, seq_offsets, dout_e4m3, e8, stream);
+  else launch_blk<128, 64>(f32, B, ntiles, dout, dout_row_stride, seq_offsets, dout_e4m3, e8, stream);
   return (int)hipGetLastError();
 }
