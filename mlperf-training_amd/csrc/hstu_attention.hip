@@ -241,7 +241,7 @@ struct AttnParams {
   // full-FP8 backward (hstu_attn_bwd_fp8)
   const uint8_t* do8;       // e4m3 dO [T, H, D], row stride do_rs bytes
   const uint8_t* e8;        // [T, H]: 127 - e of each token's dO group (dO8 = e4m3(dO * 2^e))
-  const unsigned* f8max;    // workspace: float bits of max q_scale, max k_scale
+  const unsigned* f8max;    // workspace: kScaleParts partial maxima (float bits) of q_scale, k_scale
   float p8_scale;           // e4m3 P = silu / N * p8_scale (a power of two times N-relative)
   float ds8_scale;          // e4m3 dS = dS' * (scale normaliser) * ds8_scale
   // FP8 P.V forward (hstu_attn_fwd_fp8_pv)
@@ -2193,6 +2193,17 @@ __device__ __forceinline__ uint8_t* f8_tile(const AttnParams& p, const SeqCtx& c
   return p.ds_ws + idx * F8Bwd::TILE;
 }
 
+// The largest scale of array `which` (0: q, 1: k) from the kScaleParts
+// partial maxima the set-up launch left (non-negative floats order as their
+// bits); every lane of the wave must be active.
+constexpr int kScaleParts = 64;
+__device__ __forceinline__ unsigned f8_max_scale(const unsigned* parts, int which) {
+  static_assert(kScaleParts == 64, "one partial per lane");
+  unsigned m = parts[2 * (threadIdx.x & 63) + which];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, off));
+  return __builtin_amdgcn_readfirstlane(m);
+}
 // 2^-E with E the frexp exponent of the largest scale: s * 2^-E in (0, 1).
 __device__ __forceinline__ float f8_norm(unsigned bits) {
   int e = 0;
@@ -2251,7 +2262,7 @@ __global__ void __launch_bounds__(F8Bwd::NT, 3) hstu_bwd_f8_dkdv_kernel(AttnPara
     sk = p.k_scale[(sc.start + key) * p.s_rs + h * p.s_hs];
     sv = p.v_scale[(sc.start + key) * p.s_rs + h * p.s_hs];
   }
-  const float nq = f8_norm(p.f8max[0]), nk = f8_norm(p.f8max[1]);
+  const float nq = f8_norm(f8_max_scale(p.f8max, 0)), nk = f8_norm(f8_max_scale(p.f8max, 1));
   // P8 = e4m3(t sigma kp) is computed as t sigma' with sigma' = kp sigma =
   // 1 / ((1 + 2^t) / kp); then silu'(x) kp = fma(P, fma(sigma', ln2 / kp, -ln2), sigma'),
   // and the 1 / kp goes into the dS factors
@@ -2485,7 +2496,7 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   const BufRsrc e8_rsrc = make_rsrc(p.e8 + sc.start * p.H + h, (uint32_t)(L * p.H));
   const uint32_t s_step = (uint32_t)(p.s_rs * 4);
   const BufRsrc sk_rsrc = make_rsrc(p.k_scale + sc.start * p.s_rs + h * p.s_hs, (uint32_t)(p.s_rs ? L * p.s_rs * 4 : 4));
-  const float nk = f8_norm(p.f8max[1]);
+  const float nk = f8_norm(f8_max_scale(p.f8max, 1));
   const float unscale = 1.0f / (nk * p.ds8_scale);
   const int R1 = p.bias_R - 1;
   // the wave's bias-gradient histogram, offsets 0 .. R - 1
@@ -2735,22 +2746,22 @@ __device__ __forceinline__ int64_t dq_blocks(const int64_t* seq_offsets, int b, 
 
 // base[b] = sum over sequences b' < b of f8_tiles(min(length, N)); base[B] =
 // the total; dq_base the same prefix of 128-query blocks (the bias-gradient
-// rows); and the two scale maxima (f8max) reset for f8_scale_max.
-__device__ void f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base, int64_t* dq_base,
-                               unsigned* f8max) {
+// rows).
+__device__ void f8_tile_prefix(const int64_t* seq_offsets, int B, int N, int64_t* base, int64_t* dq_base) {
   __shared__ int64_t part[1024];
-  if (threadIdx.x < 2) f8max[threadIdx.x] = 0u;
   seq_exclusive_scan(B, [&](int b) { return f8_tiles(min(seq_offsets[b + 1] - seq_offsets[b], (int64_t)N)); },
                      part, base);
   seq_exclusive_scan(B, [&](int b) { return dq_blocks(seq_offsets, b, N); }, part, dq_base);
 }
 
-// f8max[0] / [1] = float bits of the largest q / k scale over [T, H] (or the scalar).
-__global__ void __launch_bounds__(256) f8_scale_max(const float* qs, const float* ks, int64_t ntok, int H,
-                                                    int64_t srs, int64_t shs, unsigned* f8max) {
-  __shared__ float red[2][4];
+// Partial maxima of |q_scale| and |k_scale| over [T, H] (or the scalar):
+// block bx of kScaleParts 1024-thread blocks writes parts[2 bx], [2 bx + 1]
+// (float bits) over tokens bx * 1024 + tid, stepping by kScaleParts * 1024.
+__device__ void f8_scale_part(const float* qs, const float* ks, int64_t ntok, int H, int64_t srs, int64_t shs,
+                              unsigned* parts, int bx) {
+  __shared__ float red[2][16];
   float mq = 0.f, mk = 0.f;
-  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < ntok; t += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t t = bx * (int64_t)blockDim.x + threadIdx.x; t < ntok; t += (int64_t)kScaleParts * blockDim.x) {
     for (int hh = 0; hh < H; ++hh) {
       const int64_t o = t * srs + hh * shs;
       mq = fmaxf(mq, fabsf(qs[o]));
@@ -2768,10 +2779,10 @@ __global__ void __launch_bounds__(256) f8_scale_max(const float* qs, const float
     red[1][wv] = mk;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    // one atomic per block and value (the maxima are non-negative: float bits order as unsigned)
-    atomicMax(&f8max[0], __float_as_uint(fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]))));
-    atomicMax(&f8max[1], __float_as_uint(fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]))));
+  if (threadIdx.x < 2) {
+    float m = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) m = fmaxf(m, red[threadIdx.x][w]);
+    parts[2 * bx + threadIdx.x] = __float_as_uint(m);
   }
 }
 
@@ -3029,8 +3040,8 @@ __device__ void zero_rows_beyond_n(const int64_t* seq_offsets, int N, int width,
 // The small set-up work of an attention call in one launch of 1024-thread
 // blocks, by block role (each block takes one role, so every barrier inside
 // a role is block-uniform): the block schedule (one block, if sched); the FP8
-// backward's tile and dQ-block prefixes and the scale-maximum reset (one
-// block, if tile_base); the pre-clamped bias rows (bias_bx blocks per head,
+// backward's tile and dQ-block prefixes (one block) and the partial maxima of
+// its q and k scales (kScaleParts blocks), if tile_base; the pre-clamped bias rows (bias_bx blocks per head,
 // if bias_ext); rows past N zeroed in up to three outputs (kPrepZero blocks
 // per sequence, if z[0]).  The roles touch disjoint memory.
 constexpr int kPrepZero = 4;
@@ -3040,7 +3051,12 @@ struct PrepArgs {
   int* sched;  // null: no schedule block
   int64_t* tile_base;
   int64_t* dq_base;
-  unsigned* f8max;  // tile_base null: no prefix block
+  unsigned* f8max;  // tile_base null: no prefix and no scale blocks
+  const float* qs;
+  const float* ks;
+  int64_t ntok;
+  int sH;
+  int64_t srs, shs;
   const float* bias;
   float* bias_ext;  // null: no bias blocks
   int R, bias_bx;
@@ -3049,7 +3065,7 @@ struct PrepArgs {
   int64_t zrs[3];
 };
 int prep_blocks(const PrepArgs& a) {
-  return (a.sched ? 1 : 0) + (a.tile_base ? 1 : 0) + (a.bias_ext ? a.H * a.bias_bx : 0) +
+  return (a.sched ? 1 : 0) + (a.tile_base ? 1 + kScaleParts : 0) + (a.bias_ext ? a.H * a.bias_bx : 0) +
          (a.z[0] ? kPrepZero * a.B : 0);
 }
 __global__ void __launch_bounds__(1024) attn_prep(PrepArgs a) {
@@ -3063,10 +3079,14 @@ __global__ void __launch_bounds__(1024) attn_prep(PrepArgs a) {
   }
   if (a.tile_base) {
     if (blk == 0) {
-      f8_tile_prefix(a.seq_offsets, a.B, a.N, a.tile_base, a.dq_base, a.f8max);
+      f8_tile_prefix(a.seq_offsets, a.B, a.N, a.tile_base, a.dq_base);
       return;
     }
-    blk -= 1;
+    if (blk <= kScaleParts) {
+      f8_scale_part(a.qs, a.ks, a.ntok, a.sH, a.srs, a.shs, a.f8max, blk - 1);
+      return;
+    }
+    blk -= 1 + kScaleParts;
   }
   if (a.bias_ext) {
     const int nb = a.H * a.bias_bx;
@@ -3561,7 +3581,7 @@ F8Ws f8_ws(int64_t T, int B, int H, int N, int R) {
   w.dq_base = o;
   o += align256(((int64_t)B + 1) * 8);
   w.maxv = o;
-  o += 256;
+  o += align256(kScaleParts * 2 * 4);
   w.base = o;
   o += align256(((int64_t)B + 1) * 8);
   w.tiles = o;
@@ -3669,6 +3689,13 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
     pa.tile_base = (int64_t*)(ws + wl.base);
     pa.dq_base = (int64_t*)(ws + wl.dq_base);
     pa.f8max = (unsigned*)(ws + wl.maxv);
+    const bool per_token = scale_row_stride || scale_head_stride;
+    pa.qs = q_scale;
+    pa.ks = k_scale;
+    pa.ntok = per_token ? total_tokens : 1;
+    pa.sH = per_token ? H : 1;
+    pa.srs = scale_row_stride;
+    pa.shs = scale_head_stride;
     if (has_bias) {
       pa.bias = attn_bias;
       pa.R = bias_R;
@@ -3687,12 +3714,7 @@ int attn_bwd_fp8_impl(int parts, const void* dout8, const void* dout_e8, int64_t
   if (e != hipSuccess) return (int)e;
   use_schedule(p, B, H, (int*)(ws + wl.sched));
   if (parts & kBwdDkdv) {
-    // the scale maxima, after the prep launch's reset
     const bool per_token = scale_row_stride || scale_head_stride;
-    const int64_t ntok = per_token ? total_tokens : 1;
-    const int sgrid = (int)std::min<int64_t>((ntok + 255) / 256, 256);
-    hipLaunchKernelGGL(f8_scale_max, dim3(sgrid > 0 ? sgrid : 1), dim3(256), 0, stream, q_scale, k_scale, ntok,
-                       per_token ? H : 1, scale_row_stride, scale_head_stride, (unsigned*)(ws + wl.maxv));
     if (has_bias) p.bias_ext = (const float*)(ws + wl.bias_ext);
     // one scale tensor for q and k (the same device address): the shared mode
     const int sm = per_token ? kScalesPerToken : (q_scale == k_scale ? kScalesShared : kScalesPerTensor);
