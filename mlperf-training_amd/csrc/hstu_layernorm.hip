@@ -600,23 +600,38 @@ __global__ void __launch_bounds__(kThreads) ln_mul_bwd_kernel(BwdArgs a) {
   }
 }
 
-// dweight[c] / dbias[c] = sum of the blocks' partials in block order: 4 threads
-// per column each sum a quarter of the blocks, then combine in fixed order.
-__global__ void __launch_bounds__(kThreads) ln_reduce_partials(const float* partial, int nblocks, int D,
-                                                               float* dweight, float* dbias) {
-  __shared__ float part[4][64];
+// dweight / dbias: the column sums of the [nblocks, 2D] partial rows (dweight
+// columns, then dbias), in a fixed order.  Block x owns 64 columns; thread
+// (q, c) of 16 x 64 sums rows q + 16 k into accumulator k % 8 (eight loads in
+// flight per thread), adds its eight accumulators pairwise, and the 16 row
+// groups are added in a fixed tree.
+constexpr int kRedThreads = 1024;
+__global__ void __launch_bounds__(kRedThreads) ln_reduce_partials(const float* partial, int nblocks, int D,
+                                                                  float* dweight, float* dbias) {
+  __shared__ float part[16][64];
   const int cl = threadIdx.x & 63, q = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + cl;  // column of the [2, D] partial row
-  float s = 0.f;
+  const int64_t ld = 2 * (int64_t)D;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (c < 2 * D) {
-    const int per = (nblocks + 3) / 4;
-    const int b0 = q * per, b1 = min(nblocks, b0 + per);
-    for (int bk = b0; bk < b1; ++bk) s += partial[(int64_t)bk * 2 * D + c];
+    int bk = q;
+    for (; bk + 7 * 16 < nblocks; bk += 8 * 16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += partial[(int64_t)(bk + 16 * j) * ld + c];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (bk + 16 * j < nblocks) acc[j] += partial[(int64_t)(bk + 16 * j) * ld + c];
   }
-  part[q][cl] = s;
+  part[q][cl] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   __syncthreads();
+#pragma unroll
+  for (int w = 8; w > 0; w >>= 1) {
+    if (q < w) part[q][cl] += part[q + w][cl];
+    __syncthreads();
+  }
   if (q == 0 && c < 2 * D) {
-    const float t = ((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl];
+    const float t = part[0][cl];
     if (c < D) dweight[c] = t;
     else dbias[c - D] = t;
   }
@@ -1060,7 +1075,7 @@ extern "C" int hstu_ln_mul_bwd(const void* dy, int64_t lddy, const void* x, int6
   a.lddres = lddres;
   a.partial = (float*)workspace;
   launch_bwd(D, u == nullptr ? kNoU : mul_u_act, mask != nullptr, y != nullptr, a, stream);
-  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial,
+  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kRedThreads), 0, stream, a.partial,
                      u == nullptr ? kBwdBlocksMax : kBwdBlocksU, D, dweight, dbias);
   return (int)hipGetLastError();
 }
@@ -1094,7 +1109,7 @@ extern "C" int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_s
     return HSTU_E_UNSUPPORTED;
   if (rows == 0) {
     // no rows: zero weight gradients, like the standalone backward
-    hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kRedThreads), 0, stream,
                        (const float*)workspace, 0, D, dweight, dbias);
     return (int)hipGetLastError();
   }
@@ -1145,7 +1160,7 @@ extern "C" int hstu_outproj_ln_bwd(const void* g8, int64_t ldg, const float* g_s
   void* args[] = {&p};
   hipError_t e = hipLaunchKernel(fn, dim3(grid), dim3(kObThreads), args, (size_t)kObLds, stream);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kThreads), 0, stream, a.partial, grid, D,
+  hipLaunchKernelGGL(ln_reduce_partials, dim3((2 * D + 63) / 64), dim3(kRedThreads), 0, stream, a.partial, grid, D,
                      dweight, dbias);
   return (int)hipGetLastError();
 }
