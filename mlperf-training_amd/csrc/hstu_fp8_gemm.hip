@@ -1351,9 +1351,17 @@ __global__ void __launch_bounds__(256) colsum_finish_kernel(const float* __restr
   const int tid = threadIdx.x;
   if ((int)blockIdx.x < cols / 32) {
     const int c = tid & 31, g = tid >> 5, col = blockIdx.x * 32 + c;
-    float s = 0.f;
-    for (int64_t i = g; i < nstripes; i += 8) s += part_col[i * cols + col];
-    red[g][c] = s;
+    // stripes g + 8 k into accumulator k % 8: eight loads in flight
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t i = g;
+    for (; i + 7 * 8 < nstripes; i += 8 * 8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += part_col[(i + 8 * j) * cols + col];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i + 8 * j < nstripes) acc[j] += part_col[(i + 8 * j) * cols + col];
+    red[g][c] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
     __syncthreads();
     if (g == 0) {
       float t = 0.f;
@@ -1362,8 +1370,16 @@ __global__ void __launch_bounds__(256) colsum_finish_kernel(const float* __restr
       colsum[col] = t;
     }
   } else {
-    float m = 0.f;
-    for (int64_t i = tid; i < namax; i += 256) m = __builtin_fmaxf(m, part_amax[i]);
+    float m = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+    int64_t i = tid;
+    for (; i + 3 * 256 < namax; i += 4 * 256) {
+      m = __builtin_fmaxf(m, part_amax[i]);
+      m1 = __builtin_fmaxf(m1, part_amax[i + 256]);
+      m2 = __builtin_fmaxf(m2, part_amax[i + 512]);
+      m3 = __builtin_fmaxf(m3, part_amax[i + 768]);
+    }
+    for (; i < namax; i += 256) m = __builtin_fmaxf(m, part_amax[i]);
+    m = __builtin_fmaxf(__builtin_fmaxf(m, m1), __builtin_fmaxf(m2, m3));
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
     if ((tid & 63) == 0) red[0][tid >> 6] = m;
