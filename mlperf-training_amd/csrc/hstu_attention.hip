@@ -2997,15 +2997,22 @@ __global__ void dbias_chunk_sum(const float* rows, const int64_t* dq_base, int B
   chunks[((int64_t)c * H + h) * W + i] = s;
 }
 
-// dbias [H, 2R - 1] = scale * the chunks summed in chunk order.  A row of W
+// dbias [H, 2R - 1] = scale * the chunks summed in a fixed order.  A row of W
 // floats holds the offsets R - W .. R - 1; dbias entries below are zero.
 __global__ void dbias_finish(const float* chunks, int H, int W, int R, float scale, float* dbias) {
   const int j = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y, n = 2 * R - 1;
   if (j >= n) return;
   const int i = j - (n - W);
-  float s = 0.f;
-  if (i >= 0)
-    for (int c = 0; c < kDbiasChunks; ++c) s += chunks[((int64_t)c * H + h) * W + i];
+  // chunk c into accumulator c % 8 (eight loads in flight), then a fixed tree
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (i >= 0) {
+    static_assert(kDbiasChunks % 8 == 0, "whole groups of eight chunks");
+    for (int c = 0; c < kDbiasChunks; c += 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[k] += chunks[((int64_t)(c + k) * H + h) * W + i];
+    }
+  }
+  const float s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   dbias[(int64_t)h * n + j] = s * scale;
 }
 
