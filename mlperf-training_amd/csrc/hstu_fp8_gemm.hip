@@ -1229,19 +1229,31 @@ __global__ void __launch_bounds__(256) cast_unit_e4m3_kernel(const uint8_t* __re
 // when rolling, scale = max(peak, 1e-30) * factor, 1 / scale, peak = 0.
 // One block of 256 threads (a cast of config 3's gradients leaves ~10 000
 // partials); the arithmetic is the host policy's, operation for operation.
-__global__ void __launch_bounds__(256) site_update_kernel(const float* __restrict__ vals, int count,
-                                                          float* __restrict__ st, float limit, int live, int roll,
-                                                          float factor, float* __restrict__ snapshot) {
-  __shared__ float red[4];
+constexpr int kSiteThreads = 1024;
+__global__ void __launch_bounds__(kSiteThreads) site_update_kernel(const float* __restrict__ vals, int count,
+                                                                   float* __restrict__ st, float limit, int live,
+                                                                   int roll, float factor,
+                                                                   float* __restrict__ snapshot) {
+  __shared__ float red[kSiteThreads / 64];
   const int tid = threadIdx.x;
-  float m = 0.f;
-  for (int i = tid; i < count; i += 256) m = max_nan(m, vals[i]);
+  // four loads in flight per thread (max_nan is order-free)
+  float m = 0.f, m1 = 0.f, m2 = 0.f, m3 = 0.f;
+  int i = tid;
+  for (; i + 3 * kSiteThreads < count; i += 4 * kSiteThreads) {
+    m = max_nan(m, vals[i]);
+    m1 = max_nan(m1, vals[i + kSiteThreads]);
+    m2 = max_nan(m2, vals[i + 2 * kSiteThreads]);
+    m3 = max_nan(m3, vals[i + 3 * kSiteThreads]);
+  }
+  for (; i < count; i += kSiteThreads) m = max_nan(m, vals[i]);
+  m = max_nan(max_nan(m, m1), max_nan(m2, m3));
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = max_nan(m, __shfl_xor(m, off));
   if ((tid & 63) == 0) red[tid >> 6] = m;
   __syncthreads();
   if (tid != 0) return;
-  m = max_nan(max_nan(red[0], red[1]), max_nan(red[2], red[3]));
+#pragma unroll
+  for (int w = 1; w < kSiteThreads / 64; ++w) m = max_nan(m, red[w]);
   const float scale = st[0];
   if (live) st[3] = st[3] + (m > scale * limit ? 1.f : 0.f);
   const float peak = max_nan(st[2], m);
@@ -1656,7 +1668,7 @@ extern "C" int hstu_quantize_e4m3_unit(int in_dtype, const void* x, int64_t n, v
 extern "C" int hstu_fp8_site_update(const float* amax_values, int count, float* state, float limit, int live,
                                     int roll, float factor, float* snapshot, hipStream_t stream) {
   if (!amax_values || count <= 0 || !state || !(limit > 0.f)) return HSTU_E_BAD_ARG;
-  hipLaunchKernelGGL(site_update_kernel, dim3(1), dim3(256), 0, stream, amax_values, count, state, limit, live, roll,
+  hipLaunchKernelGGL(site_update_kernel, dim3(1), dim3(kSiteThreads), 0, stream, amax_values, count, state, limit, live, roll,
                      factor, snapshot);
   return (int)hipGetLastError();
 }
