@@ -570,3 +570,48 @@ def test_full_fp8_backward_prescales(hip_lib, monkeypatch, dsc_k, ssc_k):
     monkeypatch.setenv("DLRM_HSTU_FP8_BWD_FULL_DSC_K", str(dsc_k))
     for a, b in zip(got, run()):
         assert torch.equal(a, b)
+
+
+def _cut(x, lengths, N):
+    """Rows of each sequence up to max_seq_len N, in batch order."""
+    out, s = [], 0
+    for L in lengths:
+        out.append(x[s:s + min(L, N)])
+        s += L
+    return torch.cat(out)
+
+
+def test_full_fp8_backward_rows_past_max_seq_len(hip_lib):
+    """A sequence longer than max_seq_len: the full-FP8 backward leaves its
+    dq, dk and dv rows past N zero (the set-up launch zeroes them; the
+    gradient buffers start as NaN) and the other rows equal, bitwise, the
+    same call on the batch with that sequence cut at N."""
+    ops = _ops()
+    H, D = 2, 128
+    lengths, N = [300, 700, 64, 513], 512
+    alpha = 1.0 / D ** 0.5
+    q8, k8, v8, sq, sk, sv, offs, dout, _, _ = _full_fp8_case(lengths, H, D, 17, False)
+    bias = orc.make_bias(H, 256)
+    print(f"full-FP8 bwd past N: lengths={lengths} N={N}", flush=True)
+
+    def run(q8, k8, v8, sq, sk, sv, dout, offs):
+        g = [torch.full(q8.shape, float("nan"), dtype=torch.bfloat16, device=DEV) for _ in range(3)]
+        db = torch.empty(bias.shape, dtype=torch.float32, device=DEV)
+        ops.triton_hstu_attention_bwd(dout.to(DEV), *[t.to(DEV) for t in (q8, k8, v8)], *g, offs.to(DEV), None, N,
+                                      alpha, 0, 0, None, False, 0, *[s.to(DEV).contiguous() for s in (sq, sk, sv)],
+                                      attn_bias=bias.to(DEV), dbias=db, full_fp8=True)
+        torch.cuda.synchronize()
+        return [t.cpu() for t in g], db.cpu()
+
+    g, db = run(q8, k8, v8, sq, sk, sv, dout, offs)
+    cut = [min(L, N) for L in lengths]
+    gc, dbc = run(*[_cut(t, lengths, N) for t in (q8, k8, v8, sq, sk, sv, dout)], orc.offsets_from_lengths(cut))
+    keep = torch.zeros(sum(lengths), dtype=torch.bool)
+    s = 0
+    for L in lengths:
+        keep[s:s + min(L, N)] = True
+        s += L
+    for name, a, b in zip(("dq", "dk", "dv"), g, gc):
+        assert torch.equal(a[~keep], torch.zeros_like(a[~keep])), f"{name}: rows past N not zero"
+        assert torch.equal(a[keep], b), f"{name}: kept rows differ from the cut batch"
+    assert orc.rel_l2(dbc.double(), db.double()) <= 1e-6  # the same pairs, summed in another block order

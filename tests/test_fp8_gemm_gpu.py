@@ -59,7 +59,8 @@ def _operands(M, N, K, seed=0, per_row=True, per_col=True):
     return a8, sa.reshape(-1), w8t.contiguous(), sw.reshape(-1)
 
 
-@pytest.mark.parametrize("M,N,K", [(1000, 2048, 512), (129, 512, 512), (1, 128, 128), (300, 256, 1536)])
+@pytest.mark.parametrize("M,N,K", [(1000, 2048, 512), (129, 512, 512), (1, 128, 128), (300, 256, 1536),
+                                   (300, 1024, 256), (257, 1024, 2048)])
 @pytest.mark.parametrize("scales", ["rowcol", "tensor"])
 def test_gemm_bf16(hip_lib, M, N, K, scales):
     fp8 = _fp8()

@@ -179,3 +179,37 @@ def test_fwd_pv8_long_n(hip_lib):
     exact = PV.fwd_pv8(N, alpha, q8, k8, v8, sq, sk, sv, offs, attn_bias=bias, quantize=False)
     assert torch.isfinite(out.float()).all()
     _check(out, want, exact, f"lengths={lengths} N={N}")
+
+
+def test_fwd_pv8_rows_past_max_seq_len(hip_lib):
+    """A sequence longer than max_seq_len: the FP8 P.V forward's rows past N
+    are zero (zeroed by the set-up launch) and the other rows equal, bitwise,
+    the same call on the batch with that sequence cut at N."""
+    ops = _ops()
+    lengths, N = [300, 700, 64, 513], 512
+    alpha = 1.0 / 128 ** 0.5
+    q8, k8, v8, sq, sk, sv, offs = _case(lengths, seed=23)
+    bias = orc.make_bias(2, 256)
+    print(f"FP8 P.V fwd past N: lengths={lengths} N={N}", flush=True)
+    # stale NaN in the allocator's free memory, where the output will likely land
+    junk = torch.full((sum(lengths), 2, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    del junk
+    out = _run(ops, N, alpha, q8, k8, v8, sq, sk, sv, offs, bias, fp8_pv=True).cpu()
+
+    def cut(x):
+        parts, s = [], 0
+        for L in lengths:
+            parts.append(x[s:s + min(L, N)])
+            s += L
+        return torch.cat(parts)
+
+    cl = [min(L, N) for L in lengths]
+    outc = _run(ops, N, alpha, cut(q8), cut(k8), cut(v8), cut(sq), cut(sk), cut(sv), orc.offsets_from_lengths(cl),
+                bias, fp8_pv=True).cpu()
+    keep = torch.zeros(sum(lengths), dtype=torch.bool)
+    s = 0
+    for L in lengths:
+        keep[s:s + min(L, N)] = True
+        s += L
+    assert torch.equal(out[~keep], torch.zeros_like(out[~keep])), "rows past N not zero"
+    assert torch.equal(out[keep], outc), "kept rows differ from the cut batch"
