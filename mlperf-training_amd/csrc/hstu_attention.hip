@@ -1233,6 +1233,32 @@ __device__ __forceinline__ void diag_accumulate_to(float& hi, float& lo, const f
   lo += dpp_row<0x11E>(v[2]);
   lo += dpp_row<0x11D>(v[3]);
 }
+// diag_accumulate_to of the products x[r] c[r], one FMA per term (the DPP
+// move fused into v_fmac_f32, which the compiler does not do by itself); c[r]
+// is the factor of the lane the DPP reads for x[r], lane (p + r) mod 16.  A
+// DPP source written by a VALU instruction needs two wait states first: the
+// s_nop 0 and the plain FMA give them to x[1..3], and the closing s_nop 1
+// gives them to a DPP read of hi or lo that follows (the compiler's hazard
+// check does not look into inline assembly).
+__device__ __forceinline__ void diag_fma_to(float& hi, float& lo, const float (&x)[4], const float (&c)[4]) {
+  asm("s_nop 0\n\t"
+      "v_fmac_f32 %0, %2, %6\n\t"
+      "v_fmac_f32_dpp %0, %3, %7 row_shl:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %0, %4, %8 row_shl:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %0, %5, %9 row_shl:3 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %3, %7 row_shr:15 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %4, %8 row_shr:14 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "v_fmac_f32_dpp %1, %5, %9 row_shr:13 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+      "s_nop 1"
+      : "+v"(hi), "+v"(lo)
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(c[0]), "v"(c[1]), "v"(c[2]), "v"(c[3]));
+}
+// lane p of each 16-lane row <- lane (p + R) mod 16 (row_ror by 16 - R)
+template <int R>
+__device__ __forceinline__ float row_rot(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + 16 - R, 0xF, 0xF,
+                                                               false));
+}
 template <int S>
 __device__ __forceinline__ void diag_accumulate(float (&a)[4], const float (&v)[4]) {
   diag_accumulate_to(a[1 - S], a[2 - S], v);
@@ -2505,13 +2531,15 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
   if constexpr (BIAS) {
     for (int i = tid; i < 4 * p.bias_R; i += kThreads) hist0[i] = 0.f;
   }
-  // bias gradient: 2^(E8 - 127) of the dO group of this lane's query rows in half hf
+  // bias gradient: the E8 byte of the dO group of this lane's query rows in
+  // half hf as an f32 exponent field, the scale operand of the scaled e4m3
+  // conversion (which multiplies by 2^(field - 127), exactly the group scale)
   float grp[2] = {1.f, 1.f};
   if constexpr (BIAS) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const uint32_t b = buf_ldu8(e8_rsrc, (uint32_t)(m0 + 64 * hf + 8 * (g >> 1)) * (uint32_t)p.H);
-      grp[hf] = ldexpf(1.0f, (int)b - 127);
+      grp[hf] = __builtin_bit_cast(float, b << 23);
     }
   }
 
@@ -2579,17 +2607,17 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
     if (off >= R1) dclamp += dv;
     else if (off >= 0) atomicAdd(&hist[off], dv);
   };
-  // the 16 scores of sub-tile s, query sub-tile a, key sub-tile kt
-  auto piece = [&](const u32x4 (&pcs)[4], const float (&iskv)[2], int s, int a, int kt, float (&v)[4]) {
+  // the 16 scores of sub-tile s, query sub-tile a, key sub-tile kt, times
+  // their dO group scale (exact: a power of two), not yet times 1 / s_k
+  auto piece = [&](const u32x4 (&pcs)[4], int s, int a, int kt, float (&v)[4]) {
     const int hf = s >> 1, qp = s & 1;
     const uint32_t w = pcs[2 * kt + hf][2 * qp + a];
-    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-    const float c = iskv[kt] * grp[hf];
-    v[0] = lo[0] * c;
-    v[1] = lo[1] * c;
-    v[2] = hi[0] * c;
-    v[3] = hi[1] * c;
+    const f32x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, grp[hf], false);
+    const f32x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, grp[hf], true);
+    v[0] = lo[0];
+    v[1] = lo[1];
+    v[2] = hi[0];
+    v[3] = hi[1];
   };
   auto bias_grad = [&](int kb, const u32x4 (&pcs)[4], const float (&iskv)[2]) {
     const int base0 = m0 - kb * C::BN - 32 * wave;
@@ -2601,8 +2629,8 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
 #pragma unroll
           for (int kt = 0; kt < 2; ++kt) {
             float v[4];
-            piece(pcs, iskv, s, a, kt, v);
-            dclamp += (v[0] + v[1]) + (v[2] + v[3]);
+            piece(pcs, s, a, kt, v);
+            dclamp = __builtin_fmaf((v[0] + v[1]) + (v[2] + v[3]), iskv[kt], dclamp);
           }
       cr_m1 = cr_0 = cr_g1 = 0.f;
       return;
@@ -2612,18 +2640,27 @@ __global__ void __launch_bounds__(kThreads, 2) hstu_bwd_f8_dq_kernel(AttnParams 
     for (int i = 0; i < 8; ++i) bk[i] = 0.f;
     bk[8] = cr_m1;
     bk[9] = cr_0;
+    // 1 / s_k of the key that lane (p + r) mod 16 holds, per key sub-tile
+    float ck[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      ck[kt][0] = iskv[kt];
+      ck[kt][1] = row_rot<1>(iskv[kt]);
+      ck[kt][2] = row_rot<2>(iskv[kt]);
+      ck[kt][3] = row_rot<3>(iskv[kt]);
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       // rows = queries (16 a + 4 g + r), cols = keys (16 kt + li): shift kt - a
       float v00[4], v11[4], v01[4], v10[4];
-      piece(pcs, iskv, s, 0, 0, v00);
-      piece(pcs, iskv, s, 1, 1, v11);
-      piece(pcs, iskv, s, 0, 1, v01);
-      piece(pcs, iskv, s, 1, 0, v10);
-      diag_accumulate_to(bk[2 * s + 1], bk[2 * s + 2], v00);
-      diag_accumulate_to(bk[2 * s + 1], bk[2 * s + 2], v11);
-      diag_accumulate_to(bk[2 * s], bk[2 * s + 1], v01);
-      diag_accumulate_to(bk[2 * s + 2], bk[2 * s + 3], v10);
+      piece(pcs, s, 0, 0, v00);
+      piece(pcs, s, 1, 1, v11);
+      piece(pcs, s, 0, 1, v01);
+      piece(pcs, s, 1, 0, v10);
+      diag_fma_to(bk[2 * s + 1], bk[2 * s + 2], v00, ck[0]);
+      diag_fma_to(bk[2 * s + 1], bk[2 * s + 2], v11, ck[1]);
+      diag_fma_to(bk[2 * s], bk[2 * s + 1], v01, ck[1]);
+      diag_fma_to(bk[2 * s + 2], bk[2 * s + 3], v10, ck[0]);
     }
     float gu[10];  // unskewed bucket w = 1..9
 #pragma unroll
