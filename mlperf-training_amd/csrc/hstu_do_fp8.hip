@@ -53,19 +53,20 @@ __device__ __forceinline__ float group_max(float v) {
 }
 
 // HD = H * D elements per token row (128 .. 512), D = 64 or 128; F32 input
-// rows are fp32, else bf16.  8-element pieces: PPR per token row, each thread
-// owns piece column c = tid % PPR (so one head) of tokens tid / PPR + i * 256 / PPR.
-// One 64-token tile (tokens p0 .. p0 + 63 of the sequence at st, length L)
-// by a 256-thread block; amax_lds: the block's [H][2] group maxima.
-template <int HD, int D, bool F32>
+// rows are fp32, else bf16.  A tile is 64 tokens (p0 .. p0 + 63 of the
+// sequence at st, length L) by HT heads (h0 .. h0 + HT - 1), for a 256-thread
+// block.  8-element pieces: PPR per token row of the tile, each thread owns
+// piece column c = tid % PPR (so one head) of tokens tid / PPR + i * 256 / PPR;
+// amax_lds: the block's [HT][2] group maxima.
+template <int HD, int D, int HT, bool F32>
 __device__ __forceinline__ void do_tile(const uint8_t* __restrict__ x, int64_t x_rs, int64_t st, int L, int p0,
-                                        uint8_t* __restrict__ y, uint8_t* __restrict__ e8,
-                                        uint32_t (&amax_lds)[HD / D][2]) {
-  constexpr int H = HD / D, PPR = HD / 8, TPI = 256 / PPR, NP = kTile / TPI, LPH = D / 8;
+                                        int h0, uint8_t* __restrict__ y, uint8_t* __restrict__ e8,
+                                        uint32_t (&amax_lds)[HT][2]) {
+  constexpr int H = HD / D, PPR = HT * D / 8, TPI = 256 / PPR, NP = kTile / TPI, LPH = D / 8;
   constexpr int ES = F32 ? 4 : 2;
   static_assert(256 % PPR == 0 && kTile % TPI == 0 && (LPH == 8 || LPH == 16), "piece layout");
   const int tid = threadIdx.x;
-  if (tid < 2 * H) amax_lds[tid >> 1][tid & 1] = 0u;
+  if (tid < 2 * HT) amax_lds[tid >> 1][tid & 1] = 0u;
   const int c = tid % PPR, tok0 = tid / PPR, h = c / LPH;
   // all loads first; rows past the sequence are zero (they take no part in the max)
   constexpr int KW = F32 ? 2 : 1;  // 16-byte loads per piece
@@ -73,7 +74,7 @@ __device__ __forceinline__ void do_tile(const uint8_t* __restrict__ x, int64_t x
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int tok = tok0 + i * TPI;
-    const uint8_t* src = x + ((st + p0 + tok) * x_rs + (int64_t)c * 8) * ES;
+    const uint8_t* src = x + ((st + p0 + tok) * x_rs + (int64_t)h0 * D + (int64_t)c * 8) * ES;
     const bool ok = p0 + tok < L;
 #pragma unroll
     for (int k = 0; k < KW; ++k) raw[i * KW + k] = ok ? *(const u32x4*)(src + 16 * k) : u32x4{0u, 0u, 0u, 0u};
@@ -125,14 +126,14 @@ __device__ __forceinline__ void do_tile(const uint8_t* __restrict__ x, int64_t x
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], lo, true);
     int hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], 0, false);
     hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], hi, true);
-    *(u32x2*)(y + (st + p0 + tok) * HD + c * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
+    *(u32x2*)(y + (st + p0 + tok) * HD + h0 * D + c * 8) = u32x2{(uint32_t)lo, (uint32_t)hi};
   }
   // E8 bytes: one per (token, head) of the tile
-  for (int k = tid; k < kTile * H; k += 256) {
-    const int tok = k / H, hh = k - tok * H;
+  for (int k = tid; k < kTile * HT; k += 256) {
+    const int tok = k / HT, hh = k - tok * HT;
     if (p0 + tok >= L) continue;
     const float a = __builtin_bit_cast(float, amax_lds[hh][(tok & 15) < 8 ? 0 : 1]);
-    e8[(st + p0 + tok) * H + hh] = (uint8_t)(127 - group_exp(a));
+    e8[(st + p0 + tok) * H + h0 + hh] = (uint8_t)(127 - group_exp(a));
   }
 }
 
@@ -146,22 +147,26 @@ __global__ void __launch_bounds__(256) do_blk_kernel(const uint8_t* __restrict__
   const int64_t st = seq_offsets[b];
   const int L = (int)(seq_offsets[b + 1] - st);
   if (t * kTile >= L) return;
-  do_tile<HD, D, F32>(x, x_rs, st, L, t * kTile, y, e8, amax_lds);
+  do_tile<HD, D, HD / D, F32>(x, x_rs, st, L, t * kTile, 0, y, e8, amax_lds);
 }
 
-// The same tiles, only those that hold tokens, walked by a persistent grid:
-// each block first builds the tile prefix of the sequences in LDS (tiles of
-// sequence b = ceil(min(L_b, 64 ntiles) / 64)), then takes tiles blockIdx.x,
-// blockIdx.x + gridDim.x, ..., finding each tile's sequence by binary search.
-// Blocks therefore start their next tile's loads while others still store,
-// and no block is spent on the padding of short sequences.  B <= kPersistMaxB.
+// The same token tiles, only those that hold tokens, split by head and walked
+// by a persistent grid: each block first builds the tile prefix of the
+// sequences in LDS (tiles of sequence b = ceil(min(L_b, 64 ntiles) / 64)),
+// then takes (tile, head) items blockIdx.x, blockIdx.x + gridDim.x, ... (the
+// H heads of a token tile are consecutive items), finding each tile's
+// sequence by binary search.  Blocks therefore start their next item's loads
+// while others still store, no block is spent on the padding of short
+// sequences, and items of one head (16 KiB of bf16 at D = 128) balance the
+// grid's last round better than whole token tiles.  B <= kPersistMaxB.
 constexpr int kPersistMaxB = 4096;
 template <int HD, int D, bool F32>
 __global__ void __launch_bounds__(256) do_blk_persistent(const uint8_t* __restrict__ x, int64_t x_rs,
                                                           const int64_t* __restrict__ seq_offsets, int B,
                                                           int ntiles, uint8_t* __restrict__ y,
                                                           uint8_t* __restrict__ e8) {
-  __shared__ uint32_t amax_lds[HD / D][2];
+  constexpr int H = HD / D;
+  __shared__ uint32_t amax_lds[1][2];
   __shared__ int pre[kPersistMaxB + 1];
   __shared__ int part[256];
   const int tid = threadIdx.x;
@@ -192,8 +197,9 @@ __global__ void __launch_bounds__(256) do_blk_persistent(const uint8_t* __restri
   }
   if (tid == 255) pre[B] = part[255];
   __syncthreads();
-  const int total = pre[B];
-  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
+  const int total = pre[B] * H;
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    const int tile = item / H, hh = item - tile * H;
     // the last b with pre[b] <= tile (sequences without tiles share their
     // successor's prefix and are skipped by taking the last)
     int lo = 0, hi = B - 1;
@@ -204,20 +210,21 @@ __global__ void __launch_bounds__(256) do_blk_persistent(const uint8_t* __restri
     }
     const int64_t st = seq_offsets[lo];
     const int L = (int)(seq_offsets[lo + 1] - st);
-    do_tile<HD, D, F32>(x, x_rs, st, L, (tile - pre[lo]) * kTile, y, e8, amax_lds);
+    do_tile<HD, D, 1, F32>(x, x_rs, st, L, (tile - pre[lo]) * kTile, hh, y, e8, amax_lds);
     __syncthreads();  // the tile's E8 reads of amax_lds are done before the next tile resets it
   }
 }
 
-// Persistent grid: about eight blocks per CU (the kernel's occupancy), never
-// more than the B x ntiles tiles there can be.
-constexpr int kPersistBlocks = 2048;
+// Persistent grid: sixteen blocks per CU (measured at config 3: 47.9 us
+// against 53 us with 2048 blocks and 49.2 us with 8192), never more than the
+// B x ntiles x H items there can be.
+constexpr int kPersistBlocks = 4096;
 template <int HD, int D>
 void launch_blk(bool f32, int B, int ntiles, const void* x, int64_t rs, const int64_t* offs, void* y, void* e8,
                 hipStream_t s) {
   const int64_t all = (int64_t)B * ntiles;
   if (B <= kPersistMaxB) {
-    const int grid = (int)std::min<int64_t>(all, kPersistBlocks);
+    const int grid = (int)std::min<int64_t>(all * (HD / D), kPersistBlocks);
     if (f32)
       hipLaunchKernelGGL((do_blk_persistent<HD, D, true>), dim3(grid), dim3(256), 0, s, (const uint8_t*)x, rs, offs,
                          B, ntiles, (uint8_t*)y, (uint8_t*)e8);
