@@ -3023,14 +3023,23 @@ __global__ void __launch_bounds__(1024) dq_block_prefix(const int64_t* seq_offse
 }
 
 // Chunk c of head h's bias-gradient rows: the sum of rows c * per ..
-// min((c + 1) * per, n) - 1 in row order, n = dq_base[B] rows per head.
+// min((c + 1) * per, n) - 1 in a fixed order, n = dq_base[B] rows per head.
 __global__ void dbias_chunk_sum(const float* rows, const int64_t* dq_base, int B, int H, int W, float* chunks) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y, c = blockIdx.z;
   if (i >= W) return;
   const int64_t n = dq_base[B], per = (n + kDbiasChunks - 1) / kDbiasChunks;
   const int64_t r0 = c * per, r1 = min(n, r0 + per);
-  float s = 0.f;
-  for (int64_t r = r0; r < r1; ++r) s += rows[(r * H + h) * W + i];
+  // row r0 + 8 j + k into accumulator k (eight loads in flight), then a fixed tree
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t r = r0;
+  for (; r + 8 <= r1; r += 8) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] += rows[((r + k) * H + h) * W + i];
+  }
+#pragma unroll
+  for (int k = 0; k < 7; ++k)
+    if (r + k < r1) acc[k] += rows[((r + k) * H + h) * W + i];
+  const float s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
   chunks[((int64_t)c * H + h) * W + i] = s;
 }
 
